@@ -1,0 +1,72 @@
+"""Builds libdetllm_amd.so (gfx950 HIP kernels + C ABI) in-tree.
+
+Usage: python -m detllm_amd.build   (or detllm_amd.build.build_library()).
+
+Numeric flags are part of the contract: -ffp-contract=off keeps every
+multiply and add separately rounded (the reference forbids FMA), the
+correctly-rounded f32 divide/sqrt stays on, denormals stay enabled, and
+packed-FP32 instruction selection is disabled.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+OUT_DIR = PKG / "_build"
+LIB_NAME = "libdetllm_amd.so"
+ARCH = os.environ.get("DETLLM_AMD_ARCH", "gfx950")
+
+SOURCES = ["dtl_kernels.hip", "dtl_api.hip", "dtl_gguf.cpp", "dtl_range.cpp"]
+
+NUMERIC_FLAGS = [
+    "-ffp-contract=off",
+    "-fno-fast-math",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-fno-gpu-flush-denormals-to-zero",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: a ROCm toolchain is required to build detllm_amd")
+
+
+def build_library(verbose: bool = False) -> Path:
+    """Compiles every source into one shared library and returns its path."""
+    OUT_DIR.mkdir(exist_ok=True)
+    out = OUT_DIR / LIB_NAME
+    tmp = OUT_DIR / (LIB_NAME + ".tmp")
+    cmd = [
+        hipcc(),
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        *NUMERIC_FLAGS,
+        "-Wno-unused-result",
+        *[str(CSRC / s) for s in SOURCES],
+        "-o",
+        str(tmp),
+    ]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError(f"hipcc failed with exit code {res.returncode}")
+    os.replace(tmp, out)
+    return out
+
+
+if __name__ == "__main__":
+    path = build_library(verbose=True)
+    print(path)

@@ -1,0 +1,200 @@
+"""det-coder API mirror: logits -> integer CDF on the device, range coder on the host.
+
+Mirrors crates/det-coder of mii443/detllm: ``logits_to_cdf*`` /
+``logits_to_symbol_range*`` / ``uniform_*`` (src/cdf.rs:47-341),
+``RangeEncoder`` / ``RangeDecoder`` (src/range.rs:10-159) and the 56-byte
+``DtlzHeader`` (src/file.rs:1-89).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import enum
+import struct
+from dataclasses import dataclass
+
+import numpy as np
+
+from ._lib import DetllmError, check, lib, ptr
+
+M = 16_777_216
+MAX_SYMBOLS = 1 << 18
+BYTE_ESCAPE_SYMBOLS = 256
+
+
+class CdfError(enum.IntEnum):
+    Empty = 20
+    Malformed = 21
+    NonFiniteLogit = 22
+    SymbolOutOfRange = 23
+    TooManySymbols = 24
+    TotalTooLarge = 25
+
+
+class RangeError(enum.IntEnum):
+    InvalidFrequency = 30
+    UnexpectedEof = 31
+
+
+@dataclass(frozen=True)
+class SymbolRange:
+    cum: int
+    freq: int
+    total: int
+
+
+@dataclass
+class Cdf:
+    freq: np.ndarray  # u32
+    cum: np.ndarray   # u64
+    total: int
+
+
+def _logits(x) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+
+
+def _cdf(logits, tail: int) -> Cdf:
+    lg = _logits(logits)
+    n = lg.size + tail
+    freq = np.empty(max(n, 1), np.uint32)
+    cum = np.empty(max(n, 1), np.uint64)
+    total = C.c_uint64()
+    check(lib.dtl_logits_to_cdf(ptr(lg, C.c_float), lg.size, tail, ptr(freq, C.c_uint32),
+                                ptr(cum, C.c_uint64), C.byref(total)), "logits_to_cdf")
+    return Cdf(freq[:n], cum[:n], int(total.value))
+
+
+def logits_to_cdf(logits) -> Cdf:
+    """logits_to_cdf (cdf.rs:47-106)."""
+    return _cdf(logits, 0)
+
+
+def logits_to_cdf_with_byte_escapes(logits) -> Cdf:
+    """logits_to_cdf_with_byte_escapes (cdf.rs:95-106, 255-286)."""
+    return _cdf(logits, BYTE_ESCAPE_SYMBOLS)
+
+
+def _range(logits, symbol: int, tail: int) -> SymbolRange:
+    lg = _logits(logits)
+    if symbol < 0:
+        raise DetllmError(int(CdfError.SymbolOutOfRange), "logits_to_symbol_range")
+    cum, total = C.c_uint64(), C.c_uint64()
+    freq = C.c_uint32()
+    check(lib.dtl_logits_to_symbol_range(ptr(lg, C.c_float), lg.size, int(symbol), tail, C.byref(cum),
+                                         C.byref(freq), C.byref(total)), "logits_to_symbol_range")
+    return SymbolRange(int(cum.value), int(freq.value), int(total.value))
+
+
+def logits_to_symbol_range(logits, symbol: int) -> SymbolRange:
+    """logits_to_symbol_range_with_scratch (cdf.rs:123-130, 138-199)."""
+    return _range(logits, symbol, 0)
+
+
+def logits_to_symbol_range_with_byte_escapes(logits, symbol: int) -> SymbolRange:
+    """logits_to_symbol_range_with_byte_escapes (cdf.rs:131-136)."""
+    return _range(logits, symbol, BYTE_ESCAPE_SYMBOLS)
+
+
+def uniform_symbol_range(symbol: int, symbols: int) -> SymbolRange:
+    """uniform_symbol_range (cdf.rs:322-341)."""
+    cum, total = C.c_uint64(), C.c_uint64()
+    freq = C.c_uint32()
+    check(lib.dtl_uniform_symbol_range(symbol, symbols, C.byref(cum), C.byref(freq), C.byref(total)),
+          "uniform_symbol_range")
+    return SymbolRange(int(cum.value), int(freq.value), int(total.value))
+
+
+class RangeEncoder:
+    """RangeEncoder (range.rs:10-92): 64-bit low/range, carry-less renormalisation."""
+
+    def __init__(self):
+        h = C.c_void_p()
+        check(lib.dtl_range_encoder_new(C.byref(h)), "RangeEncoder::new")
+        self._h = h
+
+    def encode(self, cum: int, freq: int, total: int) -> None:
+        check(lib.dtl_range_encode(self._h, cum, freq, total), "RangeEncoder::encode")
+
+    def finish(self) -> bytes:
+        n = C.c_size_t()
+        check(lib.dtl_range_encoder_finish(self._h, None, 0, C.byref(n)), "RangeEncoder::finish")
+        buf = (C.c_uint8 * n.value)()
+        check(lib.dtl_range_encoder_finish(self._h, buf, n.value, C.byref(n)), "RangeEncoder::finish")
+        return bytes(buf)
+
+    def __del__(self):
+        try:
+            if self._h:
+                lib.dtl_range_encoder_free(self._h)
+                self._h = C.c_void_p()
+        except Exception:
+            pass
+
+
+class RangeDecoder:
+    """RangeDecoder (range.rs:94-159)."""
+
+    def __init__(self, data: bytes):
+        self._buf = (C.c_uint8 * max(len(data), 1)).from_buffer_copy(bytes(data) or b"\0")
+        h = C.c_void_p()
+        check(lib.dtl_range_decoder_new(self._buf, len(data), C.byref(h)), "RangeDecoder::new")
+        self._h = h
+
+    def decode_freq(self, total: int) -> int:
+        v = C.c_uint64()
+        check(lib.dtl_range_decode_freq(self._h, total, C.byref(v)), "RangeDecoder::decode_freq")
+        return int(v.value)
+
+    def advance(self, cum: int, freq: int, total: int) -> None:
+        check(lib.dtl_range_decode_advance(self._h, cum, freq, total), "RangeDecoder::advance")
+
+    def __del__(self):
+        try:
+            if self._h:
+                lib.dtl_range_decoder_free(self._h)
+                self._h = C.c_void_p()
+        except Exception:
+            pass
+
+
+MAGIC = b"DTLZ"
+VERSION = 1
+FLAG_BYTE_ESCAPES = 1
+HEADER_LEN = 56
+
+
+@dataclass(frozen=True)
+class DtlzHeader:
+    """DtlzHeader (file.rs:8-89): 56-byte little-endian container header."""
+
+    flags: int
+    model_sha256: bytes
+    n_ctx: int
+    overlap: int
+    orig_len: int
+
+    def validate(self) -> None:
+        if self.flags & ~FLAG_BYTE_ESCAPES:
+            raise ValueError(f"unsupported DTLZ flags {self.flags:#x}")
+        if self.n_ctx == 0:
+            raise ValueError("invalid DTLZ context")
+        if self.overlap >= self.n_ctx:
+            raise ValueError("invalid DTLZ overlap")
+
+    def encode(self) -> bytes:
+        return (MAGIC + struct.pack("<HH", VERSION, self.flags) + bytes(self.model_sha256)
+                + struct.pack("<IIQ", self.n_ctx, self.overlap, self.orig_len))
+
+    @classmethod
+    def decode(cls, data: bytes) -> "DtlzHeader":
+        if len(data) < HEADER_LEN:
+            raise ValueError("DTLZ header too short")
+        if data[:4] != MAGIC:
+            raise ValueError("bad DTLZ magic")
+        version, flags = struct.unpack_from("<HH", data, 4)
+        if version != VERSION:
+            raise ValueError(f"unsupported DTLZ version {version}")
+        n_ctx, overlap, orig_len = struct.unpack_from("<IIQ", data, 40)
+        h = cls(flags, bytes(data[8:40]), n_ctx, overlap, orig_len)
+        h.validate()
+        return h

@@ -1,0 +1,1155 @@
+// Host side of libdetllm_amd: GGUF model loading and device repacking,
+// sessions (KV cache, RoPE tables, workspace, stream), the per-layer launch
+// sequence of the decoder forward and the C ABI declared in detllm.h.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/detllm.h"
+#include "dtl_device.h"
+#include "dtl_gguf.h"
+#include "dtl_sha256.h"
+
+using namespace dtl;
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// device memory helpers
+
+struct DevBuf {
+  void* p = nullptr;
+  size_t n = 0;
+};
+
+int hip_status(hipError_t e) {
+  if (e == hipSuccess) return DTL_OK;
+  if (e == hipErrorOutOfMemory) return DTL_ERR_OUT_OF_MEMORY;
+  if (e == hipErrorNoDevice || e == hipErrorInvalidDevice) return DTL_ERR_NO_DEVICE;
+  return DTL_ERR_DEVICE;
+}
+
+#define HIP_TRY(expr)                    \
+  do {                                   \
+    hipError_t e_ = (expr);              \
+    if (e_ != hipSuccess) return hip_status(e_); \
+  } while (0)
+
+// Owner of a set of device allocations, freed together.
+class Arena {
+ public:
+  ~Arena() { release(); }
+  template <typename T>
+  int alloc(T** out, size_t count) {
+    void* p = nullptr;
+    size_t bytes = count * sizeof(T);
+    if (bytes == 0) bytes = 16;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return hip_status(e);
+    ptrs_.push_back(p);
+    bytes_ += bytes;
+    *out = static_cast<T*>(p);
+    return DTL_OK;
+  }
+  template <typename T>
+  int upload(T** out, const void* host, size_t count) {
+    int st = alloc(out, count);
+    if (st) return st;
+    return hip_status(hipMemcpy(*out, host, count * sizeof(T), hipMemcpyHostToDevice));
+  }
+  void release() {
+    for (void* p : ptrs_) (void)hipFree(p);
+    ptrs_.clear();
+    bytes_ = 0;
+  }
+  size_t bytes() const { return bytes_; }
+
+ private:
+  std::vector<void*> ptrs_;
+  size_t bytes_ = 0;
+};
+
+uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+bool f16_finite(uint16_t b) { return (b & 0x7c00) != 0x7c00; }
+
+// Bit-exact f16 -> f32 on the host (det-num f16.rs:6-34), used when F16
+// tensors are widened to F32 at load (det-model lib.rs:1753-1768).
+float f16_to_f32_host(uint16_t h) {
+  uint32_t sign = ((uint32_t)h & 0x8000u) << 16, exp = (h >> 10) & 0x1f, frac = h & 0x3ff, out;
+  if (exp == 0) {
+    if (frac == 0) {
+      out = sign;
+    } else {
+      int e = -14;
+      while ((frac & 0x400) == 0) {
+        frac <<= 1;
+        e--;
+      }
+      out = sign | ((uint32_t)(e + 127) << 23) | ((frac & 0x3ff) << 13);
+    }
+  } else if (exp == 0x1f) {
+    out = sign | 0x7f800000u | (frac << 13);
+  } else {
+    out = sign | ((exp + 112) << 23) | (frac << 13);
+  }
+  float f;
+  std::memcpy(&f, &out, 4);
+  return f;
+}
+
+// ---------------------------------------------------------------------------
+// model
+
+struct HostConfig {
+  size_t block_count = 0, d = 0, ff = 0, heads = 0, kv_heads = 0, ctx = 0, rope_dim = 0;
+  float eps = 0, attention_scale = 0, rope_base = 0;
+  int split_half = 0;
+};
+
+struct Layer {
+  float* attn_norm = nullptr;
+  float* ffn_norm = nullptr;
+  float* bq = nullptr;
+  float* bk = nullptr;
+  float* bv = nullptr;
+  DevMat wq{}, wk{}, wv{}, wo{}, gate{}, up{}, down{};
+};
+
+}  // namespace
+
+struct dtl_model {
+  HostConfig c;
+  size_t head_dim = 0, vocab = 0;
+  DevMat emb{}, out{};
+  float* out_norm = nullptr;
+  std::vector<Layer> layers;
+  int device = 0;
+  Arena arena;
+};
+
+namespace {
+
+int map_meta(GgufError e) {
+  return e == GgufError::MetadataNotFound ? DTL_ERR_MISSING_METADATA : DTL_ERR_GGUF;
+}
+
+// Repacks one GGUF tensor into the device layout of DevMat (values unchanged).
+int upload_matrix(const Gguf& g, const GgufTensor& t, size_t rows, size_t cols, Arena& arena,
+                  DevMat* out) {
+  const uint8_t* data;
+  size_t len;
+  if (g.tensor_data(t, &data, &len) != GgufError::None) return DTL_ERR_GGUF;
+  DevMat m{};
+  m.rows = (int32_t)rows;
+  m.cols = (int32_t)cols;
+  int st;
+  if (t.type == GGML_F32 || t.type == GGML_F16) {
+    std::vector<float> v(rows * cols);
+    if (t.type == GGML_F32) {
+      if (len != rows * cols * 4) return DTL_ERR_SHAPE;
+      std::memcpy(v.data(), data, len);
+      for (float f : v)
+        if (!std::isfinite(f)) return DTL_ERR_NON_FINITE;
+    } else {
+      if (len != rows * cols * 2) return DTL_ERR_SHAPE;
+      for (size_t i = 0; i < rows * cols; i++) {
+        uint16_t b = rd16(data + 2 * i);
+        if (!f16_finite(b)) return DTL_ERR_NON_FINITE;
+        v[i] = f16_to_f32_host(b);
+      }
+    }
+    m.type = GGML_F32;
+    m.nb = (int32_t)cols;
+    float* w;
+    if ((st = arena.upload(&w, v.data(), v.size()))) return st;
+    m.w = w;
+    *out = m;
+    return DTL_OK;
+  }
+  if (t.type != GGML_Q8_0 && t.type != GGML_Q4_0 && t.type != GGML_Q4_K && t.type != GGML_Q6_K)
+    return DTL_ERR_UNSUPPORTED_TENSOR_TYPE;
+  size_t bs = (t.type == GGML_Q4_K || t.type == GGML_Q6_K) ? 256 : 32;
+  if (cols % bs) return DTL_ERR_SHAPE;
+  size_t nb = cols / bs, nblk = rows * nb;
+  m.type = (int32_t)t.type;
+  m.nb = (int32_t)nb;
+  switch (t.type) {
+    case GGML_Q8_0: {
+      if (len != nblk * 34) return DTL_ERR_SHAPE;
+      std::vector<int8_t> q(nblk * 32);
+      std::vector<uint16_t> d(nblk);
+      for (size_t b = 0; b < nblk; b++) {
+        const uint8_t* p = data + b * 34;
+        d[b] = rd16(p);
+        if (!f16_finite(d[b])) return DTL_ERR_NON_FINITE;
+        std::memcpy(&q[b * 32], p + 2, 32);
+      }
+      int8_t* wq;
+      uint16_t* wd;
+      if ((st = arena.upload(&wq, q.data(), q.size()))) return st;
+      if ((st = arena.upload(&wd, d.data(), d.size()))) return st;
+      m.w = wq;
+      m.d16 = wd;
+      break;
+    }
+    case GGML_Q4_0: {
+      if (len != nblk * 18) return DTL_ERR_SHAPE;
+      std::vector<uint8_t> q(nblk * 16);
+      std::vector<uint16_t> d(nblk);
+      for (size_t b = 0; b < nblk; b++) {
+        const uint8_t* p = data + b * 18;
+        d[b] = rd16(p);
+        if (!f16_finite(d[b])) return DTL_ERR_NON_FINITE;
+        std::memcpy(&q[b * 16], p + 2, 16);
+      }
+      uint8_t* wq;
+      uint16_t* wd;
+      if ((st = arena.upload(&wq, q.data(), q.size()))) return st;
+      if ((st = arena.upload(&wd, d.data(), d.size()))) return st;
+      m.w = wq;
+      m.d16 = wd;
+      break;
+    }
+    case GGML_Q4_K: {
+      if (len != nblk * 144) return DTL_ERR_SHAPE;
+      std::vector<uint8_t> q(nblk * 128), h(nblk * 16);
+      for (size_t b = 0; b < nblk; b++) {
+        const uint8_t* p = data + b * 144;
+        if (!f16_finite(rd16(p)) || !f16_finite(rd16(p + 2))) return DTL_ERR_NON_FINITE;
+        std::memcpy(&h[b * 16], p, 16);
+        std::memcpy(&q[b * 128], p + 16, 128);
+      }
+      uint8_t *wq, *wh;
+      if ((st = arena.upload(&wq, q.data(), q.size()))) return st;
+      if ((st = arena.upload(&wh, h.data(), h.size()))) return st;
+      m.w = wq;
+      m.hdr = wh;
+      break;
+    }
+    case GGML_Q6_K: {
+      if (len != nblk * 210) return DTL_ERR_SHAPE;
+      std::vector<uint8_t> body(nblk * 208);
+      std::vector<uint16_t> d(nblk);
+      for (size_t b = 0; b < nblk; b++) {
+        const uint8_t* p = data + b * 210;
+        d[b] = rd16(p + 208);
+        if (!f16_finite(d[b])) return DTL_ERR_NON_FINITE;
+        std::memcpy(&body[b * 208], p, 208);
+      }
+      uint8_t* wb;
+      uint16_t* wd;
+      if ((st = arena.upload(&wb, body.data(), body.size()))) return st;
+      if ((st = arena.upload(&wd, d.data(), d.size()))) return st;
+      m.w = wb;
+      m.d16 = wd;
+      break;
+    }
+  }
+  *out = m;
+  return DTL_OK;
+}
+
+// read_weight_matrix (det-model lib.rs:1778-1810)
+int read_matrix(const Gguf& g, const std::string& name, size_t rows, size_t cols, Arena& arena,
+                DevMat* out) {
+  const GgufTensor* t;
+  if (g.tensor(name, &t) != GgufError::None) return DTL_ERR_GGUF;
+  if (t->dims.size() != 2 || t->dims[0] != cols || t->dims[1] != rows) return DTL_ERR_SHAPE;
+  return upload_matrix(g, *t, rows, cols, arena, out);
+}
+
+// read_f32_vector / read_dense_tensor_as_f32 (det-model lib.rs:1674-1776)
+int read_vector(const Gguf& g, const std::string& name, size_t n, Arena& arena, float** out,
+                bool optional) {
+  const GgufTensor* t;
+  GgufError e = g.tensor(name, &t);
+  if (e == GgufError::TensorNotFound && optional) {
+    *out = nullptr;
+    return DTL_OK;
+  }
+  if (e != GgufError::None) return DTL_ERR_GGUF;
+  if (t->dims.size() != 1 || t->dims[0] != n) return DTL_ERR_SHAPE;
+  const uint8_t* data;
+  size_t len;
+  if (g.tensor_data(*t, &data, &len) != GgufError::None) return DTL_ERR_GGUF;
+  std::vector<float> v(n);
+  if (t->type == GGML_F32) {
+    if (len != n * 4) return DTL_ERR_SHAPE;
+    std::memcpy(v.data(), data, len);
+    for (float f : v)
+      if (!std::isfinite(f)) return DTL_ERR_NON_FINITE;
+  } else if (t->type == GGML_F16) {
+    if (len != n * 2) return DTL_ERR_SHAPE;
+    for (size_t i = 0; i < n; i++) {
+      uint16_t b = rd16(data + 2 * i);
+      if (!f16_finite(b)) return DTL_ERR_NON_FINITE;
+      v[i] = f16_to_f32_host(b);
+    }
+  } else {
+    return DTL_ERR_UNSUPPORTED_TENSOR_TYPE;
+  }
+  return arena.upload(out, v.data(), n);
+}
+
+int opt_u32(const Gguf& g, const std::string& key, uint32_t* v, bool* present) {
+  GgufError e = g.meta_u32(key, v);
+  *present = e == GgufError::None;
+  if (e == GgufError::None || e == GgufError::MetadataNotFound) return DTL_OK;
+  return map_meta(e);
+}
+
+int opt_f32(const Gguf& g, const std::string& key, float* v, bool* present) {
+  GgufError e = g.meta_f32(key, v);
+  *present = e == GgufError::None;
+  if (e == GgufError::None || e == GgufError::MetadataNotFound) return DTL_OK;
+  return map_meta(e);
+}
+
+int opt_bool(const Gguf& g, const std::string& key, bool* v, bool* present) {
+  const GgufValue* kv = g.find(key);
+  *present = kv != nullptr;
+  if (!kv) return DTL_OK;
+  if (kv->type != GV_BOOL) return DTL_ERR_GGUF;
+  *v = kv->u != 0;
+  return DTL_OK;
+}
+
+int reject_nonzero_f32(const Gguf& g, const std::string& key) {
+  const GgufValue* kv = g.find(key);
+  if (!kv) return DTL_OK;
+  if (kv->type != GV_F32 && kv->type != GV_F64) return DTL_ERR_GGUF;
+  if (!std::isfinite(kv->f)) return DTL_ERR_SHAPE;
+  return kv->f != 0.0 ? DTL_ERR_UNSUPPORTED_MODEL_FEATURE : DTL_OK;
+}
+
+// LlamaConfig::validate (det-model lib.rs:1581-1616)
+int validate_config(const HostConfig& c) {
+  if (c.block_count == 0 || c.d == 0 || c.ff == 0 || c.heads == 0 || c.kv_heads == 0 ||
+      c.ctx == 0 || c.heads % c.kv_heads != 0 || c.rope_dim == 0 || c.rope_dim % 2 != 0 ||
+      !std::isfinite(c.eps) || c.eps <= 0.0f || !std::isfinite(c.attention_scale) ||
+      c.attention_scale <= 0.0f || !std::isfinite(c.rope_base) || c.rope_base <= 0.0f)
+    return DTL_ERR_SHAPE;
+  if (c.d % c.heads != 0 || c.rope_dim > c.d / c.heads) return DTL_ERR_SHAPE;
+  return DTL_OK;
+}
+
+// LlamaConfig::from_gguf (det-model lib.rs:1498-1565), including the
+// metadata policy that rejects unsupported model features.
+int config_from_gguf(const Gguf& g, HostConfig* c) {
+  std::string_view arch;
+  GgufError ge = g.meta_str("general.architecture", &arch);
+  if (ge != GgufError::None) return map_meta(ge);
+  if (arch != "llama" && arch != "qwen2") return DTL_ERR_UNSUPPORTED_ARCHITECTURE;
+  c->split_half = arch == "qwen2";
+  std::string p = std::string(arch) + ".";
+  uint32_t v;
+  float f;
+  bool present, b;
+  int st;
+  if ((ge = g.meta_u32(p + "attention.head_count", &v)) != GgufError::None) return map_meta(ge);
+  c->heads = v;
+  if ((st = opt_u32(g, p + "attention.head_count_kv", &v, &present))) return st;
+  c->kv_heads = present ? v : c->heads;
+  if ((ge = g.meta_u32(p + "embedding_length", &v)) != GgufError::None) return map_meta(ge);
+  c->d = v;
+  if (c->heads == 0 || c->d % c->heads != 0) return DTL_ERR_SHAPE;
+  if ((st = opt_u32(g, p + "embedding_length_out", &v, &present))) return st;
+  if (present && v != c->d) return DTL_ERR_UNSUPPORTED_MODEL_FEATURE;
+  if ((st = opt_bool(g, p + "attention.causal", &b, &present))) return st;
+  if (present && !b) return DTL_ERR_UNSUPPORTED_MODEL_FEATURE;
+  {
+    std::string_view s;
+    ge = g.meta_str(p + "rope.scaling.type", &s);
+    if (ge != GgufError::None && ge != GgufError::MetadataNotFound) return map_meta(ge);
+    if (ge == GgufError::None && s != "none") return DTL_ERR_UNSUPPORTED_ROPE_SCALING;
+  }
+  if ((st = opt_bool(g, p + "use_parallel_residual", &b, &present))) return st;
+  if (present && b) return DTL_ERR_UNSUPPORTED_MODEL_FEATURE;
+  if ((st = opt_u32(g, p + "attention.sliding_window", &v, &present))) return st;
+  if (present && v != 0) return DTL_ERR_UNSUPPORTED_MODEL_FEATURE;
+  for (const char* k : {"attention.max_alibi_bias", "attention.clamp_kqv", "attention.value_scale",
+                        "attn_logit_softcapping", "final_logit_softcapping", "logit_scale",
+                        "embedding_scale", "residual_scale"})
+    if ((st = reject_nonzero_f32(g, p + k))) return st;
+  size_t hd = c->d / c->heads;
+  for (const char* k : {"attention.key_length", "attention.value_length"}) {
+    if ((st = opt_u32(g, p + k, &v, &present))) return st;
+    if (present && v != hd) return DTL_ERR_UNSUPPORTED_ATTENTION_HEAD_LENGTH;
+  }
+  if ((st = opt_f32(g, p + "attention.scale", &f, &present))) return st;
+  c->attention_scale = present ? f : 1.0f / std::sqrt((float)hd);
+  if ((ge = g.meta_u32(p + "block_count", &v)) != GgufError::None) return map_meta(ge);
+  c->block_count = v;
+  if ((ge = g.meta_u32(p + "feed_forward_length", &v)) != GgufError::None) return map_meta(ge);
+  c->ff = v;
+  if ((ge = g.meta_f32(p + "attention.layer_norm_rms_epsilon", &f)) != GgufError::None)
+    return map_meta(ge);
+  c->eps = f;
+  if ((st = opt_f32(g, p + "rope.freq_base", &f, &present))) return st;
+  c->rope_base = present ? f : 10000.0f;
+  if ((st = opt_u32(g, p + "rope.dimension_count", &v, &present))) return st;
+  c->rope_dim = present ? v : hd;
+  if ((ge = g.meta_u32(p + "context_length", &v)) != GgufError::None) return map_meta(ge);
+  c->ctx = v;
+  return validate_config(*c);
+}
+
+// vocab_size (det-model lib.rs:1648-1672)
+int vocab_size(const Gguf& g, size_t* out) {
+  std::string_view arch;
+  GgufError ge = g.meta_str("general.architecture", &arch);
+  if (ge != GgufError::None) return map_meta(ge);
+  for (std::string key : {std::string(arch) + ".vocab_size", std::string("llama.vocab_size")}) {
+    uint32_t v;
+    ge = g.meta_u32(key, &v);
+    if (ge == GgufError::None) {
+      *out = v;
+      return DTL_OK;
+    }
+    if (ge != GgufError::MetadataNotFound) return map_meta(ge);
+  }
+  if (const GgufValue* kv = g.find("tokenizer.ggml.tokens")) {
+    if (kv->type != GV_ARRAY || kv->array_type != GV_STRING) return DTL_ERR_GGUF;
+    *out = (size_t)kv->array_len;
+    return DTL_OK;
+  }
+  const GgufTensor* t;
+  if (g.tensor("token_embd.weight", &t) != GgufError::None) return DTL_ERR_GGUF;
+  if (t->dims.size() == 2) {
+    *out = (size_t)t->dims[1];
+    return DTL_OK;
+  }
+  return DTL_ERR_MISSING_METADATA;
+}
+
+bool needs_q8a(const DevMat& m) {
+  return m.type == GGML_Q8_0 || m.type == GGML_Q4_0 || m.type == GGML_Q4_K;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// session
+
+struct dtl_session {
+  const dtl_model* m = nullptr;
+  size_t n_ctx = 0, max_chunk = 0, max_in = 0;
+  hipStream_t stream = nullptr;
+  Arena arena;
+  float *rope_cos = nullptr, *rope_sin = nullptr, *kc = nullptr, *vc = nullptr;
+  float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
+  float *g = nullptr, *u = nullptr, *ffo = nullptr, *logits = nullptr, *scores = nullptr;
+  int8_t *qa = nullptr, *qk = nullptr;
+  float *da = nullptr, *af = nullptr, *dk = nullptr;
+  uint32_t* tokens = nullptr;
+  int* err = nullptr;
+  // CDF staging
+  uint32_t *c_sym = nullptr, *c_freq = nullptr, *c_freq_tab = nullptr;
+  uint64_t *c_cum = nullptr, *c_total = nullptr, *c_values = nullptr, *c_cum_tab = nullptr;
+  size_t rows_valid = 0;  // rows of `logits` written by the last forward
+};
+
+namespace {
+
+size_t max_input_width(const dtl_model* m) {
+  size_t w = m->c.d;
+  if (m->c.ff > w) w = m->c.ff;
+  if (m->c.heads * m->head_dim > w) w = m->c.heads * m->head_dim;
+  return w;
+}
+
+int read_err(dtl_session* s, int* bits) {
+  HIP_TRY(hipMemcpyAsync(bits, s->err, sizeof(int), hipMemcpyDeviceToHost, s->stream));
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  return DTL_OK;
+}
+
+__global__ void k_clear_flag(int* p) { *p = 0; }
+
+void clear_err(dtl_session* s) { hipLaunchKernelGGL(k_clear_flag, dim3(1), dim3(1), 0, s->stream, s->err); }
+
+// Produces the activation forms the given consumers need from x[T][n].
+DevAct prepare_input(dtl_session* s, const float* x, int T, int n,
+                     std::initializer_list<const DevMat*> consumers) {
+  bool q8a = false, q8k = false;
+  for (const DevMat* m : consumers) {
+    if (needs_q8a(*m)) q8a = true;
+    if (m->type == GGML_Q6_K) q8k = true;
+  }
+  if (q8a || q8k)
+    launch_quantize(x, T, n, q8a, q8k, s->qa, s->da, s->af, s->qk, s->dk, s->err, s->stream);
+  DevAct a{};
+  a.x = x;
+  a.qa = s->qa;
+  a.da = s->da;
+  a.af = s->af;
+  a.qk = s->qk;
+  a.dk = s->dk;
+  return a;
+}
+
+// forward_one_with_workspace (det-model lib.rs:1249-1400) for T positions.
+int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t pos0) {
+  const dtl_model* m = s->m;
+  const HostConfig& c = m->c;
+  if (T <= 0 || (size_t)T > s->max_chunk || pos0 + (size_t)T > s->n_ctx) return DTL_ERR_SHAPE;
+  for (int t = 0; t < T; t++)
+    if (tokens_host[t] >= (uint32_t)m->emb.rows) return DTL_ERR_SHAPE;
+  hipStream_t st = s->stream;
+  HIP_TRY(hipSetDevice(m->device));
+  s->rows_valid = 0;
+  clear_err(s);
+  HIP_TRY(hipMemcpyAsync(s->tokens, tokens_host, T * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+  int d = (int)c.d, ff = (int)c.ff, H = (int)c.heads, KV = (int)c.kv_heads;
+  int hd = (int)m->head_dim;
+  launch_embed(m->emb, s->tokens, T, s->x, s->err, st);
+  for (size_t l = 0; l < c.block_count; l++) {
+    const Layer& L = m->layers[l];
+    launch_rmsnorm(s->x, L.attn_norm, c.eps, T, d, s->h, s->err, st);
+    DevAct a = prepare_input(s, s->h, T, d, {&L.wq, &L.wk, &L.wv});
+    launch_gemm(L.wq, a, T, s->q, L.bq, L.bq ? EPI_BIAS : EPI_STORE, s->err, st);
+    launch_gemm(L.wk, a, T, s->k, L.bk, L.bk ? EPI_BIAS : EPI_STORE, s->err, st);
+    launch_gemm(L.wv, a, T, s->v, L.bv, L.bv ? EPI_BIAS : EPI_STORE, s->err, st);
+    launch_rope_store(s->q, s->k, s->v, s->rope_cos, s->rope_sin, T, (int)pos0, H, KV, hd,
+                      (int)c.rope_dim, c.split_half, s->kc, s->vc, (int)l, (int)s->n_ctx, s->err,
+                      st);
+    launch_attention(s->q, s->kc, s->vc, (int)l, T, (int)pos0, H, KV, hd, (int)s->n_ctx,
+                     c.attention_scale, s->scores, s->attn, s->err, st);
+    a = prepare_input(s, s->attn, T, H * hd, {&L.wo});
+    launch_gemm(L.wo, a, T, s->x, nullptr, EPI_RESIDUAL, s->err, st);
+    launch_rmsnorm(s->x, L.ffn_norm, c.eps, T, d, s->h, s->err, st);
+    a = prepare_input(s, s->h, T, d, {&L.gate, &L.up});
+    launch_gemm(L.gate, a, T, s->g, nullptr, EPI_STORE, s->err, st);
+    launch_gemm(L.up, a, T, s->u, nullptr, EPI_STORE, s->err, st);
+    launch_swiglu(s->g, s->u, T * ff, s->ffo, s->err, st);
+    a = prepare_input(s, s->ffo, T, ff, {&L.down});
+    launch_gemm(L.down, a, T, s->x, nullptr, EPI_RESIDUAL, s->err, st);
+  }
+  launch_rmsnorm(s->x, m->out_norm, c.eps, T, d, s->h, s->err, st);
+  DevAct a = prepare_input(s, s->h, T, d, {&m->out});
+  launch_gemm(m->out, a, T, s->logits, nullptr, EPI_STORE, s->err, st);
+  HIP_TRY(hipGetLastError());
+  int bits = 0;
+  int rc = read_err(s, &bits);
+  if (rc) return rc;
+  if (bits & ERRBIT_NON_FINITE) return DTL_ERR_NON_FINITE;
+  s->rows_valid = (size_t)T;
+  return DTL_OK;
+}
+
+int cdf_status(int bits) {
+  if (bits & ERRBIT_CDF_NON_FINITE) return DTL_ERR_CDF_NON_FINITE_LOGIT;
+  if (bits & ERRBIT_CDF_TOTAL) return DTL_ERR_CDF_TOTAL_TOO_LARGE;
+  if (bits & ERRBIT_CDF_LOOKUP) return DTL_ERR_CDF_SYMBOL_OUT_OF_RANGE;
+  return DTL_OK;
+}
+
+constexpr size_t kMaxSymbols = 1u << 18;
+
+}  // namespace
+
+extern "C" {
+
+const char* dtl_status_string(int status) {
+  switch (status) {
+    case DTL_OK: return "ok";
+    case DTL_ERR_SHAPE: return "shape";
+    case DTL_ERR_NON_FINITE: return "non-finite";
+    case DTL_ERR_UNSUPPORTED_ARCHITECTURE: return "unsupported architecture";
+    case DTL_ERR_UNSUPPORTED_ATTENTION_HEAD_LENGTH: return "unsupported attention head length";
+    case DTL_ERR_UNSUPPORTED_MODEL_FEATURE: return "unsupported model feature";
+    case DTL_ERR_UNSUPPORTED_ROPE_SCALING: return "unsupported rope scaling";
+    case DTL_ERR_MISSING_METADATA: return "missing metadata";
+    case DTL_ERR_GGUF: return "gguf";
+    case DTL_ERR_UNSUPPORTED_TENSOR_TYPE: return "unsupported tensor type";
+    case DTL_ERR_THREAD_PANICKED: return "thread panicked";
+    case DTL_ERR_CDF_EMPTY: return "cdf: empty";
+    case DTL_ERR_CDF_MALFORMED: return "cdf: malformed";
+    case DTL_ERR_CDF_NON_FINITE_LOGIT: return "cdf: non-finite logit";
+    case DTL_ERR_CDF_SYMBOL_OUT_OF_RANGE: return "cdf: symbol out of range";
+    case DTL_ERR_CDF_TOO_MANY_SYMBOLS: return "cdf: too many symbols";
+    case DTL_ERR_CDF_TOTAL_TOO_LARGE: return "cdf: total too large";
+    case DTL_ERR_RANGE_INVALID_FREQUENCY: return "range: invalid frequency";
+    case DTL_ERR_RANGE_UNEXPECTED_EOF: return "range: unexpected eof";
+    case DTL_ERR_DEVICE: return "device error";
+    case DTL_ERR_OUT_OF_MEMORY: return "device out of memory";
+    case DTL_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case DTL_ERR_NO_DEVICE: return "no HIP device";
+    default: return "unknown status";
+  }
+}
+
+int dtl_model_load(const uint8_t* bytes, size_t len, dtl_model** out) {
+  if (!bytes || !out) return DTL_ERR_INVALID_ARGUMENT;
+  *out = nullptr;
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) return DTL_ERR_NO_DEVICE;
+  Gguf g;
+  if (g.parse(bytes, len) != GgufError::None) return DTL_ERR_GGUF;
+  std::unique_ptr<dtl_model> m(new dtl_model());
+  HIP_TRY(hipGetDevice(&m->device));
+  int st;
+  if ((st = config_from_gguf(g, &m->c))) return st;
+  const HostConfig& c = m->c;
+  m->head_dim = c.d / c.heads;
+  size_t d = c.d, ff = c.ff, hd = m->head_dim;
+  size_t vocab;
+  if ((st = vocab_size(g, &vocab))) return st;
+  if ((st = read_matrix(g, "token_embd.weight", vocab, d, m->arena, &m->emb))) return st;
+  m->layers.resize(c.block_count);
+  for (size_t l = 0; l < c.block_count; l++) {
+    Layer& L = m->layers[l];
+    std::string p = "blk." + std::to_string(l) + ".";
+    if ((st = read_vector(g, p + "attn_norm.weight", d, m->arena, &L.attn_norm, false))) return st;
+    if ((st = read_matrix(g, p + "attn_q.weight", c.heads * hd, d, m->arena, &L.wq))) return st;
+    if ((st = read_vector(g, p + "attn_q.bias", c.heads * hd, m->arena, &L.bq, true))) return st;
+    if ((st = read_matrix(g, p + "attn_k.weight", c.kv_heads * hd, d, m->arena, &L.wk))) return st;
+    if ((st = read_vector(g, p + "attn_k.bias", c.kv_heads * hd, m->arena, &L.bk, true))) return st;
+    if ((st = read_matrix(g, p + "attn_v.weight", c.kv_heads * hd, d, m->arena, &L.wv))) return st;
+    if ((st = read_vector(g, p + "attn_v.bias", c.kv_heads * hd, m->arena, &L.bv, true))) return st;
+    if ((st = read_matrix(g, p + "attn_output.weight", d, c.heads * hd, m->arena, &L.wo))) return st;
+    if ((st = read_vector(g, p + "ffn_norm.weight", d, m->arena, &L.ffn_norm, false))) return st;
+    if ((st = read_matrix(g, p + "ffn_gate.weight", ff, d, m->arena, &L.gate))) return st;
+    if ((st = read_matrix(g, p + "ffn_up.weight", ff, d, m->arena, &L.up))) return st;
+    if ((st = read_matrix(g, p + "ffn_down.weight", d, ff, m->arena, &L.down))) return st;
+  }
+  if ((st = read_vector(g, "output_norm.weight", d, m->arena, &m->out_norm, false))) return st;
+  const GgufTensor* t;
+  GgufError ge = g.tensor("output.weight", &t);
+  if (ge == GgufError::None) {
+    if ((st = read_matrix(g, "output.weight", (size_t)m->emb.rows, d, m->arena, &m->out))) return st;
+  } else if (ge == GgufError::TensorNotFound) {
+    m->out = m->emb;  // tied embeddings share the device copy
+  } else {
+    return DTL_ERR_GGUF;
+  }
+  m->vocab = (size_t)m->out.rows;
+  *out = m.release();
+  return DTL_OK;
+}
+
+void dtl_model_free(dtl_model* model) { delete model; }
+
+int dtl_model_get_config(const dtl_model* m, dtl_model_config* out) {
+  if (!m || !out) return DTL_ERR_INVALID_ARGUMENT;
+  std::memset(out, 0, sizeof *out);
+  out->block_count = m->c.block_count;
+  out->embedding_length = m->c.d;
+  out->feed_forward_length = m->c.ff;
+  out->head_count = m->c.heads;
+  out->head_count_kv = m->c.kv_heads;
+  out->head_dim = m->head_dim;
+  out->rope_dimension_count = m->c.rope_dim;
+  out->context_length = m->c.ctx;
+  out->vocab = m->vocab;
+  out->rms_epsilon = m->c.eps;
+  out->attention_scale = m->c.attention_scale;
+  out->rope_freq_base = m->c.rope_base;
+  out->rope_split_half = m->c.split_half;
+  out->embedding_type = m->emb.type;
+  out->output_type = m->out.type;
+  out->has_qkv_bias = !m->layers.empty() &&
+                      (m->layers[0].bq || m->layers[0].bk || m->layers[0].bv);
+  out->device_bytes = m->arena.bytes();
+  return DTL_OK;
+}
+
+int dtl_session_new(const dtl_model* m, size_t n_ctx, size_t max_chunk, dtl_session** out) {
+  if (!m || !out) return DTL_ERR_INVALID_ARGUMENT;
+  *out = nullptr;
+  if (n_ctx == 0 || n_ctx > m->c.ctx || max_chunk == 0) return DTL_ERR_SHAPE;
+  if (max_chunk > n_ctx) max_chunk = n_ctx;
+  HIP_TRY(hipSetDevice(m->device));
+  std::unique_ptr<dtl_session> s(new dtl_session());
+  s->m = m;
+  s->n_ctx = n_ctx;
+  s->max_chunk = max_chunk;
+  s->max_in = max_input_width(m);
+  HIP_TRY(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
+  const HostConfig& c = m->c;
+  size_t hd = m->head_dim, C = max_chunk, half = c.rope_dim / 2;
+  Arena& A = s->arena;
+  int st;
+  size_t kv = c.block_count * c.kv_heads * n_ctx * hd;
+#define ALLOC(ptr, n) \
+  if ((st = A.alloc(&s->ptr, (n)))) return st;
+  ALLOC(rope_cos, n_ctx * half);
+  ALLOC(rope_sin, n_ctx * half);
+  ALLOC(kc, kv);
+  ALLOC(vc, kv);
+  ALLOC(x, C * c.d);
+  ALLOC(h, C * c.d);
+  ALLOC(q, C * c.heads * hd);
+  ALLOC(k, C * c.kv_heads * hd);
+  ALLOC(v, C * c.kv_heads * hd);
+  ALLOC(attn, C * c.heads * hd);
+  ALLOC(g, C * c.ff);
+  ALLOC(u, C * c.ff);
+  ALLOC(ffo, C * c.ff);
+  ALLOC(logits, C * m->vocab);
+  ALLOC(scores, C * c.heads * n_ctx);
+  ALLOC(qa, C * s->max_in);
+  ALLOC(qk, C * s->max_in);
+  ALLOC(af, C * s->max_in);
+  ALLOC(da, C * (s->max_in / 32 + 1));
+  ALLOC(dk, C * (s->max_in / 256 + 1));
+  ALLOC(tokens, C);
+  ALLOC(err, 1);
+  ALLOC(c_sym, C);
+  ALLOC(c_freq, C);
+  ALLOC(c_cum, C);
+  ALLOC(c_total, C);
+  ALLOC(c_values, C);
+  ALLOC(c_freq_tab, m->vocab + 256);
+  ALLOC(c_cum_tab, m->vocab + 256);
+#undef ALLOC
+  HIP_TRY(hipMemsetAsync(s->kc, 0, kv * 4, s->stream));
+  HIP_TRY(hipMemsetAsync(s->vc, 0, kv * 4, s->stream));
+  clear_err(s.get());
+  launch_rope_table(c.rope_base, (int)c.rope_dim, (int)n_ctx, s->rope_cos, s->rope_sin, s->err,
+                    s->stream);
+  int bits = 0;
+  if ((st = read_err(s.get(), &bits))) return st;
+  if (bits) return DTL_ERR_NON_FINITE;
+  *out = s.release();
+  return DTL_OK;
+}
+
+void dtl_session_free(dtl_session* s) {
+  if (!s) return;
+  (void)hipSetDevice(s->m->device);
+  if (s->stream) {
+    (void)hipStreamSynchronize(s->stream);
+    (void)hipStreamDestroy(s->stream);
+  }
+  delete s;
+}
+
+int dtl_session_reset(dtl_session* s) {
+  if (!s) return DTL_ERR_INVALID_ARGUMENT;
+  HIP_TRY(hipSetDevice(s->m->device));
+  size_t kv = s->m->c.block_count * s->m->c.kv_heads * s->n_ctx * s->m->head_dim;
+  HIP_TRY(hipMemsetAsync(s->kc, 0, kv * 4, s->stream));
+  HIP_TRY(hipMemsetAsync(s->vc, 0, kv * 4, s->stream));
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  s->rows_valid = 0;
+  return DTL_OK;
+}
+
+int dtl_forward_chunk(dtl_session* s, const uint32_t* tokens, size_t n, size_t pos0, float* logits) {
+  if (!s || !tokens) return DTL_ERR_INVALID_ARGUMENT;
+  if (n == 0 || n > s->max_chunk) return DTL_ERR_SHAPE;
+  int st = forward_device(s, tokens, (int)n, pos0);
+  if (st) return st;
+  if (logits) {
+    HIP_TRY(hipMemcpyAsync(logits, s->logits, n * s->m->vocab * sizeof(float),
+                           hipMemcpyDeviceToHost, s->stream));
+    HIP_TRY(hipStreamSynchronize(s->stream));
+  }
+  return DTL_OK;
+}
+
+int dtl_forward_one(dtl_session* s, uint32_t token, size_t pos, float* logits) {
+  return dtl_forward_chunk(s, &token, 1, pos, logits);
+}
+
+int dtl_session_logits(dtl_session* s, size_t first, size_t n, float* out) {
+  if (!s || !out) return DTL_ERR_INVALID_ARGUMENT;
+  if (first + n > s->rows_valid) return DTL_ERR_SHAPE;
+  HIP_TRY(hipSetDevice(s->m->device));
+  HIP_TRY(hipMemcpyAsync(out, s->logits + first * s->m->vocab, n * s->m->vocab * sizeof(float),
+                         hipMemcpyDeviceToHost, s->stream));
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  return DTL_OK;
+}
+
+int dtl_logits_hash(const dtl_model* m, const uint32_t* tokens, size_t n, size_t chunk,
+                    uint8_t out[32]) {
+  if (!m || !tokens || !out) return DTL_ERR_INVALID_ARGUMENT;
+  if (n == 0 || chunk == 0 || n > m->c.ctx) return DTL_ERR_SHAPE;
+  for (size_t i = 0; i < n; i++)
+    if (tokens[i] >= (uint32_t)m->emb.rows) return DTL_ERR_SHAPE;
+  dtl_session* s;
+  size_t c = chunk < n ? chunk : n;
+  int st = dtl_session_new(m, n, c, &s);
+  if (st) return st;
+  std::vector<float> buf(c * m->vocab);
+  Sha256 sha;
+  for (size_t p = 0; p < n && !st; p += c) {
+    size_t len = n - p < c ? n - p : c;
+    st = dtl_forward_chunk(s, tokens + p, len, p, buf.data());
+    if (!st) sha.update(buf.data(), len * m->vocab * sizeof(float));
+  }
+  dtl_session_free(s);
+  if (st) return st;
+  sha.digest(out);
+  return DTL_OK;
+}
+
+// ---- det-coder on device logits -------------------------------------------
+
+int dtl_symbol_ranges(dtl_session* s, size_t first, size_t n, const uint32_t* symbols,
+                      size_t tail, uint64_t* cum, uint32_t* freq, uint64_t* total) {
+  if (!s || !symbols || !cum || !freq || !total) return DTL_ERR_INVALID_ARGUMENT;
+  size_t V = s->m->vocab;
+  if (n == 0 || first + n > s->rows_valid) return DTL_ERR_SHAPE;
+  if (V + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
+  for (size_t i = 0; i < n; i++)
+    if (symbols[i] >= V + tail) return DTL_ERR_CDF_SYMBOL_OUT_OF_RANGE;
+  HIP_TRY(hipSetDevice(s->m->device));
+  clear_err(s);
+  HIP_TRY(hipMemcpyAsync(s->c_sym, symbols, n * 4, hipMemcpyHostToDevice, s->stream));
+  launch_cdf(s->logits + first * V, (int)n, (int)V, (int)tail, 0, s->c_sym, nullptr, s->c_cum,
+             s->c_freq, s->c_total, nullptr, nullptr, nullptr, s->err, s->stream);
+  HIP_TRY(hipMemcpyAsync(cum, s->c_cum, n * 8, hipMemcpyDeviceToHost, s->stream));
+  HIP_TRY(hipMemcpyAsync(freq, s->c_freq, n * 4, hipMemcpyDeviceToHost, s->stream));
+  HIP_TRY(hipMemcpyAsync(total, s->c_total, n * 8, hipMemcpyDeviceToHost, s->stream));
+  int bits = 0, st = read_err(s, &bits);
+  return st ? st : cdf_status(bits);
+}
+
+int dtl_cdf(dtl_session* s, size_t row, size_t tail, uint32_t* freq, uint64_t* cum,
+            uint64_t* total) {
+  if (!s || !freq || !cum || !total) return DTL_ERR_INVALID_ARGUMENT;
+  size_t V = s->m->vocab;
+  if (row >= s->rows_valid) return DTL_ERR_SHAPE;
+  if (V + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
+  if (tail > 256) return DTL_ERR_INVALID_ARGUMENT;  // table staging holds vocab + 256 entries
+  HIP_TRY(hipSetDevice(s->m->device));
+  clear_err(s);
+  launch_cdf(s->logits + row * V, 1, (int)V, (int)tail, 1, nullptr, nullptr, nullptr, nullptr,
+             s->c_total, nullptr, s->c_freq_tab, s->c_cum_tab, s->err, s->stream);
+  HIP_TRY(hipMemcpyAsync(freq, s->c_freq_tab, (V + tail) * 4, hipMemcpyDeviceToHost, s->stream));
+  HIP_TRY(hipMemcpyAsync(cum, s->c_cum_tab, (V + tail) * 8, hipMemcpyDeviceToHost, s->stream));
+  HIP_TRY(hipMemcpyAsync(total, s->c_total, 8, hipMemcpyDeviceToHost, s->stream));
+  int bits = 0, st = read_err(s, &bits);
+  return st ? st : cdf_status(bits);
+}
+
+int dtl_decoder_total(dtl_session* s, size_t row, size_t tail, uint64_t* total) {
+  if (!s || !total) return DTL_ERR_INVALID_ARGUMENT;
+  size_t V = s->m->vocab;
+  if (row >= s->rows_valid) return DTL_ERR_SHAPE;
+  if (V + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
+  HIP_TRY(hipSetDevice(s->m->device));
+  clear_err(s);
+  launch_cdf(s->logits + row * V, 1, (int)V, (int)tail, 3, nullptr, nullptr, nullptr, nullptr,
+             s->c_total, nullptr, nullptr, nullptr, s->err, s->stream);
+  HIP_TRY(hipMemcpyAsync(total, s->c_total, 8, hipMemcpyDeviceToHost, s->stream));
+  int bits = 0, st = read_err(s, &bits);
+  return st ? st : cdf_status(bits);
+}
+
+int dtl_decoder_lookup(dtl_session* s, size_t row, size_t tail, uint64_t value, uint32_t* symbol,
+                       uint64_t* cum, uint32_t* freq, uint64_t* total) {
+  if (!s || !symbol || !cum || !freq || !total) return DTL_ERR_INVALID_ARGUMENT;
+  size_t V = s->m->vocab;
+  if (row >= s->rows_valid) return DTL_ERR_SHAPE;
+  if (V + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
+  HIP_TRY(hipSetDevice(s->m->device));
+  clear_err(s);
+  HIP_TRY(hipMemcpyAsync(s->c_values, &value, 8, hipMemcpyHostToDevice, s->stream));
+  launch_cdf(s->logits + row * V, 1, (int)V, (int)tail, 2, nullptr, s->c_values, s->c_cum,
+             s->c_freq, s->c_total, s->c_sym, nullptr, nullptr, s->err, s->stream);
+  HIP_TRY(hipMemcpyAsync(symbol, s->c_sym, 4, hipMemcpyDeviceToHost, s->stream));
+  HIP_TRY(hipMemcpyAsync(cum, s->c_cum, 8, hipMemcpyDeviceToHost, s->stream));
+  HIP_TRY(hipMemcpyAsync(freq, s->c_freq, 4, hipMemcpyDeviceToHost, s->stream));
+  HIP_TRY(hipMemcpyAsync(total, s->c_total, 8, hipMemcpyDeviceToHost, s->stream));
+  int bits = 0, st = read_err(s, &bits);
+  if (st) return st;
+  if (value >= *total) return DTL_ERR_CDF_SYMBOL_OUT_OF_RANGE;
+  return cdf_status(bits);
+}
+
+}  // extern "C"
+
+// ---- standalone kernels on host data -----------------------------------------
+
+namespace {
+
+// RAII scratch for the one-shot entry points.
+struct Scratch {
+  Arena arena;
+  hipStream_t stream = nullptr;
+  int* err = nullptr;
+  ~Scratch() {
+    if (stream) {
+      (void)hipStreamSynchronize(stream);
+      (void)hipStreamDestroy(stream);
+    }
+  }
+  int init() {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return DTL_ERR_NO_DEVICE;
+    HIP_TRY(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+    int st = arena.alloc(&err, 1);
+    if (st) return st;
+    HIP_TRY(hipMemsetAsync(err, 0, sizeof(int), stream));
+    return DTL_OK;
+  }
+  int finish(int* bits) {
+    HIP_TRY(hipGetLastError());
+    HIP_TRY(hipMemcpyAsync(bits, err, sizeof(int), hipMemcpyDeviceToHost, stream));
+    HIP_TRY(hipStreamSynchronize(stream));
+    return DTL_OK;
+  }
+};
+
+int run_cdf_host(const float* logits, size_t n, size_t tail, int mode, uint32_t symbol,
+                 uint64_t* cum, uint32_t* freq, uint64_t* total, uint32_t* freq_tab,
+                 uint64_t* cum_tab) {
+  if (n == 0) return DTL_ERR_CDF_EMPTY;
+  if (n + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
+  Scratch sc;
+  int st = sc.init();
+  if (st) return st;
+  float* dl;
+  uint32_t *dsym, *dfreq, *dft = nullptr;
+  uint64_t *dcum, *dtot, *dct = nullptr;
+  if ((st = sc.arena.upload(&dl, logits, n))) return st;
+  if ((st = sc.arena.upload(&dsym, &symbol, 1))) return st;
+  if ((st = sc.arena.alloc(&dfreq, 1))) return st;
+  if ((st = sc.arena.alloc(&dcum, 1))) return st;
+  if ((st = sc.arena.alloc(&dtot, 1))) return st;
+  if (mode == 1) {
+    if ((st = sc.arena.alloc(&dft, n + tail))) return st;
+    if ((st = sc.arena.alloc(&dct, n + tail))) return st;
+  }
+  launch_cdf(dl, 1, (int)n, (int)tail, mode, dsym, nullptr, dcum, dfreq, dtot, nullptr, dft, dct,
+             sc.err, sc.stream);
+  if (mode == 1) {
+    HIP_TRY(hipMemcpyAsync(freq_tab, dft, (n + tail) * 4, hipMemcpyDeviceToHost, sc.stream));
+    HIP_TRY(hipMemcpyAsync(cum_tab, dct, (n + tail) * 8, hipMemcpyDeviceToHost, sc.stream));
+  } else {
+    HIP_TRY(hipMemcpyAsync(cum, dcum, 8, hipMemcpyDeviceToHost, sc.stream));
+    HIP_TRY(hipMemcpyAsync(freq, dfreq, 4, hipMemcpyDeviceToHost, sc.stream));
+  }
+  HIP_TRY(hipMemcpyAsync(total, dtot, 8, hipMemcpyDeviceToHost, sc.stream));
+  int bits = 0;
+  if ((st = sc.finish(&bits))) return st;
+  return cdf_status(bits);
+}
+
+}  // namespace
+
+extern "C" {
+
+int dtl_logits_to_cdf(const float* logits, size_t n, size_t tail, uint32_t* freq, uint64_t* cum,
+                      uint64_t* total) {
+  if (!logits || !freq || !cum || !total) return DTL_ERR_INVALID_ARGUMENT;
+  return run_cdf_host(logits, n, tail, 1, 0, nullptr, nullptr, total, freq, cum);
+}
+
+int dtl_logits_to_symbol_range(const float* logits, size_t n, size_t symbol, size_t tail,
+                               uint64_t* cum, uint32_t* freq, uint64_t* total) {
+  if (!logits || !cum || !freq || !total) return DTL_ERR_INVALID_ARGUMENT;
+  if (n == 0) return DTL_ERR_CDF_EMPTY;
+  if (n + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
+  if (symbol >= n + tail) return DTL_ERR_CDF_SYMBOL_OUT_OF_RANGE;
+  return run_cdf_host(logits, n, tail, 0, (uint32_t)symbol, cum, freq, total, nullptr, nullptr);
+}
+
+int dtl_uniform_symbol_range(size_t symbol, size_t symbols, uint64_t* cum, uint32_t* freq,
+                             uint64_t* total) {
+  if (!cum || !freq || !total) return DTL_ERR_INVALID_ARGUMENT;
+  if (symbols == 0) return DTL_ERR_CDF_EMPTY;
+  if (symbols > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
+  if (symbol >= symbols) return DTL_ERR_CDF_SYMBOL_OUT_OF_RANGE;
+  *cum = symbol;
+  *freq = 1;
+  *total = symbols;
+  return DTL_OK;
+}
+
+int dtl_kernel_exp_f32(const float* in, float* out, size_t n) {
+  if (!in || !out) return DTL_ERR_INVALID_ARGUMENT;
+  Scratch sc;
+  int st = sc.init();
+  if (st) return st;
+  float *di, *dout;
+  if ((st = sc.arena.upload(&di, in, n))) return st;
+  if ((st = sc.arena.alloc(&dout, n))) return st;
+  launch_exp_f32(di, dout, (int)n, 0, sc.stream);
+  HIP_TRY(hipMemcpyAsync(out, dout, n * 4, hipMemcpyDeviceToHost, sc.stream));
+  int bits;
+  return sc.finish(&bits);
+}
+
+int dtl_kernel_silu_f32(const float* in, float* out, size_t n) {
+  if (!in || !out) return DTL_ERR_INVALID_ARGUMENT;
+  Scratch sc;
+  int st = sc.init();
+  if (st) return st;
+  float *di, *dout;
+  if ((st = sc.arena.upload(&di, in, n))) return st;
+  if ((st = sc.arena.alloc(&dout, n))) return st;
+  launch_exp_f32(di, dout, (int)n, 1, sc.stream);
+  HIP_TRY(hipMemcpyAsync(out, dout, n * 4, hipMemcpyDeviceToHost, sc.stream));
+  int bits;
+  return sc.finish(&bits);
+}
+
+int dtl_kernel_f16_to_f32(const uint16_t* in, float* out, size_t n) {
+  if (!in || !out) return DTL_ERR_INVALID_ARGUMENT;
+  Scratch sc;
+  int st = sc.init();
+  if (st) return st;
+  uint16_t* di;
+  float* dout;
+  if ((st = sc.arena.upload(&di, in, n))) return st;
+  if ((st = sc.arena.alloc(&dout, n))) return st;
+  launch_f16_to_f32(di, dout, (int)n, sc.stream);
+  HIP_TRY(hipMemcpyAsync(out, dout, n * 4, hipMemcpyDeviceToHost, sc.stream));
+  int bits;
+  return sc.finish(&bits);
+}
+
+int dtl_kernel_div_sqrt(const float* a, const float* b, float* quot, float* root, size_t n) {
+  if (!a || !b || !quot || !root) return DTL_ERR_INVALID_ARGUMENT;
+  Scratch sc;
+  int st = sc.init();
+  if (st) return st;
+  float *da, *db, *dq, *dr;
+  if ((st = sc.arena.upload(&da, a, n))) return st;
+  if ((st = sc.arena.upload(&db, b, n))) return st;
+  if ((st = sc.arena.alloc(&dq, n))) return st;
+  if ((st = sc.arena.alloc(&dr, n))) return st;
+  launch_div_sqrt(da, db, dq, dr, (int)n, sc.stream);
+  HIP_TRY(hipMemcpyAsync(quot, dq, n * 4, hipMemcpyDeviceToHost, sc.stream));
+  HIP_TRY(hipMemcpyAsync(root, dr, n * 4, hipMemcpyDeviceToHost, sc.stream));
+  int bits;
+  return sc.finish(&bits);
+}
+
+int dtl_kernel_quantize(const float* x, size_t rows, size_t n, float* q8a_d, int8_t* q8a_q,
+                        float* q8k_d, int8_t* q8k_q) {
+  if (!x || rows == 0 || n == 0) return DTL_ERR_INVALID_ARGUMENT;
+  bool want_a = q8a_d && q8a_q, want_k = q8k_d && q8k_q;
+  if ((want_a && n % 32) || (want_k && n % 256)) return DTL_ERR_SHAPE;
+  Scratch sc;
+  int st = sc.init();
+  if (st) return st;
+  float *dx, *da, *af, *dk;
+  int8_t *qa, *qk;
+  size_t tot = rows * n;
+  if ((st = sc.arena.upload(&dx, x, tot))) return st;
+  if ((st = sc.arena.alloc(&qa, tot))) return st;
+  if ((st = sc.arena.alloc(&qk, tot))) return st;
+  if ((st = sc.arena.alloc(&af, tot))) return st;
+  if ((st = sc.arena.alloc(&da, tot / 32 + 1))) return st;
+  if ((st = sc.arena.alloc(&dk, tot / 256 + 1))) return st;
+  launch_quantize(dx, (int)rows, (int)n, want_a, want_k, qa, da, af, qk, dk, sc.err, sc.stream);
+  if (want_a) {
+    HIP_TRY(hipMemcpyAsync(q8a_q, qa, tot, hipMemcpyDeviceToHost, sc.stream));
+    HIP_TRY(hipMemcpyAsync(q8a_d, da, tot / 32 * 4, hipMemcpyDeviceToHost, sc.stream));
+  }
+  if (want_k) {
+    HIP_TRY(hipMemcpyAsync(q8k_q, qk, tot, hipMemcpyDeviceToHost, sc.stream));
+    HIP_TRY(hipMemcpyAsync(q8k_d, dk, tot / 256 * 4, hipMemcpyDeviceToHost, sc.stream));
+  }
+  int bits = 0;
+  if ((st = sc.finish(&bits))) return st;
+  return bits ? DTL_ERR_NON_FINITE : DTL_OK;
+}
+
+int dtl_kernel_rmsnorm(const float* x, const float* w, float eps, size_t rows, size_t n,
+                       float* out) {
+  if (!x || !w || !out || rows == 0 || n == 0) return DTL_ERR_INVALID_ARGUMENT;
+  Scratch sc;
+  int st = sc.init();
+  if (st) return st;
+  float *dx, *dw, *dout;
+  if ((st = sc.arena.upload(&dx, x, rows * n))) return st;
+  if ((st = sc.arena.upload(&dw, w, n))) return st;
+  if ((st = sc.arena.alloc(&dout, rows * n))) return st;
+  launch_rmsnorm(dx, dw, eps, (int)rows, (int)n, dout, sc.err, sc.stream);
+  HIP_TRY(hipMemcpyAsync(out, dout, rows * n * 4, hipMemcpyDeviceToHost, sc.stream));
+  int bits = 0;
+  if ((st = sc.finish(&bits))) return st;
+  return bits ? DTL_ERR_NON_FINITE : DTL_OK;
+}
+
+int dtl_kernel_gemv(int ggml_type, const uint8_t* weights, size_t rows, size_t cols,
+                    const float* x, size_t T, float* out) {
+  if (!weights || !x || !out || rows == 0 || cols == 0 || T == 0) return DTL_ERR_INVALID_ARGUMENT;
+  uint64_t tb, bs;
+  if (!ggml_type_size((uint32_t)ggml_type, &tb, &bs)) return DTL_ERR_UNSUPPORTED_TENSOR_TYPE;
+  if (cols % bs) return DTL_ERR_SHAPE;
+  Scratch sc;
+  int st = sc.init();
+  if (st) return st;
+  // Wrap the bytes in a one-tensor GGUF container so the load-time repack
+  // path (upload_matrix) is the one under test.
+  size_t row_bytes = cols / bs * tb;
+  std::vector<uint8_t> file;
+  auto put = [&](const void* p, size_t k) {
+    const uint8_t* b = (const uint8_t*)p;
+    file.insert(file.end(), b, b + k);
+  };
+  uint32_t u32;
+  uint64_t u64;
+  put("GGUF", 4);
+  u32 = 3; put(&u32, 4);
+  u64 = 1; put(&u64, 8);
+  u64 = 0; put(&u64, 8);
+  u64 = 1; put(&u64, 8);
+  put("w", 1);
+  u32 = 2; put(&u32, 4);
+  u64 = cols; put(&u64, 8);
+  u64 = rows; put(&u64, 8);
+  u32 = (uint32_t)ggml_type; put(&u32, 4);
+  u64 = 0; put(&u64, 8);
+  while (file.size() % 32) file.push_back(0);
+  put(weights, rows * row_bytes);
+  Gguf g;
+  if (g.parse(file.data(), file.size()) != GgufError::None) return DTL_ERR_GGUF;
+  const GgufTensor* gt;
+  if (g.tensor("w", &gt) != GgufError::None) return DTL_ERR_GGUF;
+  DevMat W;
+  if ((st = upload_matrix(g, *gt, rows, cols, sc.arena, &W))) return st;
+  float *dx, *dout, *af, *da, *dk;
+  int8_t *qa, *qk;
+  if ((st = sc.arena.upload(&dx, x, T * cols))) return st;
+  if ((st = sc.arena.alloc(&dout, T * rows))) return st;
+  if ((st = sc.arena.alloc(&qa, T * cols))) return st;
+  if ((st = sc.arena.alloc(&qk, T * cols))) return st;
+  if ((st = sc.arena.alloc(&af, T * cols))) return st;
+  if ((st = sc.arena.alloc(&da, T * cols / 32 + 1))) return st;
+  if ((st = sc.arena.alloc(&dk, T * cols / 256 + 1))) return st;
+  bool q8a = needs_q8a(W), q8k = W.type == GGML_Q6_K;
+  if (q8a || q8k)
+    launch_quantize(dx, (int)T, (int)cols, q8a, q8k, qa, da, af, qk, dk, sc.err, sc.stream);
+  DevAct a{dx, qa, da, af, qk, dk};
+  launch_gemm(W, a, (int)T, dout, nullptr, EPI_STORE, sc.err, sc.stream);
+  HIP_TRY(hipMemcpyAsync(out, dout, T * rows * 4, hipMemcpyDeviceToHost, sc.stream));
+  int bits = 0;
+  if ((st = sc.finish(&bits))) return st;
+  return bits ? DTL_ERR_NON_FINITE : DTL_OK;
+}
+
+int dtl_kernel_rope_table(float base, size_t rope_dim, size_t positions, float* cos_out,
+                          float* sin_out) {
+  if (!cos_out || !sin_out || rope_dim == 0 || rope_dim % 2 || positions == 0)
+    return DTL_ERR_INVALID_ARGUMENT;
+  Scratch sc;
+  int st = sc.init();
+  if (st) return st;
+  size_t n = positions * rope_dim / 2;
+  float *dc, *ds;
+  if ((st = sc.arena.alloc(&dc, n))) return st;
+  if ((st = sc.arena.alloc(&ds, n))) return st;
+  launch_rope_table(base, (int)rope_dim, (int)positions, dc, ds, sc.err, sc.stream);
+  HIP_TRY(hipMemcpyAsync(cos_out, dc, n * 4, hipMemcpyDeviceToHost, sc.stream));
+  HIP_TRY(hipMemcpyAsync(sin_out, ds, n * 4, hipMemcpyDeviceToHost, sc.stream));
+  int bits = 0;
+  if ((st = sc.finish(&bits))) return st;
+  return bits ? DTL_ERR_NON_FINITE : DTL_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,87 @@
+// Device-side data layouts and kernel launchers shared by the library's
+// translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dtl {
+
+// Sticky device error bits, OR-ed into the session's flag word and read at
+// synchronisation points (the reference returns the matching error on the
+// first non-finite value it meets).
+enum : int {
+  ERRBIT_NON_FINITE = 1,         // ModelError::NonFinite
+  ERRBIT_CDF_NON_FINITE = 2,     // CdfError::NonFiniteLogit
+  ERRBIT_CDF_TOTAL = 4,          // CdfError::TotalTooLarge
+  ERRBIT_CDF_LOOKUP = 8,         // decoder value outside every symbol
+};
+
+// One weight matrix in device layout.  Values are the GGUF values exactly;
+// only the byte arrangement changes so that rows stream with wide loads:
+//   F32  : w = float[rows][cols]
+//   Q8_0 : w = int8[rows][cols],          d16 = f16[rows][cols/32]
+//   Q4_0 : w = uint8[rows][cols/32][16],  d16 = f16[rows][cols/32]
+//   Q4_K : w = uint8[rows][cols/256][128] (nibbles), hdr = uint8[rows][cols/256][16]
+//          ({f16 d, f16 dmin, u8 scales[12]})
+//   Q6_K : w = uint8[rows][cols/256][208] ({ql[128], qh[64], i8 scales[16]}),
+//          d16 = f16[rows][cols/256]
+struct DevMat {
+  int32_t type;
+  int32_t rows;
+  int32_t cols;
+  int32_t nb;  // blocks per row (32-element for Q8_0/Q4_0, 256 for K types, cols for F32)
+  const void* w;
+  const uint16_t* d16;
+  const uint8_t* hdr;
+};
+
+// Activations of T positions for one GEMM input of width cols, in every
+// form a weight type consumes (det-quant Q8A for Q8_0/Q4_0/Q4_K, Q8_K for Q6_K).
+struct DevAct {
+  const float* x;    // [T][cols] raw f32 (F32 weights)
+  const int8_t* qa;  // [T][cols]      Q8A quants
+  const float* da;   // [T][cols/32]   Q8A scales
+  const float* af;   // [T][cols]      Q8A dequantised: da * qa (Q4_K chain input)
+  const int8_t* qk;  // [T][cols]      Q8_K quants
+  const float* dk;   // [T][cols/256]  Q8_K scales
+};
+
+enum GemmEpilogue : int { EPI_STORE = 0, EPI_BIAS = 1, EPI_RESIDUAL = 2 };
+
+// ---- launchers (dtl_kernels.hip) -------------------------------------------
+void launch_embed(const DevMat& E, const uint32_t* tokens, int T, float* x, int* err,
+                  hipStream_t s);
+void launch_rmsnorm(const float* x, const float* w, float eps, int T, int n, float* out, int* err,
+                    hipStream_t s);
+// want_q8a / want_q8k select which quantisations to produce.
+void launch_quantize(const float* x, int T, int n, bool want_q8a, bool want_q8k, int8_t* qa,
+                     float* da, float* af, int8_t* qk, float* dk, int* err, hipStream_t s);
+void launch_gemm(const DevMat& W, const DevAct& A, int T, float* out, const float* bias, int epi,
+                 int* err, hipStream_t s);
+void launch_rope_store(float* q, float* k, const float* v, const float* rope_cos,
+                       const float* rope_sin, int T, int pos0, int H, int KV, int hd, int rope_dim,
+                       int split_half, float* kc, float* vc, int layer, int n_ctx, int* err,
+                       hipStream_t s);
+void launch_attention(const float* q, const float* kc, const float* vc, int layer, int T, int pos0,
+                      int H, int KV, int hd, int n_ctx, float scale, float* scores, float* out,
+                      int* err, hipStream_t s);
+void launch_swiglu(const float* g, const float* u, int count, float* out, int* err, hipStream_t s);
+void launch_rope_table(float base, int rope_dim, int positions, float* cos_out, float* sin_out,
+                       int* err, hipStream_t s);
+
+// CDF over rows of logits [R][V].
+//   mode 0: symbol range for symbols[r]        -> cum[r], freq[r], total[r]
+//   mode 1: full table for one row             -> freq_tab[V+tail], cum_tab[V+tail], total[0]
+//   mode 2: decoder lookup of values[r]        -> sym[r], cum[r], freq[r], total[r]
+//   mode 3: decoder total only                 -> total[r]
+void launch_cdf(const float* logits, int R, int V, int tail, int mode, const uint32_t* symbols,
+                const uint64_t* values, uint64_t* cum, uint32_t* freq, uint64_t* total,
+                uint32_t* sym, uint32_t* freq_tab, uint64_t* cum_tab, int* err, hipStream_t s);
+
+// Kernel-level parity entry points.
+void launch_exp_f32(const float* in, float* out, int n, int which, hipStream_t s);
+void launch_f16_to_f32(const uint16_t* in, float* out, int n, hipStream_t s);
+void launch_div_sqrt(const float* a, const float* b, float* q, float* r, int n, hipStream_t s);
+
+}  // namespace dtl

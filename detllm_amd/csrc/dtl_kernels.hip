@@ -1,0 +1,761 @@
+// gfx950 kernels for the detllm decoder forward and logits->CDF step.
+//
+// Every floating-point reduction follows the reference's fixed order:
+// one lane owns one dependent chain (a GEMV row for one position, one of
+// the 8 interleaved lanes of det-num's reductions, one P.V output element)
+// and walks it in ascending index order, while independent chains run in
+// parallel across lanes, waves and workgroups.  Integer stages (Q8_0/Q4_0
+// block sums, Q6_K lane sums, CDF prefix sums) are exact and use any order.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dtl_device.h"
+#include "dtl_numerics.h"
+
+namespace dtl {
+
+namespace {
+
+constexpr int kGgmlF32 = 0, kGgmlQ4_0 = 2, kGgmlQ8_0 = 8, kGgmlQ4K = 12, kGgmlQ6K = 14;
+
+__device__ __forceinline__ void flag(int* err, int bit) { atomicOr(err, bit); }
+
+__device__ __forceinline__ uint16_t ld_u16(const uint8_t* p) {
+  return (uint16_t)(p[0] | ((uint16_t)p[1] << 8));
+}
+
+// det-quant lib.rs:519-529: 6-bit scale and min of Q4_K sub-block `j`.
+__device__ __forceinline__ void q4k_scale_min(const uint8_t* sc, int j, int* scale, int* mn) {
+  if (j < 4) {
+    *scale = sc[j] & 0x3f;
+    *mn = sc[j + 4] & 0x3f;
+  } else {
+    *scale = (sc[j + 4] & 0x0f) | ((sc[j - 4] >> 6) << 4);
+    *mn = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+  }
+}
+
+// det-quant lib.rs:531-552: 6-bit quant of element e (0..255) of a Q6_K body.
+__device__ __forceinline__ int q6k_quant(const uint8_t* body, int e) {
+  int half = e >> 7, within = e & 127, l = within & 31, part = within >> 5;
+  uint8_t qlb = body[half * 64 + l + (part & 1) * 32];
+  int ql = (part < 2) ? (qlb & 0x0f) : (qlb >> 4);
+  int qh = (body[128 + half * 32 + l] >> (2 * part)) & 3;
+  return (ql | (qh << 4)) - 32;
+}
+
+// Scale index of element e: q6_k_scale_index (lib.rs:554-568) equals e/16.
+__device__ __forceinline__ int q6k_scale(const uint8_t* body, int e) {
+  return (int)(int8_t)body[192 + (e >> 4)];
+}
+
+// One weight value, as write_row_validated dequantises it (det-model lib.rs:667-746).
+__device__ float mat_value(const DevMat& M, int row, int i) {
+  switch (M.type) {
+    case kGgmlF32:
+      return ((const float*)M.w)[(size_t)row * M.cols + i];
+    case kGgmlQ8_0: {
+      float d = f16_to_f32(M.d16[(size_t)row * M.nb + i / 32]);
+      return d * (float)((const int8_t*)M.w)[(size_t)row * M.cols + i];
+    }
+    case kGgmlQ4_0: {
+      int b = i / 32, j = i % 32;
+      const uint8_t* qs = (const uint8_t*)M.w + ((size_t)row * M.nb + b) * 16;
+      int nib = j < 16 ? (qs[j] & 0x0f) : (qs[j - 16] >> 4);
+      float d = f16_to_f32(M.d16[(size_t)row * M.nb + b]);
+      return d * (float)(nib - 8);
+    }
+    case kGgmlQ4K: {
+      int sb = i / 256, idx = i % 256, sub = idx / 32, within = idx % 32;
+      size_t blk = (size_t)row * M.nb + sb;
+      const uint8_t* h = M.hdr + blk * 16;
+      float d = f16_to_f32(ld_u16(h)), dmin = f16_to_f32(ld_u16(h + 2));
+      int sc, mn;
+      q4k_scale_min(h + 4, sub, &sc, &mn);
+      uint8_t byte = ((const uint8_t*)M.w)[blk * 128 + (sub / 2) * 32 + within];
+      int q = (sub & 1) ? (byte >> 4) : (byte & 0x0f);
+      return (d * (float)sc) * (float)q - (dmin * (float)mn);
+    }
+    case kGgmlQ6K: {
+      int sb = i / 256, e = i % 256;
+      size_t blk = (size_t)row * M.nb + sb;
+      const uint8_t* body = (const uint8_t*)M.w + blk * 208;
+      float d = f16_to_f32(M.d16[blk]);
+      return (d * (float)q6k_scale(body, e)) * (float)q6k_quant(body, e);
+    }
+  }
+  return 0.0f;
+}
+
+// ---- row dots: one lane computes one (row, position) chain ---------------
+
+// dot_f32_ref (det-num reduce.rs:2-11)
+__device__ float row_dot_f32(const float* w, const float* x, int n) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int i = 0; i < n; i++) acc[i & 7] += w[i] * x[i];
+  return finish_8lane(acc);
+}
+
+// dot_q8_0_q8a (det-quant lib.rs:237-257): exact i32 per block, then
+// (dw*da)*isum added in block order.
+__device__ float row_dot_q8_0(const int8_t* wq, const uint16_t* wd, const int8_t* aq,
+                              const float* ad, int nb) {
+  float sum = 0.0f;
+  const int* w4 = (const int*)wq;
+  const int* a4 = (const int*)aq;
+  for (int b = 0; b < nb; b++) {
+    int isum = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) isum = __builtin_amdgcn_sdot4(w4[b * 8 + k], a4[b * 8 + k], isum, false);
+    float scale = f16_to_f32(wd[b]) * ad[b];
+    sum += scale * (float)isum;
+  }
+  return sum;
+}
+
+// dot_q4_0_q8a (lib.rs:259-279, 492-504)
+__device__ float row_dot_q4_0(const uint8_t* wq, const uint16_t* wd, const int8_t* aq,
+                              const float* ad, int nb) {
+  float sum = 0.0f;
+  for (int b = 0; b < nb; b++) {
+    const uint8_t* qs = wq + b * 16;
+    const int8_t* a = aq + b * 32;
+    int isum = 0;
+    for (int i = 0; i < 16; i++) {
+      int lo = (qs[i] & 0x0f) - 8, hi = (qs[i] >> 4) - 8;
+      isum += lo * (int)a[i];
+      isum += hi * (int)a[i + 16];
+    }
+    float scale = f16_to_f32(wd[b]) * ad[b];
+    sum += scale * (float)isum;
+  }
+  return sum;
+}
+
+// dot_q4_k_q8a (lib.rs:281-315): one sequential chain over the whole row,
+// weight = (d*sc)*q - dmin*m, activation = da*qa, sum += weight*activation.
+__device__ float row_dot_q4k(const uint8_t* qs, const uint8_t* hdr, const float* af, int nsb) {
+  float sum = 0.0f;
+  for (int sb = 0; sb < nsb; sb++) {
+    const uint8_t* h = hdr + sb * 16;
+    float d = f16_to_f32(ld_u16(h)), dmin = f16_to_f32(ld_u16(h + 2));
+    for (int sub = 0; sub < 8; sub++) {
+      int sc, mn;
+      q4k_scale_min(h + 4, sub, &sc, &mn);
+      float dsc = d * (float)sc, dm = dmin * (float)mn;
+      const uint8_t* q = qs + sb * 128 + (sub / 2) * 32;
+      const float* a = af + sb * 256 + sub * 32;
+      int shift = (sub & 1) * 4;
+      for (int w = 0; w < 32; w++) {
+        float weight = dsc * (float)((q[w] >> shift) & 0x0f) - dm;
+        sum += weight * a[w];
+      }
+    }
+  }
+  return sum;
+}
+
+// dot_q6_k_q8k (lib.rs:353-397): exact i32 lane sums (lane = index mod 8)
+// per superblock, f32 lane accumulators, sequential lane combine from 0.0.
+__device__ float row_dot_q6k(const uint8_t* body, const uint16_t* wd, const int8_t* qk,
+                             const float* dk, int nsb) {
+  float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int sb = 0; sb < nsb; sb++) {
+    const uint8_t* b = body + (size_t)sb * 208;
+    const int8_t* a = qk + sb * 256;
+    int aux[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int e = 0; e < 256; e++) aux[e & 7] += q6k_scale(b, e) * (int)a[e] * q6k_quant(b, e);
+    float d = f16_to_f32(wd[sb]) * dk[sb];
+#pragma unroll
+    for (int l = 0; l < 8; l++) sums[l] += d * (float)aux[l];
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int l = 0; l < 8; l++) sum += sums[l];
+  return sum;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// embedding: write_row_validated (det-model lib.rs:667-746)
+__global__ void k_embed(DevMat E, const uint32_t* tokens, int T, float* x, int* err) {
+  int t = blockIdx.y;
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= T || i >= E.cols) return;
+  float v = mat_value(E, (int)tokens[t], i);
+  if (!finite(v)) flag(err, ERRBIT_NON_FINITE);
+  x[(size_t)t * E.cols + i] = v;
+}
+
+void launch_embed(const DevMat& E, const uint32_t* tokens, int T, float* x, int* err,
+                  hipStream_t s) {
+  dim3 grid((E.cols + 255) / 256, T);
+  hipLaunchKernelGGL(k_embed, grid, dim3(256), 0, s, E, tokens, T, x, err);
+}
+
+// ---------------------------------------------------------------------------
+// rmsnorm (det-model lib.rs:2053-2073): ss by 8 interleaved chains, r =
+// 1/sqrt(ss/n + eps), out = (x*r)*w.  One workgroup per position.
+__global__ void __launch_bounds__(256) k_rmsnorm(const float* x, const float* w, float eps, int n,
+                                                 float* out, int* err) {
+  __shared__ float lane_sum[8];
+  __shared__ float r_sh;
+  int t = blockIdx.x;
+  const float* xr = x + (size_t)t * n;
+  float* o = out + (size_t)t * n;
+  bool bad = false;
+  for (int i = threadIdx.x; i < n; i += blockDim.x)
+    if (!finite(xr[i]) || !finite(w[i])) bad = true;
+  if (threadIdx.x < 8) {
+    float acc = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 8) acc += xr[i] * xr[i];
+    lane_sum[threadIdx.x] = acc;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float ss = finish_8lane(lane_sum);
+    float m = ss / (float)n;
+    float r = 1.0f / sqrtf(m + eps);
+    if (!finite(r)) bad = true;
+    r_sh = r;
+  }
+  __syncthreads();
+  float r = r_sh;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    float v = (xr[i] * r) * w[i];
+    if (!finite(v)) bad = true;
+    o[i] = v;
+  }
+  if (bad) flag(err, ERRBIT_NON_FINITE);
+}
+
+void launch_rmsnorm(const float* x, const float* w, float eps, int T, int n, float* out, int* err,
+                    hipStream_t s) {
+  hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(256), 0, s, x, w, eps, n, out, err);
+}
+
+// ---------------------------------------------------------------------------
+// Activation quantisation: Q8A (det-quant lib.rs:111-137) per 32-element
+// block and Q8_K (lib.rs:139-172) per 256-element block.  One workgroup of
+// 256 threads per 256 elements of one position.
+__global__ void __launch_bounds__(256) k_quantize(const float* x, int n, int want_q8a,
+                                                  int want_q8k, int8_t* qa, float* da, float* af,
+                                                  int8_t* qk, float* dk, int* err) {
+  int t = blockIdx.y;
+  int e = blockIdx.x * 256 + threadIdx.x;
+  bool in = e < n;
+  float v = in ? x[(size_t)t * n + e] : 0.0f;
+  if (in && !finite(v)) flag(err, ERRBIT_NON_FINITE);
+  float ax = v < 0.0f ? -v : v;
+  if (want_q8a) {
+    // amax over the 32-lane group (max is order independent).
+    float amax = ax;
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+    if (in) {
+      size_t off = (size_t)t * n + e;
+      if (amax == 0.0f) {
+        qa[off] = 0;
+        af[off] = 0.0f;
+        if ((e & 31) == 0) da[off / 32] = 0.0f;
+      } else {
+        float d = amax / 127.0f;
+        float y = v / d;
+        int r = y < 0.0f ? f32_as_i32(y - 0.5f) : f32_as_i32(y + 0.5f);
+        r = r < -127 ? -127 : (r > 127 ? 127 : r);
+        qa[off] = (int8_t)r;
+        af[off] = d * (float)r;
+        if ((e & 31) == 0) da[off / 32] = d;
+      }
+    }
+  }
+  if (want_q8k) {
+    // Signed max: the first element with the strictly largest |x|.  Reduce
+    // (|x|, index) taking the larger |x| and, on ties, the smaller index.
+    __shared__ float s_ax[4];
+    __shared__ int s_idx[4];
+    __shared__ float s_max;
+    float bx = in ? ax : -1.0f;
+    int bi = threadIdx.x;
+    for (int m = 32; m >= 1; m >>= 1) {
+      float ox = __shfl_xor(bx, m);
+      int oi = __shfl_xor(bi, m);
+      if (ox > bx || (ox == bx && oi < bi)) {
+        bx = ox;
+        bi = oi;
+      }
+    }
+    int wave = threadIdx.x / 64;
+    if ((threadIdx.x & 63) == 0) {
+      s_ax[wave] = bx;
+      s_idx[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float cx = s_ax[0];
+      int ci = s_idx[0];
+      for (int w = 1; w < 4; w++)
+        if (s_ax[w] > cx || (s_ax[w] == cx && s_idx[w] < ci)) {
+          cx = s_ax[w];
+          ci = s_idx[w];
+        }
+      s_max = cx == 0.0f ? 0.0f : x[(size_t)t * n + blockIdx.x * 256 + ci];
+    }
+    __syncthreads();
+    float mx = s_max;
+    if (in) {
+      size_t off = (size_t)t * n + e;
+      if (mx == 0.0f) {
+        qk[off] = 0;
+        if (threadIdx.x == 0) dk[off / 256] = 0.0f;
+      } else {
+        float iscale = -127.0f / mx;
+        float val = iscale * v + 12582912.0f;
+        int r = (int)(f2u(val) & 0x007fffffu) - 0x00400000;
+        if (r > 127) r = 127;
+        qk[off] = (int8_t)r;
+        if (threadIdx.x == 0) dk[off / 256] = 1.0f / iscale;
+      }
+    }
+  }
+}
+
+void launch_quantize(const float* x, int T, int n, bool want_q8a, bool want_q8k, int8_t* qa,
+                     float* da, float* af, int8_t* qk, float* dk, int* err, hipStream_t s) {
+  dim3 grid((n + 255) / 256, T);
+  hipLaunchKernelGGL(k_quantize, grid, dim3(256), 0, s, x, n, (int)want_q8a, (int)want_q8k, qa, da,
+                     af, qk, dk, err);
+}
+
+// ---------------------------------------------------------------------------
+// GEMM: out[t][r] = row r . activation t, one lane per (r, t), with the
+// bias add (add_optional_bias, lib.rs:1982-1998) or residual add
+// (residual_add, lib.rs:1967-1980) applied to the finished dot.
+__global__ void __launch_bounds__(256) k_gemm_rowlane(DevMat W, DevAct A, int T, float* out,
+                                                      const float* bias, int epi, int* err) {
+  int r = blockIdx.x * blockDim.x + threadIdx.x;
+  int t = blockIdx.y;
+  if (r >= W.rows || t >= T) return;
+  float v;
+  switch (W.type) {
+    case kGgmlF32:
+      v = row_dot_f32((const float*)W.w + (size_t)r * W.cols, A.x + (size_t)t * W.cols, W.cols);
+      break;
+    case kGgmlQ8_0:
+      v = row_dot_q8_0((const int8_t*)W.w + (size_t)r * W.cols, W.d16 + (size_t)r * W.nb,
+                       A.qa + (size_t)t * W.cols, A.da + (size_t)t * (W.cols / 32), W.nb);
+      break;
+    case kGgmlQ4_0:
+      v = row_dot_q4_0((const uint8_t*)W.w + (size_t)r * W.nb * 16, W.d16 + (size_t)r * W.nb,
+                       A.qa + (size_t)t * W.cols, A.da + (size_t)t * (W.cols / 32), W.nb);
+      break;
+    case kGgmlQ4K:
+      v = row_dot_q4k((const uint8_t*)W.w + (size_t)r * W.nb * 128, W.hdr + (size_t)r * W.nb * 16,
+                      A.af + (size_t)t * W.cols, W.nb);
+      break;
+    default:
+      v = row_dot_q6k((const uint8_t*)W.w + (size_t)r * W.nb * 208, W.d16 + (size_t)r * W.nb,
+                      A.qk + (size_t)t * W.cols, A.dk + (size_t)t * (W.cols / 256), W.nb);
+      break;
+  }
+  bool bad = !finite(v);
+  size_t o = (size_t)t * W.rows + r;
+  if (epi == EPI_BIAS) {
+    v = v + bias[r];
+  } else if (epi == EPI_RESIDUAL) {
+    v = out[o] + v;
+  }
+  if (bad || !finite(v)) flag(err, ERRBIT_NON_FINITE);
+  out[o] = v;
+}
+
+void launch_gemm(const DevMat& W, const DevAct& A, int T, float* out, const float* bias, int epi,
+                 int* err, hipStream_t s) {
+  dim3 grid((W.rows + 255) / 256, T);
+  hipLaunchKernelGGL(k_gemm_rowlane, grid, dim3(256), 0, s, W, A, T, out, bias, epi, err);
+}
+
+// ---------------------------------------------------------------------------
+// apply_rope on q and k (det-model lib.rs:2011-2051) and KvCache::store
+// (lib.rs:883-920).  One workgroup per position.
+__global__ void __launch_bounds__(256) k_rope_store(float* q, float* k, const float* v,
+                                                    const float* rc, const float* rs, int pos0,
+                                                    int H, int KV, int hd, int rope_dim,
+                                                    int split_half, float* kc, float* vc,
+                                                    int layer, int n_ctx, int* err) {
+  int t = blockIdx.x;
+  int pos = pos0 + t;
+  int half = rope_dim / 2;
+  bool bad = false;
+  float* qt = q + (size_t)t * H * hd;
+  float* kt = k + (size_t)t * KV * hd;
+  const float* vt = v + (size_t)t * KV * hd;
+  const float* ct = rc + (size_t)pos * half;
+  const float* st = rs + (size_t)pos * half;
+  for (int i = threadIdx.x; i < H * hd; i += blockDim.x)
+    if (!finite(qt[i])) bad = true;
+  for (int i = threadIdx.x; i < KV * hd; i += blockDim.x)
+    if (!finite(kt[i])) bad = true;
+  __syncthreads();
+  for (int p = threadIdx.x; p < (H + KV) * half; p += blockDim.x) {
+    int head = p / half, j = p % half;
+    float* base = head < H ? qt + head * hd : kt + (head - H) * hd;
+    int a = split_half ? j : 2 * j;
+    int b = split_half ? j + half : 2 * j + 1;
+    float x0 = base[a], x1 = base[b];
+    float c = ct[j], s = st[j];
+    float y0 = x0 * c - x1 * s;
+    float y1 = x0 * s + x1 * c;
+    if (!finite(y0) || !finite(y1)) bad = true;
+    base[a] = y0;
+    base[b] = y1;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < KV * hd; i += blockDim.x) {
+    int kvh = i / hd, dd = i % hd;
+    size_t off = (((size_t)layer * KV + kvh) * n_ctx + pos) * hd + dd;
+    float kv = kt[i], vv = vt[i];
+    if (!finite(kv) || !finite(vv)) bad = true;
+    kc[off] = kv;
+    vc[off] = vv;
+  }
+  if (bad) flag(err, ERRBIT_NON_FINITE);
+}
+
+void launch_rope_store(float* q, float* k, const float* v, const float* rope_cos,
+                       const float* rope_sin, int T, int pos0, int H, int KV, int hd, int rope_dim,
+                       int split_half, float* kc, float* vc, int layer, int n_ctx, int* err,
+                       hipStream_t s) {
+  hipLaunchKernelGGL(k_rope_store, dim3(T), dim3(256), 0, s, q, k, v, rope_cos, rope_sin, pos0, H,
+                     KV, hd, rope_dim, split_half, kc, vc, layer, n_ctx, err);
+}
+
+// ---------------------------------------------------------------------------
+// attention_one_head (det-model lib.rs:2300-2418) for every (head, position)
+// of the chunk: causal over cache positions 0..pos.  One wave per pair.
+__global__ void __launch_bounds__(64) k_attention(const float* q, const float* kc, const float* vc,
+                                                  int layer, int pos0, int H, int KV, int hd,
+                                                  int n_ctx, float scale, float* scores,
+                                                  float* out, int* err) {
+  int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+  int pos = pos0 + t, len = pos + 1;
+  int kvh = h / (H / KV);
+  const float* keys = kc + ((size_t)layer * KV + kvh) * n_ctx * hd;
+  const float* vals = vc + ((size_t)layer * KV + kvh) * n_ctx * hd;
+  float* o = out + (size_t)t * H * hd + (size_t)h * hd;
+  if (len == 1) {  // a single score copies V exactly (lib.rs:2319-2321)
+    for (int dd = lane; dd < hd; dd += 64) o[dd] = vals[dd];
+    return;
+  }
+  const float* qh = q + (size_t)t * H * hd + (size_t)h * hd;
+  float* sc = scores + ((size_t)t * H + h) * n_ctx;
+  bool bad = false;
+  // scores: dot_f32_ref(q, k_j) * scale
+  float mx = -__builtin_huge_valf();
+  for (int j = lane; j < len; j += 64) {
+    const float* kj = keys + (size_t)j * hd;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int i = 0; i < hd; i++) acc[i & 7] += qh[i] * kj[i];
+    float s = finish_8lane(acc) * scale;
+    if (!finite(s)) bad = true;
+    sc[j] = s;
+    mx = fmaxf(mx, s);
+  }
+  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  for (int j = lane; j < len; j += 64) sc[j] = exp_clamped(sc[j] - mx);
+  __syncthreads();
+  // Z = sum_f32_ref(e): lane c < 8 walks chain c in ascending order.
+  float acc = 0.0f;
+  if (lane < 8)
+    for (int j = lane; j < len; j += 8) acc += sc[j];
+  float part[8];
+#pragma unroll
+  for (int c = 0; c < 8; c++) part[c] = __shfl(acc, c);
+  float z = finish_8lane(part);
+  if (!finite(z) || z == 0.0f) bad = true;
+  __syncthreads();
+  for (int j = lane; j < len; j += 64) {
+    float p = sc[j] / z;
+    if (!finite(p)) bad = true;
+    sc[j] = p;
+  }
+  __syncthreads();
+  // P.V: out[d] = 0.0; out[d] += p_j * v_j[d] for j ascending.
+  for (int dd = lane; dd < hd; dd += 64) {
+    float a = 0.0f;
+    for (int j = 0; j < len; j++) a += sc[j] * vals[(size_t)j * hd + dd];
+    if (!finite(a)) bad = true;
+    o[dd] = a;
+  }
+  if (bad) flag(err, ERRBIT_NON_FINITE);
+}
+
+void launch_attention(const float* q, const float* kc, const float* vc, int layer, int T, int pos0,
+                      int H, int KV, int hd, int n_ctx, float scale, float* scores, float* out,
+                      int* err, hipStream_t s) {
+  hipLaunchKernelGGL(k_attention, dim3(H, T), dim3(64), 0, s, q, kc, vc, layer, pos0, H, KV, hd,
+                     n_ctx, scale, scores, out, err);
+}
+
+// ---------------------------------------------------------------------------
+// swiglu (det-model lib.rs:2420-2434)
+__global__ void k_swiglu(const float* g, const float* u, int count, float* out, int* err) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  float gv = g[i], uv = u[i];
+  float v = silu_det(gv) * uv;
+  if (!finite(gv) || !finite(uv) || !finite(v)) flag(err, ERRBIT_NON_FINITE);
+  out[i] = v;
+}
+
+void launch_swiglu(const float* g, const float* u, int count, float* out, int* err, hipStream_t s) {
+  hipLaunchKernelGGL(k_swiglu, dim3((count + 255) / 256), dim3(256), 0, s, g, u, count, out, err);
+}
+
+// ---------------------------------------------------------------------------
+// RopeTables::llama (det-model lib.rs:813-847) in f64 on the device.
+__global__ void k_rope_table(float base, int rope_dim, int positions, float* co, float* so,
+                             int* err) {
+  int half = rope_dim / 2;
+  int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= positions * half) return;
+  int pos = idx / half, j = idx % half;
+  double ln_base = log64((double)base);
+  double exponent = -((double)(2 * j)) / (double)rope_dim;
+  double omega = exp64(exponent * ln_base);
+  double phi = (double)pos * omega;
+  float c = (float)cos64(phi);
+  float s = (float)sin64(phi);
+  if (!finite(c) || !finite(s)) flag(err, ERRBIT_NON_FINITE);
+  co[idx] = c;
+  so[idx] = s;
+}
+
+void launch_rope_table(float base, int rope_dim, int positions, float* cos_out, float* sin_out,
+                       int* err, hipStream_t s) {
+  int n = positions * (rope_dim / 2);
+  hipLaunchKernelGGL(k_rope_table, dim3((n + 255) / 256), dim3(256), 0, s, base, rope_dim,
+                     positions, cos_out, sin_out, err);
+}
+
+// ---------------------------------------------------------------------------
+// logits -> integer CDF (det-coder cdf.rs).  One workgroup of 256 threads
+// per row.  max -> e_i = exp_f32(max(l_i - m, -88)) -> Z by the 8-lane sum
+// (8 chains over LDS tiles) -> f_i = (u32)(e_i/Z * 2^24) + 1 -> exact
+// integer sums / scans.
+namespace {
+constexpr int kCdfThreads = 256;
+constexpr int kCdfTile = kCdfThreads * 8;
+
+__device__ __forceinline__ uint32_t cdf_freq(float e, float z) {
+  float p = e / z;
+  float g = p * 16777216.0f;
+  uint32_t gi = g <= 0.0f ? 0u : (g >= 4294967296.0f ? 0xffffffffu : (uint32_t)g);
+  return gi + 1u;
+}
+
+// Block-wide inclusive scan of one u64 per thread (256 threads).
+__device__ uint64_t block_scan_u64(uint64_t v, uint64_t* sh, uint64_t* total) {
+  int tid = threadIdx.x;
+  sh[tid] = v;
+  __syncthreads();
+  for (int off = 1; off < kCdfThreads; off <<= 1) {
+    uint64_t add = tid >= off ? sh[tid - off] : 0;
+    __syncthreads();
+    sh[tid] += add;
+    __syncthreads();
+  }
+  uint64_t incl = sh[tid];
+  *total = sh[kCdfThreads - 1];
+  __syncthreads();
+  return incl;
+}
+}  // namespace
+
+__global__ void __launch_bounds__(256) k_cdf(const float* logits, int V, int tail, int mode,
+                                             const uint32_t* symbols, const uint64_t* values,
+                                             uint64_t* cum, uint32_t* freq, uint64_t* total,
+                                             uint32_t* sym, uint32_t* freq_tab, uint64_t* cum_tab,
+                                             int* err) {
+  __shared__ float tile[kCdfTile];
+  __shared__ float chain[8];
+  __shared__ float red[kCdfThreads / 64];
+  __shared__ uint64_t scan[kCdfThreads];
+  int r = blockIdx.x, tid = threadIdx.x;
+  const float* l = logits + (size_t)r * V;
+  // max (order independent) + finiteness
+  float mx = -__builtin_huge_valf();
+  bool bad = false;
+  for (int i = tid; i < V; i += kCdfThreads) {
+    float v = l[i];
+    if (!finite(v)) bad = true;
+    mx = fmaxf(mx, v);
+  }
+  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  if ((tid & 63) == 0) red[tid / 64] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  if (bad) flag(err, ERRBIT_CDF_NON_FINITE);
+  // Z: chain c (thread c < 8) adds e_i for i = c mod 8 ascending, tile by tile.
+  float acc = 0.0f;
+  for (int base = 0; base < V; base += kCdfTile) {
+    __syncthreads();
+    for (int k = tid; k < kCdfTile; k += kCdfThreads) {
+      int i = base + k;
+      tile[k] = i < V ? exp_clamped(l[i] - mx) : 0.0f;
+    }
+    __syncthreads();
+    if (tid < 8) {
+      int lim = V - base < kCdfTile ? V - base : kCdfTile;
+      for (int k = tid; k < lim; k += 8) acc += tile[k];
+    }
+  }
+  if (tid < 8) chain[tid] = acc;
+  __syncthreads();
+  float z = finish_8lane(chain);
+  // Integer pass: each thread owns 8 consecutive entries of a tile.
+  uint64_t target = 0, run = 0;
+  uint32_t want_sym = 0;
+  if (mode == 0) want_sym = symbols[r];
+  if (mode == 2) target = values[r];
+  uint64_t found_cum = 0;
+  uint32_t found_freq = 0, found_sym = 0;
+  bool found = false;
+  uint64_t below = 0;  // mode 0: sum of f_i for i < symbol (this thread's share)
+  for (int base = 0; base < V; base += kCdfTile) {
+    uint32_t f[8];
+    uint64_t local = 0;
+    int i0 = base + tid * 8;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      int i = i0 + k;
+      f[k] = i < V ? cdf_freq(exp_clamped(l[i] - mx), z) : 0u;
+      local += f[k];
+    }
+    if (mode == 0) {
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        int i = i0 + k;
+        if (i < V && (uint32_t)i < want_sym) below += f[k];
+        if (i < V && (uint32_t)i == want_sym) {
+          found = true;
+          found_freq = f[k];
+        }
+      }
+      uint64_t tot;
+      block_scan_u64(local, scan, &tot);
+      run += tot;
+    } else {
+      uint64_t tot;
+      uint64_t incl = block_scan_u64(local, scan, &tot);
+      uint64_t c = run + incl - local;
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        int i = i0 + k;
+        if (i < V) {
+          if (mode == 1) {
+            freq_tab[i] = f[k];
+            cum_tab[i] = c;
+          } else if (mode == 2 && !found && target >= c && target < c + f[k]) {
+            found = true;
+            found_sym = (uint32_t)i;
+            found_cum = c;
+            found_freq = f[k];
+          }
+          c += f[k];
+        }
+      }
+      run += tot;
+    }
+  }
+  // run = sum of all f_i over the vocabulary
+  uint64_t tot_all = run + (uint64_t)tail;
+  if (run >= (1ull << 31) || tot_all >= (1ull << 31)) {
+    if (tid == 0) flag(err, ERRBIT_CDF_TOTAL);
+  }
+  if (mode == 0) {
+    uint64_t tot;
+    uint64_t incl = block_scan_u64(below, scan, &tot);
+    (void)incl;
+    if (found) {
+      cum[r] = tot;
+      freq[r] = found_freq;
+    }
+    if (tid == 0) {
+      if (want_sym >= (uint32_t)V) {
+        cum[r] = run + (want_sym - (uint32_t)V);
+        freq[r] = 1;
+      }
+      total[r] = tot_all;
+    }
+  } else if (mode == 1) {
+    for (int k = tid; k < tail; k += kCdfThreads) {
+      freq_tab[V + k] = 1;
+      cum_tab[V + k] = run + (uint64_t)k;
+    }
+    if (tid == 0) total[0] = tot_all;
+  } else if (mode == 2) {
+    if (found) {
+      sym[r] = found_sym;
+      cum[r] = found_cum;
+      freq[r] = found_freq;
+    }
+    if (tid == 0) {
+      total[r] = tot_all;
+      if (target >= run) {
+        uint64_t off = target - run;
+        if (off < (uint64_t)tail) {
+          sym[r] = (uint32_t)(V + off);
+          cum[r] = target;
+          freq[r] = 1;
+        } else {
+          flag(err, ERRBIT_CDF_LOOKUP);
+        }
+      }
+    }
+  } else {
+    if (tid == 0) total[r] = tot_all;
+  }
+}
+
+void launch_cdf(const float* logits, int R, int V, int tail, int mode, const uint32_t* symbols,
+                const uint64_t* values, uint64_t* cum, uint32_t* freq, uint64_t* total,
+                uint32_t* sym, uint32_t* freq_tab, uint64_t* cum_tab, int* err, hipStream_t s) {
+  hipLaunchKernelGGL(k_cdf, dim3(R), dim3(kCdfThreads), 0, s, logits, V, tail, mode, symbols,
+                     values, cum, freq, total, sym, freq_tab, cum_tab, err);
+}
+
+// ---------------------------------------------------------------------------
+// parity entry points
+__global__ void k_exp(const float* in, float* out, int n, int which) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[i] = which == 0 ? expf_det(in[i]) : silu_det(in[i]);
+}
+
+void launch_exp_f32(const float* in, float* out, int n, int which, hipStream_t s) {
+  hipLaunchKernelGGL(k_exp, dim3((n + 255) / 256), dim3(256), 0, s, in, out, n, which);
+}
+
+__global__ void k_f16(const uint16_t* in, float* out, int n) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = f16_to_f32(in[i]);
+}
+
+void launch_f16_to_f32(const uint16_t* in, float* out, int n, hipStream_t s) {
+  hipLaunchKernelGGL(k_f16, dim3((n + 255) / 256), dim3(256), 0, s, in, out, n);
+}
+
+__global__ void k_div_sqrt(const float* a, const float* b, float* q, float* r, int n) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  q[i] = a[i] / b[i];
+  r[i] = sqrtf(a[i]);
+}
+
+void launch_div_sqrt(const float* a, const float* b, float* q, float* r, int n, hipStream_t s) {
+  hipLaunchKernelGGL(k_div_sqrt, dim3((n + 255) / 256), dim3(256), 0, s, a, b, q, r, n);
+}
+
+}  // namespace dtl

@@ -1,0 +1,380 @@
+// Device numerics for gfx950: bit-exact restatements of the detllm CPU
+// arithmetic.  Every routine uses only IEEE-754 operations that the device
+// rounds exactly like the host (add, sub, mul, correctly rounded div and
+// sqrt, conversions); the translation units are compiled with
+// -ffp-contract=off so no multiply-add is ever fused.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dtl {
+
+__device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
+__device__ __forceinline__ double u2d(uint64_t u) { return __longlong_as_double((long long)u); }
+__device__ __forceinline__ uint64_t d2u(double d) { return (uint64_t)__double_as_longlong(d); }
+
+__device__ __forceinline__ bool finite(float x) { return (f2u(x) & 0x7f800000u) != 0x7f800000u; }
+
+// Rust `f32 as i32`: truncation toward zero, saturating, NaN -> 0.
+__device__ __forceinline__ int32_t f32_as_i32(float x) {
+  if (x != x) return 0;
+  if (x >= 2147483648.0f) return INT32_MAX;
+  if (x < -2147483648.0f) return INT32_MIN;
+  return (int32_t)x;
+}
+
+// f16 bits -> f32 by integer construction (det-num f16.rs:6-34); exact for
+// every input including subnormals, independent of the hardware f16 mode.
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1fu;
+  uint32_t frac = h & 0x3ffu;
+  uint32_t out;
+  if (exp == 0) {
+    if (frac == 0) {
+      out = sign;
+    } else {
+      // Normalise: move the leading one of frac up to bit 10.
+      int lead = 31 - __clz(frac);          // 0..9
+      int shift = 10 - lead;
+      uint32_t f = (frac << shift) & 0x3ffu;
+      out = sign | ((uint32_t)(127 - 14 - shift) << 23) | (f << 13);
+    }
+  } else if (exp == 0x1f) {
+    out = sign | 0x7f800000u | (frac << 13);
+  } else {
+    out = sign | ((exp + 112u) << 23) | (frac << 13);
+  }
+  return u2f(out);
+}
+
+// 8-lane finishing tree (det-num reduce.rs:36-38).
+__device__ __forceinline__ float finish_8lane(const float a[8]) {
+  return ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+}
+
+// scalbnf with the two-step range handling of det-num vendored_libm.rs:94-119.
+__device__ __forceinline__ float scalbnf(float x, int n) {
+  const float x1p127 = u2f(0x7f000000u);
+  const float x1p_126 = u2f(0x00800000u);
+  if (n > 127) {
+    x *= x1p127;
+    n -= 127;
+    if (n > 127) {
+      x *= x1p127;
+      n -= 127;
+      if (n > 127) n = 127;
+    }
+  } else if (n < -126) {
+    x *= x1p_126;
+    n += 126;
+    if (n < -126) {
+      x *= x1p_126;
+      n += 126;
+      if (n < -126) n = -126;
+    }
+  }
+  return x * u2f((uint32_t)(0x7f + n) << 23);
+}
+
+// exp_f32 (det-num math.rs:5-7): the FreeBSD e_expf method restated from
+// its published description -- round x/ln2 to k, reduce with a two-part
+// ln2, approximate with x*c/(2-c), c = x - x^2(P1 + x^2 P2), scale by 2^k.
+__device__ __forceinline__ float expf_det(float x) {
+  const float ln2_hi = u2f(0x3f317200u);
+  const float ln2_lo = u2f(0x35bfbe8eu);
+  const float inv_ln2 = u2f(0x3fb8aa3bu);
+  const float p1 = u2f(0x3e2aaa8fu);
+  const float p2 = u2f(0xbb355215u);
+  uint32_t hx = f2u(x);
+  int sign = (int)(hx >> 31);
+  hx &= 0x7fffffffu;
+  if (hx >= 0x42aeac50u) {
+    if (hx > 0x7f800000u) return x;
+    if (hx >= 0x42b17218u && !sign) return x * u2f(0x7f000000u);
+    if (sign && hx >= 0x42cff1b5u) return 0.0f;
+  }
+  int k;
+  float hi, lo;
+  if (hx > 0x3eb17218u) {
+    if (hx > 0x3f851592u) {
+      k = f32_as_i32(inv_ln2 * x + (sign ? -0.5f : 0.5f));
+    } else {
+      k = 1 - sign - sign;
+    }
+    float kf = (float)k;
+    hi = x - kf * ln2_hi;
+    lo = kf * ln2_lo;
+    x = hi - lo;
+  } else if (hx > 0x39000000u) {
+    k = 0;
+    hi = x;
+    lo = 0.0f;
+  } else {
+    return 1.0f + x;
+  }
+  float xx = x * x;
+  float c = x - xx * (p1 + xx * p2);
+  float y = 1.0f + (x * c / (2.0f - c) - lo + hi);
+  return k == 0 ? y : scalbnf(y, k);
+}
+
+// silu_f32 (det-num math.rs:30-34).
+__device__ __forceinline__ float silu_det(float x) {
+  float t = expf_det(-x);
+  float d = 1.0f + t;
+  return x / d;
+}
+
+// exp clamped at -88, as used by softmax (det-model lib.rs:2375) and the
+// CDF (det-coder cdf.rs:291).
+__device__ __forceinline__ float exp_clamped(float t) { return expf_det(t < -88.0f ? -88.0f : t); }
+
+// ---- f64 transcendentals for RoPE tables (det-num vendored_libm) --------
+// fdlibm methods: e_exp.c, e_log.c, k_sin.c, k_cos.c and the Cody-Waite
+// branch of e_rem_pio2.c.
+
+__device__ inline double scalbn64(double x, int n) {
+  const double x1p1023 = u2d(0x7fe0000000000000ull);
+  const double x1p_1022 = u2d(0x0010000000000000ull);
+  if (n > 1023) {
+    x *= x1p1023;
+    n -= 1023;
+    if (n > 1023) {
+      x *= x1p1023;
+      n -= 1023;
+      if (n > 1023) n = 1023;
+    }
+  } else if (n < -1022) {
+    x *= x1p_1022;
+    n += 1022;
+    if (n < -1022) {
+      x *= x1p_1022;
+      n += 1022;
+      if (n < -1022) n = -1022;
+    }
+  }
+  return x * u2d((uint64_t)(0x3ff + n) << 52);
+}
+
+__device__ inline int32_t f64_as_i32(double x) {
+  if (x != x) return 0;
+  if (x >= 2147483648.0) return INT32_MAX;
+  if (x <= -2147483649.0) return INT32_MIN;
+  return (int32_t)x;
+}
+
+__device__ inline double exp64(double x) {
+  const double ln2hi = u2d(0x3fe62e42fee00000ull);
+  const double ln2lo = u2d(0x3dea39ef35793c76ull);
+  const double invln2 = u2d(0x3ff71547652b82feull);
+  const double P1 = u2d(0x3fc555555555553eull);
+  const double P2 = u2d(0xbf66c16c16bebd93ull);
+  const double P3 = u2d(0x3f11566aaf25de2cull);
+  const double P4 = u2d(0xbebbbd41c5d26bf1ull);
+  const double P5 = u2d(0x3e66376972bea4d0ull);
+  uint32_t hx = (uint32_t)(d2u(x) >> 32);
+  int sign = (int)(hx >> 31);
+  hx &= 0x7fffffffu;
+  if (hx >= 0x4086232bu) {
+    if (x != x) return x;
+    if (x > 709.782712893383973096) return x * u2d(0x7fe0000000000000ull);
+    if (x < -745.13321910194110842) return 0.0;
+  }
+  int k;
+  double hi, lo;
+  if (hx > 0x3fd62e42u) {
+    if (hx >= 0x3ff0a2b2u) {
+      k = f64_as_i32(invln2 * x + (sign ? -0.5 : 0.5));
+    } else {
+      k = 1 - sign - sign;
+    }
+    hi = x - (double)k * ln2hi;
+    lo = (double)k * ln2lo;
+    x = hi - lo;
+  } else if (hx > 0x3e300000u) {
+    k = 0;
+    hi = x;
+    lo = 0.0;
+  } else {
+    return 1.0 + x;
+  }
+  double xx = x * x;
+  double c = x - xx * (P1 + xx * (P2 + xx * (P3 + xx * (P4 + xx * P5))));
+  double y = 1.0 + (x * c / (2.0 - c) - lo + hi);
+  return k == 0 ? y : scalbn64(y, k);
+}
+
+__device__ inline double log64(double x) {
+  const double ln2_hi = u2d(0x3fe62e42fee00000ull);
+  const double ln2_lo = u2d(0x3dea39ef35793c76ull);
+  const double Lg1 = u2d(0x3fe5555555555593ull), Lg2 = u2d(0x3fd999999997fa04ull);
+  const double Lg3 = u2d(0x3fd2492494229359ull), Lg4 = u2d(0x3fcc71c51d8e78afull);
+  const double Lg5 = u2d(0x3fc7466496cb03deull), Lg6 = u2d(0x3fc39a09d078c69full);
+  const double Lg7 = u2d(0x3fc2f112df3e5244ull);
+  uint64_t ui = d2u(x);
+  uint32_t hx = (uint32_t)(ui >> 32);
+  int k = 0;
+  if (hx < 0x00100000u || (hx >> 31) != 0) {
+    if ((ui << 1) == 0) return -1.0 / (x * x);
+    if (hx >> 31) return (x - x) / 0.0;
+    k -= 54;
+    x *= u2d(0x4350000000000000ull);
+    ui = d2u(x);
+    hx = (uint32_t)(ui >> 32);
+  } else if (hx >= 0x7ff00000u) {
+    return x;
+  } else if (hx == 0x3ff00000u && (ui << 32) == 0) {
+    return 0.0;
+  }
+  hx += 0x3ff00000u - 0x3fe6a09eu;
+  k += (int)(hx >> 20) - 0x3ff;
+  hx = (hx & 0x000fffffu) + 0x3fe6a09eu;
+  ui = ((uint64_t)hx << 32) | (ui & 0xffffffffull);
+  x = u2d(ui);
+  double f = x - 1.0;
+  double hfsq = 0.5 * f * f;
+  double s = f / (2.0 + f);
+  double z = s * s;
+  double w = z * z;
+  double t1 = w * (Lg2 + w * (Lg4 + w * Lg6));
+  double t2 = z * (Lg1 + w * (Lg3 + w * (Lg5 + w * Lg7)));
+  double r = t2 + t1;
+  double dk = (double)k;
+  return s * (hfsq + r) + dk * ln2_lo - hfsq + f + dk * ln2_hi;
+}
+
+__device__ inline double ksin64(double x, double y, int iy) {
+  const double S1 = u2d(0xbfc5555555555549ull), S2 = u2d(0x3f8111111110f8a6ull);
+  const double S3 = u2d(0xbf2a01a019c161d5ull), S4 = u2d(0x3ec71de357b1fe7dull);
+  const double S5 = u2d(0xbe5ae5e68a2b9cebull), S6 = u2d(0x3de5d93a5acfd57cull);
+  double z = x * x;
+  double w = z * z;
+  double r = S2 + z * (S3 + z * S4) + z * w * (S5 + z * S6);
+  double v = z * x;
+  if (iy == 0) return x + v * (S1 + z * r);
+  return x - ((z * (0.5 * y - v * r) - y) - v * S1);
+}
+
+__device__ inline double kcos64(double x, double y) {
+  const double C1 = u2d(0x3fa555555555554cull), C2 = u2d(0xbf56c16c16c15177ull);
+  const double C3 = u2d(0x3efa01a019cb1590ull), C4 = u2d(0xbe927e4f809c52adull);
+  const double C5 = u2d(0x3e21ee9ebdb4b1c4ull), C6 = u2d(0xbda8fae9be8838d4ull);
+  double z = x * x;
+  double w = z * z;
+  double r = z * (C1 + z * (C2 + z * C3)) + w * w * (C4 + z * (C5 + z * C6));
+  double hz = 0.5 * z;
+  double ww = 1.0 - hz;
+  return ww + (((1.0 - ww) - hz) + (z * r - x * y));
+}
+
+// Argument reduction by pi/2 for |x| < 2^20*pi/2; returns n, y0 + y1 = x - n*pi/2.
+// Larger arguments (beyond every supported RoPE phase) yield NaN.
+__device__ inline int rem_pio2(double x, double* y0o, double* y1o) {
+  const double TO_INT = 1.5 / 2.2204460492503131e-16;
+  const double INV_PIO2 = u2d(0x3fe45f306dc9c883ull);
+  const double PIO2_1 = u2d(0x3ff921fb54400000ull), PIO2_1T = u2d(0x3dd0b4611a626331ull);
+  const double PIO2_2 = u2d(0x3dd0b4611a600000ull), PIO2_2T = u2d(0x3ba3198a2e037073ull);
+  const double PIO2_3 = u2d(0x3ba3198a2e000000ull), PIO2_3T = u2d(0x397b839a252049c1ull);
+  int sign = (int)(d2u(x) >> 63);
+  uint32_t ix = (uint32_t)(d2u(x) >> 32) & 0x7fffffffu;
+  bool medium = false;
+  int mult = 0;
+  if (ix <= 0x400f6a7au) {
+    if ((ix & 0xfffffu) == 0x921fbu) medium = true;
+    else mult = ix <= 0x4002d97cu ? 1 : 2;
+  } else if (ix <= 0x401c463bu) {
+    if (ix <= 0x4015fdbcu) {
+      if (ix == 0x4012d97cu) medium = true;
+      else mult = 3;
+    } else {
+      if (ix == 0x401921fbu) medium = true;
+      else mult = 4;
+    }
+  } else if (ix < 0x413921fbu) {
+    medium = true;
+  } else {
+    *y0o = __longlong_as_double(0x7ff8000000000000ll);
+    *y1o = *y0o;
+    return 0;
+  }
+  if (!medium) {
+    double m = (double)mult;
+    if (sign == 0) {
+      double z = x - m * PIO2_1;
+      double y0 = z - m * PIO2_1T;
+      *y0o = y0;
+      *y1o = (z - y0) - m * PIO2_1T;
+      return mult;
+    }
+    double z = x + m * PIO2_1;
+    double y0 = z + m * PIO2_1T;
+    *y0o = y0;
+    *y1o = (z - y0) + m * PIO2_1T;
+    return -mult;
+  }
+  double tmp = x * INV_PIO2 + TO_INT;
+  double f_n = tmp - TO_INT;
+  int n = f64_as_i32(f_n);
+  double r = x - f_n * PIO2_1;
+  double w = f_n * PIO2_1T;
+  double y0 = r - w;
+  int ey = (int)(d2u(y0) >> 52) & 0x7ff;
+  int ex = (int)(ix >> 20);
+  if (ex - ey > 16) {
+    double t = r;
+    w = f_n * PIO2_2;
+    r = t - w;
+    w = f_n * PIO2_2T - ((t - r) - w);
+    y0 = r - w;
+    ey = (int)(d2u(y0) >> 52) & 0x7ff;
+    if (ex - ey > 49) {
+      t = r;
+      w = f_n * PIO2_3;
+      r = t - w;
+      w = f_n * PIO2_3T - ((t - r) - w);
+      y0 = r - w;
+    }
+  }
+  *y0o = y0;
+  *y1o = (r - y0) - w;
+  return n;
+}
+
+__device__ inline double sin64(double x) {
+  uint32_t ix = (uint32_t)(d2u(x) >> 32) & 0x7fffffffu;
+  if (ix <= 0x3fe921fbu) {
+    if (ix < 0x3e500000u) return x;
+    return ksin64(x, 0.0, 0);
+  }
+  if (ix >= 0x7ff00000u) return x - x;
+  double y0, y1;
+  int n = rem_pio2(x, &y0, &y1);
+  switch (n & 3) {
+    case 0: return ksin64(y0, y1, 1);
+    case 1: return kcos64(y0, y1);
+    case 2: return -ksin64(y0, y1, 1);
+    default: return -kcos64(y0, y1);
+  }
+}
+
+__device__ inline double cos64(double x) {
+  uint32_t ix = (uint32_t)(d2u(x) >> 32) & 0x7fffffffu;
+  if (ix <= 0x3fe921fbu) {
+    if (ix < 0x3e46a09eu && f64_as_i32(x) == 0) return 1.0;
+    return kcos64(x, 0.0);
+  }
+  if (ix >= 0x7ff00000u) return x - x;
+  double y0, y1;
+  int n = rem_pio2(x, &y0, &y1);
+  switch (n & 3) {
+    case 0: return kcos64(y0, y1);
+    case 1: return -ksin64(y0, y1, 1);
+    case 2: return -kcos64(y0, y1);
+    default: return ksin64(y0, y1, 1);
+  }
+}
+
+}  // namespace dtl

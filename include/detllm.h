@@ -1,0 +1,203 @@
+/*
+ * detllm_amd — MI355X (gfx950) implementation of detllm's per-token decoder
+ * forward pass and logits -> integer-CDF step, behind a C ABI.
+ *
+ * Every entry point replaces one item of the reference Rust API of
+ * mii443/detllm (crates/det-model, crates/det-coder); the comment above each
+ * declaration names it (file:line).  Results are bit-identical to the
+ * reference CPU arithmetic: logits, CDF frequencies and range-coder bytes.
+ *
+ * Conventions
+ *   - Every function returns a dtl_status (0 = OK).  No exceptions or
+ *     unwinding cross this boundary.
+ *   - Host pointers only; the library owns all device memory.
+ *   - A dtl_model is immutable after load and may be shared by sessions on
+ *     any host thread.  A dtl_session is single-threaded: it owns one HIP
+ *     stream, a KV cache, RoPE tables and a workspace for up to max_chunk
+ *     positions (the reference's KvCache + ForwardWorkspace + RopeTables).
+ */
+#ifndef DETLLM_H
+#define DETLLM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  1-10 mirror det-model ModelError (lib.rs:48-59),
+ * 20-25 det-coder CdfError (cdf.rs:9-17), 30-31 RangeError (range.rs:4-8). */
+typedef enum {
+    DTL_OK = 0,
+    DTL_ERR_SHAPE = 1,
+    DTL_ERR_NON_FINITE = 2,
+    DTL_ERR_UNSUPPORTED_ARCHITECTURE = 3,
+    DTL_ERR_UNSUPPORTED_ATTENTION_HEAD_LENGTH = 4,
+    DTL_ERR_UNSUPPORTED_MODEL_FEATURE = 5,
+    DTL_ERR_UNSUPPORTED_ROPE_SCALING = 6,
+    DTL_ERR_MISSING_METADATA = 7,
+    DTL_ERR_GGUF = 8,
+    DTL_ERR_UNSUPPORTED_TENSOR_TYPE = 9,
+    DTL_ERR_THREAD_PANICKED = 10,
+    DTL_ERR_CDF_EMPTY = 20,
+    DTL_ERR_CDF_MALFORMED = 21,
+    DTL_ERR_CDF_NON_FINITE_LOGIT = 22,
+    DTL_ERR_CDF_SYMBOL_OUT_OF_RANGE = 23,
+    DTL_ERR_CDF_TOO_MANY_SYMBOLS = 24,
+    DTL_ERR_CDF_TOTAL_TOO_LARGE = 25,
+    DTL_ERR_RANGE_INVALID_FREQUENCY = 30,
+    DTL_ERR_RANGE_UNEXPECTED_EOF = 31,
+    /* No reference counterpart: device / argument failures of this library. */
+    DTL_ERR_DEVICE = 40,
+    DTL_ERR_OUT_OF_MEMORY = 41,
+    DTL_ERR_INVALID_ARGUMENT = 42,
+    DTL_ERR_NO_DEVICE = 43
+} dtl_status;
+
+typedef struct dtl_model dtl_model;
+typedef struct dtl_session dtl_session;
+
+/* LlamaConfig (crates/det-model/src/lib.rs:27-39) plus the output vocab. */
+typedef struct {
+    uint64_t block_count;
+    uint64_t embedding_length;
+    uint64_t feed_forward_length;
+    uint64_t head_count;
+    uint64_t head_count_kv;
+    uint64_t head_dim;
+    uint64_t rope_dimension_count;
+    uint64_t context_length;
+    uint64_t vocab;               /* output.rows() */
+    float rms_epsilon;
+    float attention_scale;
+    float rope_freq_base;
+    int32_t rope_split_half;      /* RopePairing: 0 Adjacent (llama), 1 SplitHalf (qwen2) */
+    int32_t embedding_type;       /* ggml type id of token_embd */
+    int32_t output_type;          /* ggml type id of output (or tied embedding) */
+    int32_t has_qkv_bias;
+    uint64_t device_bytes;        /* device memory held by the weights */
+} dtl_model_config;
+
+/* Human-readable name of a status code (static storage). */
+const char *dtl_status_string(int status);
+
+/* ---- det-model --------------------------------------------------------- */
+
+/* F32Llama::from_gguf (det-model lib.rs:1035-1140) with det_gguf::parse
+ * (det-gguf lib.rs:156-216).  The caller keeps ownership of the bytes; the
+ * weights are validated, repacked and copied to the current HIP device. */
+int dtl_model_load(const uint8_t *gguf, size_t len, dtl_model **out);
+void dtl_model_free(dtl_model *model);
+/* F32Llama::config + output.rows() (det-model lib.rs:27-39, 1178-1187). */
+int dtl_model_get_config(const dtl_model *model, dtl_model_config *out);
+
+/* F32Llama::forward_workspace + KvCache::new + RopeTables::llama
+ * (det-model lib.rs:1244, 850, 813).  n_ctx <= context_length positions of
+ * RoPE table and KV cache; max_chunk = most positions one dtl_forward_chunk
+ * call may carry (1 for pure decode). */
+int dtl_session_new(const dtl_model *model, size_t n_ctx, size_t max_chunk, dtl_session **out);
+void dtl_session_free(dtl_session *session);
+/* A fresh KvCache for window replay (det-cli main.rs:691-701). */
+int dtl_session_reset(dtl_session *session);
+
+/* F32Llama::forward_one_with_workspace (det-model lib.rs:1249-1400).
+ * logits: vocab floats on the host, or NULL to keep them on the device
+ * (they then feed dtl_symbol_ranges / dtl_decoder_lookup). */
+int dtl_forward_one(dtl_session *session, uint32_t token, size_t pos, float *logits);
+
+/* n consecutive forward_one_with_workspace calls at positions pos0..pos0+n-1
+ * as one batched device pass (teacher-forced encode).  Bit-identical to n
+ * single-token calls.  logits: n*vocab host floats or NULL. */
+int dtl_forward_chunk(dtl_session *session, const uint32_t *tokens, size_t n, size_t pos0,
+                      float *logits);
+
+/* Copies rows [first, first+n) of the last forward's logits to the host. */
+int dtl_session_logits(dtl_session *session, size_t first, size_t n, float *out);
+
+/* F32Llama::logits_hash_for_tokens_chunked (det-model lib.rs:1406-1465):
+ * SHA-256 of every position's f32 logits (little-endian bits), positions
+ * ascending.  chunk sets how many positions share one device pass. */
+int dtl_logits_hash(const dtl_model *model, const uint32_t *tokens, size_t n, size_t chunk,
+                    uint8_t out[32]);
+
+/* ---- det-coder on device-resident logits -------------------------------- */
+
+/* logits_to_symbol_range_with_scratch / _with_byte_escapes
+ * (det-coder cdf.rs:123-199) for rows [first, first+n) of the session's
+ * last logits: symbols[i] is coded against row first+i.  tail_symbols is 0
+ * or 256 (BYTE_ESCAPE_SYMBOLS). */
+int dtl_symbol_ranges(dtl_session *session, size_t first, size_t n, const uint32_t *symbols,
+                      size_t tail_symbols, uint64_t *cum, uint32_t *freq, uint64_t *total);
+
+/* logits_to_cdf_with_scratch / _with_byte_escapes (cdf.rs:52-106): the
+ * full table for one row; freq and cum hold vocab + tail_symbols entries. */
+int dtl_cdf(dtl_session *session, size_t row, size_t tail_symbols, uint32_t *freq, uint64_t *cum,
+            uint64_t *total);
+
+/* logits_to_decoder_distribution_* + DecoderDistribution::total
+ * (cdf.rs:108-121, 201-245, 387-390). */
+int dtl_decoder_total(dtl_session *session, size_t row, size_t tail_symbols, uint64_t *total);
+
+/* DecoderDistribution::symbol_range (cdf.rs:392-425), run on the device. */
+int dtl_decoder_lookup(dtl_session *session, size_t row, size_t tail_symbols, uint64_t value,
+                       uint32_t *symbol, uint64_t *cum, uint32_t *freq, uint64_t *total);
+
+/* logits_to_cdf / logits_to_symbol_range on caller logits (host memory):
+ * uploads them and runs the same device kernels (cdf.rs:47-199). */
+int dtl_logits_to_cdf(const float *logits, size_t n, size_t tail_symbols, uint32_t *freq,
+                      uint64_t *cum, uint64_t *total);
+int dtl_logits_to_symbol_range(const float *logits, size_t n, size_t symbol, size_t tail_symbols,
+                               uint64_t *cum, uint32_t *freq, uint64_t *total);
+
+/* uniform_symbol_range (cdf.rs:322-341). */
+int dtl_uniform_symbol_range(size_t symbol, size_t symbols, uint64_t *cum, uint32_t *freq,
+                             uint64_t *total);
+
+/* ---- det-coder range coder (host) --------------------------------------- */
+typedef struct dtl_range_encoder dtl_range_encoder;
+typedef struct dtl_range_decoder dtl_range_decoder;
+
+/* RangeEncoder::{new, encode, finish} (det-coder range.rs:30-92). */
+int dtl_range_encoder_new(dtl_range_encoder **out);
+int dtl_range_encode(dtl_range_encoder *enc, uint64_t cum, uint64_t freq, uint64_t total);
+/* Appends the 8 flush bytes and copies min(len, cap) bytes; *len = full size.
+ * The encoder stays usable (finish does not consume it). */
+int dtl_range_encoder_finish(dtl_range_encoder *enc, uint8_t *out, size_t cap, size_t *len);
+void dtl_range_encoder_free(dtl_range_encoder *enc);
+
+/* RangeDecoder::{new, decode_freq, advance} (det-coder range.rs:94-159). */
+int dtl_range_decoder_new(const uint8_t *data, size_t len, dtl_range_decoder **out);
+int dtl_range_decode_freq(dtl_range_decoder *dec, uint64_t total, uint64_t *value);
+int dtl_range_decode_advance(dtl_range_decoder *dec, uint64_t cum, uint64_t freq, uint64_t total);
+void dtl_range_decoder_free(dtl_range_decoder *dec);
+
+/* ---- det-num / det-quant kernels, exposed for parity checks ------------- */
+
+/* exp_f32 (det-num math.rs:5-7) over n values on the device. */
+int dtl_kernel_exp_f32(const float *in, float *out, size_t n);
+/* silu_f32 (math.rs:30-34). */
+int dtl_kernel_silu_f32(const float *in, float *out, size_t n);
+/* f16 -> f32 (det-num f16.rs:6-34) on the device. */
+int dtl_kernel_f16_to_f32(const uint16_t *in, float *out, size_t n);
+/* sqrt and division as used by rmsnorm / softmax / quantisers. */
+int dtl_kernel_div_sqrt(const float *a, const float *b, float *quot, float *root, size_t n);
+/* quantize_q8a_into / quantize_q8k_into (det-quant lib.rs:67-105) over rows
+ * of length n: d[rows*n/32] q[rows*n] (Q8A), d[rows*n/256] q[rows*n] (Q8_K). */
+int dtl_kernel_quantize(const float *x, size_t rows, size_t n, float *q8a_d, int8_t *q8a_q,
+                        float *q8k_d, int8_t *q8k_q);
+/* rmsnorm (det-model lib.rs:2053-2073) of rows x[rows][n]. */
+int dtl_kernel_rmsnorm(const float *x, const float *w, float eps, size_t rows, size_t n, float *out);
+/* One weight matrix in GGUF encoding (ggml type 0/1/2/8/12/14, rows x cols)
+ * against x[T][cols]: out[T][rows] exactly as WeightMatrix::gemv
+ * (det-model lib.rs:445-490) computes each token's row dots. */
+int dtl_kernel_gemv(int ggml_type, const uint8_t *weights, size_t rows, size_t cols,
+                    const float *x, size_t T, float *out);
+/* RopeTables::llama (det-model lib.rs:813-847) computed on the device. */
+int dtl_kernel_rope_table(float rope_freq_base, size_t rope_dim, size_t positions, float *cos_out,
+                          float *sin_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -229,7 +229,7 @@ size_t ref_range_encoder_finish(ref_range_encoder *e, uint8_t *out, size_t cap) 
         low <<= 8;
     }
     size_t n = e->len;
-    memcpy(out, e->out, n < cap ? n : cap);
+    if (out && cap) memcpy(out, e->out, n < cap ? n : cap);
     e->len = base;
     return n;
 }

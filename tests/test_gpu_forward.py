@@ -1,0 +1,136 @@
+"""Full decoder forward on the GPU: logits bit-identical to the reference.
+
+The tiny-f32 / tiny-qmix fixtures are checked against the reference's own
+committed SHA-256 values; the BASELINE-shaped synthetic models against the
+oracle at full width (a few positions, truncated depth where noted) and
+through size-independent properties (chunk invariance, repeatability).
+"""
+import numpy as np
+import pytest
+
+import detref
+from conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+
+def _model(data):
+    from detllm_amd.model import F32Llama
+
+    return F32Llama.from_gguf(data)
+
+
+def _fixture_tokens():
+    return [int(t) for t in (GOLDEN / "tiny.tokens.txt").read_text().strip().split(",")]
+
+
+@pytest.mark.parametrize("name", ["tiny-f32", "tiny-qmix"])
+@pytest.mark.parametrize("chunk", [1, 2, 3, 6])
+def test_fixture_hash_matches_reference_golden(name, chunk):
+    m = _model((GOLDEN / f"{name}.gguf").read_bytes())
+    want = (GOLDEN / f"{name}.logits.sha256").read_text().strip()
+    assert m.logits_hash_for_tokens_chunked(_fixture_tokens(), chunk).hex() == want
+
+
+def _compare_with_oracle(data, tokens, chunk):
+    m = _model(data)
+    ref = detref.Model(data).logits(tokens)
+    got = []
+    m.visit_logits_for_tokens_chunked(tokens, chunk, lambda row: got.append(row.copy()))
+    got = np.stack(got)
+    assert got.shape == ref.shape
+    bad = np.nonzero(got.view(np.uint32) != ref.view(np.uint32))
+    assert bad[0].size == 0, f"first mismatch at position {bad[0][:1]}, index {bad[1][:1]}"
+    return m, got
+
+
+def test_tiny_workload_matches_oracle_all_chunks():
+    from detllm_amd import synth
+
+    w = synth.WORKLOADS["tiny"]
+    data = synth.build_model(w)
+    toks = synth.tokens(w)
+    m, got = _compare_with_oracle(data, toks, w.chunk)
+    ref_hash = detref.Model(data).logits_hash(toks)
+    for chunk in (1, 2, 3, 8):
+        assert m.logits_hash_for_tokens_chunked(toks, chunk) == ref_hash
+
+
+@pytest.mark.parametrize("name,layers,n_tok,chunk", [
+    ("smollm2", 4, 5, 2),
+    ("qwen05", 3, 5, 3),
+    ("tinyllama", 2, 4, 4),
+])
+def test_baseline_shapes_match_oracle(name, layers, n_tok, chunk):
+    from detllm_amd import synth
+
+    w = synth.WORKLOADS[name]
+    data = synth.build_model(w, layers=layers)
+    _compare_with_oracle(data, synth.tokens(w, n_tok), chunk)
+
+
+def test_repeat_runs_are_bitwise_identical():
+    from detllm_amd import synth
+
+    w = synth.WORKLOADS["smollm2"]
+    m = _model(synth.build_model(w, layers=2))
+    toks = synth.tokens(w, 16)
+    hashes = {m.logits_hash_for_tokens_chunked(toks, c) for c in (1, 5, 16, 16)}
+    assert len(hashes) == 1
+
+
+def test_session_errors_mirror_reference_shape_checks():
+    from detllm_amd._lib import DetllmError
+
+    m = _model((GOLDEN / "tiny-f32.gguf").read_bytes())
+    with m.forward_workspace(4, 2) as s:
+        with pytest.raises(DetllmError) as e:
+            s.forward_chunk([0, 1, 2], 0)  # more positions than max_chunk
+        assert e.value.status == 1
+        with pytest.raises(DetllmError) as e:
+            s.forward_one(10_000, 0)      # token outside the vocabulary
+        assert e.value.status == 1
+        with pytest.raises(DetllmError) as e:
+            s.forward_one(0, 4)           # position outside the window
+        assert e.value.status == 1
+
+
+def test_cdf_on_device_logits_matches_oracle():
+    from detllm_amd import synth
+
+    w = synth.WORKLOADS["smollm2"]
+    data = synth.build_model(w, layers=2)
+    m = _model(data)
+    toks = synth.tokens(w, 6)
+    with m.forward_workspace(8, 6) as s:
+        logits = s.forward_chunk(toks, 0, want_logits=True)
+        syms = [int(t) for t in synth.tokens(w, 7)[1:7]]
+        for tail in (0, 256):
+            cum, freq, total = s.symbol_ranges(syms, 0, tail)
+            for i in range(6):
+                assert (int(cum[i]), int(freq[i]), int(total[i])) == detref.symbol_range(logits[i], syms[i], tail)
+            f, c, t = s.cdf(2, tail)
+            rf, rc, rt = detref.logits_to_cdf(logits[2], tail)
+            assert np.array_equal(f, rf) and np.array_equal(c, rc) and t == rt
+            for value in (0, int(rc[100]), int(rc[100]) + int(rf[100]) - 1, rt - 1):
+                assert s.decoder_lookup(value, 2, tail) == detref.decoder_lookup(logits[2], value, tail)
+            assert s.decoder_total(2, tail) == rt
+
+
+@pytest.mark.parametrize("V", [4, 256, 32000, 151936])
+def test_standalone_cdf_kernel_matches_oracle(V):
+    from detllm_amd import coder
+
+    rng = np.random.default_rng(V)
+    lg = rng.normal(0, 4, V).astype(np.float32)
+    if V == 4:
+        lg[:] = 0.0
+    else:
+        lg[:11] = [0.0, -1.0, 3.25, 3.25, -88.5, np.float32(2 ** -149), -12.0, 0.5, -0.25, 2.0, -1000.0]
+    for tail in (0, 256):
+        got = coder._cdf(lg, tail)
+        rf, rc, rt = detref.logits_to_cdf(lg, tail)
+        assert np.array_equal(got.freq, rf) and np.array_equal(got.cum, rc) and got.total == rt
+        for s in (0, V // 2, V - 1, V + tail - 1):
+            r = coder._range(lg, s, tail)
+            assert (r.cum, r.freq, r.total) == detref.symbol_range(lg, s, tail)

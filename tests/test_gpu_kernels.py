@@ -1,0 +1,167 @@
+"""Kernel-level parity of the HIP implementation against the oracle (bit-exact)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import detref
+import qblocks
+
+pytestmark = pytest.mark.gpu
+
+
+def _lib():
+    from detllm_amd import _lib
+
+    return _lib
+
+
+def _p(a, t):
+    return a.ctypes.data_as(C.POINTER(t))
+
+
+def gpu_exp(x, which="exp"):
+    L = _lib()
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    fn = L.lib.dtl_kernel_exp_f32 if which == "exp" else L.lib.dtl_kernel_silu_f32
+    L.check(fn(_p(x, C.c_float), _p(out, C.c_float), x.size), which)
+    return out
+
+
+def test_exp_f32_bitexact_sweep():
+    rng = np.random.default_rng(0)
+    # every f32 in [-1, 0] spaced by 64 ulps, a dense band near the clamp,
+    # random values over the whole range and the special cases
+    a = np.arange(0xBF800000, 0x80000000, -64, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    b = np.linspace(-104.0, 89.0, 400000, dtype=np.float32)
+    c = rng.uniform(-120, 100, 200000).astype(np.float32)
+    special = np.array([0.0, -0.0, -88.0, -87.33655, -88.72284, 88.72284, 88.7229, -103.972084,
+                        -103.97209, 1e-30, -1e-30, np.float32(2 ** -149), 0.3465735, -0.3465735,
+                        1.0397208, -1.0397208, np.inf, -np.inf], np.float32)
+    x = np.concatenate([a, b, c, special])
+    got = gpu_exp(x)
+    want = detref.exp_f32(x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_silu_bitexact():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.normal(0, 4, 100000), rng.uniform(-100, 100, 50000)]).astype(np.float32)
+    got = gpu_exp(x, "silu")
+    f = detref.lib().ref_silu_f32
+    want = np.array([f(float(v)) for v in x], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_f16_to_f32_exhaustive():
+    L = _lib()
+    codes = np.arange(65536, dtype=np.uint16)
+    out = np.empty(65536, np.float32)
+    L.check(L.lib.dtl_kernel_f16_to_f32(_p(codes, C.c_uint16), _p(out, C.c_float), 65536), "f16")
+    f = detref.lib().ref_f16_to_f32
+    # The oracle returns through a C double, which quiets signalling NaNs, so
+    # NaN codes are checked against numpy's bit-level half -> single widening.
+    nan = np.isnan(codes.view(np.float16))
+    want = np.array([f(int(c)) for c in codes], np.float32)
+    assert np.array_equal(out[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    want_nan = codes[nan].view(np.float16).astype(np.float32)
+    assert np.array_equal(out[nan].view(np.uint32), want_nan.view(np.uint32))
+
+
+def test_div_and_sqrt_are_correctly_rounded():
+    L = _lib()
+    rng = np.random.default_rng(2)
+    n = 1 << 20
+    a = rng.uniform(-1e3, 1e3, n).astype(np.float32)
+    b = rng.uniform(-1e3, 1e3, n).astype(np.float32)
+    a[:1000] = np.abs(rng.normal(0, 1e-38, 1000)).astype(np.float32)  # subnormal range
+    b[1000:2000] = np.float32(2 ** -140)
+    q = np.empty(n, np.float32)
+    r = np.empty(n, np.float32)
+    L.check(L.lib.dtl_kernel_div_sqrt(_p(a, C.c_float), _p(b, C.c_float), _p(q, C.c_float), _p(r, C.c_float), n), "div")
+    with np.errstate(all="ignore"):
+        assert np.array_equal(q.view(np.uint32), (a / b).view(np.uint32))
+        pos = a >= 0
+        assert np.array_equal(r[pos].view(np.uint32), np.sqrt(a[pos]).view(np.uint32))
+
+
+def test_quantize_q8a_q8k_bitexact():
+    L = _lib()
+    rng = np.random.default_rng(3)
+    rows, n = 5, 2048
+    x = rng.normal(0, 2, (rows, n)).astype(np.float32)
+    x[0, :256] = 0.0                       # all-zero blocks
+    x[1, 10], x[1, 20] = -7.5, 7.5         # |x| tie: first one wins in Q8_K
+    x[2, 0:32] = np.float32(2 ** -140)     # subnormal block
+    x[3, 64:96] = rng.integers(-3, 4, 32)  # many exact .5 ratios
+    da = np.empty(rows * n // 32, np.float32)
+    qa = np.empty(rows * n, np.int8)
+    dk = np.empty(rows * n // 256, np.float32)
+    qk = np.empty(rows * n, np.int8)
+    L.check(L.lib.dtl_kernel_quantize(_p(x, C.c_float), rows, n, _p(da, C.c_float), _p(qa, C.c_int8),
+                                      _p(dk, C.c_float), _p(qk, C.c_int8)), "quantize")
+    for r in range(rows):
+        wd, wq = detref.quantize_q8a(x[r])
+        assert np.array_equal(da[r * n // 32:(r + 1) * n // 32].view(np.uint32), wd.view(np.uint32))
+        assert np.array_equal(qa[r * n:(r + 1) * n], wq)
+        kd, kq = detref.quantize_q8k(x[r])
+        assert np.array_equal(dk[r * n // 256:(r + 1) * n // 256].view(np.uint32), kd.view(np.uint32))
+        assert np.array_equal(qk[r * n:(r + 1) * n], kq)
+
+
+def test_rmsnorm_bitexact():
+    L = _lib()
+    rng = np.random.default_rng(4)
+    for n, eps in [(64, 1e-5), (576, 1e-5), (896, 1e-6), (2048, 1e-5), (13, 1e-5)]:
+        x = rng.normal(0, 30, (3, n)).astype(np.float32)
+        w = rng.normal(1, 0.02, n).astype(np.float32)
+        out = np.empty_like(x)
+        L.check(L.lib.dtl_kernel_rmsnorm(_p(x, C.c_float), _p(w, C.c_float), eps, 3, n, _p(out, C.c_float)), "rms")
+        for r in range(3):
+            assert np.array_equal(out[r].view(np.uint32), detref.rmsnorm(x[r], w, eps).view(np.uint32))
+
+
+GEMV_CASES = [
+    (0, 37, 64, 3), (0, 20, 128, 1),
+    (8, 61, 576, 1), (8, 33, 896, 5), (8, 9, 4864, 2),
+    (2, 40, 64, 2), (2, 17, 512, 1),
+    (12, 45, 2048, 1), (12, 7, 5632, 3), (12, 30, 512, 64),
+    (14, 50, 2048, 1), (14, 9, 5632, 2), (14, 20, 512, 64),
+]
+
+
+@pytest.mark.parametrize("ggml_type,rows,cols,T", GEMV_CASES)
+def test_gemv_bitexact_against_oracle(ggml_type, rows, cols, T):
+    L = _lib()
+    rng = np.random.default_rng(ggml_type * 1000 + cols + T)
+    w = qblocks.random_row(rng, ggml_type, rows, cols)
+    x = rng.normal(0, 3, (T, cols)).astype(np.float32)
+    out = np.empty((T, rows), np.float32)
+    wb = np.frombuffer(w, np.uint8).copy()
+    L.check(L.lib.dtl_kernel_gemv(ggml_type, _p(wb, C.c_uint8), rows, cols, _p(x, C.c_float), T,
+                                  _p(out, C.c_float)), "gemv")
+    rb = qblocks.ROW_BYTES[ggml_type](cols)
+    for t in range(T):
+        want = np.array([detref.dot_row(ggml_type, w[r * rb:(r + 1) * rb], cols, x[t]) for r in range(rows)],
+                        np.float32)
+        assert np.array_equal(out[t].view(np.uint32), want.view(np.uint32)), (t,)
+
+
+@pytest.mark.parametrize("theta,rope_dim", [(1e4, 64), (1e5, 64), (1e6, 64), (1e4, 16)])
+def test_rope_table_bitexact(theta, rope_dim):
+    L = _lib()
+    from detllm_amd import synth
+    import dataclasses
+
+    positions = 2048
+    half = rope_dim // 2
+    c = np.empty(positions * half, np.float32)
+    s = np.empty(positions * half, np.float32)
+    L.check(L.lib.dtl_kernel_rope_table(theta, rope_dim, positions, _p(c, C.c_float), _p(s, C.c_float)), "rope")
+    base = synth.WORKLOADS["tiny"]
+    w = dataclasses.replace(base, rope_base=theta, d=rope_dim * 4, heads=4, kv_heads=2, ff=64, ctx=positions)
+    m = detref.Model(synth.build_model(w, layers=1))
+    wc, ws = m.rope_table(positions)
+    assert np.array_equal(c.view(np.uint32), wc.view(np.uint32))
+    assert np.array_equal(s.view(np.uint32), ws.view(np.uint32))
