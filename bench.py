@@ -1,0 +1,195 @@
+#!/usr/bin/env python3
+"""Encode throughput of the detllm hot path on one MI355X.
+
+Workload (the configuration the headline metric is quoted on): a
+TinyLlama-1.1B-shaped Llama decoder with Q4_K weights (Q6_K for attn_v, the
+ffn_down of even layers and the untied output), 22 layers, d=2048, 32/4
+heads, FFN 5632, vocab 32000, random weights from a fixed seed.  One step
+is the teacher-forced encode of 2048 Zipf-distributed tokens at n_ctx 2048
+in chunks of 64 positions: the decoder forward of every position (logits
+stay in HBM) plus, on the GPU, the logits -> integer-CDF symbol range of
+the next token with the 256 byte-escape symbols (what the range coder
+consumes).  Inputs are resident on the device when the timed region starts.
+
+Prints one JSON line.  The roofline object describes the dominant kernel
+class, timed with HIP events on the library's own stream during the timed
+steps; cpu_baseline is the oracle (the C restatement of the reference CPU
+path, threaded + AVX2 integer dots as the reference's parallel,simd build)
+on a bounded prefix of the same workload on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+# MI355X published peaks
+HBM_PEAK_GBS = 8000.0
+FP32_VECTOR_PEAK_TFLOPS = 157.3        # packed FMA rate
+# Separately rounded multiply + add without packed math (what the
+# reference's fixed-order f32 chains allow): 256 CU x 64 lanes x 2.4 GHz ops/s.
+FP32_UNFUSED_ISSUE_PEAK_TOPS = 39.3
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--workload", default="tinyllama")
+    ap.add_argument("--cpu-tokens", type=int, default=16)
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic-kib", default=None,
+                    help="FETCH_KiB,WRITE_KiB per launch of the dominant kernel from rocprofv3 --pmc")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the multi-GPU design is described in DESIGN.md", file=sys.stderr)
+        return 2
+
+    import numpy as np
+
+    from detllm_amd import synth
+    from detllm_amd.model import F32Llama
+
+    w = synth.WORKLOADS[args.workload]
+    t = time.time()
+    data = synth.build_model(w)
+    toks = synth.tokens(w)
+    log(f"[bench] built {w.name} model ({len(data) / 1e6:.1f} MB GGUF) in {time.time() - t:.1f}s")
+    t = time.time()
+    model = F32Llama.from_gguf(data)
+    log(f"[bench] loaded to device ({model.device_bytes / 1e6:.1f} MB) in {time.time() - t:.1f}s")
+    n, chunk = toks.size, w.chunk
+    sess = model.forward_workspace(n, chunk)
+    tail = 256
+
+    def step():
+        out = []
+        for p in range(0, n, chunk):
+            sess.forward_chunk(toks[p:p + chunk], p)
+            m = min(chunk, n - 1 - p)
+            if m > 0:
+                out.append(sess.symbol_ranges(toks[p + 1:p + 1 + m], 0, tail))
+        return out
+
+    for i in range(args.warmup):
+        t = time.time()
+        step()
+        log(f"[bench] warmup {i} {time.time() - t:.2f}s")
+    sess.set_profiling(True)
+    results = []
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        results.append(step())
+        log(f"[bench] step {i} done")
+    t1 = time.perf_counter()
+    prof = sess.profile()
+    sess.set_profiling(False)
+    elapsed = t1 - t0
+    tokens_per_s = n * args.steps / elapsed
+
+    # Every step must produce the same ranges (run-to-run bit determinism).
+    flat = [np.concatenate([np.concatenate([c.astype(np.uint64), f.astype(np.uint64), tt]) for c, f, tt in r])
+            for r in results]
+    deterministic = all(np.array_equal(flat[0], f) for f in flat[1:])
+
+    # Dominant kernel class by device time.
+    dom_name, dom = max(prof.items(), key=lambda kv: kv[1]["total_ms"])
+    avg_ms = dom["total_ms"] / dom["launches"]
+    per_launch_bytes = dom["bytes"] / dom["launches"]
+    per_launch_flops = 2.0 * dom["macs"] / dom["launches"]
+    compute_bound = dom["macs"] > 0 and per_launch_flops / per_launch_bytes > 20.0
+    if compute_bound:
+        achieved = per_launch_flops / (avg_ms * 1e-3) / 1e12
+        roofline = {"bound": "valu", "achieved": round(achieved, 3), "peak": FP32_VECTOR_PEAK_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(achieved / FP32_VECTOR_PEAK_TFLOPS, 4),
+                    "unfused_issue_peak": FP32_UNFUSED_ISSUE_PEAK_TOPS,
+                    "frac_of_unfused_issue_peak": round(achieved / FP32_UNFUSED_ISSUE_PEAK_TOPS, 4)}
+    else:
+        achieved = per_launch_bytes / (avg_ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4)}
+    roofline.update({"kernel": dom_name, "avg_launch_us": round(avg_ms * 1e3, 2), "launches": dom["launches"],
+                     "algorithmic_bytes_per_launch": per_launch_bytes,
+                     "algorithmic_flops_per_launch": per_launch_flops})
+    if args.traffic_kib:
+        fk, wk = (float(v) for v in args.traffic_kib.split(","))
+        roofline["traffic"] = (fk + wk) * 1024.0
+    else:
+        roofline["traffic"] = None
+    kernels = {k: {"ms_per_step": round(v["total_ms"] / args.steps, 3), "launches_per_step": v["launches"] // args.steps}
+               for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["total_ms"])}
+
+    # Parity: symbol ranges of the first positions against the oracle.
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import detref
+
+    check_n = 3
+    ref = detref.Model(data)
+    ref_logits = ref.logits(toks[:check_n])
+    parity = True
+    c0, f0, tt0 = results[0][0]
+    for i in range(check_n):
+        want = detref.symbol_range(ref_logits[i], int(toks[i + 1]), tail)
+        parity &= (int(c0[i]), int(f0[i]), int(tt0[i])) == want
+    with model.forward_workspace(check_n, check_n) as s2:
+        lg = s2.forward_chunk(toks[:check_n], 0, want_logits=True)
+    parity &= bool(np.array_equal(lg.view(np.uint32), ref_logits.view(np.uint32)))
+    log(f"[bench] parity vs oracle on {check_n} positions: {parity}; deterministic: {deterministic}")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        detref.set_threads(threads)
+        detref.set_simd(True)
+        k = args.cpu_tokens
+        t = time.perf_counter()
+        lgc = ref.logits(toks[:k])
+        for i in range(k):
+            detref.symbol_range(lgc[i], int(toks[i + 1]), tail)
+        dt = time.perf_counter() - t
+        cpu = {"value": round(k / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+               "sample": f"first {k} positions of the same 2048-token encode (forward + symbol range), "
+                         f"C oracle with {threads} threads and AVX2 integer dots"}
+        log(f"[bench] cpu baseline {cpu['value']} tok/s ({dt:.1f}s)")
+
+    line = {
+        "metric": "encode tokens/s + % HBM roofline, 1.1B Q4_K/Q6_K, 1 GPU; logits hash match",
+        "value": round(tokens_per_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": w.name, "description": w.description, "positions_per_step": int(n),
+                   "chunk": chunk, "n_ctx": n, "tail_symbols": tail,
+                   "weights": "Q4_K + Q6_K (attn_v, even ffn_down, output)"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "parity_vs_oracle": parity,
+        "deterministic": deterministic,
+        "kernels": kernels,
+    }
+    print(json.dumps(line), flush=True)
+    return 0 if parity and deterministic else 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -66,6 +66,16 @@ class ModelConfig(C.Structure):
     ]
 
 
+class KernelStat(C.Structure):
+    _fields_ = [
+        ("name", C.c_char * 32),
+        ("launches", C.c_uint64),
+        ("total_ms", C.c_double),
+        ("bytes", C.c_double),
+        ("macs", C.c_double),
+    ]
+
+
 _SIGS = {
     "dtl_status_string": (C.c_char_p, [C.c_int]),
     "dtl_model_load": (C.c_int, [C.c_char_p, sz, vpp]),
@@ -78,6 +88,8 @@ _SIGS = {
     "dtl_forward_chunk": (C.c_int, [C.c_void_p, u32p, sz, sz, f32p]),
     "dtl_session_logits": (C.c_int, [C.c_void_p, sz, sz, f32p]),
     "dtl_logits_hash": (C.c_int, [C.c_void_p, u32p, sz, sz, u8p]),
+    "dtl_session_set_profiling": (C.c_int, [C.c_void_p, C.c_int]),
+    "dtl_session_profile": (C.c_int, [C.c_void_p, C.POINTER(KernelStat), sz, C.POINTER(sz)]),
     "dtl_symbol_ranges": (C.c_int, [C.c_void_p, sz, sz, u32p, sz, u64p, u32p, u64p]),
     "dtl_cdf": (C.c_int, [C.c_void_p, sz, sz, u32p, u64p, u64p]),
     "dtl_decoder_total": (C.c_int, [C.c_void_p, sz, sz, u64p]),

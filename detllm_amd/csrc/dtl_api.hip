@@ -437,6 +437,104 @@ bool needs_q8a(const DevMat& m) {
 // ---------------------------------------------------------------------------
 // session
 
+namespace {
+
+// Event timing of every launch on the session stream, grouped by kernel class.
+class Profiler {
+ public:
+  bool on = false;
+
+  ~Profiler() {
+    for (hipEvent_t e : pool_) (void)hipEventDestroy(e);
+  }
+  void enable(bool v) {
+    on = v;
+    stats_.clear();
+    pending_.clear();
+    next_ = 0;
+  }
+  // Records one launch: `launch` is called between two events.
+  template <typename F>
+  void timed(hipStream_t s, const char* name, double bytes, double macs, F&& launch) {
+    if (!on) {
+      launch();
+      return;
+    }
+    hipEvent_t a = take(), b = take();
+    (void)hipEventRecord(a, s);
+    launch();
+    (void)hipEventRecord(b, s);
+    pending_.push_back({name, a, b, bytes, macs});
+  }
+  // Called after the stream has been synchronised.
+  void collect() {
+    for (const Pending& p : pending_) {
+      float ms = 0.0f;
+      (void)hipEventElapsedTime(&ms, p.a, p.b);
+      dtl_kernel_stat* st = find(p.name);
+      st->launches += 1;
+      st->total_ms += ms;
+      st->bytes += p.bytes;
+      st->macs += p.macs;
+    }
+    pending_.clear();
+    next_ = 0;
+  }
+  const std::vector<dtl_kernel_stat>& stats() const { return stats_; }
+
+ private:
+  struct Pending {
+    const char* name;
+    hipEvent_t a, b;
+    double bytes, macs;
+  };
+  hipEvent_t take() {
+    if (next_ == pool_.size()) {
+      hipEvent_t e;
+      (void)hipEventCreate(&e);
+      pool_.push_back(e);
+    }
+    return pool_[next_++];
+  }
+  dtl_kernel_stat* find(const char* name) {
+    for (auto& s : stats_)
+      if (std::strcmp(s.name, name) == 0) return &s;
+    dtl_kernel_stat s{};
+    std::snprintf(s.name, sizeof s.name, "%s", name);
+    stats_.push_back(s);
+    return &stats_.back();
+  }
+  std::vector<hipEvent_t> pool_;
+  size_t next_ = 0;
+  std::vector<Pending> pending_;
+  std::vector<dtl_kernel_stat> stats_;
+};
+
+// Algorithmic bytes per weight element, as stored in GGUF.
+double weight_bytes_per_elem(int type) {
+  switch (type) {
+    case GGML_F32: return 4.0;
+    case GGML_Q8_0: return 34.0 / 32.0;
+    case GGML_Q4_0: return 18.0 / 32.0;
+    case GGML_Q4_K: return 144.0 / 256.0;
+    case GGML_Q6_K: return 210.0 / 256.0;
+  }
+  return 0.0;
+}
+
+const char* gemm_class(int type) {
+  switch (type) {
+    case GGML_F32: return "gemm_f32";
+    case GGML_Q8_0: return "gemm_q8_0";
+    case GGML_Q4_0: return "gemm_q4_0";
+    case GGML_Q4_K: return "gemm_q4_k";
+    case GGML_Q6_K: return "gemm_q6_k";
+  }
+  return "gemm";
+}
+
+}  // namespace
+
 struct dtl_session {
   const dtl_model* m = nullptr;
   size_t n_ctx = 0, max_chunk = 0, max_in = 0;
@@ -453,6 +551,7 @@ struct dtl_session {
   uint32_t *c_sym = nullptr, *c_freq = nullptr, *c_freq_tab = nullptr;
   uint64_t *c_cum = nullptr, *c_total = nullptr, *c_values = nullptr, *c_cum_tab = nullptr;
   size_t rows_valid = 0;  // rows of `logits` written by the last forward
+  Profiler prof;
 };
 
 namespace {
@@ -482,8 +581,12 @@ DevAct prepare_input(dtl_session* s, const float* x, int T, int n,
     if (needs_q8a(*m)) q8a = true;
     if (m->type == GGML_Q6_K) q8k = true;
   }
-  if (q8a || q8k)
-    launch_quantize(x, T, n, q8a, q8k, s->qa, s->da, s->af, s->qk, s->dk, s->err, s->stream);
+  if (q8a || q8k) {
+    double bytes = (double)T * n * (4.0 + (q8a ? 1.0 + 4.0 / 32 + 4.0 : 0.0) + (q8k ? 1.0 + 4.0 / 256 : 0.0));
+    s->prof.timed(s->stream, "quantize", bytes, 0.0, [&] {
+      launch_quantize(x, T, n, q8a, q8k, s->qa, s->da, s->af, s->qk, s->dk, s->err, s->stream);
+    });
+  }
   DevAct a{};
   a.x = x;
   a.qa = s->qa;
@@ -508,36 +611,62 @@ int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t po
   HIP_TRY(hipMemcpyAsync(s->tokens, tokens_host, T * sizeof(uint32_t), hipMemcpyHostToDevice, st));
   int d = (int)c.d, ff = (int)c.ff, H = (int)c.heads, KV = (int)c.kv_heads;
   int hd = (int)m->head_dim;
-  launch_embed(m->emb, s->tokens, T, s->x, s->err, st);
+  Profiler& P = s->prof;
+  // Algorithmic traffic of one GEMM: weights once, quantised activations
+  // and f32 outputs per position (the residual epilogue also reads x).
+  auto gemm = [&](const DevMat& W, const DevAct& a, float* out, const float* bias, int epi) {
+    double act = W.type == GGML_F32 ? 4.0 : (W.type == GGML_Q6_K ? 1.0 + 4.0 / 256 : 1.0 + 4.0 / 32);
+    double bytes = (double)W.rows * W.cols * weight_bytes_per_elem(W.type) +
+                   (double)T * W.cols * act + (double)T * W.rows * (epi == EPI_RESIDUAL ? 8.0 : 4.0);
+    P.timed(st, gemm_class(W.type), bytes, (double)W.rows * W.cols * T,
+            [&] { launch_gemm(W, a, T, out, bias, epi, s->err, st); });
+  };
+  auto rms = [&](const float* w, float* out_h) {
+    P.timed(st, "rmsnorm", (double)T * d * 8.0 + d * 4.0, 0.0,
+            [&] { launch_rmsnorm(s->x, w, c.eps, T, d, out_h, s->err, st); });
+  };
+  P.timed(st, "embed", (double)T * d * (4.0 + weight_bytes_per_elem(m->emb.type)), 0.0,
+          [&] { launch_embed(m->emb, s->tokens, T, s->x, s->err, st); });
+  // K and V rows read by one layer's attention over the chunk (GQA heads
+  // of one group share them), and its multiply-accumulates.
+  double kv_rows = 0.0;
+  for (int t = 0; t < T; t++) kv_rows += (double)(pos0 + t + 1);
   for (size_t l = 0; l < c.block_count; l++) {
     const Layer& L = m->layers[l];
-    launch_rmsnorm(s->x, L.attn_norm, c.eps, T, d, s->h, s->err, st);
+    rms(L.attn_norm, s->h);
     DevAct a = prepare_input(s, s->h, T, d, {&L.wq, &L.wk, &L.wv});
-    launch_gemm(L.wq, a, T, s->q, L.bq, L.bq ? EPI_BIAS : EPI_STORE, s->err, st);
-    launch_gemm(L.wk, a, T, s->k, L.bk, L.bk ? EPI_BIAS : EPI_STORE, s->err, st);
-    launch_gemm(L.wv, a, T, s->v, L.bv, L.bv ? EPI_BIAS : EPI_STORE, s->err, st);
-    launch_rope_store(s->q, s->k, s->v, s->rope_cos, s->rope_sin, T, (int)pos0, H, KV, hd,
-                      (int)c.rope_dim, c.split_half, s->kc, s->vc, (int)l, (int)s->n_ctx, s->err,
-                      st);
-    launch_attention(s->q, s->kc, s->vc, (int)l, T, (int)pos0, H, KV, hd, (int)s->n_ctx,
-                     c.attention_scale, s->scores, s->attn, s->err, st);
+    gemm(L.wq, a, s->q, L.bq, L.bq ? EPI_BIAS : EPI_STORE);
+    gemm(L.wk, a, s->k, L.bk, L.bk ? EPI_BIAS : EPI_STORE);
+    gemm(L.wv, a, s->v, L.bv, L.bv ? EPI_BIAS : EPI_STORE);
+    P.timed(st, "rope_store", (double)T * (H + 3 * KV) * hd * 8.0, 0.0, [&] {
+      launch_rope_store(s->q, s->k, s->v, s->rope_cos, s->rope_sin, T, (int)pos0, H, KV, hd,
+                        (int)c.rope_dim, c.split_half, s->kc, s->vc, (int)l, (int)s->n_ctx,
+                        s->err, st);
+    });
+    P.timed(st, "attention", kv_rows * KV * hd * 8.0 + (double)T * H * hd * 8.0,
+            kv_rows * H * hd * 2.0, [&] {
+              launch_attention(s->q, s->kc, s->vc, (int)l, T, (int)pos0, H, KV, hd, (int)s->n_ctx,
+                               c.attention_scale, s->scores, s->attn, s->err, st);
+            });
     a = prepare_input(s, s->attn, T, H * hd, {&L.wo});
-    launch_gemm(L.wo, a, T, s->x, nullptr, EPI_RESIDUAL, s->err, st);
-    launch_rmsnorm(s->x, L.ffn_norm, c.eps, T, d, s->h, s->err, st);
+    gemm(L.wo, a, s->x, nullptr, EPI_RESIDUAL);
+    rms(L.ffn_norm, s->h);
     a = prepare_input(s, s->h, T, d, {&L.gate, &L.up});
-    launch_gemm(L.gate, a, T, s->g, nullptr, EPI_STORE, s->err, st);
-    launch_gemm(L.up, a, T, s->u, nullptr, EPI_STORE, s->err, st);
-    launch_swiglu(s->g, s->u, T * ff, s->ffo, s->err, st);
+    gemm(L.gate, a, s->g, nullptr, EPI_STORE);
+    gemm(L.up, a, s->u, nullptr, EPI_STORE);
+    P.timed(st, "swiglu", (double)T * ff * 12.0, 0.0,
+            [&] { launch_swiglu(s->g, s->u, T * ff, s->ffo, s->err, st); });
     a = prepare_input(s, s->ffo, T, ff, {&L.down});
-    launch_gemm(L.down, a, T, s->x, nullptr, EPI_RESIDUAL, s->err, st);
+    gemm(L.down, a, s->x, nullptr, EPI_RESIDUAL);
   }
-  launch_rmsnorm(s->x, m->out_norm, c.eps, T, d, s->h, s->err, st);
+  rms(m->out_norm, s->h);
   DevAct a = prepare_input(s, s->h, T, d, {&m->out});
-  launch_gemm(m->out, a, T, s->logits, nullptr, EPI_STORE, s->err, st);
+  gemm(m->out, a, s->logits, nullptr, EPI_STORE);
   HIP_TRY(hipGetLastError());
   int bits = 0;
   int rc = read_err(s, &bits);
   if (rc) return rc;
+  P.collect();
   if (bits & ERRBIT_NON_FINITE) return DTL_ERR_NON_FINITE;
   s->rows_valid = (size_t)T;
   return DTL_OK;
@@ -805,13 +934,31 @@ int dtl_symbol_ranges(dtl_session* s, size_t first, size_t n, const uint32_t* sy
   HIP_TRY(hipSetDevice(s->m->device));
   clear_err(s);
   HIP_TRY(hipMemcpyAsync(s->c_sym, symbols, n * 4, hipMemcpyHostToDevice, s->stream));
-  launch_cdf(s->logits + first * V, (int)n, (int)V, (int)tail, 0, s->c_sym, nullptr, s->c_cum,
-             s->c_freq, s->c_total, nullptr, nullptr, nullptr, s->err, s->stream);
+  s->prof.timed(s->stream, "cdf_symbol_range", (double)n * V * 4.0, 0.0, [&] {
+    launch_cdf(s->logits + first * V, (int)n, (int)V, (int)tail, 0, s->c_sym, nullptr, s->c_cum,
+               s->c_freq, s->c_total, nullptr, nullptr, nullptr, s->err, s->stream);
+  });
   HIP_TRY(hipMemcpyAsync(cum, s->c_cum, n * 8, hipMemcpyDeviceToHost, s->stream));
   HIP_TRY(hipMemcpyAsync(freq, s->c_freq, n * 4, hipMemcpyDeviceToHost, s->stream));
   HIP_TRY(hipMemcpyAsync(total, s->c_total, n * 8, hipMemcpyDeviceToHost, s->stream));
   int bits = 0, st = read_err(s, &bits);
+  s->prof.collect();
   return st ? st : cdf_status(bits);
+}
+
+int dtl_session_set_profiling(dtl_session* s, int enable) {
+  if (!s) return DTL_ERR_INVALID_ARGUMENT;
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  s->prof.enable(enable != 0);
+  return DTL_OK;
+}
+
+int dtl_session_profile(dtl_session* s, dtl_kernel_stat* out, size_t cap, size_t* n) {
+  if (!s || !n) return DTL_ERR_INVALID_ARGUMENT;
+  const auto& st = s->prof.stats();
+  *n = st.size();
+  for (size_t i = 0; i < st.size() && i < cap && out; i++) out[i] = st[i];
+  return DTL_OK;
 }
 
 int dtl_cdf(dtl_session* s, size_t row, size_t tail, uint32_t* freq, uint64_t* cum,

@@ -215,6 +215,23 @@ class Session:
         check(lib.dtl_session_logits(self._h, first, n, ptr(out, C.c_float)), "dtl_session_logits")
         return out
 
+    # ---- device timing ----------------------------------------------------------------
+    def set_profiling(self, enable: bool) -> None:
+        """HIP-event timing of every launch on this session's stream."""
+        check(lib.dtl_session_set_profiling(self._h, 1 if enable else 0), "dtl_session_set_profiling")
+
+    def profile(self) -> dict:
+        """{kernel class: {launches, total_ms, bytes, macs}} since profiling was enabled."""
+        n = C.c_size_t()
+        check(lib.dtl_session_profile(self._h, None, 0, C.byref(n)), "dtl_session_profile")
+        arr = (_lib.KernelStat * max(n.value, 1))()
+        check(lib.dtl_session_profile(self._h, arr, n.value, C.byref(n)), "dtl_session_profile")
+        return {
+            s.name.decode(): {"launches": int(s.launches), "total_ms": float(s.total_ms),
+                              "bytes": float(s.bytes), "macs": float(s.macs)}
+            for s in arr[: n.value]
+        }
+
     # ---- det-coder on the device-resident logits -----------------------------------
     def symbol_ranges(self, symbols: Sequence[int], first: int = 0, tail_symbols: int = 0):
         """logits_to_symbol_range_* for rows first.. of the last forward."""

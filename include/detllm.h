@@ -121,6 +121,25 @@ int dtl_session_logits(dtl_session *session, size_t first, size_t n, float *out)
 int dtl_logits_hash(const dtl_model *model, const uint32_t *tokens, size_t n, size_t chunk,
                     uint8_t out[32]);
 
+/* ---- device timing (no reference counterpart: measurement support) ------ */
+
+/* Per kernel class: launches, summed device time between HIP events
+ * recorded on the session stream around each launch, and the algorithmic
+ * HBM bytes / multiply-accumulates those launches imply. */
+typedef struct {
+    char name[32];
+    uint64_t launches;
+    double total_ms;
+    double bytes;
+    double macs;
+} dtl_kernel_stat;
+
+/* Enables (1) or disables (0) event timing of every launch; enabling
+ * clears the accumulated statistics. */
+int dtl_session_set_profiling(dtl_session *session, int enable);
+/* Copies up to cap entries; *n receives the number of kernel classes. */
+int dtl_session_profile(dtl_session *session, dtl_kernel_stat *out, size_t cap, size_t *n);
+
 /* ---- det-coder on device-resident logits -------------------------------- */
 
 /* logits_to_symbol_range_with_scratch / _with_byte_escapes
