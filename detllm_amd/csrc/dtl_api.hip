@@ -434,6 +434,40 @@ bool needs_q8a(const DevMat& m) {
 
 }  // namespace
 
+namespace {
+
+// Exact f32 copies of the Q4_K matrices the forward multiplies (the values
+// q4_k_value computes), used by the chunked-encode GEMM.  Skipped when the
+// device lacks room for them or DETLLM_NO_F32_MIRROR is set; the packed
+// kernels then serve every chunk size.
+int build_f32_mirrors(dtl_model* m) {
+  const char* off = getenv("DETLLM_NO_F32_MIRROR");
+  if (off && *off && *off != '0') return DTL_OK;
+  std::vector<DevMat*> mats;
+  for (Layer& L : m->layers)
+    for (DevMat* M : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down})
+      if (M->type == GGML_Q4_K) mats.push_back(M);
+  if (m->out.type == GGML_Q4_K) mats.push_back(&m->out);
+  size_t need = 0;
+  for (DevMat* M : mats) need += (size_t)M->rows * M->cols * sizeof(float);
+  if (mats.empty()) return DTL_OK;
+  size_t free_b = 0, total_b = 0;
+  HIP_TRY(hipMemGetInfo(&free_b, &total_b));
+  if (need + (size_t(4) << 30) > free_b) return DTL_OK;
+  for (DevMat* M : mats) {
+    float* w;
+    int st = m->arena.alloc(&w, (size_t)M->rows * M->cols);
+    if (st) return st;
+    launch_dequant_q4k(*M, w, nullptr);
+    M->w32 = w;
+  }
+  HIP_TRY(hipGetLastError());
+  HIP_TRY(hipDeviceSynchronize());
+  return DTL_OK;
+}
+
+}  // namespace
+
 // ---------------------------------------------------------------------------
 // session
 
@@ -573,20 +607,22 @@ __global__ void k_clear_flag(int* p) { *p = 0; }
 
 void clear_err(dtl_session* s) { hipLaunchKernelGGL(k_clear_flag, dim3(1), dim3(1), 0, s->stream, s->err); }
 
-// Produces the activation forms the given consumers need from x[T][n].
-DevAct prepare_input(dtl_session* s, const float* x, int T, int n,
-                     std::initializer_list<const DevMat*> consumers) {
-  bool q8a = false, q8k = false;
+// Which activation forms the given consumers need.
+void needed_forms(std::initializer_list<const DevMat*> consumers, bool* q8a, bool* q8k) {
+  *q8a = *q8k = false;
   for (const DevMat* m : consumers) {
-    if (needs_q8a(*m)) q8a = true;
-    if (m->type == GGML_Q6_K) q8k = true;
+    if (needs_q8a(*m)) *q8a = true;
+    if (m->type == GGML_Q6_K) *q8k = true;
   }
-  if (q8a || q8k) {
-    double bytes = (double)T * n * (4.0 + (q8a ? 1.0 + 4.0 / 32 + 4.0 : 0.0) + (q8k ? 1.0 + 4.0 / 256 : 0.0));
-    s->prof.timed(s->stream, "quantize", bytes, 0.0, [&] {
-      launch_quantize(x, T, n, q8a, q8k, s->qa, s->da, s->af, s->qk, s->dk, s->err, s->stream);
-    });
-  }
+}
+
+// Bytes the quantisation writes per element (Q8A: quant, dequantised f32
+// and a scale per 32; Q8_K: quant and a scale per 256).
+double quant_bytes(bool q8a, bool q8k) {
+  return (q8a ? 1.0 + 4.0 / 32 + 4.0 : 0.0) + (q8k ? 1.0 + 4.0 / 256 : 0.0);
+}
+
+DevAct session_act(dtl_session* s, const float* x) {
   DevAct a{};
   a.x = x;
   a.qa = s->qa;
@@ -595,6 +631,20 @@ DevAct prepare_input(dtl_session* s, const float* x, int T, int n,
   a.qk = s->qk;
   a.dk = s->dk;
   return a;
+}
+
+// Produces the activation forms the given consumers need from x[T][n].
+DevAct prepare_input(dtl_session* s, const float* x, int T, int n,
+                     std::initializer_list<const DevMat*> consumers) {
+  bool q8a, q8k;
+  needed_forms(consumers, &q8a, &q8k);
+  if (q8a || q8k) {
+    double bytes = (double)T * n * (4.0 + quant_bytes(q8a, q8k));
+    s->prof.timed(s->stream, "quantize", bytes, 0.0, [&] {
+      launch_quantize(x, T, n, q8a, q8k, s->qa, s->da, s->af, s->qk, s->dk, s->err, s->stream);
+    });
+  }
+  return session_act(s, x);
 }
 
 // forward_one_with_workspace (det-model lib.rs:1249-1400) for T positions.
@@ -621,9 +671,17 @@ int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t po
     P.timed(st, gemm_class(W.type), bytes, (double)W.rows * W.cols * T,
             [&] { launch_gemm(W, a, T, out, bias, epi, s->err, st); });
   };
-  auto rms = [&](const float* w, float* out_h) {
-    P.timed(st, "rmsnorm", (double)T * d * 8.0 + d * 4.0, 0.0,
-            [&] { launch_rmsnorm(s->x, w, c.eps, T, d, out_h, s->err, st); });
+  // rmsnorm of the residual stream into h, fused with the quantisation the
+  // consumers of h need.
+  auto rms = [&](const float* w, std::initializer_list<const DevMat*> consumers) {
+    bool q8a, q8k;
+    needed_forms(consumers, &q8a, &q8k);
+    P.timed(st, "rmsnorm_quantize", (double)T * d * (8.0 + quant_bytes(q8a, q8k)) + d * 4.0, 0.0,
+            [&] {
+              launch_rmsnorm_quant(s->x, w, c.eps, T, d, s->h, q8a, q8k, s->qa, s->da, s->af,
+                                   s->qk, s->dk, s->err, st);
+            });
+    return session_act(s, s->h);
   };
   P.timed(st, "embed", (double)T * d * (4.0 + weight_bytes_per_elem(m->emb.type)), 0.0,
           [&] { launch_embed(m->emb, s->tokens, T, s->x, s->err, st); });
@@ -633,8 +691,7 @@ int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t po
   for (int t = 0; t < T; t++) kv_rows += (double)(pos0 + t + 1);
   for (size_t l = 0; l < c.block_count; l++) {
     const Layer& L = m->layers[l];
-    rms(L.attn_norm, s->h);
-    DevAct a = prepare_input(s, s->h, T, d, {&L.wq, &L.wk, &L.wv});
+    DevAct a = rms(L.attn_norm, {&L.wq, &L.wk, &L.wv});
     gemm(L.wq, a, s->q, L.bq, L.bq ? EPI_BIAS : EPI_STORE);
     gemm(L.wk, a, s->k, L.bk, L.bk ? EPI_BIAS : EPI_STORE);
     gemm(L.wv, a, s->v, L.bv, L.bv ? EPI_BIAS : EPI_STORE);
@@ -650,17 +707,25 @@ int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t po
             });
     a = prepare_input(s, s->attn, T, H * hd, {&L.wo});
     gemm(L.wo, a, s->x, nullptr, EPI_RESIDUAL);
-    rms(L.ffn_norm, s->h);
-    a = prepare_input(s, s->h, T, d, {&L.gate, &L.up});
-    gemm(L.gate, a, s->g, nullptr, EPI_STORE);
-    gemm(L.up, a, s->u, nullptr, EPI_STORE);
-    P.timed(st, "swiglu", (double)T * ff * 12.0, 0.0,
-            [&] { launch_swiglu(s->g, s->u, T * ff, s->ffo, s->err, st); });
+    a = rms(L.ffn_norm, {&L.gate, &L.up});
+    if (T >= 16 && L.gate.type == GGML_Q4_K && L.up.type == GGML_Q4_K &&
+        L.gate.rows == L.up.rows && L.gate.cols == L.up.cols) {
+      // gate, up and swiglu in one pass: both chains of a row share one wave.
+      double bytes = 2.0 * L.gate.rows * L.gate.cols * weight_bytes_per_elem(GGML_Q4_K) +
+                     (double)T * d * (1.0 + 4.0 / 32) + (double)T * ff * 4.0;
+      P.timed(st, "gemm_q4_k_gate_up", bytes, 2.0 * L.gate.rows * L.gate.cols * T, [&] {
+        launch_gemm_pair_swiglu_q4k(L.gate, L.up, a, T, nullptr, nullptr, s->ffo, s->err, st);
+      });
+    } else {
+      gemm(L.gate, a, s->g, nullptr, EPI_STORE);
+      gemm(L.up, a, s->u, nullptr, EPI_STORE);
+      P.timed(st, "swiglu", (double)T * ff * 12.0, 0.0,
+              [&] { launch_swiglu(s->g, s->u, T * ff, s->ffo, s->err, st); });
+    }
     a = prepare_input(s, s->ffo, T, ff, {&L.down});
     gemm(L.down, a, s->x, nullptr, EPI_RESIDUAL);
   }
-  rms(m->out_norm, s->h);
-  DevAct a = prepare_input(s, s->h, T, d, {&m->out});
+  DevAct a = rms(m->out_norm, {&m->out});
   gemm(m->out, a, s->logits, nullptr, EPI_STORE);
   HIP_TRY(hipGetLastError());
   int bits = 0;
@@ -759,6 +824,7 @@ int dtl_model_load(const uint8_t* bytes, size_t len, dtl_model** out) {
     return DTL_ERR_GGUF;
   }
   m->vocab = (size_t)m->out.rows;
+  if ((st = build_f32_mirrors(m.get()))) return st;
   *out = m.release();
   return DTL_OK;
 }
@@ -1196,12 +1262,17 @@ int dtl_kernel_quantize(const float* x, size_t rows, size_t n, float* q8a_d, int
     HIP_TRY(hipMemcpyAsync(q8a_q, qa, tot, hipMemcpyDeviceToHost, sc.stream));
     HIP_TRY(hipMemcpyAsync(q8a_d, da, tot / 32 * 4, hipMemcpyDeviceToHost, sc.stream));
   }
+  std::vector<int8_t> perm;
   if (want_k) {
-    HIP_TRY(hipMemcpyAsync(q8k_q, qk, tot, hipMemcpyDeviceToHost, sc.stream));
+    perm.resize(tot);
+    HIP_TRY(hipMemcpyAsync(perm.data(), qk, tot, hipMemcpyDeviceToHost, sc.stream));
     HIP_TRY(hipMemcpyAsync(q8k_d, dk, tot / 256 * 4, hipMemcpyDeviceToHost, sc.stream));
   }
   int bits = 0;
   if ((st = sc.finish(&bits))) return st;
+  // Device Q8_K blocks are class-major; return them in element order.
+  for (size_t b = 0; b < perm.size() / 256; b++)
+    for (size_t e = 0; e < 256; e++) q8k_q[b * 256 + e] = perm[b * 256 + (e % 8) * 32 + e / 8];
   return bits ? DTL_ERR_NON_FINITE : DTL_OK;
 }
 

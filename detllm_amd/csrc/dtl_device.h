@@ -34,6 +34,9 @@ struct DevMat {
   const void* w;
   const uint16_t* d16;
   const uint8_t* hdr;
+  // Q4_K only (optional): float[rows][cols] holding q4_k_value of every
+  // element, used by the chunked-encode GEMM as scalar-path operands.
+  const float* w32;
 };
 
 // Activations of T positions for one GEMM input of width cols, in every
@@ -54,11 +57,25 @@ void launch_embed(const DevMat& E, const uint32_t* tokens, int T, float* x, int*
                   hipStream_t s);
 void launch_rmsnorm(const float* x, const float* w, float eps, int T, int n, float* out, int* err,
                     hipStream_t s);
+// rmsnorm followed by the activation quantisation of the normalised row, in
+// one pass (out keeps the f32 row).
+void launch_rmsnorm_quant(const float* x, const float* w, float eps, int T, int n, float* out,
+                          bool want_q8a, bool want_q8k, int8_t* qa, float* da, float* af,
+                          int8_t* qk, float* dk, int* err, hipStream_t s);
 // want_q8a / want_q8k select which quantisations to produce.
 void launch_quantize(const float* x, int T, int n, bool want_q8a, bool want_q8k, int8_t* qa,
                      float* da, float* af, int8_t* qk, float* dk, int* err, hipStream_t s);
 void launch_gemm(const DevMat& W, const DevAct& A, int T, float* out, const float* bias, int epi,
                  int* err, hipStream_t s);
+// Token-parallel GEMMs (dtl_gemm.hip) for chunks of positions.
+bool gemm_tok_supported(const DevMat& W);
+void launch_gemm_tok(const DevMat& W, const DevAct& A, int T, float* out, const float* bias,
+                     int epi, int* err, hipStream_t s);
+// Fills out[rows*cols] with the exact f32 value of every Q4_K weight.
+void launch_dequant_q4k(const DevMat& W, float* out, hipStream_t s);
+// gate and up (both Q4_K, same shape) in one pass with silu(gate)*up written to ffo.
+void launch_gemm_pair_swiglu_q4k(const DevMat& G, const DevMat& U, const DevAct& A, int T, float* g,
+                                 float* u, float* ffo, int* err, hipStream_t s);
 void launch_rope_store(float* q, float* k, const float* v, const float* rope_cos,
                        const float* rope_sin, int T, int pos0, int H, int KV, int hd, int rope_dim,
                        int split_half, float* kc, float* vc, int layer, int n_ctx, int* err,

@@ -1,0 +1,566 @@
+// Token-parallel GEMMs for chunks of positions (teacher-forced encode).
+//
+// Mapping: one lane = one position (token) of the chunk, one wave = up to 64
+// positions x R weight rows.  Every (row, position) output is a dependent
+// f32 chain that its lane walks in the reference's order; the wave
+// dequantises each weight once into LDS and all 64 lanes read it back as a
+// broadcast, so the decode cost is shared by the whole chunk and the inner
+// loop is one multiply + one add per weight (Q4_K) or one int8 dot4 per four
+// weights (Q6_K, Q8_0).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dtl_device.h"
+#include "dtl_numerics.h"
+
+namespace dtl {
+
+namespace {
+
+constexpr int kWaves = 4;  // waves per workgroup
+constexpr int kGgmlQ4K = 12, kGgmlQ6K = 14, kGgmlQ8_0 = 8;
+
+__device__ __forceinline__ void flag(int* err, int bit) { atomicOr(err, bit); }
+
+__device__ __forceinline__ uint32_t byte_of(const uint32_t w[3], int i) {
+  return (w[i >> 2] >> (8 * (i & 3))) & 0xffu;
+}
+
+// Q4_K 6-bit scale and min of sub-block j from the 12 packed bytes held as
+// three little-endian words (det-quant lib.rs:519-529).
+__device__ __forceinline__ void q4k_scale_min_w(const uint32_t s[3], int j, int* sc, int* mn) {
+  if (j < 4) {
+    *sc = (int)(byte_of(s, j) & 0x3f);
+    *mn = (int)(byte_of(s, j + 4) & 0x3f);
+  } else {
+    *sc = (int)((byte_of(s, j + 4) & 0x0f) | ((byte_of(s, j - 4) >> 6) << 4));
+    *mn = (int)((byte_of(s, j + 4) >> 4) | ((byte_of(s, j) >> 6) << 4));
+  }
+}
+
+__device__ __forceinline__ bool store_epilogue(float v, float* out, size_t o, const float* bias, int r,
+                                               int epi) {
+  bool ok = finite(v);
+  if (epi == EPI_BIAS) v = v + bias[r];
+  else if (epi == EPI_RESIDUAL) v = out[o] + v;
+  out[o] = v;
+  return ok && finite(v);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Q4_K: dot_q4_k_q8a (det-quant lib.rs:281-315).  Each lane's chain adds
+// weight*activation for every element of the row in ascending order.
+// PAIR computes rows of two matrices with the same shape (gate and up) and
+// writes silu(gate)*up (det-model lib.rs:2420-2434) in the epilogue.
+template <int R, bool PAIR>
+__global__ void __launch_bounds__(256) k_q4k_tok(DevMat W0, DevMat W1, const float* __restrict__ af,
+                                                 int T, float* out0, float* out1, float* ffo,
+                                                 const float* bias, int epi, int* err) {
+  constexpr int NM = PAIR ? 2 : 1;
+  __shared__ __align__(16) float wl[kWaves][NM * R][256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * kWaves + wave) * R;
+  const int t = blockIdx.y * 64 + lane;
+  const bool tok = t < T;
+  const int rows = W0.rows, cols = W0.cols, nsb = W0.nb;
+  const float* arow = af + (size_t)(tok ? t : 0) * cols;
+  float acc[NM * R];
+#pragma unroll
+  for (int k = 0; k < NM * R; k++) acc[k] = 0.0f;
+  // lane -> four consecutive elements of one sub-block
+  const int wi = lane & 31, hh = lane >> 5;
+  const int sub = 2 * (wi >> 3) + hh;
+  const int e0 = sub * 32 + (wi & 7) * 4;
+
+  for (int sb = 0; sb < nsb; sb++) {
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+      const DevMat& W = m ? W1 : W0;
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        int row = row0 + r;
+        float4 w4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (row < rows) {
+          size_t blk = (size_t)row * nsb + sb;
+          const uint32_t* h = (const uint32_t*)(W.hdr + blk * 16);
+          uint32_t h0 = h[0];
+          uint32_t s[3] = {h[1], h[2], h[3]};
+          float d = f16_to_f32((uint16_t)(h0 & 0xffff));
+          float dmin = f16_to_f32((uint16_t)(h0 >> 16));
+          int sc, mn;
+          q4k_scale_min_w(s, sub, &sc, &mn);
+          float dsc = d * (float)sc, dm = dmin * (float)mn;
+          uint32_t qw = ((const uint32_t*)((const uint8_t*)W.w + blk * 128))[wi];
+          uint32_t q = (qw >> (4 * hh)) & 0x0f0f0f0fu;
+          w4.x = dsc * (float)(q & 0xff) - dm;
+          w4.y = dsc * (float)((q >> 8) & 0xff) - dm;
+          w4.z = dsc * (float)((q >> 16) & 0xff) - dm;
+          w4.w = dsc * (float)(q >> 24) - dm;
+        }
+        *(float4*)&wl[wave][m * R + r][e0] = w4;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    // 16 activations per slice held in registers; each row's 16 weights
+    // come from LDS as four broadcast 128-bit reads.
+#pragma unroll 1
+    for (int s = 0; s < 16; s++) {
+      float a[16];
+      const float4* ap = (const float4*)(arow + sb * 256 + s * 16);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        float4 v = ap[i];  // rows past T read row 0 and are never stored
+        a[4 * i] = v.x;
+        a[4 * i + 1] = v.y;
+        a[4 * i + 2] = v.z;
+        a[4 * i + 3] = v.w;
+      }
+#pragma unroll
+      for (int k = 0; k < NM * R; k++) {
+        const float4* wp = (const float4*)&wl[wave][k][s * 16];
+        float c = acc[k];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          float4 w = wp[i];
+          c += w.x * a[4 * i];
+          c += w.y * a[4 * i + 1];
+          c += w.z * a[4 * i + 2];
+          c += w.w * a[4 * i + 3];
+        }
+        acc[k] = c;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  if (!tok) return;
+  bool ok = true;
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    int row = row0 + r;
+    if (row >= rows) continue;
+    size_t o = (size_t)t * rows + row;
+    if (PAIR) {
+      float g = acc[r], u = acc[R + r];
+      float v = silu_det(g) * u;
+      ok &= finite(g) && finite(u) && finite(v);
+      if (out0) out0[o] = g;
+      if (out1) out1[o] = u;
+      ffo[o] = v;
+    } else {
+      ok &= store_epilogue(acc[r], out0, o, bias, row, epi);
+    }
+  }
+  if (!ok) flag(err, ERRBIT_NON_FINITE);
+}
+
+// ---------------------------------------------------------------------------
+// Q6_K: dot_q6_k_q8k (det-quant lib.rs:353-397).  The eight lane sums
+// aux32[l] (l = element index mod 8) are exact integers: with the Q8_K
+// activations stored class-major (class l at bytes 32l..32l+31 of each
+// 256-block) and W' = scale*q6 split into int8 planes hi = W' >> 6 and
+// lo = W' & 63 in the same order, aux32[l] = 64*dot(hi_l, q_l) + dot(lo_l, q_l),
+// eight dot4 per plane.  Then sums[l] += (dw*da)*aux32[l] per superblock and
+// the final sequential combine 0 + s0 + ... + s7.
+template <int R>
+__global__ void __launch_bounds__(256) k_q6k_tok(DevMat W, const int8_t* __restrict__ qk,
+                                                 const float* __restrict__ dk, int T, float* out,
+                                                 const float* bias, int epi, int* err) {
+  __shared__ __align__(16) int8_t hl[kWaves][R][2][256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * kWaves + wave) * R;
+  const int t = blockIdx.y * 64 + lane;
+  const bool tok = t < T;
+  const int rows = W.rows, cols = W.cols, nsb = W.nb;
+  const int8_t* arow = qk + (size_t)(tok ? t : 0) * cols;
+  const float* drow = dk + (size_t)(tok ? t : 0) * nsb;
+  float sums[R][8];
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int l = 0; l < 8; l++) sums[r][l] = 0.0f;
+  // lane -> elements e0..e0+3 (same half, part and 16-element scale group)
+  const int e0 = lane * 4;
+  const int half = e0 >> 7, within = e0 & 127, l0 = within & 31, part = within >> 5;
+
+  for (int sb = 0; sb < nsb; sb++) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      int row = row0 + r;
+      uint32_t hiw = 0, low = 0;
+      if (row < rows) {
+        const uint8_t* body = (const uint8_t*)W.w + ((size_t)row * nsb + sb) * 208;
+        uint32_t qlw = *(const uint32_t*)(body + half * 64 + l0 + (part & 1) * 32);
+        uint32_t qhw = *(const uint32_t*)(body + 128 + half * 32 + l0);
+        int scale = (int)(int8_t)body[192 + (e0 >> 4)];
+        uint32_t nib = (part < 2 ? qlw : (qlw >> 4)) & 0x0f0f0f0fu;
+        uint32_t two = (qhw >> (2 * part)) & 0x03030303u;
+        uint32_t q6 = nib | (two << 4);  // four 6-bit codes
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          int v = (int)((q6 >> (8 * k)) & 0xff) - 32;
+          int wp = scale * v;           // in [-4064, 4096]
+          int hi = wp >> 6, lo = wp & 63;
+          hiw |= (uint32_t)(uint8_t)hi << (8 * k);
+          low |= (uint32_t)(uint8_t)lo << (8 * k);
+        }
+      }
+      // scatter the four bytes to their class-major positions
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        int e = e0 + k;
+        int p = (e & 7) * 32 + (e >> 3);
+        hl[wave][r][0][p] = (int8_t)(hiw >> (8 * k));
+        hl[wave][r][1][p] = (int8_t)(low >> (8 * k));
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    float da = drow[sb];
+    float d[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      int row = row0 + r < rows ? row0 + r : rows - 1;
+      d[r] = f16_to_f32(W.d16[(size_t)row * nsb + sb]) * da;
+    }
+#pragma unroll
+    for (int l = 0; l < 8; l++) {
+      // the 32 class-l activation quants of this superblock
+      const int4* ap = (const int4*)(arow + sb * 256 + l * 32);
+      int4 a0 = ap[0];
+      int4 a1 = ap[1];
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const int4* hp = (const int4*)&hl[wave][r][0][l * 32];
+        const int4* lp = (const int4*)&hl[wave][r][1][l * 32];
+        int4 h0 = hp[0], h1 = hp[1], q0 = lp[0], q1 = lp[1];
+        int dh = 0, dl = 0;
+        dh = __builtin_amdgcn_sdot4(h0.x, a0.x, dh, false);
+        dh = __builtin_amdgcn_sdot4(h0.y, a0.y, dh, false);
+        dh = __builtin_amdgcn_sdot4(h0.z, a0.z, dh, false);
+        dh = __builtin_amdgcn_sdot4(h0.w, a0.w, dh, false);
+        dh = __builtin_amdgcn_sdot4(h1.x, a1.x, dh, false);
+        dh = __builtin_amdgcn_sdot4(h1.y, a1.y, dh, false);
+        dh = __builtin_amdgcn_sdot4(h1.z, a1.z, dh, false);
+        dh = __builtin_amdgcn_sdot4(h1.w, a1.w, dh, false);
+        dl = __builtin_amdgcn_sdot4(q0.x, a0.x, dl, false);
+        dl = __builtin_amdgcn_sdot4(q0.y, a0.y, dl, false);
+        dl = __builtin_amdgcn_sdot4(q0.z, a0.z, dl, false);
+        dl = __builtin_amdgcn_sdot4(q0.w, a0.w, dl, false);
+        dl = __builtin_amdgcn_sdot4(q1.x, a1.x, dl, false);
+        dl = __builtin_amdgcn_sdot4(q1.y, a1.y, dl, false);
+        dl = __builtin_amdgcn_sdot4(q1.z, a1.z, dl, false);
+        dl = __builtin_amdgcn_sdot4(q1.w, a1.w, dl, false);
+        int aux = dh * 64 + dl;
+        sums[r][l] += d[r] * (float)aux;
+      }
+      // keep the loads of one class from being hoisted over the previous one
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  if (!tok) return;
+  bool ok = true;
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    int row = row0 + r;
+    if (row >= rows) continue;
+    float v = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 8; l++) v += sums[r][l];
+    ok &= store_epilogue(v, out, (size_t)t * rows + row, bias, row, epi);
+  }
+  if (!ok) flag(err, ERRBIT_NON_FINITE);
+}
+
+// ---------------------------------------------------------------------------
+// Q8_0: dot_q8_0_q8a (det-quant lib.rs:237-257): exact i32 block sums by
+// dot4, (dw*da)*isum, block-ordered f32 chain per lane.
+template <int R>
+__global__ void __launch_bounds__(256) k_q8_0_tok(DevMat W, const int8_t* __restrict__ qa,
+                                                  const float* __restrict__ da, int T, float* out,
+                                                  const float* bias, int epi, int* err) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * kWaves + wave) * R;
+  const int t = blockIdx.y * 64 + lane;
+  const bool tok = t < T;
+  const int rows = W.rows, cols = W.cols, nb = W.nb;
+  const int8_t* arow = qa + (size_t)(tok ? t : 0) * cols;
+  const float* drow = da + (size_t)(tok ? t : 0) * nb;
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) acc[r] = 0.0f;
+  for (int b = 0; b < nb; b++) {
+    int4 a0 = ((const int4*)(arow + b * 32))[0];
+    int4 a1 = ((const int4*)(arow + b * 32))[1];
+    float dab = drow[b];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      int row = row0 + r < rows ? row0 + r : rows - 1;
+      const int4* wp = (const int4*)((const int8_t*)W.w + (size_t)row * cols + b * 32);
+      int4 w0 = wp[0], w1 = wp[1];
+      int is = 0;
+      is = __builtin_amdgcn_sdot4(w0.x, a0.x, is, false);
+      is = __builtin_amdgcn_sdot4(w0.y, a0.y, is, false);
+      is = __builtin_amdgcn_sdot4(w0.z, a0.z, is, false);
+      is = __builtin_amdgcn_sdot4(w0.w, a0.w, is, false);
+      is = __builtin_amdgcn_sdot4(w1.x, a1.x, is, false);
+      is = __builtin_amdgcn_sdot4(w1.y, a1.y, is, false);
+      is = __builtin_amdgcn_sdot4(w1.z, a1.z, is, false);
+      is = __builtin_amdgcn_sdot4(w1.w, a1.w, is, false);
+      float scale = f16_to_f32(W.d16[(size_t)row * nb + b]) * dab;
+      acc[r] += scale * (float)is;
+    }
+  }
+  if (!tok) return;
+  bool ok = true;
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    int row = row0 + r;
+    if (row >= rows) continue;
+    ok &= store_epilogue(acc[r], out, (size_t)t * rows + row, bias, row, epi);
+  }
+  if (!ok) flag(err, ERRBIT_NON_FINITE);
+}
+
+// ---------------------------------------------------------------------------
+// Q4_K from an exact f32 copy of the weights (the values q4_k_value yields,
+// det-quant lib.rs:506-517, computed once at load).  Lanes = positions; the
+// weight rows are wave-uniform, so they are fetched with scalar loads and
+// used as SGPR operands of v_mul_f32; the workgroup stages each 64-element
+// activation slice of its 64 positions in LDS once for its four waves
+// (double-buffered).  NK rows per wave share every activation register.
+template <int NK, bool PAIR>
+__global__ void __launch_bounds__(256) k_q4k_f32w(const float* __restrict__ W0,
+                                                  const float* __restrict__ W1, int rows, int cols,
+                                                  const float* __restrict__ af, int T, float* out0,
+                                                  float* out1, float* ffo, const float* bias,
+                                                  int epi, int* err) {
+  constexpr int NM = PAIR ? 2 : 1;
+  constexpr int SL = 64;        // elements per slice
+  constexpr int LD = SL + 4;    // padded LDS row (floats)
+  __shared__ __align__(16) float at[2][64][LD];
+  __shared__ __align__(16) float wt[2][kWaves][NM * NK][SL];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = (blockIdx.x * kWaves + wave) * NK;
+  const int tbase = blockIdx.y * 64;
+  const int t = tbase + lane;
+  float acc[NM * NK];
+#pragma unroll
+  for (int k = 0; k < NM * NK; k++) acc[k] = 0.0f;
+
+  // Each thread moves four float4 of every 64x64 activation tile: the global
+  // loads for the next tile are issued before the current tile is consumed
+  // and written to LDS only afterwards, so their latency overlaps the math.
+  constexpr int PER = 64 * SL / 4 / 256;
+  int tk_[PER], c4_[PER];
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    int x = threadIdx.x + j * 256;
+    tk_[j] = x / (SL / 4);
+    c4_[j] = x % (SL / 4);
+  }
+  float4 pre[PER];
+  auto issue = [&](int e0) {
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+      int tt = tbase + tk_[j] < T ? tbase + tk_[j] : T - 1;
+      pre[j] = *(const float4*)(af + (size_t)tt * cols + e0 + c4_[j] * 4);
+    }
+  };
+  auto commit = [&](int b) {
+#pragma unroll
+    for (int j = 0; j < PER; j++) *(float4*)&at[b][tk_[j]][c4_[j] * 4] = pre[j];
+  };
+  // The wave's own weight rows go through LDS the same way (lane -> one
+  // float4 of one row) and are read back as broadcasts.
+  const int wk = lane >> 4, wc4 = lane & 15;
+  const bool wlane = wk < NM * NK;
+  const float* wsrc = nullptr;
+  if (wlane) {
+    int m = wk / NK, kk = wk % NK;
+    int row = row0 + kk < rows ? row0 + kk : rows - 1;
+    wsrc = (m ? W1 : W0) + (size_t)row * cols + wc4 * 4;
+  }
+  float4 wpre = make_float4(0.f, 0.f, 0.f, 0.f);
+  auto issue_w = [&](int e0) {
+    if (wlane) wpre = *(const float4*)(wsrc + e0);
+  };
+  auto commit_w = [&](int b) {
+    if (wlane) *(float4*)&wt[b][wave][wk][wc4 * 4] = wpre;
+  };
+  issue(0);
+  issue_w(0);
+  commit(0);
+  commit_w(0);
+  __syncthreads();
+  int buf = 0;
+  for (int e0 = 0; e0 < cols; e0 += SL) {
+    const bool more = e0 + SL < cols;
+    if (more) {
+      issue(e0 + SL);
+      issue_w(e0 + SL);
+    }
+#pragma unroll 4
+    for (int i = 0; i < SL; i += 4) {
+      float4 a = *(const float4*)&at[buf][lane][i];
+#pragma unroll
+      for (int k = 0; k < NM * NK; k++) {
+        float4 w = *(const float4*)&wt[buf][wave][k][i];
+        float c = acc[k];
+        c += w.x * a.x;
+        c += w.y * a.y;
+        c += w.z * a.z;
+        c += w.w * a.w;
+        acc[k] = c;
+      }
+    }
+    if (more) {
+      commit(buf ^ 1);
+      commit_w(buf ^ 1);
+    }
+    __syncthreads();
+    buf ^= 1;
+  }
+  if (t >= T) return;
+  bool ok = true;
+#pragma unroll
+  for (int k = 0; k < NK; k++) {
+    int row = row0 + k;
+    if (row >= rows) continue;
+    size_t o = (size_t)t * rows + row;
+    if (PAIR) {
+      float g = acc[k], u = acc[NK + k];
+      float v = silu_det(g) * u;
+      ok &= finite(g) && finite(u) && finite(v);
+      ffo[o] = v;
+    } else {
+      ok &= store_epilogue(acc[k], out0, o, bias, row, epi);
+    }
+  }
+  if (!ok) flag(err, ERRBIT_NON_FINITE);
+}
+
+// Exact f32 copy of a Q4_K matrix: q4_k_value for every element.
+__global__ void k_dequant_q4k(DevMat W, float* out) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  size_t total = (size_t)W.rows * W.cols;
+  if (i >= total) return;
+  int row = (int)(i / W.cols), c = (int)(i % W.cols);
+  int sb = c / 256, idx = c % 256, sub = idx / 32, within = idx % 32;
+  size_t blk = (size_t)row * W.nb + sb;
+  const uint32_t* h = (const uint32_t*)(W.hdr + blk * 16);
+  uint32_t h0 = h[0];
+  uint32_t s[3] = {h[1], h[2], h[3]};
+  float d = f16_to_f32((uint16_t)(h0 & 0xffff)), dmin = f16_to_f32((uint16_t)(h0 >> 16));
+  int sc, mn;
+  q4k_scale_min_w(s, sub, &sc, &mn);
+  uint8_t byte = ((const uint8_t*)W.w)[blk * 128 + (sub / 2) * 32 + within];
+  int q = (sub & 1) ? (byte >> 4) : (byte & 0x0f);
+  out[i] = (d * (float)sc) * (float)q - (dmin * (float)mn);
+}
+
+void launch_dequant_q4k(const DevMat& W, float* out, hipStream_t s) {
+  size_t total = (size_t)W.rows * W.cols;
+  hipLaunchKernelGGL(k_dequant_q4k, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, W, out);
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+
+namespace {
+// Rows per wave: enough waves to cover every SIMD, more rows when the
+// matrix is tall so the per-row decode is amortised over fewer LDS refills.
+int rows_per_wave(int rows) {
+  if (rows >= 8192) return 4;
+  if (rows >= 4096) return 2;
+  return 1;
+}
+
+// Rows per wave for the f32-weight Q4_K kernel (DETLLM_Q4K_NK overrides).
+int q4k_nk(int rows) {
+  static int forced = [] {
+    const char* e = getenv("DETLLM_Q4K_NK");
+    return e ? atoi(e) : 0;
+  }();
+  if (forced == 1 || forced == 2 || forced == 4) return forced;
+  (void)rows;
+  return 2;
+}
+
+template <bool PAIR>
+void launch_q4k_f32w(const DevMat& W0, const DevMat& W1, const DevAct& A, int T, float* out,
+                     float* ffo, const float* bias, int epi, int* err, hipStream_t s) {
+  int nk = q4k_nk(PAIR ? 2 * W0.rows : W0.rows);
+  if (PAIR && nk == 4) nk = 2;
+  dim3 grid((W0.rows + kWaves * nk - 1) / (kWaves * nk), (T + 63) / 64);
+  dim3 block(kWaves * 64);
+  const float* w1 = PAIR ? W1.w32 : nullptr;
+  if (nk == 4)
+    hipLaunchKernelGGL((k_q4k_f32w<4, PAIR>), grid, block, 0, s, W0.w32, w1, W0.rows, W0.cols, A.af, T, out, nullptr, ffo, bias, epi, err);
+  else if (nk == 2)
+    hipLaunchKernelGGL((k_q4k_f32w<2, PAIR>), grid, block, 0, s, W0.w32, w1, W0.rows, W0.cols, A.af, T, out, nullptr, ffo, bias, epi, err);
+  else
+    hipLaunchKernelGGL((k_q4k_f32w<1, PAIR>), grid, block, 0, s, W0.w32, w1, W0.rows, W0.cols, A.af, T, out, nullptr, ffo, bias, epi, err);
+}
+}  // namespace
+
+bool gemm_tok_supported(const DevMat& W) {
+  return W.type == kGgmlQ4K || W.type == kGgmlQ6K || W.type == kGgmlQ8_0;
+}
+
+void launch_gemm_tok(const DevMat& W, const DevAct& A, int T, float* out, const float* bias,
+                     int epi, int* err, hipStream_t s) {
+  DevMat none{};
+  if (W.type == kGgmlQ4K && W.w32) {
+    launch_q4k_f32w<false>(W, none, A, T, out, nullptr, bias, epi, err, s);
+    return;
+  }
+  int R = rows_per_wave(W.rows);
+  dim3 grid((W.rows + kWaves * R - 1) / (kWaves * R), (T + 63) / 64);
+  dim3 block(kWaves * 64);
+  switch (W.type) {
+    case kGgmlQ4K:
+      if (R == 4)
+        hipLaunchKernelGGL((k_q4k_tok<4, false>), grid, block, 0, s, W, none, A.af, T, out, nullptr, nullptr, bias, epi, err);
+      else if (R == 2)
+        hipLaunchKernelGGL((k_q4k_tok<2, false>), grid, block, 0, s, W, none, A.af, T, out, nullptr, nullptr, bias, epi, err);
+      else
+        hipLaunchKernelGGL((k_q4k_tok<1, false>), grid, block, 0, s, W, none, A.af, T, out, nullptr, nullptr, bias, epi, err);
+      break;
+    case kGgmlQ6K:
+      if (R == 4)
+        hipLaunchKernelGGL((k_q6k_tok<4>), grid, block, 0, s, W, A.qk, A.dk, T, out, bias, epi, err);
+      else if (R == 2)
+        hipLaunchKernelGGL((k_q6k_tok<2>), grid, block, 0, s, W, A.qk, A.dk, T, out, bias, epi, err);
+      else
+        hipLaunchKernelGGL((k_q6k_tok<1>), grid, block, 0, s, W, A.qk, A.dk, T, out, bias, epi, err);
+      break;
+    default:
+      if (R == 4)
+        hipLaunchKernelGGL((k_q8_0_tok<4>), grid, block, 0, s, W, A.qa, A.da, T, out, bias, epi, err);
+      else if (R == 2)
+        hipLaunchKernelGGL((k_q8_0_tok<2>), grid, block, 0, s, W, A.qa, A.da, T, out, bias, epi, err);
+      else
+        hipLaunchKernelGGL((k_q8_0_tok<1>), grid, block, 0, s, W, A.qa, A.da, T, out, bias, epi, err);
+      break;
+  }
+}
+
+void launch_gemm_pair_swiglu_q4k(const DevMat& G, const DevMat& U, const DevAct& A, int T, float* g,
+                                 float* u, float* ffo, int* err, hipStream_t s) {
+  if (G.w32 && U.w32 && !g && !u) {
+    launch_q4k_f32w<true>(G, U, A, T, nullptr, ffo, nullptr, 0, err, s);
+    return;
+  }
+  int R = rows_per_wave(2 * G.rows) >= 2 ? 2 : 1;
+  dim3 grid((G.rows + kWaves * R - 1) / (kWaves * R), (T + 63) / 64);
+  dim3 block(kWaves * 64);
+  if (R == 2)
+    hipLaunchKernelGGL((k_q4k_tok<2, true>), grid, block, 0, s, G, U, A.af, T, g, u, ffo, nullptr, 0, err);
+  else
+    hipLaunchKernelGGL((k_q4k_tok<1, true>), grid, block, 0, s, G, U, A.af, T, g, u, ffo, nullptr, 0, err);
+}
+
+}  // namespace dtl

@@ -164,7 +164,9 @@ __device__ float row_dot_q6k(const uint8_t* body, const uint16_t* wd, const int8
     const uint8_t* b = body + (size_t)sb * 208;
     const int8_t* a = qk + sb * 256;
     int aux[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int e = 0; e < 256; e++) aux[e & 7] += q6k_scale(b, e) * (int)a[e] * q6k_quant(b, e);
+    // Q8_K quants are stored class-major: element e sits at (e % 8) * 32 + e / 8.
+    for (int e = 0; e < 256; e++)
+      aux[e & 7] += q6k_scale(b, e) * (int)a[(e & 7) * 32 + (e >> 3)] * q6k_quant(b, e);
     float d = f16_to_f32(wd[sb]) * dk[sb];
 #pragma unroll
     for (int l = 0; l < 8; l++) sums[l] += d * (float)aux[l];
@@ -195,22 +197,172 @@ void launch_embed(const DevMat& E, const uint32_t* tokens, int T, float* x, int*
 }
 
 // ---------------------------------------------------------------------------
+// Activation quantisation: Q8A (det-quant lib.rs:111-137) per 32-element
+// block and Q8_K (lib.rs:139-172) per 256-element block.  One wave
+// quantises one 256-element span: lane l holds elements 4l..4l+3, so a Q8A
+// block is 8 lanes and a Q8_K block the whole wave; every reduction is a
+// wave shuffle.  Spans are whole Q8A blocks (n % 32 == 0) and, when Q8_K is
+// wanted, whole Q8_K blocks (n % 256 == 0).
+namespace {
+struct QuantOut {
+  int8_t* qa;
+  float* da;
+  float* af;
+  int8_t* qk;
+  float* dk;
+};
+
+// v: the lane's four elements; in: whether they exist; base: element offset
+// of the span (a multiple of 256 within the [T][n] array).
+__device__ __forceinline__ void quantize_span(const float v[4], bool in, size_t base, bool want_q8a,
+                                              bool want_q8k, const QuantOut& q) {
+  const int lane = threadIdx.x & 63;
+  const size_t off = base + 4 * lane;
+  float ax[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) ax[c] = v[c] < 0.0f ? -v[c] : v[c];
+  if (want_q8a) {
+    // amax over the 32-element block (max is order independent).
+    float amax = fmaxf(fmaxf(ax[0], ax[1]), fmaxf(ax[2], ax[3]));
+#pragma unroll
+    for (int m = 4; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
+    if (in) {
+      int8_t qv[4];
+      float fv[4];
+      float d = amax / 127.0f;
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        if (amax == 0.0f) {
+          qv[c] = 0;
+          fv[c] = 0.0f;
+        } else {
+          float y = v[c] / d;
+          int r = y < 0.0f ? f32_as_i32(y - 0.5f) : f32_as_i32(y + 0.5f);
+          r = r < -127 ? -127 : (r > 127 ? 127 : r);
+          qv[c] = (int8_t)r;
+          fv[c] = d * (float)r;
+        }
+      }
+      uint32_t packed = (uint32_t)(uint8_t)qv[0] | ((uint32_t)(uint8_t)qv[1] << 8) |
+                        ((uint32_t)(uint8_t)qv[2] << 16) | ((uint32_t)(uint8_t)qv[3] << 24);
+      *reinterpret_cast<uint32_t*>(q.qa + off) = packed;
+      *reinterpret_cast<float4*>(q.af + off) = make_float4(fv[0], fv[1], fv[2], fv[3]);
+      if ((lane & 7) == 0) q.da[off / 32] = amax == 0.0f ? 0.0f : d;
+    }
+  }
+  if (want_q8k) {
+    // Signed max: the first element with the strictly largest |x|.  Reduce
+    // (|x|, index, x) taking the larger |x| and, on ties, the smaller index.
+    float bx = -1.0f, bv = 0.0f;
+    int bi = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+      if (in && ax[c] > bx) {
+        bx = ax[c];
+        bv = v[c];
+        bi = 4 * lane + c;
+      }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      float ox = __shfl_xor(bx, m), ov = __shfl_xor(bv, m);
+      int oi = __shfl_xor(bi, m);
+      if (ox > bx || (ox == bx && oi < bi)) {
+        bx = ox;
+        bi = oi;
+        bv = ov;
+      }
+    }
+    float mx = bx == 0.0f ? 0.0f : bv;
+    if (in) {
+      // Stored class-major inside the 256-block (element e at (e % 8) * 32 + e / 8),
+      // the order the Q6_K kernels consume the eight lane sums in.
+      float iscale = -127.0f / mx;
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        int e = 4 * lane + c;
+        int r = 0;
+        if (mx != 0.0f) {
+          float val = iscale * v[c] + 12582912.0f;
+          r = (int)(f2u(val) & 0x007fffffu) - 0x00400000;
+          if (r > 127) r = 127;
+        }
+        q.qk[base + (e & 7) * 32 + (e >> 3)] = (int8_t)r;
+      }
+      if (lane == 0) q.dk[base / 256] = mx == 0.0f ? 0.0f : 1.0f / iscale;
+    }
+  }
+}
+}  // namespace
+
+// Four waves per workgroup, one 256-element span each.
+__global__ void __launch_bounds__(256) k_quantize(const float* x, int n, int want_q8a,
+                                                  int want_q8k, QuantOut q, int* err) {
+  const int t = blockIdx.y;
+  const int span = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int e = span * 256 + 4 * (threadIdx.x & 63);
+  const bool in = e < n;
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (in) {
+    float4 f = *reinterpret_cast<const float4*>(x + (size_t)t * n + e);
+    v[0] = f.x;
+    v[1] = f.y;
+    v[2] = f.z;
+    v[3] = f.w;
+    if (!finite(v[0]) || !finite(v[1]) || !finite(v[2]) || !finite(v[3]))
+      flag(err, ERRBIT_NON_FINITE);
+  }
+  if (span * 256 < n)
+    quantize_span(v, in, (size_t)t * n + (size_t)span * 256, want_q8a, want_q8k, q);
+}
+
+void launch_quantize(const float* x, int T, int n, bool want_q8a, bool want_q8k, int8_t* qa,
+                     float* da, float* af, int8_t* qk, float* dk, int* err, hipStream_t s) {
+  dim3 grid((n + 1023) / 1024, T);
+  QuantOut q{qa, da, af, qk, dk};
+  hipLaunchKernelGGL(k_quantize, grid, dim3(256), 0, s, x, n, (int)want_q8a, (int)want_q8k, q, err);
+}
+
+// ---------------------------------------------------------------------------
 // rmsnorm (det-model lib.rs:2053-2073): ss by 8 interleaved chains, r =
-// 1/sqrt(ss/n + eps), out = (x*r)*w.  One workgroup per position.
+// 1/sqrt(ss/n + eps), out = (x*r)*w.  One workgroup per position.  The
+// squares are formed in parallel and stored chain-major in LDS (chain c
+// holds x[c]^2, x[c+8]^2, ... contiguously), so each of the eight serial
+// chains streams float4 reads.  Optionally quantises the normalised row
+// (Q8A / Q8_K) in the same pass, one wave per 256-element span.
 __global__ void __launch_bounds__(256) k_rmsnorm(const float* x, const float* w, float eps, int n,
-                                                 float* out, int* err) {
+                                                 float* out, int want_q8a, int want_q8k,
+                                                 QuantOut q, int* err) {
+  extern __shared__ __align__(16) float xs[];  // [n] row, then [8][cs] squares
   __shared__ float lane_sum[8];
   __shared__ float r_sh;
-  int t = blockIdx.x;
+  const int t = blockIdx.x;
+  const int cs = (((n + 7) / 8) + 3) & ~3;    // per-chain stride, float4 aligned
+  float* sq = xs + ((n + 3) & ~3);
   const float* xr = x + (size_t)t * n;
   float* o = out + (size_t)t * n;
   bool bad = false;
-  for (int i = threadIdx.x; i < n; i += blockDim.x)
-    if (!finite(xr[i]) || !finite(w[i])) bad = true;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    float v = xr[i];
+    if (!finite(v) || !finite(w[i])) bad = true;
+    xs[i] = v;
+    sq[(i & 7) * cs + (i >> 3)] = v * v;
+  }
+  __syncthreads();
   if (threadIdx.x < 8) {
+    const int c = threadIdx.x;
+    const int cnt = (n - c + 7) / 8;  // elements c, c+8, ... below n
+    const float* my = sq + c * cs;
     float acc = 0.0f;
-    for (int i = threadIdx.x; i < n; i += 8) acc += xr[i] * xr[i];
-    lane_sum[threadIdx.x] = acc;
+    int k = 0;
+    for (; k + 4 <= cnt; k += 4) {
+      float4 f = *reinterpret_cast<const float4*>(my + k);
+      acc += f.x;
+      acc += f.y;
+      acc += f.z;
+      acc += f.w;
+    }
+    for (; k < cnt; k++) acc += my[k];
+    lane_sum[c] = acc;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -221,111 +373,49 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* x, const float* w,
     r_sh = r;
   }
   __syncthreads();
-  float r = r_sh;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    float v = (xr[i] * r) * w[i];
-    if (!finite(v)) bad = true;
-    o[i] = v;
+  const float r = r_sh;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int span = wave; span * 256 < n; span += 4) {
+    const int e0 = span * 256 + 4 * lane;
+    const bool in = e0 < n;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      int i = e0 + c;
+      if (i < n) {
+        v[c] = (xs[i] * r) * w[i];
+        if (!finite(v[c])) bad = true;
+        o[i] = v[c];
+      }
+    }
+    if (want_q8a || want_q8k)
+      quantize_span(v, in, (size_t)t * n + (size_t)span * 256, want_q8a, want_q8k, q);
   }
   if (bad) flag(err, ERRBIT_NON_FINITE);
 }
 
+size_t rmsnorm_smem(int n) {
+  return ((size_t)((n + 3) & ~3) + 8 * (size_t)((((n + 7) / 8) + 3) & ~3)) * sizeof(float);
+}
+
+void launch_rmsnorm_quant(const float* x, const float* w, float eps, int T, int n, float* out,
+                          bool want_q8a, bool want_q8k, int8_t* qa, float* da, float* af,
+                          int8_t* qk, float* dk, int* err, hipStream_t s) {
+  QuantOut q{qa, da, af, qk, dk};
+  static bool attr_set = false;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute((const void*)k_rmsnorm, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              150 * 1024);
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(256), rmsnorm_smem(n), s, x, w, eps, n, out,
+                     (int)want_q8a, (int)want_q8k, q, err);
+}
+
 void launch_rmsnorm(const float* x, const float* w, float eps, int T, int n, float* out, int* err,
                     hipStream_t s) {
-  hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(256), 0, s, x, w, eps, n, out, err);
-}
-
-// ---------------------------------------------------------------------------
-// Activation quantisation: Q8A (det-quant lib.rs:111-137) per 32-element
-// block and Q8_K (lib.rs:139-172) per 256-element block.  One workgroup of
-// 256 threads per 256 elements of one position.
-__global__ void __launch_bounds__(256) k_quantize(const float* x, int n, int want_q8a,
-                                                  int want_q8k, int8_t* qa, float* da, float* af,
-                                                  int8_t* qk, float* dk, int* err) {
-  int t = blockIdx.y;
-  int e = blockIdx.x * 256 + threadIdx.x;
-  bool in = e < n;
-  float v = in ? x[(size_t)t * n + e] : 0.0f;
-  if (in && !finite(v)) flag(err, ERRBIT_NON_FINITE);
-  float ax = v < 0.0f ? -v : v;
-  if (want_q8a) {
-    // amax over the 32-lane group (max is order independent).
-    float amax = ax;
-#pragma unroll
-    for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
-    if (in) {
-      size_t off = (size_t)t * n + e;
-      if (amax == 0.0f) {
-        qa[off] = 0;
-        af[off] = 0.0f;
-        if ((e & 31) == 0) da[off / 32] = 0.0f;
-      } else {
-        float d = amax / 127.0f;
-        float y = v / d;
-        int r = y < 0.0f ? f32_as_i32(y - 0.5f) : f32_as_i32(y + 0.5f);
-        r = r < -127 ? -127 : (r > 127 ? 127 : r);
-        qa[off] = (int8_t)r;
-        af[off] = d * (float)r;
-        if ((e & 31) == 0) da[off / 32] = d;
-      }
-    }
-  }
-  if (want_q8k) {
-    // Signed max: the first element with the strictly largest |x|.  Reduce
-    // (|x|, index) taking the larger |x| and, on ties, the smaller index.
-    __shared__ float s_ax[4];
-    __shared__ int s_idx[4];
-    __shared__ float s_max;
-    float bx = in ? ax : -1.0f;
-    int bi = threadIdx.x;
-    for (int m = 32; m >= 1; m >>= 1) {
-      float ox = __shfl_xor(bx, m);
-      int oi = __shfl_xor(bi, m);
-      if (ox > bx || (ox == bx && oi < bi)) {
-        bx = ox;
-        bi = oi;
-      }
-    }
-    int wave = threadIdx.x / 64;
-    if ((threadIdx.x & 63) == 0) {
-      s_ax[wave] = bx;
-      s_idx[wave] = bi;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float cx = s_ax[0];
-      int ci = s_idx[0];
-      for (int w = 1; w < 4; w++)
-        if (s_ax[w] > cx || (s_ax[w] == cx && s_idx[w] < ci)) {
-          cx = s_ax[w];
-          ci = s_idx[w];
-        }
-      s_max = cx == 0.0f ? 0.0f : x[(size_t)t * n + blockIdx.x * 256 + ci];
-    }
-    __syncthreads();
-    float mx = s_max;
-    if (in) {
-      size_t off = (size_t)t * n + e;
-      if (mx == 0.0f) {
-        qk[off] = 0;
-        if (threadIdx.x == 0) dk[off / 256] = 0.0f;
-      } else {
-        float iscale = -127.0f / mx;
-        float val = iscale * v + 12582912.0f;
-        int r = (int)(f2u(val) & 0x007fffffu) - 0x00400000;
-        if (r > 127) r = 127;
-        qk[off] = (int8_t)r;
-        if (threadIdx.x == 0) dk[off / 256] = 1.0f / iscale;
-      }
-    }
-  }
-}
-
-void launch_quantize(const float* x, int T, int n, bool want_q8a, bool want_q8k, int8_t* qa,
-                     float* da, float* af, int8_t* qk, float* dk, int* err, hipStream_t s) {
-  dim3 grid((n + 255) / 256, T);
-  hipLaunchKernelGGL(k_quantize, grid, dim3(256), 0, s, x, n, (int)want_q8a, (int)want_q8k, qa, da,
-                     af, qk, dk, err);
+  launch_rmsnorm_quant(x, w, eps, T, n, out, false, false, nullptr, nullptr, nullptr, nullptr,
+                       nullptr, err, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -372,6 +462,13 @@ __global__ void __launch_bounds__(256) k_gemm_rowlane(DevMat W, DevAct A, int T,
 
 void launch_gemm(const DevMat& W, const DevAct& A, int T, float* out, const float* bias, int epi,
                  int* err, hipStream_t s) {
+  // Chunks of positions take the token-parallel kernels (weights decoded once
+  // per wave and shared by up to 64 positions); short batches keep one lane
+  // per (row, position).
+  if (gemm_tok_supported(W) && (T >= 16 || (W.type == kGgmlQ6K && T >= 2))) {
+    launch_gemm_tok(W, A, T, out, bias, epi, err, s);
+    return;
+  }
   dim3 grid((W.rows + 255) / 256, T);
   hipLaunchKernelGGL(k_gemm_rowlane, grid, dim3(256), 0, s, W, A, T, out, bias, epi, err);
 }
@@ -491,9 +588,288 @@ __global__ void __launch_bounds__(64) k_attention(const float* q, const float* k
   if (bad) flag(err, ERRBIT_NON_FINITE);
 }
 
+// The same computation with the heads of one KV group in one workgroup
+// (one wave per head): K and V tiles of 64 positions are staged once in LDS
+// for the whole group, K transposed so lane j reads key j conflict-free.
+// Scores and probabilities of every head stay in LDS.
+constexpr int kAttnTile = 64;
+
+__global__ void __launch_bounds__(1024) k_attention_grp(const float* q, const float* kc,
+                                                        const float* vc, int layer, int pos0,
+                                                        int H, int KV, int hd, int n_ctx,
+                                                        float scale, float* out, int* err) {
+  extern __shared__ __align__(16) float smem[];
+  const int G = H / KV;
+  const int g = blockIdx.x, t = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int h = g * G + wave;
+  const int pos = pos0 + t, len = pos + 1;
+  const int nthreads = G * 64;
+  const float* keys = kc + ((size_t)layer * KV + g) * n_ctx * hd;
+  const float* vals = vc + ((size_t)layer * KV + g) * n_ctx * hd;
+  float* o = out + (size_t)t * H * hd + (size_t)h * hd;
+  if (len == 1) {  // a single score copies V exactly (lib.rs:2319-2321)
+    for (int dd = lane; dd < hd; dd += 64) o[dd] = vals[dd];
+    return;
+  }
+  float* sc = smem;                          // [G][n_ctx]
+  float* tile = sc + (size_t)G * n_ctx;      // K^T [hd][kAttnTile + 1] or V [kAttnTile][hd]
+  float* qs = tile + (kAttnTile + 1) * hd;   // [G][hd]
+  float* my = sc + (size_t)wave * n_ctx;
+  bool bad = false;
+  const float* qh = q + (size_t)t * H * hd + (size_t)h * hd;
+  for (int i = lane; i < hd; i += 64) qs[wave * hd + i] = qh[i];
+  // scores: dot_f32_ref(q, k_j) * scale
+  for (int j0 = 0; j0 < len; j0 += kAttnTile) {
+    int n = len - j0 < kAttnTile ? len - j0 : kAttnTile;
+    __syncthreads();
+    for (int x = threadIdx.x; x < n * hd; x += nthreads) {
+      int j = x / hd, i = x % hd;
+      tile[i * (kAttnTile + 1) + j] = keys[(size_t)(j0 + j) * hd + i];
+    }
+    __syncthreads();
+    if (lane < n) {
+      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      const float* qw = qs + wave * hd;
+      for (int i = 0; i < hd; i++) acc[i & 7] += qw[i] * tile[i * (kAttnTile + 1) + lane];
+      float s = finish_8lane(acc) * scale;
+      if (!finite(s)) bad = true;
+      my[j0 + lane] = s;
+    }
+  }
+  __syncthreads();
+  // softmax_in_place (lib.rs:2361-2388), per wave
+  float mx = -__builtin_huge_valf();
+  for (int j = lane; j < len; j += 64) mx = fmaxf(mx, my[j]);
+  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  for (int j = lane; j < len; j += 64) my[j] = exp_clamped(my[j] - mx);
+  __syncthreads();
+  float acc = 0.0f;
+  if (lane < 8)
+    for (int j = lane; j < len; j += 8) acc += my[j];
+  float part[8];
+#pragma unroll
+  for (int c = 0; c < 8; c++) part[c] = __shfl(acc, c);
+  float z = finish_8lane(part);
+  if (!finite(z) || z == 0.0f) bad = true;
+  for (int j = lane; j < len; j += 64) {
+    float p = my[j] / z;
+    if (!finite(p)) bad = true;
+    my[j] = p;
+  }
+  // P.V: out[d] = 0.0; out[d] += p_j * v_j[d] for j ascending
+  float av[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int j0 = 0; j0 < len; j0 += kAttnTile) {
+    int n = len - j0 < kAttnTile ? len - j0 : kAttnTile;
+    __syncthreads();
+    for (int x = threadIdx.x; x < n * hd; x += nthreads) tile[x] = vals[(size_t)j0 * hd + x];
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      int dd = lane + 64 * c;
+      if (dd < hd) {
+        float a = av[c];
+        for (int j = 0; j < n; j++) a += my[j0 + j] * tile[j * hd + dd];
+        av[c] = a;
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    int dd = lane + 64 * c;
+    if (dd < hd) {
+      if (!finite(av[c])) bad = true;
+      o[dd] = av[c];
+    }
+  }
+  if (bad) flag(err, ERRBIT_NON_FINITE);
+}
+
+// Head dimension 64 (every Llama/Qwen shape served here): the same
+// arithmetic as k_attention_grp, with the K/V tiles double-buffered in LDS
+// and the next tile's global loads issued before the current tile's chains
+// run, so HBM/L2 latency hides behind the multiply-adds.  q and p are read
+// as float4 broadcasts.  One workgroup per (KV group, position), one wave
+// per head of the group; kA64Per float4 of each tile per thread.
+constexpr int kA64Tile = 64;           // K/V rows per tile
+constexpr int kA64KStride = 65;        // K^T row stride (conflict-free column reads)
+constexpr int kA64Buf = 64 * kA64KStride;
+constexpr int kA64Per = 8;             // float4 loads per thread per tile (G >= 2)
+
+__global__ void __launch_bounds__(1024) k_attention_hd64(const float* q, const float* kc,
+                                                         const float* vc, int layer, int pos0,
+                                                         int H, int KV, int n_ctx, int sc_stride,
+                                                         float scale, float* out, int* err) {
+  extern __shared__ __align__(16) float smem[];
+  constexpr int hd = 64;
+  const int G = H / KV;
+  const int g = blockIdx.x, t = blockIdx.y;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int h = g * G + wave;
+  const int pos = pos0 + t, len = pos + 1;
+  const int nthreads = G * 64;
+  const float* keys = kc + ((size_t)layer * KV + g) * n_ctx * hd;
+  const float* vals = vc + ((size_t)layer * KV + g) * n_ctx * hd;
+  float* o = out + (size_t)t * H * hd + (size_t)h * hd;
+  if (len == 1) {  // a single score copies V exactly (lib.rs:2319-2321)
+    o[lane] = vals[lane];
+    return;
+  }
+  float* sc = smem;                                // [G][sc_stride]
+  float* tiles = sc + (size_t)G * sc_stride;       // [2][kA64Buf]
+  float* qs = tiles + 2 * kA64Buf;                 // [G][64]
+  float* my = sc + (size_t)wave * sc_stride;
+  bool bad = false;
+  qs[wave * hd + lane] = q[(size_t)t * H * hd + (size_t)h * hd + lane];
+  const int ntiles = (len + kA64Tile - 1) / kA64Tile;
+  float4 pre[kA64Per];
+  // Tile loads: float4 index x = threadIdx.x + c * nthreads covers rows
+  // x / 16, columns 4 * (x % 16); rows at or past len are not read.
+  auto issue = [&](const float* base, int j0) {
+#pragma unroll
+    for (int c = 0; c < kA64Per; c++) {
+      int x = threadIdx.x + c * nthreads;
+      int j = x >> 4;
+      if (x < 1024 && j0 + j < len)
+        pre[c] = *reinterpret_cast<const float4*>(base + (size_t)(j0 + j) * hd + (x & 15) * 4);
+    }
+  };
+  auto commit_k = [&](float* buf, int j0) {
+#pragma unroll
+    for (int c = 0; c < kA64Per; c++) {
+      int x = threadIdx.x + c * nthreads;
+      int j = x >> 4, i = (x & 15) * 4;
+      if (x < 1024 && j0 + j < len) {
+        buf[(i + 0) * kA64KStride + j] = pre[c].x;
+        buf[(i + 1) * kA64KStride + j] = pre[c].y;
+        buf[(i + 2) * kA64KStride + j] = pre[c].z;
+        buf[(i + 3) * kA64KStride + j] = pre[c].w;
+      }
+    }
+  };
+  auto commit_v = [&](float* buf, int j0) {
+#pragma unroll
+    for (int c = 0; c < kA64Per; c++) {
+      int x = threadIdx.x + c * nthreads;
+      if (x < 1024 && j0 + (x >> 4) < len) reinterpret_cast<float4*>(buf)[x] = pre[c];
+    }
+  };
+  // scores: dot_f32_ref(q, k_j) * scale
+  issue(keys, 0);
+  commit_k(tiles, 0);
+  __syncthreads();
+  for (int tI = 0; tI < ntiles; tI++) {
+    const int j0 = tI * kA64Tile;
+    float* cur = tiles + (tI & 1) * kA64Buf;
+    if (tI + 1 < ntiles) issue(keys, j0 + kA64Tile);
+    if (j0 + lane < len) {
+      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      const float4* qw = reinterpret_cast<const float4*>(qs + wave * hd);
+#pragma unroll
+      for (int i4 = 0; i4 < 16; i4++) {
+        float4 qv = qw[i4];
+        int i = i4 * 4;
+        acc[(i + 0) & 7] += qv.x * cur[(i + 0) * kA64KStride + lane];
+        acc[(i + 1) & 7] += qv.y * cur[(i + 1) * kA64KStride + lane];
+        acc[(i + 2) & 7] += qv.z * cur[(i + 2) * kA64KStride + lane];
+        acc[(i + 3) & 7] += qv.w * cur[(i + 3) * kA64KStride + lane];
+      }
+      float s = finish_8lane(acc) * scale;
+      if (!finite(s)) bad = true;
+      my[j0 + lane] = s;
+    }
+    if (tI + 1 < ntiles) commit_k(tiles + ((tI + 1) & 1) * kA64Buf, j0 + kA64Tile);
+    __syncthreads();
+  }
+  // First V tile loads overlap the softmax.
+  issue(vals, 0);
+  // softmax_in_place (lib.rs:2361-2388), per wave
+  float mx = -__builtin_huge_valf();
+  for (int j = lane; j < len; j += 64) mx = fmaxf(mx, my[j]);
+  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  for (int j = lane; j < len; j += 64) my[j] = exp_clamped(my[j] - mx);
+  __syncthreads();
+  float zacc = 0.0f;
+  if (lane < 8)
+    for (int j = lane; j < len; j += 8) zacc += my[j];
+  float part[8];
+#pragma unroll
+  for (int c = 0; c < 8; c++) part[c] = __shfl(zacc, c);
+  float z = finish_8lane(part);
+  if (!finite(z) || z == 0.0f) bad = true;
+  for (int j = lane; j < len; j += 64) {
+    float p = my[j] / z;
+    if (!finite(p)) bad = true;
+    my[j] = p;
+  }
+  commit_v(tiles, 0);
+  __syncthreads();
+  // P.V: out[d] = 0.0; out[d] += p_j * v_j[d] for j ascending
+  float a = 0.0f;
+  for (int tI = 0; tI < ntiles; tI++) {
+    const int j0 = tI * kA64Tile;
+    const int n = len - j0 < kA64Tile ? len - j0 : kA64Tile;
+    const float* cur = tiles + (tI & 1) * kA64Buf;
+    if (tI + 1 < ntiles) issue(vals, j0 + kA64Tile);
+    const float4* pw = reinterpret_cast<const float4*>(my + j0);
+    int j = 0;
+    for (; j + 4 <= n; j += 4) {
+      float4 pv = pw[j >> 2];
+      a += pv.x * cur[(j + 0) * hd + lane];
+      a += pv.y * cur[(j + 1) * hd + lane];
+      a += pv.z * cur[(j + 2) * hd + lane];
+      a += pv.w * cur[(j + 3) * hd + lane];
+    }
+    for (; j < n; j++) a += my[j0 + j] * cur[j * hd + lane];
+    if (tI + 1 < ntiles) commit_v(tiles + ((tI + 1) & 1) * kA64Buf, j0 + kA64Tile);
+    __syncthreads();
+  }
+  if (!finite(a)) bad = true;
+  o[lane] = a;
+  if (bad) flag(err, ERRBIT_NON_FINITE);
+}
+
+size_t attention_hd64_smem(int G, int sc_stride) {
+  return ((size_t)G * sc_stride + 2 * kA64Buf + (size_t)G * 64) * sizeof(float);
+}
+
+size_t attention_grp_smem(int H, int KV, int hd, int n_ctx) {
+  int G = H / KV;
+  return ((size_t)G * n_ctx + (size_t)(kAttnTile + 1) * hd + (size_t)G * hd) * sizeof(float);
+}
+
 void launch_attention(const float* q, const float* kc, const float* vc, int layer, int T, int pos0,
                       int H, int KV, int hd, int n_ctx, float scale, float* scores, float* out,
                       int* err, hipStream_t s) {
+  int G = H / KV;
+  if (hd == 64 && G >= 2 && G <= 16) {
+    // Scores only need the longest row of this chunk (rounded to float4).
+    int sc_stride = ((pos0 + T) + 3) & ~3;
+    size_t smem64 = attention_hd64_smem(G, sc_stride);
+    if (smem64 <= 150 * 1024) {
+      static bool attr64_set = false;
+      if (!attr64_set) {
+        (void)hipFuncSetAttribute((const void*)k_attention_hd64,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
+        attr64_set = true;
+      }
+      hipLaunchKernelGGL(k_attention_hd64, dim3(KV, T), dim3(G * 64), smem64, s, q, kc, vc, layer,
+                         pos0, H, KV, n_ctx, sc_stride, scale, out, err);
+      return;
+    }
+  }
+  size_t smem = attention_grp_smem(H, KV, hd, n_ctx);
+  if (G <= 16 && hd <= 256 && smem <= 150 * 1024) {
+    static bool attr_set = false;
+    if (!attr_set) {
+      (void)hipFuncSetAttribute((const void*)k_attention_grp,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
+      attr_set = true;
+    }
+    hipLaunchKernelGGL(k_attention_grp, dim3(KV, T), dim3(G * 64), smem, s, q, kc, vc, layer, pos0,
+                       H, KV, hd, n_ctx, scale, out, err);
+    return;
+  }
   hipLaunchKernelGGL(k_attention, dim3(H, T), dim3(64), 0, s, q, kc, vc, layer, pos0, H, KV, hd,
                      n_ctx, scale, scores, out, err);
 }

@@ -60,6 +60,11 @@ def test_tiny_workload_matches_oracle_all_chunks():
     ("smollm2", 4, 5, 2),
     ("qwen05", 3, 5, 3),
     ("tinyllama", 2, 4, 4),
+    # chunks of >= 16 positions run the token-parallel kernels (and the fused
+    # gate/up/SwiGLU pass for Q4_K), including a partial final chunk
+    ("smollm2", 2, 40, 32),
+    ("qwen05", 1, 21, 21),
+    ("tinyllama", 1, 70, 64),
 ])
 def test_baseline_shapes_match_oracle(name, layers, n_tok, chunk):
     from detllm_amd import synth
@@ -67,6 +72,16 @@ def test_baseline_shapes_match_oracle(name, layers, n_tok, chunk):
     w = synth.WORKLOADS[name]
     data = synth.build_model(w, layers=layers)
     _compare_with_oracle(data, synth.tokens(w, n_tok), chunk)
+
+
+def test_packed_q4k_chunk_path_matches_oracle(monkeypatch):
+    # Without the f32 weight copies the chunked Q4_K GEMM decodes the packed
+    # superblocks itself; both paths must give the reference bits.
+    from detllm_amd import synth
+
+    monkeypatch.setenv("DETLLM_NO_F32_MIRROR", "1")
+    w = synth.WORKLOADS["tinyllama"]
+    _compare_with_oracle(synth.build_model(w, layers=1), synth.tokens(w, 40), 40)
 
 
 def test_repeat_runs_are_bitwise_identical():

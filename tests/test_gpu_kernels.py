@@ -110,10 +110,27 @@ def test_quantize_q8a_q8k_bitexact():
         assert np.array_equal(qk[r * n:(r + 1) * n], kq)
 
 
+def test_quantize_q8a_only_partial_span():
+    # 896 = 3.5 spans of 256: the last wave quantises half a span.
+    L = _lib()
+    rng = np.random.default_rng(5)
+    rows, n = 3, 896
+    x = rng.normal(0, 1, (rows, n)).astype(np.float32)
+    x[1, 864:] = 0.0
+    da = np.empty(rows * n // 32, np.float32)
+    qa = np.empty(rows * n, np.int8)
+    L.check(L.lib.dtl_kernel_quantize(_p(x, C.c_float), rows, n, _p(da, C.c_float), _p(qa, C.c_int8),
+                                      None, None), "quantize")
+    for r in range(rows):
+        wd, wq = detref.quantize_q8a(x[r])
+        assert np.array_equal(da[r * n // 32:(r + 1) * n // 32].view(np.uint32), wd.view(np.uint32))
+        assert np.array_equal(qa[r * n:(r + 1) * n], wq)
+
+
 def test_rmsnorm_bitexact():
     L = _lib()
     rng = np.random.default_rng(4)
-    for n, eps in [(64, 1e-5), (576, 1e-5), (896, 1e-6), (2048, 1e-5), (13, 1e-5)]:
+    for n, eps in [(64, 1e-5), (576, 1e-5), (896, 1e-6), (2048, 1e-5), (13, 1e-5), (4, 1e-5), (16384, 1e-5)]:
         x = rng.normal(0, 30, (3, n)).astype(np.float32)
         w = rng.normal(1, 0.02, n).astype(np.float32)
         out = np.empty_like(x)
