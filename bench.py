@@ -37,8 +37,59 @@ FP32_VECTOR_PEAK_TFLOPS = 157.3        # packed FMA rate
 FP32_UNFUSED_ISSUE_PEAK_TOPS = 39.3
 
 
+# HBM bytes per launch of the dominant kernel, from two rocprofv3 --pmc
+# passes over this script's default run (FETCH_SIZE, then WRITE_SIZE, KiB
+# per dispatch averaged over the kernel's dispatches), each multiplied by
+# the factor that maps the same counter onto the known bytes of a plain
+# copy (--copy-probe-mib).  Keyed by kernel class; the summaries sit in
+# profiles/ under the same name.
+MEASURED_TRAFFIC = {}
+
+
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
+
+
+def copy_probe(mib: int) -> int:
+    """A plain device copy of known size (calibrates rocprofv3's HBM counters)."""
+    import torch
+
+    n = mib * 1024 * 1024 // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_read": n * 4, "copy_probe_bytes_written": n * 4, "launches": 5}))
+    return 0
+
+
+def decode_leg(model, toks, positions: int) -> dict:
+    """Single-position decode (forward_one) over the first positions of the
+    workload: tokens/s and the achieved HBM bandwidth of the GEMV classes."""
+    with model.forward_workspace(len(toks), 1) as s:
+        s.forward_one(int(toks[0]), 0)  # warm-up
+        s.reset()
+        s.set_profiling(True)
+        t = time.perf_counter()
+        for p in range(positions):
+            s.forward_one(int(toks[p]), p)
+        dt = time.perf_counter() - t
+        prof = s.profile()
+    gemv = {}
+    for k, v in prof.items():
+        if k.startswith("gemm_") and v["total_ms"] > 0:
+            gbs = v["bytes"] / (v["total_ms"] * 1e-3) / 1e9
+            gemv[k] = {"achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": round(gbs / HBM_PEAK_GBS, 4),
+                       "avg_launch_us": round(v["total_ms"] * 1e3 / v["launches"], 2),
+                       "algorithmic_bytes_per_launch": v["bytes"] / v["launches"]}
+    tot_b = sum(prof[k]["bytes"] for k in gemv)
+    tot_ms = sum(prof[k]["total_ms"] for k in gemv)
+    return {"positions": positions, "tokens_per_s": round(positions / dt, 2),
+            "gemv_all": {"achieved": round(tot_b / (tot_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(tot_b / (tot_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+            "gemv": gemv}
 
 
 def main() -> int:
@@ -47,16 +98,21 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--workload", default="tinyllama")
-    ap.add_argument("--cpu-tokens", type=int, default=16)
+    ap.add_argument("--cpu-tokens", type=int, default=96)
+    ap.add_argument("--decode-positions", type=int, default=64)
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run a plain copy of this many MiB (counter calibration) and exit")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-kib", default=None,
                     help="FETCH_KiB,WRITE_KiB per launch of the dominant kernel from rocprofv3 --pmc")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "the multi-GPU design is described in DESIGN.md", file=sys.stderr)
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus})",
+              file=sys.stderr)
         return 2
+    if args.copy_probe_mib:
+        return copy_probe(args.copy_probe_mib)
 
     import numpy as np
 
@@ -127,6 +183,9 @@ def main() -> int:
     if args.traffic_kib:
         fk, wk = (float(v) for v in args.traffic_kib.split(","))
         roofline["traffic"] = (fk + wk) * 1024.0
+    elif dom_name in MEASURED_TRAFFIC:
+        roofline["traffic"] = MEASURED_TRAFFIC[dom_name]["bytes"]
+        roofline["traffic_source"] = MEASURED_TRAFFIC[dom_name]["source"]
     else:
         roofline["traffic"] = None
     kernels = {k: {"ms_per_step": round(v["total_ms"] / args.steps, 3), "launches_per_step": v["launches"] // args.steps}
@@ -148,6 +207,11 @@ def main() -> int:
         lg = s2.forward_chunk(toks[:check_n], 0, want_logits=True)
     parity &= bool(np.array_equal(lg.view(np.uint32), ref_logits.view(np.uint32)))
     log(f"[bench] parity vs oracle on {check_n} positions: {parity}; deterministic: {deterministic}")
+
+    decode = None
+    if args.decode_positions > 0:
+        decode = decode_leg(model, toks, args.decode_positions)
+        log(f"[bench] decode {decode['tokens_per_s']} tok/s, GEMV {decode['gemv_all']['achieved']} GB/s")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -186,6 +250,7 @@ def main() -> int:
         "parity_vs_oracle": parity,
         "deterministic": deterministic,
         "kernels": kernels,
+        "decode": decode,
     }
     print(json.dumps(line), flush=True)
     return 0 if parity and deterministic else 1

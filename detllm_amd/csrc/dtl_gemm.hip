@@ -353,54 +353,61 @@ __global__ void __launch_bounds__(256) k_q4k_f32w(const float* __restrict__ W0,
   // Each thread moves four float4 of every 64x64 activation tile: the global
   // loads for the next tile are issued before the current tile is consumed
   // and written to LDS only afterwards, so their latency overlaps the math.
+  // Float4 j of thread x covers position (x + 256 j) / 16, column 4 ((x + 256 j) % 16).
   constexpr int PER = 64 * SL / 4 / 256;
-  int tk_[PER], c4_[PER];
+  static_assert(PER == 4, "tile mapping assumes 4 float4 per thread");
+  const int tk0 = threadIdx.x >> 4, c40 = threadIdx.x & 15;
+  const float* asrc[PER];
 #pragma unroll
   for (int j = 0; j < PER; j++) {
-    int x = threadIdx.x + j * 256;
-    tk_[j] = x / (SL / 4);
-    c4_[j] = x % (SL / 4);
+    int tt = tbase + tk0 + 16 * j;
+    asrc[j] = af + (size_t)(tt < T ? tt : T - 1) * cols + c40 * 4;
   }
-  float4 pre[PER];
-  auto issue = [&](int e0) {
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-      int tt = tbase + tk_[j] < T ? tbase + tk_[j] : T - 1;
-      pre[j] = *(const float4*)(af + (size_t)tt * cols + e0 + c4_[j] * 4);
-    }
-  };
-  auto commit = [&](int b) {
-#pragma unroll
-    for (int j = 0; j < PER; j++) *(float4*)&at[b][tk_[j]][c4_[j] * 4] = pre[j];
-  };
+  float4 p0, p1, p2, p3;
+#define DTL_ISSUE(e0)                                          \
+  do {                                                         \
+    p0 = *(const float4*)(asrc[0] + (e0));                     \
+    p1 = *(const float4*)(asrc[1] + (e0));                     \
+    p2 = *(const float4*)(asrc[2] + (e0));                     \
+    p3 = *(const float4*)(asrc[3] + (e0));                     \
+  } while (0)
+#define DTL_COMMIT(b)                                          \
+  do {                                                         \
+    *(float4*)&at[b][tk0][c40 * 4] = p0;                       \
+    *(float4*)&at[b][tk0 + 16][c40 * 4] = p1;                  \
+    *(float4*)&at[b][tk0 + 32][c40 * 4] = p2;                  \
+    *(float4*)&at[b][tk0 + 48][c40 * 4] = p3;                  \
+  } while (0)
   // The wave's own weight rows go through LDS the same way (lane -> one
   // float4 of one row) and are read back as broadcasts.
   const int wk = lane >> 4, wc4 = lane & 15;
   const bool wlane = wk < NM * NK;
-  const float* wsrc = nullptr;
+  const float* wsrc = W0;
   if (wlane) {
     int m = wk / NK, kk = wk % NK;
     int row = row0 + kk < rows ? row0 + kk : rows - 1;
     wsrc = (m ? W1 : W0) + (size_t)row * cols + wc4 * 4;
   }
   float4 wpre = make_float4(0.f, 0.f, 0.f, 0.f);
-  auto issue_w = [&](int e0) {
-    if (wlane) wpre = *(const float4*)(wsrc + e0);
-  };
-  auto commit_w = [&](int b) {
-    if (wlane) *(float4*)&wt[b][wave][wk][wc4 * 4] = wpre;
-  };
-  issue(0);
-  issue_w(0);
-  commit(0);
-  commit_w(0);
+#define DTL_ISSUE_W(e0)                                        \
+  do {                                                         \
+    if (wlane) wpre = *(const float4*)(wsrc + (e0));           \
+  } while (0)
+#define DTL_COMMIT_W(b)                                        \
+  do {                                                         \
+    if (wlane) *(float4*)&wt[b][wave][wk][wc4 * 4] = wpre;     \
+  } while (0)
+  DTL_ISSUE(0);
+  DTL_ISSUE_W(0);
+  DTL_COMMIT(0);
+  DTL_COMMIT_W(0);
   __syncthreads();
   int buf = 0;
   for (int e0 = 0; e0 < cols; e0 += SL) {
     const bool more = e0 + SL < cols;
     if (more) {
-      issue(e0 + SL);
-      issue_w(e0 + SL);
+      DTL_ISSUE(e0 + SL);
+      DTL_ISSUE_W(e0 + SL);
     }
 #pragma unroll 4
     for (int i = 0; i < SL; i += 4) {
@@ -417,8 +424,8 @@ __global__ void __launch_bounds__(256) k_q4k_f32w(const float* __restrict__ W0,
       }
     }
     if (more) {
-      commit(buf ^ 1);
-      commit_w(buf ^ 1);
+      DTL_COMMIT(buf ^ 1);
+      DTL_COMMIT_W(buf ^ 1);
     }
     __syncthreads();
     buf ^= 1;
@@ -441,6 +448,11 @@ __global__ void __launch_bounds__(256) k_q4k_f32w(const float* __restrict__ W0,
   }
   if (!ok) flag(err, ERRBIT_NON_FINITE);
 }
+
+#undef DTL_ISSUE
+#undef DTL_COMMIT
+#undef DTL_ISSUE_W
+#undef DTL_COMMIT_W
 
 // Exact f32 copy of a Q4_K matrix: q4_k_value for every element.
 __global__ void k_dequant_q4k(DevMat W, float* out) {
