@@ -440,9 +440,15 @@ namespace {
 // q4_k_value computes), used by the chunked-encode GEMM.  Skipped when the
 // device lacks room for them or DETLLM_NO_F32_MIRROR is set; the packed
 // kernels then serve every chunk size.
-int build_f32_mirrors(dtl_model* m) {
+// DETLLM_NO_F32_MIRROR=1 keeps Q4_K matrices packed only (the GEMMs then
+// decode the superblocks themselves).
+bool f32_mirror_enabled() {
   const char* off = getenv("DETLLM_NO_F32_MIRROR");
-  if (off && *off && *off != '0') return DTL_OK;
+  return !(off && *off && *off != '0');
+}
+
+int build_f32_mirrors(dtl_model* m) {
+  if (!f32_mirror_enabled()) return DTL_OK;
   std::vector<DevMat*> mats;
   for (Layer& L : m->layers)
     for (DevMat* M : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down})
@@ -1331,6 +1337,13 @@ int dtl_kernel_gemv(int ggml_type, const uint8_t* weights, size_t rows, size_t c
   if (g.tensor("w", &gt) != GgufError::None) return DTL_ERR_GGUF;
   DevMat W;
   if ((st = upload_matrix(g, *gt, rows, cols, sc.arena, &W))) return st;
+  if (W.type == GGML_Q4_K && f32_mirror_enabled()) {
+    // Same exact f32 copy a loaded model keeps.
+    float* w32;
+    if ((st = sc.arena.alloc(&w32, rows * cols))) return st;
+    launch_dequant_q4k(W, w32, sc.stream);
+    W.w32 = w32;
+  }
   float *dx, *dout, *af, *da, *dk;
   int8_t *qa, *qk;
   if ((st = sc.arena.upload(&dx, x, T * cols))) return st;

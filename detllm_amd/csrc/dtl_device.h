@@ -67,6 +67,10 @@ void launch_quantize(const float* x, int T, int n, bool want_q8a, bool want_q8k,
                      float* da, float* af, int8_t* qk, float* dk, int* err, hipStream_t s);
 void launch_gemm(const DevMat& W, const DevAct& A, int T, float* out, const float* bias, int epi,
                  int* err, hipStream_t s);
+// Decode GEMVs (dtl_gemv.hip) for a few positions; false when the matrix
+// shape or type has no GEMV kernel.
+bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const float* bias, int epi,
+                 int* err, hipStream_t s);
 // Token-parallel GEMMs (dtl_gemm.hip) for chunks of positions.
 bool gemm_tok_supported(const DevMat& W);
 void launch_gemm_tok(const DevMat& W, const DevAct& A, int T, float* out, const float* bias,

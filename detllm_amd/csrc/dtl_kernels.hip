@@ -460,6 +460,10 @@ __global__ void __launch_bounds__(256) k_gemm_rowlane(DevMat W, DevAct A, int T,
   out[o] = v;
 }
 
+// Up to this many positions the decode GEMVs (weights streamed once per
+// position) beat the row-lane kernel.
+constexpr int kGemvMaxT = 8;
+
 void launch_gemm(const DevMat& W, const DevAct& A, int T, float* out, const float* bias, int epi,
                  int* err, hipStream_t s) {
   // Chunks of positions take the token-parallel kernels (weights decoded once
@@ -469,6 +473,7 @@ void launch_gemm(const DevMat& W, const DevAct& A, int T, float* out, const floa
     launch_gemm_tok(W, A, T, out, bias, epi, err, s);
     return;
   }
+  if (T <= kGemvMaxT && launch_gemv(W, A, T, out, bias, epi, err, s)) return;
   dim3 grid((W.rows + 255) / 256, T);
   hipLaunchKernelGGL(k_gemm_rowlane, grid, dim3(256), 0, s, W, A, T, out, bias, epi, err);
 }

@@ -139,12 +139,16 @@ def test_rmsnorm_bitexact():
             assert np.array_equal(out[r].view(np.uint32), detref.rmsnorm(x[r], w, eps).view(np.uint32))
 
 
+# (type, rows, cols, positions): T <= 8 runs the decode GEMVs (rows per wave
+# grows with the row count: Q8_0/Q4_0 1/2/4/8, Q6_K 64/nsb, Q4_K 8/32),
+# T = 64 the token-parallel GEMMs, T in between the row-lane kernel.
 GEMV_CASES = [
     (0, 37, 64, 3), (0, 20, 128, 1),
-    (8, 61, 576, 1), (8, 33, 896, 5), (8, 9, 4864, 2),
-    (2, 40, 64, 2), (2, 17, 512, 1),
-    (12, 45, 2048, 1), (12, 7, 5632, 3), (12, 30, 512, 64),
-    (14, 50, 2048, 1), (14, 9, 5632, 2), (14, 20, 512, 64),
+    (8, 61, 576, 1), (8, 33, 896, 5), (8, 9, 4864, 2), (8, 5000, 64, 1), (8, 17000, 64, 2),
+    (8, 66000, 32, 1), (8, 300, 8192, 1), (8, 20, 576, 12),
+    (2, 40, 64, 2), (2, 17, 512, 1), (2, 66000, 64, 1), (2, 5000, 96, 3),
+    (12, 45, 2048, 1), (12, 7, 5632, 3), (12, 30, 512, 64), (12, 9000, 256, 1), (12, 13, 256, 8),
+    (14, 50, 2048, 1), (14, 9, 5632, 2), (14, 20, 512, 64), (14, 300, 256, 1), (14, 33, 4096, 1),
 ]
 
 
