@@ -43,7 +43,10 @@ FP32_UNFUSED_ISSUE_PEAK_TOPS = 39.3
 # the factor that maps the same counter onto the known bytes of a plain
 # copy (--copy-probe-mib).  Keyed by kernel class; the summaries sit in
 # profiles/ under the same name.
-MEASURED_TRAFFIC = {}
+MEASURED_TRAFFIC = {
+    "gemm_q4_k": {"bytes": (11278.7 * 2.000 + 384.0 * 1.000) * 1024.0,
+                  "source": "profiles/k_q4k_f32w_tinyllama_encode_chunk64.md"},
+}
 
 
 def log(msg: str) -> None:

@@ -479,7 +479,14 @@ int build_f32_mirrors(dtl_model* m) {
 
 namespace {
 
-// Event timing of every launch on the session stream, grouped by kernel class.
+}  // namespace
+
+thread_local dtl::LaunchTiming* dtl::tl_timing = nullptr;
+
+namespace {
+
+// Timing of every launch on the session stream, grouped by kernel class:
+// the events are bound to the kernels themselves (first start .. last end).
 class Profiler {
  public:
   bool on = false;
@@ -500,11 +507,12 @@ class Profiler {
       launch();
       return;
     }
-    hipEvent_t a = take(), b = take();
-    (void)hipEventRecord(a, s);
+    (void)s;
+    LaunchTiming lt{take(), take(), false};
+    tl_timing = &lt;
     launch();
-    (void)hipEventRecord(b, s);
-    pending_.push_back({name, a, b, bytes, macs});
+    tl_timing = nullptr;
+    if (lt.launched) pending_.push_back({name, lt.start, lt.stop, bytes, macs});
   }
   // Called after the stream has been synchronised.
   void collect() {
@@ -611,7 +619,7 @@ int read_err(dtl_session* s, int* bits) {
 
 __global__ void k_clear_flag(int* p) { *p = 0; }
 
-void clear_err(dtl_session* s) { hipLaunchKernelGGL(k_clear_flag, dim3(1), dim3(1), 0, s->stream, s->err); }
+void clear_err(dtl_session* s) { launch_kernel(k_clear_flag, dim3(1), dim3(1), 0, s->stream, s->err); }
 
 // Which activation forms the given consumers need.
 void needed_forms(std::initializer_list<const DevMat*> consumers, bool* q8a, bool* q8k) {

@@ -2,10 +2,36 @@
 // translation units.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace dtl {
+
+// Kernel-boundary timing.  While a LaunchTiming is installed on the calling
+// thread, launch_kernel binds `start` to the first kernel's start and `stop`
+// to the last kernel's end (hipExtLaunchKernel events carry the kernels' own
+// timestamps, so the interval excludes launch overhead).
+struct LaunchTiming {
+  hipEvent_t start, stop;
+  bool launched;
+};
+extern thread_local LaunchTiming* tl_timing;
+
+template <typename... KArgs, typename... Args>
+inline void launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t smem,
+                          hipStream_t stream, Args&&... args) {
+  if (LaunchTiming* lt = tl_timing) {
+    hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)smem, stream,
+                          lt->launched ? nullptr : lt->start, lt->stop, 0u,
+                          std::forward<Args>(args)...);
+    lt->launched = true;
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, smem, stream, std::forward<Args>(args)...);
+  }
+}
 
 // Sticky device error bits, OR-ed into the session's flag word and read at
 // synchronisation points (the reference returns the matching error on the

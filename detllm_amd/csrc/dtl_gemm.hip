@@ -475,7 +475,7 @@ __global__ void k_dequant_q4k(DevMat W, float* out) {
 
 void launch_dequant_q4k(const DevMat& W, float* out, hipStream_t s) {
   size_t total = (size_t)W.rows * W.cols;
-  hipLaunchKernelGGL(k_dequant_q4k, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, W, out);
+  launch_kernel(k_dequant_q4k, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, W, out);
 }
 
 // ---------------------------------------------------------------------------
@@ -510,11 +510,11 @@ void launch_q4k_f32w(const DevMat& W0, const DevMat& W1, const DevAct& A, int T,
   dim3 block(kWaves * 64);
   const float* w1 = PAIR ? W1.w32 : nullptr;
   if (nk == 4)
-    hipLaunchKernelGGL((k_q4k_f32w<4, PAIR>), grid, block, 0, s, W0.w32, w1, W0.rows, W0.cols, A.af, T, out, nullptr, ffo, bias, epi, err);
+    launch_kernel((k_q4k_f32w<4, PAIR>), grid, block, 0, s, W0.w32, w1, W0.rows, W0.cols, A.af, T, out, nullptr, ffo, bias, epi, err);
   else if (nk == 2)
-    hipLaunchKernelGGL((k_q4k_f32w<2, PAIR>), grid, block, 0, s, W0.w32, w1, W0.rows, W0.cols, A.af, T, out, nullptr, ffo, bias, epi, err);
+    launch_kernel((k_q4k_f32w<2, PAIR>), grid, block, 0, s, W0.w32, w1, W0.rows, W0.cols, A.af, T, out, nullptr, ffo, bias, epi, err);
   else
-    hipLaunchKernelGGL((k_q4k_f32w<1, PAIR>), grid, block, 0, s, W0.w32, w1, W0.rows, W0.cols, A.af, T, out, nullptr, ffo, bias, epi, err);
+    launch_kernel((k_q4k_f32w<1, PAIR>), grid, block, 0, s, W0.w32, w1, W0.rows, W0.cols, A.af, T, out, nullptr, ffo, bias, epi, err);
 }
 }  // namespace
 
@@ -535,27 +535,27 @@ void launch_gemm_tok(const DevMat& W, const DevAct& A, int T, float* out, const 
   switch (W.type) {
     case kGgmlQ4K:
       if (R == 4)
-        hipLaunchKernelGGL((k_q4k_tok<4, false>), grid, block, 0, s, W, none, A.af, T, out, nullptr, nullptr, bias, epi, err);
+        launch_kernel((k_q4k_tok<4, false>), grid, block, 0, s, W, none, A.af, T, out, nullptr, nullptr, bias, epi, err);
       else if (R == 2)
-        hipLaunchKernelGGL((k_q4k_tok<2, false>), grid, block, 0, s, W, none, A.af, T, out, nullptr, nullptr, bias, epi, err);
+        launch_kernel((k_q4k_tok<2, false>), grid, block, 0, s, W, none, A.af, T, out, nullptr, nullptr, bias, epi, err);
       else
-        hipLaunchKernelGGL((k_q4k_tok<1, false>), grid, block, 0, s, W, none, A.af, T, out, nullptr, nullptr, bias, epi, err);
+        launch_kernel((k_q4k_tok<1, false>), grid, block, 0, s, W, none, A.af, T, out, nullptr, nullptr, bias, epi, err);
       break;
     case kGgmlQ6K:
       if (R == 4)
-        hipLaunchKernelGGL((k_q6k_tok<4>), grid, block, 0, s, W, A.qk, A.dk, T, out, bias, epi, err);
+        launch_kernel((k_q6k_tok<4>), grid, block, 0, s, W, A.qk, A.dk, T, out, bias, epi, err);
       else if (R == 2)
-        hipLaunchKernelGGL((k_q6k_tok<2>), grid, block, 0, s, W, A.qk, A.dk, T, out, bias, epi, err);
+        launch_kernel((k_q6k_tok<2>), grid, block, 0, s, W, A.qk, A.dk, T, out, bias, epi, err);
       else
-        hipLaunchKernelGGL((k_q6k_tok<1>), grid, block, 0, s, W, A.qk, A.dk, T, out, bias, epi, err);
+        launch_kernel((k_q6k_tok<1>), grid, block, 0, s, W, A.qk, A.dk, T, out, bias, epi, err);
       break;
     default:
       if (R == 4)
-        hipLaunchKernelGGL((k_q8_0_tok<4>), grid, block, 0, s, W, A.qa, A.da, T, out, bias, epi, err);
+        launch_kernel((k_q8_0_tok<4>), grid, block, 0, s, W, A.qa, A.da, T, out, bias, epi, err);
       else if (R == 2)
-        hipLaunchKernelGGL((k_q8_0_tok<2>), grid, block, 0, s, W, A.qa, A.da, T, out, bias, epi, err);
+        launch_kernel((k_q8_0_tok<2>), grid, block, 0, s, W, A.qa, A.da, T, out, bias, epi, err);
       else
-        hipLaunchKernelGGL((k_q8_0_tok<1>), grid, block, 0, s, W, A.qa, A.da, T, out, bias, epi, err);
+        launch_kernel((k_q8_0_tok<1>), grid, block, 0, s, W, A.qa, A.da, T, out, bias, epi, err);
       break;
   }
 }
@@ -570,9 +570,9 @@ void launch_gemm_pair_swiglu_q4k(const DevMat& G, const DevMat& U, const DevAct&
   dim3 grid((G.rows + kWaves * R - 1) / (kWaves * R), (T + 63) / 64);
   dim3 block(kWaves * 64);
   if (R == 2)
-    hipLaunchKernelGGL((k_q4k_tok<2, true>), grid, block, 0, s, G, U, A.af, T, g, u, ffo, nullptr, 0, err);
+    launch_kernel((k_q4k_tok<2, true>), grid, block, 0, s, G, U, A.af, T, g, u, ffo, nullptr, 0, err);
   else
-    hipLaunchKernelGGL((k_q4k_tok<1, true>), grid, block, 0, s, G, U, A.af, T, g, u, ffo, nullptr, 0, err);
+    launch_kernel((k_q4k_tok<1, true>), grid, block, 0, s, G, U, A.af, T, g, u, ffo, nullptr, 0, err);
 }
 
 }  // namespace dtl

@@ -295,13 +295,13 @@ void launch_q8(const DevMat& W, const DevAct& A, int T, float* out, const float*
   size_t smem = (size_t)4 * R * W.nb * sizeof(float);
   dim3 grid((W.rows + 4 * R - 1) / (4 * R), T);
   if (R == 8)
-    hipLaunchKernelGGL((k_gemv_q8<TYPE, 8>), grid, dim3(256), smem, s, W, A.qa, A.da, out, bias, epi, err);
+    launch_kernel((k_gemv_q8<TYPE, 8>), grid, dim3(256), smem, s, W, A.qa, A.da, out, bias, epi, err);
   else if (R == 4)
-    hipLaunchKernelGGL((k_gemv_q8<TYPE, 4>), grid, dim3(256), smem, s, W, A.qa, A.da, out, bias, epi, err);
+    launch_kernel((k_gemv_q8<TYPE, 4>), grid, dim3(256), smem, s, W, A.qa, A.da, out, bias, epi, err);
   else if (R == 2)
-    hipLaunchKernelGGL((k_gemv_q8<TYPE, 2>), grid, dim3(256), smem, s, W, A.qa, A.da, out, bias, epi, err);
+    launch_kernel((k_gemv_q8<TYPE, 2>), grid, dim3(256), smem, s, W, A.qa, A.da, out, bias, epi, err);
   else
-    hipLaunchKernelGGL((k_gemv_q8<TYPE, 1>), grid, dim3(256), smem, s, W, A.qa, A.da, out, bias, epi, err);
+    launch_kernel((k_gemv_q8<TYPE, 1>), grid, dim3(256), smem, s, W, A.qa, A.da, out, bias, epi, err);
 }
 }  // namespace
 
@@ -323,7 +323,7 @@ bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const floa
     if (W.nb > 64) return false;
     int rpw = 64 / W.nb;
     dim3 grid((W.rows + rpw - 1) / rpw, T);
-    hipLaunchKernelGGL(k_gemv_q6k, grid, dim3(64), 0, s, W, A.qk, A.dk, out, bias, epi, err);
+    launch_kernel(k_gemv_q6k, grid, dim3(64), 0, s, W, A.qk, A.dk, out, bias, epi, err);
     return true;
   }
   if (W.type == kGgmlQ4K && W.w32 && W.cols % 256 == 0) {
@@ -331,9 +331,9 @@ bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const floa
     // enough to use every CU.
     dim3 grid8((W.rows + 7) / 8, T), grid32((W.rows + 31) / 32, T);
     if (W.rows <= 8192)
-      hipLaunchKernelGGL(k_gemv_q4k<8>, grid8, dim3(64), 0, s, W.w32, W.rows, W.cols, A.af, out, bias, epi, err);
+      launch_kernel(k_gemv_q4k<8>, grid8, dim3(64), 0, s, W.w32, W.rows, W.cols, A.af, out, bias, epi, err);
     else
-      hipLaunchKernelGGL(k_gemv_q4k<32>, grid32, dim3(64), 0, s, W.w32, W.rows, W.cols, A.af, out, bias, epi, err);
+      launch_kernel(k_gemv_q4k<32>, grid32, dim3(64), 0, s, W.w32, W.rows, W.cols, A.af, out, bias, epi, err);
     return true;
   }
   return false;

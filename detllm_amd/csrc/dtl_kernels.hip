@@ -193,7 +193,7 @@ __global__ void k_embed(DevMat E, const uint32_t* tokens, int T, float* x, int* 
 void launch_embed(const DevMat& E, const uint32_t* tokens, int T, float* x, int* err,
                   hipStream_t s) {
   dim3 grid((E.cols + 255) / 256, T);
-  hipLaunchKernelGGL(k_embed, grid, dim3(256), 0, s, E, tokens, T, x, err);
+  launch_kernel(k_embed, grid, dim3(256), 0, s, E, tokens, T, x, err);
 }
 
 // ---------------------------------------------------------------------------
@@ -319,7 +319,7 @@ void launch_quantize(const float* x, int T, int n, bool want_q8a, bool want_q8k,
                      float* da, float* af, int8_t* qk, float* dk, int* err, hipStream_t s) {
   dim3 grid((n + 1023) / 1024, T);
   QuantOut q{qa, da, af, qk, dk};
-  hipLaunchKernelGGL(k_quantize, grid, dim3(256), 0, s, x, n, (int)want_q8a, (int)want_q8k, q, err);
+  launch_kernel(k_quantize, grid, dim3(256), 0, s, x, n, (int)want_q8a, (int)want_q8k, q, err);
 }
 
 // ---------------------------------------------------------------------------
@@ -408,7 +408,7 @@ void launch_rmsnorm_quant(const float* x, const float* w, float eps, int T, int 
                               150 * 1024);
     attr_set = true;
   }
-  hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(256), rmsnorm_smem(n), s, x, w, eps, n, out,
+  launch_kernel(k_rmsnorm, dim3(T), dim3(256), rmsnorm_smem(n), s, x, w, eps, n, out,
                      (int)want_q8a, (int)want_q8k, q, err);
 }
 
@@ -475,7 +475,7 @@ void launch_gemm(const DevMat& W, const DevAct& A, int T, float* out, const floa
   }
   if (T <= kGemvMaxT && launch_gemv(W, A, T, out, bias, epi, err, s)) return;
   dim3 grid((W.rows + 255) / 256, T);
-  hipLaunchKernelGGL(k_gemm_rowlane, grid, dim3(256), 0, s, W, A, T, out, bias, epi, err);
+  launch_kernel(k_gemm_rowlane, grid, dim3(256), 0, s, W, A, T, out, bias, epi, err);
 }
 
 // ---------------------------------------------------------------------------
@@ -529,7 +529,7 @@ void launch_rope_store(float* q, float* k, const float* v, const float* rope_cos
                        const float* rope_sin, int T, int pos0, int H, int KV, int hd, int rope_dim,
                        int split_half, float* kc, float* vc, int layer, int n_ctx, int* err,
                        hipStream_t s) {
-  hipLaunchKernelGGL(k_rope_store, dim3(T), dim3(256), 0, s, q, k, v, rope_cos, rope_sin, pos0, H,
+  launch_kernel(k_rope_store, dim3(T), dim3(256), 0, s, q, k, v, rope_cos, rope_sin, pos0, H,
                      KV, hd, rope_dim, split_half, kc, vc, layer, n_ctx, err);
 }
 
@@ -858,7 +858,7 @@ void launch_attention(const float* q, const float* kc, const float* vc, int laye
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
         attr64_set = true;
       }
-      hipLaunchKernelGGL(k_attention_hd64, dim3(KV, T), dim3(G * 64), smem64, s, q, kc, vc, layer,
+      launch_kernel(k_attention_hd64, dim3(KV, T), dim3(G * 64), smem64, s, q, kc, vc, layer,
                          pos0, H, KV, n_ctx, sc_stride, scale, out, err);
       return;
     }
@@ -871,11 +871,11 @@ void launch_attention(const float* q, const float* kc, const float* vc, int laye
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
       attr_set = true;
     }
-    hipLaunchKernelGGL(k_attention_grp, dim3(KV, T), dim3(G * 64), smem, s, q, kc, vc, layer, pos0,
+    launch_kernel(k_attention_grp, dim3(KV, T), dim3(G * 64), smem, s, q, kc, vc, layer, pos0,
                        H, KV, hd, n_ctx, scale, out, err);
     return;
   }
-  hipLaunchKernelGGL(k_attention, dim3(H, T), dim3(64), 0, s, q, kc, vc, layer, pos0, H, KV, hd,
+  launch_kernel(k_attention, dim3(H, T), dim3(64), 0, s, q, kc, vc, layer, pos0, H, KV, hd,
                      n_ctx, scale, scores, out, err);
 }
 
@@ -891,7 +891,7 @@ __global__ void k_swiglu(const float* g, const float* u, int count, float* out, 
 }
 
 void launch_swiglu(const float* g, const float* u, int count, float* out, int* err, hipStream_t s) {
-  hipLaunchKernelGGL(k_swiglu, dim3((count + 255) / 256), dim3(256), 0, s, g, u, count, out, err);
+  launch_kernel(k_swiglu, dim3((count + 255) / 256), dim3(256), 0, s, g, u, count, out, err);
 }
 
 // ---------------------------------------------------------------------------
@@ -916,7 +916,7 @@ __global__ void k_rope_table(float base, int rope_dim, int positions, float* co,
 void launch_rope_table(float base, int rope_dim, int positions, float* cos_out, float* sin_out,
                        int* err, hipStream_t s) {
   int n = positions * (rope_dim / 2);
-  hipLaunchKernelGGL(k_rope_table, dim3((n + 255) / 256), dim3(256), 0, s, base, rope_dim,
+  launch_kernel(k_rope_table, dim3((n + 255) / 256), dim3(256), 0, s, base, rope_dim,
                      positions, cos_out, sin_out, err);
 }
 
@@ -1103,7 +1103,7 @@ __global__ void __launch_bounds__(256) k_cdf(const float* logits, int V, int tai
 void launch_cdf(const float* logits, int R, int V, int tail, int mode, const uint32_t* symbols,
                 const uint64_t* values, uint64_t* cum, uint32_t* freq, uint64_t* total,
                 uint32_t* sym, uint32_t* freq_tab, uint64_t* cum_tab, int* err, hipStream_t s) {
-  hipLaunchKernelGGL(k_cdf, dim3(R), dim3(kCdfThreads), 0, s, logits, V, tail, mode, symbols,
+  launch_kernel(k_cdf, dim3(R), dim3(kCdfThreads), 0, s, logits, V, tail, mode, symbols,
                      values, cum, freq, total, sym, freq_tab, cum_tab, err);
 }
 
@@ -1116,7 +1116,7 @@ __global__ void k_exp(const float* in, float* out, int n, int which) {
 }
 
 void launch_exp_f32(const float* in, float* out, int n, int which, hipStream_t s) {
-  hipLaunchKernelGGL(k_exp, dim3((n + 255) / 256), dim3(256), 0, s, in, out, n, which);
+  launch_kernel(k_exp, dim3((n + 255) / 256), dim3(256), 0, s, in, out, n, which);
 }
 
 __global__ void k_f16(const uint16_t* in, float* out, int n) {
@@ -1125,7 +1125,7 @@ __global__ void k_f16(const uint16_t* in, float* out, int n) {
 }
 
 void launch_f16_to_f32(const uint16_t* in, float* out, int n, hipStream_t s) {
-  hipLaunchKernelGGL(k_f16, dim3((n + 255) / 256), dim3(256), 0, s, in, out, n);
+  launch_kernel(k_f16, dim3((n + 255) / 256), dim3(256), 0, s, in, out, n);
 }
 
 __global__ void k_div_sqrt(const float* a, const float* b, float* q, float* r, int n) {
@@ -1136,7 +1136,7 @@ __global__ void k_div_sqrt(const float* a, const float* b, float* q, float* r, i
 }
 
 void launch_div_sqrt(const float* a, const float* b, float* q, float* r, int n, hipStream_t s) {
-  hipLaunchKernelGGL(k_div_sqrt, dim3((n + 255) / 256), dim3(256), 0, s, a, b, q, r, n);
+  launch_kernel(k_div_sqrt, dim3((n + 255) / 256), dim3(256), 0, s, a, b, q, r, n);
 }
 
 }  // namespace dtl

@@ -93,6 +93,10 @@ int ref_forward_one(ref_session *s, size_t token, size_t pos, float *logits);
 int ref_logits_hash(const ref_model *m, const uint32_t *tokens, size_t n, size_t chunk, uint8_t out[32]);
 int ref_logits(const ref_model *m, const uint32_t *tokens, size_t n, float *out);
 int ref_rope_table(const ref_model *m, size_t positions, float *cos_out, float *sin_out);
+/* apply_rope (det-model lib.rs:2011-2051) on heads x head_dim values with
+ * one position's cos/sin row (rope_dim/2 entries). */
+int ref_apply_rope(float *x, size_t heads, size_t head_dim, size_t rope_dim, int split_half,
+                   const float *cos_row, const float *sin_row);
 void ref_set_threads(size_t threads);
 void ref_set_simd(int on);
 

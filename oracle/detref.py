@@ -59,6 +59,7 @@ def load() -> C.CDLL:
         "ref_logits_hash": (C.c_int, [C.c_void_p, u32p, sz, sz, u8p]),
         "ref_logits": (C.c_int, [C.c_void_p, u32p, sz, f32p]),
         "ref_rope_table": (C.c_int, [C.c_void_p, sz, f32p, f32p]),
+        "ref_apply_rope": (C.c_int, [f32p, sz, sz, sz, C.c_int, f32p, f32p]),
         "ref_set_threads": (None, [sz]),
         "ref_set_simd": (None, [C.c_int]),
         "ref_logits_to_cdf": (C.c_int, [f32p, sz, sz, u32p, u64p, u64p]),
@@ -215,6 +216,16 @@ def rmsnorm(x, w, eps: float):
     out = np.empty_like(x)
     _chk(lib().ref_rmsnorm(_p(x, C.c_float), _p(w, C.c_float), eps, x.size, _p(out, C.c_float)), "ref_rmsnorm")
     return out
+
+
+def apply_rope(x, heads: int, head_dim: int, rope_dim: int, split_half: bool, cos_row, sin_row):
+    """apply_rope on a copy of x (heads*head_dim values) with one table row."""
+    x = np.array(x, np.float32)
+    c = np.ascontiguousarray(np.asarray(cos_row, np.float32))
+    s = np.ascontiguousarray(np.asarray(sin_row, np.float32))
+    _chk(lib().ref_apply_rope(_p(x, C.c_float), heads, head_dim, rope_dim, int(split_half),
+                              _p(c, C.c_float), _p(s, C.c_float)), "ref_apply_rope")
+    return x
 
 
 def exp_f32(x: np.ndarray) -> np.ndarray:

@@ -744,24 +744,35 @@ int ref_session_reset(ref_session *s) {
 }
 
 /* apply_rope (lib.rs:2011-2051) */
-static int apply_rope(const ref_session *s, float *x, size_t heads, size_t pos) {
-    const ref_model *m = s->m;
-    size_t hd = m->head_dim, half = m->c.rope_dim / 2;
-    if (!finite_slice(x, heads * hd)) return REF_ERR_NON_FINITE;
+/* apply_rope (lib.rs:2011-2051) with one position's table row: pairs
+ * (2j, 2j+1) (Adjacent) or (j, j+half) (SplitHalf) of each head's first
+ * rope_dim dims rotate by (cos_row[j], sin_row[j]); the rest are untouched. */
+int ref_apply_rope(float *x, size_t heads, size_t head_dim, size_t rope_dim, int split_half,
+                   const float *cos_row, const float *sin_row) {
+    size_t half = rope_dim / 2;
+    if (rope_dim % 2 != 0 || rope_dim > head_dim) return REF_ERR_SHAPE;
+    if (!finite_slice(x, heads * head_dim)) return REF_ERR_NON_FINITE;
     for (size_t h = 0; h < heads; h++) {
-        size_t base = h * hd;
+        size_t base = h * head_dim;
         for (size_t j = 0; j < half; j++) {
             size_t a, b;
-            if (m->c.split_half) { a = base + j; b = base + j + half; }
+            if (split_half) { a = base + j; b = base + j + half; }
             else { a = base + 2 * j; b = a + 1; }
             float x0 = x[a], x1 = x[b];
-            float cv = s->rope_cos[pos * half + j], sv = s->rope_sin[pos * half + j];
+            float cv = cos_row[j], sv = sin_row[j];
             x[a] = x0 * cv - x1 * sv;
             x[b] = x0 * sv + x1 * cv;
             if (!isfinite(x[a]) || !isfinite(x[b])) return REF_ERR_NON_FINITE;
         }
     }
     return REF_OK;
+}
+
+static int apply_rope(const ref_session *s, float *x, size_t heads, size_t pos) {
+    const ref_model *m = s->m;
+    size_t half = m->c.rope_dim / 2;
+    return ref_apply_rope(x, heads, m->head_dim, m->c.rope_dim, m->c.split_half,
+                          s->rope_cos + pos * half, s->rope_sin + pos * half);
 }
 
 /* softmax_in_place (lib.rs:2361-2388) */

@@ -237,6 +237,24 @@ def test_fixture_hash_is_thread_invariant(threads):
     assert got == want
 
 
+def test_rope_pairing_anchors():
+    # det-model lib.rs:2751-2820: position 1 of a table with cos (0, 0.5),
+    # sin (1, -0.25); adjacent and split-half pairs, and a non-rotary tail.
+    c, s = [0.0, 0.5], [1.0, -0.25]
+    bits = lambda a: np.asarray(a, np.float32).view(np.uint32)
+    got = detref.apply_rope([1, 2, 3, 4, 5, 6, 7, 8], 2, 4, 4, False, c, s)
+    assert np.array_equal(bits(got), bits([-2.0, 1.0, 2.5, 1.25, -6.0, 5.0, 5.5, 2.25]))
+    got = detref.apply_rope([1, 2, 3, 4], 1, 4, 4, True, c, s)
+    assert np.array_equal(bits(got), bits([-3.0, 2.0, 1.0, 1.5]))
+    got = detref.apply_rope([1, 2, 3, 4, 9, -9], 1, 6, 4, False, c, s)
+    assert np.array_equal(bits(got), bits([-2.0, 1.0, 2.5, 1.25, 9.0, -9.0]))
+    got = detref.apply_rope([1, 2, 3, 4, 9, -9], 1, 6, 4, True, c, s)
+    assert np.array_equal(bits(got), bits([-3.0, 2.0, 1.0, 1.5, 9.0, -9.0]))
+    # A swapped pairing or sign is caught by the same anchors.
+    assert not np.array_equal(bits(detref.apply_rope([1, 2, 3, 4], 1, 4, 4, False, c, s)),
+                              bits([-3.0, 2.0, 1.0, 1.5]))
+
+
 def test_rmsnorm_order():
     # det-model lib.rs:2442-2459
     x = np.array([1.0, -2.0, 3.0, -4.0], np.float32)
