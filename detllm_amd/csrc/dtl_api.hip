@@ -706,8 +706,19 @@ int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t po
   for (size_t l = 0; l < c.block_count; l++) {
     const Layer& L = m->layers[l];
     DevAct a = rms(L.attn_norm, {&L.wq, &L.wk, &L.wv});
-    gemm(L.wq, a, s->q, L.bq, L.bq ? EPI_BIAS : EPI_STORE);
-    gemm(L.wk, a, s->k, L.bk, L.bk ? EPI_BIAS : EPI_STORE);
+    if (L.wq.type == GGML_Q4_K && L.wk.type == GGML_Q4_K && L.wq.w32 && L.wk.w32 && T >= 16 &&
+        (L.bq != nullptr) == (L.bk != nullptr)) {
+      // wq and wk share the input: one launch over their concatenated rows.
+      double bytes = (double)(L.wq.rows + L.wk.rows) * L.wq.cols * weight_bytes_per_elem(GGML_Q4_K) +
+                     (double)T * L.wq.cols * (1.0 + 4.0 / 32) + (double)T * (L.wq.rows + L.wk.rows) * 4.0;
+      P.timed(st, gemm_class(GGML_Q4_K), bytes, (double)(L.wq.rows + L.wk.rows) * L.wq.cols * T, [&] {
+        launch_gemm_cat_q4k(L.wq, L.wk, a, T, s->q, s->k, L.bq, L.bk, L.bq ? EPI_BIAS : EPI_STORE,
+                            s->err, st);
+      });
+    } else {
+      gemm(L.wq, a, s->q, L.bq, L.bq ? EPI_BIAS : EPI_STORE);
+      gemm(L.wk, a, s->k, L.bk, L.bk ? EPI_BIAS : EPI_STORE);
+    }
     gemm(L.wv, a, s->v, L.bv, L.bv ? EPI_BIAS : EPI_STORE);
     P.timed(st, "rope_store", (double)T * (H + 3 * KV) * hd * 8.0, 0.0, [&] {
       launch_rope_store(s->q, s->k, s->v, s->rope_cos, s->rope_sin, T, (int)pos0, H, KV, hd,

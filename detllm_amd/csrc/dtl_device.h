@@ -103,6 +103,12 @@ void launch_gemm_tok(const DevMat& W, const DevAct& A, int T, float* out, const 
                      int epi, int* err, hipStream_t s);
 // Fills out[rows*cols] with the exact f32 value of every Q4_K weight.
 void launch_dequant_q4k(const DevMat& W, float* out, hipStream_t s);
+// Two Q4_K matrices with the same input and column count (wq, wk) in one
+// launch of at least 16 positions, each with its own output, bias and
+// epilogue; false (nothing launched) when the pair does not qualify.
+bool launch_gemm_cat_q4k(const DevMat& W0, const DevMat& W1, const DevAct& A, int T, float* out0,
+                         float* out1, const float* bias0, const float* bias1, int epi, int* err,
+                         hipStream_t s);
 // gate and up (both Q4_K, same shape) in one pass with silu(gate)*up written to ffo.
 void launch_gemm_pair_swiglu_q4k(const DevMat& G, const DevMat& U, const DevAct& A, int T, float* g,
                                  float* u, float* ffo, int* err, hipStream_t s);

@@ -325,22 +325,43 @@ __global__ void __launch_bounds__(256) k_q8_0_tok(DevMat W, const int8_t* __rest
 
 // ---------------------------------------------------------------------------
 // Q4_K from an exact f32 copy of the weights (the values q4_k_value yields,
-// det-quant lib.rs:506-517, computed once at load).  Lanes = positions; the
-// weight rows are wave-uniform, so they are fetched with scalar loads and
-// used as SGPR operands of v_mul_f32; the workgroup stages each 64-element
-// activation slice of its 64 positions in LDS once for its four waves
-// (double-buffered).  NK rows per wave share every activation register.
-template <int NK, bool PAIR>
-__global__ void __launch_bounds__(256) k_q4k_f32w(const float* __restrict__ W0,
-                                                  const float* __restrict__ W1, int rows, int cols,
-                                                  const float* __restrict__ af, int T, float* out0,
-                                                  float* out1, float* ffo, const float* bias,
-                                                  int epi, int* err) {
-  constexpr int NM = PAIR ? 2 : 1;
+// det-quant lib.rs:506-517, computed once at load).  Lanes = positions, NK
+// rows per wave; the workgroup stages each 64-element activation slice of
+// its 64 positions in LDS once for its four waves, and each wave stages its
+// own weight rows there too (read back as broadcasts); both are
+// double-buffered with the next slice's global loads in flight.
+//   MODE_SINGLE  one matrix
+//   MODE_PAIR    gate and up (same shape): silu(gate)*up (det-model
+//                lib.rs:2420-2434) written in the epilogue
+//   MODE_CAT     two matrices with the same input (e.g. wq and wk), their
+//                rows concatenated into one grid, separate outputs
+enum { MODE_SINGLE = 0, MODE_PAIR = 1, MODE_CAT = 2 };
+
+struct Q4kF32Args {
+  const float* w0;
+  const float* w1;
+  int rows0, rows1, cols;
+  const float* af;
+  int T;
+  float* out0;
+  float* out1;
+  float* ffo;
+  const float* bias0;
+  const float* bias1;
+  int epi;
+  int* err;
+};
+
+template <int NK, int MODE>
+__global__ void __launch_bounds__(256) k_q4k_f32w(Q4kF32Args p) {
+  constexpr int NM = MODE == MODE_PAIR ? 2 : 1;
   constexpr int SL = 64;        // elements per slice
   constexpr int LD = SL + 4;    // padded LDS row (floats)
   __shared__ __align__(16) float at[2][64][LD];
   __shared__ __align__(16) float wt[2][kWaves][NM * NK][SL];
+  const int cols = p.cols, T = p.T;
+  const int rows_total = MODE == MODE_CAT ? p.rows0 + p.rows1 : p.rows0;
+  const float* __restrict__ af = p.af;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row0 = (blockIdx.x * kWaves + wave) * NK;
@@ -382,11 +403,17 @@ __global__ void __launch_bounds__(256) k_q4k_f32w(const float* __restrict__ W0,
   // float4 of one row) and are read back as broadcasts.
   const int wk = lane >> 4, wc4 = lane & 15;
   const bool wlane = wk < NM * NK;
-  const float* wsrc = W0;
+  const float* wsrc = p.w0;
   if (wlane) {
-    int m = wk / NK, kk = wk % NK;
-    int row = row0 + kk < rows ? row0 + kk : rows - 1;
-    wsrc = (m ? W1 : W0) + (size_t)row * cols + wc4 * 4;
+    if (MODE == MODE_PAIR) {
+      int m = wk / NK, kk = wk % NK;
+      int row = row0 + kk < p.rows0 ? row0 + kk : p.rows0 - 1;
+      wsrc = (m ? p.w1 : p.w0) + (size_t)row * cols + wc4 * 4;
+    } else {
+      int g = row0 + wk < rows_total ? row0 + wk : rows_total - 1;
+      bool m = MODE == MODE_CAT && g >= p.rows0;
+      wsrc = (m ? p.w1 : p.w0) + (size_t)(m ? g - p.rows0 : g) * cols + wc4 * 4;
+    }
   }
   float4 wpre = make_float4(0.f, 0.f, 0.f, 0.f);
 #define DTL_ISSUE_W(e0)                                        \
@@ -434,19 +461,23 @@ __global__ void __launch_bounds__(256) k_q4k_f32w(const float* __restrict__ W0,
   bool ok = true;
 #pragma unroll
   for (int k = 0; k < NK; k++) {
-    int row = row0 + k;
-    if (row >= rows) continue;
-    size_t o = (size_t)t * rows + row;
-    if (PAIR) {
-      float g = acc[k], u = acc[NK + k];
-      float v = silu_det(g) * u;
-      ok &= finite(g) && finite(u) && finite(v);
-      ffo[o] = v;
+    const int g = row0 + k;
+    if (g >= rows_total) continue;
+    if (MODE == MODE_PAIR) {
+      size_t o = (size_t)t * p.rows0 + g;
+      float gv = acc[k], uv = acc[NK + k];
+      float v = silu_det(gv) * uv;
+      ok &= finite(gv) && finite(uv) && finite(v);
+      p.ffo[o] = v;
     } else {
-      ok &= store_epilogue(acc[k], out0, o, bias, row, epi);
+      const bool m = MODE == MODE_CAT && g >= p.rows0;
+      const int local = m ? g - p.rows0 : g;
+      const int R = m ? p.rows1 : p.rows0;
+      ok &= store_epilogue(acc[k], m ? p.out1 : p.out0, (size_t)t * R + local,
+                           m ? p.bias1 : p.bias0, local, p.epi);
     }
   }
-  if (!ok) flag(err, ERRBIT_NON_FINITE);
+  if (!ok) flag(p.err, ERRBIT_NON_FINITE);
 }
 
 #undef DTL_ISSUE
@@ -490,31 +521,51 @@ int rows_per_wave(int rows) {
   return 1;
 }
 
-// Rows per wave for the f32-weight Q4_K kernel (DETLLM_Q4K_NK overrides).
-int q4k_nk(int rows) {
+// Rows per wave for the f32-weight Q4_K kernel (DETLLM_Q4K_NK overrides):
+// one row per wave keeps two waves per SIMD on 2k-row matrices at 64
+// positions; the gate/up pair (and very tall matrices) have waves to spare
+// and amortise each activation read over two rows.
+int q4k_nk(int mode, int rows_total) {
   static int forced = [] {
     const char* e = getenv("DETLLM_Q4K_NK");
     return e ? atoi(e) : 0;
   }();
-  if (forced == 1 || forced == 2 || forced == 4) return forced;
-  (void)rows;
-  return 2;
+  if (forced == 1 || forced == 2) return forced;
+  if (mode == MODE_PAIR) return 2;
+  return rows_total >= 8192 ? 2 : 1;
 }
 
-template <bool PAIR>
-void launch_q4k_f32w(const DevMat& W0, const DevMat& W1, const DevAct& A, int T, float* out,
-                     float* ffo, const float* bias, int epi, int* err, hipStream_t s) {
-  int nk = q4k_nk(PAIR ? 2 * W0.rows : W0.rows);
-  if (PAIR && nk == 4) nk = 2;
-  dim3 grid((W0.rows + kWaves * nk - 1) / (kWaves * nk), (T + 63) / 64);
+template <int MODE>
+void launch_q4k_f32w(const Q4kF32Args& a, hipStream_t s) {
+  const int rows_total = MODE == MODE_CAT ? a.rows0 + a.rows1 : a.rows0;
+  const int nk = q4k_nk(MODE, rows_total);
+  dim3 grid((rows_total + kWaves * nk - 1) / (kWaves * nk), (a.T + 63) / 64);
   dim3 block(kWaves * 64);
-  const float* w1 = PAIR ? W1.w32 : nullptr;
-  if (nk == 4)
-    launch_kernel((k_q4k_f32w<4, PAIR>), grid, block, 0, s, W0.w32, w1, W0.rows, W0.cols, A.af, T, out, nullptr, ffo, bias, epi, err);
-  else if (nk == 2)
-    launch_kernel((k_q4k_f32w<2, PAIR>), grid, block, 0, s, W0.w32, w1, W0.rows, W0.cols, A.af, T, out, nullptr, ffo, bias, epi, err);
+  if (nk == 2)
+    launch_kernel(k_q4k_f32w<2, MODE>, grid, block, 0, s, a);
   else
-    launch_kernel((k_q4k_f32w<1, PAIR>), grid, block, 0, s, W0.w32, w1, W0.rows, W0.cols, A.af, T, out, nullptr, ffo, bias, epi, err);
+    launch_kernel(k_q4k_f32w<1, MODE>, grid, block, 0, s, a);
+}
+
+Q4kF32Args q4k_args(const DevMat& W0, const DevMat* W1, const DevAct& A, int T, float* out0,
+                    float* out1, float* ffo, const float* bias0, const float* bias1, int epi,
+                    int* err) {
+  Q4kF32Args a{};
+  a.w0 = W0.w32;
+  a.w1 = W1 ? W1->w32 : nullptr;
+  a.rows0 = W0.rows;
+  a.rows1 = W1 ? W1->rows : 0;
+  a.cols = W0.cols;
+  a.af = A.af;
+  a.T = T;
+  a.out0 = out0;
+  a.out1 = out1;
+  a.ffo = ffo;
+  a.bias0 = bias0;
+  a.bias1 = bias1;
+  a.epi = epi;
+  a.err = err;
+  return a;
 }
 }  // namespace
 
@@ -526,7 +577,8 @@ void launch_gemm_tok(const DevMat& W, const DevAct& A, int T, float* out, const 
                      int epi, int* err, hipStream_t s) {
   DevMat none{};
   if (W.type == kGgmlQ4K && W.w32) {
-    launch_q4k_f32w<false>(W, none, A, T, out, nullptr, bias, epi, err, s);
+    launch_q4k_f32w<MODE_SINGLE>(
+        q4k_args(W, nullptr, A, T, out, nullptr, nullptr, bias, nullptr, epi, err), s);
     return;
   }
   int R = rows_per_wave(W.rows);
@@ -563,7 +615,8 @@ void launch_gemm_tok(const DevMat& W, const DevAct& A, int T, float* out, const 
 void launch_gemm_pair_swiglu_q4k(const DevMat& G, const DevMat& U, const DevAct& A, int T, float* g,
                                  float* u, float* ffo, int* err, hipStream_t s) {
   if (G.w32 && U.w32 && !g && !u) {
-    launch_q4k_f32w<true>(G, U, A, T, nullptr, ffo, nullptr, 0, err, s);
+    launch_q4k_f32w<MODE_PAIR>(
+        q4k_args(G, &U, A, T, nullptr, nullptr, ffo, nullptr, nullptr, EPI_STORE, err), s);
     return;
   }
   int R = rows_per_wave(2 * G.rows) >= 2 ? 2 : 1;
@@ -573,6 +626,16 @@ void launch_gemm_pair_swiglu_q4k(const DevMat& G, const DevMat& U, const DevAct&
     launch_kernel((k_q4k_tok<2, true>), grid, block, 0, s, G, U, A.af, T, g, u, ffo, nullptr, 0, err);
   else
     launch_kernel((k_q4k_tok<1, true>), grid, block, 0, s, G, U, A.af, T, g, u, ffo, nullptr, 0, err);
+}
+
+bool launch_gemm_cat_q4k(const DevMat& W0, const DevMat& W1, const DevAct& A, int T, float* out0,
+                         float* out1, const float* bias0, const float* bias1, int epi, int* err,
+                         hipStream_t s) {
+  if (T < 16 || W0.type != kGgmlQ4K || W1.type != kGgmlQ4K || !W0.w32 || !W1.w32 ||
+      W0.cols != W1.cols)
+    return false;
+  launch_q4k_f32w<MODE_CAT>(q4k_args(W0, &W1, A, T, out0, out1, nullptr, bias0, bias1, epi, err), s);
+  return true;
 }
 
 }  // namespace dtl
