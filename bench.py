@@ -107,6 +107,8 @@ def main() -> int:
                     help="only run a plain copy of this many MiB (counter calibration) and exit")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-kernel-timing", action="store_true",
+                    help="time the steps without per-launch events (no roofline object)")
     ap.add_argument("--traffic-kib", default=None,
                     help="FETCH_KiB,WRITE_KiB per launch of the dominant kernel from rocprofv3 --pmc")
     args = ap.parse_args()
@@ -147,7 +149,19 @@ def main() -> int:
         t = time.time()
         step()
         log(f"[bench] warmup {i} {time.time() - t:.2f}s")
-    sess.set_profiling(True)
+    # One untimed step with every launch timed gives the per-class breakdown
+    # and picks the dominant class; the timed steps then bind events to that
+    # class's launches only, so timing barely perturbs the measured rate.
+    breakdown = {}
+    dom_name = None
+    if not args.no_kernel_timing:
+        sess.set_profiling(True)
+        step()
+        breakdown = sess.profile()
+        dom_name = max(breakdown.items(), key=lambda kv: kv[1]["total_ms"])[0]
+        sess.set_profiling(True)
+        sess.profile_only(dom_name)
+        log(f"[bench] profiled step: dominant kernel class {dom_name}")
     results = []
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -164,8 +178,11 @@ def main() -> int:
             for r in results]
     deterministic = all(np.array_equal(flat[0], f) for f in flat[1:])
 
-    # Dominant kernel class by device time.
-    dom_name, dom = max(prof.items(), key=lambda kv: kv[1]["total_ms"])
+    if not prof:
+        print(json.dumps({"value": round(tokens_per_s, 2), "ms_per_step": round(elapsed / args.steps * 1e3, 2),
+                          "deterministic": deterministic, "kernel_timing": False}), flush=True)
+        return 0 if deterministic else 1
+    dom = prof[dom_name]
     avg_ms = dom["total_ms"] / dom["launches"]
     per_launch_bytes = dom["bytes"] / dom["launches"]
     per_launch_flops = 2.0 * dom["macs"] / dom["launches"]
@@ -191,8 +208,8 @@ def main() -> int:
         roofline["traffic_source"] = MEASURED_TRAFFIC[dom_name]["source"]
     else:
         roofline["traffic"] = None
-    kernels = {k: {"ms_per_step": round(v["total_ms"] / args.steps, 3), "launches_per_step": v["launches"] // args.steps}
-               for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["total_ms"])}
+    kernels = {k: {"ms_per_step": round(v["total_ms"], 3), "launches_per_step": v["launches"]}
+               for k, v in sorted(breakdown.items(), key=lambda kv: -kv[1]["total_ms"])}
 
     # Parity: symbol ranges of the first positions against the oracle.
     sys.path.insert(0, str(ROOT / "oracle"))

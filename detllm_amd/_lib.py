@@ -90,6 +90,7 @@ _SIGS = {
     "dtl_logits_hash": (C.c_int, [C.c_void_p, u32p, sz, sz, u8p]),
     "dtl_session_set_profiling": (C.c_int, [C.c_void_p, C.c_int]),
     "dtl_session_profile": (C.c_int, [C.c_void_p, C.POINTER(KernelStat), sz, C.POINTER(sz)]),
+    "dtl_session_profile_only": (C.c_int, [C.c_void_p, C.c_char_p]),
     "dtl_symbol_ranges": (C.c_int, [C.c_void_p, sz, sz, u32p, sz, u64p, u32p, u64p]),
     "dtl_cdf": (C.c_int, [C.c_void_p, sz, sz, u32p, u64p, u64p]),
     "dtl_decoder_total": (C.c_int, [C.c_void_p, sz, sz, u64p]),

@@ -440,32 +440,47 @@ namespace {
 // q4_k_value computes), used by the chunked-encode GEMM.  Skipped when the
 // device lacks room for them or DETLLM_NO_F32_MIRROR is set; the packed
 // kernels then serve every chunk size.
-// DETLLM_NO_F32_MIRROR=1 keeps Q4_K matrices packed only (the GEMMs then
-// decode the superblocks themselves).
-bool f32_mirror_enabled() {
-  const char* off = getenv("DETLLM_NO_F32_MIRROR");
-  return !(off && *off && *off != '0');
+// Copies the chunked-encode GEMMs read instead of the GGUF blocks: the
+// exact f32 value of every Q4_K weight, and the int8 matrix-core planes of
+// every Q6_K matrix.  DETLLM_NO_F32_MIRROR=1 keeps Q4_K packed only and
+// DETLLM_NO_Q6K_PLANES=1 keeps Q6_K packed only (the GEMMs then decode the
+// superblocks themselves; results are identical either way).
+bool env_flag(const char* name) {
+  const char* v = getenv(name);
+  return v && *v && *v != '0';
 }
+bool f32_mirror_enabled() { return !env_flag("DETLLM_NO_F32_MIRROR"); }
+bool q6k_planes_enabled() { return !env_flag("DETLLM_NO_Q6K_PLANES"); }
 
-int build_f32_mirrors(dtl_model* m) {
-  if (!f32_mirror_enabled()) return DTL_OK;
-  std::vector<DevMat*> mats;
+int build_encode_copies(dtl_model* m) {
+  std::vector<DevMat*> q4k, q6k;
   for (Layer& L : m->layers)
-    for (DevMat* M : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down})
-      if (M->type == GGML_Q4_K) mats.push_back(M);
-  if (m->out.type == GGML_Q4_K) mats.push_back(&m->out);
+    for (DevMat* M : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down}) {
+      if (M->type == GGML_Q4_K && f32_mirror_enabled()) q4k.push_back(M);
+      if (M->type == GGML_Q6_K && q6k_planes_enabled()) q6k.push_back(M);
+    }
+  if (m->out.type == GGML_Q4_K && f32_mirror_enabled()) q4k.push_back(&m->out);
+  if (m->out.type == GGML_Q6_K && q6k_planes_enabled()) q6k.push_back(&m->out);
   size_t need = 0;
-  for (DevMat* M : mats) need += (size_t)M->rows * M->cols * sizeof(float);
-  if (mats.empty()) return DTL_OK;
+  for (DevMat* M : q4k) need += (size_t)M->rows * M->cols * sizeof(float);
+  for (DevMat* M : q6k) need += q6k_planes_bytes(*M);
+  if (q4k.empty() && q6k.empty()) return DTL_OK;
   size_t free_b = 0, total_b = 0;
   HIP_TRY(hipMemGetInfo(&free_b, &total_b));
   if (need + (size_t(4) << 30) > free_b) return DTL_OK;
-  for (DevMat* M : mats) {
+  for (DevMat* M : q4k) {
     float* w;
     int st = m->arena.alloc(&w, (size_t)M->rows * M->cols);
     if (st) return st;
     launch_dequant_q4k(*M, w, nullptr);
     M->w32 = w;
+  }
+  for (DevMat* M : q6k) {
+    int8_t* p;
+    int st = m->arena.alloc(&p, q6k_planes_bytes(*M));
+    if (st) return st;
+    launch_q6k_planes(*M, p, nullptr);
+    M->planes = p;
   }
   HIP_TRY(hipGetLastError());
   HIP_TRY(hipDeviceSynchronize());
@@ -496,14 +511,17 @@ class Profiler {
   }
   void enable(bool v) {
     on = v;
+    only_.clear();
     stats_.clear();
     pending_.clear();
     next_ = 0;
   }
+  // Time only launches of this class (empty: every class).
+  void only(const char* name) { only_ = name ? name : ""; }
   // Records one launch: `launch` is called between two events.
   template <typename F>
   void timed(hipStream_t s, const char* name, double bytes, double macs, F&& launch) {
-    if (!on) {
+    if (!on || (!only_.empty() && only_ != name)) {
       launch();
       return;
     }
@@ -552,6 +570,7 @@ class Profiler {
     stats_.push_back(s);
     return &stats_.back();
   }
+  std::string only_;
   std::vector<hipEvent_t> pool_;
   size_t next_ = 0;
   std::vector<Pending> pending_;
@@ -849,7 +868,7 @@ int dtl_model_load(const uint8_t* bytes, size_t len, dtl_model** out) {
     return DTL_ERR_GGUF;
   }
   m->vocab = (size_t)m->out.rows;
-  if ((st = build_f32_mirrors(m.get()))) return st;
+  if ((st = build_encode_copies(m.get()))) return st;
   *out = m.release();
   return DTL_OK;
 }
@@ -1041,6 +1060,13 @@ int dtl_session_set_profiling(dtl_session* s, int enable) {
   if (!s) return DTL_ERR_INVALID_ARGUMENT;
   HIP_TRY(hipStreamSynchronize(s->stream));
   s->prof.enable(enable != 0);
+  return DTL_OK;
+}
+
+int dtl_session_profile_only(dtl_session* s, const char* kernel_class) {
+  if (!s) return DTL_ERR_INVALID_ARGUMENT;
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  s->prof.only(kernel_class);
   return DTL_OK;
 }
 
@@ -1354,14 +1380,20 @@ int dtl_kernel_gemv(int ggml_type, const uint8_t* weights, size_t rows, size_t c
   if (g.parse(file.data(), file.size()) != GgufError::None) return DTL_ERR_GGUF;
   const GgufTensor* gt;
   if (g.tensor("w", &gt) != GgufError::None) return DTL_ERR_GGUF;
-  DevMat W;
+  DevMat W{};
   if ((st = upload_matrix(g, *gt, rows, cols, sc.arena, &W))) return st;
+  // The same encode-GEMM copies a loaded model keeps.
   if (W.type == GGML_Q4_K && f32_mirror_enabled()) {
-    // Same exact f32 copy a loaded model keeps.
     float* w32;
     if ((st = sc.arena.alloc(&w32, rows * cols))) return st;
     launch_dequant_q4k(W, w32, sc.stream);
     W.w32 = w32;
+  }
+  if (W.type == GGML_Q6_K && q6k_planes_enabled()) {
+    int8_t* planes;
+    if ((st = sc.arena.alloc(&planes, q6k_planes_bytes(W)))) return st;
+    launch_q6k_planes(W, planes, sc.stream);
+    W.planes = planes;
   }
   float *dx, *dout, *af, *da, *dk;
   int8_t *qa, *qk;

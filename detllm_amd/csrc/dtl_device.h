@@ -63,6 +63,13 @@ struct DevMat {
   // Q4_K only (optional): float[rows][cols] holding q4_k_value of every
   // element, used by the chunked-encode GEMM as scalar-path operands.
   const float* w32;
+  // Q6_K only (optional): the int8 matrix-core operands of the chunked-encode
+  // GEMM.  For 16-row tile rt, superblock sb, class c (element index mod 8)
+  // and plane p, 512 bytes at (((rt*nb + sb)*8 + c)*2 + p)*512 hold, for
+  // row r of the tile, bytes [r*32, r*32+32): W' = scale*q6 of elements
+  // 8j + c (j = 0..31) split as W' = 64*hi + lo (p = 0: hi in [-64, 64],
+  // p = 1: lo in [0, 63]).  Rows are padded with zeros to a multiple of 16.
+  const int8_t* planes;
 };
 
 // Activations of T positions for one GEMM input of width cols, in every
@@ -103,6 +110,10 @@ void launch_gemm_tok(const DevMat& W, const DevAct& A, int T, float* out, const 
                      int epi, int* err, hipStream_t s);
 // Fills out[rows*cols] with the exact f32 value of every Q4_K weight.
 void launch_dequant_q4k(const DevMat& W, float* out, hipStream_t s);
+// Bytes of the Q6_K matrix-core planes of W (see DevMat::planes).
+size_t q6k_planes_bytes(const DevMat& W);
+// Fills planes (q6k_planes_bytes(W) bytes) from W's Q6_K superblocks.
+void launch_q6k_planes(const DevMat& W, int8_t* planes, hipStream_t s);
 // Two Q4_K matrices with the same input and column count (wq, wk) in one
 // launch of at least 16 positions, each with its own output, bias and
 // epilogue; false (nothing launched) when the pair does not qualify.

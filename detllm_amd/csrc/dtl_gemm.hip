@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "dtl_blocks.h"
 #include "dtl_device.h"
 #include "dtl_numerics.h"
 
@@ -510,6 +511,178 @@ void launch_dequant_q4k(const DevMat& W, float* out, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
+// Q6_K on the int8 matrix cores (dot_q6_k_q8k, det-quant lib.rs:353-397).
+// Per superblock sb and class c (element index mod 8) the reference's exact
+// integer sums aux_c = sum_j W'[8j+c] * qa[8j+c] over the 32 elements of
+// the class form a [rows x positions] product with K = 32.  With
+// W' = scale*q6 = 64*hi + lo held as two int8 planes, aux_c is
+// 64*(hi . qa) + (lo . qa): two v_mfma_i32_16x16x64_i8 (K quarters 2 and 3
+// zero), exact in i32.  The f32 part, sums[c] += (dw*da)*aux_c per
+// superblock in order and the final 0 + sums[0] + ... + sums[7], runs on the
+// VALU as in the reference.  The Q8_K activations are class-major within
+// each 256-block, so class c's 32 bytes are contiguous.
+//
+// One workgroup per 16-row tile x NT tiles of 16 positions.  MFMA
+// operand layout (16x16x64 i8): lane l supplies row / position l % 16 and
+// K quarter l / 16 (16 bytes); result register i of lane l is row
+// 4 (l / 16) + i, position l % 16.
+typedef int dtl_v4i __attribute__((ext_vector_type(4)));
+
+__global__ void k_q6k_planes(DevMat W, int rows_pad, int8_t* planes) {
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int nb = W.nb;
+  const size_t total = (size_t)rows_pad * nb * 256;
+  if (idx >= total) return;
+  const int row = (int)(idx / ((size_t)nb * 256));
+  const int rem = (int)(idx % ((size_t)nb * 256));
+  const int sb = rem >> 8, k = rem & 255;
+  const int c = k >> 5, j = k & 31;
+  int wp = 0;
+  if (row < W.rows) {
+    const uint8_t* body = (const uint8_t*)W.w + ((size_t)row * nb + sb) * 208;
+    const int e = 8 * j + c;
+    wp = q6k_scale(body, e) * q6k_quant(body, e);
+  }
+  const size_t base = ((((size_t)(row >> 4) * nb + sb) * 8 + c) * 2) * 512 + (row & 15) * 32 + j;
+  planes[base] = (int8_t)(wp >> 6);
+  planes[base + 512] = (int8_t)(wp & 63);
+}
+
+size_t q6k_planes_bytes(const DevMat& W) {
+  return (size_t)((W.rows + 15) / 16) * 16 * W.nb * 256 * 2;
+}
+
+void launch_q6k_planes(const DevMat& W, int8_t* planes, hipStream_t s) {
+  const int rows_pad = (W.rows + 15) / 16 * 16;
+  const size_t total = (size_t)rows_pad * W.nb * 256;
+  launch_kernel(k_q6k_planes, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, W, rows_pad,
+                planes);
+}
+
+template <int NT>
+__global__ void __launch_bounds__(256) k_q6k_mfma(const int8_t* __restrict__ planes,
+                                                  const uint16_t* __restrict__ d16, int rows,
+                                                  int nb, const int8_t* __restrict__ qk,
+                                                  const float* __restrict__ dk, int T, float* out,
+                                                  const float* bias, int epi, int* err) {
+  // The eight class chains are independent until the final combine: wave w
+  // runs classes 2w and 2w+1 of the workgroup's tile.
+  __shared__ float part[8][NT][4][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rt = blockIdx.x;
+  const int p0 = blockIdx.y * 16 * NT;
+  const int q = lane >> 4, li = lane & 15;
+  const int cols = nb * 256;
+  const dtl_v4i zero = {0, 0, 0, 0};
+  // A operand: row li of the tile, bytes 16 (q & 1) .. of the class run
+  // (quarters 2 and 3 read the same bytes and are zeroed).
+  const int8_t* abase = planes + (size_t)rt * nb * 8192 + (size_t)(2 * wave) * 1024 + li * 32 +
+                        (q & 1) * 16;
+  // B operand: position p0 + 16 j + li (clamped to T - 1; not stored).
+  const int8_t* bsrc[NT];
+  const float* dsrc[NT];
+#pragma unroll
+  for (int j = 0; j < NT; j++) {
+    int pos = p0 + 16 * j + li;
+    pos = pos < T ? pos : T - 1;
+    bsrc[j] = qk + (size_t)pos * cols + (2 * wave) * 32 + (q & 1) * 16;
+    dsrc[j] = dk + (size_t)pos * nb;
+  }
+  // Rows of this lane's results: 16 rt + 4 q + i.
+  const uint16_t* dwsrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    int row = rt * 16 + 4 * q + i;
+    row = row < rows ? row : rows - 1;
+    dwsrc[i] = d16 + (size_t)row * nb;
+  }
+  float sums[NT][2][4];
+#pragma unroll
+  for (int j = 0; j < NT; j++)
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) sums[j][c][i] = 0.0f;
+  // Operands of one superblock for this wave's two classes; the next
+  // superblock's are in flight while the current one is multiplied.
+  struct Ops {
+    dtl_v4i a[2][2];
+    dtl_v4i b[NT][2];
+    uint16_t dw[4];
+    float da[NT];
+  };
+  auto load = [&](Ops& o, int sb) {
+    const int8_t* ab = abase + (size_t)sb * 8192;
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      o.a[c][0] = *(const dtl_v4i*)(ab + (2 * c) * 512);
+      o.a[c][1] = *(const dtl_v4i*)(ab + (2 * c + 1) * 512);
+    }
+#pragma unroll
+    for (int j = 0; j < NT; j++)
+#pragma unroll
+      for (int c = 0; c < 2; c++) o.b[j][c] = *(const dtl_v4i*)(bsrc[j] + sb * 256 + c * 32);
+#pragma unroll
+    for (int i = 0; i < 4; i++) o.dw[i] = dwsrc[i][sb];
+#pragma unroll
+    for (int j = 0; j < NT; j++) o.da[j] = dsrc[j][sb];
+  };
+  auto compute = [&](const Ops& o) {
+    float dd[NT][4];
+#pragma unroll
+    for (int j = 0; j < NT; j++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) dd[j][i] = f16_to_f32(o.dw[i]) * o.da[j];
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const dtl_v4i ahi = q < 2 ? o.a[c][0] : zero;
+      const dtl_v4i alo = q < 2 ? o.a[c][1] : zero;
+#pragma unroll
+      for (int j = 0; j < NT; j++) {
+        dtl_v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, o.b[j][c], zero, 0, 0, 0);
+        acc = acc * 64;
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, o.b[j][c], acc, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) sums[j][c][i] += dd[j][i] * (float)acc[i];
+      }
+    }
+  };
+  Ops x0, x1;
+  load(x0, 0);
+  int sb = 0;
+  for (; sb + 2 <= nb; sb += 2) {
+    load(x1, sb + 1);
+    compute(x0);
+    if (sb + 2 < nb) load(x0, sb + 2);
+    compute(x1);
+  }
+  if (sb < nb) compute(x0);
+#pragma unroll
+  for (int c = 0; c < 2; c++)
+#pragma unroll
+    for (int j = 0; j < NT; j++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) part[2 * wave + c][j][i][lane] = sums[j][c][i];
+  __syncthreads();
+  // Final combine 0 + sums[0] + ... + sums[7] in class order; the four
+  // waves split the (position tile, register) outputs.
+  bool ok = true;
+  for (int o = wave; o < NT * 4; o += 4) {
+    const int j = o >> 2, i = o & 3;
+    const int pos = p0 + 16 * j + li;
+    const int row = rt * 16 + 4 * q + i;
+    if (row < rows && pos < T) {
+      float v = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 8; c++) v += part[c][j][i][lane];
+      ok &= store_epilogue(v, out, (size_t)pos * rows + row, bias, row, epi);
+    }
+  }
+  if (!ok) flag(err, ERRBIT_NON_FINITE);
+}
+
+// ---------------------------------------------------------------------------
 // launchers
 
 namespace {
@@ -579,6 +752,19 @@ void launch_gemm_tok(const DevMat& W, const DevAct& A, int T, float* out, const 
   if (W.type == kGgmlQ4K && W.w32) {
     launch_q4k_f32w<MODE_SINGLE>(
         q4k_args(W, nullptr, A, T, out, nullptr, nullptr, bias, nullptr, epi, err), s);
+    return;
+  }
+  if (W.type == kGgmlQ6K && W.planes) {
+    // Tall matrices: 32 positions per wave share each weight-plane load;
+    // shorter ones split positions over waves to fill the chip.
+    const int rt = (W.rows + 15) / 16;
+    if (W.rows >= 8192) {
+      launch_kernel(k_q6k_mfma<2>, dim3(rt, (T + 31) / 32), dim3(256), 0, s, W.planes, W.d16,
+                    W.rows, W.nb, A.qk, A.dk, T, out, bias, epi, err);
+    } else {
+      launch_kernel(k_q6k_mfma<1>, dim3(rt, (T + 15) / 16), dim3(256), 0, s, W.planes, W.d16,
+                    W.rows, W.nb, A.qk, A.dk, T, out, bias, epi, err);
+    }
     return;
   }
   int R = rows_per_wave(W.rows);

@@ -10,6 +10,7 @@
 #include <stdint.h>
 
 #include "dtl_device.h"
+#include "dtl_blocks.h"
 #include "dtl_numerics.h"
 
 namespace dtl {
@@ -33,20 +34,6 @@ __device__ __forceinline__ void q4k_scale_min(const uint8_t* sc, int j, int* sca
     *scale = (sc[j + 4] & 0x0f) | ((sc[j - 4] >> 6) << 4);
     *mn = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
   }
-}
-
-// det-quant lib.rs:531-552: 6-bit quant of element e (0..255) of a Q6_K body.
-__device__ __forceinline__ int q6k_quant(const uint8_t* body, int e) {
-  int half = e >> 7, within = e & 127, l = within & 31, part = within >> 5;
-  uint8_t qlb = body[half * 64 + l + (part & 1) * 32];
-  int ql = (part < 2) ? (qlb & 0x0f) : (qlb >> 4);
-  int qh = (body[128 + half * 32 + l] >> (2 * part)) & 3;
-  return (ql | (qh << 4)) - 32;
-}
-
-// Scale index of element e: q6_k_scale_index (lib.rs:554-568) equals e/16.
-__device__ __forceinline__ int q6k_scale(const uint8_t* body, int e) {
-  return (int)(int8_t)body[192 + (e >> 4)];
 }
 
 // One weight value, as write_row_validated dequantises it (det-model lib.rs:667-746).
@@ -329,18 +316,62 @@ void launch_quantize(const float* x, int T, int n, bool want_q8a, bool want_q8k,
 // holds x[c]^2, x[c+8]^2, ... contiguously), so each of the eight serial
 // chains streams float4 reads.  Optionally quantises the normalised row
 // (Q8A / Q8_K) in the same pass, one wave per 256-element span.
+namespace {
+// Output pass of one 256-element span: (x*r)*w, then the quantised forms.
+// w4 holds the span's weights for this lane when have_w4 (else read from w).
+// Returns true when a value was non-finite.
+__device__ __forceinline__ bool rms_span(const float* xs, const float* w, float4 w4, bool have_w4,
+                                         float r, int n, int t, int span, float* o, int want_q8a,
+                                         int want_q8k, const QuantOut& q) {
+  const int lane = threadIdx.x & 63;
+  const int e0 = span * 256 + 4 * lane;
+  const bool in = e0 < n;
+  const float wl[4] = {w4.x, w4.y, w4.z, w4.w};
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  bool bad = false;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    int i = e0 + c;
+    if (i < n) {
+      float wi = have_w4 ? wl[c] : w[i];
+      v[c] = (xs[i] * r) * wi;
+      if (!finite(v[c])) bad = true;
+      o[i] = v[c];
+    }
+  }
+  if (want_q8a || want_q8k)
+    quantize_span(v, in, (size_t)t * n + (size_t)span * 256, want_q8a, want_q8k, q);
+  return bad;
+}
+}  // namespace
+
 __global__ void __launch_bounds__(256) k_rmsnorm(const float* x, const float* w, float eps, int n,
                                                  float* out, int want_q8a, int want_q8k,
                                                  QuantOut q, int* err) {
   extern __shared__ __align__(16) float xs[];  // [n] row, then [8][cs] squares
   __shared__ float lane_sum[8];
   __shared__ float r_sh;
+  constexpr int kMaxSpansPerWave = 4;  // n <= 4096 keeps w in registers
   const int t = blockIdx.x;
   const int cs = (((n + 7) / 8) + 3) & ~3;    // per-chain stride, float4 aligned
   float* sq = xs + ((n + 3) & ~3);
   const float* xr = x + (size_t)t * n;
   float* o = out + (size_t)t * n;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   bool bad = false;
+  // The norm weights this thread scales in the output pass are loaded now,
+  // alongside x, so their latency overlaps the sum of squares.
+  float wv[kMaxSpansPerWave][4];
+  const bool w_in_regs = n <= 4 * 256 * kMaxSpansPerWave;
+  if (w_in_regs) {
+#pragma unroll
+    for (int k = 0; k < kMaxSpansPerWave; k++)
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        int i = (wave + 4 * k) * 256 + 4 * lane + c;
+        wv[k][c] = i < n ? w[i] : 0.0f;
+      }
+  }
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
     float v = xr[i];
     if (!finite(v) || !finite(w[i])) bad = true;
@@ -354,12 +385,15 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* x, const float* w,
     const float* my = sq + c * cs;
     float acc = 0.0f;
     int k = 0;
-    for (; k + 4 <= cnt; k += 4) {
-      float4 f = *reinterpret_cast<const float4*>(my + k);
-      acc += f.x;
-      acc += f.y;
-      acc += f.z;
-      acc += f.w;
+    for (; k + 16 <= cnt; k += 16) {
+      float4 f0 = *reinterpret_cast<const float4*>(my + k);
+      float4 f1 = *reinterpret_cast<const float4*>(my + k + 4);
+      float4 f2 = *reinterpret_cast<const float4*>(my + k + 8);
+      float4 f3 = *reinterpret_cast<const float4*>(my + k + 12);
+      acc += f0.x; acc += f0.y; acc += f0.z; acc += f0.w;
+      acc += f1.x; acc += f1.y; acc += f1.z; acc += f1.w;
+      acc += f2.x; acc += f2.y; acc += f2.z; acc += f2.w;
+      acc += f3.x; acc += f3.y; acc += f3.z; acc += f3.w;
     }
     for (; k < cnt; k++) acc += my[k];
     lane_sum[c] = acc;
@@ -374,23 +408,17 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* x, const float* w,
   }
   __syncthreads();
   const float r = r_sh;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int span = wave; span * 256 < n; span += 4) {
-    const int e0 = span * 256 + 4 * lane;
-    const bool in = e0 < n;
-    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-      int i = e0 + c;
-      if (i < n) {
-        v[c] = (xs[i] * r) * w[i];
-        if (!finite(v[c])) bad = true;
-        o[i] = v[c];
-      }
-    }
-    if (want_q8a || want_q8k)
-      quantize_span(v, in, (size_t)t * n + (size_t)span * 256, want_q8a, want_q8k, q);
+  for (int k = 0; k < kMaxSpansPerWave; k++) {
+    const int span = wave + 4 * k;
+    if (span * 256 >= n) break;
+    float4 w4 = w_in_regs ? make_float4(wv[k][0], wv[k][1], wv[k][2], wv[k][3])
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+    bad |= rms_span(xs, w, w4, w_in_regs, r, n, t, span, o, want_q8a, want_q8k, q);
   }
+  for (int span = wave + 4 * kMaxSpansPerWave; span * 256 < n; span += 4)
+    bad |= rms_span(xs, w, make_float4(0.f, 0.f, 0.f, 0.f), false, r, n, t, span, o, want_q8a,
+                    want_q8k, q);
   if (bad) flag(err, ERRBIT_NON_FINITE);
 }
 
@@ -959,51 +987,144 @@ __global__ void __launch_bounds__(256) k_cdf(const float* logits, int V, int tai
                                              uint64_t* cum, uint32_t* freq, uint64_t* total,
                                              uint32_t* sym, uint32_t* freq_tab, uint64_t* cum_tab,
                                              int* err) {
-  __shared__ float tile[kCdfTile];
+  // Z tiles, chain-major: element idx of a tile sits at [idx % 8][idx / 8],
+  // double-buffered (wave 0 sums one while waves 1-3 fill the other).
+  constexpr int kChainLen = kCdfTile / 8;
+  constexpr int kChainStride = kChainLen + 4;
+  __shared__ __align__(16) float ztile[2][8][kChainStride];
   __shared__ float chain[8];
   __shared__ float red[kCdfThreads / 64];
   __shared__ uint64_t scan[kCdfThreads];
   int r = blockIdx.x, tid = threadIdx.x;
   const float* l = logits + (size_t)r * V;
   // max (order independent) + finiteness
+  // Strided passes over the row load 8 values ahead of their use.
+  constexpr int kBatch = 8;
   float mx = -__builtin_huge_valf();
   bool bad = false;
-  for (int i = tid; i < V; i += kCdfThreads) {
-    float v = l[i];
-    if (!finite(v)) bad = true;
-    mx = fmaxf(mx, v);
+  for (int i0 = tid; i0 < V; i0 += kBatch * kCdfThreads) {
+    float v[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; k++) {
+      int i = i0 + k * kCdfThreads;
+      v[k] = i < V ? l[i] : -__builtin_huge_valf();
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; k++) {
+      if (i0 + k * kCdfThreads < V && !finite(v[k])) bad = true;
+      mx = fmaxf(mx, v[k]);
+    }
   }
   for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
   if ((tid & 63) == 0) red[tid / 64] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   if (bad) flag(err, ERRBIT_CDF_NON_FINITE);
-  // Z: chain c (thread c < 8) adds e_i for i = c mod 8 ascending, tile by tile.
+  // Z: chain c adds e_i for i = c mod 8 ascending (tiles start at multiples
+  // of 8, so tile index idx keeps i's class).  Waves 1-3 produce tile k+1
+  // while lanes 0-7 of wave 0 consume tile k.
+  const int ntiles = (V + kCdfTile - 1) / kCdfTile;
+  constexpr int kProducers = kCdfThreads - 64;
+  constexpr int kPerProducer = (kCdfTile + kProducers - 1) / kProducers;
+  auto produce = [&](int k) {
+    const int base = k * kCdfTile;
+    float(*dst)[kChainStride] = ztile[k & 1];
+    float v[kPerProducer];
+#pragma unroll
+    for (int j = 0; j < kPerProducer; j++) {
+      int idx = tid - 64 + j * kProducers;
+      int i = base + idx;
+      v[j] = idx < kCdfTile && i < V ? l[i] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < kPerProducer; j++) {
+      int idx = tid - 64 + j * kProducers;
+      int i = base + idx;
+      if (idx < kCdfTile) dst[idx & 7][idx >> 3] = i < V ? exp_clamped(v[j] - mx) : 0.0f;
+    }
+  };
   float acc = 0.0f;
-  for (int base = 0; base < V; base += kCdfTile) {
-    __syncthreads();
-    for (int k = tid; k < kCdfTile; k += kCdfThreads) {
-      int i = base + k;
-      tile[k] = i < V ? exp_clamped(l[i] - mx) : 0.0f;
+  if (tid >= 64) produce(0);
+  __syncthreads();
+  for (int k = 0; k < ntiles; k++) {
+    if (tid >= 64) {
+      if (k + 1 < ntiles) produce(k + 1);
+    } else if (tid < 8) {
+      const int base = k * kCdfTile;
+      const int lim = V - base < kCdfTile ? V - base : kCdfTile;
+      const int cnt = (lim - tid + 7) / 8;  // elements tid, tid+8, ... below lim
+      const float* my = ztile[k & 1][tid];
+      int j = 0;
+      for (; j + 16 <= cnt; j += 16) {
+        float4 f0 = *reinterpret_cast<const float4*>(my + j);
+        float4 f1 = *reinterpret_cast<const float4*>(my + j + 4);
+        float4 f2 = *reinterpret_cast<const float4*>(my + j + 8);
+        float4 f3 = *reinterpret_cast<const float4*>(my + j + 12);
+        acc += f0.x; acc += f0.y; acc += f0.z; acc += f0.w;
+        acc += f1.x; acc += f1.y; acc += f1.z; acc += f1.w;
+        acc += f2.x; acc += f2.y; acc += f2.z; acc += f2.w;
+        acc += f3.x; acc += f3.y; acc += f3.z; acc += f3.w;
+      }
+      for (; j < cnt; j++) acc += my[j];
     }
     __syncthreads();
-    if (tid < 8) {
-      int lim = V - base < kCdfTile ? V - base : kCdfTile;
-      for (int k = tid; k < lim; k += 8) acc += tile[k];
-    }
   }
   if (tid < 8) chain[tid] = acc;
   __syncthreads();
   float z = finish_8lane(chain);
-  // Integer pass: each thread owns 8 consecutive entries of a tile.
+  if (mode == 0) {
+    // Symbol range: three plain sums (every f_i, the f_i below the symbol)
+    // and the symbol's own f; integer sums are exact in any order.
+    const uint32_t want_sym = symbols[r];
+    uint64_t run_part = 0, below_part = 0;
+    uint32_t found_freq = 0;
+    bool found = false;
+    for (int i0 = tid; i0 < V; i0 += kBatch * kCdfThreads) {
+      float v[kBatch];
+#pragma unroll
+      for (int k = 0; k < kBatch; k++) {
+        int i = i0 + k * kCdfThreads;
+        v[k] = i < V ? l[i] : 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < kBatch; k++) {
+        int i = i0 + k * kCdfThreads;
+        if (i < V) {
+          uint32_t f = cdf_freq(exp_clamped(v[k] - mx), z);
+          run_part += f;
+          if ((uint32_t)i < want_sym) below_part += f;
+          if ((uint32_t)i == want_sym) {
+            found = true;
+            found_freq = f;
+          }
+        }
+      }
+    }
+    uint64_t run, below;
+    block_scan_u64(run_part, scan, &run);
+    block_scan_u64(below_part, scan, &below);
+    uint64_t tot_all = run + (uint64_t)tail;
+    if (tid == 0 && (run >= (1ull << 31) || tot_all >= (1ull << 31))) flag(err, ERRBIT_CDF_TOTAL);
+    if (found) {
+      cum[r] = below;
+      freq[r] = found_freq;
+    }
+    if (tid == 0) {
+      if (want_sym >= (uint32_t)V) {
+        cum[r] = run + (want_sym - (uint32_t)V);
+        freq[r] = 1;
+      }
+      total[r] = tot_all;
+    }
+    return;
+  }
+  // Table / lookup / total: each thread owns 8 consecutive entries of a
+  // tile; an exact block scan gives each entry's cumulative frequency.
   uint64_t target = 0, run = 0;
-  uint32_t want_sym = 0;
-  if (mode == 0) want_sym = symbols[r];
   if (mode == 2) target = values[r];
   uint64_t found_cum = 0;
   uint32_t found_freq = 0, found_sym = 0;
   bool found = false;
-  uint64_t below = 0;  // mode 0: sum of f_i for i < symbol (this thread's share)
   for (int base = 0; base < V; base += kCdfTile) {
     uint32_t f[8];
     uint64_t local = 0;
@@ -1014,63 +1135,33 @@ __global__ void __launch_bounds__(256) k_cdf(const float* logits, int V, int tai
       f[k] = i < V ? cdf_freq(exp_clamped(l[i] - mx), z) : 0u;
       local += f[k];
     }
-    if (mode == 0) {
+    uint64_t tot;
+    uint64_t incl = block_scan_u64(local, scan, &tot);
+    uint64_t c = run + incl - local;
 #pragma unroll
-      for (int k = 0; k < 8; k++) {
-        int i = i0 + k;
-        if (i < V && (uint32_t)i < want_sym) below += f[k];
-        if (i < V && (uint32_t)i == want_sym) {
+    for (int k = 0; k < 8; k++) {
+      int i = i0 + k;
+      if (i < V) {
+        if (mode == 1) {
+          freq_tab[i] = f[k];
+          cum_tab[i] = c;
+        } else if (mode == 2 && !found && target >= c && target < c + f[k]) {
           found = true;
+          found_sym = (uint32_t)i;
+          found_cum = c;
           found_freq = f[k];
         }
+        c += f[k];
       }
-      uint64_t tot;
-      block_scan_u64(local, scan, &tot);
-      run += tot;
-    } else {
-      uint64_t tot;
-      uint64_t incl = block_scan_u64(local, scan, &tot);
-      uint64_t c = run + incl - local;
-#pragma unroll
-      for (int k = 0; k < 8; k++) {
-        int i = i0 + k;
-        if (i < V) {
-          if (mode == 1) {
-            freq_tab[i] = f[k];
-            cum_tab[i] = c;
-          } else if (mode == 2 && !found && target >= c && target < c + f[k]) {
-            found = true;
-            found_sym = (uint32_t)i;
-            found_cum = c;
-            found_freq = f[k];
-          }
-          c += f[k];
-        }
-      }
-      run += tot;
     }
+    run += tot;
   }
   // run = sum of all f_i over the vocabulary
   uint64_t tot_all = run + (uint64_t)tail;
   if (run >= (1ull << 31) || tot_all >= (1ull << 31)) {
     if (tid == 0) flag(err, ERRBIT_CDF_TOTAL);
   }
-  if (mode == 0) {
-    uint64_t tot;
-    uint64_t incl = block_scan_u64(below, scan, &tot);
-    (void)incl;
-    if (found) {
-      cum[r] = tot;
-      freq[r] = found_freq;
-    }
-    if (tid == 0) {
-      if (want_sym >= (uint32_t)V) {
-        cum[r] = run + (want_sym - (uint32_t)V);
-        freq[r] = 1;
-      }
-      total[r] = tot_all;
-    }
-  } else if (mode == 1) {
+  if (mode == 1) {
     for (int k = tid; k < tail; k += kCdfThreads) {
       freq_tab[V + k] = 1;
       cum_tab[V + k] = run + (uint64_t)k;

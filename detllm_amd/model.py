@@ -220,6 +220,11 @@ class Session:
         """HIP-event timing of every launch on this session's stream."""
         check(lib.dtl_session_set_profiling(self._h, 1 if enable else 0), "dtl_session_set_profiling")
 
+    def profile_only(self, kernel_class: Optional[str]) -> None:
+        """Restricts timing to one kernel class (None: every class)."""
+        arg = kernel_class.encode() if kernel_class else None
+        check(lib.dtl_session_profile_only(self._h, arg), "dtl_session_profile_only")
+
     def profile(self) -> dict:
         """{kernel class: {launches, total_ms, bytes, macs}} since profiling was enabled."""
         n = C.c_size_t()

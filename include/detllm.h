@@ -123,9 +123,10 @@ int dtl_logits_hash(const dtl_model *model, const uint32_t *tokens, size_t n, si
 
 /* ---- device timing (no reference counterpart: measurement support) ------ */
 
-/* Per kernel class: launches, summed device time between HIP events
- * recorded on the session stream around each launch, and the algorithmic
- * HBM bytes / multiply-accumulates those launches imply. */
+/* Per kernel class: launches, summed device time of those launches (HIP
+ * events bound to the kernels on the session stream, first kernel's start
+ * to last kernel's end of each timed launch), and the algorithmic HBM bytes /
+ * multiply-accumulates they imply. */
 typedef struct {
     char name[32];
     uint64_t launches;
@@ -137,6 +138,9 @@ typedef struct {
 /* Enables (1) or disables (0) event timing of every launch; enabling
  * clears the accumulated statistics. */
 int dtl_session_set_profiling(dtl_session *session, int enable);
+/* While profiling is enabled, time only launches of this kernel class
+ * (NULL or "": every class); the others run untimed. */
+int dtl_session_profile_only(dtl_session *session, const char *kernel_class);
 /* Copies up to cap entries; *n receives the number of kernel classes. */
 int dtl_session_profile(dtl_session *session, dtl_kernel_stat *out, size_t cap, size_t *n);
 

@@ -74,12 +74,14 @@ def test_baseline_shapes_match_oracle(name, layers, n_tok, chunk):
     _compare_with_oracle(data, synth.tokens(w, n_tok), chunk)
 
 
-def test_packed_q4k_chunk_path_matches_oracle(monkeypatch):
-    # Without the f32 weight copies the chunked Q4_K GEMM decodes the packed
-    # superblocks itself; both paths must give the reference bits.
+@pytest.mark.parametrize("env", ["DETLLM_NO_F32_MIRROR", "DETLLM_NO_Q6K_PLANES"])
+def test_packed_chunk_paths_match_oracle(monkeypatch, env):
+    # Without the encode copies (Q4_K f32 weights, Q6_K matrix-core planes)
+    # the chunked GEMMs decode the packed superblocks themselves; every path
+    # must give the reference bits.
     from detllm_amd import synth
 
-    monkeypatch.setenv("DETLLM_NO_F32_MIRROR", "1")
+    monkeypatch.setenv(env, "1")
     w = synth.WORKLOADS["tinyllama"]
     _compare_with_oracle(synth.build_model(w, layers=1), synth.tokens(w, 40), 40)
 
