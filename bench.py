@@ -81,7 +81,7 @@ def decode_leg(model, toks, positions: int) -> dict:
         prof = s.profile()
     gemv = {}
     for k, v in prof.items():
-        if k.startswith("gemm_") and v["total_ms"] > 0:
+        if (k.startswith("gemm_") or k.startswith("lm_head_")) and v["total_ms"] > 0:
             gbs = v["bytes"] / (v["total_ms"] * 1e-3) / 1e9
             gemv[k] = {"achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": round(gbs / HBM_PEAK_GBS, 4),
@@ -219,7 +219,8 @@ def main() -> int:
     ref = detref.Model(data)
     ref_logits = ref.logits(toks[:check_n])
     parity = True
-    c0, f0, tt0 = results[0][0]
+    # (cum, freq, total) of the first positions of the first timed step, across chunks
+    c0, f0, tt0 = (np.concatenate([r[k] for r in results[0]]) for k in range(3))
     for i in range(check_n):
         want = detref.symbol_range(ref_logits[i], int(toks[i + 1]), tail)
         parity &= (int(c0[i]), int(f0[i]), int(tt0[i])) == want

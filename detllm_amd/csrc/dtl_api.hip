@@ -600,6 +600,19 @@ const char* gemm_class(int type) {
   return "gemm";
 }
 
+// The output projection (lm_head) is timed as its own class: it is the one
+// large matrix of a decode step.
+const char* lm_head_class(int type) {
+  switch (type) {
+    case GGML_F32: return "lm_head_f32";
+    case GGML_Q8_0: return "lm_head_q8_0";
+    case GGML_Q4_0: return "lm_head_q4_0";
+    case GGML_Q4_K: return "lm_head_q4_k";
+    case GGML_Q6_K: return "lm_head_q6_k";
+  }
+  return "lm_head";
+}
+
 }  // namespace
 
 struct dtl_session {
@@ -697,11 +710,12 @@ int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t po
   Profiler& P = s->prof;
   // Algorithmic traffic of one GEMM: weights once, quantised activations
   // and f32 outputs per position (the residual epilogue also reads x).
-  auto gemm = [&](const DevMat& W, const DevAct& a, float* out, const float* bias, int epi) {
+  auto gemm = [&](const DevMat& W, const DevAct& a, float* out, const float* bias, int epi,
+                  const char* cls) {
     double act = W.type == GGML_F32 ? 4.0 : (W.type == GGML_Q6_K ? 1.0 + 4.0 / 256 : 1.0 + 4.0 / 32);
     double bytes = (double)W.rows * W.cols * weight_bytes_per_elem(W.type) +
                    (double)T * W.cols * act + (double)T * W.rows * (epi == EPI_RESIDUAL ? 8.0 : 4.0);
-    P.timed(st, gemm_class(W.type), bytes, (double)W.rows * W.cols * T,
+    P.timed(st, cls ? cls : gemm_class(W.type), bytes, (double)W.rows * W.cols * T,
             [&] { launch_gemm(W, a, T, out, bias, epi, s->err, st); });
   };
   // rmsnorm of the residual stream into h, fused with the quantisation the
@@ -735,10 +749,10 @@ int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t po
                             s->err, st);
       });
     } else {
-      gemm(L.wq, a, s->q, L.bq, L.bq ? EPI_BIAS : EPI_STORE);
-      gemm(L.wk, a, s->k, L.bk, L.bk ? EPI_BIAS : EPI_STORE);
+      gemm(L.wq, a, s->q, L.bq, L.bq ? EPI_BIAS : EPI_STORE, nullptr);
+      gemm(L.wk, a, s->k, L.bk, L.bk ? EPI_BIAS : EPI_STORE, nullptr);
     }
-    gemm(L.wv, a, s->v, L.bv, L.bv ? EPI_BIAS : EPI_STORE);
+    gemm(L.wv, a, s->v, L.bv, L.bv ? EPI_BIAS : EPI_STORE, nullptr);
     P.timed(st, "rope_store", (double)T * (H + 3 * KV) * hd * 8.0, 0.0, [&] {
       launch_rope_store(s->q, s->k, s->v, s->rope_cos, s->rope_sin, T, (int)pos0, H, KV, hd,
                         (int)c.rope_dim, c.split_half, s->kc, s->vc, (int)l, (int)s->n_ctx,
@@ -750,7 +764,7 @@ int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t po
                                c.attention_scale, s->scores, s->attn, s->err, st);
             });
     a = prepare_input(s, s->attn, T, H * hd, {&L.wo});
-    gemm(L.wo, a, s->x, nullptr, EPI_RESIDUAL);
+    gemm(L.wo, a, s->x, nullptr, EPI_RESIDUAL, nullptr);
     a = rms(L.ffn_norm, {&L.gate, &L.up});
     if (T >= 16 && L.gate.type == GGML_Q4_K && L.up.type == GGML_Q4_K &&
         L.gate.rows == L.up.rows && L.gate.cols == L.up.cols) {
@@ -761,16 +775,16 @@ int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t po
         launch_gemm_pair_swiglu_q4k(L.gate, L.up, a, T, nullptr, nullptr, s->ffo, s->err, st);
       });
     } else {
-      gemm(L.gate, a, s->g, nullptr, EPI_STORE);
-      gemm(L.up, a, s->u, nullptr, EPI_STORE);
+      gemm(L.gate, a, s->g, nullptr, EPI_STORE, nullptr);
+      gemm(L.up, a, s->u, nullptr, EPI_STORE, nullptr);
       P.timed(st, "swiglu", (double)T * ff * 12.0, 0.0,
               [&] { launch_swiglu(s->g, s->u, T * ff, s->ffo, s->err, st); });
     }
     a = prepare_input(s, s->ffo, T, ff, {&L.down});
-    gemm(L.down, a, s->x, nullptr, EPI_RESIDUAL);
+    gemm(L.down, a, s->x, nullptr, EPI_RESIDUAL, nullptr);
   }
   DevAct a = rms(m->out_norm, {&m->out});
-  gemm(m->out, a, s->logits, nullptr, EPI_STORE);
+  gemm(m->out, a, s->logits, nullptr, EPI_STORE, lm_head_class(m->out.type));
   HIP_TRY(hipGetLastError());
   int bits = 0;
   int rc = read_err(s, &bits);

@@ -78,57 +78,74 @@ __global__ void __launch_bounds__(256) k_gemv_q8(DevMat W, const int8_t* __restr
   // Q8_0: a 32-byte block is two 16-byte chunks (lanes c, c^1); Q4_0: one
   // 16-byte block of nibbles per lane.
   const int nchunk = TYPE == kGgmlQ8_0 ? 2 * nb : nb;
+  for (int c0 = 0; c0 < nchunk; c0 += 64) {
+    const int c = c0 + lane;
+    const bool cv = c < nchunk;
+    const int b = TYPE == kGgmlQ8_0 ? c >> 1 : c;
+    // Every load of this chunk column (R weight chunks, their block scales,
+    // the activation and its scale) is issued before any arithmetic.
+    uint4 w4[R];
+    uint16_t dsc[R];
 #pragma unroll
-  for (int r = 0; r < R; r++) {
-    const int row = row0 + r;
-    const bool rv = row < rows;
-    for (int c0 = 0; c0 < nchunk; c0 += 64) {
-      const int c = c0 + lane;
-      const bool cv = rv && c < nchunk;
+    for (int r = 0; r < R; r++) {
+      const int row = row0 + r < rows ? row0 + r : rows - 1;
+      w4[r] = make_uint4(0, 0, 0, 0);
+      dsc[r] = 0;
+      if (cv) {
+        if (TYPE == kGgmlQ8_0)
+          w4[r] = *(const uint4*)((const int8_t*)W.w + (size_t)row * cols + (size_t)c * 16);
+        else
+          w4[r] = *(const uint4*)((const uint8_t*)W.w + ((size_t)row * nb + c) * 16);
+        dsc[r] = W.d16[(size_t)row * nb + b];
+      }
+    }
+    uint4 a0 = make_uint4(0, 0, 0, 0), a1 = make_uint4(0, 0, 0, 0);
+    float dact = 0.0f;
+    if (cv) {
+      if (TYPE == kGgmlQ8_0) {
+        a0 = *(const uint4*)(arow + (size_t)c * 16);
+      } else {
+        a0 = *(const uint4*)(arow + (size_t)c * 32);
+        a1 = *(const uint4*)(arow + (size_t)c * 32 + 16);
+      }
+      dact = drow[b];
+    }
+    int asum = 0;
+    if (TYPE != kGgmlQ8_0) {
+      // Q4_0 nibbles are offset by 8: isum = sum(lo*a) + sum(hi*a') - 8*sum(a).
+      const uint32_t ones = 0x01010101u;
+      asum = dot4(ones, a0.x, asum);
+      asum = dot4(ones, a0.y, asum);
+      asum = dot4(ones, a0.z, asum);
+      asum = dot4(ones, a0.w, asum);
+      asum = dot4(ones, a1.x, asum);
+      asum = dot4(ones, a1.y, asum);
+      asum = dot4(ones, a1.z, asum);
+      asum = dot4(ones, a1.w, asum);
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
       int isum = 0;
       if (TYPE == kGgmlQ8_0) {
-        if (cv) {
-          uint4 w4 = *(const uint4*)((const int8_t*)W.w + (size_t)row * cols + (size_t)c * 16);
-          uint4 a4 = *(const uint4*)(arow + (size_t)c * 16);
-          isum = dot4(w4.x, a4.x, isum);
-          isum = dot4(w4.y, a4.y, isum);
-          isum = dot4(w4.z, a4.z, isum);
-          isum = dot4(w4.w, a4.w, isum);
-        }
+        isum = dot4(w4[r].x, a0.x, isum);
+        isum = dot4(w4[r].y, a0.y, isum);
+        isum = dot4(w4[r].z, a0.z, isum);
+        isum = dot4(w4[r].w, a0.w, isum);
         isum += __shfl_xor(isum, 1);
-        if (cv && !(c & 1)) {
-          const int b = c >> 1;
-          mine[r * nb + b] = (f16_to_f32(W.d16[(size_t)row * nb + b]) * drow[b]) * (float)isum;
-        }
       } else {
-        if (cv) {
-          // lo nibble i pairs with activation i, hi nibble with i + 16; both
-          // are offset by 8: isum = sum(lo*a) + sum(hi*a') - 8*sum(a).
-          uint4 w4 = *(const uint4*)((const uint8_t*)W.w + ((size_t)row * nb + c) * 16);
-          uint4 a0 = *(const uint4*)(arow + (size_t)c * 32);
-          uint4 a1 = *(const uint4*)(arow + (size_t)c * 32 + 16);
-          const uint32_t m = 0x0f0f0f0fu, ones = 0x01010101u;
-          isum = dot4(w4.x & m, a0.x, isum);
-          isum = dot4(w4.y & m, a0.y, isum);
-          isum = dot4(w4.z & m, a0.z, isum);
-          isum = dot4(w4.w & m, a0.w, isum);
-          isum = dot4((w4.x >> 4) & m, a1.x, isum);
-          isum = dot4((w4.y >> 4) & m, a1.y, isum);
-          isum = dot4((w4.z >> 4) & m, a1.z, isum);
-          isum = dot4((w4.w >> 4) & m, a1.w, isum);
-          int asum = 0;
-          asum = dot4(ones, a0.x, asum);
-          asum = dot4(ones, a0.y, asum);
-          asum = dot4(ones, a0.z, asum);
-          asum = dot4(ones, a0.w, asum);
-          asum = dot4(ones, a1.x, asum);
-          asum = dot4(ones, a1.y, asum);
-          asum = dot4(ones, a1.z, asum);
-          asum = dot4(ones, a1.w, asum);
-          isum -= 8 * asum;
-          mine[r * nb + c] = (f16_to_f32(W.d16[(size_t)row * nb + c]) * drow[c]) * (float)isum;
-        }
+        const uint32_t m = 0x0f0f0f0fu;
+        isum = dot4(w4[r].x & m, a0.x, isum);
+        isum = dot4(w4[r].y & m, a0.y, isum);
+        isum = dot4(w4[r].z & m, a0.z, isum);
+        isum = dot4(w4[r].w & m, a0.w, isum);
+        isum = dot4((w4[r].x >> 4) & m, a1.x, isum);
+        isum = dot4((w4[r].y >> 4) & m, a1.y, isum);
+        isum = dot4((w4[r].z >> 4) & m, a1.z, isum);
+        isum = dot4((w4[r].w >> 4) & m, a1.w, isum);
+        isum -= 8 * asum;
       }
+      const bool writer = TYPE == kGgmlQ8_0 ? cv && !(c & 1) : cv;
+      if (writer && row0 + r < rows) mine[r * nb + b] = (f16_to_f32(dsc[r]) * dact) * (float)isum;
     }
   }
   __syncthreads();
@@ -142,6 +159,88 @@ __global__ void __launch_bounds__(256) k_gemv_q8(DevMat W, const int8_t* __restr
 }
 
 // ---------------------------------------------------------------------------
+// Q8_0 streaming variant for tall matrices with at most 1024 columns (the
+// output projection of the small-vocabulary-heavy shapes): every wave walks
+// groups of R rows in a grid-stride loop, loading the next group's weights
+// and scales while it reduces the current one, so HBM sees a steady stream
+// rather than one burst per wave.  Lane c owns 16-byte chunk c of every row
+// (nchunk <= 64), so the activation chunk is loaded once per wave.
+template <int R>
+__global__ void __launch_bounds__(256) k_gemv_q8_0_stream(DevMat W, const int8_t* __restrict__ qa,
+                                                          const float* __restrict__ da, float* out,
+                                                          const float* bias, int epi, int* err) {
+  extern __shared__ __align__(16) float vb[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = blockIdx.y;
+  const int rows = W.rows, cols = W.cols, nb = W.nb;
+  const int nchunk = 2 * nb;
+  const int c = lane, b = c >> 1;
+  const bool cv = c < nchunk;
+  float* mine = vb + (size_t)wave * R * nb;
+  const int ngroups = (rows + R - 1) / R;
+  const int stride = gridDim.x * 4;
+  uint4 a0 = make_uint4(0, 0, 0, 0);
+  float dact = 0.0f;
+  if (cv) {
+    a0 = *(const uint4*)(qa + (size_t)t * cols + (size_t)c * 16);
+    dact = da[(size_t)t * nb + b];
+  }
+  uint4 w4[2][R];
+  uint16_t dsc[2][R];
+  auto load = [&](int slot, int g) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      int row = g * R + r;
+      row = row < rows ? row : rows - 1;
+      w4[slot][r] = make_uint4(0, 0, 0, 0);
+      dsc[slot][r] = 0;
+      if (cv) {
+        w4[slot][r] = *(const uint4*)((const int8_t*)W.w + (size_t)row * cols + (size_t)c * 16);
+        dsc[slot][r] = W.d16[(size_t)row * nb + b];
+      }
+    }
+  };
+  auto reduce = [&](int slot, int g) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      int isum = 0;
+      isum = dot4(w4[slot][r].x, a0.x, isum);
+      isum = dot4(w4[slot][r].y, a0.y, isum);
+      isum = dot4(w4[slot][r].z, a0.z, isum);
+      isum = dot4(w4[slot][r].w, a0.w, isum);
+      isum += __shfl_xor(isum, 1);
+      if (cv && !(c & 1)) mine[r * nb + b] = (f16_to_f32(dsc[slot][r]) * dact) * (float)isum;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    if (lane < R) {
+      const int row = g * R + lane;
+      if (row < rows) {
+        float v = chain_sum(mine + lane * nb, nb);
+        if (!epilogue(v, out, (size_t)t * rows + row, bias, row, epi)) flag(err, ERRBIT_NON_FINITE);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  };
+  int g = blockIdx.x * 4 + wave;
+  if (g >= ngroups) return;
+  load(0, g);
+  for (;;) {
+    const int gn = g + stride;
+    if (gn < ngroups) load(1, gn);
+    reduce(0, g);
+    if (gn >= ngroups) break;
+    g = gn;
+    const int gn2 = g + stride;
+    if (gn2 < ngroups) load(0, gn2);
+    reduce(1, g);
+    if (gn2 >= ngroups) break;
+    g = gn2;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Q6_K.  One wave per workgroup; lane = (row_local, superblock) with
 // rpw = 64 / nsb rows per wave.  Q8_K activations are class-major inside each
 // 256-block (element e at (e % 8) * 32 + e / 8).
@@ -149,6 +248,7 @@ __global__ void __launch_bounds__(64) k_gemv_q6k(DevMat W, const int8_t* __restr
                                                  const float* __restrict__ dk, float* out,
                                                  const float* bias, int epi, int* err) {
   __shared__ int aux_s[64][9];
+  __shared__ float d_s[64];
   const int lane = threadIdx.x;
   const int t = blockIdx.y;
   const int rows = W.rows, cols = W.cols, nsb = W.nb;
@@ -156,81 +256,87 @@ __global__ void __launch_bounds__(64) k_gemv_q6k(DevMat W, const int8_t* __restr
   const int rl = lane / nsb, sb = lane % nsb;
   const int row = blockIdx.x * rpw + rl;
   const bool active = rl < rpw && row < rows;
+  // Every load (both halves of the superblock, its activations and both
+  // scales) is issued before any arithmetic; inactive lanes read row 0.
+  const int lrow = active ? row : 0, lsb = active ? sb : 0;
+  const uint32_t* body =
+      (const uint32_t*)((const uint8_t*)W.w + ((size_t)lrow * nsb + lsb) * 208);
+  const uint32_t* act = (const uint32_t*)(qk + (size_t)t * cols + (size_t)lsb * 256);
+  uint32_t ql[2][16], qh[2][8], sc[2][2], a[2][8][4];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      uint4 v = ((const uint4*)(body + 16 * h))[i];
+      ql[h][4 * i] = v.x;
+      ql[h][4 * i + 1] = v.y;
+      ql[h][4 * i + 2] = v.z;
+      ql[h][4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      uint4 v = ((const uint4*)(body + 32 + 8 * h))[i];
+      qh[h][4 * i] = v.x;
+      qh[h][4 * i + 1] = v.y;
+      qh[h][4 * i + 2] = v.z;
+      qh[h][4 * i + 3] = v.w;
+    }
+    sc[h][0] = body[48 + 2 * h];
+    sc[h][1] = body[48 + 2 * h + 1];
+    // class k, half h: elements e = 128h + 8j + k for j in 0..15 sit at
+    // bytes 32k + 16h .. +15 of the block; dword p holds l0 = k + 8i, i = 0..3
+    // of part p.
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      uint4 v = *(const uint4*)(act + 8 * k + 4 * h);
+      a[h][k][0] = v.x;
+      a[h][k][1] = v.y;
+      a[h][k][2] = v.z;
+      a[h][k][3] = v.w;
+    }
+  }
+  const uint16_t dw = W.d16[(size_t)lrow * nsb + lsb];
+  const float da = dk[(size_t)t * nsb + lsb];
   int aux[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  if (active) {
-    const uint32_t* body =
-        (const uint32_t*)((const uint8_t*)W.w + ((size_t)row * nsb + sb) * 208);
-    const uint32_t* act = (const uint32_t*)(qk + (size_t)t * cols + (size_t)sb * 256);
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-      uint32_t ql[16], qh[8], sc[2], a[8][4];
+  for (int h = 0; h < 2; h++) {
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        uint4 v = ((const uint4*)(body + 16 * h))[i];
-        ql[4 * i] = v.x;
-        ql[4 * i + 1] = v.y;
-        ql[4 * i + 2] = v.z;
-        ql[4 * i + 3] = v.w;
-      }
+    for (int k = 0; k < 8; k++) {
+      int acc = 0;
 #pragma unroll
-      for (int i = 0; i < 2; i++) {
-        uint4 v = ((const uint4*)(body + 32 + 8 * h))[i];
-        qh[4 * i] = v.x;
-        qh[4 * i + 1] = v.y;
-        qh[4 * i + 2] = v.z;
-        qh[4 * i + 3] = v.w;
-      }
-      sc[0] = body[48 + 2 * h];
-      sc[1] = body[48 + 2 * h + 1];
-      // class k, half h: elements e = 128h + 8j + k for j in 0..15 sit at
-      // bytes 32k + 16h .. +15 of the block; dword p holds l0 = k + 8i, i = 0..3
-      // of part p.
+      for (int p = 0; p < 4; p++) {
 #pragma unroll
-      for (int k = 0; k < 8; k++) {
-        uint4 v = *(const uint4*)(act + 8 * k + 4 * h);
-        a[k][0] = v.x;
-        a[k][1] = v.y;
-        a[k][2] = v.z;
-        a[k][3] = v.w;
-      }
+        for (int pair = 0; pair < 2; pair++) {
+          // scale index 8h + l0/16 + 2p (l0 = k + 8i: i = 0,1 -> 0; 2,3 -> 1)
+          const int si = pair + 2 * p;
+          const int scale = (int)(int8_t)((sc[h][si >> 2] >> (8 * (si & 3))) & 0xffu);
+          int s = 0;
 #pragma unroll
-      for (int k = 0; k < 8; k++) {
-        int acc = 0;
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-#pragma unroll
-          for (int pair = 0; pair < 2; pair++) {
-            // scale index 8h + l0/16 + 2p (l0 = k + 8i: i = 0,1 -> 0; 2,3 -> 1)
-            const int si = pair + 2 * p;
-            const int scale = (int)(int8_t)((sc[si >> 2] >> (8 * (si & 3))) & 0xffu);
-            int s = 0;
-#pragma unroll
-            for (int ii = 0; ii < 2; ii++) {
-              const int i = 2 * pair + ii;
-              const int l0 = k + 8 * i;
-              const int qlb = l0 + 32 * (p & 1);
-              const uint32_t lo =
-                  (ql[qlb >> 2] >> (8 * (qlb & 3) + 4 * (p >> 1))) & 0x0fu;
-              const uint32_t hi = (qh[l0 >> 2] >> (8 * (l0 & 3) + 2 * p)) & 0x03u;
-              const int q6 = (int)(lo | (hi << 4)) - 32;
-              const int av = (int)(int8_t)((a[k][p] >> (8 * i)) & 0xffu);
-              s += q6 * av;
-            }
-            acc += scale * s;
+          for (int ii = 0; ii < 2; ii++) {
+            const int i = 2 * pair + ii;
+            const int l0 = k + 8 * i;
+            const int qlb = l0 + 32 * (p & 1);
+            const uint32_t lo = (ql[h][qlb >> 2] >> (8 * (qlb & 3) + 4 * (p >> 1))) & 0x0fu;
+            const uint32_t hi = (qh[h][l0 >> 2] >> (8 * (l0 & 3) + 2 * p)) & 0x03u;
+            const int q6 = (int)(lo | (hi << 4)) - 32;
+            const int av = (int)(int8_t)((a[h][k][p] >> (8 * i)) & 0xffu);
+            s += q6 * av;
           }
+          acc += scale * s;
         }
-        aux[k] += acc;
       }
+      aux[k] += acc;
     }
   }
 #pragma unroll
   for (int k = 0; k < 8; k++) aux_s[lane][k] = aux[k];
+  d_s[lane] = f16_to_f32(dw) * da;
   __syncthreads();
   if (lane < rpw && blockIdx.x * rpw + lane < rows) {
     const int r = blockIdx.x * rpw + lane;
     float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int b = 0; b < nsb; b++) {
-      const float d = f16_to_f32(W.d16[(size_t)r * nsb + b]) * dk[(size_t)t * nsb + b];
+      const float d = d_s[lane * nsb + b];
       const int* ax = aux_s[lane * nsb + b];
 #pragma unroll
       for (int l = 0; l < 8; l++) sums[l] += d * (float)ax[l];
@@ -307,6 +413,18 @@ void launch_q8(const DevMat& W, const DevAct& A, int T, float* out, const float*
 
 bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const float* bias, int epi,
                  int* err, hipStream_t s) {
+  if (W.type == kGgmlQ8_0 && W.nb <= 32 && W.rows >= 16384) {
+    // Tall, narrow Q8_0 (the output projection): streaming waves, as many
+    // workgroups as stay resident (four per CU at this kernel's occupancy).
+    constexpr int R = 8;
+    const int ngroups = (W.rows + R - 1) / R;
+    int wgs = (ngroups + 3) / 4;
+    if (wgs > 256 * 4) wgs = 256 * 4;
+    size_t smem = (size_t)4 * R * W.nb * sizeof(float);
+    launch_kernel(k_gemv_q8_0_stream<R>, dim3(wgs, T), dim3(256), smem, s, W, A.qa, A.da, out,
+                  bias, epi, err);
+    return true;
+  }
   if (W.type == kGgmlQ8_0 || W.type == kGgmlQ4_0) {
     // Rows per wave: enough waves to fill the chip on small matrices, more
     // rows per wave (fewer chain tails) on tall ones; LDS holds R*nb terms per wave.
