@@ -67,17 +67,22 @@ def copy_probe(mib: int) -> int:
     return 0
 
 
-def decode_leg(model, toks, positions: int) -> dict:
-    """Single-position decode (forward_one) over the first positions of the
-    workload: tokens/s and the achieved HBM bandwidth of the GEMV classes."""
+def decode_leg(model, toks, positions: int, workload: str) -> dict:
+    """Single-position decode (forward_one) over the first positions of a
+    workload: tokens/s and the achieved HBM bandwidth of the GEMV classes
+    (the output projection, lm_head_*, is the one large matrix per step)."""
     with model.forward_workspace(len(toks), 1) as s:
         s.forward_one(int(toks[0]), 0)  # warm-up
         s.reset()
-        s.set_profiling(True)
         t = time.perf_counter()
         for p in range(positions):
             s.forward_one(int(toks[p]), p)
         dt = time.perf_counter() - t
+        # A second pass over the same positions with every launch timed.
+        s.reset()
+        s.set_profiling(True)
+        for p in range(positions):
+            s.forward_one(int(toks[p]), p)
         prof = s.profile()
     gemv = {}
     for k, v in prof.items():
@@ -89,7 +94,7 @@ def decode_leg(model, toks, positions: int) -> dict:
                        "algorithmic_bytes_per_launch": v["bytes"] / v["launches"]}
     tot_b = sum(prof[k]["bytes"] for k in gemv)
     tot_ms = sum(prof[k]["total_ms"] for k in gemv)
-    return {"positions": positions, "tokens_per_s": round(positions / dt, 2),
+    return {"workload": workload, "positions": positions, "tokens_per_s": round(positions / dt, 2),
             "gemv_all": {"achieved": round(tot_b / (tot_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(tot_b / (tot_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
             "gemv": gemv}
@@ -103,6 +108,8 @@ def main() -> int:
     ap.add_argument("--workload", default="tinyllama")
     ap.add_argument("--cpu-tokens", type=int, default=96)
     ap.add_argument("--decode-positions", type=int, default=64)
+    ap.add_argument("--decode-workload", default="qwen05",
+                    help="model of the decode leg (qwen05: Q8_0 with a 145 MB output projection)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain copy of this many MiB (counter calibration) and exit")
     ap.add_argument("--cpu-threads", type=int, default=0)
@@ -231,7 +238,13 @@ def main() -> int:
 
     decode = None
     if args.decode_positions > 0:
-        decode = decode_leg(model, toks, args.decode_positions)
+        if args.decode_workload == w.name:
+            dmodel, dtoks = model, toks
+        else:
+            dw = synth.WORKLOADS[args.decode_workload]
+            dmodel, dtoks = F32Llama.from_gguf(synth.build_model(dw)), synth.tokens(dw)
+        decode = decode_leg(dmodel, dtoks, args.decode_positions, args.decode_workload)
+        del dmodel
         log(f"[bench] decode {decode['tokens_per_s']} tok/s, GEMV {decode['gemv_all']['achieved']} GB/s")
 
     cpu = None

@@ -630,6 +630,7 @@ struct dtl_session {
   // CDF staging
   uint32_t *c_sym = nullptr, *c_freq = nullptr, *c_freq_tab = nullptr;
   uint64_t *c_cum = nullptr, *c_total = nullptr, *c_values = nullptr, *c_cum_tab = nullptr;
+  uint8_t* c_scratch = nullptr;  // multi-workgroup CDF scratch for max_chunk rows
   size_t rows_valid = 0;  // rows of `logits` written by the last forward
   Profiler prof;
 };
@@ -744,7 +745,7 @@ int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t po
       // wq and wk share the input: one launch over their concatenated rows.
       double bytes = (double)(L.wq.rows + L.wk.rows) * L.wq.cols * weight_bytes_per_elem(GGML_Q4_K) +
                      (double)T * L.wq.cols * (1.0 + 4.0 / 32) + (double)T * (L.wq.rows + L.wk.rows) * 4.0;
-      P.timed(st, gemm_class(GGML_Q4_K), bytes, (double)(L.wq.rows + L.wk.rows) * L.wq.cols * T, [&] {
+      P.timed(st, "gemm_q4_k_qk", bytes, (double)(L.wq.rows + L.wk.rows) * L.wq.cols * T, [&] {
         launch_gemm_cat_q4k(L.wq, L.wk, a, T, s->q, s->k, L.bq, L.bk, L.bq ? EPI_BIAS : EPI_STORE,
                             s->err, st);
       });
@@ -961,6 +962,7 @@ int dtl_session_new(const dtl_model* m, size_t n_ctx, size_t max_chunk, dtl_sess
   ALLOC(c_values, C);
   ALLOC(c_freq_tab, m->vocab + 256);
   ALLOC(c_cum_tab, m->vocab + 256);
+  ALLOC(c_scratch, cdf_scratch_bytes((int)C, (int)m->vocab));
 #undef ALLOC
   HIP_TRY(hipMemsetAsync(s->kc, 0, kv * 4, s->stream));
   HIP_TRY(hipMemsetAsync(s->vc, 0, kv * 4, s->stream));
@@ -1059,8 +1061,8 @@ int dtl_symbol_ranges(dtl_session* s, size_t first, size_t n, const uint32_t* sy
   clear_err(s);
   HIP_TRY(hipMemcpyAsync(s->c_sym, symbols, n * 4, hipMemcpyHostToDevice, s->stream));
   s->prof.timed(s->stream, "cdf_symbol_range", (double)n * V * 4.0, 0.0, [&] {
-    launch_cdf(s->logits + first * V, (int)n, (int)V, (int)tail, 0, s->c_sym, nullptr, s->c_cum,
-               s->c_freq, s->c_total, nullptr, nullptr, nullptr, s->err, s->stream);
+    launch_cdf_blocks(s->logits + first * V, (int)n, (int)V, (int)tail, 0, s->c_sym, nullptr,
+                      s->c_cum, s->c_freq, s->c_total, nullptr, s->c_scratch, s->err, s->stream);
   });
   HIP_TRY(hipMemcpyAsync(cum, s->c_cum, n * 8, hipMemcpyDeviceToHost, s->stream));
   HIP_TRY(hipMemcpyAsync(freq, s->c_freq, n * 4, hipMemcpyDeviceToHost, s->stream));
@@ -1117,8 +1119,8 @@ int dtl_decoder_total(dtl_session* s, size_t row, size_t tail, uint64_t* total) 
   if (V + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
   HIP_TRY(hipSetDevice(s->m->device));
   clear_err(s);
-  launch_cdf(s->logits + row * V, 1, (int)V, (int)tail, 3, nullptr, nullptr, nullptr, nullptr,
-             s->c_total, nullptr, nullptr, nullptr, s->err, s->stream);
+  launch_cdf_blocks(s->logits + row * V, 1, (int)V, (int)tail, 3, nullptr, nullptr, nullptr,
+                    nullptr, s->c_total, nullptr, s->c_scratch, s->err, s->stream);
   HIP_TRY(hipMemcpyAsync(total, s->c_total, 8, hipMemcpyDeviceToHost, s->stream));
   int bits = 0, st = read_err(s, &bits);
   return st ? st : cdf_status(bits);
@@ -1133,8 +1135,8 @@ int dtl_decoder_lookup(dtl_session* s, size_t row, size_t tail, uint64_t value, 
   HIP_TRY(hipSetDevice(s->m->device));
   clear_err(s);
   HIP_TRY(hipMemcpyAsync(s->c_values, &value, 8, hipMemcpyHostToDevice, s->stream));
-  launch_cdf(s->logits + row * V, 1, (int)V, (int)tail, 2, nullptr, s->c_values, s->c_cum,
-             s->c_freq, s->c_total, s->c_sym, nullptr, nullptr, s->err, s->stream);
+  launch_cdf_blocks(s->logits + row * V, 1, (int)V, (int)tail, 2, nullptr, s->c_values,
+                    s->c_cum, s->c_freq, s->c_total, s->c_sym, s->c_scratch, s->err, s->stream);
   HIP_TRY(hipMemcpyAsync(symbol, s->c_sym, 4, hipMemcpyDeviceToHost, s->stream));
   HIP_TRY(hipMemcpyAsync(cum, s->c_cum, 8, hipMemcpyDeviceToHost, s->stream));
   HIP_TRY(hipMemcpyAsync(freq, s->c_freq, 4, hipMemcpyDeviceToHost, s->stream));
@@ -1199,8 +1201,15 @@ int run_cdf_host(const float* logits, size_t n, size_t tail, int mode, uint32_t 
     if ((st = sc.arena.alloc(&dft, n + tail))) return st;
     if ((st = sc.arena.alloc(&dct, n + tail))) return st;
   }
-  launch_cdf(dl, 1, (int)n, (int)tail, mode, dsym, nullptr, dcum, dfreq, dtot, nullptr, dft, dct,
-             sc.err, sc.stream);
+  if (mode == 1) {
+    launch_cdf(dl, 1, (int)n, (int)tail, mode, dsym, nullptr, dcum, dfreq, dtot, nullptr, dft, dct,
+               sc.err, sc.stream);
+  } else {
+    uint8_t* scratch;
+    if ((st = sc.arena.alloc(&scratch, cdf_scratch_bytes(1, (int)n)))) return st;
+    launch_cdf_blocks(dl, 1, (int)n, (int)tail, mode, dsym, nullptr, dcum, dfreq, dtot, nullptr,
+                      scratch, sc.err, sc.stream);
+  }
   if (mode == 1) {
     HIP_TRY(hipMemcpyAsync(freq_tab, dft, (n + tail) * 4, hipMemcpyDeviceToHost, sc.stream));
     HIP_TRY(hipMemcpyAsync(cum_tab, dct, (n + tail) * 8, hipMemcpyDeviceToHost, sc.stream));

@@ -143,6 +143,14 @@ void launch_cdf(const float* logits, int R, int V, int tail, int mode, const uin
                 const uint64_t* values, uint64_t* cum, uint32_t* freq, uint64_t* total,
                 uint32_t* sym, uint32_t* freq_tab, uint64_t* cum_tab, int* err, hipStream_t s);
 
+// Modes 0, 2 and 3 of launch_cdf spread over many workgroups per row;
+// scratch holds cdf_scratch_bytes(R, V) bytes of device memory.
+size_t cdf_scratch_bytes(int R, int V);
+void launch_cdf_blocks(const float* logits, int R, int V, int tail, int mode,
+                       const uint32_t* symbols, const uint64_t* values, uint64_t* cum,
+                       uint32_t* freq, uint64_t* total, uint32_t* sym, void* scratch, int* err,
+                       hipStream_t s);
+
 // Kernel-level parity entry points.
 void launch_exp_f32(const float* in, float* out, int n, int which, hipStream_t s);
 void launch_f16_to_f32(const uint16_t* in, float* out, int n, hipStream_t s);

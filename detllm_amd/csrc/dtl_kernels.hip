@@ -862,6 +862,101 @@ __global__ void __launch_bounds__(1024) k_attention_hd64(const float* q, const f
   if (bad) flag(err, ERRBIT_NON_FINITE);
 }
 
+// Decode shape (a few positions): one workgroup of 256 threads per (head,
+// position), so a single position still spreads over H workgroups.  All
+// threads compute scores (8-lane dot order) into LDS; a block max, the
+// clamped exps in parallel, the 8-lane Z chains (lanes 0-7), p = e / Z in
+// parallel; then wave 0 runs the 64 P.V chains (lane = dimension),
+// streaming V rows with eight loads in flight.
+__global__ void __launch_bounds__(256) k_attention_dec(const float* q, const float* kc,
+                                                       const float* vc, int layer, int pos0,
+                                                       int H, int KV, int n_ctx, float scale,
+                                                       float* out, int* err) {
+  extern __shared__ __align__(16) float sc[];  // [len] scores -> exps -> probabilities
+  __shared__ __align__(16) float qs[64];
+  __shared__ float red[4];
+  __shared__ float zc[8];
+  constexpr int hd = 64;
+  const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+  const int g = h / (H / KV);
+  const int pos = pos0 + t, len = pos + 1;
+  const float* keys = kc + ((size_t)layer * KV + g) * n_ctx * hd;
+  const float* vals = vc + ((size_t)layer * KV + g) * n_ctx * hd;
+  float* o = out + (size_t)t * H * hd + (size_t)h * hd;
+  if (len == 1) {  // a single score copies V exactly (lib.rs:2319-2321)
+    if (tid < hd) o[tid] = vals[tid];
+    return;
+  }
+  bool bad = false;
+  if (tid < hd) qs[tid] = q[(size_t)t * H * hd + (size_t)h * hd + tid];
+  __syncthreads();
+  // scores: dot_f32_ref(q, k_j) * scale
+  for (int j = tid; j < len; j += 256) {
+    const float4* kr = reinterpret_cast<const float4*>(keys + (size_t)j * hd);
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int i4 = 0; i4 < 16; i4++) {
+      const float4 kv = kr[i4];
+      const int i = 4 * i4;
+      acc[(i + 0) & 7] += qs[i + 0] * kv.x;
+      acc[(i + 1) & 7] += qs[i + 1] * kv.y;
+      acc[(i + 2) & 7] += qs[i + 2] * kv.z;
+      acc[(i + 3) & 7] += qs[i + 3] * kv.w;
+    }
+    const float s = finish_8lane(acc) * scale;
+    if (!finite(s)) bad = true;
+    sc[j] = s;
+  }
+  __syncthreads();
+  // softmax_in_place (lib.rs:2361-2388)
+  float mx = -__builtin_huge_valf();
+  for (int j = tid; j < len; j += 256) mx = fmaxf(mx, sc[j]);
+  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  for (int j = tid; j < len; j += 256) sc[j] = exp_clamped(sc[j] - mx);
+  __syncthreads();
+  if (tid < 8) {
+    float acc = 0.0f;
+    int j = tid;
+    for (; j + 56 < len; j += 64) {
+      const float e0 = sc[j], e1 = sc[j + 8], e2 = sc[j + 16], e3 = sc[j + 24];
+      const float e4 = sc[j + 32], e5 = sc[j + 40], e6 = sc[j + 48], e7 = sc[j + 56];
+      acc += e0; acc += e1; acc += e2; acc += e3;
+      acc += e4; acc += e5; acc += e6; acc += e7;
+    }
+    for (; j < len; j += 8) acc += sc[j];
+    zc[tid] = acc;
+  }
+  __syncthreads();
+  const float z = finish_8lane(zc);
+  if (!finite(z) || z == 0.0f) bad = true;
+  for (int j = tid; j < len; j += 256) {
+    const float p = sc[j] / z;
+    if (!finite(p)) bad = true;
+    sc[j] = p;
+  }
+  __syncthreads();
+  // P.V: out[d] = 0.0; out[d] += p_j * v_j[d] for j ascending
+  if (tid < hd) {
+    const float* vd = vals + tid;
+    float a = 0.0f;
+    int j = 0;
+    for (; j + 8 <= len; j += 8) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) v[k] = vd[(size_t)(j + k) * hd];
+#pragma unroll
+      for (int k = 0; k < 8; k++) a += sc[j + k] * v[k];
+    }
+    for (; j < len; j++) a += sc[j] * vd[(size_t)j * hd];
+    if (!finite(a)) bad = true;
+    o[tid] = a;
+  }
+  if (bad) flag(err, ERRBIT_NON_FINITE);
+}
+
 size_t attention_hd64_smem(int G, int sc_stride) {
   return ((size_t)G * sc_stride + 2 * kA64Buf + (size_t)G * 64) * sizeof(float);
 }
@@ -875,6 +970,21 @@ void launch_attention(const float* q, const float* kc, const float* vc, int laye
                       int H, int KV, int hd, int n_ctx, float scale, float* scores, float* out,
                       int* err, hipStream_t s) {
   int G = H / KV;
+  if (hd == 64 && T <= 4) {
+    // Decode: one workgroup per (head, position).
+    size_t smem = (size_t)(pos0 + T) * sizeof(float);
+    if (smem <= 150 * 1024) {
+      static bool attr_dec_set = false;
+      if (!attr_dec_set) {
+        (void)hipFuncSetAttribute((const void*)k_attention_dec,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
+        attr_dec_set = true;
+      }
+      launch_kernel(k_attention_dec, dim3(H, T), dim3(256), smem, s, q, kc, vc, layer, pos0, H,
+                    KV, n_ctx, scale, out, err);
+      return;
+    }
+  }
   if (hd == 64 && G >= 2 && G <= 16) {
     // Scores only need the longest row of this chunk (rounded to float4).
     int sc_stride = ((pos0 + T) + 3) & ~3;
@@ -1189,6 +1299,323 @@ __global__ void __launch_bounds__(256) k_cdf(const float* logits, int V, int tai
   } else {
     if (tid == 0) total[r] = tot_all;
   }
+}
+
+// ---------------------------------------------------------------------------
+// The same CDF split over many workgroups per row (modes 0, 2, 3): block
+// maxima, block exps written chain-major, one wave per row for the eight
+// serial Z chains, block frequency sums, and a per-row finish with the exact
+// integer sums / search.  Every f32 operation is the one k_cdf performs.
+namespace {
+constexpr int kCdfBlk = 4096;  // elements per workgroup (256 threads x 16)
+
+__host__ __device__ inline int cdf_nblk(int V) { return (V + kCdfBlk - 1) / kCdfBlk; }
+__host__ __device__ inline int cdf_v8(int V) { return (((V + 7) / 8) + 3) & ~3; }
+}  // namespace
+
+size_t cdf_scratch_bytes(int R, int V) {
+  const size_t nb = (size_t)cdf_nblk(V);
+  return (size_t)R * (nb * 4 + 8 * (size_t)cdf_v8(V) * 4 + 4 + nb * 16 + 4) + 256;
+}
+
+namespace {
+struct CdfScratch {
+  float* pmax;       // [R][nblk]
+  float* ebuf;       // [R][8][v8]
+  float* z;          // [R]
+  uint64_t* bsum;    // [R][nblk]
+  uint64_t* bbelow;  // [R][nblk]
+  uint32_t* symf;    // [R]
+};
+
+CdfScratch cdf_scratch(void* base, int R, int V) {
+  const size_t nb = (size_t)cdf_nblk(V);
+  char* p = (char*)base;
+  auto take = [&](size_t bytes) {
+    char* q = p;
+    p += (bytes + 15) & ~(size_t)15;
+    return q;
+  };
+  CdfScratch c;
+  c.bsum = (uint64_t*)take((size_t)R * nb * 8);
+  c.bbelow = (uint64_t*)take((size_t)R * nb * 8);
+  c.pmax = (float*)take((size_t)R * nb * 4);
+  c.ebuf = (float*)take((size_t)R * 8 * cdf_v8(V) * 4);
+  c.z = (float*)take((size_t)R * 4);
+  c.symf = (uint32_t*)take((size_t)R * 4);
+  return c;
+}
+
+__device__ float block_max_256(float v, float* red) {
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__device__ uint64_t block_sum_u64_256(uint64_t v, uint64_t* red) {
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint64_t s = red[0] + red[1] + red[2] + red[3];
+  __syncthreads();
+  return s;
+}
+}  // namespace
+
+// Block maxima (order independent) and finiteness.
+__global__ void __launch_bounds__(256) k_cdf_bmax(const float* logits, int V, CdfScratch cs,
+                                                  int* err) {
+  __shared__ float red[4];
+  const int r = blockIdx.y, b = blockIdx.x, nb = gridDim.x;
+  const float* l = logits + (size_t)r * V;
+  float v[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++) {
+    int i = b * kCdfBlk + k * 256 + threadIdx.x;
+    v[k] = i < V ? l[i] : -__builtin_huge_valf();
+  }
+  float mx = -__builtin_huge_valf();
+  bool bad = false;
+#pragma unroll
+  for (int k = 0; k < 16; k++) {
+    int i = b * kCdfBlk + k * 256 + threadIdx.x;
+    if (i < V && !finite(v[k])) bad = true;
+    mx = fmaxf(mx, v[k]);
+  }
+  if (bad) flag(err, ERRBIT_CDF_NON_FINITE);
+  mx = block_max_256(mx, red);
+  if (threadIdx.x == 0) cs.pmax[(size_t)r * nb + b] = mx;
+}
+
+// e_i = exp_f32(max(l_i - m, -88)) for the block, stored chain-major:
+// element i at [i % 8][i / 8] of the row's buffer.
+__global__ void __launch_bounds__(256) k_cdf_bexp(const float* logits, int V, CdfScratch cs) {
+  const int r = blockIdx.y, b = blockIdx.x, nb = gridDim.x;
+  const float* l = logits + (size_t)r * V;
+  float mx = -__builtin_huge_valf();
+  for (int k = 0; k < nb; k++) mx = fmaxf(mx, cs.pmax[(size_t)r * nb + k]);
+  const int v8 = cdf_v8(V);
+  float* e = cs.ebuf + (size_t)r * 8 * v8;
+  float v[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++) {
+    int i = b * kCdfBlk + k * 256 + threadIdx.x;
+    v[k] = i < V ? l[i] : 0.0f;
+  }
+#pragma unroll
+  for (int k = 0; k < 16; k++) {
+    int i = b * kCdfBlk + k * 256 + threadIdx.x;
+    if (i < V) e[(size_t)(i & 7) * v8 + (i >> 3)] = exp_clamped(v[k] - mx);
+  }
+}
+
+// Z = sum_f32_ref(e): lanes 0-7 of wave 0 each run one chain (i = c mod 8,
+// ascending) over a three-deep LDS ring that waves 1-3 fill from the
+// chain-major buffer.
+__global__ void __launch_bounds__(256) k_cdf_z(int V, CdfScratch cs) {
+  constexpr int kSeg = 256;  // elements per chain per ring slot
+  constexpr int kSlots = 3;
+  __shared__ __align__(16) float ring[kSlots][8][kSeg];
+  __shared__ float zc[8];
+  const int r = blockIdx.x, tid = threadIdx.x;
+  const int v8 = cdf_v8(V);
+  const float* e = cs.ebuf + (size_t)r * 8 * v8;
+  const int nseg = (v8 + kSeg - 1) / kSeg;
+  // Producers: 192 threads move one segment (8 chains x kSeg floats) per slot.
+  auto fill = [&](int sg) {
+    float(*dst)[kSeg] = ring[sg % kSlots];
+    for (int x = tid - 64; x < 8 * kSeg / 4; x += 192) {
+      const int c = x / (kSeg / 4), j4 = x % (kSeg / 4);
+      const int j = sg * kSeg + 4 * j4;
+      float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (j + 3 < v8) f = *reinterpret_cast<const float4*>(e + (size_t)c * v8 + j);
+      *reinterpret_cast<float4*>(&dst[c][4 * j4]) = f;
+    }
+  };
+  if (tid >= 64) {
+    fill(0);
+    if (nseg > 1) fill(1);
+  }
+  __syncthreads();
+  float acc = 0.0f;
+  for (int sg = 0; sg < nseg; sg++) {
+    if (tid >= 64) {
+      if (sg + 2 < nseg) fill(sg + 2);
+    } else if (tid < 8) {
+      const int c = tid;
+      const int cnt_total = (V - c + 7) / 8;  // elements of chain c
+      int cnt = cnt_total - sg * kSeg;
+      cnt = cnt < kSeg ? cnt : kSeg;
+      const float* my = ring[sg % kSlots][c];
+      int j = 0;
+      for (; j + 16 <= cnt; j += 16) {
+        float4 f0 = *reinterpret_cast<const float4*>(my + j);
+        float4 f1 = *reinterpret_cast<const float4*>(my + j + 4);
+        float4 f2 = *reinterpret_cast<const float4*>(my + j + 8);
+        float4 f3 = *reinterpret_cast<const float4*>(my + j + 12);
+        acc += f0.x; acc += f0.y; acc += f0.z; acc += f0.w;
+        acc += f1.x; acc += f1.y; acc += f1.z; acc += f1.w;
+        acc += f2.x; acc += f2.y; acc += f2.z; acc += f2.w;
+        acc += f3.x; acc += f3.y; acc += f3.z; acc += f3.w;
+      }
+      for (; j < cnt; j++) acc += my[j];
+    }
+    __syncthreads();
+  }
+  if (tid < 8) zc[tid] = acc;
+  __syncthreads();
+  if (tid == 0) cs.z[r] = finish_8lane(zc);
+}
+
+// Block sums of f_i = (u32)(e_i / Z * 2^24) + 1 (exact integers): all, and
+// (mode 0) those below the symbol, plus the symbol's own f.
+__global__ void __launch_bounds__(256) k_cdf_bfreq(int V, int mode, const uint32_t* symbols,
+                                                   CdfScratch cs) {
+  __shared__ uint64_t red[4];
+  const int r = blockIdx.y, b = blockIdx.x, nb = gridDim.x;
+  const int v8 = cdf_v8(V);
+  const float* e = cs.ebuf + (size_t)r * 8 * v8;
+  const float z = cs.z[r];
+  const uint32_t want = mode == 0 ? symbols[r] : 0xffffffffu;
+  // This block's elements b*4096 .. +4096 sit at chain positions
+  // [c][512 b .. 512 b + 511]; thread x takes c = x / 32 and 16 consecutive j.
+  const int c = threadIdx.x >> 5, j0 = b * (kCdfBlk / 8) + (threadIdx.x & 31) * 16;
+  uint64_t sum = 0, below = 0;
+#pragma unroll
+  for (int k = 0; k < 16; k += 4) {
+    float4 f4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (j0 + k + 3 < v8) f4 = *reinterpret_cast<const float4*>(e + (size_t)c * v8 + j0 + k);
+    const float ev[4] = {f4.x, f4.y, f4.z, f4.w};
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int i = 8 * (j0 + k + u) + c;
+      if (i < V) {
+        const uint32_t f = cdf_freq(ev[u], z);
+        sum += f;
+        if ((uint32_t)i < want) below += f;
+        if ((uint32_t)i == want) cs.symf[r] = f;
+      }
+    }
+  }
+  sum = block_sum_u64_256(sum, red);
+  if (mode == 0) below = block_sum_u64_256(below, red);
+  if (threadIdx.x == 0) {
+    cs.bsum[(size_t)r * nb + b] = sum;
+    if (mode == 0) cs.bbelow[(size_t)r * nb + b] = below;
+  }
+}
+
+// Per-row finish: totals (and the CdfError::TotalTooLarge check), the
+// symbol range (mode 0) or the decoder lookup (mode 2: block search, then a
+// scan of the f_i of that block in symbol order).
+__global__ void __launch_bounds__(256) k_cdf_finish(int V, int nb, int tail, int mode,
+                                                    const uint32_t* symbols,
+                                                    const uint64_t* values, uint64_t* cum,
+                                                    uint32_t* freq, uint64_t* total, uint32_t* sym,
+                                                    CdfScratch cs, int* err) {
+  __shared__ uint64_t scan[256];
+  __shared__ int blk_sh;
+  __shared__ uint64_t off_sh;
+  const int r = blockIdx.x, tid = threadIdx.x;
+  // Row totals: the block sums in order (exact, order free).
+  uint64_t run = 0, below = 0;
+  for (int b = 0; b < nb; b++) {
+    run += cs.bsum[(size_t)r * nb + b];
+    if (mode == 0) below += cs.bbelow[(size_t)r * nb + b];
+  }
+  const uint64_t tot_all = run + (uint64_t)tail;
+  if (tid == 0 && (run >= (1ull << 31) || tot_all >= (1ull << 31))) flag(err, ERRBIT_CDF_TOTAL);
+  if (mode == 0) {
+    if (tid == 0) {
+      const uint32_t s = symbols[r];
+      if (s < (uint32_t)V) {
+        cum[r] = below;
+        freq[r] = cs.symf[r];
+      } else {
+        cum[r] = run + (s - (uint32_t)V);
+        freq[r] = 1;
+      }
+      total[r] = tot_all;
+    }
+    return;
+  }
+  if (mode == 3) {
+    if (tid == 0) total[r] = tot_all;
+    return;
+  }
+  // mode 2
+  const uint64_t target = values[r];
+  if (tid == 0) {
+    total[r] = tot_all;
+    int blk = -1;
+    uint64_t off = 0;
+    if (target < run) {
+      for (int b = 0; b < nb; b++) {
+        const uint64_t sb = cs.bsum[(size_t)r * nb + b];
+        if (target < off + sb) {
+          blk = b;
+          break;
+        }
+        off += sb;
+      }
+    } else {
+      const uint64_t o = target - run;
+      if (o < (uint64_t)tail) {
+        sym[r] = (uint32_t)(V + o);
+        cum[r] = target;
+        freq[r] = 1;
+      } else {
+        flag(err, ERRBIT_CDF_LOOKUP);
+      }
+    }
+    blk_sh = blk;
+    off_sh = off;
+  }
+  __syncthreads();
+  const int blk = blk_sh;
+  if (blk < 0) return;
+  const int v8 = cdf_v8(V);
+  const float* e = cs.ebuf + (size_t)r * 8 * v8;
+  const float z = cs.z[r];
+  // thread tid owns symbols blk*4096 + 16 tid .. +15 (ascending)
+  uint32_t f[16];
+  uint64_t local = 0;
+  const int i0 = blk * kCdfBlk + 16 * tid;
+#pragma unroll
+  for (int k = 0; k < 16; k++) {
+    const int i = i0 + k;
+    f[k] = i < V ? cdf_freq(e[(size_t)(i & 7) * v8 + (i >> 3)], z) : 0u;
+    local += f[k];
+  }
+  uint64_t tot;
+  const uint64_t incl = block_scan_u64(local, scan, &tot);
+  uint64_t c0 = off_sh + incl - local;
+#pragma unroll
+  for (int k = 0; k < 16; k++) {
+    const int i = i0 + k;
+    if (i < V && target >= c0 && target < c0 + f[k]) {
+      sym[r] = (uint32_t)i;
+      cum[r] = c0;
+      freq[r] = f[k];
+    }
+    c0 += f[k];
+  }
+}
+
+void launch_cdf_blocks(const float* logits, int R, int V, int tail, int mode,
+                       const uint32_t* symbols, const uint64_t* values, uint64_t* cum,
+                       uint32_t* freq, uint64_t* total, uint32_t* sym, void* scratch, int* err,
+                       hipStream_t s) {
+  const int nb = cdf_nblk(V);
+  CdfScratch cs = cdf_scratch(scratch, R, V);
+  launch_kernel(k_cdf_bmax, dim3(nb, R), dim3(256), 0, s, logits, V, cs, err);
+  launch_kernel(k_cdf_bexp, dim3(nb, R), dim3(256), 0, s, logits, V, cs);
+  launch_kernel(k_cdf_z, dim3(R), dim3(256), 0, s, V, cs);
+  if (mode != 3) launch_kernel(k_cdf_bfreq, dim3(nb, R), dim3(256), 0, s, V, mode, symbols, cs);
+  else launch_kernel(k_cdf_bfreq, dim3(nb, R), dim3(256), 0, s, V, 3, symbols, cs);
+  launch_kernel(k_cdf_finish, dim3(R), dim3(256), 0, s, V, nb, tail, mode, symbols, values, cum,
+                freq, total, sym, cs, err);
 }
 
 void launch_cdf(const float* logits, int R, int V, int tail, int mode, const uint32_t* symbols,

@@ -129,8 +129,15 @@ def test_cdf_on_device_logits_matches_oracle():
             f, c, t = s.cdf(2, tail)
             rf, rc, rt = detref.logits_to_cdf(logits[2], tail)
             assert np.array_equal(f, rf) and np.array_equal(c, rc) and t == rt
-            for value in (0, int(rc[100]), int(rc[100]) + int(rf[100]) - 1, rt - 1):
-                assert s.decoder_lookup(value, 2, tail) == detref.decoder_lookup(logits[2], value, tail)
+            # values inside, at the start and at the end of symbols, including the
+            # 4096-symbol work-block edges, the last vocab symbol and the escapes
+            values = {0, rt - 1, int(rc[100]), int(rc[100]) + int(rf[100]) - 1}
+            for sym in (4095, 4096, 4097, 8191, 8192, len(rf) - tail - 1):
+                values |= {int(rc[sym]), int(rc[sym]) + int(rf[sym]) - 1}
+            if tail:
+                values |= {int(rc[len(rf) - tail]), int(rc[len(rf) - 1])}
+            for value in sorted(values):
+                assert s.decoder_lookup(value, 2, tail) == detref.decoder_lookup(logits[2], value, tail), value
             assert s.decoder_total(2, tail) == rt
 
 
