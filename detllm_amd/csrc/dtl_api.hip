@@ -631,6 +631,11 @@ struct dtl_session {
   uint32_t *c_sym = nullptr, *c_freq = nullptr, *c_freq_tab = nullptr;
   uint64_t *c_cum = nullptr, *c_total = nullptr, *c_values = nullptr, *c_cum_tab = nullptr;
   uint8_t* c_scratch = nullptr;  // multi-workgroup CDF scratch for max_chunk rows
+  // Captured single-position forward (see forward_device).
+  hipGraphExec_t graph = nullptr;
+  bool graph_failed = false;
+  int* pos_dev = nullptr;   // device copy of the position for the graph
+  int* pos_host = nullptr;  // pinned staging for it
   size_t rows_valid = 0;  // rows of `logits` written by the last forward
   Profiler prof;
 };
@@ -694,18 +699,15 @@ DevAct prepare_input(dtl_session* s, const float* x, int T, int n,
   return session_act(s, x);
 }
 
-// forward_one_with_workspace (det-model lib.rs:1249-1400) for T positions.
-int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t pos0) {
+// forward_one_with_workspace (det-model lib.rs:1249-1400) for the T
+// positions whose token ids are in s->tokens: enqueues every launch on the
+// session stream (no host synchronisation).  pos_dev: when set, the
+// position-dependent kernels read pos0 from that device int.
+int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev) {
   const dtl_model* m = s->m;
   const HostConfig& c = m->c;
-  if (T <= 0 || (size_t)T > s->max_chunk || pos0 + (size_t)T > s->n_ctx) return DTL_ERR_SHAPE;
-  for (int t = 0; t < T; t++)
-    if (tokens_host[t] >= (uint32_t)m->emb.rows) return DTL_ERR_SHAPE;
   hipStream_t st = s->stream;
-  HIP_TRY(hipSetDevice(m->device));
-  s->rows_valid = 0;
   clear_err(s);
-  HIP_TRY(hipMemcpyAsync(s->tokens, tokens_host, T * sizeof(uint32_t), hipMemcpyHostToDevice, st));
   int d = (int)c.d, ff = (int)c.ff, H = (int)c.heads, KV = (int)c.kv_heads;
   int hd = (int)m->head_dim;
   Profiler& P = s->prof;
@@ -757,12 +759,12 @@ int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t po
     P.timed(st, "rope_store", (double)T * (H + 3 * KV) * hd * 8.0, 0.0, [&] {
       launch_rope_store(s->q, s->k, s->v, s->rope_cos, s->rope_sin, T, (int)pos0, H, KV, hd,
                         (int)c.rope_dim, c.split_half, s->kc, s->vc, (int)l, (int)s->n_ctx,
-                        s->err, st);
+                        pos_dev, s->err, st);
     });
     P.timed(st, "attention", kv_rows * KV * hd * 8.0 + (double)T * H * hd * 8.0,
             kv_rows * H * hd * 2.0, [&] {
               launch_attention(s->q, s->kc, s->vc, (int)l, T, (int)pos0, H, KV, hd, (int)s->n_ctx,
-                               c.attention_scale, s->scores, s->attn, s->err, st);
+                               c.attention_scale, s->scores, s->attn, pos_dev, s->err, st);
             });
     a = prepare_input(s, s->attn, T, H * hd, {&L.wo});
     gemm(L.wo, a, s->x, nullptr, EPI_RESIDUAL, nullptr);
@@ -787,10 +789,62 @@ int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t po
   DevAct a = rms(m->out_norm, {&m->out});
   gemm(m->out, a, s->logits, nullptr, EPI_STORE, lm_head_class(m->out.type));
   HIP_TRY(hipGetLastError());
+  return DTL_OK;
+}
+
+// Single-position forwards replay one captured graph of the whole pass: the
+// position reaches the kernels through s->pos_dev, copied in before each
+// replay.  DETLLM_NO_GRAPH=1 keeps the eager launches.
+bool graph_eligible(const dtl_session* s) {
+  return !s->prof.on && !s->graph_failed && !env_flag("DETLLM_NO_GRAPH") &&
+         attention_pos_dev_supported((int)s->m->head_dim, 1, (int)s->n_ctx);
+}
+
+int capture_decode_graph(dtl_session* s) {
+  hipStream_t st = s->stream;
+  HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
+  int rc = enqueue_forward(s, 1, 0, s->pos_dev);
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(st, &g);
+  if (rc == DTL_OK && e == hipSuccess && g)
+    e = hipGraphInstantiate(&s->graph, g, nullptr, nullptr, 0);
+  if (g) (void)hipGraphDestroy(g);
+  if (rc != DTL_OK || e != hipSuccess) {
+    (void)hipGetLastError();
+    s->graph = nullptr;
+    s->graph_failed = true;
+    return DTL_ERR_DEVICE;
+  }
+  return DTL_OK;
+}
+
+int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t pos0) {
+  const dtl_model* m = s->m;
+  if (T <= 0 || (size_t)T > s->max_chunk || pos0 + (size_t)T > s->n_ctx) return DTL_ERR_SHAPE;
+  for (int t = 0; t < T; t++)
+    if (tokens_host[t] >= (uint32_t)m->emb.rows) return DTL_ERR_SHAPE;
+  hipStream_t st = s->stream;
+  HIP_TRY(hipSetDevice(m->device));
+  s->rows_valid = 0;
+  HIP_TRY(hipMemcpyAsync(s->tokens, tokens_host, T * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+  bool replayed = false;
+  if (T == 1 && graph_eligible(s)) {
+    if (!s->graph) (void)capture_decode_graph(s);
+    if (s->graph) {
+      *s->pos_host = (int)pos0;
+      HIP_TRY(hipMemcpyAsync(s->pos_dev, s->pos_host, sizeof(int), hipMemcpyHostToDevice, st));
+      HIP_TRY(hipGraphLaunch(s->graph, st));
+      replayed = true;
+    }
+  }
+  if (!replayed) {
+    int rc = enqueue_forward(s, T, pos0, nullptr);
+    if (rc) return rc;
+  }
   int bits = 0;
   int rc = read_err(s, &bits);
   if (rc) return rc;
-  P.collect();
+  s->prof.collect();
   if (bits & ERRBIT_NON_FINITE) return DTL_ERR_NON_FINITE;
   s->rows_valid = (size_t)T;
   return DTL_OK;
@@ -963,7 +1017,9 @@ int dtl_session_new(const dtl_model* m, size_t n_ctx, size_t max_chunk, dtl_sess
   ALLOC(c_freq_tab, m->vocab + 256);
   ALLOC(c_cum_tab, m->vocab + 256);
   ALLOC(c_scratch, cdf_scratch_bytes((int)C, (int)m->vocab));
+  ALLOC(pos_dev, 1);
 #undef ALLOC
+  HIP_TRY(hipHostMalloc((void**)&s->pos_host, sizeof(int), hipHostMallocDefault));
   HIP_TRY(hipMemsetAsync(s->kc, 0, kv * 4, s->stream));
   HIP_TRY(hipMemsetAsync(s->vc, 0, kv * 4, s->stream));
   clear_err(s.get());
@@ -983,6 +1039,8 @@ void dtl_session_free(dtl_session* s) {
     (void)hipStreamSynchronize(s->stream);
     (void)hipStreamDestroy(s->stream);
   }
+  if (s->graph) (void)hipGraphExecDestroy(s->graph);
+  if (s->pos_host) (void)hipHostFree(s->pos_host);
   delete s;
 }
 

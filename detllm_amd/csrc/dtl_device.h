@@ -123,13 +123,17 @@ bool launch_gemm_cat_q4k(const DevMat& W0, const DevMat& W1, const DevAct& A, in
 // gate and up (both Q4_K, same shape) in one pass with silu(gate)*up written to ffo.
 void launch_gemm_pair_swiglu_q4k(const DevMat& G, const DevMat& U, const DevAct& A, int T, float* g,
                                  float* u, float* ffo, int* err, hipStream_t s);
+// pos_dev (optional): device int holding pos0, read by the kernels instead of
+// the pos0 argument (lets one captured graph serve every position).
 void launch_rope_store(float* q, float* k, const float* v, const float* rope_cos,
                        const float* rope_sin, int T, int pos0, int H, int KV, int hd, int rope_dim,
-                       int split_half, float* kc, float* vc, int layer, int n_ctx, int* err,
-                       hipStream_t s);
+                       int split_half, float* kc, float* vc, int layer, int n_ctx,
+                       const int* pos_dev, int* err, hipStream_t s);
+// Whether launch_attention accepts pos_dev for this shape.
+bool attention_pos_dev_supported(int hd, int T, int n_ctx);
 void launch_attention(const float* q, const float* kc, const float* vc, int layer, int T, int pos0,
                       int H, int KV, int hd, int n_ctx, float scale, float* scores, float* out,
-                      int* err, hipStream_t s);
+                      const int* pos_dev, int* err, hipStream_t s);
 void launch_swiglu(const float* g, const float* u, int count, float* out, int* err, hipStream_t s);
 void launch_rope_table(float base, int rope_dim, int positions, float* cos_out, float* sin_out,
                        int* err, hipStream_t s);

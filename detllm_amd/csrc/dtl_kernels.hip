@@ -513,9 +513,10 @@ __global__ void __launch_bounds__(256) k_rope_store(float* q, float* k, const fl
                                                     const float* rc, const float* rs, int pos0,
                                                     int H, int KV, int hd, int rope_dim,
                                                     int split_half, float* kc, float* vc,
-                                                    int layer, int n_ctx, int* err) {
+                                                    int layer, int n_ctx, const int* pos_dev,
+                                                    int* err) {
   int t = blockIdx.x;
-  int pos = pos0 + t;
+  int pos = (pos_dev ? *pos_dev : pos0) + t;
   int half = rope_dim / 2;
   bool bad = false;
   float* qt = q + (size_t)t * H * hd;
@@ -555,10 +556,10 @@ __global__ void __launch_bounds__(256) k_rope_store(float* q, float* k, const fl
 
 void launch_rope_store(float* q, float* k, const float* v, const float* rope_cos,
                        const float* rope_sin, int T, int pos0, int H, int KV, int hd, int rope_dim,
-                       int split_half, float* kc, float* vc, int layer, int n_ctx, int* err,
-                       hipStream_t s) {
+                       int split_half, float* kc, float* vc, int layer, int n_ctx,
+                       const int* pos_dev, int* err, hipStream_t s) {
   launch_kernel(k_rope_store, dim3(T), dim3(256), 0, s, q, k, v, rope_cos, rope_sin, pos0, H,
-                     KV, hd, rope_dim, split_half, kc, vc, layer, n_ctx, err);
+                     KV, hd, rope_dim, split_half, kc, vc, layer, n_ctx, pos_dev, err);
 }
 
 // ---------------------------------------------------------------------------
@@ -871,7 +872,7 @@ __global__ void __launch_bounds__(1024) k_attention_hd64(const float* q, const f
 __global__ void __launch_bounds__(256) k_attention_dec(const float* q, const float* kc,
                                                        const float* vc, int layer, int pos0,
                                                        int H, int KV, int n_ctx, float scale,
-                                                       float* out, int* err) {
+                                                       float* out, const int* pos_dev, int* err) {
   extern __shared__ __align__(16) float sc[];  // [len] scores -> exps -> probabilities
   __shared__ __align__(16) float qs[64];
   __shared__ float red[4];
@@ -879,7 +880,7 @@ __global__ void __launch_bounds__(256) k_attention_dec(const float* q, const flo
   constexpr int hd = 64;
   const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
   const int g = h / (H / KV);
-  const int pos = pos0 + t, len = pos + 1;
+  const int pos = (pos_dev ? *pos_dev : pos0) + t, len = pos + 1;
   const float* keys = kc + ((size_t)layer * KV + g) * n_ctx * hd;
   const float* vals = vc + ((size_t)layer * KV + g) * n_ctx * hd;
   float* o = out + (size_t)t * H * hd + (size_t)h * hd;
@@ -966,13 +967,18 @@ size_t attention_grp_smem(int H, int KV, int hd, int n_ctx) {
   return ((size_t)G * n_ctx + (size_t)(kAttnTile + 1) * hd + (size_t)G * hd) * sizeof(float);
 }
 
+bool attention_pos_dev_supported(int hd, int T, int n_ctx) {
+  return hd == 64 && T <= 4 && (size_t)n_ctx * sizeof(float) <= 150 * 1024;
+}
+
 void launch_attention(const float* q, const float* kc, const float* vc, int layer, int T, int pos0,
                       int H, int KV, int hd, int n_ctx, float scale, float* scores, float* out,
-                      int* err, hipStream_t s) {
+                      const int* pos_dev, int* err, hipStream_t s) {
   int G = H / KV;
   if (hd == 64 && T <= 4) {
-    // Decode: one workgroup per (head, position).
-    size_t smem = (size_t)(pos0 + T) * sizeof(float);
+    // Decode: one workgroup per (head, position).  With the position in
+    // device memory the score buffer is sized for the whole window.
+    size_t smem = (size_t)(pos_dev ? n_ctx : pos0 + T) * sizeof(float);
     if (smem <= 150 * 1024) {
       static bool attr_dec_set = false;
       if (!attr_dec_set) {
@@ -981,7 +987,7 @@ void launch_attention(const float* q, const float* kc, const float* vc, int laye
         attr_dec_set = true;
       }
       launch_kernel(k_attention_dec, dim3(H, T), dim3(256), smem, s, q, kc, vc, layer, pos0, H,
-                    KV, n_ctx, scale, out, err);
+                    KV, n_ctx, scale, out, pos_dev, err);
       return;
     }
   }

@@ -86,6 +86,30 @@ def test_packed_chunk_paths_match_oracle(monkeypatch, env):
     _compare_with_oracle(synth.build_model(w, layers=1), synth.tokens(w, 40), 40)
 
 
+@pytest.mark.parametrize("name", ["qwen05", "tinyllama"])
+def test_single_position_graph_replay_matches_oracle(monkeypatch, name):
+    # One-position forwards replay a captured graph (the position reaches the
+    # kernels through device memory); every replay, a reset session and the
+    # eager launches must give the reference bits.
+    from detllm_amd import synth
+
+    w = synth.WORKLOADS[name]
+    data = synth.build_model(w, layers=1)
+    toks = [int(t) for t in synth.tokens(w, 12)]
+    ref = detref.Model(data).logits(toks)
+    m = _model(data)
+    with m.forward_workspace(16, 1) as s:
+        for rep in range(2):
+            for p, tok in enumerate(toks):
+                got = s.forward_one(tok, p)
+                assert np.array_equal(got.view(np.uint32), ref[p].view(np.uint32)), (rep, p)
+            s.reset()
+    monkeypatch.setenv("DETLLM_NO_GRAPH", "1")
+    with m.forward_workspace(16, 1) as s:
+        for p, tok in enumerate(toks[:4]):
+            assert np.array_equal(s.forward_one(tok, p).view(np.uint32), ref[p].view(np.uint32))
+
+
 def test_repeat_runs_are_bitwise_identical():
     from detllm_amd import synth
 
