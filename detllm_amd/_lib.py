@@ -91,7 +91,9 @@ _SIGS = {
     "dtl_session_set_profiling": (C.c_int, [C.c_void_p, C.c_int]),
     "dtl_session_profile": (C.c_int, [C.c_void_p, C.POINTER(KernelStat), sz, C.POINTER(sz)]),
     "dtl_session_profile_only": (C.c_int, [C.c_void_p, C.c_char_p]),
+    "dtl_session_get_info": (C.c_int, [C.c_void_p, C.POINTER(sz), C.POINTER(sz), C.POINTER(sz)]),
     "dtl_symbol_ranges": (C.c_int, [C.c_void_p, sz, sz, u32p, sz, u64p, u32p, u64p]),
+    "dtl_symbol_ranges_rows": (C.c_int, [C.c_void_p, sz, u32p, u32p, sz, u64p, u32p, u64p]),
     "dtl_cdf": (C.c_int, [C.c_void_p, sz, sz, u32p, u64p, u64p]),
     "dtl_decoder_total": (C.c_int, [C.c_void_p, sz, sz, u64p]),
     "dtl_decoder_lookup": (C.c_int, [C.c_void_p, sz, sz, C.c_uint64, u32p, u64p, u32p, u64p]),
@@ -106,6 +108,25 @@ _SIGS = {
     "dtl_range_decode_freq": (C.c_int, [C.c_void_p, C.c_uint64, u64p]),
     "dtl_range_decode_advance": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64]),
     "dtl_range_decoder_free": (None, [C.c_void_p]),
+    "dtl_tokenizer_from_gguf": (C.c_int, [C.c_char_p, sz, vpp]),
+    "dtl_tokenizer_free": (None, [C.c_void_p]),
+    "dtl_tokenizer_vocab_len": (sz, [C.c_void_p]),
+    "dtl_tokenizer_codec_symbols": (C.c_int, [C.c_void_p, u8p, sz, sz, u32p, sz, C.POINTER(sz)]),
+    "dtl_tokenizer_decode_symbol": (C.c_int, [C.c_void_p, C.c_uint32, sz, u8p, sz, C.POINTER(sz)]),
+    "dtl_codec_next_window_start": (sz, [sz, sz, sz, sz]),
+    "dtl_codec_encode": (C.c_int, [C.c_void_p, u32p, sz, sz, C.c_int, u8p, sz, C.POINTER(sz)]),
+    "dtl_codec_decode": (
+        C.c_int,
+        [C.c_void_p, u8p, sz, sz, C.c_int, u8p, sz, sz, u32p, C.POINTER(sz)],
+    ),
+    "dtl_dtlz_header_encode": (C.c_int, [C.c_uint16, u8p, C.c_uint32, C.c_uint32, C.c_uint64, u8p]),
+    "dtl_dtlz_header_decode": (
+        C.c_int,
+        [u8p, sz, u16p, u8p, u32p, u32p, u64p],
+    ),
+    "dtl_compress": (C.c_int, [C.c_void_p, C.c_void_p, u8p, u8p, sz, sz, sz, C.POINTER(u8p), C.POINTER(sz)]),
+    "dtl_decompress": (C.c_int, [C.c_void_p, C.c_void_p, u8p, u8p, sz, sz, C.POINTER(u8p), C.POINTER(sz)]),
+    "dtl_bytes_free": (None, [u8p]),
     "dtl_kernel_exp_f32": (C.c_int, [f32p, f32p, sz]),
     "dtl_kernel_silu_f32": (C.c_int, [f32p, f32p, sz]),
     "dtl_kernel_f16_to_f32": (C.c_int, [u16p, f32p, sz]),

@@ -21,7 +21,16 @@ OUT_DIR = PKG / "_build"
 LIB_NAME = "libdetllm_amd.so"
 ARCH = os.environ.get("DETLLM_AMD_ARCH", "gfx950")
 
-SOURCES = ["dtl_kernels.hip", "dtl_gemm.hip", "dtl_gemv.hip", "dtl_api.hip", "dtl_gguf.cpp", "dtl_range.cpp"]
+SOURCES = [
+    "dtl_kernels.hip",
+    "dtl_gemm.hip",
+    "dtl_gemv.hip",
+    "dtl_api.hip",
+    "dtl_gguf.cpp",
+    "dtl_range.cpp",
+    "dtl_token.cpp",
+    "dtl_codec.cpp",
+]
 
 NUMERIC_FLAGS = [
     "-ffp-contract=off",

@@ -163,9 +163,21 @@ FLAG_BYTE_ESCAPES = 1
 HEADER_LEN = 56
 
 
+class FileError(enum.IntEnum):
+    """det-coder FileError (file.rs:18-26) with the C ABI status values."""
+
+    TooShort = 80
+    BadMagic = 81
+    UnsupportedVersion = 82
+    UnsupportedFlags = 83
+    InvalidContext = 84
+    InvalidOverlap = 85
+
+
 @dataclass(frozen=True)
 class DtlzHeader:
-    """DtlzHeader (file.rs:8-89): 56-byte little-endian container header."""
+    """DtlzHeader (file.rs:8-89): 56-byte little-endian container header,
+    encoded and validated by dtl_dtlz_header_{encode,decode}."""
 
     flags: int
     model_sha256: bytes
@@ -173,28 +185,29 @@ class DtlzHeader:
     overlap: int
     orig_len: int
 
-    def validate(self) -> None:
-        if self.flags & ~FLAG_BYTE_ESCAPES:
-            raise ValueError(f"unsupported DTLZ flags {self.flags:#x}")
-        if self.n_ctx == 0:
-            raise ValueError("invalid DTLZ context")
-        if self.overlap >= self.n_ctx:
-            raise ValueError("invalid DTLZ overlap")
+    def encode_checked(self) -> bytes:
+        sha = (C.c_uint8 * 32).from_buffer_copy(bytes(self.model_sha256).ljust(32, b"\0")[:32])
+        out = (C.c_uint8 * HEADER_LEN)()
+        check(lib.dtl_dtlz_header_encode(self.flags, sha, self.n_ctx, self.overlap, self.orig_len, out),
+              "DtlzHeader::encode_checked")
+        return bytes(out)
 
     def encode(self) -> bytes:
+        """DtlzHeader::encode: the 56 bytes without validation (for writing
+        deliberately malformed files)."""
         return (MAGIC + struct.pack("<HH", VERSION, self.flags) + bytes(self.model_sha256)
                 + struct.pack("<IIQ", self.n_ctx, self.overlap, self.orig_len))
 
+    def validate(self) -> None:
+        self.encode_checked()
+
     @classmethod
     def decode(cls, data: bytes) -> "DtlzHeader":
-        if len(data) < HEADER_LEN:
-            raise ValueError("DTLZ header too short")
-        if data[:4] != MAGIC:
-            raise ValueError("bad DTLZ magic")
-        version, flags = struct.unpack_from("<HH", data, 4)
-        if version != VERSION:
-            raise ValueError(f"unsupported DTLZ version {version}")
-        n_ctx, overlap, orig_len = struct.unpack_from("<IIQ", data, 40)
-        h = cls(flags, bytes(data[8:40]), n_ctx, overlap, orig_len)
-        h.validate()
-        return h
+        buf = (C.c_uint8 * max(len(data), 1)).from_buffer_copy(bytes(data) or b"\0")
+        flags, n_ctx, overlap = C.c_uint16(), C.c_uint32(), C.c_uint32()
+        orig_len = C.c_uint64()
+        sha = (C.c_uint8 * 32)()
+        check(lib.dtl_dtlz_header_decode(buf, len(data), C.byref(flags), sha, C.byref(n_ctx),
+                                         C.byref(overlap), C.byref(orig_len)), "DtlzHeader::decode")
+        return cls(int(flags.value), bytes(sha), int(n_ctx.value), int(overlap.value),
+                   int(orig_len.value))

@@ -631,6 +631,9 @@ struct dtl_session {
   uint32_t *c_sym = nullptr, *c_freq = nullptr, *c_freq_tab = nullptr;
   uint64_t *c_cum = nullptr, *c_total = nullptr, *c_values = nullptr, *c_cum_tab = nullptr;
   uint8_t* c_scratch = nullptr;  // multi-workgroup CDF scratch for max_chunk rows
+  uint32_t* c_rows = nullptr;    // row index per symbol (dtl_symbol_ranges_rows)
+  // Row / tail whose decoder-total block results the scratch still holds.
+  size_t cdf_ready_row = SIZE_MAX, cdf_ready_tail = SIZE_MAX;
   // Captured single-position forward (see forward_device).
   hipGraphExec_t graph = nullptr;
   bool graph_failed = false;
@@ -826,6 +829,7 @@ int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t po
   hipStream_t st = s->stream;
   HIP_TRY(hipSetDevice(m->device));
   s->rows_valid = 0;
+  s->cdf_ready_row = SIZE_MAX;
   HIP_TRY(hipMemcpyAsync(s->tokens, tokens_host, T * sizeof(uint32_t), hipMemcpyHostToDevice, st));
   bool replayed = false;
   if (T == 1 && graph_eligible(s)) {
@@ -888,6 +892,35 @@ const char* dtl_status_string(int status) {
     case DTL_ERR_OUT_OF_MEMORY: return "device out of memory";
     case DTL_ERR_INVALID_ARGUMENT: return "invalid argument";
     case DTL_ERR_NO_DEVICE: return "no HIP device";
+    case DTL_ERR_BUFFER_TOO_SMALL: return "output buffer too small";
+    case DTL_ERR_TOKEN_MISSING_BYTE_FALLBACK: return "token: missing byte fallback";
+    case DTL_ERR_TOKEN_INVALID_TOKEN: return "token: invalid token";
+    case DTL_ERR_TOKEN_MISSING_VOCABULARY: return "token: missing vocabulary";
+    case DTL_ERR_TOKEN_MISSING_TOKEN_BYTES: return "token: missing token bytes";
+    case DTL_ERR_TOKEN_MISSING_MERGE_TOKEN: return "token: missing merge token";
+    case DTL_ERR_TOKEN_INCOMPLETE_BYTE_FALLBACK: return "token: incomplete byte fallback";
+    case DTL_ERR_TOKEN_METADATA_TYPE: return "token: metadata type";
+    case DTL_ERR_TOKEN_TYPE_LENGTH: return "token: token type length";
+    case DTL_ERR_TOKEN_INVALID_TOKEN_TYPE: return "token: invalid token type";
+    case DTL_ERR_TOKEN_SCORES_LENGTH: return "token: scores length";
+    case DTL_ERR_TOKEN_NON_FINITE_SCORE: return "token: non-finite score";
+    case DTL_ERR_TOKEN_INDEX_OVERFLOW: return "token: index overflow";
+    case DTL_ERR_TOKEN_DUPLICATE_BYTE_FALLBACK: return "token: duplicate byte fallback";
+    case DTL_ERR_TOKEN_DUPLICATE_TOKEN_ID: return "token: duplicate token id";
+    case DTL_ERR_TOKEN_DUPLICATE_TOKEN_BYTES: return "token: duplicate token bytes";
+    case DTL_ERR_TOKEN_INVALID_MERGE: return "token: invalid merge";
+    case DTL_ERR_TOKEN_DUPLICATE_MERGE: return "token: duplicate merge";
+    case DTL_ERR_TOKEN_UNSUPPORTED_MODEL: return "token: unsupported tokenizer model";
+    case DTL_ERR_FILE_TOO_SHORT: return "dtlz: too short";
+    case DTL_ERR_FILE_BAD_MAGIC: return "dtlz: bad magic";
+    case DTL_ERR_FILE_UNSUPPORTED_VERSION: return "dtlz: unsupported version";
+    case DTL_ERR_FILE_UNSUPPORTED_FLAGS: return "dtlz: unsupported flags";
+    case DTL_ERR_FILE_INVALID_CONTEXT: return "dtlz: invalid context";
+    case DTL_ERR_FILE_INVALID_OVERLAP: return "dtlz: invalid overlap";
+    case DTL_ERR_CODEC_MODEL_MISMATCH: return "codec: model SHA-256 does not match the header";
+    case DTL_ERR_CODEC_NOT_CANONICAL: return "codec: payload is not the canonical encoding";
+    case DTL_ERR_CODEC_ESCAPE_IN_TOKEN_STREAM: return "codec: byte escape in a token-only stream";
+    case DTL_ERR_CODEC_VOCAB_MISMATCH: return "codec: tokenizer vocabulary does not match the model";
     default: return "unknown status";
   }
 }
@@ -1018,6 +1051,7 @@ int dtl_session_new(const dtl_model* m, size_t n_ctx, size_t max_chunk, dtl_sess
   ALLOC(c_cum_tab, m->vocab + 256);
   ALLOC(c_scratch, cdf_scratch_bytes((int)C, (int)m->vocab));
   ALLOC(pos_dev, 1);
+  ALLOC(c_rows, C);
 #undef ALLOC
   HIP_TRY(hipHostMalloc((void**)&s->pos_host, sizeof(int), hipHostMallocDefault));
   HIP_TRY(hipMemsetAsync(s->kc, 0, kv * 4, s->stream));
@@ -1117,10 +1151,12 @@ int dtl_symbol_ranges(dtl_session* s, size_t first, size_t n, const uint32_t* sy
     if (symbols[i] >= V + tail) return DTL_ERR_CDF_SYMBOL_OUT_OF_RANGE;
   HIP_TRY(hipSetDevice(s->m->device));
   clear_err(s);
+  s->cdf_ready_row = SIZE_MAX;
   HIP_TRY(hipMemcpyAsync(s->c_sym, symbols, n * 4, hipMemcpyHostToDevice, s->stream));
   s->prof.timed(s->stream, "cdf_symbol_range", (double)n * V * 4.0, 0.0, [&] {
-    launch_cdf_blocks(s->logits + first * V, (int)n, (int)V, (int)tail, 0, s->c_sym, nullptr,
-                      s->c_cum, s->c_freq, s->c_total, nullptr, s->c_scratch, s->err, s->stream);
+    launch_cdf_blocks(s->logits + first * V, nullptr, (int)n, (int)V, (int)tail, 0, s->c_sym,
+                      nullptr, s->c_cum, s->c_freq, s->c_total, nullptr, s->c_scratch, false,
+                      s->err, s->stream);
   });
   HIP_TRY(hipMemcpyAsync(cum, s->c_cum, n * 8, hipMemcpyDeviceToHost, s->stream));
   HIP_TRY(hipMemcpyAsync(freq, s->c_freq, n * 4, hipMemcpyDeviceToHost, s->stream));
@@ -1128,6 +1164,49 @@ int dtl_symbol_ranges(dtl_session* s, size_t first, size_t n, const uint32_t* sy
   int bits = 0, st = read_err(s, &bits);
   s->prof.collect();
   return st ? st : cdf_status(bits);
+}
+
+int dtl_symbol_ranges_rows(dtl_session* s, size_t n, const uint32_t* rows, const uint32_t* symbols,
+                           size_t tail, uint64_t* cum, uint32_t* freq, uint64_t* total) {
+  if (!s || !rows || !symbols || !cum || !freq || !total) return DTL_ERR_INVALID_ARGUMENT;
+  size_t V = s->m->vocab;
+  if (n == 0) return DTL_ERR_SHAPE;
+  if (V + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
+  for (size_t i = 0; i < n; i++) {
+    if (rows[i] >= s->rows_valid) return DTL_ERR_SHAPE;
+    if (symbols[i] >= V + tail) return DTL_ERR_CDF_SYMBOL_OUT_OF_RANGE;
+  }
+  HIP_TRY(hipSetDevice(s->m->device));
+  s->cdf_ready_row = SIZE_MAX;
+  // batches of at most max_chunk symbols (the size of the staging buffers
+  // and of the CDF scratch)
+  for (size_t b0 = 0; b0 < n; b0 += s->max_chunk) {
+    const size_t m = std::min(s->max_chunk, n - b0);
+    clear_err(s);
+    HIP_TRY(hipMemcpyAsync(s->c_sym, symbols + b0, m * 4, hipMemcpyHostToDevice, s->stream));
+    HIP_TRY(hipMemcpyAsync(s->c_rows, rows + b0, m * 4, hipMemcpyHostToDevice, s->stream));
+    s->prof.timed(s->stream, "cdf_symbol_range", (double)m * V * 4.0, 0.0, [&] {
+      launch_cdf_blocks(s->logits, s->c_rows, (int)m, (int)V, (int)tail, 0, s->c_sym, nullptr,
+                        s->c_cum, s->c_freq, s->c_total, nullptr, s->c_scratch, false, s->err,
+                        s->stream);
+    });
+    HIP_TRY(hipMemcpyAsync(cum + b0, s->c_cum, m * 8, hipMemcpyDeviceToHost, s->stream));
+    HIP_TRY(hipMemcpyAsync(freq + b0, s->c_freq, m * 4, hipMemcpyDeviceToHost, s->stream));
+    HIP_TRY(hipMemcpyAsync(total + b0, s->c_total, m * 8, hipMemcpyDeviceToHost, s->stream));
+    int bits = 0, st = read_err(s, &bits);
+    s->prof.collect();
+    if (st) return st;
+    if ((st = cdf_status(bits))) return st;
+  }
+  return DTL_OK;
+}
+
+int dtl_session_get_info(const dtl_session* s, size_t* n_ctx, size_t* max_chunk, size_t* vocab) {
+  if (!s) return DTL_ERR_INVALID_ARGUMENT;
+  if (n_ctx) *n_ctx = s->n_ctx;
+  if (max_chunk) *max_chunk = s->max_chunk;
+  if (vocab) *vocab = s->m->vocab;
+  return DTL_OK;
 }
 
 int dtl_session_set_profiling(dtl_session* s, int enable) {
@@ -1177,11 +1256,18 @@ int dtl_decoder_total(dtl_session* s, size_t row, size_t tail, uint64_t* total) 
   if (V + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
   HIP_TRY(hipSetDevice(s->m->device));
   clear_err(s);
-  launch_cdf_blocks(s->logits + row * V, 1, (int)V, (int)tail, 3, nullptr, nullptr, nullptr,
-                    nullptr, s->c_total, nullptr, s->c_scratch, s->err, s->stream);
+  launch_cdf_blocks(s->logits + row * V, nullptr, 1, (int)V, (int)tail, 3, nullptr, nullptr,
+                    nullptr, nullptr, s->c_total, nullptr, s->c_scratch, false, s->err, s->stream);
   HIP_TRY(hipMemcpyAsync(total, s->c_total, 8, hipMemcpyDeviceToHost, s->stream));
   int bits = 0, st = read_err(s, &bits);
-  return st ? st : cdf_status(bits);
+  if (st) return st;
+  st = cdf_status(bits);
+  if (st == DTL_OK) {
+    // The block results of this row stay in the scratch for a lookup.
+    s->cdf_ready_row = row;
+    s->cdf_ready_tail = tail;
+  }
+  return st;
 }
 
 int dtl_decoder_lookup(dtl_session* s, size_t row, size_t tail, uint64_t value, uint32_t* symbol,
@@ -1193,8 +1279,10 @@ int dtl_decoder_lookup(dtl_session* s, size_t row, size_t tail, uint64_t value, 
   HIP_TRY(hipSetDevice(s->m->device));
   clear_err(s);
   HIP_TRY(hipMemcpyAsync(s->c_values, &value, 8, hipMemcpyHostToDevice, s->stream));
-  launch_cdf_blocks(s->logits + row * V, 1, (int)V, (int)tail, 2, nullptr, s->c_values,
-                    s->c_cum, s->c_freq, s->c_total, s->c_sym, s->c_scratch, s->err, s->stream);
+  const bool reuse = s->cdf_ready_row == row && s->cdf_ready_tail == tail;
+  launch_cdf_blocks(s->logits + row * V, nullptr, 1, (int)V, (int)tail, 2, nullptr, s->c_values,
+                    s->c_cum, s->c_freq, s->c_total, s->c_sym, s->c_scratch, reuse, s->err,
+                    s->stream);
   HIP_TRY(hipMemcpyAsync(symbol, s->c_sym, 4, hipMemcpyDeviceToHost, s->stream));
   HIP_TRY(hipMemcpyAsync(cum, s->c_cum, 8, hipMemcpyDeviceToHost, s->stream));
   HIP_TRY(hipMemcpyAsync(freq, s->c_freq, 4, hipMemcpyDeviceToHost, s->stream));
@@ -1265,8 +1353,8 @@ int run_cdf_host(const float* logits, size_t n, size_t tail, int mode, uint32_t 
   } else {
     uint8_t* scratch;
     if ((st = sc.arena.alloc(&scratch, cdf_scratch_bytes(1, (int)n)))) return st;
-    launch_cdf_blocks(dl, 1, (int)n, (int)tail, mode, dsym, nullptr, dcum, dfreq, dtot, nullptr,
-                      scratch, sc.err, sc.stream);
+    launch_cdf_blocks(dl, nullptr, 1, (int)n, (int)tail, mode, dsym, nullptr, dcum, dfreq, dtot,
+                      nullptr, scratch, false, sc.err, sc.stream);
   }
   if (mode == 1) {
     HIP_TRY(hipMemcpyAsync(freq_tab, dft, (n + tail) * 4, hipMemcpyDeviceToHost, sc.stream));

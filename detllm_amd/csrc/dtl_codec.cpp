@@ -1,0 +1,442 @@
+// Windowed model codec and the DTLZ file (crates/det-cli/src/main.rs:431-808
+// and crates/det-coder/src/file.rs of mii443/detllm), on top of this
+// library's session, CDF and range-coder entry points.
+//
+// The reference advances the model one token at a time.  Encoding knows
+// every token in advance, so here each window's forwards run as chunks of
+// positions on the device and the symbol ranges of all symbols coded against
+// a chunk's rows are computed in one call; the (cum, freq, total) triplets
+// are then range-coded in symbol order.  Decoding is sequential as in the
+// reference: one forward per decoded token.
+#include <algorithm>
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "../../include/detllm.h"
+
+namespace {
+
+constexpr size_t kEscapes = 256;  // BYTE_ESCAPE_SYMBOLS
+
+struct Info {
+  size_t n_ctx, max_chunk, vocab;
+};
+
+int session_info(dtl_session* s, Info* in) {
+  return dtl_session_get_info(s, &in->n_ctx, &in->max_chunk, &in->vocab);
+}
+
+// validate_window (main.rs:810-825) against the session's window.
+int validate_window(size_t n_ctx, size_t overlap) {
+  if (n_ctx == 0) return DTL_ERR_FILE_INVALID_CONTEXT;
+  if (overlap >= n_ctx) return DTL_ERR_FILE_INVALID_OVERLAP;
+  return DTL_OK;
+}
+
+
+struct Range3 {
+  uint64_t cum, total;
+  uint32_t freq;
+};
+
+// encode_symbols_with_model (main.rs:521-551).
+int encode_payload(dtl_session* s, const uint32_t* symbols, size_t n, size_t overlap,
+                   int byte_escapes, std::vector<uint8_t>* payload) {
+  Info in;
+  int st = session_info(s, &in);
+  if (st) return st;
+  if ((st = validate_window(in.n_ctx, overlap))) return st;
+  const size_t V = in.vocab, tail = byte_escapes ? kEscapes : 0;
+  // Plan: the window each symbol falls in and the window position of the
+  // forward whose logits code it (SIZE_MAX: uniform, the window is empty).
+  struct Window {
+    size_t start;                // first context token of the window
+    std::vector<uint32_t> toks;  // the window's forwards, in order
+  };
+  std::vector<Window> windows;
+  std::vector<size_t> sym_window(n), sym_row(n);
+  std::vector<uint32_t> context;
+  size_t window_start = 0;
+  windows.push_back({0, {}});
+  for (size_t k = 0; k < n; k++) {
+    const uint32_t sym = symbols[k];
+    if (sym >= V + tail) return DTL_ERR_CDF_SYMBOL_OUT_OF_RANGE;
+    const size_t pos = context.size();
+    const size_t next = dtl_codec_next_window_start(pos, window_start, in.n_ctx, overlap);
+    if (next != window_start) {
+      window_start = next;
+      windows.push_back({next, std::vector<uint32_t>(context.begin() + next, context.end())});
+    }
+    Window& w = windows.back();
+    sym_window[k] = windows.size() - 1;
+    sym_row[k] = w.toks.empty() ? SIZE_MAX : w.toks.size() - 1;
+    if (sym < V) {
+      context.push_back(sym);
+      w.toks.push_back(sym);
+    }
+  }
+  // Device work: each window from a fresh cache, forwards in chunks of up to
+  // max_chunk positions; the symbols coded against a chunk's rows get their
+  // ranges from one call.
+  std::vector<Range3> ranges(n);
+  std::vector<size_t> by_window_start(windows.size() + 1, 0);
+  {
+    // symbols are ordered by window already: find each window's first symbol
+    size_t k = 0;
+    for (size_t w = 0; w < windows.size(); w++) {
+      by_window_start[w] = k;
+      while (k < n && sym_window[k] == w) k++;
+    }
+    by_window_start[windows.size()] = n;
+  }
+  std::vector<uint32_t> rows, syms;
+  std::vector<uint64_t> cum, total;
+  std::vector<uint32_t> freq;
+  for (size_t w = 0; w < windows.size(); w++) {
+    const Window& win = windows[w];
+    const size_t k0 = by_window_start[w], k1 = by_window_start[w + 1];
+    // uniform symbols (empty window)
+    for (size_t k = k0; k < k1; k++) {
+      if (sym_row[k] != SIZE_MAX) continue;
+      uint64_t c, t;
+      uint32_t f;
+      if ((st = dtl_uniform_symbol_range(symbols[k], V + tail, &c, &f, &t))) return st;
+      ranges[k] = {c, t, f};
+    }
+    if (win.toks.empty()) continue;
+    if ((st = dtl_session_reset(s))) return st;
+    size_t k = k0;
+    for (size_t p0 = 0; p0 < win.toks.size(); p0 += in.max_chunk) {
+      const size_t T = std::min(in.max_chunk, win.toks.size() - p0);
+      if ((st = dtl_forward_chunk(s, win.toks.data() + p0, T, p0, nullptr))) return st;
+      rows.clear();
+      syms.clear();
+      const size_t kfirst = k;
+      for (; k < k1; k++) {
+        if (sym_row[k] == SIZE_MAX) continue;
+        if (sym_row[k] >= p0 + T) break;
+        rows.push_back((uint32_t)(sym_row[k] - p0));
+        syms.push_back(symbols[k]);
+      }
+      if (rows.empty()) continue;
+      cum.resize(rows.size());
+      freq.resize(rows.size());
+      total.resize(rows.size());
+      if ((st = dtl_symbol_ranges_rows(s, rows.size(), rows.data(), syms.data(), tail, cum.data(),
+                                       freq.data(), total.data())))
+        return st;
+      size_t j = 0;
+      for (size_t q = kfirst; q < k; q++) {
+        if (sym_row[q] == SIZE_MAX) continue;
+        ranges[q] = {cum[j], total[j], freq[j]};
+        j++;
+      }
+    }
+  }
+  dtl_range_encoder* enc = nullptr;
+  if ((st = dtl_range_encoder_new(&enc))) return st;
+  for (size_t k = 0; k < n && st == DTL_OK; k++)
+    st = dtl_range_encode(enc, ranges[k].cum, ranges[k].freq, ranges[k].total);
+  size_t len = 0;
+  if (st == DTL_OK) st = dtl_range_encoder_finish(enc, nullptr, 0, &len);
+  if (st == DTL_OK) {
+    payload->resize(len);
+    st = dtl_range_encoder_finish(enc, payload->data(), len, &len);
+  }
+  dtl_range_encoder_free(enc);
+  return st;
+}
+
+// decode_bytes_with_model (main.rs:573-632) over WindowedModelState
+// (main.rs:634-799), symbols appended to *out.
+int decode_symbols(dtl_session* s, const uint8_t* payload, size_t plen, size_t overlap,
+                   int byte_escapes, const uint8_t* piece_len, size_t byte_len, size_t max_symbols,
+                   std::vector<uint32_t>* out) {
+  Info in;
+  int st = session_info(s, &in);
+  if (st) return st;
+  if ((st = validate_window(in.n_ctx, overlap))) return st;
+  const size_t V = in.vocab, tail = byte_escapes ? kEscapes : 0;
+  dtl_range_decoder* dec = nullptr;
+  if ((st = dtl_range_decoder_new(payload, plen, &dec))) return st;
+  std::vector<uint32_t> context;
+  size_t window_start = 0, context_len = 0, last_row = 0, bytes = 0;
+  if ((st = dtl_session_reset(s))) goto done;
+  while (out->size() < max_symbols && (piece_len ? bytes < byte_len : true)) {
+    const size_t pos = context.size();
+    const size_t next = dtl_codec_next_window_start(pos, window_start, in.n_ctx, overlap);
+    if (next != window_start) {
+      // replay (main.rs:690-701): fresh cache, the window's tokens re-forwarded
+      window_start = next;
+      context_len = 0;
+      if ((st = dtl_session_reset(s))) goto done;
+      for (size_t p0 = next; p0 < pos; p0 += in.max_chunk) {
+        const size_t T = std::min(in.max_chunk, pos - p0);
+        if ((st = dtl_forward_chunk(s, context.data() + p0, T, p0 - next, nullptr))) goto done;
+        context_len += T;
+        last_row = T - 1;
+      }
+    }
+    uint32_t sym;
+    uint64_t value;
+    if (context_len == 0) {
+      // uniform_cdf[_with_byte_escapes]: symbol v covers [v, v + 1)
+      const uint64_t total = V + tail;
+      if ((st = dtl_range_decode_freq(dec, total, &value))) goto done;
+      sym = (uint32_t)value;
+      if ((st = dtl_range_decode_advance(dec, value, 1, total))) goto done;
+    } else {
+      uint64_t total, cum;
+      uint32_t freq;
+      if ((st = dtl_decoder_total(s, last_row, tail, &total))) goto done;
+      if ((st = dtl_range_decode_freq(dec, total, &value))) goto done;
+      if ((st = dtl_decoder_lookup(s, last_row, tail, value, &sym, &cum, &freq, &total))) goto done;
+      if ((st = dtl_range_decode_advance(dec, cum, freq, total))) goto done;
+    }
+    if (!byte_escapes && sym >= V) {
+      st = DTL_ERR_CODEC_ESCAPE_IN_TOKEN_STREAM;
+      goto done;
+    }
+    if (piece_len) {
+      if (piece_len[sym] == 0) {  // "decoded symbol produced no bytes"
+        st = DTL_ERR_TOKEN_INVALID_TOKEN;
+        goto done;
+      }
+      bytes += piece_len[sym];
+    }
+    out->push_back(sym);
+    if (sym < V) {
+      if (context_len >= in.n_ctx) {  // "context window invariant violated"
+        st = DTL_ERR_SHAPE;
+        goto done;
+      }
+      if ((st = dtl_forward_one(s, sym, context_len, nullptr))) goto done;
+      context.push_back(sym);
+      context_len++;
+      last_row = 0;
+    }
+  }
+done:
+  dtl_range_decoder_free(dec);
+  return st;
+}
+
+}  // namespace
+
+extern "C" {
+
+// next_window_start (main.rs:801-808): a new window starts overlap tokens
+// back once the current one holds n_ctx tokens.
+size_t dtl_codec_next_window_start(size_t pos, size_t window_start, size_t n_ctx, size_t overlap) {
+  return pos - std::min(pos, window_start) >= n_ctx ? pos - std::min(pos, overlap) : window_start;
+}
+
+int dtl_codec_encode(dtl_session* s, const uint32_t* symbols, size_t n, size_t overlap,
+                     int byte_escapes, uint8_t* out, size_t cap, size_t* len) {
+  if (!s || (!symbols && n) || !len) return DTL_ERR_INVALID_ARGUMENT;
+  try {
+    std::vector<uint8_t> payload;
+    const int st = encode_payload(s, symbols, n, overlap, byte_escapes, &payload);
+    if (st) return st;
+    *len = payload.size();
+    if (!out) return DTL_OK;
+    if (cap < payload.size()) return DTL_ERR_BUFFER_TOO_SMALL;
+    if (!payload.empty()) std::memcpy(out, payload.data(), payload.size());
+    return DTL_OK;
+  } catch (const std::bad_alloc&) {
+    return DTL_ERR_OUT_OF_MEMORY;
+  }
+}
+
+// decode_bytes_with_model / decode_tokens_with_model (main.rs:553-632) and
+// WindowedModelState (main.rs:634-799): one forward per decoded token.
+// Stops after max_symbols symbols, or once piece_len (when given) sums to
+// byte_len.
+int dtl_codec_decode(dtl_session* s, const uint8_t* payload, size_t plen, size_t overlap,
+                     int byte_escapes, const uint8_t* piece_len, size_t byte_len,
+                     size_t max_symbols, uint32_t* symbols, size_t* n_out) {
+  if (!s || (!payload && plen) || (!symbols && max_symbols) || !n_out)
+    return DTL_ERR_INVALID_ARGUMENT;
+  *n_out = 0;
+  try {
+    std::vector<uint32_t> out;
+    out.reserve(std::min<size_t>(max_symbols, 1 << 16));
+    const int st = decode_symbols(s, payload, plen, overlap, byte_escapes, piece_len, byte_len,
+                                  max_symbols, &out);
+    if (!out.empty()) std::memcpy(symbols, out.data(), out.size() * 4);
+    *n_out = out.size();
+    return st;
+  } catch (const std::bad_alloc&) {
+    return DTL_ERR_OUT_OF_MEMORY;
+  }
+}
+
+// DtlzHeader::{encode, decode, validate} (det-coder file.rs:1-89).
+int dtl_dtlz_header_encode(uint16_t flags, const uint8_t model_sha256[32], uint32_t n_ctx,
+                           uint32_t overlap, uint64_t orig_len, uint8_t out[56]) {
+  if (!model_sha256 || !out) return DTL_ERR_INVALID_ARGUMENT;
+  if (flags & ~(uint16_t)DTL_DTLZ_FLAG_BYTE_ESCAPES) return DTL_ERR_FILE_UNSUPPORTED_FLAGS;
+  if (n_ctx == 0) return DTL_ERR_FILE_INVALID_CONTEXT;
+  if (overlap >= n_ctx) return DTL_ERR_FILE_INVALID_OVERLAP;
+  const uint16_t version = 1;
+  std::memcpy(out, "DTLZ", 4);
+  std::memcpy(out + 4, &version, 2);
+  std::memcpy(out + 6, &flags, 2);
+  std::memcpy(out + 8, model_sha256, 32);
+  std::memcpy(out + 40, &n_ctx, 4);
+  std::memcpy(out + 44, &overlap, 4);
+  std::memcpy(out + 48, &orig_len, 8);
+  return DTL_OK;
+}
+
+int dtl_dtlz_header_decode(const uint8_t* bytes, size_t len, uint16_t* flags,
+                           uint8_t model_sha256[32], uint32_t* n_ctx, uint32_t* overlap,
+                           uint64_t* orig_len) {
+  if (!bytes && len) return DTL_ERR_INVALID_ARGUMENT;
+  if (len < 56) return DTL_ERR_FILE_TOO_SHORT;
+  if (std::memcmp(bytes, "DTLZ", 4) != 0) return DTL_ERR_FILE_BAD_MAGIC;
+  uint16_t version, f;
+  std::memcpy(&version, bytes + 4, 2);
+  if (version != 1) return DTL_ERR_FILE_UNSUPPORTED_VERSION;
+  std::memcpy(&f, bytes + 6, 2);
+  if (f & ~(uint16_t)DTL_DTLZ_FLAG_BYTE_ESCAPES) return DTL_ERR_FILE_UNSUPPORTED_FLAGS;
+  uint32_t nc, ov;
+  uint64_t ol;
+  std::memcpy(&nc, bytes + 40, 4);
+  std::memcpy(&ov, bytes + 44, 4);
+  std::memcpy(&ol, bytes + 48, 8);
+  if (nc == 0) return DTL_ERR_FILE_INVALID_CONTEXT;
+  if (ov >= nc) return DTL_ERR_FILE_INVALID_OVERLAP;
+  if (flags) *flags = f;
+  if (model_sha256) std::memcpy(model_sha256, bytes + 8, 32);
+  if (n_ctx) *n_ctx = nc;
+  if (overlap) *overlap = ov;
+  if (orig_len) *orig_len = ol;
+  return DTL_OK;
+}
+
+// Library-owned result buffer of dtl_compress / dtl_decompress.
+static int hand_out(const std::vector<uint8_t>& v, uint8_t** out, size_t* len) {
+  uint8_t* p = static_cast<uint8_t*>(std::malloc(v.empty() ? 1 : v.size()));
+  if (!p) return DTL_ERR_OUT_OF_MEMORY;
+  if (!v.empty()) std::memcpy(p, v.data(), v.size());
+  *out = p;
+  *len = v.size();
+  return DTL_OK;
+}
+
+void dtl_bytes_free(uint8_t* p) { std::free(p); }
+
+// LoadedModel::load checks (main.rs:932-1000): the tokenizer's vocabulary is
+// the model's, and vocab + 256 escapes fit the CDF symbol limit.
+static int check_codec_model(const dtl_model_config& cfg, const dtl_tokenizer* tok) {
+  if (dtl_tokenizer_vocab_len(tok) != cfg.vocab) return DTL_ERR_CODEC_VOCAB_MISMATCH;
+  if (cfg.vocab + kEscapes > (1u << 18)) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
+  return DTL_OK;
+}
+
+// compress (main.rs:431-462): byte-fallback codec symbols, window n_ctx,
+// overlap n_ctx / 4, byte escapes on; header + payload.
+int dtl_compress(const dtl_model* model, const dtl_tokenizer* tok, const uint8_t model_sha256[32],
+                 const uint8_t* input, size_t n, size_t n_ctx, size_t max_chunk, uint8_t** out,
+                 size_t* len) {
+  if (!model || !tok || !model_sha256 || (!input && n) || !out || !len)
+    return DTL_ERR_INVALID_ARGUMENT;
+  *out = nullptr;
+  *len = 0;
+  try {
+    dtl_model_config cfg;
+    int st = dtl_model_get_config(model, &cfg);
+    if (st) return st;
+    if ((st = check_codec_model(cfg, tok))) return st;
+    if (n_ctx == 0) n_ctx = cfg.context_length;
+    // validate_window (main.rs:810-825) with overlap n_ctx / 4
+    if (n_ctx == 0 || n_ctx > cfg.context_length || n_ctx > 0xffffffffull)
+      return DTL_ERR_FILE_INVALID_CONTEXT;
+    const size_t overlap = n_ctx / 4;
+    std::vector<uint32_t> symbols(n);
+    size_t ns = 0;
+    if ((st = dtl_tokenizer_codec_symbols(tok, input, n, cfg.vocab, symbols.data(), n, &ns)))
+      return st;
+    dtl_session* s = nullptr;
+    if ((st = dtl_session_new(model, n_ctx, max_chunk ? max_chunk : 64, &s))) return st;
+    std::vector<uint8_t> file(DTL_DTLZ_HEADER_LEN);
+    std::vector<uint8_t> payload;
+    st = encode_payload(s, symbols.data(), ns, overlap, 1, &payload);
+    dtl_session_free(s);
+    if (st) return st;
+    if ((st = dtl_dtlz_header_encode(DTL_DTLZ_FLAG_BYTE_ESCAPES, model_sha256, (uint32_t)n_ctx,
+                                     (uint32_t)overlap, (uint64_t)n, file.data())))
+      return st;
+    file.insert(file.end(), payload.begin(), payload.end());
+    return hand_out(file, out, len);
+  } catch (const std::bad_alloc&) {
+    return DTL_ERR_OUT_OF_MEMORY;
+  }
+}
+
+// decompress (main.rs:464-512): header first (before any model work), model
+// hash check, window check, decode to the original length, then the
+// canonical re-encode check.
+int dtl_decompress(const dtl_model* model, const dtl_tokenizer* tok,
+                   const uint8_t model_sha256[32], const uint8_t* file, size_t len,
+                   size_t max_chunk, uint8_t** out, size_t* out_len) {
+  if ((!file && len) || !out || !out_len) return DTL_ERR_INVALID_ARGUMENT;
+  *out = nullptr;
+  *out_len = 0;
+  uint16_t flags;
+  uint8_t sha[32];
+  uint32_t n_ctx, overlap;
+  uint64_t orig_len;
+  int st = dtl_dtlz_header_decode(file, len, &flags, sha, &n_ctx, &overlap, &orig_len);
+  if (st) return st;
+  if (!model || !tok || !model_sha256) return DTL_ERR_INVALID_ARGUMENT;
+  try {
+    dtl_model_config cfg;
+    if ((st = dtl_model_get_config(model, &cfg))) return st;
+    if ((st = check_codec_model(cfg, tok))) return st;
+    if (std::memcmp(sha, model_sha256, 32) != 0) return DTL_ERR_CODEC_MODEL_MISMATCH;
+    if (n_ctx > cfg.context_length) return DTL_ERR_FILE_INVALID_CONTEXT;
+    const int escapes = (flags & DTL_DTLZ_FLAG_BYTE_ESCAPES) ? 1 : 0;
+    const size_t V = cfg.vocab;
+    // bytes of each symbol (0: decodes to nothing) and, for the byte-fallback
+    // kind, the one byte itself
+    std::vector<uint8_t> piece(V + kEscapes, 0), one(V + kEscapes, 0);
+    for (size_t sym = 0; sym < V + kEscapes; sym++) {
+      size_t nb = 0;
+      uint8_t b;
+      if (dtl_tokenizer_decode_symbol(tok, (uint32_t)sym, V, &b, 1, &nb) == DTL_OK && nb == 1) {
+        piece[sym] = 1;
+        one[sym] = b;
+      }
+    }
+    dtl_session* s = nullptr;
+    if ((st = dtl_session_new(model, n_ctx, max_chunk ? max_chunk : 64, &s))) return st;
+    std::vector<uint32_t> symbols;
+    symbols.reserve((size_t)std::min<uint64_t>(orig_len, 8192));
+    // orig_len beyond what the payload codes ends in a range-coder error
+    // (UnexpectedEof), as in the reference
+    st = decode_symbols(s, file + DTL_DTLZ_HEADER_LEN, len - DTL_DTLZ_HEADER_LEN, overlap, escapes,
+                        piece.data(), orig_len > SIZE_MAX ? SIZE_MAX : (size_t)orig_len, SIZE_MAX,
+                        &symbols);
+    std::vector<uint8_t> again;
+    if (st == DTL_OK) st = encode_payload(s, symbols.data(), symbols.size(), overlap, escapes, &again);
+    dtl_session_free(s);
+    if (st) return st;
+    if (again.size() != len - DTL_DTLZ_HEADER_LEN ||
+        std::memcmp(again.data(), file + DTL_DTLZ_HEADER_LEN, again.size()) != 0)
+      return DTL_ERR_CODEC_NOT_CANONICAL;
+    std::vector<uint8_t> bytes;
+    bytes.reserve(symbols.size());
+    for (uint32_t sym : symbols) bytes.push_back(one[sym]);
+    bytes.resize((size_t)orig_len);
+    return hand_out(bytes, out, out_len);
+  } catch (const std::bad_alloc&) {
+    return DTL_ERR_OUT_OF_MEMORY;
+  }
+}
+
+}  // extern "C"

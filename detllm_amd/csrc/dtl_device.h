@@ -148,12 +148,15 @@ void launch_cdf(const float* logits, int R, int V, int tail, int mode, const uin
                 uint32_t* sym, uint32_t* freq_tab, uint64_t* cum_tab, int* err, hipStream_t s);
 
 // Modes 0, 2 and 3 of launch_cdf spread over many workgroups per row;
-// scratch holds cdf_scratch_bytes(R, V) bytes of device memory.
+// scratch holds cdf_scratch_bytes(R, V) bytes of device memory.  rows
+// (device, optional): row r of the launch is logits row rows[r].
+// finish_only: the scratch already holds this row's block results (a
+// decoder total for the same row and tail): only the per-row finish runs.
 size_t cdf_scratch_bytes(int R, int V);
-void launch_cdf_blocks(const float* logits, int R, int V, int tail, int mode,
+void launch_cdf_blocks(const float* logits, const uint32_t* rows, int R, int V, int tail, int mode,
                        const uint32_t* symbols, const uint64_t* values, uint64_t* cum,
-                       uint32_t* freq, uint64_t* total, uint32_t* sym, void* scratch, int* err,
-                       hipStream_t s);
+                       uint32_t* freq, uint64_t* total, uint32_t* sym, void* scratch,
+                       bool finish_only, int* err, hipStream_t s);
 
 // Kernel-level parity entry points.
 void launch_exp_f32(const float* in, float* out, int n, int which, hipStream_t s);

@@ -280,6 +280,53 @@ GgufError Gguf::meta_f32(std::string_view key, float* out) const {
   return GgufError::None;
 }
 
+GgufError Gguf::array_strings(std::string_view key, std::vector<std::string_view>* out) const {
+  const GgufValue* v = find(key);
+  if (!v) return GgufError::MetadataNotFound;
+  if (v->type != GV_ARRAY || v->array_type != GV_STRING) return GgufError::MetadataTypeMismatch;
+  out->clear();
+  out->reserve((size_t)v->array_len);
+  size_t pos = v->array_offset;
+  for (uint64_t k = 0; k < v->array_len; k++) {
+    uint64_t n;
+    std::memcpy(&n, bytes_ + pos, 8);  // validated by parse()
+    out->emplace_back((const char*)bytes_ + pos + 8, (size_t)n);
+    pos += 8 + (size_t)n;
+  }
+  return GgufError::None;
+}
+
+GgufError Gguf::array_ints(std::string_view key, std::vector<int64_t>* out) const {
+  const GgufValue* v = find(key);
+  if (!v) return GgufError::MetadataNotFound;
+  if (v->type != GV_ARRAY) return GgufError::MetadataTypeMismatch;
+  size_t width;
+  switch (v->array_type) {
+    case GV_U8: case GV_I8: width = 1; break;
+    case GV_U16: case GV_I16: width = 2; break;
+    case GV_U32: case GV_I32: width = 4; break;
+    case GV_U64: case GV_I64: width = 8; break;
+    default: return GgufError::MetadataTypeMismatch;
+  }
+  out->clear();
+  out->reserve((size_t)v->array_len);
+  const uint8_t* p = bytes_ + v->array_offset;
+  for (uint64_t k = 0; k < v->array_len; k++, p += width) {
+    int64_t x = 0;
+    switch (v->array_type) {
+      case GV_U8: x = p[0]; break;
+      case GV_I8: x = (int8_t)p[0]; break;
+      case GV_U16: { uint16_t t; std::memcpy(&t, p, 2); x = t; break; }
+      case GV_I16: { int16_t t; std::memcpy(&t, p, 2); x = t; break; }
+      case GV_U32: { uint32_t t; std::memcpy(&t, p, 4); x = t; break; }
+      case GV_I32: { int32_t t; std::memcpy(&t, p, 4); x = t; break; }
+      default: std::memcpy(&x, p, 8); break;
+    }
+    out->push_back(x);
+  }
+  return GgufError::None;
+}
+
 GgufError Gguf::meta_str(std::string_view key, std::string_view* out) const {
   const GgufValue* v = find(key);
   if (!v) return GgufError::MetadataNotFound;

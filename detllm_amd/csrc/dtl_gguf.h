@@ -61,6 +61,10 @@ class Gguf {
   GgufError meta_u32(std::string_view key, uint32_t* out) const;
   GgufError meta_f32(std::string_view key, float* out) const;
   GgufError meta_str(std::string_view key, std::string_view* out) const;
+  // Elements of an array-of-strings / array-of-integers metadata value
+  // (MetadataTypeMismatch for another element type).
+  GgufError array_strings(std::string_view key, std::vector<std::string_view>* out) const;
+  GgufError array_ints(std::string_view key, std::vector<int64_t>* out) const;
   GgufError tensor_data(const GgufTensor& t, const uint8_t** data, size_t* len) const;
   static GgufError element_count(const GgufTensor& t, uint64_t* n);
   static GgufError encoded_len(const GgufTensor& t, uint64_t* n);

@@ -1370,11 +1370,11 @@ __device__ uint64_t block_sum_u64_256(uint64_t v, uint64_t* red) {
 }  // namespace
 
 // Block maxima (order independent) and finiteness.
-__global__ void __launch_bounds__(256) k_cdf_bmax(const float* logits, int V, CdfScratch cs,
-                                                  int* err) {
+__global__ void __launch_bounds__(256) k_cdf_bmax(const float* logits, const uint32_t* rows, int V,
+                                                  CdfScratch cs, int* err) {
   __shared__ float red[4];
   const int r = blockIdx.y, b = blockIdx.x, nb = gridDim.x;
-  const float* l = logits + (size_t)r * V;
+  const float* l = logits + (size_t)(rows ? rows[r] : r) * V;
   float v[16];
 #pragma unroll
   for (int k = 0; k < 16; k++) {
@@ -1396,9 +1396,10 @@ __global__ void __launch_bounds__(256) k_cdf_bmax(const float* logits, int V, Cd
 
 // e_i = exp_f32(max(l_i - m, -88)) for the block, stored chain-major:
 // element i at [i % 8][i / 8] of the row's buffer.
-__global__ void __launch_bounds__(256) k_cdf_bexp(const float* logits, int V, CdfScratch cs) {
+__global__ void __launch_bounds__(256) k_cdf_bexp(const float* logits, const uint32_t* rows, int V,
+                                                  CdfScratch cs) {
   const int r = blockIdx.y, b = blockIdx.x, nb = gridDim.x;
-  const float* l = logits + (size_t)r * V;
+  const float* l = logits + (size_t)(rows ? rows[r] : r) * V;
   float mx = -__builtin_huge_valf();
   for (int k = 0; k < nb; k++) mx = fmaxf(mx, cs.pmax[(size_t)r * nb + k]);
   const int v8 = cdf_v8(V);
@@ -1609,17 +1610,18 @@ __global__ void __launch_bounds__(256) k_cdf_finish(int V, int nb, int tail, int
   }
 }
 
-void launch_cdf_blocks(const float* logits, int R, int V, int tail, int mode,
+void launch_cdf_blocks(const float* logits, const uint32_t* rows, int R, int V, int tail, int mode,
                        const uint32_t* symbols, const uint64_t* values, uint64_t* cum,
-                       uint32_t* freq, uint64_t* total, uint32_t* sym, void* scratch, int* err,
-                       hipStream_t s) {
+                       uint32_t* freq, uint64_t* total, uint32_t* sym, void* scratch,
+                       bool finish_only, int* err, hipStream_t s) {
   const int nb = cdf_nblk(V);
   CdfScratch cs = cdf_scratch(scratch, R, V);
-  launch_kernel(k_cdf_bmax, dim3(nb, R), dim3(256), 0, s, logits, V, cs, err);
-  launch_kernel(k_cdf_bexp, dim3(nb, R), dim3(256), 0, s, logits, V, cs);
-  launch_kernel(k_cdf_z, dim3(R), dim3(256), 0, s, V, cs);
-  if (mode != 3) launch_kernel(k_cdf_bfreq, dim3(nb, R), dim3(256), 0, s, V, mode, symbols, cs);
-  else launch_kernel(k_cdf_bfreq, dim3(nb, R), dim3(256), 0, s, V, 3, symbols, cs);
+  if (!finish_only) {
+    launch_kernel(k_cdf_bmax, dim3(nb, R), dim3(256), 0, s, logits, rows, V, cs, err);
+    launch_kernel(k_cdf_bexp, dim3(nb, R), dim3(256), 0, s, logits, rows, V, cs);
+    launch_kernel(k_cdf_z, dim3(R), dim3(256), 0, s, V, cs);
+    launch_kernel(k_cdf_bfreq, dim3(nb, R), dim3(256), 0, s, V, mode, symbols, cs);
+  }
   launch_kernel(k_cdf_finish, dim3(R), dim3(256), 0, s, V, nb, tail, mode, symbols, values, cum,
                 freq, total, sym, cs, err);
 }

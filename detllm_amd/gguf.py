@@ -51,7 +51,10 @@ class GgufWriter:
         self.metadata.append((key, _STR, v))
 
     def add_str_array(self, key: str, v: List[str]) -> None:
-        self.metadata.append((key, _ARR, list(v)))
+        self.metadata.append((key, _ARR, (_STR, list(v))))
+
+    def add_i32_array(self, key: str, v: List[int]) -> None:
+        self.metadata.append((key, _ARR, (_I32, [int(x) for x in v])))
 
     def add_tensor(self, name: str, dims: Tuple[int, ...], ggml_type: int, data: Union[bytes, np.ndarray]) -> None:
         raw = data.tobytes() if isinstance(data, np.ndarray) else bytes(data)
@@ -82,9 +85,13 @@ class GgufWriter:
             elif ty == _STR:
                 out += self._str(v)
             elif ty == _ARR:
-                out += struct.pack("<IQ", _STR, len(v))
-                for s in v:
-                    out += self._str(s)
+                ety, items = v
+                out += struct.pack("<IQ", ety, len(items))
+                if ety == _STR:
+                    for s in items:
+                        out += self._str(s)
+                else:
+                    out += struct.pack(f"<{len(items)}i", *items)
             else:
                 raise ValueError(ty)
         offset = 0

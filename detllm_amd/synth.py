@@ -18,7 +18,7 @@ Workloads (shapes of well-known checkpoints, random weights):
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Dict, Optional
+from typing import Tuple, List, Dict, Optional
 
 import numpy as np
 
@@ -200,6 +200,20 @@ WORKLOADS: Dict[str, Workload] = {
 }
 
 
+# Byte tokens the synthetic vocabularies mark non-emittable (GGUF token type
+# 3, control): the byte-fallback tokenizer codes these bytes as escapes.
+ESCAPED_BYTES = (0x7A, 0x7E)
+
+
+def vocabulary(vocab: int) -> Tuple[List[str], List[int]]:
+    """Synthetic vocabulary: ids 0..255 are the byte-fallback tokens <0x00>
+    .. <0xFF> (type 6, byte; ESCAPED_BYTES type 3), the rest plain tokens
+    (type 1) that the byte-fallback path never emits."""
+    tokens = [f"<0x{b:02X}>" for b in range(256)] + [f"<synth_{i}>" for i in range(256, vocab)]
+    types = [3 if b in ESCAPED_BYTES else 6 for b in range(256)] + [1] * (vocab - 256)
+    return tokens, types
+
+
 def build_model(w: Workload, layers: Optional[int] = None) -> bytes:
     """Writes the workload's model as GGUF bytes.  `layers` truncates depth
     (used by quick tests); the benchmark always uses the full depth."""
@@ -217,6 +231,9 @@ def build_model(w: Workload, layers: Optional[int] = None) -> bytes:
     g.add_f32(p + "rope.freq_base", w.rope_base)
     g.add_f32(p + "attention.layer_norm_rms_epsilon", w.eps)
     g.add_u32(p + "vocab_size", w.vocab)
+    tokens, types = vocabulary(w.vocab)
+    g.add_str_array("tokenizer.ggml.tokens", tokens)
+    g.add_i32_array("tokenizer.ggml.token_type", types)
 
     def mat(name: str, rows: int, cols: int, kind: str) -> None:
         st = Stream(w.seed, name)
@@ -270,3 +287,140 @@ def tokens(w: Workload, n: Optional[int] = None) -> np.ndarray:
     if w.token_dist == "uniform":
         return Stream(w.seed, "tokens").ints(n, 0, w.vocab - 1).astype(np.uint32)
     return zipf_tokens(w.seed, "tokens", n, w.vocab)
+
+
+def _pattern(n: int, period: int, scale: float) -> np.ndarray:
+    """((i % period) - period // 2) * scale in f32, the fixture weight pattern."""
+    i = np.arange(n)
+    return (((i % period).astype(np.float32) - np.float32(period // 2)) * np.float32(scale)).astype(np.float32)
+
+
+def cli_fixture_gguf(vocab_size: int = 256, token_override: Optional[Tuple[int, str]] = None,
+                     include_bpe: bool = False) -> bytes:
+    """The byte-fallback test model of the reference codec tests
+    (det-cli main.rs:1976-2047): Llama 1 layer, d 4, FFN 6, 2/1 heads,
+    rope_dim 2, n_ctx 16, F32 weights ((i % 13) - 6) * scale; the
+    vocabulary is <0x00>..<0xFF> (+ "ab" and a merge with include_bpe)."""
+    g = GgufWriter()
+    g.add_str("general.architecture", "llama")
+    for k, v in (("block_count", 1), ("embedding_length", 4), ("feed_forward_length", 6),
+                 ("attention.head_count", 2), ("attention.head_count_kv", 1)):
+        g.add_u32("llama." + k, v)
+    g.add_f32("llama.attention.layer_norm_rms_epsilon", 1e-5)
+    g.add_f32("llama.rope.freq_base", 10_000.0)
+    g.add_u32("llama.rope.dimension_count", 2)
+    g.add_u32("llama.context_length", 16)
+    g.add_u32("llama.vocab_size", vocab_size)
+    toks = [f"<0x{b:02X}>" for b in range(256)]
+    if token_override is not None:
+        toks[token_override[0]] = token_override[1]
+    if include_bpe:
+        toks.append("ab")
+    g.add_str_array("tokenizer.ggml.tokens", toks)
+    if include_bpe:
+        g.add_str("tokenizer.ggml.model", "gpt2")
+        g.add_str_array("tokenizer.ggml.merges", ["<0x61> <0x62>"])
+
+    def mat(name: str, rows: int, cols: int, scale: float) -> None:
+        g.add_tensor(name, (cols, rows), GGML_F32, _pattern(rows * cols, 13, scale))
+
+    def vec(name: str, n: int) -> None:
+        g.add_tensor(name, (n,), GGML_F32, np.ones(n, np.float32))
+
+    mat("token_embd.weight", vocab_size, 4, 0.001)
+    vec("blk.0.attn_norm.weight", 4)
+    mat("blk.0.attn_q.weight", 4, 4, 0.002)
+    mat("blk.0.attn_k.weight", 2, 4, -0.0015)
+    mat("blk.0.attn_v.weight", 2, 4, 0.0025)
+    mat("blk.0.attn_output.weight", 4, 4, -0.002)
+    vec("blk.0.ffn_norm.weight", 4)
+    mat("blk.0.ffn_gate.weight", 6, 4, 0.003)
+    mat("blk.0.ffn_up.weight", 6, 4, -0.0025)
+    mat("blk.0.ffn_down.weight", 4, 6, 0.0018)
+    vec("output_norm.weight", 4)
+    mat("output.weight", vocab_size, 4, 0.0022)
+    return g.to_bytes()
+
+
+def codec_fixture_gguf() -> bytes:
+    """The 4-token model of the reference's token-codec tests
+    (det-cli main.rs:390-431): d 4, FFN 6, 2/1 heads, rope_dim 2, n_ctx 8,
+    F32 weights ((i % 9) - 4) * scale."""
+    g = GgufWriter()
+    g.add_str("general.architecture", "llama")
+    for k, v in (("block_count", 1), ("embedding_length", 4), ("feed_forward_length", 6),
+                 ("attention.head_count", 2), ("attention.head_count_kv", 1)):
+        g.add_u32("llama." + k, v)
+    g.add_f32("llama.attention.layer_norm_rms_epsilon", 1e-5)
+    g.add_f32("llama.rope.freq_base", 10_000.0)
+    g.add_u32("llama.rope.dimension_count", 2)
+    g.add_u32("llama.context_length", 8)
+    g.add_u32("llama.vocab_size", 4)
+
+    def mat(name: str, rows: int, cols: int, scale: float) -> None:
+        g.add_tensor(name, (cols, rows), GGML_F32, _pattern(rows * cols, 9, scale))
+
+    def vec(name: str, n: int) -> None:
+        g.add_tensor(name, (n,), GGML_F32, np.ones(n, np.float32))
+
+    mat("token_embd.weight", 4, 4, 0.01)
+    vec("blk.0.attn_norm.weight", 4)
+    mat("blk.0.attn_q.weight", 4, 4, 0.02)
+    mat("blk.0.attn_k.weight", 2, 4, -0.015)
+    mat("blk.0.attn_v.weight", 2, 4, 0.025)
+    mat("blk.0.attn_output.weight", 4, 4, -0.02)
+    vec("blk.0.ffn_norm.weight", 4)
+    mat("blk.0.ffn_gate.weight", 6, 4, 0.03)
+    mat("blk.0.ffn_up.weight", 6, 4, -0.025)
+    mat("blk.0.ffn_down.weight", 4, 6, 0.018)
+    vec("output_norm.weight", 4)
+    mat("output.weight", 4, 4, 0.022)
+    return g.to_bytes()
+
+
+def markov_bytes(seed: int, n: int) -> bytes:
+    """n bytes of seeded order-3 Markov text over printable ASCII + newline.
+
+    Words have Zipf(1.1) lengths in 1..16 and are separated by spaces;
+    lines hold Zipf(1.1) 1..20 words.  Each word character is drawn by
+    rank from a Zipf(1.1) law over the 94 visible characters, and the
+    rank -> character map is a seeded permutation chosen by the previous
+    three bytes (4096 hashed contexts), which makes the source order-3."""
+    visible = np.arange(0x21, 0x7F, dtype=np.uint8)  # 94 characters
+    nctx = 4096
+    perms = np.argsort(Stream(seed, "markov.perm").u64(nctx * 94).reshape(nctx, 94), axis=1, kind="stable")
+    table = visible[perms]  # [ctx][rank] -> byte
+
+    def zipf_ranks(key: str, count: int, k: int) -> np.ndarray:
+        w = _exp(-1.1 * _ln(np.arange(1, k + 1, dtype=np.float64)))
+        cdf = np.cumsum(w)
+        cdf = cdf / cdf[-1]
+        return np.minimum(np.searchsorted(cdf, Stream(seed, key).unit(count), side="right"), k - 1)
+
+    ranks = zipf_ranks("markov.char", n, 94)
+    word_len = zipf_ranks("markov.word", n // 2 + 2, 16) + 1
+    line_words = zipf_ranks("markov.line", n // 2 + 2, 20) + 1
+    out = bytearray(n)
+    c1 = c2 = c3 = 0x0A
+    i = wi = li = ri = 0
+    left_in_word = int(word_len[0])
+    left_in_line = int(line_words[0])
+    while i < n:
+        if left_in_word == 0:
+            left_in_line -= 1
+            if left_in_line == 0:
+                b = 0x0A
+                li += 1
+                left_in_line = int(line_words[li])
+            else:
+                b = 0x20
+            wi += 1
+            left_in_word = int(word_len[wi])
+        else:
+            b = int(table[((c1 * 961) + (c2 * 31) + c3) & (nctx - 1), ranks[ri]])
+            ri += 1
+            left_in_word -= 1
+        out[i] = b
+        c1, c2, c3 = c2, c3, b
+        i += 1
+    return bytes(out)

@@ -52,7 +52,42 @@ typedef enum {
     DTL_ERR_DEVICE = 40,
     DTL_ERR_OUT_OF_MEMORY = 41,
     DTL_ERR_INVALID_ARGUMENT = 42,
-    DTL_ERR_NO_DEVICE = 43
+    DTL_ERR_NO_DEVICE = 43,
+    DTL_ERR_BUFFER_TOO_SMALL = 44, /* output capacity below the size in *len */
+    /* 60-77: det-token TokenError (crates/det-token/src/lib.rs:6-25), in order;
+     * 77 also reports a BPE / SentencePiece vocabulary, which this library
+     * does not tokenize. */
+    DTL_ERR_TOKEN_MISSING_BYTE_FALLBACK = 60,
+    DTL_ERR_TOKEN_INVALID_TOKEN = 61,
+    DTL_ERR_TOKEN_MISSING_VOCABULARY = 62,
+    DTL_ERR_TOKEN_MISSING_TOKEN_BYTES = 63,
+    DTL_ERR_TOKEN_MISSING_MERGE_TOKEN = 64,
+    DTL_ERR_TOKEN_INCOMPLETE_BYTE_FALLBACK = 65,
+    DTL_ERR_TOKEN_METADATA_TYPE = 66,
+    DTL_ERR_TOKEN_TYPE_LENGTH = 67,
+    DTL_ERR_TOKEN_INVALID_TOKEN_TYPE = 68,
+    DTL_ERR_TOKEN_SCORES_LENGTH = 69,
+    DTL_ERR_TOKEN_NON_FINITE_SCORE = 70,
+    DTL_ERR_TOKEN_INDEX_OVERFLOW = 71,
+    DTL_ERR_TOKEN_DUPLICATE_BYTE_FALLBACK = 72,
+    DTL_ERR_TOKEN_DUPLICATE_TOKEN_ID = 73,
+    DTL_ERR_TOKEN_DUPLICATE_TOKEN_BYTES = 74,
+    DTL_ERR_TOKEN_INVALID_MERGE = 75,
+    DTL_ERR_TOKEN_DUPLICATE_MERGE = 76,
+    DTL_ERR_TOKEN_UNSUPPORTED_MODEL = 77,
+    /* 80-85: det-coder FileError (crates/det-coder/src/file.rs:18-25). */
+    DTL_ERR_FILE_TOO_SHORT = 80,
+    DTL_ERR_FILE_BAD_MAGIC = 81,
+    DTL_ERR_FILE_UNSUPPORTED_VERSION = 82,
+    DTL_ERR_FILE_UNSUPPORTED_FLAGS = 83,
+    DTL_ERR_FILE_INVALID_CONTEXT = 84,
+    DTL_ERR_FILE_INVALID_OVERLAP = 85,
+    /* 90-92: the codec failures det-cli reports as messages
+     * (crates/det-cli/src/main.rs:478-480, 503-507, 571-573). */
+    DTL_ERR_CODEC_MODEL_MISMATCH = 90,
+    DTL_ERR_CODEC_NOT_CANONICAL = 91,
+    DTL_ERR_CODEC_ESCAPE_IN_TOKEN_STREAM = 92,
+    DTL_ERR_CODEC_VOCAB_MISMATCH = 93 /* tokenizer vocabulary != model vocabulary */
 } dtl_status;
 
 typedef struct dtl_model dtl_model;
@@ -115,6 +150,11 @@ int dtl_forward_chunk(dtl_session *session, const uint32_t *tokens, size_t n, si
 /* Copies rows [first, first+n) of the last forward's logits to the host. */
 int dtl_session_logits(dtl_session *session, size_t first, size_t n, float *out);
 
+/* The session's window (n_ctx), chunk capacity and the model's output vocab
+ * (no reference counterpart: lets host drivers size their work). */
+int dtl_session_get_info(const dtl_session *session, size_t *n_ctx, size_t *max_chunk,
+                         size_t *vocab);
+
 /* F32Llama::logits_hash_for_tokens_chunked (det-model lib.rs:1406-1465):
  * SHA-256 of every position's f32 logits (little-endian bits), positions
  * ascending.  chunk sets how many positions share one device pass. */
@@ -152,6 +192,13 @@ int dtl_session_profile(dtl_session *session, dtl_kernel_stat *out, size_t cap, 
  * or 256 (BYTE_ESCAPE_SYMBOLS). */
 int dtl_symbol_ranges(dtl_session *session, size_t first, size_t n, const uint32_t *symbols,
                       size_t tail_symbols, uint64_t *cum, uint32_t *freq, uint64_t *total);
+
+/* The same for an arbitrary row of the last forward per symbol: symbols[i]
+ * is coded against row rows[i] (several symbols may share a row, as byte
+ * escapes share the logits of the last token in det-cli's codec loop). */
+int dtl_symbol_ranges_rows(dtl_session *session, size_t n, const uint32_t *rows,
+                           const uint32_t *symbols, size_t tail_symbols, uint64_t *cum,
+                           uint32_t *freq, uint64_t *total);
 
 /* logits_to_cdf_with_scratch / _with_byte_escapes (cdf.rs:52-106): the
  * full table for one row; freq and cum hold vocab + tail_symbols entries. */
@@ -194,6 +241,74 @@ int dtl_range_decoder_new(const uint8_t *data, size_t len, dtl_range_decoder **o
 int dtl_range_decode_freq(dtl_range_decoder *dec, uint64_t total, uint64_t *value);
 int dtl_range_decode_advance(dtl_range_decoder *dec, uint64_t cum, uint64_t freq, uint64_t total);
 void dtl_range_decoder_free(dtl_range_decoder *dec);
+
+/* ---- det-token byte-fallback tokenizer (host) ---------------------------- */
+typedef struct dtl_tokenizer dtl_tokenizer;
+
+/* Tokenizer::from_gguf (det-token lib.rs:86-131) for the byte-fallback kind
+ * (ByteFallbackTokenizer::from_tokens_and_emit_mask, lib.rs:262-317): the
+ * "<0xHH>" vocabulary tokens and the token-type emit mask of the GGUF. */
+int dtl_tokenizer_from_gguf(const uint8_t *gguf, size_t len, dtl_tokenizer **out);
+void dtl_tokenizer_free(dtl_tokenizer *tok);
+/* Number of vocabulary tokens the tokenizer was built from. */
+size_t dtl_tokenizer_vocab_len(const dtl_tokenizer *tok);
+/* Tokenizer::codec_symbols (lib.rs:150-159): one symbol per input byte, the
+ * byte's token or the escape vocab_len + byte.  *n_out receives the count;
+ * out may be NULL to query it. */
+int dtl_tokenizer_codec_symbols(const dtl_tokenizer *tok, const uint8_t *input, size_t n,
+                                size_t vocab_len, uint32_t *out, size_t cap, size_t *n_out);
+/* Tokenizer::decode_codec_symbol (lib.rs:182-196): the bytes of one symbol. */
+int dtl_tokenizer_decode_symbol(const dtl_tokenizer *tok, uint32_t symbol, size_t vocab_len,
+                                uint8_t *out, size_t cap, size_t *n_out);
+
+/* ---- det-cli windowed codec + DTLZ file (host driver over the device) ---- */
+
+#define DTL_DTLZ_FLAG_BYTE_ESCAPES 1u
+#define DTL_DTLZ_HEADER_LEN 56u
+
+/* next_window_start (det-cli main.rs:801-808): the start of the codec
+ * window for position pos (a rollover starts it overlap tokens back once
+ * the window holds n_ctx tokens). */
+size_t dtl_codec_next_window_start(size_t pos, size_t window_start, size_t n_ctx, size_t overlap);
+/* encode_symbols_with_model (det-cli main.rs:521-551): codec symbols coded
+ * window by window (window = the session's n_ctx, overlap tokens replayed
+ * at each rollover), each against the logits of the window's last token or
+ * uniformly when the window is empty.  *len = payload size; out NULL is a
+ * size query (it runs the whole encode), cap < *len returns
+ * DTL_ERR_BUFFER_TOO_SMALL.  The session's cache is overwritten. */
+int dtl_codec_encode(dtl_session *session, const uint32_t *symbols, size_t n, size_t overlap,
+                     int byte_escapes, uint8_t *out, size_t cap, size_t *len);
+/* decode_bytes_with_model / decode_tokens_with_model (main.rs:553-632):
+ * decodes symbols until piece_len (bytes per symbol, vocab + 256 entries, 0
+ * for a symbol that decodes to nothing) sums to byte_len, or max_symbols
+ * symbols when piece_len is NULL. */
+int dtl_codec_decode(dtl_session *session, const uint8_t *payload, size_t len, size_t overlap,
+                     int byte_escapes, const uint8_t *piece_len, size_t byte_len,
+                     size_t max_symbols, uint32_t *symbols, size_t *n_out);
+/* DtlzHeader::{encode_checked, decode} (det-coder file.rs:1-89): 56 bytes. */
+int dtl_dtlz_header_encode(uint16_t flags, const uint8_t model_sha256[32], uint32_t n_ctx,
+                           uint32_t overlap, uint64_t orig_len, uint8_t out[56]);
+int dtl_dtlz_header_decode(const uint8_t *bytes, size_t len, uint16_t *flags,
+                           uint8_t model_sha256[32], uint32_t *n_ctx, uint32_t *overlap,
+                           uint64_t *orig_len);
+/* compress (det-cli main.rs:431-462): header (model SHA-256, n_ctx, overlap
+ * n_ctx/4, byte escapes on, original length) + payload.  n_ctx 0 = the
+ * model's context length; max_chunk (0 = 64) positions per device pass.
+ * The tokenizer must be the model's (LoadedModel::load, main.rs:932-1000).
+ * *out is allocated by the library: release it with dtl_bytes_free. */
+int dtl_compress(const dtl_model *model, const dtl_tokenizer *tok, const uint8_t model_sha256[32],
+                 const uint8_t *input, size_t n, size_t n_ctx, size_t max_chunk, uint8_t **out,
+                 size_t *len);
+/* decompress (main.rs:464-512): validates the header before touching the
+ * model (model and tok may be NULL for a header that fails), checks the
+ * model hash, decodes up to the header's original length, and requires the
+ * payload to be the canonical encoding of what it decoded.  *out as for
+ * dtl_compress. */
+int dtl_decompress(const dtl_model *model, const dtl_tokenizer *tok,
+                   const uint8_t model_sha256[32], const uint8_t *file, size_t len,
+                   size_t max_chunk, uint8_t **out, size_t *out_len);
+/* Releases a buffer returned by dtl_compress / dtl_decompress. */
+void dtl_bytes_free(uint8_t *p);
 
 /* ---- det-num / det-quant kernels, exposed for parity checks ------------- */
 

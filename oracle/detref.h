@@ -124,6 +124,19 @@ int ref_range_decode_freq(ref_range_decoder *d, uint64_t total, uint64_t *value)
 int ref_range_decode_advance(ref_range_decoder *d, uint64_t cum, uint64_t freq, uint64_t total);
 void ref_range_decoder_free(ref_range_decoder *d);
 
+/* ---- det-token byte fallback + det-cli windowed codec ----------------- */
+int ref_canonical_byte_token(const char *tok, size_t len);
+int ref_byte_fallback_tables(const char *text, const size_t *off, size_t n, const uint8_t *emit,
+                             int32_t byte_to_token[256], int16_t *token_to_byte);
+void ref_codec_symbols(const int32_t byte_to_token[256], const uint8_t *in, size_t n,
+                       size_t vocab_len, uint32_t *out);
+size_t ref_next_window_start(size_t pos, size_t window_start, size_t n_ctx, size_t overlap);
+int ref_codec_encode(const ref_model *m, const uint32_t *symbols, size_t n, size_t n_ctx,
+                     size_t overlap, int escapes, uint8_t *out, size_t cap, size_t *len);
+int ref_codec_decode(const ref_model *m, const int16_t *token_to_byte, const uint8_t *payload,
+                     size_t plen, size_t byte_len, size_t n_ctx, size_t overlap, int escapes,
+                     uint32_t *symbols, uint8_t *bytes, size_t *n_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -75,6 +75,14 @@ def load() -> C.CDLL:
         "ref_range_decode_freq": (C.c_int, [C.c_void_p, C.c_uint64, u64p]),
         "ref_range_decode_advance": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64]),
         "ref_range_decoder_free": (None, [C.c_void_p]),
+        "ref_canonical_byte_token": (C.c_int, [C.c_char_p, sz]),
+        "ref_byte_fallback_tables": (C.c_int, [C.c_char_p, C.POINTER(sz), sz, u8p,
+                                               C.POINTER(C.c_int32), C.POINTER(C.c_int16)]),
+        "ref_codec_symbols": (None, [C.POINTER(C.c_int32), u8p, sz, sz, u32p]),
+        "ref_next_window_start": (sz, [sz, sz, sz, sz]),
+        "ref_codec_encode": (C.c_int, [C.c_void_p, u32p, sz, sz, sz, C.c_int, u8p, sz, C.POINTER(sz)]),
+        "ref_codec_decode": (C.c_int, [C.c_void_p, C.POINTER(C.c_int16), u8p, sz, sz, sz, sz, C.c_int,
+                                       u32p, u8p, C.POINTER(sz)]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -245,3 +253,65 @@ def range_encode(triples) -> bytes:
         return bytes(buf)
     finally:
         L.ref_range_encoder_free(e)
+
+
+# ---- det-token byte fallback + det-cli windowed codec -----------------------
+def canonical_byte_token(tok: str) -> int:
+    """canonical_byte_fallback_token: the byte, or -1."""
+    b = tok.encode()
+    return int(lib().ref_canonical_byte_token(b, len(b)))
+
+
+def byte_fallback_tables(tokens, emit=None):
+    """(byte_to_token int32[256], token_to_byte int16[n]) of a vocabulary."""
+    enc = [t.encode() for t in tokens]
+    off = np.zeros(len(enc) + 1, np.uint64)
+    off[1:] = np.cumsum([len(e) for e in enc]) if enc else []
+    text = b"".join(enc)
+    b2t = np.empty(256, np.int32)
+    t2b = np.empty(max(len(enc), 1), np.int16)
+    em = None if emit is None else np.ascontiguousarray(np.asarray(emit, np.uint8))
+    _chk(lib().ref_byte_fallback_tables(text, off.ctypes.data_as(C.POINTER(C.c_size_t)), len(enc),
+                                        None if em is None else _p(em, C.c_uint8),
+                                        _p(b2t, C.c_int32), _p(t2b, C.c_int16)),
+         "ref_byte_fallback_tables")
+    return b2t, t2b[: len(enc)]
+
+
+def codec_symbols(byte_to_token, data: bytes, vocab_len: int) -> np.ndarray:
+    b2t = np.ascontiguousarray(np.asarray(byte_to_token, np.int32))
+    src = np.frombuffer(bytes(data), np.uint8).copy()
+    out = np.empty(max(src.size, 1), np.uint32)
+    lib().ref_codec_symbols(_p(b2t, C.c_int32), _p(src, C.c_uint8), src.size, vocab_len,
+                            _p(out, C.c_uint32))
+    return out[: src.size]
+
+
+def next_window_start(pos: int, window_start: int, n_ctx: int, overlap: int) -> int:
+    return int(lib().ref_next_window_start(pos, window_start, n_ctx, overlap))
+
+
+def codec_encode(model: Model, symbols, n_ctx: int, overlap: int, escapes: bool = True) -> bytes:
+    """encode_symbols_with_model, one forward per token as the reference runs it."""
+    sym = np.ascontiguousarray(np.asarray(symbols, np.uint32))
+    n = C.c_size_t()
+    _chk(lib().ref_codec_encode(model._h, _p(sym, C.c_uint32), sym.size, n_ctx, overlap, int(escapes),
+                                None, 0, C.byref(n)), "ref_codec_encode")
+    buf = (C.c_uint8 * n.value)()
+    _chk(lib().ref_codec_encode(model._h, _p(sym, C.c_uint32), sym.size, n_ctx, overlap, int(escapes),
+                                buf, n.value, C.byref(n)), "ref_codec_encode")
+    return bytes(buf)
+
+
+def codec_decode(model: Model, token_to_byte, payload: bytes, byte_len: int, n_ctx: int, overlap: int,
+                 escapes: bool = True):
+    """decode_bytes_with_model for a byte-fallback vocabulary: (symbols, bytes)."""
+    t2b = np.ascontiguousarray(np.asarray(token_to_byte, np.int16))
+    pl = np.frombuffer(bytes(payload), np.uint8).copy()
+    syms = np.empty(max(byte_len, 1), np.uint32)
+    out = np.empty(max(byte_len, 1), np.uint8)
+    n = C.c_size_t()
+    _chk(lib().ref_codec_decode(model._h, _p(t2b, C.c_int16), _p(pl, C.c_uint8), pl.size, byte_len, n_ctx,
+                                overlap, int(escapes), _p(syms, C.c_uint32), _p(out, C.c_uint8),
+                                C.byref(n)), "ref_codec_decode")
+    return syms[: n.value], bytes(out[: n.value])

@@ -84,6 +84,7 @@ def test_dtlz_header_roundtrip():
     from detllm_amd.coder import HEADER_LEN, DtlzHeader
 
     h = DtlzHeader(1, bytes(range(32)), 2048, 512, 1 << 20)
-    raw = h.encode()
+    raw = h.encode_checked()
     assert len(raw) == HEADER_LEN == 56 and raw[:4] == b"DTLZ"
+    assert raw == h.encode()
     assert DtlzHeader.decode(raw) == h
