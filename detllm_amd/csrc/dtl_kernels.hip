@@ -863,22 +863,30 @@ __global__ void __launch_bounds__(1024) k_attention_hd64(const float* q, const f
   if (bad) flag(err, ERRBIT_NON_FINITE);
 }
 
-// Decode shape (a few positions): one workgroup of 256 threads per (head,
-// position), so a single position still spreads over H workgroups.  All
-// threads compute scores (8-lane dot order) into LDS; a block max, the
-// clamped exps in parallel, the 8-lane Z chains (lanes 0-7), p = e / Z in
-// parallel; then wave 0 runs the 64 P.V chains (lane = dimension),
-// streaming V rows with eight loads in flight.
-__global__ void __launch_bounds__(256) k_attention_dec(const float* q, const float* kc,
-                                                       const float* vc, int layer, int pos0,
-                                                       int H, int KV, int n_ctx, float scale,
-                                                       float* out, const int* pos_dev, int* err) {
+// Decode shape (a few positions): one workgroup of 1024 threads per (head,
+// position).  All threads compute scores (8-lane dot order) into LDS; a block
+// max, the clamped exps in parallel, the 8-lane Z chains (lanes 0-7), p = e /
+// Z in parallel.  P.V (lib.rs:2390-2420: out[d] = 0; out[d] += p_j * v_j[d]
+// for j ascending) splits into the products, which every thread forms for
+// one float4 of a 64-position V tile and stores dimension-major in LDS, and
+// the 64 serial sums, which wave 0 runs over the stored products (lane =
+// dimension, four products per LDS read).  V tiles stream through a ring of
+// kDecDepth registers per thread, so kDecDepth tiles of loads are in flight
+// while wave 0 sums.
+constexpr int kDecThreads = 1024, kDecTile = 64, kDecStride = 68, kDecDepth = 8;
+
+__global__ void __launch_bounds__(kDecThreads) k_attention_dec(const float* q, const float* kc,
+                                                               const float* vc, int layer, int pos0,
+                                                               int H, int KV, int n_ctx, float scale,
+                                                               float* out, const int* pos_dev,
+                                                               int* err) {
   extern __shared__ __align__(16) float sc[];  // [len] scores -> exps -> probabilities
+  __shared__ __align__(16) float prod[2][64 * kDecStride];  // [dim][position in tile]
   __shared__ __align__(16) float qs[64];
-  __shared__ float red[4];
+  __shared__ float red[kDecThreads / 64];
   __shared__ float zc[8];
   constexpr int hd = 64;
-  const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+  const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = h / (H / KV);
   const int pos = (pos_dev ? *pos_dev : pos0) + t, len = pos + 1;
   const float* keys = kc + ((size_t)layer * KV + g) * n_ctx * hd;
@@ -892,17 +900,22 @@ __global__ void __launch_bounds__(256) k_attention_dec(const float* q, const flo
   if (tid < hd) qs[tid] = q[(size_t)t * H * hd + (size_t)h * hd + tid];
   __syncthreads();
   // scores: dot_f32_ref(q, k_j) * scale
-  for (int j = tid; j < len; j += 256) {
+  for (int j = tid; j < len; j += kDecThreads) {
     const float4* kr = reinterpret_cast<const float4*>(keys + (size_t)j * hd);
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-    for (int i4 = 0; i4 < 16; i4++) {
-      const float4 kv = kr[i4];
-      const int i = 4 * i4;
-      acc[(i + 0) & 7] += qs[i + 0] * kv.x;
-      acc[(i + 1) & 7] += qs[i + 1] * kv.y;
-      acc[(i + 2) & 7] += qs[i + 2] * kv.z;
-      acc[(i + 3) & 7] += qs[i + 3] * kv.w;
+    for (int half = 0; half < 2; half++) {
+      float4 kv[8];
+#pragma unroll
+      for (int i4 = 0; i4 < 8; i4++) kv[i4] = kr[8 * half + i4];
+#pragma unroll
+      for (int i4 = 0; i4 < 8; i4++) {
+        const int i = 32 * half + 4 * i4;
+        acc[(i + 0) & 7] += qs[i + 0] * kv[i4].x;
+        acc[(i + 1) & 7] += qs[i + 1] * kv[i4].y;
+        acc[(i + 2) & 7] += qs[i + 2] * kv[i4].z;
+        acc[(i + 3) & 7] += qs[i + 3] * kv[i4].w;
+      }
     }
     const float s = finish_8lane(acc) * scale;
     if (!finite(s)) bad = true;
@@ -911,12 +924,14 @@ __global__ void __launch_bounds__(256) k_attention_dec(const float* q, const flo
   __syncthreads();
   // softmax_in_place (lib.rs:2361-2388)
   float mx = -__builtin_huge_valf();
-  for (int j = tid; j < len; j += 256) mx = fmaxf(mx, sc[j]);
+  for (int j = tid; j < len; j += kDecThreads) mx = fmaxf(mx, sc[j]);
   for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
-  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  if (lane == 0) red[wave] = mx;
   __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  for (int j = tid; j < len; j += 256) sc[j] = exp_clamped(sc[j] - mx);
+  mx = red[0];
+#pragma unroll
+  for (int w = 1; w < kDecThreads / 64; w++) mx = fmaxf(mx, red[w]);
+  for (int j = tid; j < len; j += kDecThreads) sc[j] = exp_clamped(sc[j] - mx);
   __syncthreads();
   if (tid < 8) {
     float acc = 0.0f;
@@ -933,27 +948,62 @@ __global__ void __launch_bounds__(256) k_attention_dec(const float* q, const flo
   __syncthreads();
   const float z = finish_8lane(zc);
   if (!finite(z) || z == 0.0f) bad = true;
-  for (int j = tid; j < len; j += 256) {
+  for (int j = tid; j < len; j += kDecThreads) {
     const float p = sc[j] / z;
     if (!finite(p)) bad = true;
     sc[j] = p;
   }
   __syncthreads();
-  // P.V: out[d] = 0.0; out[d] += p_j * v_j[d] for j ascending
-  if (tid < hd) {
-    const float* vd = vals + tid;
-    float a = 0.0f;
-    int j = 0;
-    for (; j + 8 <= len; j += 8) {
-      float v[8];
+  // P.V.  Thread tid owns row jr of each tile and dimensions c4 .. c4 + 3.
+  const int ntiles = (len + kDecTile - 1) / kDecTile;
+  const int jr = tid >> 4, c4 = (tid & 15) * 4;
+  const float* vbase = vals + (size_t)jr * hd + c4;
+  float4 ring[kDecDepth];
 #pragma unroll
-      for (int k = 0; k < 8; k++) v[k] = vd[(size_t)(j + k) * hd];
+  for (int u = 0; u < kDecDepth; u++) {
+    const int j = u * kDecTile + jr;
+    ring[u] = j < len ? *reinterpret_cast<const float4*>(vbase + (size_t)u * kDecTile * hd)
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float a = 0.0f;
+  for (int k0 = 0; k0 < ntiles; k0 += kDecDepth) {
 #pragma unroll
-      for (int k = 0; k < 8; k++) a += sc[j + k] * v[k];
+    for (int u = 0; u < kDecDepth; u++) {
+      const int k = k0 + u;
+      if (k < ntiles) {
+        const int j = k * kDecTile + jr;
+        const float p = j < len ? sc[j] : 0.0f;
+        float* pr = prod[k & 1];
+        pr[(c4 + 0) * kDecStride + jr] = p * ring[u].x;
+        pr[(c4 + 1) * kDecStride + jr] = p * ring[u].y;
+        pr[(c4 + 2) * kDecStride + jr] = p * ring[u].z;
+        pr[(c4 + 3) * kDecStride + jr] = p * ring[u].w;
+        const int jn = j + kDecDepth * kDecTile;
+        if (jn < len)
+          ring[u] = *reinterpret_cast<const float4*>(vbase + (size_t)(k + kDecDepth) * kDecTile * hd);
+      }
+      __syncthreads();
+      if (k < ntiles && wave == 0) {
+        const float* pr = prod[k & 1] + lane * kDecStride;
+        const int n = min(kDecTile, len - k * kDecTile);
+        if (n == kDecTile) {
+#pragma unroll
+          for (int jj = 0; jj < kDecTile; jj += 4) {
+            const float4 p4 = *reinterpret_cast<const float4*>(pr + jj);
+            a += p4.x;
+            a += p4.y;
+            a += p4.z;
+            a += p4.w;
+          }
+        } else {
+          for (int jj = 0; jj < n; jj++) a += pr[jj];
+        }
+      }
     }
-    for (; j < len; j++) a += sc[j] * vd[(size_t)j * hd];
+  }
+  if (wave == 0) {
     if (!finite(a)) bad = true;
-    o[tid] = a;
+    o[lane] = a;
   }
   if (bad) flag(err, ERRBIT_NON_FINITE);
 }
@@ -967,8 +1017,12 @@ size_t attention_grp_smem(int H, int KV, int hd, int n_ctx) {
   return ((size_t)G * n_ctx + (size_t)(kAttnTile + 1) * hd + (size_t)G * hd) * sizeof(float);
 }
 
+// Dynamic LDS of k_attention_dec (the score row); its static LDS holds the
+// product tiles.
+constexpr size_t kDecMaxScoreBytes = 112 * 1024;
+
 bool attention_pos_dev_supported(int hd, int T, int n_ctx) {
-  return hd == 64 && T <= 4 && (size_t)n_ctx * sizeof(float) <= 150 * 1024;
+  return hd == 64 && T <= 4 && (size_t)n_ctx * sizeof(float) <= kDecMaxScoreBytes;
 }
 
 void launch_attention(const float* q, const float* kc, const float* vc, int layer, int T, int pos0,
@@ -979,15 +1033,16 @@ void launch_attention(const float* q, const float* kc, const float* vc, int laye
     // Decode: one workgroup per (head, position).  With the position in
     // device memory the score buffer is sized for the whole window.
     size_t smem = (size_t)(pos_dev ? n_ctx : pos0 + T) * sizeof(float);
-    if (smem <= 150 * 1024) {
+    if (smem <= kDecMaxScoreBytes) {
       static bool attr_dec_set = false;
       if (!attr_dec_set) {
         (void)hipFuncSetAttribute((const void*)k_attention_dec,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)kDecMaxScoreBytes);
         attr_dec_set = true;
       }
-      launch_kernel(k_attention_dec, dim3(H, T), dim3(256), smem, s, q, kc, vc, layer, pos0, H,
-                    KV, n_ctx, scale, out, pos_dev, err);
+      launch_kernel(k_attention_dec, dim3(H, T), dim3(kDecThreads), smem, s, q, kc, vc, layer,
+                    pos0, H, KV, n_ctx, scale, out, pos_dev, err);
       return;
     }
   }
