@@ -100,6 +100,54 @@ def decode_leg(model, toks, positions: int, workload: str) -> dict:
             "gemv": gemv}
 
 
+def codec_leg(gguf: bytes, workload: str, nbytes: int, cpu_bytes: int, threads: int) -> dict:
+    """End-to-end DTLZ compress + decompress of a prefix of the seeded
+    order-3 Markov byte stream on the device (window n_ctx 2048, overlap
+    512, byte escapes), and the first cpu_bytes of the device-encoded
+    payload decoded by the oracle on the host (GPU-encode -> CPU-decode)."""
+    import numpy as np
+
+    from detllm_amd import synth
+    from detllm_amd.codec import LoadedModel, compress, decompress, next_window_start
+
+    n_ctx = 2048
+    lm = LoadedModel.load(gguf)
+    data = synth.markov_bytes(0xDE711005, nbytes)
+    t = time.perf_counter()
+    out = compress(lm, data, n_ctx, max_chunk=64)
+    t_c = time.perf_counter() - t
+    t = time.perf_counter()
+    back = decompress(lm, out, max_chunk=64)
+    t_d = time.perf_counter() - t
+    sym = lm.tokenizer.codec_symbols(data, lm.model.vocab)
+    ntok = int((sym < lm.model.vocab).sum())
+    starts, ws = 1, 0
+    for pos in range(ntok):
+        nxt = next_window_start(pos, ws, n_ctx, n_ctx // 4)
+        starts += nxt != ws
+        ws = nxt
+    res = {"workload": workload, "bytes": nbytes, "symbols": int(sym.size),
+           "byte_escapes": int(sym.size - ntok), "n_ctx": n_ctx, "overlap": n_ctx // 4, "windows": starts,
+           "file_bytes": len(out), "compress_s": round(t_c, 3), "decompress_s": round(t_d, 3),
+           "compress_bytes_per_s": round(nbytes / t_c, 1), "decompress_bytes_per_s": round(nbytes / t_d, 1),
+           "roundtrip": back == data, "canonical_check": "decompress re-encodes and compares",
+           "data": "seeded order-3 Markov text (printable ASCII + newline, Zipf word lengths)"}
+    if cpu_bytes > 0:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import detref
+
+        detref.set_threads(threads)
+        detref.set_simd(True)
+        tokens, types = synth.vocabulary(lm.model.vocab)
+        _, t2b = detref.byte_fallback_tables(tokens, [1 if ty in (1, 4, 6) else 0 for ty in types])
+        k = min(cpu_bytes, nbytes)
+        t = time.perf_counter()
+        _, got = detref.codec_decode(detref.Model(gguf), t2b, out[56:], k, n_ctx, n_ctx // 4, True)
+        res["cpu_decode_prefix"] = {"bytes": k, "ok": got == data[:k],
+                                    "s": round(time.perf_counter() - t, 2), "threads": threads}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -110,6 +158,10 @@ def main() -> int:
     ap.add_argument("--decode-positions", type=int, default=64)
     ap.add_argument("--decode-workload", default="qwen05",
                     help="model of the decode leg (qwen05: Q8_0 with a 145 MB output projection)")
+    ap.add_argument("--codec-bytes", type=int, default=8192,
+                    help="prefix of the 1 MiB Markov stream compressed + decompressed (0: skip)")
+    ap.add_argument("--codec-cpu-bytes", type=int, default=96,
+                    help="bytes of the device payload the oracle decodes on the host")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain copy of this many MiB (counter calibration) and exit")
     ap.add_argument("--cpu-threads", type=int, default=0)
@@ -248,19 +300,24 @@ def main() -> int:
     log(f"[bench] parity vs oracle on {check_n} positions: {parity}; deterministic: {deterministic}")
 
     decode = None
-    if args.decode_positions > 0:
-        if args.decode_workload == w.name:
-            dmodel, dtoks = model, toks
-        else:
-            dw = synth.WORKLOADS[args.decode_workload]
-            dmodel, dtoks = F32Llama.from_gguf(synth.build_model(dw)), synth.tokens(dw)
-        decode = decode_leg(dmodel, dtoks, args.decode_positions, args.decode_workload)
-        del dmodel
-        log(f"[bench] decode {decode['tokens_per_s']} tok/s, GEMV {decode['gemv_all']['achieved']} GB/s")
+    codec = None
+    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    if args.decode_positions > 0 or args.codec_bytes > 0:
+        dw = synth.WORKLOADS[args.decode_workload]
+        ddata = data if dw.name == w.name else synth.build_model(dw)
+        if args.decode_positions > 0:
+            dmodel = model if dw.name == w.name else F32Llama.from_gguf(ddata)
+            decode = decode_leg(dmodel, synth.tokens(dw), args.decode_positions, dw.name)
+            del dmodel
+            log(f"[bench] decode {decode['tokens_per_s']} tok/s, GEMV {decode['gemv_all']['achieved']} GB/s")
+        if args.codec_bytes > 0:
+            codec = codec_leg(ddata, dw.name, args.codec_bytes, args.codec_cpu_bytes, threads)
+            log(f"[bench] codec {codec['bytes']} B: compress {codec['compress_bytes_per_s']} B/s, "
+                f"decompress {codec['decompress_bytes_per_s']} B/s, roundtrip {codec['roundtrip']}")
+        del ddata
 
     cpu = None
     if not args.no_cpu_baseline:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         detref.set_threads(threads)
         detref.set_simd(True)
         k = args.cpu_tokens
@@ -296,9 +353,11 @@ def main() -> int:
         "deterministic": deterministic,
         "kernels": kernels,
         "decode": decode,
+        "codec": codec,
     }
     print(json.dumps(line), flush=True)
-    return 0 if parity and deterministic else 1
+    codec_ok = codec is None or (codec["roundtrip"] and codec.get("cpu_decode_prefix", {"ok": True})["ok"])
+    return 0 if parity and deterministic and codec_ok else 1
 
 
 if __name__ == "__main__":
