@@ -86,7 +86,7 @@ def decode_leg(model, toks, positions: int, workload: str) -> dict:
         prof = s.profile()
     gemv = {}
     for k, v in prof.items():
-        if (k.startswith("gemm_") or k.startswith("lm_head_")) and v["total_ms"] > 0:
+        if (k.startswith("gemm_") or k.startswith("gemv_") or k.startswith("lm_head_")) and v["total_ms"] > 0:
             gbs = v["bytes"] / (v["total_ms"] * 1e-3) / 1e9
             gemv[k] = {"achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": round(gbs / HBM_PEAK_GBS, 4),

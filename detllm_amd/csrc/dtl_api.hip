@@ -742,52 +742,132 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev) {
   // of one group share them), and its multiply-accumulates.
   double kv_rows = 0.0;
   for (int t = 0; t < T; t++) kv_rows += (double)(pos0 + t + 1);
+  // Decode shapes with Q8_0 / Q4_0 weights fold the rmsnorm and the
+  // activation quantisation into the GEMV launches (each workgroup forms
+  // the Q8A activations it needs), q/k/v share one launch, and gate/up
+  // finish as swiglu in theirs.
+  const bool fuse = T <= kGemvMaxT && !env_flag("DETLLM_NO_FUSED_DECODE");
+  auto fused = [&](std::initializer_list<const DevMat*> ms, bool pair, std::initializer_list<float*> outs,
+                   std::initializer_list<const float*> biases, std::initializer_list<int> epis,
+                   const float* x, const float* norm_w, const char* cls) {
+    const DevMat* mv[3];
+    float* ov[3];
+    const float* bv[3];
+    int ev[3];
+    int nm = 0;
+    double bytes = 0.0, macs = 0.0;
+    for (const DevMat* mm : ms) {
+      mv[nm++] = mm;
+      bytes += (double)mm->rows * mm->cols * weight_bytes_per_elem(mm->type);
+      macs += (double)mm->rows * mm->cols * T;
+    }
+    int i = 0;
+    for (float* o : outs) ov[i++] = o;
+    i = 0;
+    for (const float* b : biases) bv[i++] = b;
+    i = 0;
+    for (int e : epis) ev[i++] = e;
+    const int rows_out = pair ? mv[0]->rows : (int)(macs / T / mv[0]->cols);
+    bytes += (double)T * mv[0]->cols * 4.0 + (double)T * rows_out * 4.0;
+    FusedIn in{x, norm_w, c.eps};
+    P.timed(st, cls, bytes, macs,
+            [&] { (void)launch_gemv_fused(mv, nm, pair, ov, bv, ev, in, T, s->err, st); });
+  };
+  auto fits = [&](std::initializer_list<const DevMat*> ms, bool pair, bool norm) {
+    const DevMat* mv[3];
+    int nm = 0;
+    for (const DevMat* mm : ms) mv[nm++] = mm;
+    return fuse && gemv_fused_fits(mv, nm, pair, norm, T);
+  };
   for (size_t l = 0; l < c.block_count; l++) {
     const Layer& L = m->layers[l];
-    DevAct a = rms(L.attn_norm, {&L.wq, &L.wk, &L.wv});
-    if (L.wq.type == GGML_Q4_K && L.wk.type == GGML_Q4_K && L.wq.w32 && L.wk.w32 && T >= 16 &&
-        (L.bq != nullptr) == (L.bk != nullptr)) {
-      // wq and wk share the input: one launch over their concatenated rows.
-      double bytes = (double)(L.wq.rows + L.wk.rows) * L.wq.cols * weight_bytes_per_elem(GGML_Q4_K) +
-                     (double)T * L.wq.cols * (1.0 + 4.0 / 32) + (double)T * (L.wq.rows + L.wk.rows) * 4.0;
-      P.timed(st, "gemm_q4_k_qk", bytes, (double)(L.wq.rows + L.wk.rows) * L.wq.cols * T, [&] {
-        launch_gemm_cat_q4k(L.wq, L.wk, a, T, s->q, s->k, L.bq, L.bk, L.bq ? EPI_BIAS : EPI_STORE,
-                            s->err, st);
-      });
+    const int e_q = L.bq ? EPI_BIAS : EPI_STORE, e_k = L.bk ? EPI_BIAS : EPI_STORE;
+    const int e_v = L.bv ? EPI_BIAS : EPI_STORE;
+    DevAct a{};
+    if (fits({&L.wq, &L.wk, &L.wv}, false, true)) {
+      fused({&L.wq, &L.wk, &L.wv}, false, {s->q, s->k, s->v}, {L.bq, L.bk, L.bv}, {e_q, e_k, e_v},
+            s->x, L.attn_norm, "gemv_fused_qkv");
+    } else if (fits({&L.wq}, false, true) && fits({&L.wk}, false, true) &&
+               fits({&L.wv}, false, true)) {
+      fused({&L.wq}, false, {s->q}, {L.bq}, {e_q}, s->x, L.attn_norm, "gemv_fused_qkv");
+      fused({&L.wk}, false, {s->k}, {L.bk}, {e_k}, s->x, L.attn_norm, "gemv_fused_qkv");
+      fused({&L.wv}, false, {s->v}, {L.bv}, {e_v}, s->x, L.attn_norm, "gemv_fused_qkv");
     } else {
-      gemm(L.wq, a, s->q, L.bq, L.bq ? EPI_BIAS : EPI_STORE, nullptr);
-      gemm(L.wk, a, s->k, L.bk, L.bk ? EPI_BIAS : EPI_STORE, nullptr);
+      a = rms(L.attn_norm, {&L.wq, &L.wk, &L.wv});
+      if (L.wq.type == GGML_Q4_K && L.wk.type == GGML_Q4_K && L.wq.w32 && L.wk.w32 && T >= 16 &&
+          (L.bq != nullptr) == (L.bk != nullptr)) {
+        // wq and wk share the input: one launch over their concatenated rows.
+        double bytes = (double)(L.wq.rows + L.wk.rows) * L.wq.cols * weight_bytes_per_elem(GGML_Q4_K) +
+                       (double)T * L.wq.cols * (1.0 + 4.0 / 32) + (double)T * (L.wq.rows + L.wk.rows) * 4.0;
+        P.timed(st, "gemm_q4_k_qk", bytes, (double)(L.wq.rows + L.wk.rows) * L.wq.cols * T, [&] {
+          launch_gemm_cat_q4k(L.wq, L.wk, a, T, s->q, s->k, L.bq, L.bk, L.bq ? EPI_BIAS : EPI_STORE,
+                              s->err, st);
+        });
+      } else {
+        gemm(L.wq, a, s->q, L.bq, L.bq ? EPI_BIAS : EPI_STORE, nullptr);
+        gemm(L.wk, a, s->k, L.bk, L.bk ? EPI_BIAS : EPI_STORE, nullptr);
+      }
+      gemm(L.wv, a, s->v, L.bv, L.bv ? EPI_BIAS : EPI_STORE, nullptr);
     }
-    gemm(L.wv, a, s->v, L.bv, L.bv ? EPI_BIAS : EPI_STORE, nullptr);
-    P.timed(st, "rope_store", (double)T * (H + 3 * KV) * hd * 8.0, 0.0, [&] {
-      launch_rope_store(s->q, s->k, s->v, s->rope_cos, s->rope_sin, T, (int)pos0, H, KV, hd,
-                        (int)c.rope_dim, c.split_half, s->kc, s->vc, (int)l, (int)s->n_ctx,
-                        pos_dev, s->err, st);
-    });
-    P.timed(st, "attention", kv_rows * KV * hd * 8.0 + (double)T * H * hd * 8.0,
-            kv_rows * H * hd * 2.0, [&] {
-              launch_attention(s->q, s->kc, s->vc, (int)l, T, (int)pos0, H, KV, hd, (int)s->n_ctx,
-                               c.attention_scale, s->scores, s->attn, pos_dev, s->err, st);
-            });
-    a = prepare_input(s, s->attn, T, H * hd, {&L.wo});
-    gemm(L.wo, a, s->x, nullptr, EPI_RESIDUAL, nullptr);
-    a = rms(L.ffn_norm, {&L.gate, &L.up});
-    if (T >= 16 && L.gate.type == GGML_Q4_K && L.up.type == GGML_Q4_K &&
-        L.gate.rows == L.up.rows && L.gate.cols == L.up.cols) {
-      // gate, up and swiglu in one pass: both chains of a row share one wave.
-      double bytes = 2.0 * L.gate.rows * L.gate.cols * weight_bytes_per_elem(GGML_Q4_K) +
-                     (double)T * d * (1.0 + 4.0 / 32) + (double)T * ff * 4.0;
-      P.timed(st, "gemm_q4_k_gate_up", bytes, 2.0 * L.gate.rows * L.gate.cols * T, [&] {
-        launch_gemm_pair_swiglu_q4k(L.gate, L.up, a, T, nullptr, nullptr, s->ffo, s->err, st);
-      });
+    if (attention_dec_applies(hd, T, (int)pos0, (int)s->n_ctx, pos_dev != nullptr)) {
+      // RoPE and the cache store happen inside the decode attention.
+      const RopeIn R{s->k, s->v, s->rope_cos, s->rope_sin, (int)c.rope_dim, c.split_half ? 1 : 0,
+                     s->kc, s->vc};
+      P.timed(st, "attention", kv_rows * KV * hd * 8.0 + (double)T * (H + 3 * KV) * hd * 4.0,
+              kv_rows * H * hd * 2.0, [&] {
+                launch_attention_dec(s->q, R, (int)l, T, (int)pos0, H, KV, (int)s->n_ctx,
+                                     c.attention_scale, s->attn, pos_dev, s->err, st);
+              });
     } else {
-      gemm(L.gate, a, s->g, nullptr, EPI_STORE, nullptr);
-      gemm(L.up, a, s->u, nullptr, EPI_STORE, nullptr);
+      P.timed(st, "rope_store", (double)T * (H + 3 * KV) * hd * 8.0, 0.0, [&] {
+        launch_rope_store(s->q, s->k, s->v, s->rope_cos, s->rope_sin, T, (int)pos0, H, KV, hd,
+                          (int)c.rope_dim, c.split_half, s->kc, s->vc, (int)l, (int)s->n_ctx,
+                          pos_dev, s->err, st);
+      });
+      P.timed(st, "attention", kv_rows * KV * hd * 8.0 + (double)T * H * hd * 8.0,
+              kv_rows * H * hd * 2.0, [&] {
+                launch_attention(s->q, s->kc, s->vc, (int)l, T, (int)pos0, H, KV, hd,
+                                 (int)s->n_ctx, c.attention_scale, s->scores, s->attn, pos_dev,
+                                 s->err, st);
+              });
+    }
+    if (fits({&L.wo}, false, false)) {
+      fused({&L.wo}, false, {s->x}, {nullptr}, {EPI_RESIDUAL}, s->attn, nullptr, "gemv_fused_o");
+    } else {
+      a = prepare_input(s, s->attn, T, H * hd, {&L.wo});
+      gemm(L.wo, a, s->x, nullptr, EPI_RESIDUAL, nullptr);
+    }
+    if (fits({&L.gate, &L.up}, true, true)) {
+      fused({&L.gate, &L.up}, true, {s->ffo}, {nullptr, nullptr}, {EPI_STORE, EPI_STORE}, s->x,
+            L.ffn_norm, "gemv_fused_gate_up");
+    } else if (fits({&L.gate}, false, true) && fits({&L.up}, false, true)) {
+      fused({&L.gate}, false, {s->g}, {nullptr}, {EPI_STORE}, s->x, L.ffn_norm, "gemv_fused_gate_up");
+      fused({&L.up}, false, {s->u}, {nullptr}, {EPI_STORE}, s->x, L.ffn_norm, "gemv_fused_gate_up");
       P.timed(st, "swiglu", (double)T * ff * 12.0, 0.0,
               [&] { launch_swiglu(s->g, s->u, T * ff, s->ffo, s->err, st); });
+    } else {
+      a = rms(L.ffn_norm, {&L.gate, &L.up});
+      if (T >= 16 && L.gate.type == GGML_Q4_K && L.up.type == GGML_Q4_K &&
+          L.gate.rows == L.up.rows && L.gate.cols == L.up.cols) {
+        // gate, up and swiglu in one pass: both chains of a row share one wave.
+        double bytes = 2.0 * L.gate.rows * L.gate.cols * weight_bytes_per_elem(GGML_Q4_K) +
+                       (double)T * d * (1.0 + 4.0 / 32) + (double)T * ff * 4.0;
+        P.timed(st, "gemm_q4_k_gate_up", bytes, 2.0 * L.gate.rows * L.gate.cols * T, [&] {
+          launch_gemm_pair_swiglu_q4k(L.gate, L.up, a, T, nullptr, nullptr, s->ffo, s->err, st);
+        });
+      } else {
+        gemm(L.gate, a, s->g, nullptr, EPI_STORE, nullptr);
+        gemm(L.up, a, s->u, nullptr, EPI_STORE, nullptr);
+        P.timed(st, "swiglu", (double)T * ff * 12.0, 0.0,
+                [&] { launch_swiglu(s->g, s->u, T * ff, s->ffo, s->err, st); });
+      }
     }
-    a = prepare_input(s, s->ffo, T, ff, {&L.down});
-    gemm(L.down, a, s->x, nullptr, EPI_RESIDUAL, nullptr);
+    if (fits({&L.down}, false, false)) {
+      fused({&L.down}, false, {s->x}, {nullptr}, {EPI_RESIDUAL}, s->ffo, nullptr, "gemv_fused_down");
+    } else {
+      a = prepare_input(s, s->ffo, T, ff, {&L.down});
+      gemm(L.down, a, s->x, nullptr, EPI_RESIDUAL, nullptr);
+    }
   }
   DevAct a = rms(m->out_norm, {&m->out});
   gemm(m->out, a, s->logits, nullptr, EPI_STORE, lm_head_class(m->out.type));

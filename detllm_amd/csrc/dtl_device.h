@@ -85,6 +85,31 @@ struct DevAct {
 
 enum GemmEpilogue : int { EPI_STORE = 0, EPI_BIAS = 1, EPI_RESIDUAL = 2 };
 
+// Positions up to which the decode GEMVs (one weight pass per position)
+// replace the chunked-encode GEMMs.
+constexpr int kGemvMaxT = 8;
+
+// Matrices of one fused decode GEMV launch (same type, cols and input).
+struct FusedMats {
+  const void* w[3];
+  const uint16_t* d16[3];
+  float* out[3];
+  const float* bias[3];
+  int epi[3];
+  int rows[3];
+  int row_end[3];  // prefix sums of rows (concatenated launches)
+  int total_rows;
+  int cols, nb;
+};
+
+// Input of a fused decode GEMV: f32 rows [T][cols], normalised first when
+// norm_w is set.
+struct FusedIn {
+  const float* x;
+  const float* norm_w;
+  float eps;
+};
+
 // ---- launchers (dtl_kernels.hip) -------------------------------------------
 void launch_embed(const DevMat& E, const uint32_t* tokens, int T, float* x, int* err,
                   hipStream_t s);
@@ -104,6 +129,14 @@ void launch_gemm(const DevMat& W, const DevAct& A, int T, float* out, const floa
 // shape or type has no GEMV kernel.
 bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const float* bias, int epi,
                  int* err, hipStream_t s);
+// Q8_0 / Q4_0 decode GEMV with its activation quantisation (and rmsnorm when
+// in.norm_w is set) fused in: nm matrices over concatenated rows, or gate and
+// up (nm == 2, pair_swiglu) whose dots finish as swiglu into outs[0].
+// Returns false when the shapes do not fit (the caller uses separate launches).
+bool gemv_fused_fits(const DevMat* const* mats, int nm, bool pair_swiglu, bool norm, int T);
+bool launch_gemv_fused(const DevMat* const* mats, int nm, bool pair_swiglu, float* const* outs,
+                       const float* const* biases, const int* epis, const FusedIn& in, int T,
+                       int* err, hipStream_t s);
 // Token-parallel GEMMs (dtl_gemm.hip) for chunks of positions.
 bool gemm_tok_supported(const DevMat& W);
 void launch_gemm_tok(const DevMat& W, const DevAct& A, int T, float* out, const float* bias,
@@ -129,6 +162,24 @@ void launch_rope_store(float* q, float* k, const float* v, const float* rope_cos
                        const float* rope_sin, int T, int pos0, int H, int KV, int hd, int rope_dim,
                        int split_half, float* kc, float* vc, int layer, int n_ctx,
                        const int* pos_dev, int* err, hipStream_t s);
+// The chunk's raw keys / values and RoPE tables for the decode attention,
+// which applies RoPE and stores the chunk's cache rows itself.
+struct RopeIn {
+  const float* k;  // [T][KV][hd] keys before RoPE
+  const float* v;  // [T][KV][hd] values
+  const float* rc;  // [n_ctx][rope_dim / 2] cos / sin tables
+  const float* rs;
+  int rope_dim;
+  int split_half;
+  float* kc;  // [layer][KV][n_ctx][hd] caches
+  float* vc;
+};
+// Whether launch_attention_dec takes this shape (hd 64, at most four
+// positions, the score row within LDS).
+bool attention_dec_applies(int hd, int T, int pos0, int n_ctx, bool pos_in_device);
+void launch_attention_dec(const float* q, const RopeIn& R, int layer, int T, int pos0, int H,
+                          int KV, int n_ctx, float scale, float* out, const int* pos_dev,
+                          int* err, hipStream_t s);
 // Whether launch_attention accepts pos_dev for this shape.
 bool attention_pos_dev_supported(int hd, int T, int n_ctx);
 void launch_attention(const float* q, const float* kc, const float* vc, int layer, int T, int pos0,

@@ -21,6 +21,7 @@
 
 #include "dtl_device.h"
 #include "dtl_numerics.h"
+#include "dtl_quant.h"
 
 namespace dtl {
 
@@ -57,7 +58,6 @@ __device__ __forceinline__ float chain_sum(const float* v, int n) {
   for (; b < n; b++) s += v[b];
   return s;
 }
-
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -394,6 +394,291 @@ __global__ void __launch_bounds__(64) k_gemv_q4k(const float* __restrict__ w32, 
 }
 
 // ---------------------------------------------------------------------------
+// Fused decode GEMV for Q8_0 / Q4_0 weights.  Every workgroup first forms
+// the Q8A activations of its position in LDS from the f32 input: after
+// rmsnorm (det-model lib.rs:2053-2073: ss = sum_squares_f32_ref(x), r =
+// 1 / sqrt(ss / n + eps), y = (x * r) * w) when a norm weight is given,
+// else straight from x (the re-quantisation of wo / down inputs,
+// lib.rs:1310-1316, 1366-1372).  The weight loads of the first chunk
+// column are issued before that prologue.  The matrices of one launch share
+// the input: either concatenated rows (q, k, v: up to three outputs with
+// their own bias / epilogue) or two matrices over the same rows whose dots
+// finish as swiglu (gate, up: out = silu(g) * u, lib.rs:2420-2434).  Every
+// value is computed exactly as by the separate launches.
+namespace {
+
+// Float4s per thread (norm pass) or 256-element spans per wave (plain
+// pass) loaded at once: inputs of up to 4096 elements take one round trip.
+constexpr int kProBatch = 4;
+
+__device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols, bool norm,
+                                             float* xs, float* ws, float* sq, int cs,
+                                             int8_t* qa_s, float* da_s, float* misc) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const float* x = in.x + (size_t)t * cols;
+  const QuantOut q{qa_s, da_s, nullptr, nullptr, nullptr};
+  bool bad = false;
+  if (norm) {
+    for (int base = 0; base < cols; base += 1024 * kProBatch) {
+      float4 xv[kProBatch], wv[kProBatch];
+#pragma unroll
+      for (int k = 0; k < kProBatch; k++) {
+        const int i = base + 1024 * k + 4 * tid;
+        xv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        wv[k] = xv[k];
+        if (i < cols) {
+          xv[k] = *reinterpret_cast<const float4*>(x + i);
+          wv[k] = *reinterpret_cast<const float4*>(in.norm_w + i);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kProBatch; k++) {
+        const int i = base + 1024 * k + 4 * tid;
+        if (i < cols) {
+          const float xe[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
+          const float we[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
+          *reinterpret_cast<float4*>(xs + i) = xv[k];
+          *reinterpret_cast<float4*>(ws + i) = wv[k];
+#pragma unroll
+          for (int c = 0; c < 4; c++) {
+            bad |= !finite(xe[c]) | !finite(we[c]);
+            sq[((i & 7) + c) * cs + (i >> 3)] = xe[c] * xe[c];
+          }
+        }
+      }
+    }
+    __syncthreads();
+    if (tid < 8) {
+      const int cnt = (cols - tid + 7) / 8;
+      const float* my = sq + tid * cs;
+      float acc = 0.0f;
+      int k = 0;
+      for (; k + 8 <= cnt; k += 8) {
+        const float4 f0 = *reinterpret_cast<const float4*>(my + k);
+        const float4 f1 = *reinterpret_cast<const float4*>(my + k + 4);
+        acc += f0.x; acc += f0.y; acc += f0.z; acc += f0.w;
+        acc += f1.x; acc += f1.y; acc += f1.z; acc += f1.w;
+      }
+      for (; k < cnt; k++) acc += my[k];
+      misc[tid] = acc;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      const float ss = finish_8lane(misc);
+      const float m = ss / (float)cols;
+      const float r = 1.0f / sqrtf(m + in.eps);
+      if (!finite(r)) bad = true;
+      misc[8] = r;
+    }
+    __syncthreads();
+    const float r = misc[8];
+    for (int span = wave; span * 256 < cols; span += 4) {
+      const int e = span * 256 + 4 * lane;
+      const bool inb = e < cols;
+      float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (inb) {
+        const float4 xf = *reinterpret_cast<const float4*>(xs + e);
+        const float4 wf = *reinterpret_cast<const float4*>(ws + e);
+        v[0] = (xf.x * r) * wf.x;
+        v[1] = (xf.y * r) * wf.y;
+        v[2] = (xf.z * r) * wf.z;
+        v[3] = (xf.w * r) * wf.w;
+#pragma unroll
+        for (int c = 0; c < 4; c++) bad |= !finite(v[c]);
+      }
+      quantize_span(v, inb, (size_t)span * 256, true, false, q);
+    }
+  } else {
+    for (int s0 = wave; s0 * 256 < cols; s0 += 4 * kProBatch) {
+      float4 f[kProBatch];
+#pragma unroll
+      for (int k = 0; k < kProBatch; k++) {
+        const int e = (s0 + 4 * k) * 256 + 4 * lane;
+        f[k] = e < cols ? *reinterpret_cast<const float4*>(x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int k = 0; k < kProBatch; k++) {
+        const int span = s0 + 4 * k;
+        if (span * 256 < cols) {
+          const int e = span * 256 + 4 * lane;
+          const bool inb = e < cols;
+          float v[4] = {f[k].x, f[k].y, f[k].z, f[k].w};
+          if (inb) bad |= !finite(v[0]) | !finite(v[1]) | !finite(v[2]) | !finite(v[3]);
+          quantize_span(v, inb, (size_t)span * 256, true, false, q);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  return bad;
+}
+
+}  // namespace
+
+// LDS bytes of k_gemv_q8f: block terms, the Q8A activations and, with a
+// norm, its scratch (the row, the weights, the chain-major squares).
+size_t gemv_fused_smem(int nr, int cols, int nb, bool norm) {
+  const size_t cs = (size_t)((((cols + 7) / 8) + 3) & ~3);
+  size_t b = (size_t)4 * nr * nb * 4 + (size_t)((cols + 15) & ~15) + (size_t)((nb + 3) & ~3) * 4;
+  if (norm) b += 2 * (size_t)((cols + 3) & ~3) * 4 + 8 * cs * 4 + 16 * 4;
+  return b;
+}
+
+template <int TYPE, int R, bool PAIR>
+__global__ void __launch_bounds__(256) k_gemv_q8f(FusedMats M, FusedIn in, int* err) {
+  constexpr int NR = PAIR ? 2 * R : R;
+  extern __shared__ __align__(16) float lds[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = blockIdx.y;
+  const int cols = M.cols, nb = M.nb;
+  const int cs = (((cols + 7) / 8) + 3) & ~3;
+  float* vb = lds;
+  int8_t* qa_s = reinterpret_cast<int8_t*>(lds + 4 * NR * nb);
+  float* da_s = reinterpret_cast<float*>(qa_s + ((cols + 15) & ~15));
+  float* xs = da_s + ((nb + 3) & ~3);
+  float* ws = xs + ((cols + 3) & ~3);
+  float* sq = ws + ((cols + 3) & ~3);
+  float* misc = sq + 8 * cs;
+  float* mine = vb + (size_t)wave * NR * nb;
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+  // Slot r: (matrix, row) of the r-th dot of this wave.  Matrix choice is
+  // wave-uniform, so the selects below stay scalar.
+  const void* wp[NR];
+  const uint16_t* dp[NR];
+  int srow[NR];
+  bool sval[NR];
+#pragma unroll
+  for (int r = 0; r < NR; r++) {
+    int mi, row;
+    if (PAIR) {
+      mi = r < R ? 0 : 1;
+      row = row0 + (r < R ? r : r - R);
+      sval[r] = row < M.rows[0];
+    } else {
+      const int gr = row0 + r;
+      mi = gr < M.row_end[0] ? 0 : (gr < M.row_end[1] ? 1 : 2);
+      row = gr - (mi == 0 ? 0 : (mi == 1 ? M.row_end[0] : M.row_end[1]));
+      sval[r] = gr < M.total_rows;
+    }
+    if (!sval[r]) {
+      mi = 0;
+      row = 0;
+    }
+    wp[r] = mi == 0 ? M.w[0] : (mi == 1 ? M.w[1] : M.w[2]);
+    dp[r] = mi == 0 ? M.d16[0] : (mi == 1 ? M.d16[1] : M.d16[2]);
+    srow[r] = row;
+  }
+  const int nchunk = TYPE == kGgmlQ8_0 ? 2 * nb : nb;
+  bool bad = false;
+  // One chunk column of 64 lanes per pass (batching several passes' loads
+  // measured slower: the extra registers cost more than the round trips).
+  constexpr int NI = 1;
+  for (int cb = 0; cb < nchunk; cb += 64 * NI) {
+    uint4 w4[NI][NR];
+    uint16_t dsc[NI][NR];
+#pragma unroll
+    for (int ii = 0; ii < NI; ii++) {
+      const int c = cb + 64 * ii + lane;
+      const bool cv = c < nchunk;
+      const int b = TYPE == kGgmlQ8_0 ? c >> 1 : c;
+#pragma unroll
+      for (int r = 0; r < NR; r++) {
+        w4[ii][r] = make_uint4(0, 0, 0, 0);
+        dsc[ii][r] = 0;
+        if (cv) {
+          if (TYPE == kGgmlQ8_0)
+            w4[ii][r] = *(const uint4*)((const int8_t*)wp[r] + (size_t)srow[r] * cols + (size_t)c * 16);
+          else
+            w4[ii][r] = *(const uint4*)((const uint8_t*)wp[r] + ((size_t)srow[r] * nb + c) * 16);
+          dsc[ii][r] = dp[r][(size_t)srow[r] * nb + b];
+        }
+      }
+    }
+    if (cb == 0)
+      bad |= q8a_prologue(in, t, cols, in.norm_w != nullptr, xs, ws, sq, cs, qa_s, da_s, misc);
+#pragma unroll
+    for (int ii = 0; ii < NI; ii++) {
+      const int c = cb + 64 * ii + lane;
+      const bool cv = c < nchunk;
+      const int b = TYPE == kGgmlQ8_0 ? c >> 1 : c;
+      uint4 a0 = make_uint4(0, 0, 0, 0), a1 = make_uint4(0, 0, 0, 0);
+      float dact = 0.0f;
+      if (cv) {
+        if (TYPE == kGgmlQ8_0) {
+          a0 = *(const uint4*)(qa_s + (size_t)c * 16);
+        } else {
+          a0 = *(const uint4*)(qa_s + (size_t)c * 32);
+          a1 = *(const uint4*)(qa_s + (size_t)c * 32 + 16);
+        }
+        dact = da_s[b];
+      }
+      int asum = 0;
+      if (TYPE != kGgmlQ8_0) {
+        const uint32_t ones = 0x01010101u;
+        asum = dot4(ones, a0.x, asum);
+        asum = dot4(ones, a0.y, asum);
+        asum = dot4(ones, a0.z, asum);
+        asum = dot4(ones, a0.w, asum);
+        asum = dot4(ones, a1.x, asum);
+        asum = dot4(ones, a1.y, asum);
+        asum = dot4(ones, a1.z, asum);
+        asum = dot4(ones, a1.w, asum);
+      }
+#pragma unroll
+      for (int r = 0; r < NR; r++) {
+        int isum = 0;
+        if (TYPE == kGgmlQ8_0) {
+          isum = dot4(w4[ii][r].x, a0.x, isum);
+          isum = dot4(w4[ii][r].y, a0.y, isum);
+          isum = dot4(w4[ii][r].z, a0.z, isum);
+          isum = dot4(w4[ii][r].w, a0.w, isum);
+          isum += __shfl_xor(isum, 1);
+        } else {
+          const uint32_t m = 0x0f0f0f0fu;
+          isum = dot4(w4[ii][r].x & m, a0.x, isum);
+          isum = dot4(w4[ii][r].y & m, a0.y, isum);
+          isum = dot4(w4[ii][r].z & m, a0.z, isum);
+          isum = dot4(w4[ii][r].w & m, a0.w, isum);
+          isum = dot4((w4[ii][r].x >> 4) & m, a1.x, isum);
+          isum = dot4((w4[ii][r].y >> 4) & m, a1.y, isum);
+          isum = dot4((w4[ii][r].z >> 4) & m, a1.z, isum);
+          isum = dot4((w4[ii][r].w >> 4) & m, a1.w, isum);
+          isum -= 8 * asum;
+        }
+        const bool writer = TYPE == kGgmlQ8_0 ? cv && !(c & 1) : cv;
+        if (writer) mine[r * nb + b] = (f16_to_f32(dsc[ii][r]) * dact) * (float)isum;
+      }
+    }
+  }
+  __syncthreads();
+  if (lane < R) {
+    if (PAIR) {
+      const int row = row0 + lane;
+      if (row < M.rows[0]) {
+        const float g = chain_sum(mine + lane * nb, nb);
+        const float u = chain_sum(mine + (R + lane) * nb, nb);
+        const float v = silu_det(g) * u;
+        if (!finite(g) || !finite(u) || !finite(v)) bad = true;
+        M.out[0][(size_t)t * M.rows[0] + row] = v;
+      }
+    } else {
+      const int gr = row0 + lane;
+      if (gr < M.total_rows) {
+        const int mi = gr < M.row_end[0] ? 0 : (gr < M.row_end[1] ? 1 : 2);
+        const int row = gr - (mi == 0 ? 0 : (mi == 1 ? M.row_end[0] : M.row_end[1]));
+        float* out = mi == 0 ? M.out[0] : (mi == 1 ? M.out[1] : M.out[2]);
+        const float* bias = mi == 0 ? M.bias[0] : (mi == 1 ? M.bias[1] : M.bias[2]);
+        const int epi = mi == 0 ? M.epi[0] : (mi == 1 ? M.epi[1] : M.epi[2]);
+        const int rows = mi == 0 ? M.rows[0] : (mi == 1 ? M.rows[1] : M.rows[2]);
+        const float v = chain_sum(mine + lane * nb, nb);
+        if (!epilogue(v, out, (size_t)t * rows + row, bias, row, epi)) bad = true;
+      }
+    }
+  }
+  if (bad) flag(err, ERRBIT_NON_FINITE);
+}
+
+// ---------------------------------------------------------------------------
 namespace {
 template <int TYPE>
 void launch_q8(const DevMat& W, const DevAct& A, int T, float* out, const float* bias, int epi,
@@ -455,6 +740,79 @@ bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const floa
     return true;
   }
   return false;
+}
+
+namespace {
+template <int TYPE, bool PAIR>
+void launch_q8f(const FusedMats& M, const FusedIn& in, int T, int R, bool norm, int* err,
+                hipStream_t s) {
+  const int nr = PAIR ? 2 * R : R;
+  const int rows = PAIR ? M.rows[0] : M.total_rows;
+  dim3 grid((rows + 4 * R - 1) / (4 * R), T);
+  const size_t smem = gemv_fused_smem(nr, M.cols, M.nb, norm);
+  if (R == 4)
+    launch_kernel((k_gemv_q8f<TYPE, 4, PAIR>), grid, dim3(256), smem, s, M, in, err);
+  else if (R == 2)
+    launch_kernel((k_gemv_q8f<TYPE, 2, PAIR>), grid, dim3(256), smem, s, M, in, err);
+  else
+    launch_kernel((k_gemv_q8f<TYPE, 1, PAIR>), grid, dim3(256), smem, s, M, in, err);
+}
+}  // namespace
+
+bool gemv_fused_fits(const DevMat* const* mats, int nm, bool pair_swiglu, bool norm, int T) {
+  if (nm < 1 || nm > 3 || (pair_swiglu && nm != 2) || T < 1 || T > kGemvMaxT) return false;
+  const DevMat& m0 = *mats[0];
+  if (m0.type != kGgmlQ8_0 && m0.type != kGgmlQ4_0) return false;
+  for (int i = 0; i < nm; i++) {
+    const DevMat& m = *mats[i];
+    if (m.type != m0.type || m.cols != m0.cols || m.nb != m0.nb) return false;
+    if (pair_swiglu && m.rows != m0.rows) return false;
+  }
+  return m0.cols % 32 == 0 && gemv_fused_smem(pair_swiglu ? 2 : 1, m0.cols, m0.nb, norm) <= 64 * 1024;
+}
+
+bool launch_gemv_fused(const DevMat* const* mats, int nm, bool pair_swiglu, float* const* outs,
+                       const float* const* biases, const int* epis, const FusedIn& in, int T,
+                       int* err, hipStream_t s) {
+  const bool norm = in.norm_w != nullptr;
+  if (!gemv_fused_fits(mats, nm, pair_swiglu, norm, T)) return false;
+  const DevMat& m0 = *mats[0];
+  FusedMats M{};
+  int acc = 0;
+  for (int i = 0; i < nm; i++) {
+    const DevMat& m = *mats[i];
+    if (m.type != m0.type || m.cols != m0.cols || m.nb != m0.nb) return false;
+    if (pair_swiglu && m.rows != m0.rows) return false;
+    M.w[i] = m.w;
+    M.d16[i] = m.d16;
+    M.rows[i] = m.rows;
+    acc += m.rows;
+    M.row_end[i] = acc;
+    if (!pair_swiglu) {
+      M.out[i] = outs[i];
+      M.bias[i] = biases[i];
+      M.epi[i] = epis[i];
+    }
+  }
+  for (int i = nm; i < 3; i++) M.row_end[i] = acc;
+  if (pair_swiglu) M.out[0] = outs[0];
+  M.total_rows = acc;
+  M.cols = m0.cols;
+  M.nb = m0.nb;
+  const int rows = pair_swiglu ? m0.rows : acc;
+  // Rows per wave as the unfused kernel chooses them; LDS bounds the rest.
+  int R = rows >= 16384 ? 4 : (rows >= 4096 ? 2 : 1);
+  const int mult = pair_swiglu ? 2 : 1;
+  while (R > 1 && gemv_fused_smem(mult * R, m0.cols, m0.nb, norm) > 64 * 1024) R >>= 1;
+  if (gemv_fused_smem(mult * R, m0.cols, m0.nb, norm) > 64 * 1024) return false;
+  if (m0.type == kGgmlQ8_0) {
+    if (pair_swiglu) launch_q8f<kGgmlQ8_0, true>(M, in, T, R, norm, err, s);
+    else launch_q8f<kGgmlQ8_0, false>(M, in, T, R, norm, err, s);
+  } else {
+    if (pair_swiglu) launch_q8f<kGgmlQ4_0, true>(M, in, T, R, norm, err, s);
+    else launch_q8f<kGgmlQ4_0, false>(M, in, T, R, norm, err, s);
+  }
+  return true;
 }
 
 }  // namespace dtl

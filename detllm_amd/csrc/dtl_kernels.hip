@@ -12,6 +12,7 @@
 #include "dtl_device.h"
 #include "dtl_blocks.h"
 #include "dtl_numerics.h"
+#include "dtl_quant.h"
 
 namespace dtl {
 
@@ -190,96 +191,6 @@ void launch_embed(const DevMat& E, const uint32_t* tokens, int T, float* x, int*
 // block is 8 lanes and a Q8_K block the whole wave; every reduction is a
 // wave shuffle.  Spans are whole Q8A blocks (n % 32 == 0) and, when Q8_K is
 // wanted, whole Q8_K blocks (n % 256 == 0).
-namespace {
-struct QuantOut {
-  int8_t* qa;
-  float* da;
-  float* af;
-  int8_t* qk;
-  float* dk;
-};
-
-// v: the lane's four elements; in: whether they exist; base: element offset
-// of the span (a multiple of 256 within the [T][n] array).
-__device__ __forceinline__ void quantize_span(const float v[4], bool in, size_t base, bool want_q8a,
-                                              bool want_q8k, const QuantOut& q) {
-  const int lane = threadIdx.x & 63;
-  const size_t off = base + 4 * lane;
-  float ax[4];
-#pragma unroll
-  for (int c = 0; c < 4; c++) ax[c] = v[c] < 0.0f ? -v[c] : v[c];
-  if (want_q8a) {
-    // amax over the 32-element block (max is order independent).
-    float amax = fmaxf(fmaxf(ax[0], ax[1]), fmaxf(ax[2], ax[3]));
-#pragma unroll
-    for (int m = 4; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
-    if (in) {
-      int8_t qv[4];
-      float fv[4];
-      float d = amax / 127.0f;
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        if (amax == 0.0f) {
-          qv[c] = 0;
-          fv[c] = 0.0f;
-        } else {
-          float y = v[c] / d;
-          int r = y < 0.0f ? f32_as_i32(y - 0.5f) : f32_as_i32(y + 0.5f);
-          r = r < -127 ? -127 : (r > 127 ? 127 : r);
-          qv[c] = (int8_t)r;
-          fv[c] = d * (float)r;
-        }
-      }
-      uint32_t packed = (uint32_t)(uint8_t)qv[0] | ((uint32_t)(uint8_t)qv[1] << 8) |
-                        ((uint32_t)(uint8_t)qv[2] << 16) | ((uint32_t)(uint8_t)qv[3] << 24);
-      *reinterpret_cast<uint32_t*>(q.qa + off) = packed;
-      *reinterpret_cast<float4*>(q.af + off) = make_float4(fv[0], fv[1], fv[2], fv[3]);
-      if ((lane & 7) == 0) q.da[off / 32] = amax == 0.0f ? 0.0f : d;
-    }
-  }
-  if (want_q8k) {
-    // Signed max: the first element with the strictly largest |x|.  Reduce
-    // (|x|, index, x) taking the larger |x| and, on ties, the smaller index.
-    float bx = -1.0f, bv = 0.0f;
-    int bi = 0;
-#pragma unroll
-    for (int c = 0; c < 4; c++)
-      if (in && ax[c] > bx) {
-        bx = ax[c];
-        bv = v[c];
-        bi = 4 * lane + c;
-      }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      float ox = __shfl_xor(bx, m), ov = __shfl_xor(bv, m);
-      int oi = __shfl_xor(bi, m);
-      if (ox > bx || (ox == bx && oi < bi)) {
-        bx = ox;
-        bi = oi;
-        bv = ov;
-      }
-    }
-    float mx = bx == 0.0f ? 0.0f : bv;
-    if (in) {
-      // Stored class-major inside the 256-block (element e at (e % 8) * 32 + e / 8),
-      // the order the Q6_K kernels consume the eight lane sums in.
-      float iscale = -127.0f / mx;
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        int e = 4 * lane + c;
-        int r = 0;
-        if (mx != 0.0f) {
-          float val = iscale * v[c] + 12582912.0f;
-          r = (int)(f2u(val) & 0x007fffffu) - 0x00400000;
-          if (r > 127) r = 127;
-        }
-        q.qk[base + (e & 7) * 32 + (e >> 3)] = (int8_t)r;
-      }
-      if (lane == 0) q.dk[base / 256] = mx == 0.0f ? 0.0f : 1.0f / iscale;
-    }
-  }
-}
-}  // namespace
 
 // Four waves per workgroup, one 256-element span each.
 __global__ void __launch_bounds__(256) k_quantize(const float* x, int n, int want_q8a,
@@ -487,10 +398,6 @@ __global__ void __launch_bounds__(256) k_gemm_rowlane(DevMat W, DevAct A, int T,
   if (bad || !finite(v)) flag(err, ERRBIT_NON_FINITE);
   out[o] = v;
 }
-
-// Up to this many positions the decode GEMVs (weights streamed once per
-// position) beat the row-lane kernel.
-constexpr int kGemvMaxT = 8;
 
 void launch_gemm(const DevMat& W, const DevAct& A, int T, float* out, const float* bias, int epi,
                  int* err, hipStream_t s) {
@@ -864,62 +771,110 @@ __global__ void __launch_bounds__(1024) k_attention_hd64(const float* q, const f
 }
 
 // Decode shape (a few positions): one workgroup of 1024 threads per (head,
-// position).  All threads compute scores (8-lane dot order) into LDS; a block
-// max, the clamped exps in parallel, the 8-lane Z chains (lanes 0-7), p = e /
-// Z in parallel.  P.V (lib.rs:2390-2420: out[d] = 0; out[d] += p_j * v_j[d]
-// for j ascending) splits into the products, which every thread forms for
-// one float4 of a 64-position V tile and stores dimension-major in LDS, and
-// the 64 serial sums, which wave 0 runs over the stored products (lane =
+// position), with the RoPE and cache store of the chunk folded in.  The
+// workgroup applies RoPE (lib.rs:2011-2051) to its query head and to the
+// chunk's new keys of its KV group in LDS, and the first head of each group
+// stores its position's key and value; cache rows before the chunk come from
+// memory, the chunk's own rows from LDS, so no workgroup reads a row another
+// one writes.  Then: scores (8-lane dot order), a block max, the clamped
+// exps in parallel, the 8-lane Z chains (lanes 0-7), p = e / Z in parallel.
+// P.V (lib.rs:2390-2420: out[d] = 0; out[d] += p_j * v_j[d] for j
+// ascending) splits into the products, which every thread forms for one
+// float4 of a 64-position V tile and stores dimension-major in LDS, and the
+// 64 serial sums, which wave 0 runs over the stored products (lane =
 // dimension, four products per LDS read).  V tiles stream through a ring of
 // kDecDepth registers per thread, so kDecDepth tiles of loads are in flight
 // while wave 0 sums.
-constexpr int kDecThreads = 1024, kDecTile = 64, kDecStride = 68, kDecDepth = 8;
+constexpr int kDecThreads = 1024, kDecTile = 64, kDecStride = 68, kDecDepth = 8, kDecMaxT = 4;
 
-__global__ void __launch_bounds__(kDecThreads) k_attention_dec(const float* q, const float* kc,
-                                                               const float* vc, int layer, int pos0,
-                                                               int H, int KV, int n_ctx, float scale,
-                                                               float* out, const int* pos_dev,
-                                                               int* err) {
+// dot_f32_ref of a 64-element query and key row (global or LDS), 8-lane order.
+__device__ __forceinline__ float dot64_8lane(const float* qs, const float* krow) {
+  const float4* kr = reinterpret_cast<const float4*>(krow);
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int half = 0; half < 2; half++) {
+    float4 kv[8];
+#pragma unroll
+    for (int i4 = 0; i4 < 8; i4++) kv[i4] = kr[8 * half + i4];
+#pragma unroll
+    for (int i4 = 0; i4 < 8; i4++) {
+      const int i = 32 * half + 4 * i4;
+      acc[(i + 0) & 7] += qs[i + 0] * kv[i4].x;
+      acc[(i + 1) & 7] += qs[i + 1] * kv[i4].y;
+      acc[(i + 2) & 7] += qs[i + 2] * kv[i4].z;
+      acc[(i + 3) & 7] += qs[i + 3] * kv[i4].w;
+    }
+  }
+  return finish_8lane(acc);
+}
+
+__global__ void __launch_bounds__(kDecThreads) k_attention_dec(const float* q, RopeIn R, int layer,
+                                                               int pos0, int H, int KV, int n_ctx,
+                                                               float scale, float* out,
+                                                               const int* pos_dev, int* err) {
   extern __shared__ __align__(16) float sc[];  // [len] scores -> exps -> probabilities
   __shared__ __align__(16) float prod[2][64 * kDecStride];  // [dim][position in tile]
   __shared__ __align__(16) float qs[64];
+  __shared__ __align__(16) float kn[kDecMaxT][64];  // the chunk's keys (after RoPE)
+  __shared__ __align__(16) float vn[kDecMaxT][64];  // the chunk's values
   __shared__ float red[kDecThreads / 64];
   __shared__ float zc[8];
   constexpr int hd = 64;
   const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int g = h / (H / KV);
-  const int pos = (pos_dev ? *pos_dev : pos0) + t, len = pos + 1;
-  const float* keys = kc + ((size_t)layer * KV + g) * n_ctx * hd;
-  const float* vals = vc + ((size_t)layer * KV + g) * n_ctx * hd;
+  const int G = H / KV, g = h / G;
+  const int pb = pos_dev ? *pos_dev : pos0;  // first position of the chunk
+  const int pos = pb + t, len = pos + 1;
+  const int half = R.rope_dim / 2;
+  const float* keys = R.kc + ((size_t)layer * KV + g) * n_ctx * hd;
+  const float* vals = R.vc + ((size_t)layer * KV + g) * n_ctx * hd;
   float* o = out + (size_t)t * H * hd + (size_t)h * hd;
+  bool bad = false;
+  // Raw rows: the query head, then the group's keys and values of chunk
+  // positions 0..t.
+  for (int i = tid; i < (t + 2) * hd; i += kDecThreads) {
+    const int r = i >> 6, d = i & 63;
+    const float v = r == 0 ? q[((size_t)t * H + h) * hd + d] : R.k[((size_t)(r - 1) * KV + g) * hd + d];
+    bad |= !finite(v);
+    if (r == 0) qs[d] = v;
+    else kn[r - 1][d] = v;
+  }
+  for (int i = tid; i < (t + 1) * hd; i += kDecThreads)
+    vn[i >> 6][i & 63] = R.v[((size_t)(i >> 6) * KV + g) * hd + (i & 63)];
+  __syncthreads();
+  // RoPE: x0*c - x1*s, x0*s + x1*c on pairs (2j, 2j+1) or (j, j + half).
+  for (int p = tid; p < (t + 2) * half; p += kDecThreads) {
+    const int r = p / half, j = p - r * half;
+    float* base = r == 0 ? qs : kn[r - 1];
+    const int ppos = r == 0 ? pos : pb + r - 1;
+    const int ia = R.split_half ? j : 2 * j;
+    const int ib = R.split_half ? j + half : 2 * j + 1;
+    const float x0 = base[ia], x1 = base[ib];
+    const float c = R.rc[(size_t)ppos * half + j], sn = R.rs[(size_t)ppos * half + j];
+    const float y0 = x0 * c - x1 * sn;
+    const float y1 = x0 * sn + x1 * c;
+    bad |= !finite(y0) | !finite(y1);
+    base[ia] = y0;
+    base[ib] = y1;
+  }
+  __syncthreads();
+  if (h % G == 0 && tid < hd) {
+    const size_t off = (((size_t)layer * KV + g) * n_ctx + pos) * hd + tid;
+    const float kv = kn[t][tid], vv = vn[t][tid];
+    bad |= !finite(kv) | !finite(vv);
+    R.kc[off] = kv;
+    R.vc[off] = vv;
+  }
   if (len == 1) {  // a single score copies V exactly (lib.rs:2319-2321)
-    if (tid < hd) o[tid] = vals[tid];
+    if (tid < hd) o[tid] = vn[0][tid];
+    if (bad) flag(err, ERRBIT_NON_FINITE);
     return;
   }
-  bool bad = false;
-  if (tid < hd) qs[tid] = q[(size_t)t * H * hd + (size_t)h * hd + tid];
-  __syncthreads();
   // scores: dot_f32_ref(q, k_j) * scale
   for (int j = tid; j < len; j += kDecThreads) {
-    const float4* kr = reinterpret_cast<const float4*>(keys + (size_t)j * hd);
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-    for (int half = 0; half < 2; half++) {
-      float4 kv[8];
-#pragma unroll
-      for (int i4 = 0; i4 < 8; i4++) kv[i4] = kr[8 * half + i4];
-#pragma unroll
-      for (int i4 = 0; i4 < 8; i4++) {
-        const int i = 32 * half + 4 * i4;
-        acc[(i + 0) & 7] += qs[i + 0] * kv[i4].x;
-        acc[(i + 1) & 7] += qs[i + 1] * kv[i4].y;
-        acc[(i + 2) & 7] += qs[i + 2] * kv[i4].z;
-        acc[(i + 3) & 7] += qs[i + 3] * kv[i4].w;
-      }
-    }
-    const float s = finish_8lane(acc) * scale;
-    if (!finite(s)) bad = true;
-    sc[j] = s;
+    const float d = j < pb ? dot64_8lane(qs, keys + (size_t)j * hd) : dot64_8lane(qs, kn[j - pb]);
+    const float sv = d * scale;
+    if (!finite(sv)) bad = true;
+    sc[j] = sv;
   }
   __syncthreads();
   // softmax_in_place (lib.rs:2361-2388)
@@ -957,13 +912,13 @@ __global__ void __launch_bounds__(kDecThreads) k_attention_dec(const float* q, c
   // P.V.  Thread tid owns row jr of each tile and dimensions c4 .. c4 + 3.
   const int ntiles = (len + kDecTile - 1) / kDecTile;
   const int jr = tid >> 4, c4 = (tid & 15) * 4;
-  const float* vbase = vals + (size_t)jr * hd + c4;
   float4 ring[kDecDepth];
 #pragma unroll
   for (int u = 0; u < kDecDepth; u++) {
     const int j = u * kDecTile + jr;
-    ring[u] = j < len ? *reinterpret_cast<const float4*>(vbase + (size_t)u * kDecTile * hd)
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
+    ring[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (j < pb) ring[u] = *reinterpret_cast<const float4*>(vals + (size_t)j * hd + c4);
+    else if (j < len) ring[u] = *reinterpret_cast<const float4*>(&vn[j - pb][c4]);
   }
   float a = 0.0f;
   for (int k0 = 0; k0 < ntiles; k0 += kDecDepth) {
@@ -979,8 +934,8 @@ __global__ void __launch_bounds__(kDecThreads) k_attention_dec(const float* q, c
         pr[(c4 + 2) * kDecStride + jr] = p * ring[u].z;
         pr[(c4 + 3) * kDecStride + jr] = p * ring[u].w;
         const int jn = j + kDecDepth * kDecTile;
-        if (jn < len)
-          ring[u] = *reinterpret_cast<const float4*>(vbase + (size_t)(k + kDecDepth) * kDecTile * hd);
+        if (jn < pb) ring[u] = *reinterpret_cast<const float4*>(vals + (size_t)jn * hd + c4);
+        else if (jn < len) ring[u] = *reinterpret_cast<const float4*>(&vn[jn - pb][c4]);
       }
       __syncthreads();
       if (k < ntiles && wave == 0) {
@@ -1022,30 +977,34 @@ size_t attention_grp_smem(int H, int KV, int hd, int n_ctx) {
 constexpr size_t kDecMaxScoreBytes = 112 * 1024;
 
 bool attention_pos_dev_supported(int hd, int T, int n_ctx) {
-  return hd == 64 && T <= 4 && (size_t)n_ctx * sizeof(float) <= kDecMaxScoreBytes;
+  return hd == 64 && T <= kDecMaxT && (size_t)n_ctx * sizeof(float) <= kDecMaxScoreBytes;
+}
+
+bool attention_dec_applies(int hd, int T, int pos0, int n_ctx, bool pos_in_device) {
+  const size_t smem = (size_t)(pos_in_device ? n_ctx : pos0 + T) * sizeof(float);
+  return hd == 64 && T <= kDecMaxT && smem <= kDecMaxScoreBytes;
+}
+
+void launch_attention_dec(const float* q, const RopeIn& R, int layer, int T, int pos0, int H,
+                          int KV, int n_ctx, float scale, float* out, const int* pos_dev,
+                          int* err, hipStream_t s) {
+  // One workgroup per (head, position).  With the position in device
+  // memory the score buffer is sized for the whole window.
+  const size_t smem = (size_t)(pos_dev ? n_ctx : pos0 + T) * sizeof(float);
+  static bool attr_dec_set = false;
+  if (!attr_dec_set) {
+    (void)hipFuncSetAttribute((const void*)k_attention_dec,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDecMaxScoreBytes);
+    attr_dec_set = true;
+  }
+  launch_kernel(k_attention_dec, dim3(H, T), dim3(kDecThreads), smem, s, q, R, layer, pos0, H, KV,
+                n_ctx, scale, out, pos_dev, err);
 }
 
 void launch_attention(const float* q, const float* kc, const float* vc, int layer, int T, int pos0,
                       int H, int KV, int hd, int n_ctx, float scale, float* scores, float* out,
                       const int* pos_dev, int* err, hipStream_t s) {
   int G = H / KV;
-  if (hd == 64 && T <= 4) {
-    // Decode: one workgroup per (head, position).  With the position in
-    // device memory the score buffer is sized for the whole window.
-    size_t smem = (size_t)(pos_dev ? n_ctx : pos0 + T) * sizeof(float);
-    if (smem <= kDecMaxScoreBytes) {
-      static bool attr_dec_set = false;
-      if (!attr_dec_set) {
-        (void)hipFuncSetAttribute((const void*)k_attention_dec,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)kDecMaxScoreBytes);
-        attr_dec_set = true;
-      }
-      launch_kernel(k_attention_dec, dim3(H, T), dim3(kDecThreads), smem, s, q, kc, vc, layer,
-                    pos0, H, KV, n_ctx, scale, out, pos_dev, err);
-      return;
-    }
-  }
   if (hd == 64 && G >= 2 && G <= 16) {
     // Scores only need the longest row of this chunk (rounded to float4).
     int sc_stride = ((pos0 + T) + 3) & ~3;

@@ -260,3 +260,29 @@ def test_oracle_byte_codec_multi_window_round_trips():
             assert enc == _replay_payload(m, list(sym), 8, 2)
         got_sym, got = detref.codec_decode(m, t2b, enc, len(data), 8, 2, True)
         assert got == data and list(got_sym) == list(sym)
+
+
+# Payload sizes the reference records for its bundled fixtures
+# (docs/validation.md:511 and 1263-1264): n_ctx 8, overlap 2, byte escapes.
+SIZE_PINS = [
+    ("tiny-f32", b"detllm deterministic compression smoke\n", 102 - 56),
+    ("tiny-f32", None, 19),   # None: the bundled tiny.tokens.txt (12 bytes)
+    ("tiny-qmix", None, 19),
+]
+
+
+@pytest.mark.parametrize("model,data,payload", SIZE_PINS)
+def test_oracle_codec_payload_sizes_match_reference_records(model, data, payload):
+    from conftest import GOLDEN
+
+    g = (GOLDEN / f"{model}.gguf").read_bytes()
+    if data is None:
+        data = (GOLDEN / "tiny.tokens.txt").read_bytes()
+        assert len(data) == 12
+    m = detref.Model(g)
+    b2t, t2b = detref.byte_fallback_tables([f"<0x{b:02X}>" for b in range(256)])
+    sym = detref.codec_symbols(b2t, data, m.vocab)
+    enc = detref.codec_encode(m, sym, 8, 2, True)
+    assert len(enc) == payload
+    _, back = detref.codec_decode(m, t2b, enc, len(data), 8, 2, True)
+    assert back == data

@@ -163,3 +163,23 @@ def test_byte_codec_with_escapes_matches_oracle(workload, layers, n, n_ctx, chun
         assert enc == want
         dec = decode_bytes_with_model(s, tok, enc, len(data), overlap, True)
         assert dec.bytes == data and dec.symbols == [int(x) for x in sym]
+
+
+@pytest.mark.parametrize("model,text,size", [
+    ("tiny-f32", b"detllm deterministic compression smoke\n", 102),
+    ("tiny-f32", None, 75),
+    ("tiny-qmix", None, 75),
+])
+def test_dtlz_sizes_match_reference_records(model, text, size):
+    """DTLZ sizes recorded for the bundled fixtures (docs/validation.md:511,
+    1263-1264), n_ctx 8; the payload also equals the oracle's."""
+    from conftest import GOLDEN
+    from detllm_amd.codec import compress, decompress
+
+    g = (GOLDEN / f"{model}.gguf").read_bytes()
+    data = text if text is not None else (GOLDEN / "tiny.tokens.txt").read_bytes()
+    lm = _loaded(g)
+    out = compress(lm, data, 8)
+    assert len(out) == size
+    assert out[56:] == _oracle_file(g, data, 8)
+    assert decompress(lm, out) == data

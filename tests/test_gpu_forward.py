@@ -74,6 +74,30 @@ def test_baseline_shapes_match_oracle(name, layers, n_tok, chunk):
     _compare_with_oracle(data, synth.tokens(w, n_tok), chunk)
 
 
+@pytest.mark.parametrize("name,chunk", [("qwen05", 1), ("qwen05", 8), ("smollm2", 5)])
+@pytest.mark.parametrize("fused", [True, False])
+def test_decode_gemv_fusion_matches_oracle(monkeypatch, name, chunk, fused):
+    # Up to eight positions the Q8_0 layers run the fused decode GEMVs
+    # (rmsnorm / quantisation in the GEMV prologue, q/k/v in one launch,
+    # gate/up finishing as swiglu); both that and the separate launches must
+    # give the reference bits.
+    from detllm_amd import synth
+
+    if not fused:
+        monkeypatch.setenv("DETLLM_NO_FUSED_DECODE", "1")
+    monkeypatch.setenv("DETLLM_NO_GRAPH", "1")
+    w = synth.WORKLOADS[name]
+    _compare_with_oracle(synth.build_model(w, layers=2), synth.tokens(w, 10), chunk)
+
+
+def test_fused_decode_mixed_q8_0_q4_0_fixture():
+    # tiny-qmix mixes Q8_0 and Q4_0 within q/k/v and gate/up: each matrix
+    # gets its own fused launch; the reference's golden hash must hold.
+    m = _model((GOLDEN / "tiny-qmix.gguf").read_bytes())
+    want = (GOLDEN / "tiny-qmix.logits.sha256").read_text().strip()
+    assert m.logits_hash_for_tokens_chunked(_fixture_tokens(), 1).hex() == want
+
+
 @pytest.mark.parametrize("env", ["DETLLM_NO_F32_MIRROR", "DETLLM_NO_Q6K_PLANES"])
 def test_packed_chunk_paths_match_oracle(monkeypatch, env):
     # Without the encode copies (Q4_K f32 weights, Q6_K matrix-core planes)
