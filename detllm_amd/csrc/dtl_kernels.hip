@@ -283,11 +283,43 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* x, const float* w,
         wv[k][c] = i < n ? w[i] : 0.0f;
       }
   }
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    float v = xr[i];
-    if (!finite(v) || !finite(w[i])) bad = true;
-    xs[i] = v;
-    sq[(i & 7) * cs + (i >> 3)] = v * v;
+  // x (and the finiteness of x and w) in float4 batches: every load of a
+  // batch is issued before any is used, so the row costs one round trip.
+  constexpr int kRowBatch = 4;  // float4 per thread per batch: 4096 elements
+  if (n % 4 != 0) {  // rows not float4-aligned (only the kernel-level entry point)
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      const float v = xr[i];
+      bad |= !finite(v) | !finite(w[i]);
+      xs[i] = v;
+      sq[(i & 7) * cs + (i >> 3)] = v * v;
+    }
+  }
+  for (int base = 0; n % 4 == 0 && base < n; base += 1024 * kRowBatch) {
+    float4 xv[kRowBatch], wq[kRowBatch];
+#pragma unroll
+    for (int k = 0; k < kRowBatch; k++) {
+      const int i = base + 1024 * k + 4 * threadIdx.x;
+      xv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      wq[k] = xv[k];
+      if (i < n) {
+        xv[k] = *reinterpret_cast<const float4*>(xr + i);
+        wq[k] = *reinterpret_cast<const float4*>(w + i);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kRowBatch; k++) {
+      const int i = base + 1024 * k + 4 * threadIdx.x;
+      if (i < n) {
+        const float xe[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
+        const float we[4] = {wq[k].x, wq[k].y, wq[k].z, wq[k].w};
+        *reinterpret_cast<float4*>(xs + i) = xv[k];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          bad |= !finite(xe[c]) | !finite(we[c]);
+          sq[((i & 7) + c) * cs + (i >> 3)] = xe[c] * xe[c];
+        }
+      }
+    }
   }
   __syncthreads();
   if (threadIdx.x < 8) {
@@ -627,17 +659,19 @@ __global__ void __launch_bounds__(1024) k_attention_grp(const float* q, const fl
 }
 
 // Head dimension 64 (every Llama/Qwen shape served here): the same
-// arithmetic as k_attention_grp, with the K/V tiles double-buffered in LDS
-// and the next tile's global loads issued before the current tile's chains
-// run, so HBM/L2 latency hides behind the multiply-adds.  q and p are read
-// as float4 broadcasts.  One workgroup per (KV group, position), one wave
-// per head of the group; kA64Per float4 of each tile per thread.
+// arithmetic as k_attention_grp.  One workgroup per (KV group, position),
+// one wave per head of the group.  K and V stream through LDS in 64-row
+// tiles (K transposed); each thread holds PER float4 of a tile, and a ring of
+// D tiles is in flight in registers, so a tile's global loads have D tiles
+// of compute to land (one tile of compute is far shorter than one HBM/L2
+// round trip).  The serial chains (the softmax Z and P.V, one per lane) read
+// sixteen operands from LDS ahead of their adds.
 constexpr int kA64Tile = 64;           // K/V rows per tile
 constexpr int kA64KStride = 65;        // K^T row stride (conflict-free column reads)
 constexpr int kA64Buf = 64 * kA64KStride;
-constexpr int kA64Per = 8;             // float4 loads per thread per tile (G >= 2)
 
-__global__ void __launch_bounds__(1024) k_attention_hd64(const float* q, const float* kc,
+template <int PER, int D>
+__global__ void __launch_bounds__(PER <= 2 ? 1024 : (PER <= 4 ? 512 : 256)) k_attention_hd64(const float* q, const float* kc,
                                                          const float* vc, int layer, int pos0,
                                                          int H, int KV, int n_ctx, int sc_stride,
                                                          float scale, float* out, int* err) {
@@ -663,67 +697,83 @@ __global__ void __launch_bounds__(1024) k_attention_hd64(const float* q, const f
   bool bad = false;
   qs[wave * hd + lane] = q[(size_t)t * H * hd + (size_t)h * hd + lane];
   const int ntiles = (len + kA64Tile - 1) / kA64Tile;
-  float4 pre[kA64Per];
-  // Tile loads: float4 index x = threadIdx.x + c * nthreads covers rows
+  // Tile loads: float4 index x = threadIdx.x + c * nthreads covers row
   // x / 16, columns 4 * (x % 16); rows at or past len are not read.
-  auto issue = [&](const float* base, int j0) {
+  float4 ring[D][PER];
+  auto issue = [&](float4 (&dst)[PER], const float* base, int j0) {
 #pragma unroll
-    for (int c = 0; c < kA64Per; c++) {
-      int x = threadIdx.x + c * nthreads;
-      int j = x >> 4;
+    for (int c = 0; c < PER; c++) {
+      const int x = threadIdx.x + c * nthreads;
+      const int j = x >> 4;
       if (x < 1024 && j0 + j < len)
-        pre[c] = *reinterpret_cast<const float4*>(base + (size_t)(j0 + j) * hd + (x & 15) * 4);
+        dst[c] = *reinterpret_cast<const float4*>(base + (size_t)(j0 + j) * hd + (x & 15) * 4);
     }
   };
-  auto commit_k = [&](float* buf, int j0) {
+  auto commit_k = [&](const float4 (&src)[PER], float* buf, int j0) {
 #pragma unroll
-    for (int c = 0; c < kA64Per; c++) {
-      int x = threadIdx.x + c * nthreads;
-      int j = x >> 4, i = (x & 15) * 4;
+    for (int c = 0; c < PER; c++) {
+      const int x = threadIdx.x + c * nthreads;
+      const int j = x >> 4, i = (x & 15) * 4;
       if (x < 1024 && j0 + j < len) {
-        buf[(i + 0) * kA64KStride + j] = pre[c].x;
-        buf[(i + 1) * kA64KStride + j] = pre[c].y;
-        buf[(i + 2) * kA64KStride + j] = pre[c].z;
-        buf[(i + 3) * kA64KStride + j] = pre[c].w;
+        buf[(i + 0) * kA64KStride + j] = src[c].x;
+        buf[(i + 1) * kA64KStride + j] = src[c].y;
+        buf[(i + 2) * kA64KStride + j] = src[c].z;
+        buf[(i + 3) * kA64KStride + j] = src[c].w;
       }
     }
   };
-  auto commit_v = [&](float* buf, int j0) {
+  auto commit_v = [&](const float4 (&src)[PER], float* buf, int j0) {
 #pragma unroll
-    for (int c = 0; c < kA64Per; c++) {
-      int x = threadIdx.x + c * nthreads;
-      if (x < 1024 && j0 + (x >> 4) < len) reinterpret_cast<float4*>(buf)[x] = pre[c];
+    for (int c = 0; c < PER; c++) {
+      const int x = threadIdx.x + c * nthreads;
+      if (x < 1024 && j0 + (x >> 4) < len) reinterpret_cast<float4*>(buf)[x] = src[c];
     }
   };
-  // scores: dot_f32_ref(q, k_j) * scale
-  issue(keys, 0);
-  commit_k(tiles, 0);
+  // scores: dot_f32_ref(q, k_j) * scale.  Tile k sits in ring slot k % D.
+#pragma unroll
+  for (int u = 0; u < D; u++)
+    if (u < ntiles) issue(ring[u], keys, u * kA64Tile);
+  commit_k(ring[0], tiles, 0);
+  if (D < ntiles) issue(ring[0], keys, D * kA64Tile);
   __syncthreads();
-  for (int tI = 0; tI < ntiles; tI++) {
-    const int j0 = tI * kA64Tile;
-    float* cur = tiles + (tI & 1) * kA64Buf;
-    if (tI + 1 < ntiles) issue(keys, j0 + kA64Tile);
-    if (j0 + lane < len) {
-      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      const float4* qw = reinterpret_cast<const float4*>(qs + wave * hd);
+  for (int k0 = 0; k0 < ntiles; k0 += D) {
 #pragma unroll
-      for (int i4 = 0; i4 < 16; i4++) {
-        float4 qv = qw[i4];
-        int i = i4 * 4;
-        acc[(i + 0) & 7] += qv.x * cur[(i + 0) * kA64KStride + lane];
-        acc[(i + 1) & 7] += qv.y * cur[(i + 1) * kA64KStride + lane];
-        acc[(i + 2) & 7] += qv.z * cur[(i + 2) * kA64KStride + lane];
-        acc[(i + 3) & 7] += qv.w * cur[(i + 3) * kA64KStride + lane];
+    for (int u = 0; u < D; u++) {
+      const int k = k0 + u;
+      if (k < ntiles) {
+        const int j0 = k * kA64Tile;
+        const float* cur = tiles + (k & 1) * kA64Buf;
+        if (j0 + lane < len) {
+          float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+          const float4* qw = reinterpret_cast<const float4*>(qs + wave * hd);
+#pragma unroll
+          for (int i4 = 0; i4 < 16; i4++) {
+            const float4 qv = qw[i4];
+            const int i = i4 * 4;
+            acc[(i + 0) & 7] += qv.x * cur[(i + 0) * kA64KStride + lane];
+            acc[(i + 1) & 7] += qv.y * cur[(i + 1) * kA64KStride + lane];
+            acc[(i + 2) & 7] += qv.z * cur[(i + 2) * kA64KStride + lane];
+            acc[(i + 3) & 7] += qv.w * cur[(i + 3) * kA64KStride + lane];
+          }
+          const float sv = finish_8lane(acc) * scale;
+          if (!finite(sv)) bad = true;
+          my[j0 + lane] = sv;
+        }
+        // tile k + 1 into the other buffer (its last reader, tile k - 1,
+        // finished before the previous barrier); its slot then takes
+        // tile k + 1 + D
+        if (k + 1 < ntiles) {
+          commit_k(ring[(u + 1) % D], tiles + ((k + 1) & 1) * kA64Buf, j0 + kA64Tile);
+          if (k + 1 + D < ntiles) issue(ring[(u + 1) % D], keys, j0 + (1 + D) * kA64Tile);
+        }
       }
-      float s = finish_8lane(acc) * scale;
-      if (!finite(s)) bad = true;
-      my[j0 + lane] = s;
+      __syncthreads();
     }
-    if (tI + 1 < ntiles) commit_k(tiles + ((tI + 1) & 1) * kA64Buf, j0 + kA64Tile);
-    __syncthreads();
   }
-  // First V tile loads overlap the softmax.
-  issue(vals, 0);
+  // The first V tiles' loads overlap the softmax.
+#pragma unroll
+  for (int u = 0; u < D; u++)
+    if (u < ntiles) issue(ring[u], vals, u * kA64Tile);
   // softmax_in_place (lib.rs:2361-2388), per wave
   float mx = -__builtin_huge_valf();
   for (int j = lane; j < len; j += 64) mx = fmaxf(mx, my[j]);
@@ -731,39 +781,67 @@ __global__ void __launch_bounds__(1024) k_attention_hd64(const float* q, const f
   for (int j = lane; j < len; j += 64) my[j] = exp_clamped(my[j] - mx);
   __syncthreads();
   float zacc = 0.0f;
-  if (lane < 8)
-    for (int j = lane; j < len; j += 8) zacc += my[j];
+  if (lane < 8) {
+    int j = lane;
+    for (; j + 8 * 15 < len; j += 8 * 16) {
+      float e[16];
+#pragma unroll
+      for (int k = 0; k < 16; k++) e[k] = my[j + 8 * k];
+#pragma unroll
+      for (int k = 0; k < 16; k++) zacc += e[k];
+    }
+    for (; j < len; j += 8) zacc += my[j];
+  }
   float part[8];
 #pragma unroll
   for (int c = 0; c < 8; c++) part[c] = __shfl(zacc, c);
-  float z = finish_8lane(part);
+  const float z = finish_8lane(part);
   if (!finite(z) || z == 0.0f) bad = true;
   for (int j = lane; j < len; j += 64) {
-    float p = my[j] / z;
+    const float p = my[j] / z;
     if (!finite(p)) bad = true;
     my[j] = p;
   }
-  commit_v(tiles, 0);
+  commit_v(ring[0], tiles, 0);
+  if (D < ntiles) issue(ring[0], vals, D * kA64Tile);
   __syncthreads();
   // P.V: out[d] = 0.0; out[d] += p_j * v_j[d] for j ascending
   float a = 0.0f;
-  for (int tI = 0; tI < ntiles; tI++) {
-    const int j0 = tI * kA64Tile;
-    const int n = len - j0 < kA64Tile ? len - j0 : kA64Tile;
-    const float* cur = tiles + (tI & 1) * kA64Buf;
-    if (tI + 1 < ntiles) issue(vals, j0 + kA64Tile);
-    const float4* pw = reinterpret_cast<const float4*>(my + j0);
-    int j = 0;
-    for (; j + 4 <= n; j += 4) {
-      float4 pv = pw[j >> 2];
-      a += pv.x * cur[(j + 0) * hd + lane];
-      a += pv.y * cur[(j + 1) * hd + lane];
-      a += pv.z * cur[(j + 2) * hd + lane];
-      a += pv.w * cur[(j + 3) * hd + lane];
+  for (int k0 = 0; k0 < ntiles; k0 += D) {
+#pragma unroll
+    for (int u = 0; u < D; u++) {
+      const int k = k0 + u;
+      if (k < ntiles) {
+        const int j0 = k * kA64Tile;
+        const int n = len - j0 < kA64Tile ? len - j0 : kA64Tile;
+        const float* cur = tiles + (k & 1) * kA64Buf;
+        if (n == kA64Tile) {
+#pragma unroll
+          for (int jb = 0; jb < kA64Tile; jb += 16) {
+            float v[16];
+            float4 pv[4];
+#pragma unroll
+            for (int kk = 0; kk < 16; kk++) v[kk] = cur[(jb + kk) * hd + lane];
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) pv[kk] = reinterpret_cast<const float4*>(my + j0 + jb)[kk];
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+              a += pv[kk].x * v[4 * kk + 0];
+              a += pv[kk].y * v[4 * kk + 1];
+              a += pv[kk].z * v[4 * kk + 2];
+              a += pv[kk].w * v[4 * kk + 3];
+            }
+          }
+        } else {
+          for (int j = 0; j < n; j++) a += my[j0 + j] * cur[j * hd + lane];
+        }
+        if (k + 1 < ntiles) {
+          commit_v(ring[(u + 1) % D], tiles + ((k + 1) & 1) * kA64Buf, j0 + kA64Tile);
+          if (k + 1 + D < ntiles) issue(ring[(u + 1) % D], vals, j0 + (1 + D) * kA64Tile);
+        }
+      }
+      __syncthreads();
     }
-    for (; j < n; j++) a += my[j0 + j] * cur[j * hd + lane];
-    if (tI + 1 < ntiles) commit_v(tiles + ((tI + 1) & 1) * kA64Buf, j0 + kA64Tile);
-    __syncthreads();
   }
   if (!finite(a)) bad = true;
   o[lane] = a;
@@ -1010,14 +1088,21 @@ void launch_attention(const float* q, const float* kc, const float* vc, int laye
     int sc_stride = ((pos0 + T) + 3) & ~3;
     size_t smem64 = attention_hd64_smem(G, sc_stride);
     if (smem64 <= 150 * 1024) {
-      static bool attr64_set = false;
-      if (!attr64_set) {
-        (void)hipFuncSetAttribute((const void*)k_attention_hd64,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
-        attr64_set = true;
-      }
-      launch_kernel(k_attention_hd64, dim3(KV, T), dim3(G * 64), smem64, s, q, kc, vc, layer,
-                         pos0, H, KV, n_ctx, sc_stride, scale, out, err);
+      // float4 per thread per tile (64 rows x 16) and tiles in flight
+      const int per = (1024 + G * 64 - 1) / (G * 64);
+      auto go = [&](auto kern) {
+        static bool attr64_set = false;
+        if (!attr64_set) {
+          (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    150 * 1024);
+          attr64_set = true;
+        }
+        launch_kernel(kern, dim3(KV, T), dim3(G * 64), smem64, s, q, kc, vc, layer, pos0, H, KV,
+                      n_ctx, sc_stride, scale, out, err);
+      };
+      if (per <= 2) go(k_attention_hd64<2, 8>);
+      else if (per <= 4) go(k_attention_hd64<4, 4>);
+      else go(k_attention_hd64<8, 2>);
       return;
     }
   }
