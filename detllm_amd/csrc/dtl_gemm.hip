@@ -486,146 +486,6 @@ __global__ void __launch_bounds__(256) k_q4k_f32w(Q4kF32Args p) {
 #undef DTL_ISSUE_W
 #undef DTL_COMMIT_W
 
-// The same product with D slices of activations and weights in flight in
-// registers (slice k + 1 is written to LDS while slice k is consumed; slice
-// k + 1 + D is then issued into the freed registers), for launches with one
-// wave per SIMD, where a single slice of prefetch cannot cover an HBM/L2
-// round trip.  Arithmetic and order are those of k_q4k_f32w.
-template <int NK, int MODE, int D>
-__global__ void __launch_bounds__(256) k_q4k_ring(Q4kF32Args p) {
-  static_assert(D == 2 || D == 4, "slice k uses LDS buffer k & 1 = u & 1; steps expand for D <= 4");
-  constexpr int NM = MODE == MODE_PAIR ? 2 : 1;
-  constexpr int SL = 64;
-  constexpr int LD = SL + 4;
-  __shared__ __align__(16) float at[2][64][LD];
-  __shared__ __align__(16) float wt[2][kWaves][NM * NK][SL];
-  const int cols = p.cols, T = p.T;
-  const int rows_total = MODE == MODE_CAT ? p.rows0 + p.rows1 : p.rows0;
-  const float* __restrict__ af = p.af;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int row0 = (blockIdx.x * kWaves + wave) * NK;
-  const int tbase = blockIdx.y * 64;
-  const int t = tbase + lane;
-  float acc[NM * NK];
-#pragma unroll
-  for (int k = 0; k < NM * NK; k++) acc[k] = 0.0f;
-  const int tk0 = threadIdx.x >> 4, c40 = threadIdx.x & 15;
-  const float* asrc[4];
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    int tt = tbase + tk0 + 16 * j;
-    asrc[j] = af + (size_t)(tt < T ? tt : T - 1) * cols + c40 * 4;
-  }
-  const int wk = lane >> 4, wc4 = lane & 15;
-  const bool wlane = wk < NM * NK;
-  const float* wsrc = p.w0;
-  if (wlane) {
-    if (MODE == MODE_PAIR) {
-      int m = wk / NK, kk = wk % NK;
-      int row = row0 + kk < p.rows0 ? row0 + kk : p.rows0 - 1;
-      wsrc = (m ? p.w1 : p.w0) + (size_t)row * cols + wc4 * 4;
-    } else {
-      int g = row0 + wk < rows_total ? row0 + wk : rows_total - 1;
-      bool m = MODE == MODE_CAT && g >= p.rows0;
-      wsrc = (m ? p.w1 : p.w0) + (size_t)(m ? g - p.rows0 : g) * cols + wc4 * 4;
-    }
-  }
-  // Ring slots as named registers (slot is a literal at every use).
-  float4 ra0_0, ra0_1, ra0_2, ra0_3, rw0;
-  float4 ra1_0, ra1_1, ra1_2, ra1_3, rw1;
-  float4 ra2_0, ra2_1, ra2_2, ra2_3, rw2;
-  float4 ra3_0, ra3_1, ra3_2, ra3_3, rw3;
-  rw0 = rw1 = rw2 = rw3 = make_float4(0.f, 0.f, 0.f, 0.f);
-#define DTL_RISSUE(slot, e0)                                          \
-  do {                                                                \
-    ra##slot##_0 = *(const float4*)(asrc[0] + (e0));                  \
-    ra##slot##_1 = *(const float4*)(asrc[1] + (e0));                  \
-    ra##slot##_2 = *(const float4*)(asrc[2] + (e0));                  \
-    ra##slot##_3 = *(const float4*)(asrc[3] + (e0));                  \
-    if (wlane) rw##slot = *(const float4*)(wsrc + (e0));              \
-  } while (0)
-#define DTL_RCOMMIT(slot, b)                                          \
-  do {                                                                \
-    *(float4*)&at[b][tk0][c40 * 4] = ra##slot##_0;                    \
-    *(float4*)&at[b][tk0 + 16][c40 * 4] = ra##slot##_1;               \
-    *(float4*)&at[b][tk0 + 32][c40 * 4] = ra##slot##_2;               \
-    *(float4*)&at[b][tk0 + 48][c40 * 4] = ra##slot##_3;               \
-    if (wlane) *(float4*)&wt[b][wave][wk][wc4 * 4] = rw##slot;        \
-  } while (0)
-  DTL_RISSUE(0, 0);
-  if (SL < cols) DTL_RISSUE(1, SL);
-  if constexpr (D >= 4) {
-    if (2 * SL < cols) DTL_RISSUE(2, 2 * SL);
-    if (3 * SL < cols) DTL_RISSUE(3, 3 * SL);
-  }
-  DTL_RCOMMIT(0, 0);
-  if (D * SL < cols) DTL_RISSUE(0, D * SL);
-  __syncthreads();
-  // One slice step; u is a literal in every expansion, so the ring slots are
-  // registers, never scratch.
-#define DTL_RSTEP(u, un)                                                    \
-  do {                                                                      \
-    const int e = e0 + (u) * SL;                                            \
-    if (e < cols) {                                                         \
-      constexpr int buf = (u) & 1;                                          \
-      _Pragma("unroll 4") for (int i = 0; i < SL; i += 4) {                 \
-        float4 a = *(const float4*)&at[buf][lane][i];                       \
-        _Pragma("unroll") for (int k = 0; k < NM * NK; k++) {               \
-          float4 w = *(const float4*)&wt[buf][wave][k][i];                  \
-          float c = acc[k];                                                 \
-          c += w.x * a.x;                                                   \
-          c += w.y * a.y;                                                   \
-          c += w.z * a.z;                                                   \
-          c += w.w * a.w;                                                   \
-          acc[k] = c;                                                       \
-        }                                                                   \
-      }                                                                     \
-      if (e + SL < cols) {                                                  \
-        DTL_RCOMMIT(un, buf ^ 1);                                           \
-        if (e + (1 + D) * SL < cols) DTL_RISSUE(un, e + (1 + D) * SL);      \
-      }                                                                     \
-    }                                                                       \
-    __syncthreads();                                                        \
-  } while (0)
-  for (int e0 = 0; e0 < cols; e0 += D * SL) {
-    if constexpr (D == 4) {
-      DTL_RSTEP(0, 1);
-      DTL_RSTEP(1, 2);
-      DTL_RSTEP(2, 3);
-      DTL_RSTEP(3, 0);
-    } else {
-      DTL_RSTEP(0, 1);
-      DTL_RSTEP(1, 0);
-    }
-  }
-#undef DTL_RSTEP
-  if (t >= T) return;
-  bool ok = true;
-#pragma unroll
-  for (int k = 0; k < NK; k++) {
-    const int g = row0 + k;
-    if (g >= rows_total) continue;
-    if (MODE == MODE_PAIR) {
-      size_t o = (size_t)t * p.rows0 + g;
-      float gv = acc[k], uv = acc[NK + k];
-      float v = silu_det(gv) * uv;
-      ok &= finite(gv) && finite(uv) && finite(v);
-      p.ffo[o] = v;
-    } else {
-      const bool m = MODE == MODE_CAT && g >= p.rows0;
-      const int local = m ? g - p.rows0 : g;
-      const int R = m ? p.rows1 : p.rows0;
-      ok &= store_epilogue(acc[k], m ? p.out1 : p.out0, (size_t)t * R + local,
-                           m ? p.bias1 : p.bias0, local, p.epi);
-    }
-  }
-  if (!ok) flag(p.err, ERRBIT_NON_FINITE);
-}
-
-#undef DTL_RISSUE
-#undef DTL_RCOMMIT
-
 // Exact f32 copy of a Q4_K matrix: q4_k_value for every element.
 __global__ void k_dequant_q4k(DevMat W, float* out) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -848,37 +708,16 @@ int q4k_nk(int mode, int rows_total) {
   return rows_total >= 8192 ? 2 : 1;
 }
 
-// Slices in flight of the register-ring variant (0: the double-buffered
-// kernel); DETLLM_Q4K_RING overrides it.
-int q4k_ring(int mode, int nk) {
-  static int forced = [] {
-    const char* e = getenv("DETLLM_Q4K_RING");
-    return e ? atoi(e) : -1;
-  }();
-  if (forced >= 0) return forced;
-  (void)mode;
-  (void)nk;
-  return 0;
-}
-
 template <int MODE>
 void launch_q4k_f32w(const Q4kF32Args& a, hipStream_t s) {
   const int rows_total = MODE == MODE_CAT ? a.rows0 + a.rows1 : a.rows0;
   const int nk = q4k_nk(MODE, rows_total);
   dim3 grid((rows_total + kWaves * nk - 1) / (kWaves * nk), (a.T + 63) / 64);
   dim3 block(kWaves * 64);
-  const int ring = q4k_ring(MODE, nk);
-  if (ring == 4) {
-    if (nk == 2) launch_kernel(k_q4k_ring<2, MODE, 4>, grid, block, 0, s, a);
-    else launch_kernel(k_q4k_ring<1, MODE, 4>, grid, block, 0, s, a);
-  } else if (ring == 2) {
-    if (nk == 2) launch_kernel(k_q4k_ring<2, MODE, 2>, grid, block, 0, s, a);
-    else launch_kernel(k_q4k_ring<1, MODE, 2>, grid, block, 0, s, a);
-  } else if (nk == 2) {
+  if (nk == 2)
     launch_kernel(k_q4k_f32w<2, MODE>, grid, block, 0, s, a);
-  } else {
+  else
     launch_kernel(k_q4k_f32w<1, MODE>, grid, block, 0, s, a);
-  }
 }
 
 Q4kF32Args q4k_args(const DevMat& W0, const DevMat* W1, const DevAct& A, int T, float* out0,
