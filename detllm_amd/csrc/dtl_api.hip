@@ -784,6 +784,7 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev) {
     const int e_q = L.bq ? EPI_BIAS : EPI_STORE, e_k = L.bk ? EPI_BIAS : EPI_STORE;
     const int e_v = L.bv ? EPI_BIAS : EPI_STORE;
     DevAct a{};
+    bool attn_quantized = false;
     if (fits({&L.wq, &L.wk, &L.wv}, false, true)) {
       fused({&L.wq, &L.wk, &L.wv}, false, {s->q, s->k, s->v}, {L.bq, L.bk, L.bv}, {e_q, e_k, e_v},
             s->x, L.attn_norm, "gemv_fused_qkv");
@@ -824,17 +825,25 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev) {
                           (int)c.rope_dim, c.split_half, s->kc, s->vc, (int)l, (int)s->n_ctx,
                           pos_dev, s->err, st);
       });
+      // The chunked attention also writes the Q8A form wo reads, when that
+      // is the only form wo needs.
+      bool q8a, q8k;
+      needed_forms({&L.wo}, &q8a, &q8k);
+      attn_quantized = q8a && !q8k && !fits({&L.wo}, false, false) &&
+                       attention_quantizes_q8a(hd, H, KV, T, (int)pos0, (int)s->n_ctx);
       P.timed(st, "attention", kv_rows * KV * hd * 8.0 + (double)T * H * hd * 8.0,
               kv_rows * H * hd * 2.0, [&] {
                 launch_attention(s->q, s->kc, s->vc, (int)l, T, (int)pos0, H, KV, hd,
                                  (int)s->n_ctx, c.attention_scale, s->scores, s->attn, pos_dev,
-                                 s->err, st);
+                                 s->err, st, attn_quantized ? s->qa : nullptr,
+                                 attn_quantized ? s->da : nullptr,
+                                 attn_quantized ? s->af : nullptr);
               });
     }
     if (fits({&L.wo}, false, false)) {
       fused({&L.wo}, false, {s->x}, {nullptr}, {EPI_RESIDUAL}, s->attn, nullptr, "gemv_fused_o");
     } else {
-      a = prepare_input(s, s->attn, T, H * hd, {&L.wo});
+      a = attn_quantized ? session_act(s, s->attn) : prepare_input(s, s->attn, T, H * hd, {&L.wo});
       gemm(L.wo, a, s->x, nullptr, EPI_RESIDUAL, nullptr);
     }
     if (fits({&L.gate, &L.up}, true, true)) {

@@ -674,7 +674,8 @@ template <int PER, int D>
 __global__ void __launch_bounds__(PER <= 2 ? 1024 : (PER <= 4 ? 512 : 256)) k_attention_hd64(const float* q, const float* kc,
                                                          const float* vc, int layer, int pos0,
                                                          int H, int KV, int n_ctx, int sc_stride,
-                                                         float scale, float* out, int* err) {
+                                                         float scale, float* out, QuantOut oq,
+                                                         int* err) {
   extern __shared__ __align__(16) float smem[];
   constexpr int hd = 64;
   const int G = H / KV;
@@ -686,8 +687,13 @@ __global__ void __launch_bounds__(PER <= 2 ? 1024 : (PER <= 4 ? 512 : 256)) k_at
   const float* keys = kc + ((size_t)layer * KV + g) * n_ctx * hd;
   const float* vals = vc + ((size_t)layer * KV + g) * n_ctx * hd;
   float* o = out + (size_t)t * H * hd + (size_t)h * hd;
+  // With oq.qa set, the wave also writes the Q8A form of its head's output
+  // (the input of wo): two 32-element blocks per head.
+  const size_t qbase = (size_t)t * H * hd + (size_t)h * hd;
   if (len == 1) {  // a single score copies V exactly (lib.rs:2319-2321)
-    o[lane] = vals[lane];
+    const float v0 = vals[lane];
+    o[lane] = v0;
+    if (oq.qa) quantize_q8a_lanes(v0, qbase, oq);
     return;
   }
   float* sc = smem;                                // [G][sc_stride]
@@ -845,6 +851,7 @@ __global__ void __launch_bounds__(PER <= 2 ? 1024 : (PER <= 4 ? 512 : 256)) k_at
   }
   if (!finite(a)) bad = true;
   o[lane] = a;
+  if (oq.qa) quantize_q8a_lanes(a, qbase, oq);
   if (bad) flag(err, ERRBIT_NON_FINITE);
 }
 
@@ -1079,9 +1086,17 @@ void launch_attention_dec(const float* q, const RopeIn& R, int layer, int T, int
                 n_ctx, scale, out, pos_dev, err);
 }
 
+bool attention_quantizes_q8a(int hd, int H, int KV, int T, int pos0, int n_ctx) {
+  const int G = H / KV;
+  if (attention_dec_applies(hd, T, pos0, n_ctx, false)) return false;
+  return hd == 64 && G >= 2 && G <= 16 &&
+         attention_hd64_smem(G, ((pos0 + T) + 3) & ~3) <= 150 * 1024;
+}
+
 void launch_attention(const float* q, const float* kc, const float* vc, int layer, int T, int pos0,
                       int H, int KV, int hd, int n_ctx, float scale, float* scores, float* out,
-                      const int* pos_dev, int* err, hipStream_t s) {
+                      const int* pos_dev, int* err, hipStream_t s, int8_t* qa, float* da,
+                      float* af) {
   int G = H / KV;
   if (hd == 64 && G >= 2 && G <= 16) {
     // Scores only need the longest row of this chunk (rounded to float4).
@@ -1097,8 +1112,9 @@ void launch_attention(const float* q, const float* kc, const float* vc, int laye
                                     150 * 1024);
           attr64_set = true;
         }
+        const QuantOut oq{qa, da, af, nullptr, nullptr};
         launch_kernel(kern, dim3(KV, T), dim3(G * 64), smem64, s, q, kc, vc, layer, pos0, H, KV,
-                      n_ctx, sc_stride, scale, out, err);
+                      n_ctx, sc_stride, scale, out, oq, err);
       };
       if (per <= 2) go(k_attention_hd64<2, 8>);
       else if (per <= 4) go(k_attention_hd64<4, 4>);

@@ -102,4 +102,27 @@ __device__ __forceinline__ void quantize_span(const float v[4], bool in, size_t 
   }
 }
 
+// Q8A of one value per lane, 32-lane blocks (lanes 0-31 and 32-63 of a
+// wave are two blocks): the same amax, scale and rounding as quantize_span.
+// base: element offset of lane 0 (a multiple of 32).
+__device__ __forceinline__ void quantize_q8a_lanes(float v, size_t base, const QuantOut& q) {
+  const int lane = threadIdx.x & 63;
+  float amax = v < 0.0f ? -v : v;
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
+  int8_t qv = 0;
+  float fv = 0.0f;
+  const float d = amax / 127.0f;
+  if (amax != 0.0f) {
+    const float y = v / d;
+    int r = y < 0.0f ? f32_as_i32(y - 0.5f) : f32_as_i32(y + 0.5f);
+    r = r < -127 ? -127 : (r > 127 ? 127 : r);
+    qv = (int8_t)r;
+    fv = d * (float)r;
+  }
+  q.qa[base + lane] = qv;
+  if (q.af) q.af[base + lane] = fv;
+  if ((lane & 31) == 0) q.da[(base + lane) / 32] = amax == 0.0f ? 0.0f : d;
+}
+
 }  // namespace dtl
