@@ -100,6 +100,55 @@ def decode_leg(model, toks, positions: int, workload: str) -> dict:
             "gemv": gemv}
 
 
+def config_legs(built: dict) -> dict:
+    """The other configurations, each at its own size: C1 (tiny F32) logits
+    hash against the oracle; C2 (SmolLM2-135M shape) single-token decode of
+    512 positions; C3 (Qwen2.5-0.5B shape) single-token decode of 1024
+    positions with the next token's symbol range (256 byte escapes) after
+    every position.  Decode rates are wall time of the whole loop; parity is
+    the first positions' logits against the oracle."""
+    import numpy as np
+
+    from detllm_amd import synth
+    from detllm_amd.model import F32Llama
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import detref
+
+    out = {}
+    w = synth.WORKLOADS["tiny"]
+    data, toks = synth.build_model(w), synth.tokens(w)
+    got = F32Llama.from_gguf(data).logits_hash_for_tokens_chunked(toks, w.chunk).hex()
+    out["C1"] = {"workload": w.name, "logits_sha256": got,
+                 "oracle_match": got == detref.Model(data).logits_hash(toks, w.chunk).hex()}
+    for name, with_range in (("smollm2", False), ("qwen05", True)):
+        w = synth.WORKLOADS[name]
+        data = built.get(name) or synth.build_model(w)
+        toks = synth.tokens(w)
+        m = F32Llama.from_gguf(data)
+        n = toks.size
+        with m.forward_workspace(w.ctx, 1) as s:
+            s.forward_one(int(toks[0]), 0, want_logits=False)  # warm-up (graph capture)
+            s.reset()
+            first = []
+            t = time.perf_counter()
+            for p in range(n):
+                lg = s.forward_one(int(toks[p]), p, want_logits=p < 3)
+                if lg is not None:
+                    first.append(lg.copy())
+                if with_range and p + 1 < n:
+                    s.symbol_ranges([int(toks[p + 1])], 0, 256)
+            dt = time.perf_counter() - t
+        ref = detref.Model(data).logits(toks[:3])
+        parity = all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(first, ref))
+        key = "C2" if name == "smollm2" else "C3"
+        out[key] = {"workload": name, "positions": int(n), "tokens_per_s": round(n / dt, 2),
+                    "per_position": "forward_one" + (" + next-token symbol range" if with_range else ""),
+                    "parity_first_3_positions": parity}
+        del m
+    return out
+
+
 def codec_leg(gguf: bytes, workload: str, nbytes: int, cpu_bytes: int, threads: int) -> dict:
     """End-to-end DTLZ compress + decompress of a prefix of the seeded
     order-3 Markov byte stream on the device (window n_ctx 2048, overlap
@@ -158,6 +207,8 @@ def main() -> int:
     ap.add_argument("--decode-positions", type=int, default=64)
     ap.add_argument("--decode-workload", default="qwen05",
                     help="model of the decode leg (qwen05: Q8_0 with a 145 MB output projection)")
+    ap.add_argument("--no-config-legs", action="store_true",
+                    help="skip the C1 hash / C2 and C3 decode legs")
     ap.add_argument("--codec-bytes", type=int, default=8192,
                     help="prefix of the 1 MiB Markov stream compressed + decompressed (0: skip)")
     ap.add_argument("--codec-cpu-bytes", type=int, default=96,
@@ -314,6 +365,13 @@ def main() -> int:
             codec = codec_leg(ddata, dw.name, args.codec_bytes, args.codec_cpu_bytes, threads)
             log(f"[bench] codec {codec['bytes']} B: compress {codec['compress_bytes_per_s']} B/s, "
                 f"decompress {codec['decompress_bytes_per_s']} B/s, roundtrip {codec['roundtrip']}")
+    per_config = None
+    if not args.no_config_legs:
+        built = {dw.name: ddata} if args.decode_positions > 0 or args.codec_bytes > 0 else {}
+        per_config = config_legs(built)
+        log(f"[bench] configs: C1 hash match {per_config['C1']['oracle_match']}, "
+            f"C2 {per_config['C2']['tokens_per_s']} tok/s, C3 {per_config['C3']['tokens_per_s']} tok/s")
+    if args.decode_positions > 0 or args.codec_bytes > 0:
         del ddata
 
     cpu = None
@@ -354,10 +412,14 @@ def main() -> int:
         "kernels": kernels,
         "decode": decode,
         "codec": codec,
+        "configs": per_config,
     }
     print(json.dumps(line), flush=True)
     codec_ok = codec is None or (codec["roundtrip"] and codec.get("cpu_decode_prefix", {"ok": True})["ok"])
-    return 0 if parity and deterministic and codec_ok else 1
+    configs_ok = per_config is None or (per_config["C1"]["oracle_match"] and
+                                        per_config["C2"]["parity_first_3_positions"] and
+                                        per_config["C3"]["parity_first_3_positions"])
+    return 0 if parity and deterministic and codec_ok and configs_ok else 1
 
 
 if __name__ == "__main__":
