@@ -834,8 +834,8 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev) {
       P.timed(st, "attention", kv_rows * KV * hd * 8.0 + (double)T * H * hd * 8.0,
               kv_rows * H * hd * 2.0, [&] {
                 launch_attention(s->q, s->kc, s->vc, (int)l, T, (int)pos0, H, KV, hd,
-                                 (int)s->n_ctx, c.attention_scale, s->scores, s->attn, pos_dev,
-                                 s->err, st, attn_quantized ? s->qa : nullptr,
+                                 (int)s->n_ctx, c.attention_scale, s->scores, s->attn, s->err, st,
+                                 attn_quantized ? s->qa : nullptr,
                                  attn_quantized ? s->da : nullptr,
                                  attn_quantized ? s->af : nullptr);
               });

@@ -180,15 +180,16 @@ bool attention_dec_applies(int hd, int T, int pos0, int n_ctx, bool pos_in_devic
 void launch_attention_dec(const float* q, const RopeIn& R, int layer, int T, int pos0, int H,
                           int KV, int n_ctx, float scale, float* out, const int* pos_dev,
                           int* err, hipStream_t s);
-// Whether launch_attention accepts pos_dev for this shape.
+// Whether the decode attention (launch_attention_dec) takes the position
+// from device memory for this shape (graph replay of single-position forwards).
 bool attention_pos_dev_supported(int hd, int T, int n_ctx);
 // Whether launch_attention writes the Q8A form of its output itself (the
 // chunked kernel, when qa / da / af are passed).
 bool attention_quantizes_q8a(int hd, int H, int KV, int T, int pos0, int n_ctx);
 void launch_attention(const float* q, const float* kc, const float* vc, int layer, int T, int pos0,
                       int H, int KV, int hd, int n_ctx, float scale, float* scores, float* out,
-                      const int* pos_dev, int* err, hipStream_t s, int8_t* qa = nullptr,
-                      float* da = nullptr, float* af = nullptr);
+                      int* err, hipStream_t s, int8_t* qa = nullptr, float* da = nullptr,
+                      float* af = nullptr);
 void launch_swiglu(const float* g, const float* u, int count, float* out, int* err, hipStream_t s);
 void launch_rope_table(float base, int rope_dim, int positions, float* cos_out, float* sin_out,
                        int* err, hipStream_t s);

@@ -332,7 +332,7 @@ __global__ void __launch_bounds__(64) k_gemv_q6k(DevMat W, const int8_t* __restr
   for (int k = 0; k < 8; k++) aux_s[lane][k] = aux[k];
   d_s[lane] = f16_to_f32(dw) * da;
   __syncthreads();
-  if (lane < rpw && blockIdx.x * rpw + lane < rows) {
+  if (lane < rpw && (int)blockIdx.x * rpw + lane < rows) {
     const int r = blockIdx.x * rpw + lane;
     float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int b = 0; b < nsb; b++) {
@@ -441,7 +441,7 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
           *reinterpret_cast<float4*>(ws + i) = wv[k];
 #pragma unroll
           for (int c = 0; c < 4; c++) {
-            bad |= !finite(xe[c]) | !finite(we[c]);
+            bad |= any_nonfinite(xe[c], we[c]);
             sq[((i & 7) + c) * cs + (i >> 3)] = xe[c] * xe[c];
           }
         }
@@ -503,7 +503,7 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
           const int e = span * 256 + 4 * lane;
           const bool inb = e < cols;
           float v[4] = {f[k].x, f[k].y, f[k].z, f[k].w};
-          if (inb) bad |= !finite(v[0]) | !finite(v[1]) | !finite(v[2]) | !finite(v[3]);
+          if (inb) bad |= any_nonfinite(v[0], v[1], v[2], v[3]);
           quantize_span(v, inb, (size_t)span * 256, true, false, q);
         }
       }

@@ -289,7 +289,7 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* x, const float* w,
   if (n % 4 != 0) {  // rows not float4-aligned (only the kernel-level entry point)
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
       const float v = xr[i];
-      bad |= !finite(v) | !finite(w[i]);
+      bad |= any_nonfinite(v, w[i]);
       xs[i] = v;
       sq[(i & 7) * cs + (i >> 3)] = v * v;
     }
@@ -315,7 +315,7 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* x, const float* w,
         *reinterpret_cast<float4*>(xs + i) = xv[k];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-          bad |= !finite(xe[c]) | !finite(we[c]);
+          bad |= any_nonfinite(xe[c], we[c]);
           sq[((i & 7) + c) * cs + (i >> 3)] = xe[c] * xe[c];
         }
       }
@@ -937,7 +937,7 @@ __global__ void __launch_bounds__(kDecThreads) k_attention_dec(const float* q, R
     const float c = R.rc[(size_t)ppos * half + j], sn = R.rs[(size_t)ppos * half + j];
     const float y0 = x0 * c - x1 * sn;
     const float y1 = x0 * sn + x1 * c;
-    bad |= !finite(y0) | !finite(y1);
+    bad |= any_nonfinite(y0, y1);
     base[ia] = y0;
     base[ib] = y1;
   }
@@ -945,7 +945,7 @@ __global__ void __launch_bounds__(kDecThreads) k_attention_dec(const float* q, R
   if (h % G == 0 && tid < hd) {
     const size_t off = (((size_t)layer * KV + g) * n_ctx + pos) * hd + tid;
     const float kv = kn[t][tid], vv = vn[t][tid];
-    bad |= !finite(kv) | !finite(vv);
+    bad |= any_nonfinite(kv, vv);
     R.kc[off] = kv;
     R.vc[off] = vv;
   }
@@ -1095,8 +1095,7 @@ bool attention_quantizes_q8a(int hd, int H, int KV, int T, int pos0, int n_ctx) 
 
 void launch_attention(const float* q, const float* kc, const float* vc, int layer, int T, int pos0,
                       int H, int KV, int hd, int n_ctx, float scale, float* scores, float* out,
-                      const int* pos_dev, int* err, hipStream_t s, int8_t* qa, float* da,
-                      float* af) {
+                      int* err, hipStream_t s, int8_t* qa, float* da, float* af) {
   int G = H / KV;
   if (hd == 64 && G >= 2 && G <= 16) {
     // Scores only need the longest row of this chunk (rounded to float4).

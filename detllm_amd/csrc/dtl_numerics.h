@@ -16,6 +16,14 @@ __device__ __forceinline__ double u2d(uint64_t u) { return __longlong_as_double(
 __device__ __forceinline__ uint64_t d2u(double d) { return (uint64_t)__double_as_longlong(d); }
 
 __device__ __forceinline__ bool finite(float x) { return (f2u(x) & 0x7f800000u) != 0x7f800000u; }
+// Whether any argument is Inf/NaN, without short-circuit branches (so the
+// loads behind the arguments are not serialised).
+__device__ __forceinline__ bool any_nonfinite(float a, float b) {
+  return ((int)!finite(a) | (int)!finite(b)) != 0;
+}
+__device__ __forceinline__ bool any_nonfinite(float a, float b, float c, float d) {
+  return ((int)!finite(a) | (int)!finite(b) | (int)!finite(c) | (int)!finite(d)) != 0;
+}
 
 // Rust `f32 as i32`: truncation toward zero, saturating, NaN -> 0.
 __device__ __forceinline__ int32_t f32_as_i32(float x) {
