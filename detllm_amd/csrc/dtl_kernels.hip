@@ -706,13 +706,16 @@ __global__ void __launch_bounds__(PER <= 2 ? 1024 : (PER <= 4 ? 512 : 256)) k_at
   // Tile loads: float4 index x = threadIdx.x + c * nthreads covers row
   // x / 16, columns 4 * (x % 16); rows at or past len are not read.
   float4 ring[D][PER];
+  // Loads are unconditional (slots past the tile or the row range read row
+  // 0, which commit never stores), so the compiler counts the loads in
+  // flight instead of draining them at every tile.
   auto issue = [&](float4 (&dst)[PER], const float* base, int j0) {
 #pragma unroll
     for (int c = 0; c < PER; c++) {
       const int x = threadIdx.x + c * nthreads;
       const int j = x >> 4;
-      if (x < 1024 && j0 + j < len)
-        dst[c] = *reinterpret_cast<const float4*>(base + (size_t)(j0 + j) * hd + (x & 15) * 4);
+      const bool ok = x < 1024 && j0 + j < len;
+      dst[c] = *reinterpret_cast<const float4*>(base + (size_t)(ok ? j0 + j : 0) * hd + (x & 15) * 4);
     }
   };
   auto commit_k = [&](const float4 (&src)[PER], float* buf, int j0) {
@@ -737,10 +740,9 @@ __global__ void __launch_bounds__(PER <= 2 ? 1024 : (PER <= 4 ? 512 : 256)) k_at
   };
   // scores: dot_f32_ref(q, k_j) * scale.  Tile k sits in ring slot k % D.
 #pragma unroll
-  for (int u = 0; u < D; u++)
-    if (u < ntiles) issue(ring[u], keys, u * kA64Tile);
+  for (int u = 0; u < D; u++) issue(ring[u], keys, u * kA64Tile);
   commit_k(ring[0], tiles, 0);
-  if (D < ntiles) issue(ring[0], keys, D * kA64Tile);
+  issue(ring[0], keys, D * kA64Tile);
   __syncthreads();
   for (int k0 = 0; k0 < ntiles; k0 += D) {
 #pragma unroll
@@ -768,18 +770,15 @@ __global__ void __launch_bounds__(PER <= 2 ? 1024 : (PER <= 4 ? 512 : 256)) k_at
         // tile k + 1 into the other buffer (its last reader, tile k - 1,
         // finished before the previous barrier); its slot then takes
         // tile k + 1 + D
-        if (k + 1 < ntiles) {
-          commit_k(ring[(u + 1) % D], tiles + ((k + 1) & 1) * kA64Buf, j0 + kA64Tile);
-          if (k + 1 + D < ntiles) issue(ring[(u + 1) % D], keys, j0 + (1 + D) * kA64Tile);
-        }
+        if (k + 1 < ntiles) commit_k(ring[(u + 1) % D], tiles + ((k + 1) & 1) * kA64Buf, j0 + kA64Tile);
       }
+      issue(ring[(u + 1) % D], keys, (k0 + u + 1 + D) * kA64Tile);
       __syncthreads();
     }
   }
   // The first V tiles' loads overlap the softmax.
 #pragma unroll
-  for (int u = 0; u < D; u++)
-    if (u < ntiles) issue(ring[u], vals, u * kA64Tile);
+  for (int u = 0; u < D; u++) issue(ring[u], vals, u * kA64Tile);
   // softmax_in_place (lib.rs:2361-2388), per wave
   float mx = -__builtin_huge_valf();
   for (int j = lane; j < len; j += 64) mx = fmaxf(mx, my[j]);
@@ -809,7 +808,7 @@ __global__ void __launch_bounds__(PER <= 2 ? 1024 : (PER <= 4 ? 512 : 256)) k_at
     my[j] = p;
   }
   commit_v(ring[0], tiles, 0);
-  if (D < ntiles) issue(ring[0], vals, D * kA64Tile);
+  issue(ring[0], vals, D * kA64Tile);
   __syncthreads();
   // P.V: out[d] = 0.0; out[d] += p_j * v_j[d] for j ascending
   float a = 0.0f;
@@ -841,11 +840,9 @@ __global__ void __launch_bounds__(PER <= 2 ? 1024 : (PER <= 4 ? 512 : 256)) k_at
         } else {
           for (int j = 0; j < n; j++) a += my[j0 + j] * cur[j * hd + lane];
         }
-        if (k + 1 < ntiles) {
-          commit_v(ring[(u + 1) % D], tiles + ((k + 1) & 1) * kA64Buf, j0 + kA64Tile);
-          if (k + 1 + D < ntiles) issue(ring[(u + 1) % D], vals, j0 + (1 + D) * kA64Tile);
-        }
+        if (k + 1 < ntiles) commit_v(ring[(u + 1) % D], tiles + ((k + 1) & 1) * kA64Buf, j0 + kA64Tile);
       }
+      issue(ring[(u + 1) % D], vals, (k0 + u + 1 + D) * kA64Tile);
       __syncthreads();
     }
   }
@@ -871,27 +868,6 @@ __global__ void __launch_bounds__(PER <= 2 ? 1024 : (PER <= 4 ? 512 : 256)) k_at
 // kDecDepth registers per thread, so kDecDepth tiles of loads are in flight
 // while wave 0 sums.
 constexpr int kDecThreads = 1024, kDecTile = 64, kDecStride = 68, kDecDepth = 8, kDecMaxT = 4;
-
-// dot_f32_ref of a 64-element query and key row (global or LDS), 8-lane order.
-__device__ __forceinline__ float dot64_8lane(const float* qs, const float* krow) {
-  const float4* kr = reinterpret_cast<const float4*>(krow);
-  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-  for (int half = 0; half < 2; half++) {
-    float4 kv[8];
-#pragma unroll
-    for (int i4 = 0; i4 < 8; i4++) kv[i4] = kr[8 * half + i4];
-#pragma unroll
-    for (int i4 = 0; i4 < 8; i4++) {
-      const int i = 32 * half + 4 * i4;
-      acc[(i + 0) & 7] += qs[i + 0] * kv[i4].x;
-      acc[(i + 1) & 7] += qs[i + 1] * kv[i4].y;
-      acc[(i + 2) & 7] += qs[i + 2] * kv[i4].z;
-      acc[(i + 3) & 7] += qs[i + 3] * kv[i4].w;
-    }
-  }
-  return finish_8lane(acc);
-}
 
 __global__ void __launch_bounds__(kDecThreads) k_attention_dec(const float* q, RopeIn R, int layer,
                                                                int pos0, int H, int KV, int n_ctx,
@@ -954,12 +930,49 @@ __global__ void __launch_bounds__(kDecThreads) k_attention_dec(const float* q, R
     if (bad) flag(err, ERRBIT_NON_FINITE);
     return;
   }
-  // scores: dot_f32_ref(q, k_j) * scale
-  for (int j = tid; j < len; j += kDecThreads) {
-    const float d = j < pb ? dot64_8lane(qs, keys + (size_t)j * hd) : dot64_8lane(qs, kn[j - pb]);
-    const float sv = d * scale;
-    if (!finite(sv)) bad = true;
-    sc[j] = sv;
+  // scores: dot_f32_ref(q, k_j) * scale.  Eight lanes per key: lane r forms
+  // the 8-lane accumulator r (dims r, r + 8, ..., r + 56 in order), three
+  // shuffle levels then give ((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)).  A round
+  // covers 128 keys; the key rows of kScoreDepth rounds are in flight.
+  {
+    constexpr int kKeysPerRound = kDecThreads / 8, kScoreDepth = 4;
+    const int r = tid & 7, kq = tid >> 3;
+    float qr[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) qr[u] = qs[r + 8 * u];
+    const int nrounds = (len + kKeysPerRound - 1) / kKeysPerRound;
+    // Key rows are loaded unconditionally (rows outside the cached part read
+    // row 0 and are replaced from LDS at use), so the loads in flight are
+    // counted rather than drained.
+    float kb[kScoreDepth][8];
+    auto load_keys = [&](float (&dst)[8], int round) {
+      const int j = kq + kKeysPerRound * round;
+      const float* kr = keys + (size_t)(j < pb ? j : 0) * hd + r;
+#pragma unroll
+      for (int u = 0; u < 8; u++) dst[u] = kr[8 * u];
+    };
+#pragma unroll
+    for (int d = 0; d < kScoreDepth; d++) load_keys(kb[d], d);
+    for (int r0 = 0; r0 < nrounds; r0 += kScoreDepth) {
+#pragma unroll
+      for (int d = 0; d < kScoreDepth; d++) {
+        const int round = r0 + d;
+        const int j = kq + kKeysPerRound * round;
+        const int jv = j - pb < 0 ? 0 : (j - pb < kDecMaxT ? j - pb : kDecMaxT - 1);
+        float acc = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc += qr[u] * (j < pb ? kb[d][u] : kn[jv][r + 8 * u]);
+        const float s1 = acc + __shfl_xor(acc, 1);
+        const float s2 = s1 + __shfl_xor(s1, 2);
+        const float s3 = s2 + __shfl_xor(s2, 4);
+        if (r == 0 && j < len) {
+          const float sv = s3 * scale;
+          if (!finite(sv)) bad = true;
+          sc[j] = sv;
+        }
+        load_keys(kb[d], round + kScoreDepth);
+      }
+    }
   }
   __syncthreads();
   // softmax_in_place (lib.rs:2361-2388)
@@ -994,46 +1007,58 @@ __global__ void __launch_bounds__(kDecThreads) k_attention_dec(const float* q, R
     sc[j] = p;
   }
   __syncthreads();
-  // P.V.  Thread tid owns row jr of each tile and dimensions c4 .. c4 + 3.
+  // P.V.  Thread tid owns row jr of each tile and dimensions c4 .. c4 + 3:
+  // a wave covers 16 rows x 16 dimensions, so its product stores (dimension-
+  // major) spread over all LDS banks while each row's 64 bytes stay one
+  // coalesced global segment.
   const int ntiles = (len + kDecTile - 1) / kDecTile;
-  const int jr = tid >> 4, c4 = (tid & 15) * 4;
+  const int jr = 16 * (wave & 3) + (lane & 15), c4 = 16 * (wave >> 2) + 4 * (lane >> 4);
+  // Every ring load is issued unconditionally (rows past the cached part
+  // read row 0 and are replaced at use), so the compiler can count the
+  // loads in flight instead of draining them all at each tile.
   float4 ring[kDecDepth];
 #pragma unroll
   for (int u = 0; u < kDecDepth; u++) {
     const int j = u * kDecTile + jr;
-    ring[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (j < pb) ring[u] = *reinterpret_cast<const float4*>(vals + (size_t)j * hd + c4);
-    else if (j < len) ring[u] = *reinterpret_cast<const float4*>(&vn[j - pb][c4]);
+    ring[u] = *reinterpret_cast<const float4*>(vals + (size_t)(j < pb ? j : 0) * hd + c4);
   }
   float a = 0.0f;
   for (int k0 = 0; k0 < ntiles; k0 += kDecDepth) {
 #pragma unroll
     for (int u = 0; u < kDecDepth; u++) {
       const int k = k0 + u;
+      const int j = k * kDecTile + jr;
+      // chunk rows come from LDS; rows past len contribute nothing
+      const int jv = j - pb < 0 ? 0 : (j - pb < kDecMaxT ? j - pb : kDecMaxT - 1);
+      const float4 vl = *reinterpret_cast<const float4*>(&vn[jv][c4]);
+      const float4 v = j < pb ? ring[u] : (j < len ? vl : make_float4(0.f, 0.f, 0.f, 0.f));
+      const float p = j < len ? sc[j < len ? j : 0] : 0.0f;
       if (k < ntiles) {
-        const int j = k * kDecTile + jr;
-        const float p = j < len ? sc[j] : 0.0f;
         float* pr = prod[k & 1];
-        pr[(c4 + 0) * kDecStride + jr] = p * ring[u].x;
-        pr[(c4 + 1) * kDecStride + jr] = p * ring[u].y;
-        pr[(c4 + 2) * kDecStride + jr] = p * ring[u].z;
-        pr[(c4 + 3) * kDecStride + jr] = p * ring[u].w;
-        const int jn = j + kDecDepth * kDecTile;
-        if (jn < pb) ring[u] = *reinterpret_cast<const float4*>(vals + (size_t)jn * hd + c4);
-        else if (jn < len) ring[u] = *reinterpret_cast<const float4*>(&vn[jn - pb][c4]);
+        pr[(c4 + 0) * kDecStride + jr] = p * v.x;
+        pr[(c4 + 1) * kDecStride + jr] = p * v.y;
+        pr[(c4 + 2) * kDecStride + jr] = p * v.z;
+        pr[(c4 + 3) * kDecStride + jr] = p * v.w;
       }
+      // issued on every step (rows outside the cached part read row 0)
+      const int jn = j + kDecDepth * kDecTile;
+      ring[u] = *reinterpret_cast<const float4*>(vals + (size_t)(jn < pb ? jn : 0) * hd + c4);
       __syncthreads();
       if (k < ntiles && wave == 0) {
         const float* pr = prod[k & 1] + lane * kDecStride;
         const int n = min(kDecTile, len - k * kDecTile);
         if (n == kDecTile) {
+          // all sixteen reads first, then the 64 adds in order
+          float4 p4[kDecTile / 4];
 #pragma unroll
-          for (int jj = 0; jj < kDecTile; jj += 4) {
-            const float4 p4 = *reinterpret_cast<const float4*>(pr + jj);
-            a += p4.x;
-            a += p4.y;
-            a += p4.z;
-            a += p4.w;
+          for (int q4 = 0; q4 < kDecTile / 4; q4++)
+            p4[q4] = *reinterpret_cast<const float4*>(pr + 4 * q4);
+#pragma unroll
+          for (int q4 = 0; q4 < kDecTile / 4; q4++) {
+            a += p4[q4].x;
+            a += p4[q4].y;
+            a += p4[q4].z;
+            a += p4[q4].w;
           }
         } else {
           for (int jj = 0; jj < n; jj++) a += pr[jj];
