@@ -695,16 +695,17 @@ int rows_per_wave(int rows) {
 }
 
 // Rows per wave for the f32-weight Q4_K kernel (DETLLM_Q4K_NK overrides):
-// one row per wave keeps two waves per SIMD on 2k-row matrices at 64
-// positions; the gate/up pair (and very tall matrices) have waves to spare
-// and amortise each activation read over two rows.
+// one row per wave keeps two waves per SIMD on 2k-row single matrices at 64
+// positions (measured fastest for wo and ffn_down); the gate/up pair, the
+// concatenated wq+wk and very tall matrices run faster amortising each
+// activation read over two rows.
 int q4k_nk(int mode, int rows_total) {
   static int forced = [] {
     const char* e = getenv("DETLLM_Q4K_NK");
     return e ? atoi(e) : 0;
   }();
   if (forced == 1 || forced == 2) return forced;
-  if (mode == MODE_PAIR) return 2;
+  if (mode == MODE_PAIR || mode == MODE_CAT) return 2;
   return rows_total >= 8192 ? 2 : 1;
 }
 

@@ -670,8 +670,8 @@ constexpr int kA64Tile = 64;           // K/V rows per tile
 constexpr int kA64KStride = 65;        // K^T row stride (conflict-free column reads)
 constexpr int kA64Buf = 64 * kA64KStride;
 
-template <int PER, int D>
-__global__ void __launch_bounds__(PER <= 2 ? 1024 : (PER <= 4 ? 512 : 256)) k_attention_hd64(const float* q, const float* kc,
+template <int PER, int D, int NT>
+__global__ void __launch_bounds__(NT) k_attention_hd64(const float* q, const float* kc,
                                                          const float* vc, int layer, int pos0,
                                                          int H, int KV, int n_ctx, int sc_stride,
                                                          float scale, float* out, QuantOut oq,
@@ -702,6 +702,22 @@ __global__ void __launch_bounds__(PER <= 2 ? 1024 : (PER <= 4 ? 512 : 256)) k_at
   float* my = sc + (size_t)wave * sc_stride;
   bool bad = false;
   qs[wave * hd + lane] = q[(size_t)t * H * hd + (size_t)h * hd + lane];
+  // With up to 512 threads there are registers for the whole query row in
+  // every lane (read once from memory, the same address for the wave), so
+  // the score loop reads only keys from LDS.
+  constexpr bool kQReg = NT <= 512;
+  float qr[kQReg ? 64 : 1];
+  if constexpr (kQReg) {
+    const float4* qg = reinterpret_cast<const float4*>(q + (size_t)t * H * hd + (size_t)h * hd);
+#pragma unroll
+    for (int i4 = 0; i4 < 16; i4++) {
+      const float4 v = qg[i4];
+      qr[4 * i4 + 0] = v.x;
+      qr[4 * i4 + 1] = v.y;
+      qr[4 * i4 + 2] = v.z;
+      qr[4 * i4 + 3] = v.w;
+    }
+  }
   const int ntiles = (len + kA64Tile - 1) / kA64Tile;
   // Tile loads: float4 index x = threadIdx.x + c * nthreads covers row
   // x / 16, columns 4 * (x % 16); rows at or past len are not read.
@@ -753,15 +769,24 @@ __global__ void __launch_bounds__(PER <= 2 ? 1024 : (PER <= 4 ? 512 : 256)) k_at
         const float* cur = tiles + (k & 1) * kA64Buf;
         if (j0 + lane < len) {
           float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-          const float4* qw = reinterpret_cast<const float4*>(qs + wave * hd);
+          if constexpr (kQReg) {
+            // the key column read in one batch, then 64 multiply-adds
+            float kv[64];
 #pragma unroll
-          for (int i4 = 0; i4 < 16; i4++) {
-            const float4 qv = qw[i4];
-            const int i = i4 * 4;
-            acc[(i + 0) & 7] += qv.x * cur[(i + 0) * kA64KStride + lane];
-            acc[(i + 1) & 7] += qv.y * cur[(i + 1) * kA64KStride + lane];
-            acc[(i + 2) & 7] += qv.z * cur[(i + 2) * kA64KStride + lane];
-            acc[(i + 3) & 7] += qv.w * cur[(i + 3) * kA64KStride + lane];
+            for (int i = 0; i < 64; i++) kv[i] = cur[i * kA64KStride + lane];
+#pragma unroll
+            for (int i = 0; i < 64; i++) acc[i & 7] += qr[i] * kv[i];
+          } else {
+            const float4* qw = reinterpret_cast<const float4*>(qs + wave * hd);
+#pragma unroll
+            for (int i4 = 0; i4 < 16; i4++) {
+              const float4 qv = qw[i4];
+              const int i = i4 * 4;
+              acc[(i + 0) & 7] += qv.x * cur[(i + 0) * kA64KStride + lane];
+              acc[(i + 1) & 7] += qv.y * cur[(i + 1) * kA64KStride + lane];
+              acc[(i + 2) & 7] += qv.z * cur[(i + 2) * kA64KStride + lane];
+              acc[(i + 3) & 7] += qv.w * cur[(i + 3) * kA64KStride + lane];
+            }
           }
           const float sv = finish_8lane(acc) * scale;
           if (!finite(sv)) bad = true;
@@ -1140,9 +1165,10 @@ void launch_attention(const float* q, const float* kc, const float* vc, int laye
         launch_kernel(kern, dim3(KV, T), dim3(G * 64), smem64, s, q, kc, vc, layer, pos0, H, KV,
                       n_ctx, sc_stride, scale, out, oq, err);
       };
-      if (per <= 2) go(k_attention_hd64<2, 8>);
-      else if (per <= 4) go(k_attention_hd64<4, 4>);
-      else go(k_attention_hd64<8, 2>);
+      if (G * 64 > 512) go(k_attention_hd64<2, 8, 1024>);
+      else if (per <= 2) go(k_attention_hd64<2, 8, 512>);
+      else if (per <= 4) go(k_attention_hd64<4, 4, 512>);
+      else go(k_attention_hd64<8, 2, 256>);
       return;
     }
   }
