@@ -246,56 +246,65 @@ def main() -> int:
     sess = model.forward_workspace(n, chunk)
     tail = 256
 
+    rows = np.arange(n - 1, dtype=np.uint32)
+    syms = toks[1:]
+
     def step():
-        out = []
+        """One teacher-forced encode: every position's forward and the range of
+        the next token, two chunks in flight (dtl_forward_ranges)."""
+        return sess.forward_ranges(toks, 0, rows, syms, tail)
+
+    def step_chunked():
+        """The same work one chunk at a time (dtl_forward_chunk +
+        dtl_symbol_ranges): launches never overlap, so per-launch events time
+        each kernel alone."""
+        out = [[], [], []]
         for p in range(0, n, chunk):
             sess.forward_chunk(toks[p:p + chunk], p)
             m = min(chunk, n - 1 - p)
             if m > 0:
-                out.append(sess.symbol_ranges(toks[p + 1:p + 1 + m], 0, tail))
-        return out
+                for dst, src in zip(out, sess.symbol_ranges(toks[p + 1:p + 1 + m], 0, tail)):
+                    dst.append(src)
+        return tuple(np.concatenate(x) for x in out)
 
     for i in range(args.warmup):
         t = time.time()
         step()
         log(f"[bench] warmup {i} {time.time() - t:.2f}s")
-    # One untimed step with every launch timed gives the per-class breakdown
-    # and picks the dominant class; the timed steps then bind events to that
-    # class's launches only, so timing barely perturbs the measured rate.
-    # Single-position workloads replay a captured graph per position, which
-    # per-launch events would disable: their timed steps run untimed and the
-    # roofline comes from the profiled step's (eager) launches.
-    graph_steps = chunk == 1
+    # Kernel timing runs on chunk-at-a-time steps, whose launches do not
+    # overlap: one step with every launch timed gives the per-class breakdown
+    # and picks the dominant class, a second times that class alone.  The
+    # timed steps then run the pipelined encode without per-launch events.
     breakdown = {}
     dom_name = None
-    dom_profiled = None
+    prof = {}
+    chunked = None
     if not args.no_kernel_timing:
         sess.set_profiling(True)
-        step()
+        chunked = step_chunked()
         breakdown = sess.profile()
         dom_name = max(breakdown.items(), key=lambda kv: kv[1]["total_ms"])[0]
-        dom_profiled = breakdown[dom_name]
-        if graph_steps:
-            sess.set_profiling(False)
-        else:
-            sess.set_profiling(True)
-            sess.profile_only(dom_name)
-        log(f"[bench] profiled step: dominant kernel class {dom_name}")
+        sess.set_profiling(True)
+        sess.profile_only(dom_name)
+        step_chunked()
+        prof = sess.profile()
+        sess.set_profiling(False)
+        log(f"[bench] profiled chunk-at-a-time steps: dominant kernel class {dom_name}")
     results = []
     t0 = time.perf_counter()
     for i in range(args.steps):
         results.append(step())
         log(f"[bench] step {i} done")
     t1 = time.perf_counter()
-    prof = sess.profile() if not graph_steps else ({dom_name: dom_profiled} if dom_name else {})
-    sess.set_profiling(False)
     elapsed = t1 - t0
     tokens_per_s = n * args.steps / elapsed
 
-    # Every step must produce the same ranges (run-to-run bit determinism).
-    flat = [np.concatenate([np.concatenate([c.astype(np.uint64), f.astype(np.uint64), tt]) for c, f, tt in r])
-            for r in results]
+    # Every step must produce the same ranges (run-to-run bit determinism),
+    # equal to the chunk-at-a-time path's.
+    flat = [np.concatenate([c.astype(np.uint64), f.astype(np.uint64), tt]) for c, f, tt in results]
     deterministic = all(np.array_equal(flat[0], f) for f in flat[1:])
+    if chunked is not None:
+        deterministic &= all(np.array_equal(a, b) for a, b in zip(results[0], chunked))
 
     if not prof:
         print(json.dumps({"value": round(tokens_per_s, 2), "ms_per_step": round(elapsed / args.steps * 1e3, 2),
@@ -316,8 +325,8 @@ def main() -> int:
         achieved = per_launch_bytes / (avg_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBS, 4)}
-    if graph_steps:
-        roofline["timed_over"] = "profiled step (eager launches); timed steps replay the captured graph"
+    roofline["timed_over"] = ("one chunk-at-a-time step timing the dominant class alone (launches not "
+                              "overlapped); the timed steps run two chunks in flight")
     roofline.update({"kernel": dom_name, "avg_launch_us": round(avg_ms * 1e3, 2), "launches": dom["launches"],
                      "algorithmic_bytes_per_launch": per_launch_bytes,
                      "algorithmic_flops_per_launch": per_launch_flops})
@@ -340,8 +349,8 @@ def main() -> int:
     ref = detref.Model(data)
     ref_logits = ref.logits(toks[:check_n])
     parity = True
-    # (cum, freq, total) of the first positions of the first timed step, across chunks
-    c0, f0, tt0 = (np.concatenate([r[k] for r in results[0]]) for k in range(3))
+    # (cum, freq, total) of the first positions of the first timed step
+    c0, f0, tt0 = results[0]
     for i in range(check_n):
         want = detref.symbol_range(ref_logits[i], int(toks[i + 1]), tail)
         parity &= (int(c0[i]), int(f0[i]), int(tt0[i])) == want

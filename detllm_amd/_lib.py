@@ -94,6 +94,7 @@ _SIGS = {
     "dtl_session_get_info": (C.c_int, [C.c_void_p, C.POINTER(sz), C.POINTER(sz), C.POINTER(sz)]),
     "dtl_symbol_ranges": (C.c_int, [C.c_void_p, sz, sz, u32p, sz, u64p, u32p, u64p]),
     "dtl_symbol_ranges_rows": (C.c_int, [C.c_void_p, sz, u32p, u32p, sz, u64p, u32p, u64p]),
+    "dtl_forward_ranges": (C.c_int, [C.c_void_p, u32p, sz, sz, sz, u32p, u32p, sz, u64p, u32p, u64p]),
     "dtl_cdf": (C.c_int, [C.c_void_p, sz, sz, u32p, u64p, u64p]),
     "dtl_decoder_total": (C.c_int, [C.c_void_p, sz, sz, u64p]),
     "dtl_decoder_lookup": (C.c_int, [C.c_void_p, sz, sz, C.c_uint64, u32p, u64p, u32p, u64p]),

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <memory>
@@ -34,10 +35,20 @@ int hip_status(hipError_t e) {
   return DTL_ERR_DEVICE;
 }
 
-#define HIP_TRY(expr)                    \
-  do {                                   \
-    hipError_t e_ = (expr);              \
-    if (e_ != hipSuccess) return hip_status(e_); \
+// DETLLM_TRACE_ERRORS=1 names the failing runtime call on stderr.
+int hip_fail(hipError_t e, const char* expr, int line) {
+  static const bool trace = [] {
+    const char* v = getenv("DETLLM_TRACE_ERRORS");
+    return v && *v && *v != '0';
+  }();
+  if (trace) std::fprintf(stderr, "detllm: %s (dtl_api.hip:%d): %s\n", expr, line, hipGetErrorString(e));
+  return hip_status(e);
+}
+
+#define HIP_TRY(expr)                                              \
+  do {                                                             \
+    hipError_t e_ = (expr);                                        \
+    if (e_ != hipSuccess) return hip_fail(e_, #expr, __LINE__);    \
   } while (0)
 
 // Owner of a set of device allocations, freed together.
@@ -615,12 +626,12 @@ const char* lm_head_class(int type) {
 
 }  // namespace
 
-struct dtl_session {
-  const dtl_model* m = nullptr;
-  size_t n_ctx = 0, max_chunk = 0, max_in = 0;
+// The buffers of one chunk in flight: activations, logits, the CDF staging,
+// the error flag and the stream its launches go to.  A session has two, so
+// the pipelined encode (dtl_forward_ranges) runs chunk c + 1 beside chunk c;
+// every other entry point works on lane 0.
+struct Lane {
   hipStream_t stream = nullptr;
-  Arena arena;
-  float *rope_cos = nullptr, *rope_sin = nullptr, *kc = nullptr, *vc = nullptr;
   float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
   float *g = nullptr, *u = nullptr, *ffo = nullptr, *logits = nullptr, *scores = nullptr;
   int8_t *qa = nullptr, *qk = nullptr;
@@ -634,13 +645,63 @@ struct dtl_session {
   uint32_t* c_rows = nullptr;    // row index per symbol (dtl_symbol_ranges_rows)
   // Row / tail whose decoder-total block results the scratch still holds.
   size_t cdf_ready_row = SIZE_MAX, cdf_ready_tail = SIZE_MAX;
-  // Captured single-position forward (see forward_device).
+  size_t rows_valid = 0;  // rows of `logits` written by the last forward
+  // Per layer: recorded once this lane's chunk has stored its K/V rows
+  // (pipelined encode only).
+  std::vector<hipEvent_t> kv_ready;
+  // Pinned host staging of the pipelined encode: token ids, symbol rows and
+  // symbols in; ranges and the error flag out.
+  uint32_t *h_tokens = nullptr, *h_rows = nullptr, *h_sym = nullptr, *h_freq = nullptr;
+  uint64_t *h_cum = nullptr, *h_total = nullptr;
+  int* h_err = nullptr;
+  size_t h_cap = 0;  // symbols the h_rows .. h_total staging holds
+};
+
+// Grows a lane's pinned symbol staging to n symbols (the lane must be idle).
+static int lane_reserve(Lane& L, size_t n) {
+  if (n <= L.h_cap) return DTL_OK;
+  for (void* p : {(void*)L.h_rows, (void*)L.h_sym, (void*)L.h_freq, (void*)L.h_cum, (void*)L.h_total})
+    if (p) (void)hipHostFree(p);
+  L.h_rows = L.h_sym = L.h_freq = nullptr;
+  L.h_cum = L.h_total = nullptr;
+  L.h_cap = 0;
+  HIP_TRY(hipHostMalloc((void**)&L.h_rows, n * 4, hipHostMallocDefault));
+  HIP_TRY(hipHostMalloc((void**)&L.h_sym, n * 4, hipHostMallocDefault));
+  HIP_TRY(hipHostMalloc((void**)&L.h_freq, n * 4, hipHostMallocDefault));
+  HIP_TRY(hipHostMalloc((void**)&L.h_cum, n * 8, hipHostMallocDefault));
+  HIP_TRY(hipHostMalloc((void**)&L.h_total, n * 8, hipHostMallocDefault));
+  L.h_cap = n;
+  return DTL_OK;
+}
+
+struct dtl_session {
+  const dtl_model* m = nullptr;
+  size_t n_ctx = 0, max_chunk = 0, max_in = 0;
+  Arena arena;
+  float *rope_cos = nullptr, *rope_sin = nullptr, *kc = nullptr, *vc = nullptr;
+  Lane lanes[2];
+  Lane* ln = &lanes[0];  // the lane the launches below go to
+  // Captured single-position forward (see forward_device), on lane 0.
   hipGraphExec_t graph = nullptr;
   bool graph_failed = false;
   int* pos_dev = nullptr;   // device copy of the position for the graph
   int* pos_host = nullptr;  // pinned staging for it
-  size_t rows_valid = 0;  // rows of `logits` written by the last forward
   Profiler prof;
+  ~dtl_session() {
+    for (Lane& L : lanes) {
+      if (L.stream) {
+        (void)hipStreamSynchronize(L.stream);
+        (void)hipStreamDestroy(L.stream);
+      }
+      for (hipEvent_t e : L.kv_ready)
+        if (e) (void)hipEventDestroy(e);
+      for (void* p : {(void*)L.h_tokens, (void*)L.h_rows, (void*)L.h_sym, (void*)L.h_freq,
+                      (void*)L.h_cum, (void*)L.h_total, (void*)L.h_err})
+        if (p) (void)hipHostFree(p);
+    }
+    if (graph) (void)hipGraphExecDestroy(graph);
+    if (pos_host) (void)hipHostFree(pos_host);
+  }
 };
 
 namespace {
@@ -653,14 +714,14 @@ size_t max_input_width(const dtl_model* m) {
 }
 
 int read_err(dtl_session* s, int* bits) {
-  HIP_TRY(hipMemcpyAsync(bits, s->err, sizeof(int), hipMemcpyDeviceToHost, s->stream));
-  HIP_TRY(hipStreamSynchronize(s->stream));
+  HIP_TRY(hipMemcpyAsync(bits, s->ln->err, sizeof(int), hipMemcpyDeviceToHost, s->ln->stream));
+  HIP_TRY(hipStreamSynchronize(s->ln->stream));
   return DTL_OK;
 }
 
 __global__ void k_clear_flag(int* p) { *p = 0; }
 
-void clear_err(dtl_session* s) { launch_kernel(k_clear_flag, dim3(1), dim3(1), 0, s->stream, s->err); }
+void clear_err(dtl_session* s) { launch_kernel(k_clear_flag, dim3(1), dim3(1), 0, s->ln->stream, s->ln->err); }
 
 // Which activation forms the given consumers need.
 void needed_forms(std::initializer_list<const DevMat*> consumers, bool* q8a, bool* q8k) {
@@ -680,11 +741,11 @@ double quant_bytes(bool q8a, bool q8k) {
 DevAct session_act(dtl_session* s, const float* x) {
   DevAct a{};
   a.x = x;
-  a.qa = s->qa;
-  a.da = s->da;
-  a.af = s->af;
-  a.qk = s->qk;
-  a.dk = s->dk;
+  a.qa = s->ln->qa;
+  a.da = s->ln->da;
+  a.af = s->ln->af;
+  a.qk = s->ln->qk;
+  a.dk = s->ln->dk;
   return a;
 }
 
@@ -695,21 +756,26 @@ DevAct prepare_input(dtl_session* s, const float* x, int T, int n,
   needed_forms(consumers, &q8a, &q8k);
   if (q8a || q8k) {
     double bytes = (double)T * n * (4.0 + quant_bytes(q8a, q8k));
-    s->prof.timed(s->stream, "quantize", bytes, 0.0, [&] {
-      launch_quantize(x, T, n, q8a, q8k, s->qa, s->da, s->af, s->qk, s->dk, s->err, s->stream);
+    s->prof.timed(s->ln->stream, "quantize", bytes, 0.0, [&] {
+      launch_quantize(x, T, n, q8a, q8k, s->ln->qa, s->ln->da, s->ln->af, s->ln->qk, s->ln->dk, s->ln->err, s->ln->stream);
     });
   }
   return session_act(s, x);
 }
 
 // forward_one_with_workspace (det-model lib.rs:1249-1400) for the T
-// positions whose token ids are in s->tokens: enqueues every launch on the
-// session stream (no host synchronisation).  pos_dev: when set, the
-// position-dependent kernels read pos0 from that device int.
-int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev) {
+// positions whose token ids are in the current lane's tokens: enqueues
+// every launch on the lane's stream (no host synchronisation).  pos_dev:
+// when set, the position-dependent kernels read pos0 from that device int.
+// after: a lane whose chunk (the positions just before these) is still in
+// flight; each layer's attention waits for that chunk's K/V rows of the
+// layer.  record_kv: record the lane's kv_ready event once each layer's rows
+// are stored.
+int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
+                    const Lane* after = nullptr, bool record_kv = false) {
   const dtl_model* m = s->m;
   const HostConfig& c = m->c;
-  hipStream_t st = s->stream;
+  hipStream_t st = s->ln->stream;
   clear_err(s);
   int d = (int)c.d, ff = (int)c.ff, H = (int)c.heads, KV = (int)c.kv_heads;
   int hd = (int)m->head_dim;
@@ -722,7 +788,7 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev) {
     double bytes = (double)W.rows * W.cols * weight_bytes_per_elem(W.type) +
                    (double)T * W.cols * act + (double)T * W.rows * (epi == EPI_RESIDUAL ? 8.0 : 4.0);
     P.timed(st, cls ? cls : gemm_class(W.type), bytes, (double)W.rows * W.cols * T,
-            [&] { launch_gemm(W, a, T, out, bias, epi, s->err, st); });
+            [&] { launch_gemm(W, a, T, out, bias, epi, s->ln->err, st); });
   };
   // rmsnorm of the residual stream into h, fused with the quantisation the
   // consumers of h need.
@@ -731,13 +797,13 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev) {
     needed_forms(consumers, &q8a, &q8k);
     P.timed(st, "rmsnorm_quantize", (double)T * d * (8.0 + quant_bytes(q8a, q8k)) + d * 4.0, 0.0,
             [&] {
-              launch_rmsnorm_quant(s->x, w, c.eps, T, d, s->h, q8a, q8k, s->qa, s->da, s->af,
-                                   s->qk, s->dk, s->err, st);
+              launch_rmsnorm_quant(s->ln->x, w, c.eps, T, d, s->ln->h, q8a, q8k, s->ln->qa, s->ln->da, s->ln->af,
+                                   s->ln->qk, s->ln->dk, s->ln->err, st);
             });
-    return session_act(s, s->h);
+    return session_act(s, s->ln->h);
   };
   P.timed(st, "embed", (double)T * d * (4.0 + weight_bytes_per_elem(m->emb.type)), 0.0,
-          [&] { launch_embed(m->emb, s->tokens, T, s->x, s->err, st); });
+          [&] { launch_embed(m->emb, s->ln->tokens, T, s->ln->x, s->ln->err, st); });
   // K and V rows read by one layer's attention over the chunk (GQA heads
   // of one group share them), and its multiply-accumulates.
   double kv_rows = 0.0;
@@ -771,7 +837,7 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev) {
     bytes += (double)T * mv[0]->cols * 4.0 + (double)T * rows_out * 4.0;
     FusedIn in{x, norm_w, c.eps};
     P.timed(st, cls, bytes, macs,
-            [&] { (void)launch_gemv_fused(mv, nm, pair, ov, bv, ev, in, T, s->err, st); });
+            [&] { (void)launch_gemv_fused(mv, nm, pair, ov, bv, ev, in, T, s->ln->err, st); });
   };
   auto fits = [&](std::initializer_list<const DevMat*> ms, bool pair, bool norm) {
     const DevMat* mv[3];
@@ -786,13 +852,13 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev) {
     DevAct a{};
     bool attn_quantized = false;
     if (fits({&L.wq, &L.wk, &L.wv}, false, true)) {
-      fused({&L.wq, &L.wk, &L.wv}, false, {s->q, s->k, s->v}, {L.bq, L.bk, L.bv}, {e_q, e_k, e_v},
-            s->x, L.attn_norm, "gemv_fused_qkv");
+      fused({&L.wq, &L.wk, &L.wv}, false, {s->ln->q, s->ln->k, s->ln->v}, {L.bq, L.bk, L.bv}, {e_q, e_k, e_v},
+            s->ln->x, L.attn_norm, "gemv_fused_qkv");
     } else if (fits({&L.wq}, false, true) && fits({&L.wk}, false, true) &&
                fits({&L.wv}, false, true)) {
-      fused({&L.wq}, false, {s->q}, {L.bq}, {e_q}, s->x, L.attn_norm, "gemv_fused_qkv");
-      fused({&L.wk}, false, {s->k}, {L.bk}, {e_k}, s->x, L.attn_norm, "gemv_fused_qkv");
-      fused({&L.wv}, false, {s->v}, {L.bv}, {e_v}, s->x, L.attn_norm, "gemv_fused_qkv");
+      fused({&L.wq}, false, {s->ln->q}, {L.bq}, {e_q}, s->ln->x, L.attn_norm, "gemv_fused_qkv");
+      fused({&L.wk}, false, {s->ln->k}, {L.bk}, {e_k}, s->ln->x, L.attn_norm, "gemv_fused_qkv");
+      fused({&L.wv}, false, {s->ln->v}, {L.bv}, {e_v}, s->ln->x, L.attn_norm, "gemv_fused_qkv");
     } else {
       a = rms(L.attn_norm, {&L.wq, &L.wk, &L.wv});
       if (L.wq.type == GGML_Q4_K && L.wk.type == GGML_Q4_K && L.wq.w32 && L.wk.w32 && T >= 16 &&
@@ -801,30 +867,36 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev) {
         double bytes = (double)(L.wq.rows + L.wk.rows) * L.wq.cols * weight_bytes_per_elem(GGML_Q4_K) +
                        (double)T * L.wq.cols * (1.0 + 4.0 / 32) + (double)T * (L.wq.rows + L.wk.rows) * 4.0;
         P.timed(st, "gemm_q4_k_qk", bytes, (double)(L.wq.rows + L.wk.rows) * L.wq.cols * T, [&] {
-          launch_gemm_cat_q4k(L.wq, L.wk, a, T, s->q, s->k, L.bq, L.bk, L.bq ? EPI_BIAS : EPI_STORE,
-                              s->err, st);
+          launch_gemm_cat_q4k(L.wq, L.wk, a, T, s->ln->q, s->ln->k, L.bq, L.bk, L.bq ? EPI_BIAS : EPI_STORE,
+                              s->ln->err, st);
         });
       } else {
-        gemm(L.wq, a, s->q, L.bq, L.bq ? EPI_BIAS : EPI_STORE, nullptr);
-        gemm(L.wk, a, s->k, L.bk, L.bk ? EPI_BIAS : EPI_STORE, nullptr);
+        gemm(L.wq, a, s->ln->q, L.bq, L.bq ? EPI_BIAS : EPI_STORE, nullptr);
+        gemm(L.wk, a, s->ln->k, L.bk, L.bk ? EPI_BIAS : EPI_STORE, nullptr);
       }
-      gemm(L.wv, a, s->v, L.bv, L.bv ? EPI_BIAS : EPI_STORE, nullptr);
+      gemm(L.wv, a, s->ln->v, L.bv, L.bv ? EPI_BIAS : EPI_STORE, nullptr);
     }
     if (attention_dec_applies(hd, T, (int)pos0, (int)s->n_ctx, pos_dev != nullptr)) {
       // RoPE and the cache store happen inside the decode attention.
-      const RopeIn R{s->k, s->v, s->rope_cos, s->rope_sin, (int)c.rope_dim, c.split_half ? 1 : 0,
+      if (after) HIP_TRY(hipStreamWaitEvent(st, after->kv_ready[l], 0));
+      const RopeIn R{s->ln->k, s->ln->v, s->rope_cos, s->rope_sin, (int)c.rope_dim, c.split_half ? 1 : 0,
                      s->kc, s->vc};
       P.timed(st, "attention", kv_rows * KV * hd * 8.0 + (double)T * (H + 3 * KV) * hd * 4.0,
               kv_rows * H * hd * 2.0, [&] {
-                launch_attention_dec(s->q, R, (int)l, T, (int)pos0, H, KV, (int)s->n_ctx,
-                                     c.attention_scale, s->attn, pos_dev, s->err, st);
+                launch_attention_dec(s->ln->q, R, (int)l, T, (int)pos0, H, KV, (int)s->n_ctx,
+                                     c.attention_scale, s->ln->attn, pos_dev, s->ln->err, st);
               });
+      if (record_kv) HIP_TRY(hipEventRecord(s->ln->kv_ready[l], st));
     } else {
       P.timed(st, "rope_store", (double)T * (H + 3 * KV) * hd * 8.0, 0.0, [&] {
-        launch_rope_store(s->q, s->k, s->v, s->rope_cos, s->rope_sin, T, (int)pos0, H, KV, hd,
+        launch_rope_store(s->ln->q, s->ln->k, s->ln->v, s->rope_cos, s->rope_sin, T, (int)pos0, H, KV, hd,
                           (int)c.rope_dim, c.split_half, s->kc, s->vc, (int)l, (int)s->n_ctx,
-                          pos_dev, s->err, st);
+                          pos_dev, s->ln->err, st);
       });
+      if (record_kv) HIP_TRY(hipEventRecord(s->ln->kv_ready[l], st));
+      // The store above writes only this chunk's rows; the attention below
+      // also reads the previous chunk's.
+      if (after) HIP_TRY(hipStreamWaitEvent(st, after->kv_ready[l], 0));
       // The chunked attention also writes the Q8A form wo reads, when that
       // is the only form wo needs.
       bool q8a, q8k;
@@ -833,27 +905,27 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev) {
                        attention_quantizes_q8a(hd, H, KV, T, (int)pos0, (int)s->n_ctx);
       P.timed(st, "attention", kv_rows * KV * hd * 8.0 + (double)T * H * hd * 8.0,
               kv_rows * H * hd * 2.0, [&] {
-                launch_attention(s->q, s->kc, s->vc, (int)l, T, (int)pos0, H, KV, hd,
-                                 (int)s->n_ctx, c.attention_scale, s->scores, s->attn, s->err, st,
-                                 attn_quantized ? s->qa : nullptr,
-                                 attn_quantized ? s->da : nullptr,
-                                 attn_quantized ? s->af : nullptr);
+                launch_attention(s->ln->q, s->kc, s->vc, (int)l, T, (int)pos0, H, KV, hd,
+                                 (int)s->n_ctx, c.attention_scale, s->ln->scores, s->ln->attn, s->ln->err, st,
+                                 attn_quantized ? s->ln->qa : nullptr,
+                                 attn_quantized ? s->ln->da : nullptr,
+                                 attn_quantized ? s->ln->af : nullptr);
               });
     }
     if (fits({&L.wo}, false, false)) {
-      fused({&L.wo}, false, {s->x}, {nullptr}, {EPI_RESIDUAL}, s->attn, nullptr, "gemv_fused_o");
+      fused({&L.wo}, false, {s->ln->x}, {nullptr}, {EPI_RESIDUAL}, s->ln->attn, nullptr, "gemv_fused_o");
     } else {
-      a = attn_quantized ? session_act(s, s->attn) : prepare_input(s, s->attn, T, H * hd, {&L.wo});
-      gemm(L.wo, a, s->x, nullptr, EPI_RESIDUAL, nullptr);
+      a = attn_quantized ? session_act(s, s->ln->attn) : prepare_input(s, s->ln->attn, T, H * hd, {&L.wo});
+      gemm(L.wo, a, s->ln->x, nullptr, EPI_RESIDUAL, nullptr);
     }
     if (fits({&L.gate, &L.up}, true, true)) {
-      fused({&L.gate, &L.up}, true, {s->ffo}, {nullptr, nullptr}, {EPI_STORE, EPI_STORE}, s->x,
+      fused({&L.gate, &L.up}, true, {s->ln->ffo}, {nullptr, nullptr}, {EPI_STORE, EPI_STORE}, s->ln->x,
             L.ffn_norm, "gemv_fused_gate_up");
     } else if (fits({&L.gate}, false, true) && fits({&L.up}, false, true)) {
-      fused({&L.gate}, false, {s->g}, {nullptr}, {EPI_STORE}, s->x, L.ffn_norm, "gemv_fused_gate_up");
-      fused({&L.up}, false, {s->u}, {nullptr}, {EPI_STORE}, s->x, L.ffn_norm, "gemv_fused_gate_up");
+      fused({&L.gate}, false, {s->ln->g}, {nullptr}, {EPI_STORE}, s->ln->x, L.ffn_norm, "gemv_fused_gate_up");
+      fused({&L.up}, false, {s->ln->u}, {nullptr}, {EPI_STORE}, s->ln->x, L.ffn_norm, "gemv_fused_gate_up");
       P.timed(st, "swiglu", (double)T * ff * 12.0, 0.0,
-              [&] { launch_swiglu(s->g, s->u, T * ff, s->ffo, s->err, st); });
+              [&] { launch_swiglu(s->ln->g, s->ln->u, T * ff, s->ln->ffo, s->ln->err, st); });
     } else {
       a = rms(L.ffn_norm, {&L.gate, &L.up});
       if (T >= 16 && L.gate.type == GGML_Q4_K && L.up.type == GGML_Q4_K &&
@@ -862,24 +934,24 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev) {
         double bytes = 2.0 * L.gate.rows * L.gate.cols * weight_bytes_per_elem(GGML_Q4_K) +
                        (double)T * d * (1.0 + 4.0 / 32) + (double)T * ff * 4.0;
         P.timed(st, "gemm_q4_k_gate_up", bytes, 2.0 * L.gate.rows * L.gate.cols * T, [&] {
-          launch_gemm_pair_swiglu_q4k(L.gate, L.up, a, T, nullptr, nullptr, s->ffo, s->err, st);
+          launch_gemm_pair_swiglu_q4k(L.gate, L.up, a, T, nullptr, nullptr, s->ln->ffo, s->ln->err, st);
         });
       } else {
-        gemm(L.gate, a, s->g, nullptr, EPI_STORE, nullptr);
-        gemm(L.up, a, s->u, nullptr, EPI_STORE, nullptr);
+        gemm(L.gate, a, s->ln->g, nullptr, EPI_STORE, nullptr);
+        gemm(L.up, a, s->ln->u, nullptr, EPI_STORE, nullptr);
         P.timed(st, "swiglu", (double)T * ff * 12.0, 0.0,
-                [&] { launch_swiglu(s->g, s->u, T * ff, s->ffo, s->err, st); });
+                [&] { launch_swiglu(s->ln->g, s->ln->u, T * ff, s->ln->ffo, s->ln->err, st); });
       }
     }
     if (fits({&L.down}, false, false)) {
-      fused({&L.down}, false, {s->x}, {nullptr}, {EPI_RESIDUAL}, s->ffo, nullptr, "gemv_fused_down");
+      fused({&L.down}, false, {s->ln->x}, {nullptr}, {EPI_RESIDUAL}, s->ln->ffo, nullptr, "gemv_fused_down");
     } else {
-      a = prepare_input(s, s->ffo, T, ff, {&L.down});
-      gemm(L.down, a, s->x, nullptr, EPI_RESIDUAL, nullptr);
+      a = prepare_input(s, s->ln->ffo, T, ff, {&L.down});
+      gemm(L.down, a, s->ln->x, nullptr, EPI_RESIDUAL, nullptr);
     }
   }
   DevAct a = rms(m->out_norm, {&m->out});
-  gemm(m->out, a, s->logits, nullptr, EPI_STORE, lm_head_class(m->out.type));
+  gemm(m->out, a, s->ln->logits, nullptr, EPI_STORE, lm_head_class(m->out.type));
   HIP_TRY(hipGetLastError());
   return DTL_OK;
 }
@@ -893,7 +965,7 @@ bool graph_eligible(const dtl_session* s) {
 }
 
 int capture_decode_graph(dtl_session* s) {
-  hipStream_t st = s->stream;
+  hipStream_t st = s->ln->stream;
   HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
   int rc = enqueue_forward(s, 1, 0, s->pos_dev);
   hipGraph_t g = nullptr;
@@ -915,11 +987,11 @@ int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t po
   if (T <= 0 || (size_t)T > s->max_chunk || pos0 + (size_t)T > s->n_ctx) return DTL_ERR_SHAPE;
   for (int t = 0; t < T; t++)
     if (tokens_host[t] >= (uint32_t)m->emb.rows) return DTL_ERR_SHAPE;
-  hipStream_t st = s->stream;
+  hipStream_t st = s->ln->stream;
   HIP_TRY(hipSetDevice(m->device));
-  s->rows_valid = 0;
-  s->cdf_ready_row = SIZE_MAX;
-  HIP_TRY(hipMemcpyAsync(s->tokens, tokens_host, T * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+  s->ln->rows_valid = 0;
+  s->ln->cdf_ready_row = SIZE_MAX;
+  HIP_TRY(hipMemcpyAsync(s->ln->tokens, tokens_host, T * sizeof(uint32_t), hipMemcpyHostToDevice, st));
   bool replayed = false;
   if (T == 1 && graph_eligible(s)) {
     if (!s->graph) (void)capture_decode_graph(s);
@@ -939,7 +1011,7 @@ int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t po
   if (rc) return rc;
   s->prof.collect();
   if (bits & ERRBIT_NON_FINITE) return DTL_ERR_NON_FINITE;
-  s->rows_valid = (size_t)T;
+  s->ln->rows_valid = (size_t)T;
   return DTL_OK;
 }
 
@@ -1101,7 +1173,6 @@ int dtl_session_new(const dtl_model* m, size_t n_ctx, size_t max_chunk, dtl_sess
   s->n_ctx = n_ctx;
   s->max_chunk = max_chunk;
   s->max_in = max_input_width(m);
-  HIP_TRY(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
   const HostConfig& c = m->c;
   size_t hd = m->head_dim, C = max_chunk, half = c.rope_dim / 2;
   Arena& A = s->arena;
@@ -1113,41 +1184,52 @@ int dtl_session_new(const dtl_model* m, size_t n_ctx, size_t max_chunk, dtl_sess
   ALLOC(rope_sin, n_ctx * half);
   ALLOC(kc, kv);
   ALLOC(vc, kv);
-  ALLOC(x, C * c.d);
-  ALLOC(h, C * c.d);
-  ALLOC(q, C * c.heads * hd);
-  ALLOC(k, C * c.kv_heads * hd);
-  ALLOC(v, C * c.kv_heads * hd);
-  ALLOC(attn, C * c.heads * hd);
-  ALLOC(g, C * c.ff);
-  ALLOC(u, C * c.ff);
-  ALLOC(ffo, C * c.ff);
-  ALLOC(logits, C * m->vocab);
-  ALLOC(scores, C * c.heads * n_ctx);
-  ALLOC(qa, C * s->max_in);
-  ALLOC(qk, C * s->max_in);
-  ALLOC(af, C * s->max_in);
-  ALLOC(da, C * (s->max_in / 32 + 1));
-  ALLOC(dk, C * (s->max_in / 256 + 1));
-  ALLOC(tokens, C);
-  ALLOC(err, 1);
-  ALLOC(c_sym, C);
-  ALLOC(c_freq, C);
-  ALLOC(c_cum, C);
-  ALLOC(c_total, C);
-  ALLOC(c_values, C);
-  ALLOC(c_freq_tab, m->vocab + 256);
-  ALLOC(c_cum_tab, m->vocab + 256);
-  ALLOC(c_scratch, cdf_scratch_bytes((int)C, (int)m->vocab));
   ALLOC(pos_dev, 1);
-  ALLOC(c_rows, C);
 #undef ALLOC
+  for (Lane& L : s->lanes) {
+    HIP_TRY(hipStreamCreateWithFlags(&L.stream, hipStreamNonBlocking));
+#define ALLOC(ptr, n) \
+  if ((st = A.alloc(&L.ptr, (n)))) return st;
+    ALLOC(x, C * c.d);
+    ALLOC(h, C * c.d);
+    ALLOC(q, C * c.heads * hd);
+    ALLOC(k, C * c.kv_heads * hd);
+    ALLOC(v, C * c.kv_heads * hd);
+    ALLOC(attn, C * c.heads * hd);
+    ALLOC(g, C * c.ff);
+    ALLOC(u, C * c.ff);
+    ALLOC(ffo, C * c.ff);
+    ALLOC(logits, C * m->vocab);
+    ALLOC(scores, C * c.heads * n_ctx);
+    ALLOC(qa, C * s->max_in);
+    ALLOC(qk, C * s->max_in);
+    ALLOC(af, C * s->max_in);
+    ALLOC(da, C * (s->max_in / 32 + 1));
+    ALLOC(dk, C * (s->max_in / 256 + 1));
+    ALLOC(tokens, C);
+    ALLOC(err, 1);
+    ALLOC(c_sym, C);
+    ALLOC(c_freq, C);
+    ALLOC(c_cum, C);
+    ALLOC(c_total, C);
+    ALLOC(c_values, C);
+    ALLOC(c_freq_tab, m->vocab + 256);
+    ALLOC(c_cum_tab, m->vocab + 256);
+    ALLOC(c_scratch, cdf_scratch_bytes((int)C, (int)m->vocab));
+    ALLOC(c_rows, C);
+#undef ALLOC
+    L.kv_ready.assign(c.block_count, nullptr);
+    for (hipEvent_t& e : L.kv_ready) HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    HIP_TRY(hipHostMalloc((void**)&L.h_tokens, C * 4, hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc((void**)&L.h_err, sizeof(int), hipHostMallocDefault));
+    if ((st = lane_reserve(L, C))) return st;
+  }
   HIP_TRY(hipHostMalloc((void**)&s->pos_host, sizeof(int), hipHostMallocDefault));
-  HIP_TRY(hipMemsetAsync(s->kc, 0, kv * 4, s->stream));
-  HIP_TRY(hipMemsetAsync(s->vc, 0, kv * 4, s->stream));
+  HIP_TRY(hipMemsetAsync(s->kc, 0, kv * 4, s->ln->stream));
+  HIP_TRY(hipMemsetAsync(s->vc, 0, kv * 4, s->ln->stream));
   clear_err(s.get());
-  launch_rope_table(c.rope_base, (int)c.rope_dim, (int)n_ctx, s->rope_cos, s->rope_sin, s->err,
-                    s->stream);
+  launch_rope_table(c.rope_base, (int)c.rope_dim, (int)n_ctx, s->rope_cos, s->rope_sin, s->ln->err,
+                    s->ln->stream);
   int bits = 0;
   if ((st = read_err(s.get(), &bits))) return st;
   if (bits) return DTL_ERR_NON_FINITE;
@@ -1158,23 +1240,17 @@ int dtl_session_new(const dtl_model* m, size_t n_ctx, size_t max_chunk, dtl_sess
 void dtl_session_free(dtl_session* s) {
   if (!s) return;
   (void)hipSetDevice(s->m->device);
-  if (s->stream) {
-    (void)hipStreamSynchronize(s->stream);
-    (void)hipStreamDestroy(s->stream);
-  }
-  if (s->graph) (void)hipGraphExecDestroy(s->graph);
-  if (s->pos_host) (void)hipHostFree(s->pos_host);
-  delete s;
+  delete s;  // ~dtl_session drains the lanes' streams before releasing them
 }
 
 int dtl_session_reset(dtl_session* s) {
   if (!s) return DTL_ERR_INVALID_ARGUMENT;
   HIP_TRY(hipSetDevice(s->m->device));
   size_t kv = s->m->c.block_count * s->m->c.kv_heads * s->n_ctx * s->m->head_dim;
-  HIP_TRY(hipMemsetAsync(s->kc, 0, kv * 4, s->stream));
-  HIP_TRY(hipMemsetAsync(s->vc, 0, kv * 4, s->stream));
-  HIP_TRY(hipStreamSynchronize(s->stream));
-  s->rows_valid = 0;
+  HIP_TRY(hipMemsetAsync(s->kc, 0, kv * 4, s->ln->stream));
+  HIP_TRY(hipMemsetAsync(s->vc, 0, kv * 4, s->ln->stream));
+  HIP_TRY(hipStreamSynchronize(s->ln->stream));
+  s->ln->rows_valid = 0;
   return DTL_OK;
 }
 
@@ -1184,9 +1260,9 @@ int dtl_forward_chunk(dtl_session* s, const uint32_t* tokens, size_t n, size_t p
   int st = forward_device(s, tokens, (int)n, pos0);
   if (st) return st;
   if (logits) {
-    HIP_TRY(hipMemcpyAsync(logits, s->logits, n * s->m->vocab * sizeof(float),
-                           hipMemcpyDeviceToHost, s->stream));
-    HIP_TRY(hipStreamSynchronize(s->stream));
+    HIP_TRY(hipMemcpyAsync(logits, s->ln->logits, n * s->m->vocab * sizeof(float),
+                           hipMemcpyDeviceToHost, s->ln->stream));
+    HIP_TRY(hipStreamSynchronize(s->ln->stream));
   }
   return DTL_OK;
 }
@@ -1197,11 +1273,11 @@ int dtl_forward_one(dtl_session* s, uint32_t token, size_t pos, float* logits) {
 
 int dtl_session_logits(dtl_session* s, size_t first, size_t n, float* out) {
   if (!s || !out) return DTL_ERR_INVALID_ARGUMENT;
-  if (first + n > s->rows_valid) return DTL_ERR_SHAPE;
+  if (first + n > s->ln->rows_valid) return DTL_ERR_SHAPE;
   HIP_TRY(hipSetDevice(s->m->device));
-  HIP_TRY(hipMemcpyAsync(out, s->logits + first * s->m->vocab, n * s->m->vocab * sizeof(float),
-                         hipMemcpyDeviceToHost, s->stream));
-  HIP_TRY(hipStreamSynchronize(s->stream));
+  HIP_TRY(hipMemcpyAsync(out, s->ln->logits + first * s->m->vocab, n * s->m->vocab * sizeof(float),
+                         hipMemcpyDeviceToHost, s->ln->stream));
+  HIP_TRY(hipStreamSynchronize(s->ln->stream));
   return DTL_OK;
 }
 
@@ -1234,22 +1310,22 @@ int dtl_symbol_ranges(dtl_session* s, size_t first, size_t n, const uint32_t* sy
                       size_t tail, uint64_t* cum, uint32_t* freq, uint64_t* total) {
   if (!s || !symbols || !cum || !freq || !total) return DTL_ERR_INVALID_ARGUMENT;
   size_t V = s->m->vocab;
-  if (n == 0 || first + n > s->rows_valid) return DTL_ERR_SHAPE;
+  if (n == 0 || first + n > s->ln->rows_valid) return DTL_ERR_SHAPE;
   if (V + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
   for (size_t i = 0; i < n; i++)
     if (symbols[i] >= V + tail) return DTL_ERR_CDF_SYMBOL_OUT_OF_RANGE;
   HIP_TRY(hipSetDevice(s->m->device));
   clear_err(s);
-  s->cdf_ready_row = SIZE_MAX;
-  HIP_TRY(hipMemcpyAsync(s->c_sym, symbols, n * 4, hipMemcpyHostToDevice, s->stream));
-  s->prof.timed(s->stream, "cdf_symbol_range", (double)n * V * 4.0, 0.0, [&] {
-    launch_cdf_blocks(s->logits + first * V, nullptr, (int)n, (int)V, (int)tail, 0, s->c_sym,
-                      nullptr, s->c_cum, s->c_freq, s->c_total, nullptr, s->c_scratch, false,
-                      s->err, s->stream);
+  s->ln->cdf_ready_row = SIZE_MAX;
+  HIP_TRY(hipMemcpyAsync(s->ln->c_sym, symbols, n * 4, hipMemcpyHostToDevice, s->ln->stream));
+  s->prof.timed(s->ln->stream, "cdf_symbol_range", (double)n * V * 4.0, 0.0, [&] {
+    launch_cdf_blocks(s->ln->logits + first * V, nullptr, (int)n, (int)V, (int)tail, 0, s->ln->c_sym,
+                      nullptr, s->ln->c_cum, s->ln->c_freq, s->ln->c_total, nullptr, s->ln->c_scratch, false,
+                      s->ln->err, s->ln->stream);
   });
-  HIP_TRY(hipMemcpyAsync(cum, s->c_cum, n * 8, hipMemcpyDeviceToHost, s->stream));
-  HIP_TRY(hipMemcpyAsync(freq, s->c_freq, n * 4, hipMemcpyDeviceToHost, s->stream));
-  HIP_TRY(hipMemcpyAsync(total, s->c_total, n * 8, hipMemcpyDeviceToHost, s->stream));
+  HIP_TRY(hipMemcpyAsync(cum, s->ln->c_cum, n * 8, hipMemcpyDeviceToHost, s->ln->stream));
+  HIP_TRY(hipMemcpyAsync(freq, s->ln->c_freq, n * 4, hipMemcpyDeviceToHost, s->ln->stream));
+  HIP_TRY(hipMemcpyAsync(total, s->ln->c_total, n * 8, hipMemcpyDeviceToHost, s->ln->stream));
   int bits = 0, st = read_err(s, &bits);
   s->prof.collect();
   return st ? st : cdf_status(bits);
@@ -1262,31 +1338,128 @@ int dtl_symbol_ranges_rows(dtl_session* s, size_t n, const uint32_t* rows, const
   if (n == 0) return DTL_ERR_SHAPE;
   if (V + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
   for (size_t i = 0; i < n; i++) {
-    if (rows[i] >= s->rows_valid) return DTL_ERR_SHAPE;
+    if (rows[i] >= s->ln->rows_valid) return DTL_ERR_SHAPE;
     if (symbols[i] >= V + tail) return DTL_ERR_CDF_SYMBOL_OUT_OF_RANGE;
   }
   HIP_TRY(hipSetDevice(s->m->device));
-  s->cdf_ready_row = SIZE_MAX;
+  s->ln->cdf_ready_row = SIZE_MAX;
   // batches of at most max_chunk symbols (the size of the staging buffers
   // and of the CDF scratch)
   for (size_t b0 = 0; b0 < n; b0 += s->max_chunk) {
     const size_t m = std::min(s->max_chunk, n - b0);
     clear_err(s);
-    HIP_TRY(hipMemcpyAsync(s->c_sym, symbols + b0, m * 4, hipMemcpyHostToDevice, s->stream));
-    HIP_TRY(hipMemcpyAsync(s->c_rows, rows + b0, m * 4, hipMemcpyHostToDevice, s->stream));
-    s->prof.timed(s->stream, "cdf_symbol_range", (double)m * V * 4.0, 0.0, [&] {
-      launch_cdf_blocks(s->logits, s->c_rows, (int)m, (int)V, (int)tail, 0, s->c_sym, nullptr,
-                        s->c_cum, s->c_freq, s->c_total, nullptr, s->c_scratch, false, s->err,
-                        s->stream);
+    HIP_TRY(hipMemcpyAsync(s->ln->c_sym, symbols + b0, m * 4, hipMemcpyHostToDevice, s->ln->stream));
+    HIP_TRY(hipMemcpyAsync(s->ln->c_rows, rows + b0, m * 4, hipMemcpyHostToDevice, s->ln->stream));
+    s->prof.timed(s->ln->stream, "cdf_symbol_range", (double)m * V * 4.0, 0.0, [&] {
+      launch_cdf_blocks(s->ln->logits, s->ln->c_rows, (int)m, (int)V, (int)tail, 0, s->ln->c_sym, nullptr,
+                        s->ln->c_cum, s->ln->c_freq, s->ln->c_total, nullptr, s->ln->c_scratch, false, s->ln->err,
+                        s->ln->stream);
     });
-    HIP_TRY(hipMemcpyAsync(cum + b0, s->c_cum, m * 8, hipMemcpyDeviceToHost, s->stream));
-    HIP_TRY(hipMemcpyAsync(freq + b0, s->c_freq, m * 4, hipMemcpyDeviceToHost, s->stream));
-    HIP_TRY(hipMemcpyAsync(total + b0, s->c_total, m * 8, hipMemcpyDeviceToHost, s->stream));
+    HIP_TRY(hipMemcpyAsync(cum + b0, s->ln->c_cum, m * 8, hipMemcpyDeviceToHost, s->ln->stream));
+    HIP_TRY(hipMemcpyAsync(freq + b0, s->ln->c_freq, m * 4, hipMemcpyDeviceToHost, s->ln->stream));
+    HIP_TRY(hipMemcpyAsync(total + b0, s->ln->c_total, m * 8, hipMemcpyDeviceToHost, s->ln->stream));
     int bits = 0, st = read_err(s, &bits);
     s->prof.collect();
     if (st) return st;
     if ((st = cdf_status(bits))) return st;
   }
+  return DTL_OK;
+}
+
+// The forwards and symbol ranges of encode_symbols_with_model (det-cli
+// main.rs:521-551) for one window, with two chunks in flight: chunk c runs
+// on lane c % 2, and chunk c + 1 starts while chunk c is still running (its
+// attention at each layer waits for chunk c's K/V rows of that layer; every
+// other launch is independent).  The host collects a lane's ranges before
+// reusing it.  Results equal dtl_forward_chunk + dtl_symbol_ranges_rows per
+// chunk.
+int dtl_forward_ranges(dtl_session* s, const uint32_t* tokens, size_t n, size_t pos0, size_t n_sym,
+                       const uint32_t* rows, const uint32_t* symbols, size_t tail, uint64_t* cum,
+                       uint32_t* freq, uint64_t* total) {
+  if (!s || !tokens || (n_sym && (!rows || !symbols || !cum || !freq || !total)))
+    return DTL_ERR_INVALID_ARGUMENT;
+  const dtl_model* m = s->m;
+  const size_t V = m->vocab, C = s->max_chunk;
+  if (n == 0 || pos0 + n > s->n_ctx) return DTL_ERR_SHAPE;
+  if (V + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
+  for (size_t i = 0; i < n; i++)
+    if (tokens[i] >= (uint32_t)m->emb.rows) return DTL_ERR_SHAPE;
+  for (size_t i = 0; i < n_sym; i++) {
+    if (rows[i] >= n || (i && rows[i] < rows[i - 1])) return DTL_ERR_SHAPE;
+    if (symbols[i] >= V + tail) return DTL_ERR_CDF_SYMBOL_OUT_OF_RANGE;
+  }
+  HIP_TRY(hipSetDevice(m->device));
+  // Back on lane 0 with both lanes drained however this returns.
+  struct Restore {
+    dtl_session* s;
+    ~Restore() {
+      for (Lane& L : s->lanes) (void)hipStreamSynchronize(L.stream);
+      s->ln = &s->lanes[0];
+    }
+  } restore{s};
+  for (Lane& L : s->lanes) {
+    L.rows_valid = 0;
+    L.cdf_ready_row = SIZE_MAX;
+  }
+  size_t first[2] = {0, 0}, count[2] = {0, 0};  // symbols of each lane's chunk
+  auto collect = [&](int li) -> int {
+    Lane& L = s->lanes[li];
+    HIP_TRY(hipStreamSynchronize(L.stream));
+    if (*L.h_err & ERRBIT_NON_FINITE) return DTL_ERR_NON_FINITE;
+    if (int st = cdf_status(*L.h_err)) return st;
+    for (size_t i = 0; i < count[li]; i++) {
+      cum[first[li] + i] = L.h_cum[i];
+      freq[first[li] + i] = L.h_freq[i];
+      total[first[li] + i] = L.h_total[i];
+    }
+    count[li] = 0;
+    return DTL_OK;
+  };
+  const size_t nchunks = (n + C - 1) / C;
+  size_t k = 0;
+  for (size_t c = 0; c < nchunks; c++) {
+    const int li = (int)(c & 1);
+    if (c >= 2)
+      if (int st = collect(li)) return st;
+    Lane& L = s->lanes[li];
+    s->ln = &L;
+    const size_t p0 = c * C, T = std::min(C, n - p0);
+    std::memcpy(L.h_tokens, tokens + p0, T * sizeof(uint32_t));
+    HIP_TRY(hipMemcpyAsync(L.tokens, L.h_tokens, T * 4, hipMemcpyHostToDevice, L.stream));
+    int rc = enqueue_forward(s, (int)T, pos0 + p0, nullptr, c ? &s->lanes[li ^ 1] : nullptr, true);
+    if (rc) return rc;
+    const size_t k0 = k;
+    while (k < n_sym && rows[k] < p0 + T) k++;
+    // Several symbols may share a row (byte escapes), so a chunk can code
+    // more symbols than it has rows: the host staging grows to fit, the
+    // device staging and CDF scratch take max_chunk symbols per launch.
+    const size_t ms = k - k0;
+    if (int st = lane_reserve(L, ms)) return st;
+    for (size_t i = 0; i < ms; i++) {
+      L.h_rows[i] = (uint32_t)(rows[k0 + i] - p0);
+      L.h_sym[i] = symbols[k0 + i];
+    }
+    for (size_t b0 = 0; b0 < ms; b0 += C) {
+      const size_t mb = std::min(C, ms - b0);
+      HIP_TRY(hipMemcpyAsync(L.c_rows, L.h_rows + b0, mb * 4, hipMemcpyHostToDevice, L.stream));
+      HIP_TRY(hipMemcpyAsync(L.c_sym, L.h_sym + b0, mb * 4, hipMemcpyHostToDevice, L.stream));
+      s->prof.timed(L.stream, "cdf_symbol_range", (double)mb * V * 4.0, 0.0, [&] {
+        launch_cdf_blocks(L.logits, L.c_rows, (int)mb, (int)V, (int)tail, 0, L.c_sym, nullptr,
+                          L.c_cum, L.c_freq, L.c_total, nullptr, L.c_scratch, false, L.err,
+                          L.stream);
+      });
+      HIP_TRY(hipMemcpyAsync(L.h_cum + b0, L.c_cum, mb * 8, hipMemcpyDeviceToHost, L.stream));
+      HIP_TRY(hipMemcpyAsync(L.h_freq + b0, L.c_freq, mb * 4, hipMemcpyDeviceToHost, L.stream));
+      HIP_TRY(hipMemcpyAsync(L.h_total + b0, L.c_total, mb * 8, hipMemcpyDeviceToHost, L.stream));
+    }
+    HIP_TRY(hipMemcpyAsync(L.h_err, L.err, sizeof(int), hipMemcpyDeviceToHost, L.stream));
+    first[li] = k0;
+    count[li] = ms;
+  }
+  // the last two chunks, oldest first
+  for (size_t c = nchunks > 2 ? nchunks - 2 : 0; c < nchunks; c++)
+    if (int st = collect((int)(c & 1))) return st;
+  s->prof.collect();
   return DTL_OK;
 }
 
@@ -1300,14 +1473,14 @@ int dtl_session_get_info(const dtl_session* s, size_t* n_ctx, size_t* max_chunk,
 
 int dtl_session_set_profiling(dtl_session* s, int enable) {
   if (!s) return DTL_ERR_INVALID_ARGUMENT;
-  HIP_TRY(hipStreamSynchronize(s->stream));
+  HIP_TRY(hipStreamSynchronize(s->ln->stream));
   s->prof.enable(enable != 0);
   return DTL_OK;
 }
 
 int dtl_session_profile_only(dtl_session* s, const char* kernel_class) {
   if (!s) return DTL_ERR_INVALID_ARGUMENT;
-  HIP_TRY(hipStreamSynchronize(s->stream));
+  HIP_TRY(hipStreamSynchronize(s->ln->stream));
   s->prof.only(kernel_class);
   return DTL_OK;
 }
@@ -1324,16 +1497,16 @@ int dtl_cdf(dtl_session* s, size_t row, size_t tail, uint32_t* freq, uint64_t* c
             uint64_t* total) {
   if (!s || !freq || !cum || !total) return DTL_ERR_INVALID_ARGUMENT;
   size_t V = s->m->vocab;
-  if (row >= s->rows_valid) return DTL_ERR_SHAPE;
+  if (row >= s->ln->rows_valid) return DTL_ERR_SHAPE;
   if (V + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
   if (tail > 256) return DTL_ERR_INVALID_ARGUMENT;  // table staging holds vocab + 256 entries
   HIP_TRY(hipSetDevice(s->m->device));
   clear_err(s);
-  launch_cdf(s->logits + row * V, 1, (int)V, (int)tail, 1, nullptr, nullptr, nullptr, nullptr,
-             s->c_total, nullptr, s->c_freq_tab, s->c_cum_tab, s->err, s->stream);
-  HIP_TRY(hipMemcpyAsync(freq, s->c_freq_tab, (V + tail) * 4, hipMemcpyDeviceToHost, s->stream));
-  HIP_TRY(hipMemcpyAsync(cum, s->c_cum_tab, (V + tail) * 8, hipMemcpyDeviceToHost, s->stream));
-  HIP_TRY(hipMemcpyAsync(total, s->c_total, 8, hipMemcpyDeviceToHost, s->stream));
+  launch_cdf(s->ln->logits + row * V, 1, (int)V, (int)tail, 1, nullptr, nullptr, nullptr, nullptr,
+             s->ln->c_total, nullptr, s->ln->c_freq_tab, s->ln->c_cum_tab, s->ln->err, s->ln->stream);
+  HIP_TRY(hipMemcpyAsync(freq, s->ln->c_freq_tab, (V + tail) * 4, hipMemcpyDeviceToHost, s->ln->stream));
+  HIP_TRY(hipMemcpyAsync(cum, s->ln->c_cum_tab, (V + tail) * 8, hipMemcpyDeviceToHost, s->ln->stream));
+  HIP_TRY(hipMemcpyAsync(total, s->ln->c_total, 8, hipMemcpyDeviceToHost, s->ln->stream));
   int bits = 0, st = read_err(s, &bits);
   return st ? st : cdf_status(bits);
 }
@@ -1341,20 +1514,20 @@ int dtl_cdf(dtl_session* s, size_t row, size_t tail, uint32_t* freq, uint64_t* c
 int dtl_decoder_total(dtl_session* s, size_t row, size_t tail, uint64_t* total) {
   if (!s || !total) return DTL_ERR_INVALID_ARGUMENT;
   size_t V = s->m->vocab;
-  if (row >= s->rows_valid) return DTL_ERR_SHAPE;
+  if (row >= s->ln->rows_valid) return DTL_ERR_SHAPE;
   if (V + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
   HIP_TRY(hipSetDevice(s->m->device));
   clear_err(s);
-  launch_cdf_blocks(s->logits + row * V, nullptr, 1, (int)V, (int)tail, 3, nullptr, nullptr,
-                    nullptr, nullptr, s->c_total, nullptr, s->c_scratch, false, s->err, s->stream);
-  HIP_TRY(hipMemcpyAsync(total, s->c_total, 8, hipMemcpyDeviceToHost, s->stream));
+  launch_cdf_blocks(s->ln->logits + row * V, nullptr, 1, (int)V, (int)tail, 3, nullptr, nullptr,
+                    nullptr, nullptr, s->ln->c_total, nullptr, s->ln->c_scratch, false, s->ln->err, s->ln->stream);
+  HIP_TRY(hipMemcpyAsync(total, s->ln->c_total, 8, hipMemcpyDeviceToHost, s->ln->stream));
   int bits = 0, st = read_err(s, &bits);
   if (st) return st;
   st = cdf_status(bits);
   if (st == DTL_OK) {
     // The block results of this row stay in the scratch for a lookup.
-    s->cdf_ready_row = row;
-    s->cdf_ready_tail = tail;
+    s->ln->cdf_ready_row = row;
+    s->ln->cdf_ready_tail = tail;
   }
   return st;
 }
@@ -1363,19 +1536,19 @@ int dtl_decoder_lookup(dtl_session* s, size_t row, size_t tail, uint64_t value, 
                        uint64_t* cum, uint32_t* freq, uint64_t* total) {
   if (!s || !symbol || !cum || !freq || !total) return DTL_ERR_INVALID_ARGUMENT;
   size_t V = s->m->vocab;
-  if (row >= s->rows_valid) return DTL_ERR_SHAPE;
+  if (row >= s->ln->rows_valid) return DTL_ERR_SHAPE;
   if (V + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
   HIP_TRY(hipSetDevice(s->m->device));
   clear_err(s);
-  HIP_TRY(hipMemcpyAsync(s->c_values, &value, 8, hipMemcpyHostToDevice, s->stream));
-  const bool reuse = s->cdf_ready_row == row && s->cdf_ready_tail == tail;
-  launch_cdf_blocks(s->logits + row * V, nullptr, 1, (int)V, (int)tail, 2, nullptr, s->c_values,
-                    s->c_cum, s->c_freq, s->c_total, s->c_sym, s->c_scratch, reuse, s->err,
-                    s->stream);
-  HIP_TRY(hipMemcpyAsync(symbol, s->c_sym, 4, hipMemcpyDeviceToHost, s->stream));
-  HIP_TRY(hipMemcpyAsync(cum, s->c_cum, 8, hipMemcpyDeviceToHost, s->stream));
-  HIP_TRY(hipMemcpyAsync(freq, s->c_freq, 4, hipMemcpyDeviceToHost, s->stream));
-  HIP_TRY(hipMemcpyAsync(total, s->c_total, 8, hipMemcpyDeviceToHost, s->stream));
+  HIP_TRY(hipMemcpyAsync(s->ln->c_values, &value, 8, hipMemcpyHostToDevice, s->ln->stream));
+  const bool reuse = s->ln->cdf_ready_row == row && s->ln->cdf_ready_tail == tail;
+  launch_cdf_blocks(s->ln->logits + row * V, nullptr, 1, (int)V, (int)tail, 2, nullptr, s->ln->c_values,
+                    s->ln->c_cum, s->ln->c_freq, s->ln->c_total, s->ln->c_sym, s->ln->c_scratch, reuse, s->ln->err,
+                    s->ln->stream);
+  HIP_TRY(hipMemcpyAsync(symbol, s->ln->c_sym, 4, hipMemcpyDeviceToHost, s->ln->stream));
+  HIP_TRY(hipMemcpyAsync(cum, s->ln->c_cum, 8, hipMemcpyDeviceToHost, s->ln->stream));
+  HIP_TRY(hipMemcpyAsync(freq, s->ln->c_freq, 4, hipMemcpyDeviceToHost, s->ln->stream));
+  HIP_TRY(hipMemcpyAsync(total, s->ln->c_total, 8, hipMemcpyDeviceToHost, s->ln->stream));
   int bits = 0, st = read_err(s, &bits);
   if (st) return st;
   if (value >= *total) return DTL_ERR_CDF_SYMBOL_OUT_OF_RANGE;

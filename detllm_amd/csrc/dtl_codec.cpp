@@ -78,9 +78,8 @@ int encode_payload(dtl_session* s, const uint32_t* symbols, size_t n, size_t ove
       w.toks.push_back(sym);
     }
   }
-  // Device work: each window from a fresh cache, forwards in chunks of up to
-  // max_chunk positions; the symbols coded against a chunk's rows get their
-  // ranges from one call.
+  // Device work: each window from a fresh cache; its forwards and the
+  // ranges of the symbols coded against them come from one pipelined call.
   std::vector<Range3> ranges(n);
   std::vector<size_t> by_window_start(windows.size() + 1, 0);
   {
@@ -106,34 +105,29 @@ int encode_payload(dtl_session* s, const uint32_t* symbols, size_t n, size_t ove
       if ((st = dtl_uniform_symbol_range(symbols[k], V + tail, &c, &f, &t))) return st;
       ranges[k] = {c, t, f};
     }
-    if (win.toks.empty()) continue;
+    rows.clear();
+    syms.clear();
+    for (size_t k = k0; k < k1; k++) {
+      if (sym_row[k] == SIZE_MAX) continue;
+      rows.push_back((uint32_t)sym_row[k]);
+      syms.push_back(symbols[k]);
+    }
+    if (rows.empty()) continue;
     if ((st = dtl_session_reset(s))) return st;
-    size_t k = k0;
-    for (size_t p0 = 0; p0 < win.toks.size(); p0 += in.max_chunk) {
-      const size_t T = std::min(in.max_chunk, win.toks.size() - p0);
-      if ((st = dtl_forward_chunk(s, win.toks.data() + p0, T, p0, nullptr))) return st;
-      rows.clear();
-      syms.clear();
-      const size_t kfirst = k;
-      for (; k < k1; k++) {
-        if (sym_row[k] == SIZE_MAX) continue;
-        if (sym_row[k] >= p0 + T) break;
-        rows.push_back((uint32_t)(sym_row[k] - p0));
-        syms.push_back(symbols[k]);
-      }
-      if (rows.empty()) continue;
-      cum.resize(rows.size());
-      freq.resize(rows.size());
-      total.resize(rows.size());
-      if ((st = dtl_symbol_ranges_rows(s, rows.size(), rows.data(), syms.data(), tail, cum.data(),
-                                       freq.data(), total.data())))
-        return st;
-      size_t j = 0;
-      for (size_t q = kfirst; q < k; q++) {
-        if (sym_row[q] == SIZE_MAX) continue;
-        ranges[q] = {cum[j], total[j], freq[j]};
-        j++;
-      }
+    // Tokens after the last coded row only advance a state the next window
+    // discards, so the forwards stop there.
+    cum.resize(rows.size());
+    freq.resize(rows.size());
+    total.resize(rows.size());
+    if ((st = dtl_forward_ranges(s, win.toks.data(), (size_t)rows.back() + 1, 0, rows.size(),
+                                 rows.data(), syms.data(), tail, cum.data(), freq.data(),
+                                 total.data())))
+      return st;
+    size_t j = 0;
+    for (size_t k = k0; k < k1; k++) {
+      if (sym_row[k] == SIZE_MAX) continue;
+      ranges[k] = {cum[j], total[j], freq[j]};
+      j++;
     }
   }
   dtl_range_encoder* enc = nullptr;

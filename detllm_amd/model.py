@@ -252,6 +252,44 @@ class Session:
         )
         return cum, freq, total
 
+    def symbol_ranges_rows(self, rows: Sequence[int], symbols: Sequence[int], tail_symbols: int = 0):
+        """logits_to_symbol_range_* of symbols[i] against row rows[i] of the last forward."""
+        r = np.ascontiguousarray(np.asarray(rows, dtype=np.uint32))
+        sym = np.ascontiguousarray(np.asarray(symbols, dtype=np.uint32))
+        if r.size != sym.size:
+            raise ValueError("rows and symbols differ in length")
+        n = sym.size
+        cum = np.empty(n, np.uint64)
+        freq = np.empty(n, np.uint32)
+        total = np.empty(n, np.uint64)
+        check(
+            lib.dtl_symbol_ranges_rows(self._h, n, ptr(r, C.c_uint32), ptr(sym, C.c_uint32), tail_symbols,
+                                       ptr(cum, C.c_uint64), ptr(freq, C.c_uint32), ptr(total, C.c_uint64)),
+            "dtl_symbol_ranges_rows",
+        )
+        return cum, freq, total
+
+    def forward_ranges(self, tokens: Sequence[int], pos0: int, rows: Sequence[int], symbols: Sequence[int],
+                       tail_symbols: int = 0):
+        """Forwards of tokens at pos0.. (chunks of max_chunk, two in flight) and the
+        range of symbols[i] under the logits of token rows[i]: (cum, freq, total)."""
+        toks = _tokens(tokens)
+        r = np.ascontiguousarray(np.asarray(rows, dtype=np.uint32))
+        sym = np.ascontiguousarray(np.asarray(symbols, dtype=np.uint32))
+        if r.size != sym.size:
+            raise ValueError("rows and symbols differ in length")
+        n = sym.size
+        cum = np.empty(max(n, 1), np.uint64)
+        freq = np.empty(max(n, 1), np.uint32)
+        total = np.empty(max(n, 1), np.uint64)
+        check(
+            lib.dtl_forward_ranges(self._h, ptr(toks, C.c_uint32), toks.size, int(pos0), n,
+                                   ptr(r, C.c_uint32), ptr(sym, C.c_uint32), tail_symbols,
+                                   ptr(cum, C.c_uint64), ptr(freq, C.c_uint32), ptr(total, C.c_uint64)),
+            "dtl_forward_ranges",
+        )
+        return cum[:n], freq[:n], total[:n]
+
     def cdf(self, row: int = 0, tail_symbols: int = 0):
         """logits_to_cdf_* of one row: (freq[u32], cum[u64], total)."""
         n = self.model.vocab + tail_symbols

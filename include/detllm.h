@@ -200,6 +200,19 @@ int dtl_symbol_ranges_rows(dtl_session *session, size_t n, const uint32_t *rows,
                            const uint32_t *symbols, size_t tail_symbols, uint64_t *cum,
                            uint32_t *freq, uint64_t *total);
 
+/* The forwards and symbol ranges of one codec window in one call: the
+ * per-token loop of encode_symbols_with_model (det-cli main.rs:521-551:
+ * state.sync / symbol_range / advance), batched.  Forwards tokens[0..n) at
+ * positions pos0.. in chunks of the session's max_chunk and codes
+ * symbols[i] against the logits of token rows[i] (rows relative to pos0,
+ * non-decreasing, < n).  The same results as dtl_forward_chunk followed by
+ * dtl_symbol_ranges_rows per chunk; two chunks are in flight on two
+ * streams.  Afterwards no logits rows are valid (dtl_session_logits and
+ * dtl_cdf need a new forward). */
+int dtl_forward_ranges(dtl_session *session, const uint32_t *tokens, size_t n, size_t pos0,
+                       size_t n_sym, const uint32_t *rows, const uint32_t *symbols,
+                       size_t tail_symbols, uint64_t *cum, uint32_t *freq, uint64_t *total);
+
 /* logits_to_cdf_with_scratch / _with_byte_escapes (cdf.rs:52-106): the
  * full table for one row; freq and cum hold vocab + tail_symbols entries. */
 int dtl_cdf(dtl_session *session, size_t row, size_t tail_symbols, uint32_t *freq, uint64_t *cum,
