@@ -251,7 +251,7 @@ def main() -> int:
 
     def step():
         """One teacher-forced encode: every position's forward and the range of
-        the next token, two chunks in flight (dtl_forward_ranges)."""
+        the next token, three chunks in flight (dtl_forward_ranges)."""
         return sess.forward_ranges(toks, 0, rows, syms, tail)
 
     def step_chunked():
@@ -326,7 +326,7 @@ def main() -> int:
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBS, 4)}
     roofline["timed_over"] = ("one chunk-at-a-time step timing the dominant class alone (launches not "
-                              "overlapped); the timed steps run two chunks in flight")
+                              "overlapped); the timed steps run three chunks in flight")
     roofline.update({"kernel": dom_name, "avg_launch_us": round(avg_ms * 1e3, 2), "launches": dom["launches"],
                      "algorithmic_bytes_per_launch": per_launch_bytes,
                      "algorithmic_flops_per_launch": per_launch_flops})

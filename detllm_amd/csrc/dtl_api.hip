@@ -627,9 +627,13 @@ const char* lm_head_class(int type) {
 }  // namespace
 
 // The buffers of one chunk in flight: activations, logits, the CDF staging,
-// the error flag and the stream its launches go to.  A session has two, so
-// the pipelined encode (dtl_forward_ranges) runs chunk c + 1 beside chunk c;
-// every other entry point works on lane 0.
+// the error flag and the stream its launches go to.  A session has kLanes of
+// them, so the pipelined encode (dtl_forward_ranges) runs chunks c + 1 and
+// c + 2 beside chunk c; every other entry point works on lane 0.
+// Three measured fastest on MI355X for the 64-position encode (two: 12.5k,
+// four: 12.0k tokens/s; the process has four hardware queues).
+constexpr int kLanes = 3;
+
 struct Lane {
   hipStream_t stream = nullptr;
   float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
@@ -679,7 +683,7 @@ struct dtl_session {
   size_t n_ctx = 0, max_chunk = 0, max_in = 0;
   Arena arena;
   float *rope_cos = nullptr, *rope_sin = nullptr, *kc = nullptr, *vc = nullptr;
-  Lane lanes[2];
+  Lane lanes[kLanes];
   Lane* ln = &lanes[0];  // the lane the launches below go to
   // Captured single-position forward (see forward_device), on lane 0.
   hipGraphExec_t graph = nullptr;
@@ -768,9 +772,10 @@ DevAct prepare_input(dtl_session* s, const float* x, int T, int n,
 // every launch on the lane's stream (no host synchronisation).  pos_dev:
 // when set, the position-dependent kernels read pos0 from that device int.
 // after: a lane whose chunk (the positions just before these) is still in
-// flight; each layer's attention waits for that chunk's K/V rows of the
-// layer.  record_kv: record the lane's kv_ready event once each layer's rows
-// are stored.
+// flight; each layer's attention waits for that lane's kv_ready event of the
+// layer.  record_kv: record this lane's kv_ready event of each layer once
+// its rows are stored and the wait above has passed, so the event covers
+// the rows of every earlier chunk too (the chain of lanes is transitive).
 int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
                     const Lane* after = nullptr, bool record_kv = false) {
   const dtl_model* m = s->m;
@@ -893,10 +898,11 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
                           (int)c.rope_dim, c.split_half, s->kc, s->vc, (int)l, (int)s->n_ctx,
                           pos_dev, s->ln->err, st);
       });
-      if (record_kv) HIP_TRY(hipEventRecord(s->ln->kv_ready[l], st));
       // The store above writes only this chunk's rows; the attention below
-      // also reads the previous chunk's.
+      // also reads the earlier chunks'.  The event is recorded after the
+      // wait, so it marks every chunk's rows up to this one as stored.
       if (after) HIP_TRY(hipStreamWaitEvent(st, after->kv_ready[l], 0));
+      if (record_kv) HIP_TRY(hipEventRecord(s->ln->kv_ready[l], st));
       // The chunked attention also writes the Q8A form wo reads, when that
       // is the only form wo needs.
       bool q8a, q8k;
@@ -1367,12 +1373,12 @@ int dtl_symbol_ranges_rows(dtl_session* s, size_t n, const uint32_t* rows, const
 }
 
 // The forwards and symbol ranges of encode_symbols_with_model (det-cli
-// main.rs:521-551) for one window, with two chunks in flight: chunk c runs
-// on lane c % 2, and chunk c + 1 starts while chunk c is still running (its
-// attention at each layer waits for chunk c's K/V rows of that layer; every
-// other launch is independent).  The host collects a lane's ranges before
-// reusing it.  Results equal dtl_forward_chunk + dtl_symbol_ranges_rows per
-// chunk.
+// main.rs:521-551) for one window, with kLanes chunks in flight: chunk c
+// runs on lane c % kLanes and starts while the chunks before it are still
+// running (its attention at each layer waits for chunk c - 1's K/V rows of
+// that layer; every other launch is independent).  The host collects a
+// lane's ranges before reusing it.  Results equal dtl_forward_chunk +
+// dtl_symbol_ranges_rows per chunk.
 int dtl_forward_ranges(dtl_session* s, const uint32_t* tokens, size_t n, size_t pos0, size_t n_sym,
                        const uint32_t* rows, const uint32_t* symbols, size_t tail, uint64_t* cum,
                        uint32_t* freq, uint64_t* total) {
@@ -1401,7 +1407,7 @@ int dtl_forward_ranges(dtl_session* s, const uint32_t* tokens, size_t n, size_t 
     L.rows_valid = 0;
     L.cdf_ready_row = SIZE_MAX;
   }
-  size_t first[2] = {0, 0}, count[2] = {0, 0};  // symbols of each lane's chunk
+  size_t first[kLanes] = {}, count[kLanes] = {};  // symbols of each lane's chunk
   auto collect = [&](int li) -> int {
     Lane& L = s->lanes[li];
     HIP_TRY(hipStreamSynchronize(L.stream));
@@ -1418,15 +1424,16 @@ int dtl_forward_ranges(dtl_session* s, const uint32_t* tokens, size_t n, size_t 
   const size_t nchunks = (n + C - 1) / C;
   size_t k = 0;
   for (size_t c = 0; c < nchunks; c++) {
-    const int li = (int)(c & 1);
-    if (c >= 2)
+    const int li = (int)(c % kLanes);
+    if (c >= (size_t)kLanes)
       if (int st = collect(li)) return st;
     Lane& L = s->lanes[li];
     s->ln = &L;
     const size_t p0 = c * C, T = std::min(C, n - p0);
     std::memcpy(L.h_tokens, tokens + p0, T * sizeof(uint32_t));
     HIP_TRY(hipMemcpyAsync(L.tokens, L.h_tokens, T * 4, hipMemcpyHostToDevice, L.stream));
-    int rc = enqueue_forward(s, (int)T, pos0 + p0, nullptr, c ? &s->lanes[li ^ 1] : nullptr, true);
+    const Lane* prev = c ? &s->lanes[(c - 1) % kLanes] : nullptr;
+    int rc = enqueue_forward(s, (int)T, pos0 + p0, nullptr, prev, true);
     if (rc) return rc;
     const size_t k0 = k;
     while (k < n_sym && rows[k] < p0 + T) k++;
@@ -1456,9 +1463,9 @@ int dtl_forward_ranges(dtl_session* s, const uint32_t* tokens, size_t n, size_t 
     first[li] = k0;
     count[li] = ms;
   }
-  // the last two chunks, oldest first
-  for (size_t c = nchunks > 2 ? nchunks - 2 : 0; c < nchunks; c++)
-    if (int st = collect((int)(c & 1))) return st;
+  // the chunks still in flight, oldest first
+  for (size_t c = nchunks > (size_t)kLanes ? nchunks - kLanes : 0; c < nchunks; c++)
+    if (int st = collect((int)(c % kLanes))) return st;
   s->prof.collect();
   return DTL_OK;
 }

@@ -271,7 +271,7 @@ class Session:
 
     def forward_ranges(self, tokens: Sequence[int], pos0: int, rows: Sequence[int], symbols: Sequence[int],
                        tail_symbols: int = 0):
-        """Forwards of tokens at pos0.. (chunks of max_chunk, two in flight) and the
+        """Forwards of tokens at pos0.. (chunks of max_chunk, three in flight) and the
         range of symbols[i] under the logits of token rows[i]: (cum, freq, total)."""
         toks = _tokens(tokens)
         r = np.ascontiguousarray(np.asarray(rows, dtype=np.uint32))

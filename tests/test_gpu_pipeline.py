@@ -1,5 +1,5 @@
-"""dtl_forward_ranges: the codec window's forwards and symbol ranges with two
-chunks in flight on two streams.  Every range must equal the oracle's
+"""dtl_forward_ranges: the codec window's forwards and symbol ranges with several
+chunks in flight on separate streams.  Every range must equal the oracle's
 (det-coder logits_to_symbol_range over det-model logits) and the
 chunk-at-a-time path's, whatever the chunk split, the final chunk's size
 (the decode-attention path below five positions) or the start position.
