@@ -1586,41 +1586,83 @@ __global__ void __launch_bounds__(256) k_cdf_bexp(const float* logits, const uin
 // ascending) over a three-deep LDS ring that waves 1-3 fill from the
 // chain-major buffer.
 __global__ void __launch_bounds__(256) k_cdf_z(int V, CdfScratch cs) {
-  constexpr int kSeg = 256;  // elements per chain per ring slot
+  // Lanes 0-7 of wave 0 run the eight chains; waves 1-3 stream the chain-
+  // major exps through a ring of LDS segments.  A producer thread holds the
+  // next segment in registers for a whole segment's worth of adds before it
+  // stores it, so the global-load latency never reaches the chain.
+  constexpr int kSeg = 1024;  // elements per chain per ring slot
   constexpr int kSlots = 3;
-  __shared__ __align__(16) float ring[kSlots][8][kSeg];
+  constexpr int kProducers = 192;
+  constexpr int kF4 = 8 * kSeg / 4;                            // float4 per segment
+  constexpr int kPer = (kF4 + kProducers - 1) / kProducers;    // per producer thread
+  extern __shared__ __align__(16) float zring[];               // [kSlots][8][kSeg]
   __shared__ float zc[8];
   const int r = blockIdx.x, tid = threadIdx.x;
   const int v8 = cdf_v8(V);
   const float* e = cs.ebuf + (size_t)r * 8 * v8;
   const int nseg = (v8 + kSeg - 1) / kSeg;
-  // Producers: 192 threads move one segment (8 chains x kSeg floats) per slot.
-  auto fill = [&](int sg) {
-    float(*dst)[kSeg] = ring[sg % kSlots];
-    for (int x = tid - 64; x < 8 * kSeg / 4; x += 192) {
-      const int c = x / (kSeg / 4), j4 = x % (kSeg / 4);
-      const int j = sg * kSeg + 4 * j4;
-      float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (j + 3 < v8) f = *reinterpret_cast<const float4*>(e + (size_t)c * v8 + j);
-      *reinterpret_cast<float4*>(&dst[c][4 * j4]) = f;
+  float4 pre[kPer];
+  auto load = [&](int sg) {
+#pragma unroll
+    for (int k = 0; k < kPer; k++) {
+      const int x = tid - 64 + kProducers * k;
+      const int c = x / (kSeg / 4), j = sg * kSeg + 4 * (x % (kSeg / 4));
+      pre[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (x < kF4 && j + 3 < v8) pre[k] = *reinterpret_cast<const float4*>(e + (size_t)c * v8 + j);
+    }
+  };
+  auto store = [&](int sg) {
+    float* dst = zring + (size_t)(sg % kSlots) * 8 * kSeg;
+#pragma unroll
+    for (int k = 0; k < kPer; k++) {
+      const int x = tid - 64 + kProducers * k;
+      if (x < kF4) reinterpret_cast<float4*>(dst)[x] = pre[k];  // [c][j]: x = c * kSeg / 4 + j / 4
     }
   };
   if (tid >= 64) {
-    fill(0);
-    if (nseg > 1) fill(1);
+    load(0);
+    store(0);
+    if (nseg > 1) {
+      load(1);
+      store(1);
+    }
+    if (nseg > 2) load(2);
   }
   __syncthreads();
   float acc = 0.0f;
   for (int sg = 0; sg < nseg; sg++) {
     if (tid >= 64) {
-      if (sg + 2 < nseg) fill(sg + 2);
+      if (sg + 2 < nseg) store(sg + 2);  // slot of segment sg - 1, released at the last barrier
+      if (sg + 3 < nseg) load(sg + 3);
     } else if (tid < 8) {
       const int c = tid;
       const int cnt_total = (V - c + 7) / 8;  // elements of chain c
       int cnt = cnt_total - sg * kSeg;
       cnt = cnt < kSeg ? cnt : kSeg;
-      const float* my = ring[sg % kSlots][c];
+      const float* my = zring + (size_t)(sg % kSlots) * 8 * kSeg + (size_t)c * kSeg;
       int j = 0;
+      if (cnt == kSeg) {
+        // A full segment through a ring of twelve float4: each read is
+        // issued twelve float4 (48 adds) before its values are added, so the
+        // chain waits on its own adds, not on LDS.
+        constexpr int kRing = 12;
+        const float4* my4 = reinterpret_cast<const float4*>(my);
+        float4 v[kRing];
+#pragma unroll
+        for (int q = 0; q < kRing; q++) v[q] = my4[q];
+#pragma unroll
+        for (int q = 0; q < kSeg / 4; q++) {
+          const float4 w = v[q % kRing];
+          if (q + kRing < kSeg / 4) v[q % kRing] = my4[q + kRing];
+          acc += w.x;
+          acc += w.y;
+          acc += w.z;
+          acc += w.w;
+          // keeps the scheduler from sinking the read back to its use
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        j = kSeg;
+      }
       for (; j + 16 <= cnt; j += 16) {
         float4 f0 = *reinterpret_cast<const float4*>(my + j);
         float4 f1 = *reinterpret_cast<const float4*>(my + j + 4);
@@ -1784,7 +1826,14 @@ void launch_cdf_blocks(const float* logits, const uint32_t* rows, int R, int V, 
   if (!finish_only) {
     launch_kernel(k_cdf_bmax, dim3(nb, R), dim3(256), 0, s, logits, rows, V, cs, err);
     launch_kernel(k_cdf_bexp, dim3(nb, R), dim3(256), 0, s, logits, rows, V, cs);
-    launch_kernel(k_cdf_z, dim3(R), dim3(256), 0, s, V, cs);
+    constexpr size_t kZRing = 3 * 8 * 1024 * sizeof(float);  // k_cdf_z's segment ring
+    static bool z_attr_set = false;
+    if (!z_attr_set) {
+      (void)hipFuncSetAttribute((const void*)k_cdf_z, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)kZRing);
+      z_attr_set = true;
+    }
+    launch_kernel(k_cdf_z, dim3(R), dim3(256), kZRing, s, V, cs);
     launch_kernel(k_cdf_bfreq, dim3(nb, R), dim3(256), 0, s, V, mode, symbols, cs);
   }
   launch_kernel(k_cdf_finish, dim3(R), dim3(256), 0, s, V, nb, tail, mode, symbols, values, cum,
