@@ -889,7 +889,8 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
       P.timed(st, "attention", kv_rows * KV * hd * 8.0 + (double)T * (H + 3 * KV) * hd * 4.0,
               kv_rows * H * hd * 2.0, [&] {
                 launch_attention_dec(s->ln->q, R, (int)l, T, (int)pos0, H, KV, (int)s->n_ctx,
-                                     c.attention_scale, s->ln->attn, pos_dev, s->ln->err, st);
+                                     c.attention_scale, s->ln->scores, s->ln->attn, pos_dev,
+                                     s->ln->err, st);
               });
       if (record_kv) HIP_TRY(hipEventRecord(s->ln->kv_ready[l], st));
     } else {

@@ -1098,6 +1098,299 @@ __global__ void __launch_bounds__(kDecThreads) k_attention_dec(const float* q, R
   if (bad) flag(err, ERRBIT_NON_FINITE);
 }
 
+// Decode shape split over many workgroups.  One workgroup per (head,
+// position) streams the whole K and V prefix through a single CU, whose
+// load bandwidth then bounds the launch (about 800 KB at position 1560 for a
+// Qwen2.5-0.5B-shaped head).  Here k_attn_split_scores gives every 128-key
+// block its own workgroup, and k_attn_split_pv gives every 16 dimensions of
+// a head its own, so the K and V streams spread over the chip.  Values and
+// order are those of k_attention_dec: the same 8-lane dot per score (the
+// scores cross the launch boundary through memory as f32), the same max,
+// clamped exps, 8-lane Z chains and divisions, and per dimension the same
+// ascending chain of products p_j * v_j[d].
+constexpr int kSplitKeys = 128;   // keys per score workgroup
+constexpr int kSplitDims = 16;    // dimensions per P.V workgroup
+
+// RoPE (lib.rs:2011-2051) of the query head and of the chunk's keys of its
+// group into LDS, from the raw projections; returns whether any input or
+// output is non-finite.
+__device__ bool split_rope_rows(const float* q, const RopeIn& R, int h, int g, int t, int KV, int H,
+                                int pb, float* qs, float (*kn)[64]) {
+  constexpr int hd = 64;
+  const int tid = threadIdx.x, nt = blockDim.x, half = R.rope_dim / 2;
+  bool bad = false;
+  for (int i = tid; i < (t + 2) * hd; i += nt) {
+    const int r = i >> 6, d = i & 63;
+    const float v = r == 0 ? q[((size_t)t * H + h) * hd + d] : R.k[((size_t)(r - 1) * KV + g) * hd + d];
+    bad |= !finite(v);
+    if (r == 0) qs[d] = v;
+    else kn[r - 1][d] = v;
+  }
+  __syncthreads();
+  for (int p = tid; p < (t + 2) * half; p += nt) {
+    const int r = p / half, j = p - r * half;
+    float* base = r == 0 ? qs : kn[r - 1];
+    const int ppos = r == 0 ? pb + t : pb + r - 1;
+    const int ia = R.split_half ? j : 2 * j;
+    const int ib = R.split_half ? j + half : 2 * j + 1;
+    const float x0 = base[ia], x1 = base[ib];
+    const float c = R.rc[(size_t)ppos * half + j], sn = R.rs[(size_t)ppos * half + j];
+    const float y0 = x0 * c - x1 * sn;
+    const float y1 = x0 * sn + x1 * c;
+    bad |= any_nonfinite(y0, y1);
+    base[ia] = y0;
+    base[ib] = y1;
+  }
+  __syncthreads();
+  return bad;
+}
+
+// Scores of keys [128 b, 128 b + 128) for (head h, chunk position t); the
+// workgroup holding key `pos` of the group's first head also stores the
+// position's key and value rows into the cache.  scores: [T][H][n_ctx].
+__global__ void __launch_bounds__(256) k_attn_split_scores(const float* q, RopeIn R, int layer,
+                                                           int pos0, int H, int KV, int n_ctx,
+                                                           float scale, float* scores,
+                                                           const int* pos_dev, int* err) {
+  __shared__ __align__(16) float qs[64];
+  __shared__ __align__(16) float kn[kDecMaxT][64];
+  constexpr int hd = 64;
+  const int b = blockIdx.x, h = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
+  const int G = H / KV, g = h / G;
+  const int pb = pos_dev ? *pos_dev : pos0;
+  const int pos = pb + t, len = pos + 1;
+  const int j0 = b * kSplitKeys;
+  if (j0 >= len) return;  // the grid covers the longest row the launch can see
+  bool bad = split_rope_rows(q, R, h, g, t, KV, H, pb, qs, kn);
+  if (h % G == 0 && pos / kSplitKeys == b && tid < hd) {
+    const size_t off = (((size_t)layer * KV + g) * n_ctx + pos) * hd + tid;
+    const float kv = kn[t][tid], vv = R.v[((size_t)t * KV + g) * hd + tid];
+    bad |= any_nonfinite(kv, vv);
+    R.kc[off] = kv;
+    R.vc[off] = vv;
+  }
+  if (len > 1) {  // a single score is never formed (the output copies V)
+    const float* keys = R.kc + ((size_t)layer * KV + g) * n_ctx * hd;
+    float* srow = scores + ((size_t)t * H + h) * n_ctx;
+    // Eight lanes per key: lane r forms the 8-lane accumulator r (dims r,
+    // r + 8, ..., r + 56 in order); three shuffle levels give
+    // ((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)).  All four rounds' key rows are
+    // loaded first (rows outside the cached part read row 0 and are
+    // replaced from LDS at use).
+    constexpr int kRounds = kSplitKeys / 32;
+    const int r = tid & 7, kq = tid >> 3;
+    float qr[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) qr[u] = qs[r + 8 * u];
+    float kb[kRounds][8];
+#pragma unroll
+    for (int d = 0; d < kRounds; d++) {
+      const int j = j0 + kq + 32 * d;
+      const float* kr = keys + (size_t)(j < pb ? j : 0) * hd + r;
+#pragma unroll
+      for (int u = 0; u < 8; u++) kb[d][u] = kr[8 * u];
+    }
+#pragma unroll
+    for (int d = 0; d < kRounds; d++) {
+      const int j = j0 + kq + 32 * d;
+      const int jv = j - pb < 0 ? 0 : (j - pb < kDecMaxT ? j - pb : kDecMaxT - 1);
+      float acc = 0.0f;
+#pragma unroll
+      for (int u = 0; u < 8; u++) acc += qr[u] * (j < pb ? kb[d][u] : kn[jv][r + 8 * u]);
+      const float s1 = acc + __shfl_xor(acc, 1);
+      const float s2 = s1 + __shfl_xor(s1, 2);
+      const float s3 = s2 + __shfl_xor(s2, 4);
+      if (r == 0 && j < len) {
+        const float sv = s3 * scale;
+        bad |= !finite(sv);
+        srow[j] = sv;
+      }
+    }
+  }
+  if (bad) flag(err, ERRBIT_NON_FINITE);
+}
+
+// softmax_in_place (lib.rs:2361-2388) of the score row, then
+// out[d] = 0; out[d] += p_j * v_j[d] (j ascending, lib.rs:2390-2420) for
+// dimensions [16 blockIdx.x, +16).  Each thread issues its V loads (rows
+// tid / 4 + 64 i, four dimensions) before the softmax, so their latency
+// overlaps it.  The exps are also stored chain-major (element j at chain
+// j % 8, slot j / 8), so each 8-lane Z chain reads its terms four at a time;
+// the products p_j * v_j[d] are stored dimension-major, and lanes 0-15 of
+// wave 0 run the sixteen chains over them without a barrier.  Every serial
+// chain reads through a ring of sixteen float4, refilled four at a time,
+// so it waits on its own adds, not on LDS.
+constexpr int kSplitMaxRows = 2048;  // positions the register staging covers
+constexpr int kSplitVPer = kSplitMaxRows / 64;
+constexpr int kChainRing = 12;       // float4 in flight per chain
+constexpr int kChainGroup = 1;       // float4 per refill group
+
+struct SplitLayout {  // LDS of k_attn_split_pv, in floats
+  int len4, zs, stride, zoff, poff, total;
+};
+
+__host__ __device__ inline SplitLayout split_layout(int maxlen) {
+  SplitLayout L;
+  L.len4 = (maxlen + 3) & ~3;
+  L.zs = (((maxlen + 7) / 8 + 3) & ~3) + 4;  // chain-major row (a multiple of 4)
+  L.stride = L.len4 + 4;                       // product row
+  L.zoff = L.len4;
+  L.poff = L.zoff + 8 * L.zs;
+  L.total = L.poff + kSplitDims * L.stride;
+  return L;
+}
+
+size_t split_pv_smem(int maxlen) { return (size_t)split_layout(maxlen).total * sizeof(float); }
+
+// Adds n4 float4 of my4 (in order, x y z w) to a, through a ring of
+// kChainRing reads refilled kChainGroup at a time.
+__device__ __forceinline__ float chain_sum4(float a, const float4* my4, int n4) {
+  int q4 = 0;
+  if (n4 >= kChainRing) {
+    float4 v[kChainRing];
+#pragma unroll
+    for (int q = 0; q < kChainRing; q++) v[q] = my4[q];
+    for (; q4 + 2 * kChainRing <= n4; q4 += kChainRing) {
+#pragma unroll
+      for (int g0 = 0; g0 < kChainRing; g0 += kChainGroup) {
+#pragma unroll
+        for (int q = g0; q < g0 + kChainGroup; q++) {
+          // the slot's adds first, then its refill into the same registers
+          // (a loop-carried ring needs no copies that way)
+          a += v[q].x;
+          a += v[q].y;
+          a += v[q].z;
+          a += v[q].w;
+          v[q] = my4[q4 + kChainRing + q];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kChainRing; q++) {
+      a += v[q].x;
+      a += v[q].y;
+      a += v[q].z;
+      a += v[q].w;
+    }
+    q4 += kChainRing;
+  }
+  for (; q4 < n4; q4++) {
+    const float4 w = my4[q4];
+    a += w.x;
+    a += w.y;
+    a += w.z;
+    a += w.w;
+  }
+  return a;
+}
+
+__global__ void __launch_bounds__(256) k_attn_split_pv(const float* scores, RopeIn R, int layer,
+                                                       int pos0, int H, int KV, int n_ctx,
+                                                       int maxlen, float* out,
+                                                       const int* pos_dev, int* err) {
+  // [len4] scores -> probabilities, [8][zs] exps chain-major, [16][stride] products
+  extern __shared__ __align__(16) float pr[];
+  __shared__ float red[4];
+  __shared__ float zc[8];
+  constexpr int hd = 64;
+  const int dg = blockIdx.x, h = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int G = H / KV, g = h / G;
+  const int pb = pos_dev ? *pos_dev : pos0;
+  const int pos = pb + t, len = pos + 1;
+  const int d0 = dg * kSplitDims;
+  const SplitLayout L = split_layout(maxlen);
+  float* zcm = pr + L.zoff;
+  float* prod = pr + L.poff;
+  const float* vals = R.vc + ((size_t)layer * KV + g) * n_ctx * hd;
+  // chunk rows (j >= pb) come from the raw projection, never from the cache
+  auto vrow = [&](int j) -> const float* {
+    return j < pb ? vals + (size_t)j * hd : R.v + ((size_t)(j - pb) * KV + g) * hd;
+  };
+  float* o = out + ((size_t)t * H + h) * hd + d0;
+  bool bad = false;
+  if (len == 1) {  // a single score copies V exactly (lib.rs:2319-2321)
+    if (tid < kSplitDims) o[tid] = vrow(0)[d0 + tid];
+    return;
+  }
+  const int jr = tid >> 2, c = 4 * (tid & 3);
+  float4 vreg[kSplitVPer];
+#pragma unroll
+  for (int i = 0; i < kSplitVPer; i++)
+    if (64 * i < len) {
+      const int j = 64 * i + jr;
+      vreg[i] = *reinterpret_cast<const float4*>(vrow(j < len ? j : len - 1) + d0 + c);
+    }
+  const float* srow = scores + ((size_t)t * H + h) * n_ctx;
+  float mx = -__builtin_huge_valf();
+  for (int j = tid; j < len; j += 256) {
+    const float sv = srow[j];
+    pr[j] = sv;
+    mx = fmaxf(mx, sv);
+  }
+  for (int i = tid; i < 8 * L.zs; i += 256) zcm[i] = 0.0f;  // chain padding adds +0.0
+  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  // eight independent exps per thread at a time
+  for (int j0 = 0; j0 < len; j0 += 8 * 256) {
+    float e[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int j = j0 + tid + 256 * k;
+      e[k] = j < len ? exp_clamped(pr[j < len ? j : 0] - mx) : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int j = j0 + tid + 256 * k;
+      if (j < len) {
+        pr[j] = e[k];
+        zcm[(j & 7) * L.zs + (j >> 3)] = e[k];
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < 8) {
+    const int cnt = (len - tid + 7) / 8;  // terms of chain tid
+    zc[tid] = chain_sum4(0.0f, reinterpret_cast<const float4*>(zcm + tid * L.zs), (cnt + 3) / 4);
+  }
+  __syncthreads();
+  const float z = finish_8lane(zc);
+  bad |= !finite(z) || z == 0.0f;
+  for (int j = tid; j < len; j += 256) {
+    const float p = pr[j] / z;
+    bad |= !finite(p);
+    pr[j] = p;
+  }
+  __syncthreads();
+  // Products, dimension-major; rows len .. len4 hold zeros, so the chains
+  // below take whole float4 (adding +0.0 leaves a chain that starts at +0.0
+  // exactly as it is: a round-to-nearest sum is -0.0 only when both terms
+  // are).
+  const int len4 = (len + 3) & ~3;
+#pragma unroll
+  for (int i = 0; i < kSplitVPer; i++) {
+    const int j = 64 * i + jr;
+    if (j < len4) {
+      const float p = j < len ? pr[j < len ? j : 0] : 0.0f;
+      const float4 v = j < len ? vreg[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      prod[(c + 0) * L.stride + j] = p * v.x;
+      prod[(c + 1) * L.stride + j] = p * v.y;
+      prod[(c + 2) * L.stride + j] = p * v.z;
+      prod[(c + 3) * L.stride + j] = p * v.w;
+    }
+  }
+  __syncthreads();
+  if (wave == 0 && lane < kSplitDims) {
+    const float a = chain_sum4(0.0f, reinterpret_cast<const float4*>(prod + lane * L.stride), len4 / 4);
+    bad |= !finite(a);
+    o[lane] = a;
+  }
+  if (bad) flag(err, ERRBIT_NON_FINITE);
+}
+
 size_t attention_hd64_smem(int G, int sc_stride) {
   return ((size_t)G * sc_stride + 2 * kA64Buf + (size_t)G * 64) * sizeof(float);
 }
@@ -1121,11 +1414,32 @@ bool attention_dec_applies(int hd, int T, int pos0, int n_ctx, bool pos_in_devic
 }
 
 void launch_attention_dec(const float* q, const RopeIn& R, int layer, int T, int pos0, int H,
-                          int KV, int n_ctx, float scale, float* out, const int* pos_dev,
-                          int* err, hipStream_t s) {
-  // One workgroup per (head, position).  With the position in device
-  // memory the score buffer is sized for the whole window.
-  const size_t smem = (size_t)(pos_dev ? n_ctx : pos0 + T) * sizeof(float);
+                          int KV, int n_ctx, float scale, float* scores, float* out,
+                          const int* pos_dev, int* err, hipStream_t s) {
+  // With the position in device memory the grids and the score buffer are
+  // sized for the whole window.
+  const int maxlen = pos_dev ? n_ctx : pos0 + T;
+  const size_t smem = (size_t)maxlen * sizeof(float);
+  static const bool single = [] {
+    const char* e = getenv("DETLLM_ATTN_DEC_SINGLE");
+    return e && *e && *e != '0';
+  }();
+  const size_t pv_smem = split_pv_smem(maxlen);
+  if (!single && maxlen <= kSplitMaxRows && pv_smem <= 158 * 1024) {
+    static bool attr_pv_set = false;
+    if (!attr_pv_set) {
+      (void)hipFuncSetAttribute((const void*)k_attn_split_pv,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 158 * 1024);
+      attr_pv_set = true;
+    }
+    launch_kernel(k_attn_split_scores, dim3((maxlen + kSplitKeys - 1) / kSplitKeys, H, T), dim3(256),
+                  0, s, q, R, layer, pos0, H, KV, n_ctx, scale, scores, pos_dev, err);
+    launch_kernel(k_attn_split_pv, dim3(64 / kSplitDims, H, T), dim3(256), pv_smem, s, scores, R,
+                  layer, pos0, H, KV, n_ctx, maxlen, out, pos_dev, err);
+    return;
+  }
+  // Longer windows (or DETLLM_ATTN_DEC_SINGLE=1): one workgroup per
+  // (head, position).
   static bool attr_dec_set = false;
   if (!attr_dec_set) {
     (void)hipFuncSetAttribute((const void*)k_attention_dec,

@@ -25,12 +25,16 @@ __device__ __forceinline__ bool any_nonfinite(float a, float b, float c, float d
   return ((int)!finite(a) | (int)!finite(b) | (int)!finite(c) | (int)!finite(d)) != 0;
 }
 
-// Rust `f32 as i32`: truncation toward zero, saturating, NaN -> 0.
+// Rust `f32 as i32`: truncation toward zero, saturating, NaN -> 0.  Written
+// with selects (no branches): the conversion sees a value clamped into
+// [-2^31, largest float below 2^31], which truncates exactly as the
+// unclamped in-range value would, and the two out-of-range cases and NaN
+// are selected afterwards.
 __device__ __forceinline__ int32_t f32_as_i32(float x) {
-  if (x != x) return 0;
-  if (x >= 2147483648.0f) return INT32_MAX;
-  if (x < -2147483648.0f) return INT32_MIN;
-  return (int32_t)x;
+  const float xc = fminf(fmaxf(x, -2147483648.0f), 2147483520.0f);
+  int32_t r = (int32_t)xc;
+  r = x >= 2147483648.0f ? INT32_MAX : r;
+  return x != x ? 0 : r;
 }
 
 // f16 bits -> f32 by integer construction (det-num f16.rs:6-34); exact for
@@ -63,70 +67,67 @@ __device__ __forceinline__ float finish_8lane(const float a[8]) {
   return ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
 }
 
-// scalbnf with the two-step range handling of det-num vendored_libm.rs:94-119.
+// scalbnf with the two-step range handling of det-num vendored_libm.rs:94-119,
+// written with selects: the upward steps apply when the original n is above
+// 127, the downward ones when it is below -126, each step exactly as the
+// branches take it.
 __device__ __forceinline__ float scalbnf(float x, int n) {
   const float x1p127 = u2f(0x7f000000u);
   const float x1p_126 = u2f(0x00800000u);
-  if (n > 127) {
-    x *= x1p127;
-    n -= 127;
-    if (n > 127) {
-      x *= x1p127;
-      n -= 127;
-      if (n > 127) n = 127;
-    }
-  } else if (n < -126) {
-    x *= x1p_126;
-    n += 126;
-    if (n < -126) {
-      x *= x1p_126;
-      n += 126;
-      if (n < -126) n = -126;
-    }
-  }
+  const int n0 = n;
+  const bool up1 = n0 > 127;
+  x = up1 ? x * x1p127 : x;
+  n = up1 ? n - 127 : n;
+  const bool up2 = up1 && n > 127;
+  x = up2 ? x * x1p127 : x;
+  n = up2 ? n - 127 : n;
+  n = up2 && n > 127 ? 127 : n;
+  const bool dn1 = n0 < -126;
+  x = dn1 ? x * x1p_126 : x;
+  n = dn1 ? n + 126 : n;
+  const bool dn2 = dn1 && n < -126;
+  x = dn2 ? x * x1p_126 : x;
+  n = dn2 ? n + 126 : n;
+  n = dn2 && n < -126 ? -126 : n;
   return x * u2f((uint32_t)(0x7f + n) << 23);
 }
 
 // exp_f32 (det-num math.rs:5-7): the FreeBSD e_expf method restated from
 // its published description -- round x/ln2 to k, reduce with a two-part
 // ln2, approximate with x*c/(2-c), c = x - x^2(P1 + x^2 P2), scale by 2^k.
+//
+// Every path is computed and the result selected, so a wave of mixed inputs
+// runs one straight sequence (the branches of the method became selects;
+// each path's arithmetic is unchanged).
 __device__ __forceinline__ float expf_det(float x) {
   const float ln2_hi = u2f(0x3f317200u);
   const float ln2_lo = u2f(0x35bfbe8eu);
   const float inv_ln2 = u2f(0x3fb8aa3bu);
   const float p1 = u2f(0x3e2aaa8fu);
   const float p2 = u2f(0xbb355215u);
-  uint32_t hx = f2u(x);
-  int sign = (int)(hx >> 31);
-  hx &= 0x7fffffffu;
-  if (hx >= 0x42aeac50u) {
-    if (hx > 0x7f800000u) return x;
-    if (hx >= 0x42b17218u && !sign) return x * u2f(0x7f000000u);
-    if (sign && hx >= 0x42cff1b5u) return 0.0f;
-  }
-  int k;
-  float hi, lo;
-  if (hx > 0x3eb17218u) {
-    if (hx > 0x3f851592u) {
-      k = f32_as_i32(inv_ln2 * x + (sign ? -0.5f : 0.5f));
-    } else {
-      k = 1 - sign - sign;
-    }
-    float kf = (float)k;
-    hi = x - kf * ln2_hi;
-    lo = kf * ln2_lo;
-    x = hi - lo;
-  } else if (hx > 0x39000000u) {
-    k = 0;
-    hi = x;
-    lo = 0.0f;
-  } else {
-    return 1.0f + x;
-  }
-  float xx = x * x;
-  float c = x - xx * (p1 + xx * p2);
-  float y = 1.0f + (x * c / (2.0f - c) - lo + hi);
-  return k == 0 ? y : scalbnf(y, k);
+  const uint32_t ux = f2u(x);
+  const int sign = (int)(ux >> 31);
+  const uint32_t hx = ux & 0x7fffffffu;
+  // |x| > 0.5 ln2: reduce by k ln2 (k from the rounding of x / ln2 above
+  // 1.5 ln2, else +-1)
+  const int kr = hx > 0x3f851592u ? f32_as_i32(inv_ln2 * x + (sign ? -0.5f : 0.5f)) : 1 - sign - sign;
+  const float kf = (float)kr;
+  const float hi_r = x - kf * ln2_hi;
+  const float lo_r = kf * ln2_lo;
+  const bool reduce = hx > 0x3eb17218u;
+  const int k = reduce ? kr : 0;
+  const float hi = reduce ? hi_r : x;
+  const float lo = reduce ? lo_r : 0.0f;
+  const float xr = reduce ? hi_r - lo_r : x;
+  const float xx = xr * xr;
+  const float c = xr - xx * (p1 + xx * p2);
+  const float y = 1.0f + (xr * c / (2.0f - c) - lo + hi);
+  float r = k == 0 ? y : scalbnf(y, k);
+  r = hx > 0x39000000u ? r : 1.0f + x;  // |x| < 2^-14
+  // special cases, lowest priority first
+  r = sign && hx >= 0x42cff1b5u ? 0.0f : r;                 // underflow
+  r = !sign && hx >= 0x42b17218u ? x * u2f(0x7f000000u) : r;  // overflow
+  return hx > 0x7f800000u ? x : r;                          // NaN
 }
 
 // silu_f32 (det-num math.rs:30-34).
