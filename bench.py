@@ -44,7 +44,7 @@ FP32_UNFUSED_ISSUE_PEAK_TOPS = 39.3
 # copy (--copy-probe-mib).  Keyed by kernel class; the summaries sit in
 # profiles/ under the same name.
 MEASURED_TRAFFIC = {
-    "gemm_q4_k_gate_up": {"bytes": (47158.0 * 2.000 + 1408.0 * 1.000) * 1024.0,
+    "gemm_q4_k_gate_up": {"bytes": (47141.5 * 2.000 + 1408.0 * 1.000) * 1024.0,
                           "source": "profiles/k_q4k_f32w_pair_tinyllama_encode_chunk64.md"},
 }
 
