@@ -46,18 +46,9 @@ __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
 }
 
 // Sequential sum of n block terms (block order), from LDS.
-__device__ __forceinline__ float chain_sum(const float* v, int n) {
-  float s = 0.0f;
-  int b = 0;
-  for (; b + 4 <= n; b += 4) {
-    s += v[b];
-    s += v[b + 1];
-    s += v[b + 2];
-    s += v[b + 3];
-  }
-  for (; b < n; b++) s += v[b];
-  return s;
-}
+// Block-term rows in LDS start on 16-byte boundaries (chain_sum_lds reads
+// them four at a time): row stride nb rounded up to a multiple of 4.
+__host__ __device__ inline int nb_stride(int nb) { return (nb + 3) & ~3; }
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -72,7 +63,8 @@ __global__ void __launch_bounds__(256) k_gemv_q8(DevMat W, const int8_t* __restr
   const int t = blockIdx.y;
   const int rows = W.rows, cols = W.cols, nb = W.nb;
   const int row0 = (blockIdx.x * 4 + wave) * R;
-  float* mine = vb + (size_t)wave * R * nb;
+  const int nbs = nb_stride(nb);
+  float* mine = vb + (size_t)wave * R * nbs;
   const int8_t* arow = qa + (size_t)t * cols;
   const float* drow = da + (size_t)t * nb;
   // Q8_0: a 32-byte block is two 16-byte chunks (lanes c, c^1); Q4_0: one
@@ -145,14 +137,14 @@ __global__ void __launch_bounds__(256) k_gemv_q8(DevMat W, const int8_t* __restr
         isum -= 8 * asum;
       }
       const bool writer = TYPE == kGgmlQ8_0 ? cv && !(c & 1) : cv;
-      if (writer && row0 + r < rows) mine[r * nb + b] = (f16_to_f32(dsc[r]) * dact) * (float)isum;
+      if (writer && row0 + r < rows) mine[r * nbs + b] = (f16_to_f32(dsc[r]) * dact) * (float)isum;
     }
   }
   __syncthreads();
   if (lane < R) {
     const int row = row0 + lane;
     if (row < rows) {
-      float v = chain_sum(mine + lane * nb, nb);
+      float v = chain_sum_lds(0.0f, mine + lane * nbs, nb);
       if (!epilogue(v, out, (size_t)t * rows + row, bias, row, epi)) flag(err, ERRBIT_NON_FINITE);
     }
   }
@@ -176,7 +168,8 @@ __global__ void __launch_bounds__(256) k_gemv_q8_0_stream(DevMat W, const int8_t
   const int nchunk = 2 * nb;
   const int c = lane, b = c >> 1;
   const bool cv = c < nchunk;
-  float* mine = vb + (size_t)wave * R * nb;
+  const int nbs = nb_stride(nb);
+  float* mine = vb + (size_t)wave * R * nbs;
   const int ngroups = (rows + R - 1) / R;
   const int stride = gridDim.x * 4;
   uint4 a0 = make_uint4(0, 0, 0, 0);
@@ -209,14 +202,14 @@ __global__ void __launch_bounds__(256) k_gemv_q8_0_stream(DevMat W, const int8_t
       isum = dot4(w4[slot][r].z, a0.z, isum);
       isum = dot4(w4[slot][r].w, a0.w, isum);
       isum += __shfl_xor(isum, 1);
-      if (cv && !(c & 1)) mine[r * nb + b] = (f16_to_f32(dsc[slot][r]) * dact) * (float)isum;
+      if (cv && !(c & 1)) mine[r * nbs + b] = (f16_to_f32(dsc[slot][r]) * dact) * (float)isum;
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     if (lane < R) {
       const int row = g * R + lane;
       if (row < rows) {
-        float v = chain_sum(mine + lane * nb, nb);
+        float v = chain_sum_lds(0.0f, mine + lane * nbs, nb);
         if (!epilogue(v, out, (size_t)t * rows + row, bias, row, epi)) flag(err, ERRBIT_NON_FINITE);
       }
     }
@@ -448,20 +441,7 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
       }
     }
     __syncthreads();
-    if (tid < 8) {
-      const int cnt = (cols - tid + 7) / 8;
-      const float* my = sq + tid * cs;
-      float acc = 0.0f;
-      int k = 0;
-      for (; k + 8 <= cnt; k += 8) {
-        const float4 f0 = *reinterpret_cast<const float4*>(my + k);
-        const float4 f1 = *reinterpret_cast<const float4*>(my + k + 4);
-        acc += f0.x; acc += f0.y; acc += f0.z; acc += f0.w;
-        acc += f1.x; acc += f1.y; acc += f1.z; acc += f1.w;
-      }
-      for (; k < cnt; k++) acc += my[k];
-      misc[tid] = acc;
-    }
+    if (tid < 8) misc[tid] = chain_sum_lds(0.0f, sq + tid * cs, (cols - tid + 7) / 8);
     __syncthreads();
     if (tid == 0) {
       const float ss = finish_8lane(misc);
@@ -519,7 +499,7 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
 // norm, its scratch (the row, the weights, the chain-major squares).
 size_t gemv_fused_smem(int nr, int cols, int nb, bool norm) {
   const size_t cs = (size_t)((((cols + 7) / 8) + 3) & ~3);
-  size_t b = (size_t)4 * nr * nb * 4 + (size_t)((cols + 15) & ~15) + (size_t)((nb + 3) & ~3) * 4;
+  size_t b = (size_t)4 * nr * nb_stride(nb) * 4 + (size_t)((cols + 15) & ~15) + (size_t)((nb + 3) & ~3) * 4;
   if (norm) b += 2 * (size_t)((cols + 3) & ~3) * 4 + 8 * cs * 4 + 16 * 4;
   return b;
 }
@@ -532,14 +512,15 @@ __global__ void __launch_bounds__(256) k_gemv_q8f(FusedMats M, FusedIn in, int* 
   const int t = blockIdx.y;
   const int cols = M.cols, nb = M.nb;
   const int cs = (((cols + 7) / 8) + 3) & ~3;
+  const int nbs = nb_stride(nb);
   float* vb = lds;
-  int8_t* qa_s = reinterpret_cast<int8_t*>(lds + 4 * NR * nb);
+  int8_t* qa_s = reinterpret_cast<int8_t*>(lds + 4 * NR * nbs);
   float* da_s = reinterpret_cast<float*>(qa_s + ((cols + 15) & ~15));
   float* xs = da_s + ((nb + 3) & ~3);
   float* ws = xs + ((cols + 3) & ~3);
   float* sq = ws + ((cols + 3) & ~3);
   float* misc = sq + 8 * cs;
-  float* mine = vb + (size_t)wave * NR * nb;
+  float* mine = vb + (size_t)wave * NR * nbs;
   const int row0 = (blockIdx.x * 4 + wave) * R;
   // Slot r: (matrix, row) of the r-th dot of this wave.  Matrix choice is
   // wave-uniform, so the selects below stay scalar.
@@ -646,7 +627,7 @@ __global__ void __launch_bounds__(256) k_gemv_q8f(FusedMats M, FusedIn in, int* 
           isum -= 8 * asum;
         }
         const bool writer = TYPE == kGgmlQ8_0 ? cv && !(c & 1) : cv;
-        if (writer) mine[r * nb + b] = (f16_to_f32(dsc[ii][r]) * dact) * (float)isum;
+        if (writer) mine[r * nbs + b] = (f16_to_f32(dsc[ii][r]) * dact) * (float)isum;
       }
     }
   }
@@ -655,8 +636,8 @@ __global__ void __launch_bounds__(256) k_gemv_q8f(FusedMats M, FusedIn in, int* 
     if (PAIR) {
       const int row = row0 + lane;
       if (row < M.rows[0]) {
-        const float g = chain_sum(mine + lane * nb, nb);
-        const float u = chain_sum(mine + (R + lane) * nb, nb);
+        const float g = chain_sum_lds(0.0f, mine + lane * nbs, nb);
+        const float u = chain_sum_lds(0.0f, mine + (R + lane) * nbs, nb);
         const float v = silu_det(g) * u;
         if (!finite(g) || !finite(u) || !finite(v)) bad = true;
         M.out[0][(size_t)t * M.rows[0] + row] = v;
@@ -670,7 +651,7 @@ __global__ void __launch_bounds__(256) k_gemv_q8f(FusedMats M, FusedIn in, int* 
         const float* bias = mi == 0 ? M.bias[0] : (mi == 1 ? M.bias[1] : M.bias[2]);
         const int epi = mi == 0 ? M.epi[0] : (mi == 1 ? M.epi[1] : M.epi[2]);
         const int rows = mi == 0 ? M.rows[0] : (mi == 1 ? M.rows[1] : M.rows[2]);
-        const float v = chain_sum(mine + lane * nb, nb);
+        const float v = chain_sum_lds(0.0f, mine + lane * nbs, nb);
         if (!epilogue(v, out, (size_t)t * rows + row, bias, row, epi)) bad = true;
       }
     }
@@ -683,7 +664,7 @@ namespace {
 template <int TYPE>
 void launch_q8(const DevMat& W, const DevAct& A, int T, float* out, const float* bias, int epi,
                int* err, hipStream_t s, int R) {
-  size_t smem = (size_t)4 * R * W.nb * sizeof(float);
+  size_t smem = (size_t)4 * R * nb_stride(W.nb) * sizeof(float);
   dim3 grid((W.rows + 4 * R - 1) / (4 * R), T);
   if (R == 8)
     launch_kernel((k_gemv_q8<TYPE, 8>), grid, dim3(256), smem, s, W, A.qa, A.da, out, bias, epi, err);
@@ -705,7 +686,7 @@ bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const floa
     const int ngroups = (W.rows + R - 1) / R;
     int wgs = (ngroups + 3) / 4;
     if (wgs > 256 * 4) wgs = 256 * 4;
-    size_t smem = (size_t)4 * R * W.nb * sizeof(float);
+    size_t smem = (size_t)4 * R * nb_stride(W.nb) * sizeof(float);
     launch_kernel(k_gemv_q8_0_stream<R>, dim3(wgs, T), dim3(256), smem, s, W, A.qa, A.da, out,
                   bias, epi, err);
     return true;
@@ -714,8 +695,8 @@ bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const floa
     // Rows per wave: enough waves to fill the chip on small matrices, more
     // rows per wave (fewer chain tails) on tall ones; LDS holds R*nb terms per wave.
     int R = W.rows >= 65536 ? 8 : (W.rows >= 16384 ? 4 : (W.rows >= 4096 ? 2 : 1));
-    while (R > 1 && (size_t)4 * R * W.nb * sizeof(float) > 64 * 1024) R >>= 1;
-    if ((size_t)4 * R * W.nb * sizeof(float) > 64 * 1024) return false;
+    while (R > 1 && (size_t)4 * R * nb_stride(W.nb) * sizeof(float) > 64 * 1024) R >>= 1;
+    if ((size_t)4 * R * nb_stride(W.nb) * sizeof(float) > 64 * 1024) return false;
     if (W.type == kGgmlQ8_0)
       launch_q8<kGgmlQ8_0>(W, A, T, out, bias, epi, err, s, R);
     else

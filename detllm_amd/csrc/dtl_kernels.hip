@@ -323,23 +323,8 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* x, const float* w,
   }
   __syncthreads();
   if (threadIdx.x < 8) {
-    const int c = threadIdx.x;
-    const int cnt = (n - c + 7) / 8;  // elements c, c+8, ... below n
-    const float* my = sq + c * cs;
-    float acc = 0.0f;
-    int k = 0;
-    for (; k + 16 <= cnt; k += 16) {
-      float4 f0 = *reinterpret_cast<const float4*>(my + k);
-      float4 f1 = *reinterpret_cast<const float4*>(my + k + 4);
-      float4 f2 = *reinterpret_cast<const float4*>(my + k + 8);
-      float4 f3 = *reinterpret_cast<const float4*>(my + k + 12);
-      acc += f0.x; acc += f0.y; acc += f0.z; acc += f0.w;
-      acc += f1.x; acc += f1.y; acc += f1.z; acc += f1.w;
-      acc += f2.x; acc += f2.y; acc += f2.z; acc += f2.w;
-      acc += f3.x; acc += f3.y; acc += f3.z; acc += f3.w;
-    }
-    for (; k < cnt; k++) acc += my[k];
-    lane_sum[c] = acc;
+    const int c = threadIdx.x;  // elements c, c+8, ... below n
+    lane_sum[c] = chain_sum_lds(0.0f, sq + c * cs, (n - c + 7) / 8);
   }
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -1217,13 +1202,9 @@ __global__ void __launch_bounds__(256) k_attn_split_scores(const float* q, RopeI
 // overlaps it.  The exps are also stored chain-major (element j at chain
 // j % 8, slot j / 8), so each 8-lane Z chain reads its terms four at a time;
 // the products p_j * v_j[d] are stored dimension-major, and lanes 0-15 of
-// wave 0 run the sixteen chains over them without a barrier.  Every serial
-// chain reads through a ring of sixteen float4, refilled four at a time,
-// so it waits on its own adds, not on LDS.
+// wave 0 run the sixteen chains over them without a barrier (chain_sum_lds).
 constexpr int kSplitMaxRows = 2048;  // positions the register staging covers
 constexpr int kSplitVPer = kSplitMaxRows / 64;
-constexpr int kChainRing = 12;       // float4 in flight per chain
-constexpr int kChainGroup = 1;       // float4 per refill group
 
 struct SplitLayout {  // LDS of k_attn_split_pv, in floats
   int len4, zs, stride, zoff, poff, total;
@@ -1241,49 +1222,6 @@ __host__ __device__ inline SplitLayout split_layout(int maxlen) {
 }
 
 size_t split_pv_smem(int maxlen) { return (size_t)split_layout(maxlen).total * sizeof(float); }
-
-// Adds n4 float4 of my4 (in order, x y z w) to a, through a ring of
-// kChainRing reads refilled kChainGroup at a time.
-__device__ __forceinline__ float chain_sum4(float a, const float4* my4, int n4) {
-  int q4 = 0;
-  if (n4 >= kChainRing) {
-    float4 v[kChainRing];
-#pragma unroll
-    for (int q = 0; q < kChainRing; q++) v[q] = my4[q];
-    for (; q4 + 2 * kChainRing <= n4; q4 += kChainRing) {
-#pragma unroll
-      for (int g0 = 0; g0 < kChainRing; g0 += kChainGroup) {
-#pragma unroll
-        for (int q = g0; q < g0 + kChainGroup; q++) {
-          // the slot's adds first, then its refill into the same registers
-          // (a loop-carried ring needs no copies that way)
-          a += v[q].x;
-          a += v[q].y;
-          a += v[q].z;
-          a += v[q].w;
-          v[q] = my4[q4 + kChainRing + q];
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < kChainRing; q++) {
-      a += v[q].x;
-      a += v[q].y;
-      a += v[q].z;
-      a += v[q].w;
-    }
-    q4 += kChainRing;
-  }
-  for (; q4 < n4; q4++) {
-    const float4 w = my4[q4];
-    a += w.x;
-    a += w.y;
-    a += w.z;
-    a += w.w;
-  }
-  return a;
-}
 
 __global__ void __launch_bounds__(256) k_attn_split_pv(const float* scores, RopeIn R, int layer,
                                                        int pos0, int H, int KV, int n_ctx,
@@ -1329,7 +1267,6 @@ __global__ void __launch_bounds__(256) k_attn_split_pv(const float* scores, Rope
     pr[j] = sv;
     mx = fmaxf(mx, sv);
   }
-  for (int i = tid; i < 8 * L.zs; i += 256) zcm[i] = 0.0f;  // chain padding adds +0.0
   for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
   if (lane == 0) red[wave] = mx;
   __syncthreads();
@@ -1354,7 +1291,7 @@ __global__ void __launch_bounds__(256) k_attn_split_pv(const float* scores, Rope
   __syncthreads();
   if (tid < 8) {
     const int cnt = (len - tid + 7) / 8;  // terms of chain tid
-    zc[tid] = chain_sum4(0.0f, reinterpret_cast<const float4*>(zcm + tid * L.zs), (cnt + 3) / 4);
+    zc[tid] = chain_sum_lds(0.0f, zcm + tid * L.zs, cnt);
   }
   __syncthreads();
   const float z = finish_8lane(zc);
@@ -1365,26 +1302,21 @@ __global__ void __launch_bounds__(256) k_attn_split_pv(const float* scores, Rope
     pr[j] = p;
   }
   __syncthreads();
-  // Products, dimension-major; rows len .. len4 hold zeros, so the chains
-  // below take whole float4 (adding +0.0 leaves a chain that starts at +0.0
-  // exactly as it is: a round-to-nearest sum is -0.0 only when both terms
-  // are).
-  const int len4 = (len + 3) & ~3;
+  // Products, dimension-major.
 #pragma unroll
   for (int i = 0; i < kSplitVPer; i++) {
     const int j = 64 * i + jr;
-    if (j < len4) {
-      const float p = j < len ? pr[j < len ? j : 0] : 0.0f;
-      const float4 v = j < len ? vreg[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-      prod[(c + 0) * L.stride + j] = p * v.x;
-      prod[(c + 1) * L.stride + j] = p * v.y;
-      prod[(c + 2) * L.stride + j] = p * v.z;
-      prod[(c + 3) * L.stride + j] = p * v.w;
+    if (j < len) {
+      const float p = pr[j];
+      prod[(c + 0) * L.stride + j] = p * vreg[i].x;
+      prod[(c + 1) * L.stride + j] = p * vreg[i].y;
+      prod[(c + 2) * L.stride + j] = p * vreg[i].z;
+      prod[(c + 3) * L.stride + j] = p * vreg[i].w;
     }
   }
   __syncthreads();
   if (wave == 0 && lane < kSplitDims) {
-    const float a = chain_sum4(0.0f, reinterpret_cast<const float4*>(prod + lane * L.stride), len4 / 4);
+    const float a = chain_sum_lds(0.0f, prod + lane * L.stride, len);
     bad |= !finite(a);
     o[lane] = a;
   }

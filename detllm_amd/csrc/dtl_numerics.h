@@ -130,6 +130,52 @@ __device__ __forceinline__ float expf_det(float x) {
   return hx > 0x7f800000u ? x : r;                          // NaN
 }
 
+// a + v[0] + v[1] + ... + v[n - 1], one add at a time in that order, from
+// 16-byte aligned LDS.  The serial chain waits on its own adds, not on LDS:
+// whole float4 go through a ring of twelve reads issued twelve float4 ahead
+// of their adds (the slot's adds first, then its refill into the same
+// registers, so a loop-carried ring needs no copies; the scheduling barrier
+// keeps each refill where it is).  The last n % 4 terms are added singly.
+__device__ __forceinline__ float chain_sum_lds(float a, const float* v, int n) {
+  constexpr int kRing = 12;
+  const float4* v4 = reinterpret_cast<const float4*>(v);
+  const int n4 = n >> 2;
+  int q4 = 0;
+  if (n4 >= kRing) {
+    float4 r[kRing];
+#pragma unroll
+    for (int q = 0; q < kRing; q++) r[q] = v4[q];
+    for (; q4 + 2 * kRing <= n4; q4 += kRing) {
+#pragma unroll
+      for (int q = 0; q < kRing; q++) {
+        a += r[q].x;
+        a += r[q].y;
+        a += r[q].z;
+        a += r[q].w;
+        r[q] = v4[q4 + kRing + q];
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kRing; q++) {
+      a += r[q].x;
+      a += r[q].y;
+      a += r[q].z;
+      a += r[q].w;
+    }
+    q4 += kRing;
+  }
+  for (; q4 < n4; q4++) {
+    const float4 w = v4[q4];
+    a += w.x;
+    a += w.y;
+    a += w.z;
+    a += w.w;
+  }
+  for (int i = 4 * n4; i < n; i++) a += v[i];
+  return a;
+}
+
 // silu_f32 (det-num math.rs:30-34).
 __device__ __forceinline__ float silu_det(float x) {
   float t = expf_det(-x);
