@@ -820,7 +820,8 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
   const bool fuse = T <= kGemvMaxT && !env_flag("DETLLM_NO_FUSED_DECODE");
   auto fused = [&](std::initializer_list<const DevMat*> ms, bool pair, std::initializer_list<float*> outs,
                    std::initializer_list<const float*> biases, std::initializer_list<int> epis,
-                   const float* x, const float* norm_w, const char* cls) {
+                   const float* x, const float* norm_w, const char* cls, int8_t* out_qa = nullptr,
+                   float* out_da = nullptr) {
     const DevMat* mv[3];
     float* ov[3];
     const float* bv[3];
@@ -840,7 +841,7 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
     for (int e : epis) ev[i++] = e;
     const int rows_out = pair ? mv[0]->rows : (int)(macs / T / mv[0]->cols);
     bytes += (double)T * mv[0]->cols * 4.0 + (double)T * rows_out * 4.0;
-    FusedIn in{x, norm_w, c.eps};
+    FusedIn in{x, norm_w, c.eps, out_qa, out_da};
     P.timed(st, cls, bytes, macs,
             [&] { (void)launch_gemv_fused(mv, nm, pair, ov, bv, ev, in, T, s->ln->err, st); });
   };
@@ -925,9 +926,15 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
       a = attn_quantized ? session_act(s, s->ln->attn) : prepare_input(s, s->ln->attn, T, H * hd, {&L.wo});
       gemm(L.wo, a, s->ln->x, nullptr, EPI_RESIDUAL, nullptr);
     }
+    // When down is a fused-shape Q8_0 / Q4_0 GEMV too, the gate/up launch
+    // also writes the Q8A form of its output, so down reads it directly.
+    bool down_input_quantized = false;
     if (fits({&L.gate, &L.up}, true, true)) {
+      down_input_quantized = fits({&L.down}, false, false) && needs_q8a(L.down) &&
+                             gemv_fused_pair_quantizes(L.gate, L.up, true, T);
       fused({&L.gate, &L.up}, true, {s->ln->ffo}, {nullptr, nullptr}, {EPI_STORE, EPI_STORE}, s->ln->x,
-            L.ffn_norm, "gemv_fused_gate_up");
+            L.ffn_norm, "gemv_fused_gate_up", down_input_quantized ? s->ln->qa : nullptr,
+            down_input_quantized ? s->ln->da : nullptr);
     } else if (fits({&L.gate}, false, true) && fits({&L.up}, false, true)) {
       fused({&L.gate}, false, {s->ln->g}, {nullptr}, {EPI_STORE}, s->ln->x, L.ffn_norm, "gemv_fused_gate_up");
       fused({&L.up}, false, {s->ln->u}, {nullptr}, {EPI_STORE}, s->ln->x, L.ffn_norm, "gemv_fused_gate_up");
@@ -950,7 +957,9 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
                 [&] { launch_swiglu(s->ln->g, s->ln->u, T * ff, s->ln->ffo, s->ln->err, st); });
       }
     }
-    if (fits({&L.down}, false, false)) {
+    if (down_input_quantized) {
+      gemm(L.down, session_act(s, s->ln->ffo), s->ln->x, nullptr, EPI_RESIDUAL, "gemv_down");
+    } else if (fits({&L.down}, false, false)) {
       fused({&L.down}, false, {s->ln->x}, {nullptr}, {EPI_RESIDUAL}, s->ln->ffo, nullptr, "gemv_fused_down");
     } else {
       a = prepare_input(s, s->ln->ffo, T, ff, {&L.down});

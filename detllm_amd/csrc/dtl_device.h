@@ -103,11 +103,15 @@ struct FusedMats {
 };
 
 // Input of a fused decode GEMV: f32 rows [T][cols], normalised first when
-// norm_w is set.
+// norm_w is set.  out_qa / out_da (gate/up pair only): also write the Q8A
+// form of the SwiGLU output (the next projection's input), [T][rows] and
+// [T][rows / 32]; gemv_fused_pair_quantizes says when a pair can.
 struct FusedIn {
   const float* x;
   const float* norm_w;
   float eps;
+  int8_t* out_qa = nullptr;
+  float* out_da = nullptr;
 };
 
 // ---- launchers (dtl_kernels.hip) -------------------------------------------
@@ -134,6 +138,7 @@ bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const floa
 // up (nm == 2, pair_swiglu) whose dots finish as swiglu into outs[0].
 // Returns false when the shapes do not fit (the caller uses separate launches).
 bool gemv_fused_fits(const DevMat* const* mats, int nm, bool pair_swiglu, bool norm, int T);
+bool gemv_fused_pair_quantizes(const DevMat& gate, const DevMat& up, bool norm, int T);
 bool launch_gemv_fused(const DevMat* const* mats, int nm, bool pair_swiglu, float* const* outs,
                        const float* const* biases, const int* epis, const FusedIn& in, int T,
                        int* err, hipStream_t s);

@@ -68,76 +68,105 @@ __global__ void __launch_bounds__(256) k_gemv_q8(DevMat W, const int8_t* __restr
   const int8_t* arow = qa + (size_t)t * cols;
   const float* drow = da + (size_t)t * nb;
   // Q8_0: a 32-byte block is two 16-byte chunks (lanes c, c^1); Q4_0: one
-  // 16-byte block of nibbles per lane.
+  // 16-byte block of nibbles per lane.  A pass covers 64 chunks.
   const int nchunk = TYPE == kGgmlQ8_0 ? 2 * nb : nb;
-  for (int c0 = 0; c0 < nchunk; c0 += 64) {
+  struct Pass {
+    uint4 w4[R];
+    uint16_t dsc[R];
+    uint4 a0, a1;
+    float dact;
+  };
+  // Every load of a pass (R weight chunks, their block scales, the
+  // activation and its scale) is issued before any of its arithmetic.
+  auto load = [&](Pass& P, int c0) __attribute__((always_inline)) {
     const int c = c0 + lane;
     const bool cv = c < nchunk;
     const int b = TYPE == kGgmlQ8_0 ? c >> 1 : c;
-    // Every load of this chunk column (R weight chunks, their block scales,
-    // the activation and its scale) is issued before any arithmetic.
-    uint4 w4[R];
-    uint16_t dsc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
       const int row = row0 + r < rows ? row0 + r : rows - 1;
-      w4[r] = make_uint4(0, 0, 0, 0);
-      dsc[r] = 0;
+      P.w4[r] = make_uint4(0, 0, 0, 0);
+      P.dsc[r] = 0;
       if (cv) {
         if (TYPE == kGgmlQ8_0)
-          w4[r] = *(const uint4*)((const int8_t*)W.w + (size_t)row * cols + (size_t)c * 16);
+          P.w4[r] = *(const uint4*)((const int8_t*)W.w + (size_t)row * cols + (size_t)c * 16);
         else
-          w4[r] = *(const uint4*)((const uint8_t*)W.w + ((size_t)row * nb + c) * 16);
-        dsc[r] = W.d16[(size_t)row * nb + b];
+          P.w4[r] = *(const uint4*)((const uint8_t*)W.w + ((size_t)row * nb + c) * 16);
+        P.dsc[r] = W.d16[(size_t)row * nb + b];
       }
     }
-    uint4 a0 = make_uint4(0, 0, 0, 0), a1 = make_uint4(0, 0, 0, 0);
-    float dact = 0.0f;
+    P.a0 = make_uint4(0, 0, 0, 0);
+    P.a1 = make_uint4(0, 0, 0, 0);
+    P.dact = 0.0f;
     if (cv) {
       if (TYPE == kGgmlQ8_0) {
-        a0 = *(const uint4*)(arow + (size_t)c * 16);
+        P.a0 = *(const uint4*)(arow + (size_t)c * 16);
       } else {
-        a0 = *(const uint4*)(arow + (size_t)c * 32);
-        a1 = *(const uint4*)(arow + (size_t)c * 32 + 16);
+        P.a0 = *(const uint4*)(arow + (size_t)c * 32);
+        P.a1 = *(const uint4*)(arow + (size_t)c * 32 + 16);
       }
-      dact = drow[b];
+      P.dact = drow[b];
     }
+  };
+  auto reduce = [&](const Pass& P, int c0) __attribute__((always_inline)) {
+    const int c = c0 + lane;
+    const bool cv = c < nchunk;
+    const int b = TYPE == kGgmlQ8_0 ? c >> 1 : c;
     int asum = 0;
     if (TYPE != kGgmlQ8_0) {
       // Q4_0 nibbles are offset by 8: isum = sum(lo*a) + sum(hi*a') - 8*sum(a).
       const uint32_t ones = 0x01010101u;
-      asum = dot4(ones, a0.x, asum);
-      asum = dot4(ones, a0.y, asum);
-      asum = dot4(ones, a0.z, asum);
-      asum = dot4(ones, a0.w, asum);
-      asum = dot4(ones, a1.x, asum);
-      asum = dot4(ones, a1.y, asum);
-      asum = dot4(ones, a1.z, asum);
-      asum = dot4(ones, a1.w, asum);
+      asum = dot4(ones, P.a0.x, asum);
+      asum = dot4(ones, P.a0.y, asum);
+      asum = dot4(ones, P.a0.z, asum);
+      asum = dot4(ones, P.a0.w, asum);
+      asum = dot4(ones, P.a1.x, asum);
+      asum = dot4(ones, P.a1.y, asum);
+      asum = dot4(ones, P.a1.z, asum);
+      asum = dot4(ones, P.a1.w, asum);
     }
 #pragma unroll
     for (int r = 0; r < R; r++) {
       int isum = 0;
       if (TYPE == kGgmlQ8_0) {
-        isum = dot4(w4[r].x, a0.x, isum);
-        isum = dot4(w4[r].y, a0.y, isum);
-        isum = dot4(w4[r].z, a0.z, isum);
-        isum = dot4(w4[r].w, a0.w, isum);
+        isum = dot4(P.w4[r].x, P.a0.x, isum);
+        isum = dot4(P.w4[r].y, P.a0.y, isum);
+        isum = dot4(P.w4[r].z, P.a0.z, isum);
+        isum = dot4(P.w4[r].w, P.a0.w, isum);
         isum += __shfl_xor(isum, 1);
       } else {
         const uint32_t m = 0x0f0f0f0fu;
-        isum = dot4(w4[r].x & m, a0.x, isum);
-        isum = dot4(w4[r].y & m, a0.y, isum);
-        isum = dot4(w4[r].z & m, a0.z, isum);
-        isum = dot4(w4[r].w & m, a0.w, isum);
-        isum = dot4((w4[r].x >> 4) & m, a1.x, isum);
-        isum = dot4((w4[r].y >> 4) & m, a1.y, isum);
-        isum = dot4((w4[r].z >> 4) & m, a1.z, isum);
-        isum = dot4((w4[r].w >> 4) & m, a1.w, isum);
+        isum = dot4(P.w4[r].x & m, P.a0.x, isum);
+        isum = dot4(P.w4[r].y & m, P.a0.y, isum);
+        isum = dot4(P.w4[r].z & m, P.a0.z, isum);
+        isum = dot4(P.w4[r].w & m, P.a0.w, isum);
+        isum = dot4((P.w4[r].x >> 4) & m, P.a1.x, isum);
+        isum = dot4((P.w4[r].y >> 4) & m, P.a1.y, isum);
+        isum = dot4((P.w4[r].z >> 4) & m, P.a1.z, isum);
+        isum = dot4((P.w4[r].w >> 4) & m, P.a1.w, isum);
         isum -= 8 * asum;
       }
       const bool writer = TYPE == kGgmlQ8_0 ? cv && !(c & 1) : cv;
-      if (writer && row0 + r < rows) mine[r * nbs + b] = (f16_to_f32(dsc[r]) * dact) * (float)isum;
+      if (writer && row0 + r < rows) mine[r * nbs + b] = (f16_to_f32(P.dsc[r]) * P.dact) * (float)isum;
+    }
+  };
+  // Rows of up to kPre passes (8192 Q8_0 columns) with few rows per wave:
+  // all passes' loads go out before the first pass's arithmetic.
+  constexpr int kPre = R <= 2 ? 8 : 1;
+  const int npass = (nchunk + 63) / 64;
+  if (kPre > 1 && npass <= kPre) {
+    Pass P[kPre];
+#pragma unroll
+    for (int p = 0; p < kPre; p++)
+      if (p < npass) load(P[p], 64 * p);
+#pragma unroll
+    for (int p = 0; p < kPre; p++)
+      if (p < npass) reduce(P[p], 64 * p);
+  } else {
+    for (int c0 = 0; c0 < nchunk; c0 += 64) {
+      Pass P;
+      load(P, c0);
+      reduce(P, c0);
     }
   }
   __syncthreads();
@@ -401,22 +430,27 @@ __global__ void __launch_bounds__(64) k_gemv_q4k(const float* __restrict__ w32, 
 namespace {
 
 // Float4s per thread (norm pass) or 256-element spans per wave (plain
-// pass) loaded at once: inputs of up to 4096 elements take one round trip.
-constexpr int kProBatch = 4;
+// pass) loaded at once: inputs of up to 4096 elements take one round trip
+// (with 4 waves; one batch already covers that with 16).
+template <int NW>
+constexpr int pro_batch() { return NW >= 16 ? 1 : 4; }
 
+template <int NW>  // waves per workgroup
 __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols, bool norm,
                                              float* xs, float* ws, float* sq, int cs,
                                              int8_t* qa_s, float* da_s, float* misc) {
+  constexpr int kProBatch = pro_batch<NW>();
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const float* x = in.x + (size_t)t * cols;
   const QuantOut q{qa_s, da_s, nullptr, nullptr, nullptr};
   bool bad = false;
   if (norm) {
-    for (int base = 0; base < cols; base += 1024 * kProBatch) {
+    constexpr int kStep = 4 * 64 * NW;  // elements per float4 pass of the workgroup
+    for (int base = 0; base < cols; base += kStep * kProBatch) {
       float4 xv[kProBatch], wv[kProBatch];
 #pragma unroll
       for (int k = 0; k < kProBatch; k++) {
-        const int i = base + 1024 * k + 4 * tid;
+        const int i = base + kStep * k + 4 * tid;
         xv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
         wv[k] = xv[k];
         if (i < cols) {
@@ -426,7 +460,7 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
       }
 #pragma unroll
       for (int k = 0; k < kProBatch; k++) {
-        const int i = base + 1024 * k + 4 * tid;
+        const int i = base + kStep * k + 4 * tid;
         if (i < cols) {
           const float xe[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
           const float we[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
@@ -452,7 +486,7 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
     }
     __syncthreads();
     const float r = misc[8];
-    for (int span = wave; span * 256 < cols; span += 4) {
+    for (int span = wave; span * 256 < cols; span += NW) {
       const int e = span * 256 + 4 * lane;
       const bool inb = e < cols;
       float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -469,16 +503,16 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
       quantize_span(v, inb, (size_t)span * 256, true, false, q);
     }
   } else {
-    for (int s0 = wave; s0 * 256 < cols; s0 += 4 * kProBatch) {
+    for (int s0 = wave; s0 * 256 < cols; s0 += NW * kProBatch) {
       float4 f[kProBatch];
 #pragma unroll
       for (int k = 0; k < kProBatch; k++) {
-        const int e = (s0 + 4 * k) * 256 + 4 * lane;
+        const int e = (s0 + NW * k) * 256 + 4 * lane;
         f[k] = e < cols ? *reinterpret_cast<const float4*>(x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
       }
 #pragma unroll
       for (int k = 0; k < kProBatch; k++) {
-        const int span = s0 + 4 * k;
+        const int span = s0 + NW * k;
         if (span * 256 < cols) {
           const int e = span * 256 + 4 * lane;
           const bool inb = e < cols;
@@ -497,31 +531,33 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
 
 // LDS bytes of k_gemv_q8f: block terms, the Q8A activations and, with a
 // norm, its scratch (the row, the weights, the chain-major squares).
-size_t gemv_fused_smem(int nr, int cols, int nb, bool norm) {
+size_t gemv_fused_smem(int nr, int cols, int nb, bool norm, int nw) {
   const size_t cs = (size_t)((((cols + 7) / 8) + 3) & ~3);
-  size_t b = (size_t)4 * nr * nb_stride(nb) * 4 + (size_t)((cols + 15) & ~15) + (size_t)((nb + 3) & ~3) * 4;
+  size_t b = (size_t)nw * nr * nb_stride(nb) * 4 + (size_t)((cols + 15) & ~15) + (size_t)((nb + 3) & ~3) * 4;
   if (norm) b += 2 * (size_t)((cols + 3) & ~3) * 4 + 8 * cs * 4 + 16 * 4;
   return b;
 }
 
-template <int TYPE, int R, bool PAIR>
-__global__ void __launch_bounds__(256) k_gemv_q8f(FusedMats M, FusedIn in, int* err) {
+template <int TYPE, int R, bool PAIR, bool QOUT = false, int NW = 4>
+__global__ void __launch_bounds__(64 * NW) k_gemv_q8f(FusedMats M, FusedIn in, int* err) {
   constexpr int NR = PAIR ? 2 * R : R;
+  static_assert(!QOUT || (PAIR && NW * R == 32), "quantized output: one 32-row Q8A block per workgroup");
   extern __shared__ __align__(16) float lds[];
+  __shared__ float vq[QOUT ? 32 : 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t = blockIdx.y;
   const int cols = M.cols, nb = M.nb;
   const int cs = (((cols + 7) / 8) + 3) & ~3;
   const int nbs = nb_stride(nb);
   float* vb = lds;
-  int8_t* qa_s = reinterpret_cast<int8_t*>(lds + 4 * NR * nbs);
+  int8_t* qa_s = reinterpret_cast<int8_t*>(lds + NW * NR * nbs);
   float* da_s = reinterpret_cast<float*>(qa_s + ((cols + 15) & ~15));
   float* xs = da_s + ((nb + 3) & ~3);
   float* ws = xs + ((cols + 3) & ~3);
   float* sq = ws + ((cols + 3) & ~3);
   float* misc = sq + 8 * cs;
   float* mine = vb + (size_t)wave * NR * nbs;
-  const int row0 = (blockIdx.x * 4 + wave) * R;
+  const int row0 = (blockIdx.x * NW + wave) * R;
   // Slot r: (matrix, row) of the r-th dot of this wave.  Matrix choice is
   // wave-uniform, so the selects below stay scalar.
   const void* wp[NR];
@@ -576,7 +612,7 @@ __global__ void __launch_bounds__(256) k_gemv_q8f(FusedMats M, FusedIn in, int* 
       }
     }
     if (cb == 0)
-      bad |= q8a_prologue(in, t, cols, in.norm_w != nullptr, xs, ws, sq, cs, qa_s, da_s, misc);
+      bad |= q8a_prologue<NW>(in, t, cols, in.norm_w != nullptr, xs, ws, sq, cs, qa_s, da_s, misc);
 #pragma unroll
     for (int ii = 0; ii < NI; ii++) {
       const int c = cb + 64 * ii + lane;
@@ -641,6 +677,7 @@ __global__ void __launch_bounds__(256) k_gemv_q8f(FusedMats M, FusedIn in, int* 
         const float v = silu_det(g) * u;
         if (!finite(g) || !finite(u) || !finite(v)) bad = true;
         M.out[0][(size_t)t * M.rows[0] + row] = v;
+        if (QOUT) vq[wave * R + lane] = v;
       }
     } else {
       const int gr = row0 + lane;
@@ -654,6 +691,17 @@ __global__ void __launch_bounds__(256) k_gemv_q8f(FusedMats M, FusedIn in, int* 
         const float v = chain_sum_lds(0.0f, mine + lane * nbs, nb);
         if (!epilogue(v, out, (size_t)t * rows + row, bias, row, epi)) bad = true;
       }
+    }
+  }
+  if (QOUT) {
+    // The workgroup's 32 rows are one Q8A block of the SwiGLU output
+    // (quantize_q8a_into, det-quant lib.rs:111-137): lanes 0-31 of wave 0
+    // form it, lanes 32-63 only take part in the reductions.
+    __syncthreads();
+    if (wave == 0) {
+      const QuantOut q{in.out_qa, in.out_da, nullptr, nullptr, nullptr};
+      quantize_q8a_lanes(lane < 32 ? vq[lane] : 0.0f, (size_t)t * M.rows[0] + (size_t)blockIdx.x * 32,
+                         q, lane < 32);
     }
   }
   if (bad) flag(err, ERRBIT_NON_FINITE);
@@ -730,7 +778,15 @@ void launch_q8f(const FusedMats& M, const FusedIn& in, int T, int R, bool norm, 
   const int nr = PAIR ? 2 * R : R;
   const int rows = PAIR ? M.rows[0] : M.total_rows;
   dim3 grid((rows + 4 * R - 1) / (4 * R), T);
-  const size_t smem = gemv_fused_smem(nr, M.cols, M.nb, norm);
+  const size_t smem = gemv_fused_smem(nr, M.cols, M.nb, norm, 4);
+  if constexpr (PAIR) {
+    if (in.out_qa) {
+      // two rows per wave, sixteen waves: one 32-row Q8A block per workgroup
+      launch_kernel((k_gemv_q8f<TYPE, 2, true, true, 16>), dim3(rows / 32, T), dim3(1024),
+                    gemv_fused_smem(4, M.cols, M.nb, norm, 16), s, M, in, err);
+      return;
+    }
+  }
   if (R == 4)
     launch_kernel((k_gemv_q8f<TYPE, 4, PAIR>), grid, dim3(256), smem, s, M, in, err);
   else if (R == 2)
@@ -749,7 +805,13 @@ bool gemv_fused_fits(const DevMat* const* mats, int nm, bool pair_swiglu, bool n
     if (m.type != m0.type || m.cols != m0.cols || m.nb != m0.nb) return false;
     if (pair_swiglu && m.rows != m0.rows) return false;
   }
-  return m0.cols % 32 == 0 && gemv_fused_smem(pair_swiglu ? 2 : 1, m0.cols, m0.nb, norm) <= 64 * 1024;
+  return m0.cols % 32 == 0 && gemv_fused_smem(pair_swiglu ? 2 : 1, m0.cols, m0.nb, norm, 4) <= 64 * 1024;
+}
+
+bool gemv_fused_pair_quantizes(const DevMat& gate, const DevMat& up, bool norm, int T) {
+  const DevMat* mats[2] = {&gate, &up};
+  return gemv_fused_fits(mats, 2, true, norm, T) && gate.rows % 32 == 0 &&
+         gemv_fused_smem(4, gate.cols, gate.nb, norm, 16) <= 64 * 1024;
 }
 
 bool launch_gemv_fused(const DevMat* const* mats, int nm, bool pair_swiglu, float* const* outs,
@@ -784,8 +846,10 @@ bool launch_gemv_fused(const DevMat* const* mats, int nm, bool pair_swiglu, floa
   // Rows per wave as the unfused kernel chooses them; LDS bounds the rest.
   int R = rows >= 16384 ? 4 : (rows >= 4096 ? 2 : 1);
   const int mult = pair_swiglu ? 2 : 1;
-  while (R > 1 && gemv_fused_smem(mult * R, m0.cols, m0.nb, norm) > 64 * 1024) R >>= 1;
-  if (gemv_fused_smem(mult * R, m0.cols, m0.nb, norm) > 64 * 1024) return false;
+  if (in.out_qa && (!pair_swiglu || !gemv_fused_pair_quantizes(*mats[0], *mats[1], norm, T)))
+    return false;
+  while (R > 1 && gemv_fused_smem(mult * R, m0.cols, m0.nb, norm, 4) > 64 * 1024) R >>= 1;
+  if (gemv_fused_smem(mult * R, m0.cols, m0.nb, norm, 4) > 64 * 1024) return false;
   if (m0.type == kGgmlQ8_0) {
     if (pair_swiglu) launch_q8f<kGgmlQ8_0, true>(M, in, T, R, norm, err, s);
     else launch_q8f<kGgmlQ8_0, false>(M, in, T, R, norm, err, s);

@@ -104,8 +104,10 @@ __device__ __forceinline__ void quantize_span(const float v[4], bool in, size_t 
 
 // Q8A of one value per lane, 32-lane blocks (lanes 0-31 and 32-63 of a
 // wave are two blocks): the same amax, scale and rounding as quantize_span.
-// base: element offset of lane 0 (a multiple of 32).
-__device__ __forceinline__ void quantize_q8a_lanes(float v, size_t base, const QuantOut& q) {
+// base: element offset of lane 0 (a multiple of 32).  Lanes with store off
+// take part in the reductions only.
+__device__ __forceinline__ void quantize_q8a_lanes(float v, size_t base, const QuantOut& q,
+                                                   bool store = true) {
   const int lane = threadIdx.x & 63;
   float amax = v < 0.0f ? -v : v;
 #pragma unroll
@@ -120,6 +122,7 @@ __device__ __forceinline__ void quantize_q8a_lanes(float v, size_t base, const Q
     qv = (int8_t)r;
     fv = d * (float)r;
   }
+  if (!store) return;
   q.qa[base + lane] = qv;
   if (q.af) q.af[base + lane] = fv;
   if ((lane & 31) == 0) q.da[(base + lane) / 32] = amax == 0.0f ? 0.0f : d;
