@@ -1252,20 +1252,33 @@ __global__ void __launch_bounds__(256) k_attn_split_pv(const float* scores, Rope
     if (tid < kSplitDims) o[tid] = vrow(0)[d0 + tid];
     return;
   }
+  // The score row is loaded first (the max needs it at once), the V rows
+  // right after, so they arrive while the softmax runs.
+  const float* srow = scores + ((size_t)t * H + h) * n_ctx;
+  // Every load is unconditional (indices past len re-read a valid entry),
+  // so the wait before the max counts the V loads still in flight instead
+  // of draining them.
+  float sv[kSplitMaxRows / 256];
+#pragma unroll
+  for (int k = 0; k < kSplitMaxRows / 256; k++) {
+    const int j = 256 * k + tid;
+    sv[k] = srow[j < len ? j : 0];
+  }
   const int jr = tid >> 2, c = 4 * (tid & 3);
   float4 vreg[kSplitVPer];
 #pragma unroll
-  for (int i = 0; i < kSplitVPer; i++)
-    if (64 * i < len) {
-      const int j = 64 * i + jr;
-      vreg[i] = *reinterpret_cast<const float4*>(vrow(j < len ? j : len - 1) + d0 + c);
-    }
-  const float* srow = scores + ((size_t)t * H + h) * n_ctx;
+  for (int i = 0; i < kSplitVPer; i++) {
+    const int j = 64 * i + jr;
+    vreg[i] = *reinterpret_cast<const float4*>(vrow(j < len ? j : len - 1) + d0 + c);
+  }
   float mx = -__builtin_huge_valf();
-  for (int j = tid; j < len; j += 256) {
-    const float sv = srow[j];
-    pr[j] = sv;
-    mx = fmaxf(mx, sv);
+#pragma unroll
+  for (int k = 0; k < kSplitMaxRows / 256; k++) {
+    const int j = 256 * k + tid;
+    if (j < len) {
+      pr[j] = sv[k];
+      mx = fmaxf(mx, sv[k]);
+    }
   }
   for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
   if (lane == 0) red[wave] = mx;
