@@ -9,6 +9,9 @@
 // weights (Q6_K, Q8_0).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdio.h>
+
+#include <array>
 
 #include "dtl_blocks.h"
 #include "dtl_device.h"
@@ -486,6 +489,134 @@ __global__ void __launch_bounds__(256) k_q4k_f32w(Q4kF32Args p) {
 #undef DTL_ISSUE_W
 #undef DTL_COMMIT_W
 
+// The same product with the lanes of a wave split over rows and positions:
+// lane = (position p = lane % PW, row r = lane / PW), RW = 64 / PW rows per
+// wave.  A workgroup is WP x WR waves covering PB = WP * PW positions of
+// RB = WR * RW rows; it stages each 64-element slice of those positions'
+// activations and rows' weights in LDS once (double-buffered, the next
+// slice's global loads in flight) and every lane walks one chain per matrix
+// in element order.  Lanes of one position (or one row) read the same LDS
+// address, so per four elements a wave reads PW activation and RW weight
+// float4 instead of 64 and one: with one chain per lane the activation reads
+// of the one-row-per-wave mapping ask the LDS for as many bytes per cycle as
+// it delivers.
+template <int PW, int WP, int WR, int MODE>
+__global__ void __launch_bounds__(64 * WP * WR) k_q4k_f32m(Q4kF32Args p) {
+  constexpr int NT = 64 * WP * WR;
+  constexpr int NM = MODE == MODE_PAIR ? 2 : 1;
+  constexpr int RW = 64 / PW;
+  constexpr int PB = WP * PW;            // positions per workgroup
+  constexpr int RB = WR * RW;            // rows per workgroup (of each matrix)
+  constexpr int NR = PB + NM * RB;       // staged LDS rows per slice
+  constexpr int SL = 64, LD = SL + 4;    // elements per slice, padded LDS row
+  constexpr int F = NR * SL / 4;         // float4 per slice
+  constexpr int PERT = (F + NT - 1) / NT;
+  static_assert(PERT >= 1 && PERT <= 4, "staging slots per thread");
+  __shared__ __align__(16) float st[2][NR][LD];
+  const int cols = p.cols, T = p.T;
+  const int rows_total = MODE == MODE_CAT ? p.rows0 + p.rows1 : p.rows0;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wp = wave % WP, wr = wave / WP;
+  const int pl = lane % PW, rl = lane / PW;
+  const int t = blockIdx.y * PB + wp * PW + pl;
+  const int rloc = wr * RW + rl;
+  const int g = blockIdx.x * RB + rloc;  // this lane's row (of the concatenation)
+  float acc[NM];
+#pragma unroll
+  for (int m = 0; m < NM; m++) acc[m] = 0.0f;
+
+  // Staging slot k of thread x moves float4 f = x + k NT of the slice: LDS
+  // row f / 16 (activations of position f / 16 first, then the weight rows,
+  // matrix by matrix), columns 4 (f % 16).  Out-of-range positions and rows
+  // read the last valid one; slots past the slice load a valid address and
+  // store nothing, so every load is unconditional.
+  auto slot_src = [&](int f) -> const float* {
+    const int sr = f < F ? f >> 4 : 0, c4 = f & 15;
+    if (sr < PB) {
+      const int tt = blockIdx.y * PB + sr;
+      return p.af + (size_t)(tt < T ? tt : T - 1) * cols + c4 * 4;
+    }
+    const int wrow = sr - PB;
+    if (MODE == MODE_PAIR) {
+      const int m = wrow / RB, rr = blockIdx.x * RB + wrow % RB;
+      return (m ? p.w1 : p.w0) + (size_t)(rr < p.rows0 ? rr : p.rows0 - 1) * cols + c4 * 4;
+    }
+    int gg = blockIdx.x * RB + wrow;
+    gg = gg < rows_total ? gg : rows_total - 1;
+    const bool m = MODE == MODE_CAT && gg >= p.rows0;
+    return (m ? p.w1 : p.w0) + (size_t)(m ? gg - p.rows0 : gg) * cols + c4 * 4;
+  };
+  const int x = threadIdx.x;
+  const float* s0 = slot_src(x);
+  const float* s1 = slot_src(x + NT);
+  const float* s2 = slot_src(x + 2 * NT);
+  const float* s3 = slot_src(x + 3 * NT);
+  auto slot_dst = [&](int f) { return (f >> 4) * LD + (f & 15) * 4; };
+  const int d0 = slot_dst(x), d1 = slot_dst(x + NT), d2 = slot_dst(x + 2 * NT),
+            d3 = slot_dst(x + 3 * NT);
+  const bool k0 = x < F, k1 = x + NT < F, k2 = x + 2 * NT < F, k3 = x + 3 * NT < F;
+  float4 q0, q1, q2, q3;
+#define DTL_ISSUE_M(e0)                                                       \
+  do {                                                                        \
+    q0 = *(const float4*)(s0 + (e0));                                         \
+    if (PERT > 1) q1 = *(const float4*)(s1 + (e0));                           \
+    if (PERT > 2) q2 = *(const float4*)(s2 + (e0));                           \
+    if (PERT > 3) q3 = *(const float4*)(s3 + (e0));                           \
+  } while (0)
+#define DTL_COMMIT_M(b)                                                       \
+  do {                                                                        \
+    float* sb = &st[b][0][0];                                                 \
+    if (k0) *(float4*)(sb + d0) = q0;                                         \
+    if (PERT > 1 && k1) *(float4*)(sb + d1) = q1;                             \
+    if (PERT > 2 && k2) *(float4*)(sb + d2) = q2;                             \
+    if (PERT > 3 && k3) *(float4*)(sb + d3) = q3;                             \
+  } while (0)
+  DTL_ISSUE_M(0);
+  DTL_COMMIT_M(0);
+  __syncthreads();
+  int buf = 0;
+  for (int e0 = 0; e0 < cols; e0 += SL) {
+    const bool more = e0 + SL < cols;
+    if (more) DTL_ISSUE_M(e0 + SL);
+    const float* ar = &st[buf][wp * PW + pl][0];
+#pragma unroll 4
+    for (int i = 0; i < SL; i += 4) {
+      const float4 a = *(const float4*)(ar + i);
+#pragma unroll
+      for (int m = 0; m < NM; m++) {
+        const float4 w = *(const float4*)&st[buf][PB + m * RB + rloc][i];
+        float c = acc[m];
+        c += w.x * a.x;
+        c += w.y * a.y;
+        c += w.z * a.z;
+        c += w.w * a.w;
+        acc[m] = c;
+      }
+    }
+    if (more) DTL_COMMIT_M(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+#undef DTL_ISSUE_M
+#undef DTL_COMMIT_M
+  if (t >= T || g >= rows_total) return;
+  bool ok = true;
+  if (MODE == MODE_PAIR) {
+    const float gv = acc[0], uv = acc[NM - 1];
+    const float v = silu_det(gv) * uv;
+    ok = finite(gv) && finite(uv) && finite(v);
+    p.ffo[(size_t)t * p.rows0 + g] = v;
+  } else {
+    const bool m = MODE == MODE_CAT && g >= p.rows0;
+    const int local = m ? g - p.rows0 : g;
+    const int R = m ? p.rows1 : p.rows0;
+    ok = store_epilogue(acc[0], m ? p.out1 : p.out0, (size_t)t * R + local, m ? p.bias1 : p.bias0,
+                        local, p.epi);
+  }
+  if (!ok) flag(p.err, ERRBIT_NON_FINITE);
+}
+
 // Exact f32 copy of a Q4_K matrix: q4_k_value for every element.
 __global__ void k_dequant_q4k(DevMat W, float* out) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -709,9 +840,43 @@ int q4k_nk(int mode, int rows_total) {
   return rows_total >= 8192 ? 2 : 1;
 }
 
+// Tile of the split mapping as PW * 100 + WP * 10 + WR (0: k_q4k_f32w), per
+// mode; DETLLM_Q4K_MAP="single,pair,cat" overrides.  Measured at 64
+// positions on the 2048-column TinyLlama shapes: single matrices (wo, 2048 x
+// 2048, and ffn_down, 2048 x 5632) 26% faster with 8 positions x 8 rows per
+// wave and 2 x 4 waves, the wq+wk concatenation 14% faster with 2 x 2 waves;
+// the gate/up pair (two chains per lane at 16 positions x 4 rows, or four
+// in k_q4k_f32w) runs at the same rate either way and keeps k_q4k_f32w,
+// which overlapped better with the other chunks in flight.
+int q4k_map(int mode) {
+  static const std::array<int, 3> forced = [] {
+    std::array<int, 3> f{-1, -1, -1};
+    if (const char* e = getenv("DETLLM_Q4K_MAP")) sscanf(e, "%d,%d,%d", &f[0], &f[1], &f[2]);
+    return f;
+  }();
+  if (forced[mode] >= 0) return forced[mode];
+  static constexpr int kDefault[3] = {842, 0, 822};  // single, pair, cat
+  return kDefault[mode];
+}
+
+template <int PW, int WP, int WR, int MODE>
+void launch_q4k_f32m(const Q4kF32Args& a, int rows_total, hipStream_t s) {
+  constexpr int RB = WR * 64 / PW, PB = WP * PW;
+  dim3 grid((rows_total + RB - 1) / RB, (a.T + PB - 1) / PB);
+  launch_kernel(k_q4k_f32m<PW, WP, WR, MODE>, grid, dim3(64 * WP * WR), 0, s, a);
+}
+
 template <int MODE>
 void launch_q4k_f32w(const Q4kF32Args& a, hipStream_t s) {
   const int rows_total = MODE == MODE_CAT ? a.rows0 + a.rows1 : a.rows0;
+  switch (q4k_map(MODE)) {
+    case 841: return launch_q4k_f32m<8, 4, 1, MODE>(a, rows_total, s);
+    case 822: return launch_q4k_f32m<8, 2, 2, MODE>(a, rows_total, s);
+    case 842: return launch_q4k_f32m<8, 4, 2, MODE>(a, rows_total, s);
+    case 1642: return launch_q4k_f32m<16, 4, 2, MODE>(a, rows_total, s);
+    case 1622: return launch_q4k_f32m<16, 2, 2, MODE>(a, rows_total, s);
+    default: break;
+  }
   const int nk = q4k_nk(MODE, rows_total);
   dim3 grid((rows_total + kWaves * nk - 1) / (kWaves * nk), (a.T + 63) / 64);
   dim3 block(kWaves * 64);

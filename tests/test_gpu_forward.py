@@ -65,6 +65,7 @@ def test_tiny_workload_matches_oracle_all_chunks():
     ("smollm2", 2, 40, 32),
     ("qwen05", 1, 21, 21),
     ("tinyllama", 1, 70, 64),
+    ("tinyllama", 1, 37, 37),   # Q4_K GEMM tiles with positions past the chunk
 ])
 def test_baseline_shapes_match_oracle(name, layers, n_tok, chunk):
     from detllm_amd import synth

@@ -164,6 +164,7 @@ GEMV_CASES = [
     (8, 66000, 32, 1), (8, 300, 8192, 1), (8, 20, 576, 12),
     (2, 40, 64, 2), (2, 17, 512, 1), (2, 66000, 64, 1), (2, 5000, 96, 3),
     (12, 45, 2048, 1), (12, 7, 5632, 3), (12, 30, 512, 64), (12, 9000, 256, 1), (12, 13, 256, 8),
+    (12, 45, 256, 37), (12, 100, 768, 20),
     (14, 50, 2048, 1), (14, 9, 5632, 2), (14, 20, 512, 64), (14, 300, 256, 1), (14, 33, 4096, 1),
 ]
 
