@@ -876,6 +876,13 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
           launch_gemm_cat_q4k(L.wq, L.wk, a, T, s->ln->q, s->ln->k, L.bq, L.bk, L.bq ? EPI_BIAS : EPI_STORE,
                               s->ln->err, st);
         });
+      } else if (gemv_q4k_two_fit(L.wq, L.wk, false, T)) {
+        // decode: the same pair in one GEMV launch
+        double bytes = (double)(L.wq.rows + L.wk.rows) * L.wq.cols * weight_bytes_per_elem(GGML_Q4_K) +
+                       (double)T * L.wq.cols * (1.0 + 4.0 / 32) + (double)T * (L.wq.rows + L.wk.rows) * 4.0;
+        P.timed(st, "gemv_q4_k_qk", bytes, (double)(L.wq.rows + L.wk.rows) * L.wq.cols * T, [&] {
+          launch_gemv_cat_q4k(L.wq, L.wk, a, T, s->ln->q, s->ln->k, L.bq, L.bk, e_q, e_k, s->ln->err, st);
+        });
       } else {
         gemm(L.wq, a, s->ln->q, L.bq, L.bq ? EPI_BIAS : EPI_STORE, nullptr);
         gemm(L.wk, a, s->ln->k, L.bk, L.bk ? EPI_BIAS : EPI_STORE, nullptr);
@@ -949,6 +956,13 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
                        (double)T * d * (1.0 + 4.0 / 32) + (double)T * ff * 4.0;
         P.timed(st, "gemm_q4_k_gate_up", bytes, 2.0 * L.gate.rows * L.gate.cols * T, [&] {
           launch_gemm_pair_swiglu_q4k(L.gate, L.up, a, T, nullptr, nullptr, s->ln->ffo, s->ln->err, st);
+        });
+      } else if (gemv_q4k_two_fit(L.gate, L.up, true, T)) {
+        // decode: gate, up and swiglu in one GEMV launch
+        double bytes = 2.0 * L.gate.rows * L.gate.cols * weight_bytes_per_elem(GGML_Q4_K) +
+                       (double)T * d * (1.0 + 4.0 / 32) + (double)T * ff * 4.0;
+        P.timed(st, "gemv_q4_k_gate_up", bytes, 2.0 * L.gate.rows * L.gate.cols * T, [&] {
+          launch_gemv_pair_swiglu_q4k(L.gate, L.up, a, T, s->ln->ffo, s->ln->err, st);
         });
       } else {
         gemm(L.gate, a, s->ln->g, nullptr, EPI_STORE, nullptr);
