@@ -787,6 +787,11 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
   Profiler& P = s->prof;
   // Algorithmic traffic of one GEMM: weights once, quantised activations
   // and f32 outputs per position (the residual epilogue also reads x).
+  // Q4_K decode GEMV from the raw f32 input, residual epilogue.
+  auto q4k_gemv_bytes = [&](const DevMat& W, int Tn, bool residual) {
+    return (double)W.rows * W.cols * weight_bytes_per_elem(GGML_Q4_K) + (double)Tn * W.cols * 4.0 +
+           (double)Tn * W.rows * (residual ? 8.0 : 4.0);
+  };
   auto gemm = [&](const DevMat& W, const DevAct& a, float* out, const float* bias, int epi,
                   const char* cls) {
     double act = W.type == GGML_F32 ? 4.0 : (W.type == GGML_Q6_K ? 1.0 + 4.0 / 256 : 1.0 + 4.0 / 32);
@@ -876,12 +881,13 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
           launch_gemm_cat_q4k(L.wq, L.wk, a, T, s->ln->q, s->ln->k, L.bq, L.bk, L.bq ? EPI_BIAS : EPI_STORE,
                               s->ln->err, st);
         });
-      } else if (gemv_q4k_two_fit(L.wq, L.wk, false, T)) {
+      } else if (gemv_q4k_fit(L.wq, &L.wk, false, false, T)) {
         // decode: the same pair in one GEMV launch
         double bytes = (double)(L.wq.rows + L.wk.rows) * L.wq.cols * weight_bytes_per_elem(GGML_Q4_K) +
-                       (double)T * L.wq.cols * (1.0 + 4.0 / 32) + (double)T * (L.wq.rows + L.wk.rows) * 4.0;
+                       (double)T * L.wq.cols * 4.0 + (double)T * (L.wq.rows + L.wk.rows) * 4.0;
         P.timed(st, "gemv_q4_k_qk", bytes, (double)(L.wq.rows + L.wk.rows) * L.wq.cols * T, [&] {
-          launch_gemv_cat_q4k(L.wq, L.wk, a, T, s->ln->q, s->ln->k, L.bq, L.bk, e_q, e_k, s->ln->err, st);
+          launch_gemv_q4k(L.wq, &L.wk, false, Q4kIn{a.af, nullptr, nullptr, 0.0f}, T, s->ln->q, s->ln->k,
+                          L.bq, L.bk, e_q, e_k, s->ln->err, st);
         });
       } else {
         gemm(L.wq, a, s->ln->q, L.bq, L.bq ? EPI_BIAS : EPI_STORE, nullptr);
@@ -929,6 +935,12 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
     }
     if (fits({&L.wo}, false, false)) {
       fused({&L.wo}, false, {s->ln->x}, {nullptr}, {EPI_RESIDUAL}, s->ln->attn, nullptr, "gemv_fused_o");
+    } else if (!attn_quantized && gemv_q4k_fit(L.wo, nullptr, false, true, T)) {
+      // decode: the attention output's quantisation inside the wo launch
+      P.timed(st, "gemv_q4_k_o", q4k_gemv_bytes(L.wo, T, true), (double)L.wo.rows * L.wo.cols * T, [&] {
+        launch_gemv_q4k(L.wo, nullptr, false, Q4kIn{nullptr, s->ln->attn, nullptr, 0.0f}, T, s->ln->x,
+                        nullptr, nullptr, nullptr, EPI_RESIDUAL, 0, s->ln->err, st);
+      });
     } else {
       a = attn_quantized ? session_act(s, s->ln->attn) : prepare_input(s, s->ln->attn, T, H * hd, {&L.wo});
       gemm(L.wo, a, s->ln->x, nullptr, EPI_RESIDUAL, nullptr);
@@ -947,6 +959,14 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
       fused({&L.up}, false, {s->ln->u}, {nullptr}, {EPI_STORE}, s->ln->x, L.ffn_norm, "gemv_fused_gate_up");
       P.timed(st, "swiglu", (double)T * ff * 12.0, 0.0,
               [&] { launch_swiglu(s->ln->g, s->ln->u, T * ff, s->ln->ffo, s->ln->err, st); });
+    } else if (gemv_q4k_fit(L.gate, &L.up, true, true, T)) {
+      // decode: the FFN rmsnorm, its quantisation, gate, up and swiglu in one launch
+      double bytes = 2.0 * L.gate.rows * L.gate.cols * weight_bytes_per_elem(GGML_Q4_K) +
+                     (double)T * d * 4.0 + (double)d * 4.0 + (double)T * ff * 4.0;
+      P.timed(st, "gemv_q4_k_gate_up", bytes, 2.0 * L.gate.rows * L.gate.cols * T, [&] {
+        launch_gemv_q4k(L.gate, &L.up, true, Q4kIn{nullptr, s->ln->x, L.ffn_norm, c.eps}, T, s->ln->ffo,
+                        nullptr, nullptr, nullptr, EPI_STORE, EPI_STORE, s->ln->err, st);
+      });
     } else {
       a = rms(L.ffn_norm, {&L.gate, &L.up});
       if (T >= 16 && L.gate.type == GGML_Q4_K && L.up.type == GGML_Q4_K &&
@@ -956,13 +976,6 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
                        (double)T * d * (1.0 + 4.0 / 32) + (double)T * ff * 4.0;
         P.timed(st, "gemm_q4_k_gate_up", bytes, 2.0 * L.gate.rows * L.gate.cols * T, [&] {
           launch_gemm_pair_swiglu_q4k(L.gate, L.up, a, T, nullptr, nullptr, s->ln->ffo, s->ln->err, st);
-        });
-      } else if (gemv_q4k_two_fit(L.gate, L.up, true, T)) {
-        // decode: gate, up and swiglu in one GEMV launch
-        double bytes = 2.0 * L.gate.rows * L.gate.cols * weight_bytes_per_elem(GGML_Q4_K) +
-                       (double)T * d * (1.0 + 4.0 / 32) + (double)T * ff * 4.0;
-        P.timed(st, "gemv_q4_k_gate_up", bytes, 2.0 * L.gate.rows * L.gate.cols * T, [&] {
-          launch_gemv_pair_swiglu_q4k(L.gate, L.up, a, T, s->ln->ffo, s->ln->err, st);
         });
       } else {
         gemm(L.gate, a, s->ln->g, nullptr, EPI_STORE, nullptr);
@@ -975,6 +988,12 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
       gemm(L.down, session_act(s, s->ln->ffo), s->ln->x, nullptr, EPI_RESIDUAL, "gemv_down");
     } else if (fits({&L.down}, false, false)) {
       fused({&L.down}, false, {s->ln->x}, {nullptr}, {EPI_RESIDUAL}, s->ln->ffo, nullptr, "gemv_fused_down");
+    } else if (gemv_q4k_fit(L.down, nullptr, false, true, T)) {
+      // decode: the FFN product's quantisation inside the down launch
+      P.timed(st, "gemv_q4_k_down", q4k_gemv_bytes(L.down, T, true), (double)L.down.rows * L.down.cols * T, [&] {
+        launch_gemv_q4k(L.down, nullptr, false, Q4kIn{nullptr, s->ln->ffo, nullptr, 0.0f}, T, s->ln->x,
+                        nullptr, nullptr, nullptr, EPI_RESIDUAL, 0, s->ln->err, st);
+      });
     } else {
       a = prepare_input(s, s->ln->ffo, T, ff, {&L.down});
       gemm(L.down, a, s->ln->x, nullptr, EPI_RESIDUAL, nullptr);

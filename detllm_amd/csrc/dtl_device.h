@@ -142,16 +142,23 @@ bool gemv_fused_pair_quantizes(const DevMat& gate, const DevMat& up, bool norm, 
 bool launch_gemv_fused(const DevMat* const* mats, int nm, bool pair_swiglu, float* const* outs,
                        const float* const* biases, const int* epis, const FusedIn& in, int T,
                        int* err, hipStream_t s);
-// Q4_K decode GEMVs over two matrices with the same input: wq and wk
-// (concatenated rows, each its own output, bias and epilogue) and gate and
-// up finishing as silu(gate) * up into ffo.  false (nothing launched) when
-// the shapes or types do not qualify.
-bool gemv_q4k_two_fit(const DevMat& W0, const DevMat& W1, bool pair, int T);
-bool launch_gemv_cat_q4k(const DevMat& W0, const DevMat& W1, const DevAct& A, int T, float* out0,
-                         float* out1, const float* bias0, const float* bias1, int epi0, int epi1,
-                         int* err, hipStream_t s);
-bool launch_gemv_pair_swiglu_q4k(const DevMat& G, const DevMat& U, const DevAct& A, int T,
-                                 float* ffo, int* err, hipStream_t s);
+// Q4_K decode GEMVs (T <= kGemvMaxT) with the products and chains split:
+// one matrix (W1 null), two over concatenated rows with the same input (wq
+// and wk: each its own output, bias and epilogue), or gate and up (pair)
+// finishing as silu(gate) * up into out0.  The input is either the Q8A
+// values (in.af) or the raw f32 rows the kernel normalises (in.norm_w) and
+// quantises itself (in.x).  false (nothing launched) when the shapes or
+// types do not qualify.
+struct Q4kIn {
+  const float* af;
+  const float* x;
+  const float* norm_w;
+  float eps;
+};
+bool gemv_q4k_fit(const DevMat& W0, const DevMat* W1, bool pair, bool prologue, int T);
+bool launch_gemv_q4k(const DevMat& W0, const DevMat* W1, bool pair, const Q4kIn& in, int T,
+                     float* out0, float* out1, const float* bias0, const float* bias1, int epi0,
+                     int epi1, int* err, hipStream_t s);
 // Token-parallel GEMMs (dtl_gemm.hip) for chunks of positions.
 bool gemm_tok_supported(const DevMat& W);
 void launch_gemm_tok(const DevMat& W, const DevAct& A, int T, float* out, const float* bias,

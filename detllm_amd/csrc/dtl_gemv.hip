@@ -415,234 +415,6 @@ __global__ void __launch_bounds__(64) k_gemv_q4k(const float* __restrict__ w32, 
   if (!epilogue(sum, out, (size_t)t * rows + row, bias, row, epi)) flag(err, ERRBIT_NON_FINITE);
 }
 
-// Q4_K decode with the products and the chains on different lanes.  A
-// workgroup of four waves owns RB rows.  Every thread streams its share of
-// the weight rows through an NS-deep register ring (one SL-column stage per
-// slot, loads issued unconditionally), multiplies them by the activations
-// (all T positions, staged in LDS once) and stores the rounded products
-// row-major in LDS; after the stage's barrier, wave 0's lanes (row r,
-// position t) add their row of products in element order, twelve float4
-// ahead of the adds, while the other waves already form the next stage.
-// The chain, the one serial part, therefore runs one add per element with
-// its operands in LDS; the weights' HBM latency is covered by NS stages.
-template <int N4>
-__device__ __forceinline__ float chain_sum_lds_n(float a, const float* v) {
-  constexpr int kRing = N4 < 12 ? N4 : 12;
-  constexpr int kLoop = (N4 - kRing) / kRing;  // ring turns with a refill per slot
-  constexpr int kRem = N4 - kLoop * kRing;     // then kRem float4, kRing of them in the ring
-  const float4* v4 = reinterpret_cast<const float4*>(v);
-  float4 r[kRing];
-#pragma unroll
-  for (int q = 0; q < kRing; q++) r[q] = v4[q];
-  // a rolled loop: fully unrolled, the reads would be hoisted out of the ring
-#pragma unroll 1
-  for (int it = 0; it < kLoop; it++) {
-#pragma unroll
-    for (int q = 0; q < kRing; q++) {
-      a += r[q].x;
-      a += r[q].y;
-      a += r[q].z;
-      a += r[q].w;
-      r[q] = v4[(it + 1) * kRing + q];
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-#pragma unroll
-  for (int q = 0; q < kRem; q++) {
-    const int slot = q % kRing;
-    a += r[slot].x;
-    a += r[slot].y;
-    a += r[slot].z;
-    a += r[slot].w;
-    if (q + kRing < kRem) r[slot] = v4[kLoop * kRing + kRing + q];
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  return a;
-}
-
-// Matrices of one launch: one matrix (rows0), two over the same input with
-// their rows concatenated (wq and wk: rows0 + rows1, each its own output,
-// bias and epilogue), or gate and up (rows0 each) finishing as
-// silu(gate) * up (det-model lib.rs:2420-2434).
-enum { PC_SINGLE = 0, PC_CAT = 1, PC_PAIR = 2 };
-
-struct Q4kPcArgs {
-  const float* w0;
-  const float* w1;
-  int rows0, rows1, cols, T;
-  const float* af;
-  float* out0;
-  float* out1;
-  const float* bias0;
-  const float* bias1;
-  int epi0, epi1;
-  int* err;
-};
-
-constexpr int kPcThreads = 512;  // eight waves: wave 0 runs the chains
-constexpr int kPcMaxPer = 3;     // weight float4 per thread and stage
-
-template <int SL, int NS, int MODE>
-__global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB) {
-  constexpr int NM = MODE == PC_PAIR ? 2 : 1;
-  constexpr int LDP = SL + 4;             // product row stride (floats)
-  constexpr int C4 = SL / 4;              // float4 per row and stage
-  const int NR = NM * RB;                 // staged rows (gate rows, then up rows)
-  const int WPS = NR * C4;                // weight float4 per stage
-  extern __shared__ __align__(16) float smem[];
-  const int cols = p.cols, T = p.T;
-  const int rows_total = MODE == PC_CAT ? p.rows0 + p.rows1 : p.rows0;
-  float* as = smem;                       // [T][cols] activations
-  float* prod = smem + (size_t)T * cols;  // [2][NR * T][LDP] products
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int row0 = blockIdx.x * RB;
-  const int nst = cols / SL;
-  // weight float4 j of this thread: f = tid + 512 j, staged row f / C4,
-  // float4 f % C4 of the stage; rows past the end read the last row,
-  // slots past WPS read the workgroup's first row and store nothing
-  auto src_of = [&](int f) {
-    const bool ok = f < WPS;
-    const int j = ok ? f / C4 : 0;
-    const float* w;
-    int row;
-    if (MODE == PC_PAIR) {
-      w = j < RB ? p.w0 : p.w1;
-      row = row0 + j % RB;
-      row = row < p.rows0 ? row : p.rows0 - 1;
-    } else {
-      int g = row0 + j;
-      g = g < rows_total ? g : rows_total - 1;
-      const bool m = MODE == PC_CAT && g >= p.rows0;
-      w = m ? p.w1 : p.w0;
-      row = m ? g - p.rows0 : g;
-    }
-    return w + (size_t)row * cols + (ok ? f % C4 : 0) * 4;
-  };
-  const float* s0 = src_of(tid);
-  const float* s1 = src_of(tid + kPcThreads);
-  const float* s2 = src_of(tid + 2 * kPcThreads);
-  // the weights' first NS stages are in flight before the activations load
-  float4 ring0[NS], ring1[NS], ring2[NS];
-#pragma unroll
-  for (int u = 0; u < NS; u++) {
-    const size_t o = (size_t)(u < nst ? u : nst - 1) * SL;
-    ring0[u] = *reinterpret_cast<const float4*>(s0 + o);
-    ring1[u] = *reinterpret_cast<const float4*>(s1 + o);
-    ring2[u] = *reinterpret_cast<const float4*>(s2 + o);
-  }
-  for (int i = tid; i < T * cols / 4; i += kPcThreads)
-    reinterpret_cast<float4*>(as)[i] = reinterpret_cast<const float4*>(p.af)[i];
-  __syncthreads();
-  // chain lane = staged row j + NR * position t
-  const bool chain = wave == 0 && lane < NR * T;
-  float sum = 0.0f;
-  auto products = [&](float* pb, int e, int f, const float4& w) {
-    if (f >= WPS) return;
-    const int r = f / C4, c = (f % C4) * 4;
-    for (int t = 0; t < T; t++) {
-      const float4 a = *reinterpret_cast<const float4*>(as + (size_t)t * cols + e + c);
-      *reinterpret_cast<float4*>(pb + (r + NR * t) * LDP + c) =
-          make_float4(w.x * a.x, w.y * a.y, w.z * a.z, w.w * a.w);
-    }
-  };
-  for (int base = 0; base < nst; base += NS) {
-#pragma unroll
-    for (int u = 0; u < NS; u++) {
-      const int k = base + u;  // stages past the end form unused products
-      float* pb = prod + (size_t)(k & 1) * NR * T * LDP;
-      const int e = (k < nst ? k : nst - 1) * SL;
-      products(pb, e, tid, ring0[u]);
-      products(pb, e, tid + kPcThreads, ring1[u]);
-      products(pb, e, tid + 2 * kPcThreads, ring2[u]);
-      const size_t o = (size_t)(k + NS < nst ? k + NS : nst - 1) * SL;
-      ring0[u] = *reinterpret_cast<const float4*>(s0 + o);
-      ring1[u] = *reinterpret_cast<const float4*>(s1 + o);
-      ring2[u] = *reinterpret_cast<const float4*>(s2 + o);
-      __syncthreads();
-      if (chain && k < nst) sum = chain_sum_lds_n<C4>(sum, pb + lane * LDP);
-    }
-  }
-  if (wave != 0) return;
-  const int j = lane % NR, t = lane / NR;
-  if (MODE == PC_PAIR) {
-    const float u = __shfl(sum, lane + RB);  // the up chain of the same row and position
-    const int row = row0 + j;
-    if (!chain || j >= RB || row >= p.rows0) return;
-    const float v = silu_det(sum) * u;
-    p.out0[(size_t)t * p.rows0 + row] = v;
-    if (!(finite(sum) && finite(u) && finite(v))) flag(p.err, ERRBIT_NON_FINITE);
-    return;
-  }
-  const int g = row0 + j;
-  if (!chain || g >= rows_total) return;
-  const bool m = MODE == PC_CAT && g >= p.rows0;
-  const int row = m ? g - p.rows0 : g, R = m ? p.rows1 : p.rows0;
-  if (!epilogue(sum, m ? p.out1 : p.out0, (size_t)t * R + row, m ? p.bias1 : p.bias0, row,
-                m ? p.epi1 : p.epi0))
-    flag(p.err, ERRBIT_NON_FINITE);
-}
-
-size_t q4k_pc_smem(int T, int cols, int NR, int SL) {
-  return ((size_t)T * cols + (size_t)2 * NR * T * (SL + 4)) * sizeof(float);
-}
-
-// DETLLM_Q4K_GEMV_CHAIN=1 keeps the one-lane-per-row Q4_K decode kernel.
-bool q4k_pc_enabled() {
-  static const bool on = !getenv("DETLLM_Q4K_GEMV_CHAIN");
-  return on;
-}
-
-// Rows per workgroup and columns per stage.  A chain wave runs far slower
-// when it shares its SIMD with another one, so the rows are spread over at
-// most one workgroup per CU (at least eight rows each); the chain lanes
-// (staged rows x positions) must fit one wave and the stage's weights
-// kPcMaxPer float4 per thread.  256-column stages where those allow.
-bool q4k_pc_plan(int mode, int rows_total, int cols, int T, int* RB, int* SL, size_t* smem) {
-  if (!q4k_pc_enabled() || cols % 256 != 0 || T < 1) return false;
-  static const int cus = [] {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      return 256;
-    return n;
-  }();
-  const int NM = mode == PC_PAIR ? 2 : 1;
-  int rb = (rows_total + cus - 1) / cus;  // rows_total: of each matrix for the pair
-  rb = rb < 8 ? 8 : rb;
-  if (NM * rb * T > 64) rb = 64 / (NM * T);
-  if (rb < 1) return false;
-  const int NR = NM * rb;
-  int sl = 256;
-  if (NR * (sl / 4) > kPcMaxPer * kPcThreads || q4k_pc_smem(T, cols, NR, sl) > 64 * 1024) sl = 128;
-  if (NR * (sl / 4) > kPcMaxPer * kPcThreads) return false;
-  *RB = rb;
-  *SL = sl;
-  *smem = q4k_pc_smem(T, cols, NR, sl);
-  return *smem <= 150 * 1024;
-}
-
-template <int MODE>
-bool launch_q4k_pc(const Q4kPcArgs& a, hipStream_t s) {
-  const int rows_total = MODE == PC_CAT ? a.rows0 + a.rows1 : a.rows0;
-  int RB, SL;
-  size_t smem;
-  if (!q4k_pc_plan(MODE, rows_total, a.cols, a.T, &RB, &SL, &smem)) return false;
-  const dim3 grid((rows_total + RB - 1) / RB);
-#define DTL_Q4K_PC(sl, ns)                                                                       \
-  do {                                                                                           \
-    static const bool attr = hipFuncSetAttribute((const void*)k_gemv_q4k_pc<sl, ns, MODE>,         \
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize,      \
-                                                 150 * 1024) == hipSuccess;                       \
-    (void)attr;                                                                                  \
-    launch_kernel((k_gemv_q4k_pc<sl, ns, MODE>), grid, dim3(kPcThreads), smem, s, a, RB);         \
-  } while (0)
-  if (SL == 256) DTL_Q4K_PC(256, 4);
-  else DTL_Q4K_PC(128, 6);
-#undef DTL_Q4K_PC
-  return true;
-}
-
 // ---------------------------------------------------------------------------
 // Fused decode GEMV for Q8_0 / Q4_0 weights.  Every workgroup first forms
 // the Q8A activations of its position in LDS from the f32 input: after
@@ -756,6 +528,266 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
 }
 
 }  // namespace
+
+// Q4_K decode with the products and the chains on different lanes.  A
+// workgroup of four waves owns RB rows.  Every thread streams its share of
+// the weight rows through an NS-deep register ring (one SL-column stage per
+// slot, loads issued unconditionally), multiplies them by the activations
+// (all T positions, staged in LDS once) and stores the rounded products
+// row-major in LDS; after the stage's barrier, wave 0's lanes (row r,
+// position t) add their row of products in element order, twelve float4
+// ahead of the adds, while the other waves already form the next stage.
+// The chain, the one serial part, therefore runs one add per element with
+// its operands in LDS; the weights' HBM latency is covered by NS stages.
+template <int N4>
+__device__ __forceinline__ float chain_sum_lds_n(float a, const float* v) {
+  constexpr int kRing = N4 < 12 ? N4 : 12;
+  constexpr int kLoop = (N4 - kRing) / kRing;  // ring turns with a refill per slot
+  constexpr int kRem = N4 - kLoop * kRing;     // then kRem float4, kRing of them in the ring
+  const float4* v4 = reinterpret_cast<const float4*>(v);
+  float4 r[kRing];
+#pragma unroll
+  for (int q = 0; q < kRing; q++) r[q] = v4[q];
+  // a rolled loop: fully unrolled, the reads would be hoisted out of the ring
+#pragma unroll 1
+  for (int it = 0; it < kLoop; it++) {
+#pragma unroll
+    for (int q = 0; q < kRing; q++) {
+      a += r[q].x;
+      a += r[q].y;
+      a += r[q].z;
+      a += r[q].w;
+      r[q] = v4[(it + 1) * kRing + q];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < kRem; q++) {
+    const int slot = q % kRing;
+    a += r[slot].x;
+    a += r[slot].y;
+    a += r[slot].z;
+    a += r[slot].w;
+    if (q + kRing < kRem) r[slot] = v4[kLoop * kRing + kRing + q];
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  return a;
+}
+
+// Matrices of one launch: one matrix (rows0), two over the same input with
+// their rows concatenated (wq and wk: rows0 + rows1, each its own output,
+// bias and epilogue), or gate and up (rows0 each) finishing as
+// silu(gate) * up (det-model lib.rs:2420-2434).
+enum { PC_SINGLE = 0, PC_CAT = 1, PC_PAIR = 2 };
+
+struct Q4kPcArgs {
+  const float* w0;
+  const float* w1;
+  int rows0, rows1, cols, T;
+  const float* af;      // the Q8A values of the input, or null: formed from x
+  const float* x;       // raw input (with af null), normed first when norm_w is set
+  const float* norm_w;
+  float eps;
+  float* out0;
+  float* out1;
+  const float* bias0;
+  const float* bias1;
+  int epi0, epi1;
+  int* err;
+};
+
+constexpr int kPcThreads = 512;  // eight waves: wave 0 runs the chains
+constexpr int kPcMaxPer = 3;     // weight float4 per thread and stage
+
+template <int SL, int NS, int MODE>
+__global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB) {
+  constexpr int NM = MODE == PC_PAIR ? 2 : 1;
+  constexpr int LDP = SL + 4;             // product row stride (floats)
+  constexpr int C4 = SL / 4;              // float4 per row and stage
+  const int NR = NM * RB;                 // staged rows (gate rows, then up rows)
+  const int WPS = NR * C4;                // weight float4 per stage
+  extern __shared__ __align__(16) float smem[];
+  const int cols = p.cols, T = p.T;
+  const int rows_total = MODE == PC_CAT ? p.rows0 + p.rows1 : p.rows0;
+  float* as = smem;                       // [T][cols] activations
+  float* prod = smem + (size_t)T * cols;  // [2][NR * T][LDP] products
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int row0 = blockIdx.x * RB;
+  const int nst = cols / SL;
+  // weight float4 j of this thread: f = tid + 512 j, staged row f / C4,
+  // float4 f % C4 of the stage; rows past the end read the last row,
+  // slots past WPS read the workgroup's first row and store nothing
+  auto src_of = [&](int f) {
+    const bool ok = f < WPS;
+    const int j = ok ? f / C4 : 0;
+    const float* w;
+    int row;
+    if (MODE == PC_PAIR) {
+      w = j < RB ? p.w0 : p.w1;
+      row = row0 + j % RB;
+      row = row < p.rows0 ? row : p.rows0 - 1;
+    } else {
+      int g = row0 + j;
+      g = g < rows_total ? g : rows_total - 1;
+      const bool m = MODE == PC_CAT && g >= p.rows0;
+      w = m ? p.w1 : p.w0;
+      row = m ? g - p.rows0 : g;
+    }
+    return w + (size_t)row * cols + (ok ? f % C4 : 0) * 4;
+  };
+  const float* s0 = src_of(tid);
+  const float* s1 = src_of(tid + kPcThreads);
+  const float* s2 = src_of(tid + 2 * kPcThreads);
+  // the weights' first NS stages are in flight before the activations load
+  float4 ring0[NS], ring1[NS], ring2[NS];
+#pragma unroll
+  for (int u = 0; u < NS; u++) {
+    const size_t o = (size_t)(u < nst ? u : nst - 1) * SL;
+    ring0[u] = *reinterpret_cast<const float4*>(s0 + o);
+    ring1[u] = *reinterpret_cast<const float4*>(s1 + o);
+    ring2[u] = *reinterpret_cast<const float4*>(s2 + o);
+  }
+  if (p.af) {
+    for (int i = tid; i < T * cols / 4; i += kPcThreads)
+      reinterpret_cast<float4*>(as)[i] = reinterpret_cast<const float4*>(p.af)[i];
+  } else {
+    // The input's rmsnorm (with norm_w) and Q8A quantisation, as the
+    // separate kernels form them, into the f32 values d * q.
+    const int cs = (((cols + 7) / 8) + 3) & ~3;
+    float* xs = prod + (size_t)2 * NR * T * LDP;
+    float* ws = xs + cols;
+    float* sq = ws + cols;
+    float* misc = sq + 8 * cs;
+    float* da_s = misc + 16;
+    int8_t* qa_s = reinterpret_cast<int8_t*>(da_s + cols / 32);
+    const FusedIn in{p.x, p.norm_w, p.eps};
+    bool bad = false;
+    for (int t = 0; t < T; t++) {
+      bad |= q8a_prologue<kPcThreads / 64>(in, t, cols, p.norm_w != nullptr, xs, ws, sq, cs, qa_s,
+                                           da_s, misc);
+      for (int e = tid; e < cols; e += kPcThreads)
+        as[(size_t)t * cols + e] = da_s[e / 32] * (float)qa_s[e];
+      __syncthreads();
+    }
+    if (bad && tid == 0) flag(p.err, ERRBIT_NON_FINITE);
+  }
+  __syncthreads();
+  // chain lane = staged row j + NR * position t
+  const bool chain = wave == 0 && lane < NR * T;
+  float sum = 0.0f;
+  auto products = [&](float* pb, int e, int f, const float4& w) {
+    if (f >= WPS) return;
+    const int r = f / C4, c = (f % C4) * 4;
+    for (int t = 0; t < T; t++) {
+      const float4 a = *reinterpret_cast<const float4*>(as + (size_t)t * cols + e + c);
+      *reinterpret_cast<float4*>(pb + (r + NR * t) * LDP + c) =
+          make_float4(w.x * a.x, w.y * a.y, w.z * a.z, w.w * a.w);
+    }
+  };
+  for (int base = 0; base < nst; base += NS) {
+#pragma unroll
+    for (int u = 0; u < NS; u++) {
+      const int k = base + u;  // stages past the end form unused products
+      float* pb = prod + (size_t)(k & 1) * NR * T * LDP;
+      const int e = (k < nst ? k : nst - 1) * SL;
+      products(pb, e, tid, ring0[u]);
+      products(pb, e, tid + kPcThreads, ring1[u]);
+      products(pb, e, tid + 2 * kPcThreads, ring2[u]);
+      const size_t o = (size_t)(k + NS < nst ? k + NS : nst - 1) * SL;
+      ring0[u] = *reinterpret_cast<const float4*>(s0 + o);
+      ring1[u] = *reinterpret_cast<const float4*>(s1 + o);
+      ring2[u] = *reinterpret_cast<const float4*>(s2 + o);
+      __syncthreads();
+      if (chain && k < nst) sum = chain_sum_lds_n<C4>(sum, pb + lane * LDP);
+    }
+  }
+  if (wave != 0) return;
+  const int j = lane % NR, t = lane / NR;
+  if (MODE == PC_PAIR) {
+    const float u = __shfl(sum, lane + RB);  // the up chain of the same row and position
+    const int row = row0 + j;
+    if (!chain || j >= RB || row >= p.rows0) return;
+    const float v = silu_det(sum) * u;
+    p.out0[(size_t)t * p.rows0 + row] = v;
+    if (!(finite(sum) && finite(u) && finite(v))) flag(p.err, ERRBIT_NON_FINITE);
+    return;
+  }
+  const int g = row0 + j;
+  if (!chain || g >= rows_total) return;
+  const bool m = MODE == PC_CAT && g >= p.rows0;
+  const int row = m ? g - p.rows0 : g, R = m ? p.rows1 : p.rows0;
+  if (!epilogue(sum, m ? p.out1 : p.out0, (size_t)t * R + row, m ? p.bias1 : p.bias0, row,
+                m ? p.epi1 : p.epi0))
+    flag(p.err, ERRBIT_NON_FINITE);
+}
+
+// LDS bytes: activations, two product buffers and, when the kernel forms
+// the activations itself, the prologue's row, norm weights, chain-major
+// squares, scratch, scales and int8 values.
+size_t q4k_pc_smem(int T, int cols, int NR, int SL, bool prologue) {
+  size_t f = (size_t)T * cols + (size_t)2 * NR * T * (SL + 4);
+  if (prologue) f += 2 * (size_t)cols + 8 * (size_t)((((cols + 7) / 8) + 3) & ~3) + 16 + cols / 32 + cols / 4;
+  return f * sizeof(float);
+}
+
+// DETLLM_Q4K_GEMV_CHAIN=1 keeps the one-lane-per-row Q4_K decode kernel.
+bool q4k_pc_enabled() {
+  static const bool on = !getenv("DETLLM_Q4K_GEMV_CHAIN");
+  return on;
+}
+
+// Rows per workgroup and columns per stage.  A chain wave runs far slower
+// when it shares its SIMD with another one, so the rows are spread over at
+// most one workgroup per CU (at least eight rows each); the chain lanes
+// (staged rows x positions) must fit one wave and the stage's weights
+// kPcMaxPer float4 per thread.  256-column stages where those allow.
+bool q4k_pc_plan(int mode, int rows_total, int cols, int T, bool prologue, int* RB, int* SL,
+                 size_t* smem) {
+  if (!q4k_pc_enabled() || cols % 256 != 0 || T < 1) return false;
+  static const int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      return 256;
+    return n;
+  }();
+  const int NM = mode == PC_PAIR ? 2 : 1;
+  int rb = (rows_total + cus - 1) / cus;  // rows_total: of each matrix for the pair
+  rb = rb < 8 ? 8 : rb;
+  if (NM * rb * T > 64) rb = 64 / (NM * T);
+  if (rb < 1) return false;
+  const int NR = NM * rb;
+  int sl = 256;
+  if (NR * (sl / 4) > kPcMaxPer * kPcThreads || q4k_pc_smem(T, cols, NR, sl, prologue) > 80 * 1024)
+    sl = 128;
+  if (NR * (sl / 4) > kPcMaxPer * kPcThreads) return false;
+  *RB = rb;
+  *SL = sl;
+  *smem = q4k_pc_smem(T, cols, NR, sl, prologue);
+  return *smem <= 150 * 1024;
+}
+
+template <int MODE>
+bool launch_q4k_pc(const Q4kPcArgs& a, hipStream_t s) {
+  const int rows_total = MODE == PC_CAT ? a.rows0 + a.rows1 : a.rows0;
+  int RB, SL;
+  size_t smem;
+  if (!q4k_pc_plan(MODE, rows_total, a.cols, a.T, a.af == nullptr, &RB, &SL, &smem)) return false;
+  const dim3 grid((rows_total + RB - 1) / RB);
+#define DTL_Q4K_PC(sl, ns)                                                                       \
+  do {                                                                                           \
+    static const bool attr = hipFuncSetAttribute((const void*)k_gemv_q4k_pc<sl, ns, MODE>,         \
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,      \
+                                                 150 * 1024) == hipSuccess;                       \
+    (void)attr;                                                                                  \
+    launch_kernel((k_gemv_q4k_pc<sl, ns, MODE>), grid, dim3(kPcThreads), smem, s, a, RB);         \
+  } while (0)
+  if (SL == 256) DTL_Q4K_PC(256, 4);
+  else DTL_Q4K_PC(128, 6);
+#undef DTL_Q4K_PC
+  return true;
+}
 
 // LDS bytes of k_gemv_q8f: block terms, the Q8A activations and, with a
 // norm, its scratch (the row, the weights, the chain-major squares).
@@ -998,7 +1030,8 @@ bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const floa
     return true;
   }
   if (W.type == kGgmlQ4K && W.w32) {
-    Q4kPcArgs a{W.w32, nullptr, W.rows, 0, W.cols, T, A.af, out, nullptr, bias, nullptr, epi, 0, err};
+    Q4kPcArgs a{W.w32, nullptr, W.rows, 0, W.cols, T, A.af, nullptr, nullptr, 0.0f,
+                out, nullptr, bias, nullptr, epi, 0, err};
     if (launch_q4k_pc<PC_SINGLE>(a, s)) return true;
   }
   if (W.type == kGgmlQ4K && W.w32 && W.cols % 256 == 0) {
@@ -1103,34 +1136,26 @@ bool launch_gemv_fused(const DevMat* const* mats, int nm, bool pair_swiglu, floa
   return true;
 }
 
-bool gemv_q4k_two_fit(const DevMat& W0, const DevMat& W1, bool pair, int T) {
+bool gemv_q4k_fit(const DevMat& W0, const DevMat* W1, bool pair, bool prologue, int T) {
   int RB, SL;
   size_t smem;
-  return T <= kGemvMaxT && W0.type == kGgmlQ4K && W1.type == kGgmlQ4K && W0.w32 && W1.w32 &&
-         W0.cols == W1.cols && (!pair || W0.rows == W1.rows) &&
-         q4k_pc_plan(pair ? PC_PAIR : PC_CAT, pair ? W0.rows : W0.rows + W1.rows, W0.cols, T, &RB,
-                     &SL, &smem);
+  if (T > kGemvMaxT || W0.type != kGgmlQ4K || !W0.w32) return false;
+  if (W1 && (W1->type != kGgmlQ4K || !W1->w32 || W1->cols != W0.cols || (pair && W1->rows != W0.rows)))
+    return false;
+  const int mode = pair ? PC_PAIR : (W1 ? PC_CAT : PC_SINGLE);
+  const int rows = pair || !W1 ? W0.rows : W0.rows + W1->rows;
+  return q4k_pc_plan(mode, rows, W0.cols, T, prologue, &RB, &SL, &smem);
 }
 
-bool launch_gemv_cat_q4k(const DevMat& W0, const DevMat& W1, const DevAct& A, int T, float* out0,
-                         float* out1, const float* bias0, const float* bias1, int epi0, int epi1,
-                         int* err, hipStream_t s) {
-  if (T > kGemvMaxT || W0.type != kGgmlQ4K || W1.type != kGgmlQ4K || !W0.w32 || !W1.w32 ||
-      W0.cols != W1.cols)
-    return false;
-  Q4kPcArgs a{W0.w32, W1.w32, W0.rows, W1.rows, W0.cols, T, A.af, out0, out1, bias0, bias1,
-              epi0, epi1, err};
-  return launch_q4k_pc<PC_CAT>(a, s);
-}
-
-bool launch_gemv_pair_swiglu_q4k(const DevMat& G, const DevMat& U, const DevAct& A, int T,
-                                 float* ffo, int* err, hipStream_t s) {
-  if (T > kGemvMaxT || G.type != kGgmlQ4K || U.type != kGgmlQ4K || !G.w32 || !U.w32 ||
-      G.rows != U.rows || G.cols != U.cols)
-    return false;
-  Q4kPcArgs a{G.w32, U.w32, G.rows, 0, G.cols, T, A.af, ffo, nullptr, nullptr, nullptr,
-              EPI_STORE, EPI_STORE, err};
-  return launch_q4k_pc<PC_PAIR>(a, s);
+bool launch_gemv_q4k(const DevMat& W0, const DevMat* W1, bool pair, const Q4kIn& in, int T,
+                     float* out0, float* out1, const float* bias0, const float* bias1, int epi0,
+                     int epi1, int* err, hipStream_t s) {
+  if (!gemv_q4k_fit(W0, W1, pair, in.af == nullptr, T)) return false;
+  Q4kPcArgs a{W0.w32, W1 ? W1->w32 : nullptr, W0.rows, W1 && !pair ? W1->rows : 0, W0.cols, T,
+              in.af, in.x, in.norm_w, in.eps, out0, out1, bias0, bias1, epi0, epi1, err};
+  if (pair) return launch_q4k_pc<PC_PAIR>(a, s);
+  if (W1) return launch_q4k_pc<PC_CAT>(a, s);
+  return launch_q4k_pc<PC_SINGLE>(a, s);
 }
 
 }  // namespace dtl
