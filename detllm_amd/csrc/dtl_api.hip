@@ -870,6 +870,16 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
       fused({&L.wq}, false, {s->ln->q}, {L.bq}, {e_q}, s->ln->x, L.attn_norm, "gemv_fused_qkv");
       fused({&L.wk}, false, {s->ln->k}, {L.bk}, {e_k}, s->ln->x, L.attn_norm, "gemv_fused_qkv");
       fused({&L.wv}, false, {s->ln->v}, {L.bv}, {e_v}, s->ln->x, L.attn_norm, "gemv_fused_qkv");
+    } else if (L.wv.type == GGML_Q6_K && gemv_q4k_fit(L.wq, &L.wk, false, true, T)) {
+      // decode: the attention rmsnorm and its quantisation inside the
+      // wq+wk launch, whose first workgroup also writes the Q8_K form wv reads
+      double bytes = (double)(L.wq.rows + L.wk.rows) * L.wq.cols * weight_bytes_per_elem(GGML_Q4_K) +
+                     (double)T * d * 4.0 + (double)d * 4.0 + (double)T * (L.wq.rows + L.wk.rows) * 4.0;
+      P.timed(st, "gemv_q4_k_qk", bytes, (double)(L.wq.rows + L.wk.rows) * L.wq.cols * T, [&] {
+        launch_gemv_q4k(L.wq, &L.wk, false, Q4kIn{nullptr, s->ln->x, L.attn_norm, c.eps, s->ln->qk, s->ln->dk},
+                        T, s->ln->q, s->ln->k, L.bq, L.bk, e_q, e_k, s->ln->err, st);
+      });
+      gemm(L.wv, session_act(s, s->ln->h), s->ln->v, L.bv, e_v, nullptr);
     } else {
       a = rms(L.attn_norm, {&L.wq, &L.wk, &L.wv});
       if (L.wq.type == GGML_Q4_K && L.wk.type == GGML_Q4_K && L.wq.w32 && L.wk.w32 && T >= 16 &&

@@ -154,6 +154,8 @@ struct Q4kIn {
   const float* x;
   const float* norm_w;
   float eps;
+  int8_t* side_qk = nullptr;  // with x: also the input's Q8_K form (for a Q6_K consumer)
+  float* side_dk = nullptr;
 };
 bool gemv_q4k_fit(const DevMat& W0, const DevMat* W1, bool pair, bool prologue, int T);
 bool launch_gemv_q4k(const DevMat& W0, const DevMat* W1, bool pair, const Q4kIn& in, int T,

@@ -436,13 +436,18 @@ template <int NW>
 constexpr int pro_batch() { return NW >= 16 ? 1 : 4; }
 
 template <int NW>  // waves per workgroup
+// k_qk / k_dk (optional): also the Q8_K form of the (normed) row, written
+// to memory for position t.
 __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols, bool norm,
                                              float* xs, float* ws, float* sq, int cs,
-                                             int8_t* qa_s, float* da_s, float* misc) {
+                                             int8_t* qa_s, float* da_s, float* misc,
+                                             int8_t* k_qk = nullptr, float* k_dk = nullptr) {
   constexpr int kProBatch = pro_batch<NW>();
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const float* x = in.x + (size_t)t * cols;
-  const QuantOut q{qa_s, da_s, nullptr, nullptr, nullptr};
+  const bool want_k = k_qk != nullptr;
+  const QuantOut q{qa_s, da_s, nullptr, want_k ? k_qk + (size_t)t * cols : nullptr,
+                   want_k ? k_dk + (size_t)t * (cols / 256) : nullptr};
   bool bad = false;
   if (norm) {
     constexpr int kStep = 4 * 64 * NW;  // elements per float4 pass of the workgroup
@@ -500,7 +505,7 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
 #pragma unroll
         for (int c = 0; c < 4; c++) bad |= !finite(v[c]);
       }
-      quantize_span(v, inb, (size_t)span * 256, true, false, q);
+      quantize_span(v, inb, (size_t)span * 256, true, want_k, q);
     }
   } else {
     for (int s0 = wave; s0 * 256 < cols; s0 += NW * kProBatch) {
@@ -518,7 +523,7 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
           const bool inb = e < cols;
           float v[4] = {f[k].x, f[k].y, f[k].z, f[k].w};
           if (inb) bad |= any_nonfinite(v[0], v[1], v[2], v[3]);
-          quantize_span(v, inb, (size_t)span * 256, true, false, q);
+          quantize_span(v, inb, (size_t)span * 256, true, want_k, q);
         }
       }
     }
@@ -588,6 +593,8 @@ struct Q4kPcArgs {
   const float* x;       // raw input (with af null), normed first when norm_w is set
   const float* norm_w;
   float eps;
+  int8_t* side_qk;      // with x: the first workgroup also writes the input's Q8_K form
+  float* side_dk;
   float* out0;
   float* out1;
   const float* bias0;
@@ -597,7 +604,8 @@ struct Q4kPcArgs {
 };
 
 constexpr int kPcThreads = 512;  // eight waves: wave 0 runs the chains
-constexpr int kPcMaxPer = 3;     // weight float4 per thread and stage
+constexpr int kPcProducers = kPcThreads - 64;  // waves 1-7 form the products
+constexpr int kPcMaxPer = 4;     // weight float4 per producer thread and stage
 
 template <int SL, int NS, int MODE>
 __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB) {
@@ -615,9 +623,10 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int row0 = blockIdx.x * RB;
   const int nst = cols / SL;
-  // weight float4 j of this thread: f = tid + 512 j, staged row f / C4,
-  // float4 f % C4 of the stage; rows past the end read the last row,
-  // slots past WPS read the workgroup's first row and store nothing
+  // weight float4 j of producer thread x = tid - 64: f = x + 448 j, staged
+  // row f / C4, float4 f % C4 of the stage; rows past the end read the last
+  // row, slots past WPS read the workgroup's first row and store nothing.
+  // Wave 0 loads wave 1's slots (unused: it only runs the chains).
   auto src_of = [&](int f) {
     const bool ok = f < WPS;
     const int j = ok ? f / C4 : 0;
@@ -636,17 +645,20 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
     }
     return w + (size_t)row * cols + (ok ? f % C4 : 0) * 4;
   };
-  const float* s0 = src_of(tid);
-  const float* s1 = src_of(tid + kPcThreads);
-  const float* s2 = src_of(tid + 2 * kPcThreads);
+  const int ptid = wave == 0 ? tid : tid - 64;
+  const float* s0 = src_of(ptid);
+  const float* s1 = src_of(ptid + kPcProducers);
+  const float* s2 = src_of(ptid + 2 * kPcProducers);
+  const float* s3 = src_of(ptid + 3 * kPcProducers);
   // the weights' first NS stages are in flight before the activations load
-  float4 ring0[NS], ring1[NS], ring2[NS];
+  float4 ring0[NS], ring1[NS], ring2[NS], ring3[NS];
 #pragma unroll
   for (int u = 0; u < NS; u++) {
     const size_t o = (size_t)(u < nst ? u : nst - 1) * SL;
     ring0[u] = *reinterpret_cast<const float4*>(s0 + o);
     ring1[u] = *reinterpret_cast<const float4*>(s1 + o);
     ring2[u] = *reinterpret_cast<const float4*>(s2 + o);
+    ring3[u] = *reinterpret_cast<const float4*>(s3 + o);
   }
   if (p.af) {
     for (int i = tid; i < T * cols / 4; i += kPcThreads)
@@ -664,8 +676,10 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
     const FusedIn in{p.x, p.norm_w, p.eps};
     bool bad = false;
     for (int t = 0; t < T; t++) {
+      const bool side = blockIdx.x == 0 && p.side_qk;
       bad |= q8a_prologue<kPcThreads / 64>(in, t, cols, p.norm_w != nullptr, xs, ws, sq, cs, qa_s,
-                                           da_s, misc);
+                                           da_s, misc, side ? p.side_qk : nullptr,
+                                           side ? p.side_dk : nullptr);
       for (int e = tid; e < cols; e += kPcThreads)
         as[(size_t)t * cols + e] = da_s[e / 32] * (float)qa_s[e];
       __syncthreads();
@@ -691,13 +705,17 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
       const int k = base + u;  // stages past the end form unused products
       float* pb = prod + (size_t)(k & 1) * NR * T * LDP;
       const int e = (k < nst ? k : nst - 1) * SL;
-      products(pb, e, tid, ring0[u]);
-      products(pb, e, tid + kPcThreads, ring1[u]);
-      products(pb, e, tid + 2 * kPcThreads, ring2[u]);
+      if (wave != 0) {
+        products(pb, e, ptid, ring0[u]);
+        products(pb, e, ptid + kPcProducers, ring1[u]);
+        products(pb, e, ptid + 2 * kPcProducers, ring2[u]);
+        products(pb, e, ptid + 3 * kPcProducers, ring3[u]);
+      }
       const size_t o = (size_t)(k + NS < nst ? k + NS : nst - 1) * SL;
       ring0[u] = *reinterpret_cast<const float4*>(s0 + o);
       ring1[u] = *reinterpret_cast<const float4*>(s1 + o);
       ring2[u] = *reinterpret_cast<const float4*>(s2 + o);
+      ring3[u] = *reinterpret_cast<const float4*>(s3 + o);
       __syncthreads();
       if (chain && k < nst) sum = chain_sum_lds_n<C4>(sum, pb + lane * LDP);
     }
@@ -758,10 +776,13 @@ bool q4k_pc_plan(int mode, int rows_total, int cols, int T, bool prologue, int* 
   if (NM * rb * T > 64) rb = 64 / (NM * T);
   if (rb < 1) return false;
   const int NR = NM * rb;
-  int sl = 256;
-  if (NR * (sl / 4) > kPcMaxPer * kPcThreads || q4k_pc_smem(T, cols, NR, sl, prologue) > 80 * 1024)
-    sl = 128;
-  if (NR * (sl / 4) > kPcMaxPer * kPcThreads) return false;
+  // the longest stage (fewest barriers and ring refills) whose weights and
+  // products fit
+  int sl = 512;
+  while (sl > 128 && (NR * (sl / 4) > kPcMaxPer * kPcProducers ||
+                      q4k_pc_smem(T, cols, NR, sl, prologue) > 150 * 1024 || cols % sl != 0))
+    sl /= 2;
+  if (NR * (sl / 4) > kPcMaxPer * kPcProducers || cols % sl != 0) return false;
   *RB = rb;
   *SL = sl;
   *smem = q4k_pc_smem(T, cols, NR, sl, prologue);
@@ -783,7 +804,8 @@ bool launch_q4k_pc(const Q4kPcArgs& a, hipStream_t s) {
     (void)attr;                                                                                  \
     launch_kernel((k_gemv_q4k_pc<sl, ns, MODE>), grid, dim3(kPcThreads), smem, s, a, RB);         \
   } while (0)
-  if (SL == 256) DTL_Q4K_PC(256, 4);
+  if (SL == 512) DTL_Q4K_PC(512, 3);
+  else if (SL == 256) DTL_Q4K_PC(256, 4);
   else DTL_Q4K_PC(128, 6);
 #undef DTL_Q4K_PC
   return true;
@@ -1030,7 +1052,7 @@ bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const floa
     return true;
   }
   if (W.type == kGgmlQ4K && W.w32) {
-    Q4kPcArgs a{W.w32, nullptr, W.rows, 0, W.cols, T, A.af, nullptr, nullptr, 0.0f,
+    Q4kPcArgs a{W.w32, nullptr, W.rows, 0, W.cols, T, A.af, nullptr, nullptr, 0.0f, nullptr, nullptr,
                 out, nullptr, bias, nullptr, epi, 0, err};
     if (launch_q4k_pc<PC_SINGLE>(a, s)) return true;
   }
@@ -1151,8 +1173,10 @@ bool launch_gemv_q4k(const DevMat& W0, const DevMat* W1, bool pair, const Q4kIn&
                      float* out0, float* out1, const float* bias0, const float* bias1, int epi0,
                      int epi1, int* err, hipStream_t s) {
   if (!gemv_q4k_fit(W0, W1, pair, in.af == nullptr, T)) return false;
+  if (in.side_qk && (in.af || W0.cols % 256 != 0)) return false;
   Q4kPcArgs a{W0.w32, W1 ? W1->w32 : nullptr, W0.rows, W1 && !pair ? W1->rows : 0, W0.cols, T,
-              in.af, in.x, in.norm_w, in.eps, out0, out1, bias0, bias1, epi0, epi1, err};
+              in.af, in.x, in.norm_w, in.eps, in.side_qk, in.side_dk, out0, out1, bias0, bias1,
+              epi0, epi1, err};
   if (pair) return launch_q4k_pc<PC_PAIR>(a, s);
   if (W1) return launch_q4k_pc<PC_CAT>(a, s);
   return launch_q4k_pc<PC_SINGLE>(a, s);
