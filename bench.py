@@ -359,6 +359,11 @@ def main() -> int:
     parity &= bool(np.array_equal(lg.view(np.uint32), ref_logits.view(np.uint32)))
     log(f"[bench] parity vs oracle on {check_n} positions: {parity}; deterministic: {deterministic}")
 
+    # single-position decode of the same model (the per-token forward)
+    decode_main = None
+    if args.decode_positions > 0:
+        decode_main = decode_leg(model, toks, args.decode_positions, w.name)
+        log(f"[bench] {w.name} decode {decode_main['tokens_per_s']} tok/s")
     decode = None
     codec = None
     threads = args.cpu_threads or min(16, os.cpu_count() or 1)
@@ -419,6 +424,7 @@ def main() -> int:
         "parity_vs_oracle": parity,
         "deterministic": deterministic,
         "kernels": kernels,
+        "decode_main_workload": decode_main,
         "decode": decode,
         "codec": codec,
         "configs": per_config,
