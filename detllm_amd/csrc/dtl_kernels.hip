@@ -862,6 +862,226 @@ __global__ void __launch_bounds__(NT) k_attention_hd64(const float* q, const flo
   if (bad) flag(err, ERRBIT_NON_FINITE);
 }
 
+// Head dimension 64 and at most eight heads per KV group: the arithmetic of
+// k_attention_hd64 with the lanes split over keys and heads.  Eight waves
+// per (KV group, position).
+//   scores  wave w takes keys 8w..8w+7 of each 64-key tile, lane = (key
+//           lane % 8, head lane / 8); a lane holds its head's query row in
+//           registers and reads its key's row (row-major in LDS) as float4.
+//   softmax wave h < G over head h's scores, as in k_attention_hd64.
+//   P.V     lane = (head lane / 8, dimension 8w + lane % 8); the V tile is
+//           stored transposed, so a lane reads four keys' values of its
+//           dimension and its head's four probabilities as two float4.
+// Per four elements a wave reads 8 key rows (scores) or 8 value rows and 8
+// probability rows (P.V) from LDS, each shared by eight lanes, where the
+// wave-per-head kernel reads 64 distinct addresses; its LDS reads then no
+// longer keep pace with the VALU work.
+constexpr int kS64Stride = 68;  // K rows and V^T rows (floats): 8 rows x float4 on 32 banks
+constexpr int kS64Buf = 64 * kS64Stride;
+
+__host__ __device__ constexpr int attn_split_lane_stride(int len_max) {
+  return ((len_max + 63) & ~63) + 4;  // 8 probability rows x float4 on 32 banks
+}
+
+template <int D>
+__global__ void __launch_bounds__(512) k_attention_hd64s(const float* q, const float* kc,
+                                                       const float* vc, int layer, int pos0,
+                                                       int H, int KV, int n_ctx, int scs,
+                                                       float scale, float* out, QuantOut oq,
+                                                       int* err) {
+  extern __shared__ __align__(16) float smem[];
+  constexpr int hd = 64, NT = 512, PER = 2;  // a 64 x 64 tile is 1024 float4
+  const int G = H / KV;
+  const int g = blockIdx.x, t = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int pos = pos0 + t, len = pos + 1;
+  const float* keys = kc + ((size_t)layer * KV + g) * n_ctx * hd;
+  const float* vals = vc + ((size_t)layer * KV + g) * n_ctx * hd;
+  if (len == 1) {  // a single score copies V exactly (lib.rs:2319-2321)
+    if (wave < G) {
+      const int h = g * G + wave;
+      const float v0 = vals[lane];
+      out[(size_t)t * H * hd + (size_t)h * hd + lane] = v0;
+      if (oq.qa) quantize_q8a_lanes(v0, (size_t)t * H * hd + (size_t)h * hd, oq);
+    }
+    return;
+  }
+  float* sc = smem;                         // [G][scs] scores -> probabilities
+  float* tiles = sc + (size_t)G * scs;      // [2][kS64Buf]
+  bool bad = false;
+  const int kk = lane & 7, hh = lane >> 3;  // scores: key and head of the lane
+  const int hq = hh < G ? hh : 0;
+  float qr[64];
+  {
+    const float4* qg = reinterpret_cast<const float4*>(q + (size_t)t * H * hd + (size_t)(g * G + hq) * hd);
+#pragma unroll
+    for (int i4 = 0; i4 < 16; i4++) {
+      const float4 v = qg[i4];
+      qr[4 * i4 + 0] = v.x;
+      qr[4 * i4 + 1] = v.y;
+      qr[4 * i4 + 2] = v.z;
+      qr[4 * i4 + 3] = v.w;
+    }
+  }
+  const int ntiles = (len + 63) / 64;
+  // Tile loads: float4 x = tid + c * 512 covers row x / 16, columns 4 (x % 16);
+  // rows past len read row 0 and are not stored.
+  float4 ring[D][PER];
+  auto issue = [&](float4 (&dst)[PER], const float* base, int j0) {
+#pragma unroll
+    for (int c = 0; c < PER; c++) {
+      const int x = tid + c * NT;
+      const int j = x >> 4;
+      dst[c] = *reinterpret_cast<const float4*>(base + (size_t)(j0 + j < len ? j0 + j : 0) * hd + (x & 15) * 4);
+    }
+  };
+  auto commit_k = [&](const float4 (&src)[PER], float* buf, int j0) {
+#pragma unroll
+    for (int c = 0; c < PER; c++) {
+      const int x = tid + c * NT;
+      if (j0 + (x >> 4) < len)
+        *reinterpret_cast<float4*>(buf + (x >> 4) * kS64Stride + (x & 15) * 4) = src[c];
+    }
+  };
+  auto commit_v = [&](const float4 (&src)[PER], float* buf, int j0) {
+#pragma unroll
+    for (int c = 0; c < PER; c++) {
+      const int x = tid + c * NT;
+      const int j = x >> 4, i = (x & 15) * 4;
+      if (j0 + j < len) {
+        buf[(i + 0) * kS64Stride + j] = src[c].x;
+        buf[(i + 1) * kS64Stride + j] = src[c].y;
+        buf[(i + 2) * kS64Stride + j] = src[c].z;
+        buf[(i + 3) * kS64Stride + j] = src[c].w;
+      }
+    }
+  };
+  // scores: dot_f32_ref(q, k_j) * scale (8-lane order).  Tile k sits in ring slot k % D.
+#pragma unroll
+  for (int u = 0; u < D; u++) issue(ring[u], keys, u * 64);
+  commit_k(ring[0], tiles, 0);
+  issue(ring[0], keys, D * 64);
+  __syncthreads();
+  for (int k0 = 0; k0 < ntiles; k0 += D) {
+#pragma unroll
+    for (int u = 0; u < D; u++) {
+      const int k = k0 + u;
+      if (k < ntiles) {
+        const int j0 = k * 64;
+        const int j = j0 + 8 * wave + kk;
+        if (j < len && hh < G) {
+          const float* kr = tiles + (k & 1) * kS64Buf + (8 * wave + kk) * kS64Stride;
+          float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+          for (int i4 = 0; i4 < 16; i4++) {
+            const float4 kv = *reinterpret_cast<const float4*>(kr + 4 * i4);
+            const int i = 4 * i4;
+            acc[(i + 0) & 7] += qr[i + 0] * kv.x;
+            acc[(i + 1) & 7] += qr[i + 1] * kv.y;
+            acc[(i + 2) & 7] += qr[i + 2] * kv.z;
+            acc[(i + 3) & 7] += qr[i + 3] * kv.w;
+          }
+          const float sv = finish_8lane(acc) * scale;
+          if (!finite(sv)) bad = true;
+          sc[(size_t)hh * scs + j] = sv;
+        }
+        if (k + 1 < ntiles) commit_k(ring[(u + 1) % D], tiles + ((k + 1) & 1) * kS64Buf, j0 + 64);
+      }
+      issue(ring[(u + 1) % D], keys, (k0 + u + 1 + D) * 64);
+      __syncthreads();
+    }
+  }
+  // The first V tiles' loads overlap the softmax.
+#pragma unroll
+  for (int u = 0; u < D; u++) issue(ring[u], vals, u * 64);
+  // softmax_in_place (lib.rs:2361-2388), wave h for head h
+  if (wave < G) {
+    float* my = sc + (size_t)wave * scs;
+    float mx = -__builtin_huge_valf();
+    for (int j = lane; j < len; j += 64) mx = fmaxf(mx, my[j]);
+    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+    for (int j = lane; j < len; j += 64) my[j] = exp_clamped(my[j] - mx);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float zacc = 0.0f;
+    if (lane < 8) {
+      int j = lane;
+      for (; j + 8 * 15 < len; j += 8 * 16) {
+        float e[16];
+#pragma unroll
+        for (int c = 0; c < 16; c++) e[c] = my[j + 8 * c];
+#pragma unroll
+        for (int c = 0; c < 16; c++) zacc += e[c];
+      }
+      for (; j < len; j += 8) zacc += my[j];
+    }
+    float part[8];
+#pragma unroll
+    for (int c = 0; c < 8; c++) part[c] = __shfl(zacc, c);
+    const float z = finish_8lane(part);
+    if (!finite(z) || z == 0.0f) bad = true;
+    for (int j = lane; j < len; j += 64) {
+      const float p = my[j] / z;
+      if (!finite(p)) bad = true;
+      my[j] = p;
+    }
+  }
+  commit_v(ring[0], tiles, 0);
+  issue(ring[0], vals, D * 64);
+  __syncthreads();
+  // P.V: out[d] = 0.0; out[d] += p_j * v_j[d] for j ascending
+  const int ph = lane >> 3, pd = 8 * wave + (lane & 7);
+  const float* prow = sc + (size_t)(ph < G ? ph : 0) * scs;
+  float a = 0.0f;
+  for (int k0 = 0; k0 < ntiles; k0 += D) {
+#pragma unroll
+    for (int u = 0; u < D; u++) {
+      const int k = k0 + u;
+      if (k < ntiles) {
+        const int j0 = k * 64;
+        const int n = len - j0 < 64 ? len - j0 : 64;
+        const float* vr = tiles + (k & 1) * kS64Buf + pd * kS64Stride;
+        const float* pr = prow + j0;
+        if (n == 64) {
+#pragma unroll
+          for (int jb = 0; jb < 64; jb += 4) {
+            const float4 v4 = *reinterpret_cast<const float4*>(vr + jb);
+            const float4 p4 = *reinterpret_cast<const float4*>(pr + jb);
+            a += p4.x * v4.x;
+            a += p4.y * v4.y;
+            a += p4.z * v4.z;
+            a += p4.w * v4.w;
+          }
+        } else {
+          for (int j = 0; j < n; j++) a += pr[j] * vr[j];
+        }
+        if (k + 1 < ntiles) commit_v(ring[(u + 1) % D], tiles + ((k + 1) & 1) * kS64Buf, j0 + 64);
+      }
+      issue(ring[(u + 1) % D], vals, (k0 + u + 1 + D) * 64);
+      __syncthreads();
+    }
+  }
+  // out through LDS so that each head's 64 values sit in one wave (its Q8A
+  // form is two 32-element blocks)
+  float* ob = tiles;  // [8][64], free after the last tile's barrier
+  if (ph < G) ob[ph * 64 + pd] = a;
+  __syncthreads();
+  if (wave < G) {
+    const float v = ob[wave * 64 + lane];
+    if (!finite(v)) bad = true;
+    const size_t base = (size_t)t * H * hd + (size_t)(g * G + wave) * hd;
+    out[base + lane] = v;
+    if (oq.qa) quantize_q8a_lanes(v, base, oq);
+  }
+  if (bad) flag(err, ERRBIT_NON_FINITE);
+}
+
+size_t attention_hd64s_smem(int G, int scs) {
+  return ((size_t)G * scs + 2 * kS64Buf) * sizeof(float);
+}
+
 // Decode shape (a few positions): one workgroup of 1024 threads per (head,
 // position), with the RoPE and cache store of the chunk folded in.  The
 // workgroup applies RoPE (lib.rs:2011-2051) to its query head and to the
@@ -1402,10 +1622,30 @@ bool attention_quantizes_q8a(int hd, int H, int KV, int T, int pos0, int n_ctx) 
          attention_hd64_smem(G, ((pos0 + T) + 3) & ~3) <= 150 * 1024;
 }
 
+// DETLLM_ATTN_WAVE_PER_HEAD=1 keeps k_attention_hd64 for groups of <= 8 heads.
+static bool attn_split_lanes() {
+  static const bool on = !getenv("DETLLM_ATTN_WAVE_PER_HEAD");
+  return on;
+}
+
 void launch_attention(const float* q, const float* kc, const float* vc, int layer, int T, int pos0,
                       int H, int KV, int hd, int n_ctx, float scale, float* scores, float* out,
                       int* err, hipStream_t s, int8_t* qa, float* da, float* af) {
   int G = H / KV;
+  if (hd == 64 && G >= 1 && G <= 8 && attn_split_lanes()) {
+    const int scs = attn_split_lane_stride(pos0 + T);
+    const size_t smem = attention_hd64s_smem(G, scs);
+    if (smem <= 150 * 1024) {
+      static const bool attr = hipFuncSetAttribute((const void*)k_attention_hd64s<8>,
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   150 * 1024) == hipSuccess;
+      (void)attr;
+      const QuantOut oq{qa, da, af, nullptr, nullptr};
+      launch_kernel(k_attention_hd64s<8>, dim3(KV, T), dim3(512), smem, s, q, kc, vc, layer, pos0, H,
+                    KV, n_ctx, scs, scale, out, oq, err);
+      return;
+    }
+  }
   if (hd == 64 && G >= 2 && G <= 16) {
     // Scores only need the longest row of this chunk (rounded to float4).
     int sc_stride = ((pos0 + T) + 3) & ~3;
