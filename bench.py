@@ -26,6 +26,11 @@ import sys
 import time
 from pathlib import Path
 
+# Eight hardware queues for this process (HIP's default is four), so that
+# each of the four streams of the pipelined encode gets its own; set before
+# anything initialises HIP.
+os.environ["GPU_MAX_HW_QUEUES"] = "8"
+
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 

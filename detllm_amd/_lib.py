@@ -7,6 +7,7 @@ raises, so no product path can silently run on the CPU.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
 from .build import LIB_NAME, OUT_DIR
@@ -32,6 +33,11 @@ def _load() -> C.CDLL:
     return C.CDLL(str(LIB_PATH))
 
 
+# With at least five hardware queues per process the pipelined encode keeps
+# four chunks in flight on four streams, else three (HIP's default is four
+# queues).  Eight queues unless the caller chose otherwise; HIP reads the
+# setting when it initialises, i.e. at the library's first HIP call.
+os.environ.setdefault("GPU_MAX_HW_QUEUES", "8")
 lib = _load()
 
 u8p = C.POINTER(C.c_uint8)

@@ -627,12 +627,25 @@ const char* lm_head_class(int type) {
 }  // namespace
 
 // The buffers of one chunk in flight: activations, logits, the CDF staging,
-// the error flag and the stream its launches go to.  A session has kLanes of
-// them, so the pipelined encode (dtl_forward_ranges) runs chunks c + 1 and
-// c + 2 beside chunk c; every other entry point works on lane 0.
-// Three measured fastest on MI355X for the 64-position encode (two: 12.5k,
-// four: 12.0k tokens/s; the process has four hardware queues).
-constexpr int kLanes = 3;
+// the error flag and the stream its launches go to.  A session has 3 or 4 of
+// them, so the pipelined encode (dtl_forward_ranges) runs the next chunks
+// beside chunk c; every other entry point works on lane 0.
+// Measured on MI355X for the 64-position encode: with HIP's default of four
+// hardware queues per process three lanes (14.6k tokens/s; four lanes make
+// two streams share a queue: 13.0k); with GPU_MAX_HW_QUEUES=8 four lanes
+// (15.2k; five: 14.1k).  A session takes four lanes when the process has at
+// least five queues, else three; DETLLM_LANES (1-4) overrides.
+constexpr int kMaxLanes = 4;
+
+static int lane_count() {
+  if (const char* l = getenv("DETLLM_LANES")) {
+    const int n = atoi(l);
+    if (n >= 1 && n <= kMaxLanes) return n;
+  }
+  const char* e = getenv("GPU_MAX_HW_QUEUES");
+  const int queues = e && *e ? atoi(e) : 4;
+  return queues >= 5 ? 4 : 3;
+}
 
 struct Lane {
   hipStream_t stream = nullptr;
@@ -683,7 +696,8 @@ struct dtl_session {
   size_t n_ctx = 0, max_chunk = 0, max_in = 0;
   Arena arena;
   float *rope_cos = nullptr, *rope_sin = nullptr, *kc = nullptr, *vc = nullptr;
-  Lane lanes[kLanes];
+  Lane lanes[kMaxLanes];
+  int nlanes = 1;        // lanes set up (the rest stay empty)
   Lane* ln = &lanes[0];  // the lane the launches below go to
   // Captured single-position forward (see forward_device), on lane 0.
   hipGraphExec_t graph = nullptr;
@@ -1245,7 +1259,9 @@ int dtl_session_new(const dtl_model* m, size_t n_ctx, size_t max_chunk, dtl_sess
   ALLOC(vc, kv);
   ALLOC(pos_dev, 1);
 #undef ALLOC
-  for (Lane& L : s->lanes) {
+  s->nlanes = lane_count();
+  for (int li = 0; li < s->nlanes; li++) {
+    Lane& L = s->lanes[li];
     HIP_TRY(hipStreamCreateWithFlags(&L.stream, hipStreamNonBlocking));
 #define ALLOC(ptr, n) \
   if ((st = A.alloc(&L.ptr, (n)))) return st;
@@ -1426,8 +1442,8 @@ int dtl_symbol_ranges_rows(dtl_session* s, size_t n, const uint32_t* rows, const
 }
 
 // The forwards and symbol ranges of encode_symbols_with_model (det-cli
-// main.rs:521-551) for one window, with kLanes chunks in flight: chunk c
-// runs on lane c % kLanes and starts while the chunks before it are still
+// main.rs:521-551) for one window, with one chunk in flight per lane: chunk
+// c runs on lane c % nlanes and starts while the chunks before it are still
 // running (its attention at each layer waits for chunk c - 1's K/V rows of
 // that layer; every other launch is independent).  The host collects a
 // lane's ranges before reusing it.  Results equal dtl_forward_chunk +
@@ -1452,7 +1468,7 @@ int dtl_forward_ranges(dtl_session* s, const uint32_t* tokens, size_t n, size_t 
   struct Restore {
     dtl_session* s;
     ~Restore() {
-      for (Lane& L : s->lanes) (void)hipStreamSynchronize(L.stream);
+      for (int li = 0; li < s->nlanes; li++) (void)hipStreamSynchronize(s->lanes[li].stream);
       s->ln = &s->lanes[0];
     }
   } restore{s};
@@ -1460,7 +1476,8 @@ int dtl_forward_ranges(dtl_session* s, const uint32_t* tokens, size_t n, size_t 
     L.rows_valid = 0;
     L.cdf_ready_row = SIZE_MAX;
   }
-  size_t first[kLanes] = {}, count[kLanes] = {};  // symbols of each lane's chunk
+  const int nl = s->nlanes;
+  size_t first[kMaxLanes] = {}, count[kMaxLanes] = {};  // symbols of each lane's chunk
   auto collect = [&](int li) -> int {
     Lane& L = s->lanes[li];
     HIP_TRY(hipStreamSynchronize(L.stream));
@@ -1477,15 +1494,15 @@ int dtl_forward_ranges(dtl_session* s, const uint32_t* tokens, size_t n, size_t 
   const size_t nchunks = (n + C - 1) / C;
   size_t k = 0;
   for (size_t c = 0; c < nchunks; c++) {
-    const int li = (int)(c % kLanes);
-    if (c >= (size_t)kLanes)
+    const int li = (int)(c % nl);
+    if (c >= (size_t)nl)
       if (int st = collect(li)) return st;
     Lane& L = s->lanes[li];
     s->ln = &L;
     const size_t p0 = c * C, T = std::min(C, n - p0);
     std::memcpy(L.h_tokens, tokens + p0, T * sizeof(uint32_t));
     HIP_TRY(hipMemcpyAsync(L.tokens, L.h_tokens, T * 4, hipMemcpyHostToDevice, L.stream));
-    const Lane* prev = c ? &s->lanes[(c - 1) % kLanes] : nullptr;
+    const Lane* prev = c ? &s->lanes[(c - 1) % nl] : nullptr;
     int rc = enqueue_forward(s, (int)T, pos0 + p0, nullptr, prev, true);
     if (rc) return rc;
     const size_t k0 = k;
@@ -1517,8 +1534,8 @@ int dtl_forward_ranges(dtl_session* s, const uint32_t* tokens, size_t n, size_t 
     count[li] = ms;
   }
   // the chunks still in flight, oldest first
-  for (size_t c = nchunks > (size_t)kLanes ? nchunks - kLanes : 0; c < nchunks; c++)
-    if (int st = collect((int)(c % kLanes))) return st;
+  for (size_t c = nchunks > (size_t)nl ? nchunks - nl : 0; c < nchunks; c++)
+    if (int st = collect((int)(c % nl))) return st;
   s->prof.collect();
   return DTL_OK;
 }

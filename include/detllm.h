@@ -206,7 +206,7 @@ int dtl_symbol_ranges_rows(dtl_session *session, size_t n, const uint32_t *rows,
  * positions pos0.. in chunks of the session's max_chunk and codes
  * symbols[i] against the logits of token rows[i] (rows relative to pos0,
  * non-decreasing, < n).  The same results as dtl_forward_chunk followed by
- * dtl_symbol_ranges_rows per chunk; three chunks are in flight on three
+ * dtl_symbol_ranges_rows per chunk; four chunks are in flight on four
  * streams.  Afterwards no logits rows are valid (dtl_session_logits and
  * dtl_cdf need a new forward). */
 int dtl_forward_ranges(dtl_session *session, const uint32_t *tokens, size_t n, size_t pos0,

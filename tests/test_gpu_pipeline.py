@@ -53,14 +53,19 @@ def test_forward_ranges_matches_oracle(n, chunk, pos0, tail):
     assert got == _oracle_ranges(data, toks, pos0, rows, syms, tail)
 
 
-@pytest.mark.parametrize("name,layers,n,chunk", [
-    ("tinyllama", 2, 194, 64),   # final chunk of 2: decode attention with its own K/V store
-    ("tinyllama", 1, 197, 64),   # final chunk of 5: chunked attention
-    ("qwen05", 2, 70, 16),       # Q8_0 with bias
+@pytest.mark.parametrize("name,layers,n,chunk,lanes", [
+    ("tinyllama", 2, 194, 64, None),  # final chunk of 2: decode attention with its own K/V store
+    ("tinyllama", 1, 197, 64, None),  # final chunk of 5: chunked attention
+    ("qwen05", 2, 70, 16, None),      # Q8_0 with bias
+    ("qwen05", 1, 90, 16, "4"),       # four chunks in flight, whatever the queue count
+    ("qwen05", 1, 90, 16, "1"),
 ])
-def test_forward_ranges_equals_chunk_at_a_time(name, layers, n, chunk):
+def test_forward_ranges_equals_chunk_at_a_time(monkeypatch, name, layers, n, chunk, lanes):
     from detllm_amd import synth
     from detllm_amd.model import F32Llama
+
+    if lanes:
+        monkeypatch.setenv("DETLLM_LANES", lanes)  # read when the session is created
 
     w = synth.WORKLOADS[name]
     data = synth.build_model(w, layers=layers)
@@ -68,7 +73,7 @@ def test_forward_ranges_equals_chunk_at_a_time(name, layers, n, chunk):
     m = F32Llama.from_gguf(data)
     tail = 256
     rows, syms = _rows_symbols(n, m.vocab, tail, seed=n)
-    print(f"forward_ranges {name} layers={layers} n={n} chunk={chunk}", flush=True)
+    print(f"forward_ranges {name} layers={layers} n={n} chunk={chunk} lanes={lanes}", flush=True)
     with m.forward_workspace(n, chunk) as s:
         cum, freq, total = s.forward_ranges(toks, 0, rows, syms, tail)
         again = s.forward_ranges(toks, 0, rows, syms, tail)
