@@ -884,6 +884,21 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
       fused({&L.wq}, false, {s->ln->q}, {L.bq}, {e_q}, s->ln->x, L.attn_norm, "gemv_fused_qkv");
       fused({&L.wk}, false, {s->ln->k}, {L.bk}, {e_k}, s->ln->x, L.attn_norm, "gemv_fused_qkv");
       fused({&L.wv}, false, {s->ln->v}, {L.bv}, {e_v}, s->ln->x, L.attn_norm, "gemv_fused_qkv");
+    } else if (gemv_q4k_fit(L.wq, &L.wk, false, true, T, &L.wv)) {
+      // decode: the attention rmsnorm, its Q8A and Q8_K forms, wq+wk and
+      // wv (Q6_K, its rows on the workgroups' spare waves) in one launch
+      double bytes = (double)(L.wq.rows + L.wk.rows) * L.wq.cols * weight_bytes_per_elem(GGML_Q4_K) +
+                     (double)L.wv.rows * L.wv.cols * weight_bytes_per_elem(L.wv.type) +
+                     (double)T * d * 4.0 + (double)d * 4.0 +
+                     (double)T * (L.wq.rows + L.wk.rows + L.wv.rows) * 4.0;
+      Q4kIn in{nullptr, s->ln->x, L.attn_norm, c.eps};
+      in.v6 = &L.wv;
+      in.v6out = s->ln->v;
+      in.v6bias = L.bv;
+      in.v6epi = e_v;
+      P.timed(st, "gemv_q4_k_qkv", bytes, (double)(L.wq.rows + L.wk.rows + L.wv.rows) * L.wq.cols * T, [&] {
+        launch_gemv_q4k(L.wq, &L.wk, false, in, T, s->ln->q, s->ln->k, L.bq, L.bk, e_q, e_k, s->ln->err, st);
+      });
     } else if (L.wv.type == GGML_Q6_K && gemv_q4k_fit(L.wq, &L.wk, false, true, T)) {
       // decode: the attention rmsnorm and its quantisation inside the
       // wq+wk launch, whose first workgroup also writes the Q8_K form wv reads

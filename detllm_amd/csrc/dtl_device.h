@@ -156,8 +156,15 @@ struct Q4kIn {
   float eps;
   int8_t* side_qk = nullptr;  // with x: also the input's Q8_K form (for a Q6_K consumer)
   float* side_dk = nullptr;
+  // with x: a Q6_K matrix over the same normed input computed in the same
+  // launch (at most eight superblocks per row), its output, bias and epilogue
+  const DevMat* v6 = nullptr;
+  float* v6out = nullptr;
+  const float* v6bias = nullptr;
+  int v6epi = 0;
 };
-bool gemv_q4k_fit(const DevMat& W0, const DevMat* W1, bool pair, bool prologue, int T);
+bool gemv_q4k_fit(const DevMat& W0, const DevMat* W1, bool pair, bool prologue, int T,
+                  const DevMat* v6 = nullptr);
 bool launch_gemv_q4k(const DevMat& W0, const DevMat* W1, bool pair, const Q4kIn& in, int T,
                      float* out0, float* out1, const float* bias0, const float* bias1, int epi0,
                      int epi1, int* err, hipStream_t s);

@@ -595,6 +595,15 @@ struct Q4kPcArgs {
   float eps;
   int8_t* side_qk;      // with x: the first workgroup also writes the input's Q8_K form
   float* side_dk;
+  // With x: a Q6_K matrix over the same normed input (wv), one row per
+  // wave 1-7 of each workgroup (row blockIdx.x + (wave - 1) * gridDim.x),
+  // at most eight superblocks per row.
+  const uint32_t* v6w;  // 208-byte superblock bodies as 52 words
+  const uint16_t* v6d;
+  int v6rows, v6nb;
+  float* v6out;
+  const float* v6bias;
+  int v6epi;
   float* out0;
   float* out1;
   const float* bias0;
@@ -603,6 +612,12 @@ struct Q4kPcArgs {
   int* err;
 };
 
+// Floats of the input prologue's scratch: row, norm weights, chain-major
+// squares, 16 of scratch, Q8A scales and int8 values.
+__host__ __device__ constexpr size_t q4k_pc_prologue_floats(int cols) {
+  return 2 * (size_t)cols + 8 * (size_t)((((cols + 7) / 8) + 3) & ~3) + 16 + cols / 32 + cols / 4;
+}
+
 constexpr int kPcThreads = 512;  // eight waves: wave 0 runs the chains
 constexpr int kPcProducers = kPcThreads - 64;  // waves 1-7 form the products
 constexpr int kPcMaxPer = 4;     // weight float4 per producer thread and stage
@@ -610,6 +625,9 @@ constexpr int kPcMaxPer = 4;     // weight float4 per producer thread and stage
 template <int SL, int NS, int MODE>
 __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB) {
   constexpr int NM = MODE == PC_PAIR ? 2 : 1;
+  // fused Q6_K rows: wq+wk launches with 512-column stages only (the
+  // 128-column variants have no registers to spare for them)
+  constexpr bool V6 = MODE == PC_CAT && SL == 512;
   constexpr int LDP = SL + 4;             // product row stride (floats)
   constexpr int C4 = SL / 4;              // float4 per row and stage
   const int NR = NM * RB;                 // staged rows (gate rows, then up rows)
@@ -619,6 +637,13 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
   const int rows_total = MODE == PC_CAT ? p.rows0 + p.rows1 : p.rows0;
   float* as = smem;                       // [T][cols] activations
   float* prod = smem + (size_t)T * cols;  // [2][NR * T][LDP] products
+  // fused Q6_K rows: the input's Q8_K form [T][cols] (int8) and scales
+  // [T][cols / 256], then per wave 1-7 eight superblocks' class sums and scales
+  float* v6area = prod + (size_t)2 * NR * T * LDP + q4k_pc_prologue_floats(cols);
+  int8_t* v6q = reinterpret_cast<int8_t*>(v6area);
+  float* v6dk = v6area + (size_t)T * cols / 4;
+  int* v6aux = reinterpret_cast<int*>(v6dk + (size_t)T * (cols / 256));  // [7][8][8]
+  float* v6ds = reinterpret_cast<float*>(v6aux + 7 * 64);                 // [7][8]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int row0 = blockIdx.x * RB;
@@ -660,6 +685,24 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
     ring2[u] = *reinterpret_cast<const float4*>(s2 + o);
     ring3[u] = *reinterpret_cast<const float4*>(s3 + o);
   }
+  // The fused Q6_K row's superblock words of this lane (see below), loaded
+  // now so that they arrive during the stages; waves past the rows load row 0.
+  uint4 v6a{}, v6b{}, v6c{}, v6e{};
+  uint32_t v6sc = 0;
+  uint16_t v6dw = 0;
+  if (V6 && p.v6w) {
+    int r6 = blockIdx.x + (wave > 0 ? wave - 1 : 0) * gridDim.x;
+    r6 = r6 < p.v6rows ? r6 : 0;
+    const int sb = lane >> 3, h = (lane >> 2) & 1, pp = lane & 3;
+    const int sbl = sb < p.v6nb ? sb : 0;
+    const uint32_t* body = p.v6w + ((size_t)r6 * p.v6nb + sbl) * 52;
+    v6a = reinterpret_cast<const uint4*>(body + 16 * h + 8 * (pp & 1))[0];
+    v6b = reinterpret_cast<const uint4*>(body + 16 * h + 8 * (pp & 1))[1];
+    v6c = reinterpret_cast<const uint4*>(body + 32 + 8 * h)[0];
+    v6e = reinterpret_cast<const uint4*>(body + 32 + 8 * h)[1];
+    v6sc = body[48 + 2 * h + (pp >> 1)];
+    v6dw = p.v6d[(size_t)r6 * p.v6nb + sbl];
+  }
   if (p.af) {
     for (int i = tid; i < T * cols / 4; i += kPcThreads)
       reinterpret_cast<float4*>(as)[i] = reinterpret_cast<const float4*>(p.af)[i];
@@ -676,10 +719,12 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
     const FusedIn in{p.x, p.norm_w, p.eps};
     bool bad = false;
     for (int t = 0; t < T; t++) {
+      // the Q8_K form: to LDS for the fused Q6_K rows, else (first
+      // workgroup) to memory for a separate Q6_K launch
       const bool side = blockIdx.x == 0 && p.side_qk;
       bad |= q8a_prologue<kPcThreads / 64>(in, t, cols, p.norm_w != nullptr, xs, ws, sq, cs, qa_s,
-                                           da_s, misc, side ? p.side_qk : nullptr,
-                                           side ? p.side_dk : nullptr);
+                                           da_s, misc, p.v6w ? v6q : (side ? p.side_qk : nullptr),
+                                           p.v6w ? v6dk : (side ? p.side_dk : nullptr));
       for (int e = tid; e < cols; e += kPcThreads)
         as[(size_t)t * cols + e] = da_s[e / 32] * (float)qa_s[e];
       __syncthreads();
@@ -720,6 +765,81 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
       if (chain && k < nst) sum = chain_sum_lds_n<C4>(sum, pb + lane * LDP);
     }
   }
+  if (V6 && p.v6w && wave >= 1) {
+    const int r6 = blockIdx.x + (wave - 1) * gridDim.x;
+    if (r6 < p.v6rows) {
+      // dot_q6_k_q8k (det-quant lib.rs:353-397): lane = (superblock sb,
+      // half h, part pp) forms its share of the eight class sums (exact
+      // integers, reduced over the eight lanes of the superblock); lane 0
+      // then runs sums[l] += (dw * da) * aux[l] over the superblocks in order
+      // and adds the eight sums.
+      const int nsb = p.v6nb;
+      const int sb = lane >> 3, h = (lane >> 2) & 1, pp = lane & 3;
+      const int sbl = sb < nsb ? sb : 0;
+      const uint32_t qlw[8] = {v6a.x, v6a.y, v6a.z, v6a.w, v6b.x, v6b.y, v6b.z, v6b.w};
+      const uint32_t qhw[8] = {v6c.x, v6c.y, v6c.z, v6c.w, v6e.x, v6e.y, v6e.z, v6e.w};
+      const uint32_t scw = v6sc;
+      const float dwf = f16_to_f32(v6dw);
+      int* aux_w = v6aux + (wave - 1) * 64;
+      float* ds_w = v6ds + (wave - 1) * 8;
+      for (int t = 0; t < T; t++) {
+        const uint32_t* act = reinterpret_cast<const uint32_t*>(v6q + (size_t)t * cols + (size_t)sbl * 256);
+        int aux[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+          const uint32_t aw = act[8 * k + 4 * h + pp];
+          int acc = 0;
+#pragma unroll
+          for (int pair = 0; pair < 2; pair++) {
+            const int scale = (int)(int8_t)((scw >> (8 * (pair + 2 * (pp & 1)))) & 0xffu);
+            int sum = 0;
+#pragma unroll
+            for (int ii = 0; ii < 2; ii++) {
+              const int i = 2 * pair + ii;
+              const int l0 = k + 8 * i;
+              const uint32_t lo = (qlw[l0 >> 2] >> (8 * (l0 & 3) + 4 * (pp >> 1))) & 0x0fu;
+              const uint32_t hi = (qhw[l0 >> 2] >> (8 * (l0 & 3) + 2 * pp)) & 0x03u;
+              const int q6 = (int)(lo | (hi << 4)) - 32;
+              const int av = (int)(int8_t)((aw >> (8 * i)) & 0xffu);
+              sum += q6 * av;
+            }
+            acc += scale * sum;
+          }
+          aux[k] = acc;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+          aux[k] += __shfl_xor(aux[k], 1);
+          aux[k] += __shfl_xor(aux[k], 2);
+          aux[k] += __shfl_xor(aux[k], 4);
+        }
+        if ((lane & 7) == 0 && sb < nsb) {
+#pragma unroll
+          for (int k = 0; k < 8; k++) aux_w[sb * 8 + k] = aux[k];
+          ds_w[sb] = dwf * v6dk[(size_t)t * (cols / 256) + sb];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane == 0) {
+          float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+          for (int b = 0; b < nsb; b++) {
+            const float d = ds_w[b];
+#pragma unroll
+            for (int l = 0; l < 8; l++) sums[l] += d * (float)aux_w[b * 8 + l];
+          }
+          float v = 0.0f;
+#pragma unroll
+          for (int l = 0; l < 8; l++) v += sums[l];
+          if (!epilogue(v, p.v6out, (size_t)t * p.v6rows + r6, p.v6bias, r6, p.v6epi))
+            flag(p.err, ERRBIT_NON_FINITE);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+    }
+  }
   if (wave != 0) return;
   const int j = lane % NR, t = lane / NR;
   if (MODE == PC_PAIR) {
@@ -743,9 +863,10 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
 // LDS bytes: activations, two product buffers and, when the kernel forms
 // the activations itself, the prologue's row, norm weights, chain-major
 // squares, scratch, scales and int8 values.
-size_t q4k_pc_smem(int T, int cols, int NR, int SL, bool prologue) {
+size_t q4k_pc_smem(int T, int cols, int NR, int SL, bool prologue, bool v6) {
   size_t f = (size_t)T * cols + (size_t)2 * NR * T * (SL + 4);
-  if (prologue) f += 2 * (size_t)cols + 8 * (size_t)((((cols + 7) / 8) + 3) & ~3) + 16 + cols / 32 + cols / 4;
+  if (prologue || v6) f += q4k_pc_prologue_floats(cols);
+  if (v6) f += (size_t)T * cols / 4 + (size_t)T * (cols / 256) + 7 * 64 + 7 * 8;
   return f * sizeof(float);
 }
 
@@ -760,8 +881,8 @@ bool q4k_pc_enabled() {
 // most one workgroup per CU (at least eight rows each); the chain lanes
 // (staged rows x positions) must fit one wave and the stage's weights
 // kPcMaxPer float4 per thread.  256-column stages where those allow.
-bool q4k_pc_plan(int mode, int rows_total, int cols, int T, bool prologue, int* RB, int* SL,
-                 size_t* smem) {
+bool q4k_pc_plan(int mode, int rows_total, int cols, int T, bool prologue, bool v6, int* RB,
+                 int* SL, size_t* smem) {
   if (!q4k_pc_enabled() || cols % 256 != 0 || T < 1) return false;
   static const int cus = [] {
     int dev = 0, n = 0;
@@ -780,12 +901,13 @@ bool q4k_pc_plan(int mode, int rows_total, int cols, int T, bool prologue, int* 
   // products fit
   int sl = 512;
   while (sl > 128 && (NR * (sl / 4) > kPcMaxPer * kPcProducers ||
-                      q4k_pc_smem(T, cols, NR, sl, prologue) > 150 * 1024 || cols % sl != 0))
+                      q4k_pc_smem(T, cols, NR, sl, prologue, v6) > 150 * 1024 || cols % sl != 0))
     sl /= 2;
   if (NR * (sl / 4) > kPcMaxPer * kPcProducers || cols % sl != 0) return false;
+  if (v6 && (mode != PC_CAT || sl != 512)) return false;  // where the kernel has the fused rows
   *RB = rb;
   *SL = sl;
-  *smem = q4k_pc_smem(T, cols, NR, sl, prologue);
+  *smem = q4k_pc_smem(T, cols, NR, sl, prologue, v6);
   return *smem <= 150 * 1024;
 }
 
@@ -794,8 +916,11 @@ bool launch_q4k_pc(const Q4kPcArgs& a, hipStream_t s) {
   const int rows_total = MODE == PC_CAT ? a.rows0 + a.rows1 : a.rows0;
   int RB, SL;
   size_t smem;
-  if (!q4k_pc_plan(MODE, rows_total, a.cols, a.T, a.af == nullptr, &RB, &SL, &smem)) return false;
+  if (!q4k_pc_plan(MODE, rows_total, a.cols, a.T, a.af == nullptr, a.v6w != nullptr, &RB, &SL, &smem))
+    return false;
   const dim3 grid((rows_total + RB - 1) / RB);
+  // the fused Q6_K rows need waves 1-7 of the grid to cover them
+  if (a.v6w && (a.af || a.v6nb > 8 || (int)grid.x * (kPcThreads / 64 - 1) < a.v6rows)) return false;
 #define DTL_Q4K_PC(sl, ns)                                                                       \
   do {                                                                                           \
     static const bool attr = hipFuncSetAttribute((const void*)k_gemv_q4k_pc<sl, ns, MODE>,         \
@@ -1053,7 +1178,7 @@ bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const floa
   }
   if (W.type == kGgmlQ4K && W.w32) {
     Q4kPcArgs a{W.w32, nullptr, W.rows, 0, W.cols, T, A.af, nullptr, nullptr, 0.0f, nullptr, nullptr,
-                out, nullptr, bias, nullptr, epi, 0, err};
+                nullptr, nullptr, 0, 0, nullptr, nullptr, 0, out, nullptr, bias, nullptr, epi, 0, err};
     if (launch_q4k_pc<PC_SINGLE>(a, s)) return true;
   }
   if (W.type == kGgmlQ4K && W.w32 && W.cols % 256 == 0) {
@@ -1158,25 +1283,31 @@ bool launch_gemv_fused(const DevMat* const* mats, int nm, bool pair_swiglu, floa
   return true;
 }
 
-bool gemv_q4k_fit(const DevMat& W0, const DevMat* W1, bool pair, bool prologue, int T) {
+bool gemv_q4k_fit(const DevMat& W0, const DevMat* W1, bool pair, bool prologue, int T,
+                  const DevMat* v6) {
   int RB, SL;
   size_t smem;
   if (T > kGemvMaxT || W0.type != kGgmlQ4K || !W0.w32) return false;
   if (W1 && (W1->type != kGgmlQ4K || !W1->w32 || W1->cols != W0.cols || (pair && W1->rows != W0.rows)))
     return false;
+  if (v6 && (!prologue || v6->type != kGgmlQ6K || v6->cols != W0.cols || v6->nb > 8)) return false;
   const int mode = pair ? PC_PAIR : (W1 ? PC_CAT : PC_SINGLE);
   const int rows = pair || !W1 ? W0.rows : W0.rows + W1->rows;
-  return q4k_pc_plan(mode, rows, W0.cols, T, prologue, &RB, &SL, &smem);
+  if (!q4k_pc_plan(mode, rows, W0.cols, T, prologue, v6 != nullptr, &RB, &SL, &smem)) return false;
+  return !v6 || ((rows + RB - 1) / RB) * (kPcThreads / 64 - 1) >= v6->rows;
 }
 
 bool launch_gemv_q4k(const DevMat& W0, const DevMat* W1, bool pair, const Q4kIn& in, int T,
                      float* out0, float* out1, const float* bias0, const float* bias1, int epi0,
                      int epi1, int* err, hipStream_t s) {
-  if (!gemv_q4k_fit(W0, W1, pair, in.af == nullptr, T)) return false;
+  if (!gemv_q4k_fit(W0, W1, pair, in.af == nullptr, T, in.v6)) return false;
   if (in.side_qk && (in.af || W0.cols % 256 != 0)) return false;
+  const DevMat* v6 = in.v6;
   Q4kPcArgs a{W0.w32, W1 ? W1->w32 : nullptr, W0.rows, W1 && !pair ? W1->rows : 0, W0.cols, T,
-              in.af, in.x, in.norm_w, in.eps, in.side_qk, in.side_dk, out0, out1, bias0, bias1,
-              epi0, epi1, err};
+              in.af, in.x, in.norm_w, in.eps, in.side_qk, in.side_dk,
+              v6 ? static_cast<const uint32_t*>(v6->w) : nullptr, v6 ? v6->d16 : nullptr,
+              v6 ? v6->rows : 0, v6 ? v6->nb : 0, in.v6out, in.v6bias, in.v6epi,
+              out0, out1, bias0, bias1, epi0, epi1, err};
   if (pair) return launch_q4k_pc<PC_PAIR>(a, s);
   if (W1) return launch_q4k_pc<PC_CAT>(a, s);
   return launch_q4k_pc<PC_SINGLE>(a, s);
