@@ -370,6 +370,85 @@ __global__ void __launch_bounds__(64) k_gemv_q6k(DevMat W, const int8_t* __restr
   }
 }
 
+// Q6_K with each superblock split over eight lanes: one row per workgroup
+// of 8 * nsb lanes (rounded up to whole waves), lane = (superblock sb, half
+// h, part pp) as in the fused wv rows of k_gemv_q4k_pc.  A lane forms its
+// share (32 elements) of the eight exact class sums, the eight lanes of a
+// superblock add theirs (integers: any order), and thread 0 runs the
+// per-superblock f32 chain and the final combine as k_gemv_q6k does.  A
+// lane thus does an eighth of k_gemv_q6k's per-lane unpacking.
+__global__ void __launch_bounds__(256) k_gemv_q6k_split(DevMat W, const int8_t* __restrict__ qk,
+                                                       const float* __restrict__ dk, float* out,
+                                                       const float* bias, int epi, int* err) {
+  __shared__ int aux_s[32][8];
+  __shared__ float d_s[32];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int t = blockIdx.y, r = blockIdx.x;
+  const int rows = W.rows, cols = W.cols, nsb = W.nb;
+  const int sb = tid >> 3, h = (tid >> 2) & 1, pp = tid & 3;
+  const int sbl = sb < nsb ? sb : 0;
+  const uint32_t* body = (const uint32_t*)((const uint8_t*)W.w + ((size_t)r * nsb + sbl) * 208);
+  const uint4 qa4 = reinterpret_cast<const uint4*>(body + 16 * h + 8 * (pp & 1))[0];
+  const uint4 qb4 = reinterpret_cast<const uint4*>(body + 16 * h + 8 * (pp & 1))[1];
+  const uint4 ha4 = reinterpret_cast<const uint4*>(body + 32 + 8 * h)[0];
+  const uint4 hb4 = reinterpret_cast<const uint4*>(body + 32 + 8 * h)[1];
+  const uint32_t scw = body[48 + 2 * h + (pp >> 1)];
+  const uint32_t* act = (const uint32_t*)(qk + (size_t)t * cols + (size_t)sbl * 256);
+  uint32_t aw[8];
+#pragma unroll
+  for (int k = 0; k < 8; k++) aw[k] = act[8 * k + 4 * h + pp];
+  const uint16_t dw = W.d16[(size_t)r * nsb + sbl];
+  const float da = dk[(size_t)t * nsb + sbl];
+  const uint32_t qlw[8] = {qa4.x, qa4.y, qa4.z, qa4.w, qb4.x, qb4.y, qb4.z, qb4.w};
+  const uint32_t qhw[8] = {ha4.x, ha4.y, ha4.z, ha4.w, hb4.x, hb4.y, hb4.z, hb4.w};
+  int aux[8];
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    int acc = 0;
+#pragma unroll
+    for (int pair = 0; pair < 2; pair++) {
+      const int scale = (int)(int8_t)((scw >> (8 * (pair + 2 * (pp & 1)))) & 0xffu);
+      int sum = 0;
+#pragma unroll
+      for (int ii = 0; ii < 2; ii++) {
+        const int i = 2 * pair + ii;
+        const int l0 = k + 8 * i;
+        const uint32_t lo = (qlw[l0 >> 2] >> (8 * (l0 & 3) + 4 * (pp >> 1))) & 0x0fu;
+        const uint32_t hi = (qhw[l0 >> 2] >> (8 * (l0 & 3) + 2 * pp)) & 0x03u;
+        const int q6 = (int)(lo | (hi << 4)) - 32;
+        const int av = (int)(int8_t)((aw[k] >> (8 * i)) & 0xffu);
+        sum += q6 * av;
+      }
+      acc += scale * sum;
+    }
+    aux[k] = acc;
+  }
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    aux[k] += __shfl_xor(aux[k], 1);
+    aux[k] += __shfl_xor(aux[k], 2);
+    aux[k] += __shfl_xor(aux[k], 4);
+  }
+  if ((lane & 7) == 0 && sb < nsb) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) aux_s[sb][k] = aux[k];
+    d_s[sb] = f16_to_f32(dw) * da;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int b = 0; b < nsb; b++) {
+      const float d = d_s[b];
+#pragma unroll
+      for (int l = 0; l < 8; l++) sums[l] += d * (float)aux_s[b][l];
+    }
+    float v = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 8; l++) v += sums[l];
+    if (!epilogue(v, out, (size_t)t * rows + r, bias, r, epi)) flag(err, ERRBIT_NON_FINITE);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Q4_K from the exact f32 weights.  One wave per workgroup, RL rows (lanes)
 // per wave so that the short-lived chains spread over many CUs; the
@@ -1132,6 +1211,12 @@ void launch_q8(const DevMat& W, const DevAct& A, int T, float* out, const float*
 }
 }  // namespace
 
+// DETLLM_Q6K_GEMV_LANE_PER_SUPERBLOCK=1 keeps k_gemv_q6k.
+static bool q6k_split_enabled() {
+  static const bool on = !getenv("DETLLM_Q6K_GEMV_LANE_PER_SUPERBLOCK");
+  return on;
+}
+
 bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const float* bias, int epi,
                  int* err, hipStream_t s) {
   if (W.type == kGgmlQ8_0 && W.nb <= 32 && W.rows >= 16384) {
@@ -1167,6 +1252,15 @@ bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const floa
       launch_q8<kGgmlQ8_0>(W, A, T, out, bias, epi, err, s, R);
     else
       launch_q8<kGgmlQ4_0>(W, A, T, out, bias, epi, err, s, R);
+    return true;
+  }
+  // Split superblocks for the per-layer matrices (ffn_down: 11.9 -> 10.0 us
+  // per launch); the tall output projection keeps k_gemv_q6k (24.6 us, the
+  // split's one workgroup per row measured 29.1).
+  if (W.type == kGgmlQ6K && W.nb <= 32 && W.rows <= 16384 && q6k_split_enabled()) {
+    const int threads = (8 * W.nb + 63) / 64 * 64;
+    launch_kernel(k_gemv_q6k_split, dim3(W.rows, T), dim3(threads), 0, s, W, A.qk, A.dk, out, bias,
+                  epi, err);
     return true;
   }
   if (W.type == kGgmlQ6K) {
