@@ -168,10 +168,10 @@ def codec_leg(gguf: bytes, workload: str, nbytes: int, cpu_bytes: int, threads: 
     lm = LoadedModel.load(gguf)
     data = synth.markov_bytes(0xDE711005, nbytes)
     t = time.perf_counter()
-    out = compress(lm, data, n_ctx, max_chunk=64)
+    out = compress(lm, data, n_ctx)
     t_c = time.perf_counter() - t
     t = time.perf_counter()
-    back = decompress(lm, out, max_chunk=64)
+    back = decompress(lm, out)
     t_d = time.perf_counter() - t
     sym = lm.tokenizer.codec_symbols(data, lm.model.vocab)
     ntok = int((sym < lm.model.vocab).sum())

@@ -218,7 +218,15 @@ def _take(p, n: int) -> bytes:
         lib.dtl_bytes_free(p)
 
 
-def compress(loaded: LoadedModel, data: bytes, n_ctx: Optional[int] = None, max_chunk: int = 64) -> bytes:
+# Positions per forward chunk of the codec's sessions.  The bytes do not
+# depend on it (every position's logits are the same whatever the chunking);
+# 512 measured fastest on the Qwen2.5-0.5B shape (8 KiB compress: 8.9 KB/s at
+# 64, 10.0k at 128, 11.2k at 512, 11.4k at 1024).
+CODEC_CHUNK = 512
+
+
+def compress(loaded: LoadedModel, data: bytes, n_ctx: Optional[int] = None,
+             max_chunk: int = CODEC_CHUNK) -> bytes:
     """compress (main.rs:431-462): DTLZ header + payload."""
     src, n = _u8(data)
     sha, _ = _u8(loaded.model_sha256)
@@ -229,7 +237,7 @@ def compress(loaded: LoadedModel, data: bytes, n_ctx: Optional[int] = None, max_
     return _take(out, size.value)
 
 
-def decompress(loaded: Optional[LoadedModel], file: bytes, max_chunk: int = 64) -> bytes:
+def decompress(loaded: Optional[LoadedModel], file: bytes, max_chunk: int = CODEC_CHUNK) -> bytes:
     """decompress (main.rs:464-512).  The header is validated first, so a
     malformed file fails even without a model."""
     src, n = _u8(file)

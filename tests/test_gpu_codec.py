@@ -183,3 +183,20 @@ def test_dtlz_sizes_match_reference_records(model, text, size):
     assert len(out) == size
     assert out[56:] == _oracle_file(g, data, 8)
     assert decompress(lm, out) == data
+
+
+def test_compress_bytes_independent_of_chunk_size():
+    """The codec's chunk size is a schedule, not a parameter of the output:
+    the Qwen-shaped model (two layers) over several windows gives the same
+    file at chunks of 64 and of the default 512, and it decompresses."""
+    from detllm_amd import synth as sy
+    from detllm_amd.codec import CODEC_CHUNK, LoadedModel, compress, decompress
+
+    w = sy.WORKLOADS["qwen05"]
+    lm = LoadedModel.load(sy.build_model(w, layers=2))
+    data = sy.markov_bytes(0xDE711005, 1500)
+    print(f"codec chunks 64 / {CODEC_CHUNK}: {len(data)} bytes, n_ctx 256", flush=True)
+    a = compress(lm, data, 256, max_chunk=64)
+    b = compress(lm, data, 256)
+    assert a == b
+    assert decompress(lm, b) == data
