@@ -658,6 +658,7 @@ struct Lane {
   // CDF staging
   uint32_t *c_sym = nullptr, *c_freq = nullptr, *c_freq_tab = nullptr;
   uint64_t *c_cum = nullptr, *c_total = nullptr, *c_values = nullptr, *c_cum_tab = nullptr;
+  uint64_t* c_pack = nullptr;  // a decoder call's results and error bits, for one copy out
   uint8_t* c_scratch = nullptr;  // multi-workgroup CDF scratch for max_chunk rows
   uint32_t* c_rows = nullptr;    // row index per symbol (dtl_symbol_ranges_rows)
   // Row / tail whose decoder-total block results the scratch still holds.
@@ -672,6 +673,9 @@ struct Lane {
   uint64_t *h_cum = nullptr, *h_total = nullptr;
   int* h_err = nullptr;
   size_t h_cap = 0;  // symbols the h_rows .. h_total staging holds
+  // Pinned staging of the decoder entry points (value in, results out), so
+  // that their copies are plain DMA rather than staged pageable copies.
+  uint64_t* h_io = nullptr;
 };
 
 // Grows a lane's pinned symbol staging to n symbols (the lane must be idle).
@@ -714,7 +718,7 @@ struct dtl_session {
       for (hipEvent_t e : L.kv_ready)
         if (e) (void)hipEventDestroy(e);
       for (void* p : {(void*)L.h_tokens, (void*)L.h_rows, (void*)L.h_sym, (void*)L.h_freq,
-                      (void*)L.h_cum, (void*)L.h_total, (void*)L.h_err})
+                      (void*)L.h_cum, (void*)L.h_total, (void*)L.h_err, (void*)L.h_io})
         if (p) (void)hipHostFree(p);
     }
     if (graph) (void)hipGraphExecDestroy(graph);
@@ -732,12 +736,35 @@ size_t max_input_width(const dtl_model* m) {
 }
 
 int read_err(dtl_session* s, int* bits) {
-  HIP_TRY(hipMemcpyAsync(bits, s->ln->err, sizeof(int), hipMemcpyDeviceToHost, s->ln->stream));
+  HIP_TRY(hipMemcpyAsync(s->ln->h_err, s->ln->err, sizeof(int), hipMemcpyDeviceToHost, s->ln->stream));
   HIP_TRY(hipStreamSynchronize(s->ln->stream));
+  *bits = *s->ln->h_err;
   return DTL_OK;
 }
 
 __global__ void k_clear_flag(int* p) { *p = 0; }
+
+// The decoder entry points' results in one buffer: symbol, cum, freq, total
+// (absent ones 0) and the error bits.
+__global__ void k_pack_decoder(const uint32_t* sym, const uint64_t* cum, const uint32_t* freq,
+                               const uint64_t* total, const int* err, uint64_t* out) {
+  out[0] = sym ? sym[0] : 0;
+  out[1] = cum ? cum[0] : 0;
+  out[2] = freq ? freq[0] : 0;
+  out[3] = total[0];
+  out[4] = (uint64_t)(uint32_t)err[0];
+}
+
+// Packs, copies to the lane's pinned staging (h_io[2..6]) and waits.
+int read_decoder(dtl_session* s, const uint32_t* sym, const uint64_t* cum, const uint32_t* freq,
+                 int* bits) {
+  Lane& L = *s->ln;
+  launch_kernel(k_pack_decoder, dim3(1), dim3(1), 0, L.stream, sym, cum, freq, L.c_total, L.err, L.c_pack);
+  HIP_TRY(hipMemcpyAsync(L.h_io + 2, L.c_pack, 5 * sizeof(uint64_t), hipMemcpyDeviceToHost, L.stream));
+  HIP_TRY(hipStreamSynchronize(L.stream));
+  *bits = (int)(uint32_t)L.h_io[6];
+  return DTL_OK;
+}
 
 void clear_err(dtl_session* s) { launch_kernel(k_clear_flag, dim3(1), dim3(1), 0, s->ln->stream, s->ln->err); }
 
@@ -1303,6 +1330,7 @@ int dtl_session_new(const dtl_model* m, size_t n_ctx, size_t max_chunk, dtl_sess
     ALLOC(c_cum, C);
     ALLOC(c_total, C);
     ALLOC(c_values, C);
+    ALLOC(c_pack, 8);
     ALLOC(c_freq_tab, m->vocab + 256);
     ALLOC(c_cum_tab, m->vocab + 256);
     ALLOC(c_scratch, cdf_scratch_bytes((int)C, (int)m->vocab));
@@ -1312,6 +1340,7 @@ int dtl_session_new(const dtl_model* m, size_t n_ctx, size_t max_chunk, dtl_sess
     for (hipEvent_t& e : L.kv_ready) HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     HIP_TRY(hipHostMalloc((void**)&L.h_tokens, C * 4, hipHostMallocDefault));
     HIP_TRY(hipHostMalloc((void**)&L.h_err, sizeof(int), hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc((void**)&L.h_io, 8 * sizeof(uint64_t), hipHostMallocDefault));
     if ((st = lane_reserve(L, C))) return st;
   }
   HIP_TRY(hipHostMalloc((void**)&s->pos_host, sizeof(int), hipHostMallocDefault));
@@ -1612,9 +1641,9 @@ int dtl_decoder_total(dtl_session* s, size_t row, size_t tail, uint64_t* total) 
   clear_err(s);
   launch_cdf_blocks(s->ln->logits + row * V, nullptr, 1, (int)V, (int)tail, 3, nullptr, nullptr,
                     nullptr, nullptr, s->ln->c_total, nullptr, s->ln->c_scratch, false, s->ln->err, s->ln->stream);
-  HIP_TRY(hipMemcpyAsync(total, s->ln->c_total, 8, hipMemcpyDeviceToHost, s->ln->stream));
-  int bits = 0, st = read_err(s, &bits);
+  int bits = 0, st = read_decoder(s, nullptr, nullptr, nullptr, &bits);
   if (st) return st;
+  *total = s->ln->h_io[5];
   st = cdf_status(bits);
   if (st == DTL_OK) {
     // The block results of this row stay in the scratch for a lookup.
@@ -1632,17 +1661,19 @@ int dtl_decoder_lookup(dtl_session* s, size_t row, size_t tail, uint64_t value, 
   if (V + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
   HIP_TRY(hipSetDevice(s->m->device));
   clear_err(s);
-  HIP_TRY(hipMemcpyAsync(s->ln->c_values, &value, 8, hipMemcpyHostToDevice, s->ln->stream));
+  uint64_t* io = s->ln->h_io;  // [1] value in; [2] symbol, [3] cum, [4] freq, [5] total, [6] error bits out
+  io[1] = value;
+  HIP_TRY(hipMemcpyAsync(s->ln->c_values, io + 1, 8, hipMemcpyHostToDevice, s->ln->stream));
   const bool reuse = s->ln->cdf_ready_row == row && s->ln->cdf_ready_tail == tail;
   launch_cdf_blocks(s->ln->logits + row * V, nullptr, 1, (int)V, (int)tail, 2, nullptr, s->ln->c_values,
                     s->ln->c_cum, s->ln->c_freq, s->ln->c_total, s->ln->c_sym, s->ln->c_scratch, reuse, s->ln->err,
                     s->ln->stream);
-  HIP_TRY(hipMemcpyAsync(symbol, s->ln->c_sym, 4, hipMemcpyDeviceToHost, s->ln->stream));
-  HIP_TRY(hipMemcpyAsync(cum, s->ln->c_cum, 8, hipMemcpyDeviceToHost, s->ln->stream));
-  HIP_TRY(hipMemcpyAsync(freq, s->ln->c_freq, 4, hipMemcpyDeviceToHost, s->ln->stream));
-  HIP_TRY(hipMemcpyAsync(total, s->ln->c_total, 8, hipMemcpyDeviceToHost, s->ln->stream));
-  int bits = 0, st = read_err(s, &bits);
+  int bits = 0, st = read_decoder(s, s->ln->c_sym, s->ln->c_cum, s->ln->c_freq, &bits);
   if (st) return st;
+  *symbol = (uint32_t)io[2];
+  *cum = io[3];
+  *freq = (uint32_t)io[4];
+  *total = io[5];
   if (value >= *total) return DTL_ERR_CDF_SYMBOL_OUT_OF_RANGE;
   return cdf_status(bits);
 }
