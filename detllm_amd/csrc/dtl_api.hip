@@ -1435,19 +1435,25 @@ int dtl_symbol_ranges(dtl_session* s, size_t first, size_t n, const uint32_t* sy
     if (symbols[i] >= V + tail) return DTL_ERR_CDF_SYMBOL_OUT_OF_RANGE;
   HIP_TRY(hipSetDevice(s->m->device));
   clear_err(s);
-  s->ln->cdf_ready_row = SIZE_MAX;
-  HIP_TRY(hipMemcpyAsync(s->ln->c_sym, symbols, n * 4, hipMemcpyHostToDevice, s->ln->stream));
-  s->prof.timed(s->ln->stream, "cdf_symbol_range", (double)n * V * 4.0, 0.0, [&] {
-    launch_cdf_blocks(s->ln->logits + first * V, nullptr, (int)n, (int)V, (int)tail, 0, s->ln->c_sym,
-                      nullptr, s->ln->c_cum, s->ln->c_freq, s->ln->c_total, nullptr, s->ln->c_scratch, false,
-                      s->ln->err, s->ln->stream);
+  Lane& L = *s->ln;
+  L.cdf_ready_row = SIZE_MAX;
+  // through the lane's pinned staging (n <= max_chunk symbols fit it)
+  std::memcpy(L.h_sym, symbols, n * 4);
+  HIP_TRY(hipMemcpyAsync(L.c_sym, L.h_sym, n * 4, hipMemcpyHostToDevice, L.stream));
+  s->prof.timed(L.stream, "cdf_symbol_range", (double)n * V * 4.0, 0.0, [&] {
+    launch_cdf_blocks(L.logits + first * V, nullptr, (int)n, (int)V, (int)tail, 0, L.c_sym, nullptr,
+                      L.c_cum, L.c_freq, L.c_total, nullptr, L.c_scratch, false, L.err, L.stream);
   });
-  HIP_TRY(hipMemcpyAsync(cum, s->ln->c_cum, n * 8, hipMemcpyDeviceToHost, s->ln->stream));
-  HIP_TRY(hipMemcpyAsync(freq, s->ln->c_freq, n * 4, hipMemcpyDeviceToHost, s->ln->stream));
-  HIP_TRY(hipMemcpyAsync(total, s->ln->c_total, n * 8, hipMemcpyDeviceToHost, s->ln->stream));
+  HIP_TRY(hipMemcpyAsync(L.h_cum, L.c_cum, n * 8, hipMemcpyDeviceToHost, L.stream));
+  HIP_TRY(hipMemcpyAsync(L.h_freq, L.c_freq, n * 4, hipMemcpyDeviceToHost, L.stream));
+  HIP_TRY(hipMemcpyAsync(L.h_total, L.c_total, n * 8, hipMemcpyDeviceToHost, L.stream));
   int bits = 0, st = read_err(s, &bits);
   s->prof.collect();
-  return st ? st : cdf_status(bits);
+  if (st) return st;
+  std::memcpy(cum, L.h_cum, n * 8);
+  std::memcpy(freq, L.h_freq, n * 4);
+  std::memcpy(total, L.h_total, n * 8);
+  return cdf_status(bits);
 }
 
 int dtl_symbol_ranges_rows(dtl_session* s, size_t n, const uint32_t* rows, const uint32_t* symbols,
