@@ -13,6 +13,7 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
@@ -48,30 +49,31 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: a ROCm toolchain is required to build detllm_amd")
 
 
-def build_library(verbose: bool = False) -> Path:
-    """Compiles every source into one shared library and returns its path."""
-    OUT_DIR.mkdir(exist_ok=True)
-    out = OUT_DIR / LIB_NAME
-    tmp = OUT_DIR / (LIB_NAME + ".tmp")
-    cmd = [
-        hipcc(),
-        f"--offload-arch={ARCH}",
-        "-O3",
-        "-std=c++17",
-        "-fPIC",
-        "-shared",
-        *NUMERIC_FLAGS,
-        "-Wno-unused-result",
-        *[str(CSRC / s) for s in SOURCES],
-        "-o",
-        str(tmp),
-    ]
+def _run(cmd, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed with exit code {res.returncode}")
+        raise RuntimeError(f"hipcc failed with exit code {res.returncode}: {' '.join(cmd[-3:])}")
+
+
+def build_library(verbose: bool = False, jobs: int = 0) -> Path:
+    """Compiles every source (one hipcc per file, in parallel) and links
+    them into one shared library; returns its path."""
+    OUT_DIR.mkdir(exist_ok=True)
+    out = OUT_DIR / LIB_NAME
+    tmp = OUT_DIR / (LIB_NAME + ".tmp")
+    common = [hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", *NUMERIC_FLAGS,
+              "-Wno-unused-result"]
+    objs = [OUT_DIR / (Path(s).stem + ".o") for s in SOURCES]
+    cmds = [common + ["-c", str(CSRC / s), "-o", str(o)] for s, o in zip(SOURCES, objs)]
+    jobs = jobs or min(len(cmds), os.cpu_count() or 1, 16)
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        for f in [ex.submit(_run, c, verbose) for c in cmds]:
+            f.result()
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *[str(o) for o in objs], "-o", str(tmp)],
+         verbose)
     os.replace(tmp, out)
     return out
 

@@ -452,8 +452,8 @@ namespace {
 // device lacks room for them or DETLLM_NO_F32_MIRROR is set; the packed
 // kernels then serve every chunk size.
 // Copies the chunked-encode GEMMs read instead of the GGUF blocks: the
-// exact f32 value of every Q4_K weight, and the int8 matrix-core planes of
-// every Q6_K matrix.  DETLLM_NO_F32_MIRROR=1 keeps Q4_K packed only and
+// exact f32 value of every Q4_K weight, the int8 matrix-core planes of
+// every Q6_K matrix and the int8 values of every Q4_0 matrix.  DETLLM_NO_F32_MIRROR=1 keeps Q4_K packed only and
 // DETLLM_NO_Q6K_PLANES=1 keeps Q6_K packed only (the GEMMs then decode the
 // superblocks themselves; results are identical either way).
 bool env_flag(const char* name) {
@@ -464,18 +464,20 @@ bool f32_mirror_enabled() { return !env_flag("DETLLM_NO_F32_MIRROR"); }
 bool q6k_planes_enabled() { return !env_flag("DETLLM_NO_Q6K_PLANES"); }
 
 int build_encode_copies(dtl_model* m) {
-  std::vector<DevMat*> q4k, q6k;
+  std::vector<DevMat*> q4k, q6k, q40;
+  auto add = [&](DevMat* M) {
+    if (M->type == GGML_Q4_K && f32_mirror_enabled()) q4k.push_back(M);
+    if (M->type == GGML_Q6_K && q6k_planes_enabled()) q6k.push_back(M);
+    if (M->type == GGML_Q4_0) q40.push_back(M);
+  };
   for (Layer& L : m->layers)
-    for (DevMat* M : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down}) {
-      if (M->type == GGML_Q4_K && f32_mirror_enabled()) q4k.push_back(M);
-      if (M->type == GGML_Q6_K && q6k_planes_enabled()) q6k.push_back(M);
-    }
-  if (m->out.type == GGML_Q4_K && f32_mirror_enabled()) q4k.push_back(&m->out);
-  if (m->out.type == GGML_Q6_K && q6k_planes_enabled()) q6k.push_back(&m->out);
+    for (DevMat* M : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down}) add(M);
+  add(&m->out);
   size_t need = 0;
   for (DevMat* M : q4k) need += (size_t)M->rows * M->cols * sizeof(float);
   for (DevMat* M : q6k) need += q6k_planes_bytes(*M);
-  if (q4k.empty() && q6k.empty()) return DTL_OK;
+  for (DevMat* M : q40) need += (size_t)M->rows * M->cols;
+  if (q4k.empty() && q6k.empty() && q40.empty()) return DTL_OK;
   size_t free_b = 0, total_b = 0;
   HIP_TRY(hipMemGetInfo(&free_b, &total_b));
   if (need + (size_t(4) << 30) > free_b) return DTL_OK;
@@ -492,6 +494,13 @@ int build_encode_copies(dtl_model* m) {
     if (st) return st;
     launch_q6k_planes(*M, p, nullptr);
     M->planes = p;
+  }
+  for (DevMat* M : q40) {
+    int8_t* p;
+    int st = m->arena.alloc(&p, (size_t)M->rows * M->cols);
+    if (st) return st;
+    launch_q4_0_i8(*M, p, nullptr);
+    M->i8 = p;
   }
   HIP_TRY(hipGetLastError());
   HIP_TRY(hipDeviceSynchronize());
@@ -1954,6 +1963,12 @@ int dtl_kernel_gemv(int ggml_type, const uint8_t* weights, size_t rows, size_t c
     if ((st = sc.arena.alloc(&planes, q6k_planes_bytes(W)))) return st;
     launch_q6k_planes(W, planes, sc.stream);
     W.planes = planes;
+  }
+  if (W.type == GGML_Q4_0) {
+    int8_t* i8;
+    if ((st = sc.arena.alloc(&i8, rows * cols))) return st;
+    launch_q4_0_i8(W, i8, sc.stream);
+    W.i8 = i8;
   }
   float *dx, *dout, *af, *da, *dk;
   int8_t *qa, *qk;

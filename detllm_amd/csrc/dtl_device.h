@@ -70,6 +70,10 @@ struct DevMat {
   // 8j + c (j = 0..31) split as W' = 64*hi + lo (p = 0: hi in [-64, 64],
   // p = 1: lo in [0, 63]).  Rows are padded with zeros to a multiple of 16.
   const int8_t* planes;
+  // Q4_0 only (optional): int8[rows][cols], nibble - 8 of every element in
+  // element order, the A operand of the chunked-encode GEMM on the int8
+  // matrix cores (Q8_0 uses w itself).
+  const int8_t* i8;
 };
 
 // Activations of T positions for one GEMM input of width cols, in every
@@ -178,6 +182,8 @@ void launch_dequant_q4k(const DevMat& W, float* out, hipStream_t s);
 size_t q6k_planes_bytes(const DevMat& W);
 // Fills planes (q6k_planes_bytes(W) bytes) from W's Q6_K superblocks.
 void launch_q6k_planes(const DevMat& W, int8_t* planes, hipStream_t s);
+// Fills out (rows * cols bytes) with the int8 values of W's Q4_0 blocks.
+void launch_q4_0_i8(const DevMat& W, int8_t* out, hipStream_t s);
 // Two Q4_K matrices with the same input and column count (wq, wk) in one
 // launch of at least 16 positions, each with its own output, bias and
 // epilogue; false (nothing launched) when the pair does not qualify.

@@ -22,7 +22,7 @@ namespace dtl {
 namespace {
 
 constexpr int kWaves = 4;  // waves per workgroup
-constexpr int kGgmlQ4K = 12, kGgmlQ6K = 14, kGgmlQ8_0 = 8;
+constexpr int kGgmlQ4_0 = 2, kGgmlQ4K = 12, kGgmlQ6K = 14, kGgmlQ8_0 = 8;
 
 __device__ __forceinline__ void flag(int* err, int bit) { atomicOr(err, bit); }
 
@@ -814,6 +814,150 @@ __global__ void __launch_bounds__(256) k_q6k_mfma(const int8_t* __restrict__ pla
 }
 
 // ---------------------------------------------------------------------------
+// Q8_0 / Q4_0 on the int8 matrix cores: dot_q8_0_q8a / dot_q4_0_q8a
+// (det-quant lib.rs:237-279).  Per 32-element block b the reference forms
+// the exact integer isum = sum_e qw[e] * qa[e], then c = (dw * da) * isum
+// and one f32 chain per (row, position) over the blocks in order.  With K =
+// 64 covering blocks 2p and 2p+1, v_mfma_i32_16x16x64_i8 gives block 2p's
+// isum when the A operand's K quarters 2 and 3 are zero and block 2p+1's
+// when quarters 0 and 1 are: both exact in i32.  The f32 part runs on the
+// VALU in the reference's order.  Q4_0 uses the int8 copy of its weights
+// (nibble - 8, element order) built at load.
+//
+// MFMA operand layout (16x16x64 i8): lane l supplies row / position l % 16
+// and K quarter l / 16 (16 bytes); result register i of lane l is row
+// 4 (l / 16) + i, position l % 16.  A wave covers 16 rows x 16 NT
+// positions; a workgroup 4 / (4 / NT) row tiles x 64 positions.
+template <int NT>
+__global__ void __launch_bounds__(256) k_q8_mfma(const int8_t* __restrict__ w8,
+                                                 const uint16_t* __restrict__ d16, int rows, int nb,
+                                                 const int8_t* __restrict__ qa,
+                                                 const float* __restrict__ da, int T, float* out,
+                                                 const float* bias, int epi, int* err) {
+  constexpr int PT = 4 / NT;  // position tiles (of 16 NT) per workgroup
+  constexpr int RT = 4 / PT;  // row tiles per workgroup
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q = lane >> 4, li = lane & 15;
+  const int row0 = (blockIdx.x * RT + wave / PT) * 16;
+  const int p0 = blockIdx.y * 64 + (wave % PT) * 16 * NT;
+  const int cols = nb * 32;
+  const dtl_v4i zero = {0, 0, 0, 0};
+  int arow = row0 + li;
+  arow = arow < rows ? arow : rows - 1;
+  const int8_t* asrc = w8 + (size_t)arow * cols + 16 * q;
+  const int8_t* bsrc[NT];
+  const float* dsrc[NT];
+#pragma unroll
+  for (int j = 0; j < NT; j++) {
+    int pos = p0 + 16 * j + li;
+    pos = pos < T ? pos : T - 1;
+    bsrc[j] = qa + (size_t)pos * cols + 16 * q;
+    dsrc[j] = da + (size_t)pos * nb;
+  }
+  const uint16_t* dwsrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    int row = row0 + 4 * q + i;
+    row = row < rows ? row : rows - 1;
+    dwsrc[i] = d16 + (size_t)row * nb;
+  }
+  float sums[NT][4];
+#pragma unroll
+  for (int j = 0; j < NT; j++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) sums[j][i] = 0.0f;
+  // Operands of one block pair; the next pair's are in flight while the
+  // current one is multiplied.  In an odd last pair the second block's
+  // quarters re-read the first block's bytes and are zeroed.
+  struct Ops {
+    dtl_v4i a;
+    dtl_v4i b[NT];
+    uint16_t dw[2][4];
+    float dav[2][NT];
+  };
+  auto load = [&](Ops& o, int pr) {
+    const int b0 = 2 * pr;
+    const bool two = b0 + 1 < nb;
+    const int off = b0 * 32 + (two || q < 2 ? 0 : -32);
+    o.a = *(const dtl_v4i*)(asrc + off);
+#pragma unroll
+    for (int j = 0; j < NT; j++) o.b[j] = *(const dtl_v4i*)(bsrc[j] + off);
+    const int b1 = two ? b0 + 1 : b0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      o.dw[0][i] = dwsrc[i][b0];
+      o.dw[1][i] = dwsrc[i][b1];
+    }
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+      o.dav[0][j] = dsrc[j][b0];
+      o.dav[1][j] = dsrc[j][b1];
+    }
+  };
+  auto compute = [&](const Ops& o, bool two) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      if (h == 1 && !two) break;
+      const dtl_v4i a = (q >> 1) == h ? o.a : zero;
+      float dw[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) dw[i] = f16_to_f32(o.dw[h][i]);
+#pragma unroll
+      for (int j = 0; j < NT; j++) {
+        const dtl_v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, o.b[j], zero, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float dd = dw[i] * o.dav[h][j];
+          sums[j][i] += dd * (float)acc[i];
+        }
+      }
+    }
+  };
+  const int np = (nb + 1) / 2;
+  Ops x0, x1;
+  load(x0, 0);
+  int pr = 0;
+  for (; pr + 2 <= np; pr += 2) {
+    load(x1, pr + 1);
+    compute(x0, 2 * pr + 1 < nb);
+    if (pr + 2 < np) load(x0, pr + 2);
+    compute(x1, 2 * pr + 3 < nb);
+  }
+  if (pr < np) compute(x0, 2 * pr + 1 < nb);
+  bool ok = true;
+#pragma unroll
+  for (int j = 0; j < NT; j++) {
+    const int pos = p0 + 16 * j + li;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = row0 + 4 * q + i;
+      if (row < rows && pos < T)
+        ok &= store_epilogue(sums[j][i], out, (size_t)pos * rows + row, bias, row, epi);
+    }
+  }
+  if (!ok) flag(err, ERRBIT_NON_FINITE);
+}
+
+// int8 copy of a Q4_0 matrix in element order (nibble - 8; det-quant
+// lib.rs:259-279: element i < 16 is the low nibble of byte i, element
+// i + 16 its high nibble), the A operand of k_q8_mfma.
+__global__ void k_q4_0_i8(DevMat W, int8_t* out) {
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t total = (size_t)W.rows * W.cols;
+  if (idx >= total) return;
+  const size_t blk = idx / 32;
+  const int e = (int)(idx % 32);
+  const uint8_t b = ((const uint8_t*)W.w)[blk * 16 + (e & 15)];
+  out[idx] = (int8_t)((e < 16 ? (b & 15) : (b >> 4)) - 8);
+}
+
+void launch_q4_0_i8(const DevMat& W, int8_t* out, hipStream_t s) {
+  const size_t total = (size_t)W.rows * W.cols;
+  launch_kernel(k_q4_0_i8, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, W, out);
+}
+
+// ---------------------------------------------------------------------------
 // launchers
 
 namespace {
@@ -909,7 +1053,8 @@ Q4kF32Args q4k_args(const DevMat& W0, const DevMat* W1, const DevAct& A, int T, 
 }  // namespace
 
 bool gemm_tok_supported(const DevMat& W) {
-  return W.type == kGgmlQ4K || W.type == kGgmlQ6K || W.type == kGgmlQ8_0;
+  return W.type == kGgmlQ4K || W.type == kGgmlQ6K || W.type == kGgmlQ8_0 ||
+         (W.type == kGgmlQ4_0 && W.i8);
 }
 
 void launch_gemm_tok(const DevMat& W, const DevAct& A, int T, float* out, const float* bias,
@@ -931,6 +1076,22 @@ void launch_gemm_tok(const DevMat& W, const DevAct& A, int T, float* out, const 
       launch_kernel(k_q6k_mfma<1>, dim3(rt, (T + 15) / 16), dim3(256), 0, s, W.planes, W.d16,
                     W.rows, W.nb, A.qk, A.dk, T, out, bias, epi, err);
     }
+    return;
+  }
+  if ((W.type == kGgmlQ8_0 || (W.type == kGgmlQ4_0 && W.i8)) && T >= 16) {
+    // Q8_0 / Q4_0 on the int8 matrix cores: one workgroup per 64 positions
+    // and 16 (short matrices: every wave its own 16 positions), 32 or 64 rows.
+    const int8_t* w8 = W.type == kGgmlQ8_0 ? (const int8_t*)W.w : W.i8;
+    const dim3 gy(1, (T + 63) / 64);
+    if (W.rows >= 8192)
+      launch_kernel(k_q8_mfma<4>, dim3((W.rows + 63) / 64, gy.y), dim3(256), 0, s, w8, W.d16, W.rows,
+                    W.nb, A.qa, A.da, T, out, bias, epi, err);
+    else if (W.rows >= 2048)
+      launch_kernel(k_q8_mfma<2>, dim3((W.rows + 31) / 32, gy.y), dim3(256), 0, s, w8, W.d16, W.rows,
+                    W.nb, A.qa, A.da, T, out, bias, epi, err);
+    else
+      launch_kernel(k_q8_mfma<1>, dim3((W.rows + 15) / 16, gy.y), dim3(256), 0, s, w8, W.d16, W.rows,
+                    W.nb, A.qa, A.da, T, out, bias, epi, err);
     return;
   }
   int R = rows_per_wave(W.rows);

@@ -18,11 +18,11 @@ Workloads (shapes of well-known checkpoints, random weights):
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Tuple, List, Dict, Optional
+from typing import Callable, Dict, List, Optional, Tuple
 
 import numpy as np
 
-from .gguf import GGML_F32, GGML_Q4_K, GGML_Q6_K, GGML_Q8_0, GgufWriter
+from .gguf import GGML_F32, GGML_Q4_K, GGML_Q6_K, GGML_Q8_0, GgufWriter, Tensor
 
 GAMMA = np.uint64(0x9E3779B97F4A7C15)
 M1 = np.uint64(0xBF58476D1CE4E5B9)
@@ -214,9 +214,12 @@ def vocabulary(vocab: int) -> Tuple[List[str], List[int]]:
     return tokens, types
 
 
-def build_model(w: Workload, layers: Optional[int] = None) -> bytes:
+def build_model(w: Workload, layers: Optional[int] = None,
+                edit: Optional[Callable[[Tensor], None]] = None) -> bytes:
     """Writes the workload's model as GGUF bytes.  `layers` truncates depth
-    (used by quick tests); the benchmark always uses the full depth."""
+    (used by quick tests); the benchmark always uses the full depth.
+    `edit`, when given, may rewrite each tensor's bytes before the file is
+    written (tests plant non-finite or out-of-range values with it)."""
     L = w.layers if layers is None else layers
     hd = w.d // w.heads
     g = GgufWriter()
@@ -279,6 +282,9 @@ def build_model(w: Workload, layers: Optional[int] = None) -> bytes:
     norm("output_norm.weight", w.d)
     if not w.tied:
         mat("output.weight", w.vocab, w.d, kind_of("output", -1))
+    if edit is not None:
+        for t in g.tensors:
+            edit(t)
     return g.to_bytes()
 
 

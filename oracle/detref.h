@@ -86,6 +86,9 @@ void ref_model_free(ref_model *m);
  * pairing (0 adjacent, 1 split-half), context_length, vocab,
  * rms_eps bits, attention_scale bits, rope_base bits, emb type, out type, has_bias */
 void ref_model_config(const ref_model *m, int64_t out[16]);
+/* One layer's q (which 0), k (1) or v (2) bias: copies min(len, cap)
+ * values into out and returns len, 0 when absent. */
+size_t ref_model_bias(const ref_model *m, size_t layer, int which, float *out, size_t cap);
 ref_session *ref_session_new(const ref_model *m, size_t max_ctx, int *status);
 void ref_session_free(ref_session *s);
 int ref_session_reset(ref_session *s);

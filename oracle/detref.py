@@ -52,6 +52,7 @@ def load() -> C.CDLL:
         "ref_model_load": (C.c_void_p, [C.c_char_p, sz, C.POINTER(C.c_int)]),
         "ref_model_free": (None, [C.c_void_p]),
         "ref_model_config": (None, [C.c_void_p, C.POINTER(C.c_int64)]),
+        "ref_model_bias": (sz, [C.c_void_p, sz, C.c_int, f32p, sz]),
         "ref_session_new": (C.c_void_p, [C.c_void_p, sz, C.POINTER(C.c_int)]),
         "ref_session_free": (None, [C.c_void_p]),
         "ref_session_reset": (C.c_int, [C.c_void_p]),
@@ -136,6 +137,12 @@ class Model:
             lib().ref_model_free(self._h)
         except Exception:
             pass
+
+    def bias(self, layer: int, which: int):
+        """Layer bias q (0), k (1) or v (2) as loaded, or None when absent."""
+        buf = np.empty(1 << 16, np.float32)
+        n = lib().ref_model_bias(self._h, layer, which, _p(buf, C.c_float), buf.size)
+        return buf[:n].copy() if n else None
 
     def logits(self, tokens) -> np.ndarray:
         t = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32))

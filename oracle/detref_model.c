@@ -672,6 +672,19 @@ void ref_model_config(const ref_model *m, int64_t out[16]) {
     memcpy(out, v, sizeof v);
 }
 
+/* The q (which 0), k (1) or v (2) bias vector of one layer, as loaded by
+ * F32Llama::from_gguf (lib.rs:1060-1092): copies min(len, cap) values and
+ * returns len, or 0 when the layer has no such bias. */
+size_t ref_model_bias(const ref_model *m, size_t layer, int which, float *out, size_t cap) {
+    if (layer >= m->c.block_count || which < 0 || which > 2) return 0;
+    const layer_w *L = &m->layers[layer];
+    const float *b = which == 0 ? L->bq : which == 1 ? L->bk : L->bv;
+    if (!b) return 0;
+    size_t n = (which == 0 ? m->c.heads : m->c.kv_heads) * m->head_dim;
+    memcpy(out, b, (n < cap ? n : cap) * sizeof(float));
+    return n;
+}
+
 /* ---------------------------------------------------------------------- */
 /* RoPE tables (lib.rs:813-847)                                             */
 /* ---------------------------------------------------------------------- */

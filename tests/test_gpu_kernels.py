@@ -157,7 +157,8 @@ def test_rmsnorm_bitexact():
 
 # (type, rows, cols, positions): T <= 8 runs the decode GEMVs (rows per wave
 # grows with the row count: Q8_0/Q4_0 1/2/4/8, Q6_K 64/nsb, Q4_K 8/32),
-# T = 64 the token-parallel GEMMs, T in between the row-lane kernel.
+# T >= 16 the token-parallel GEMMs (Q8_0 / Q4_0 / Q6_K on the matrix
+# cores), T in between the row-lane kernel.
 GEMV_CASES = [
     (0, 37, 64, 3), (0, 20, 128, 1),
     (8, 61, 576, 1), (8, 33, 896, 5), (8, 9, 4864, 2), (8, 5000, 64, 1), (8, 17000, 64, 2),
@@ -166,6 +167,10 @@ GEMV_CASES = [
     (12, 45, 2048, 1), (12, 7, 5632, 3), (12, 30, 512, 64), (12, 9000, 256, 1), (12, 13, 256, 8),
     (12, 45, 256, 37), (12, 100, 768, 20),
     (14, 50, 2048, 1), (14, 9, 5632, 2), (14, 20, 512, 64), (14, 300, 256, 1), (14, 33, 4096, 1),
+    # Q8_0 / Q4_0 on the int8 matrix cores (T >= 16): odd block counts (a
+    # half block pair), row tiles of 16 / 32 / 64, partial position tiles
+    (8, 40, 32, 16), (8, 37, 96, 33), (8, 2100, 160, 17), (8, 8200, 64, 16), (8, 100, 896, 64),
+    (8, 64, 576, 100), (2, 40, 64, 16), (2, 33, 96, 70), (2, 2050, 64, 16),
 ]
 
 
