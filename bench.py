@@ -36,10 +36,14 @@ sys.path.insert(0, str(ROOT))
 
 # MI355X published peaks
 HBM_PEAK_GBS = 8000.0
-FP32_VECTOR_PEAK_TFLOPS = 157.3        # packed FMA rate
-# Separately rounded multiply + add without packed math (what the
-# reference's fixed-order f32 chains allow): 256 CU x 64 lanes x 2.4 GHz ops/s.
-FP32_UNFUSED_ISSUE_PEAK_TOPS = 39.3
+FP32_VECTOR_PEAK_TFLOPS = 157.3        # FMA counted as two flops
+# The reference's f32 chains allow no FMA: every multiply-accumulate is a
+# separately rounded multiply and add, two VALU instructions.  A wave64 f32
+# VALU instruction issues every two cycles per SIMD (measured: 58 T lane-ops/s
+# from an unrolled mul/add loop at 8 waves per SIMD), i.e. 256 CU x 4 SIMD x
+# 32 lanes x 2.4 GHz = 78.6 T instructions/s: 39.3 T MAC/s = 78.6 TFLOP/s,
+# half the FMA peak.
+FP32_UNFUSED_PEAK_TFLOPS = 78.6
 
 
 # HBM bytes per launch of the dominant kernel, from two rocprofv3 --pmc
@@ -202,13 +206,104 @@ def codec_leg(gguf: bytes, workload: str, nbytes: int, cpu_bytes: int, threads: 
     return res
 
 
+def host_cores() -> int:
+    """Cores this process may use (the box's share for one GPU is 16)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def cpu_baseline(ref, toks, tail: int, stride: int, threads: int) -> dict:
+    """The oracle (the C restatement of the reference's parallel,simd CPU
+    path) on positions 0, stride, 2 stride, ... of the same window: each a
+    forward_one at its real context length (the cache rows below it are
+    zero-filled, which costs the same arithmetic) plus the next token's
+    symbol range.  Timed at all host cores and at 8 threads."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import detref
+
+    detref.set_simd(True)
+    n = len(toks)
+    pos = list(range(0, n, stride))
+    nxt = [int(toks[p + 1]) if p + 1 < n else 0 for p in pos]
+    cores = threads or host_cores()
+    rates = {}
+    for th in (cores, 8):
+        detref.set_threads(th)
+        t = time.perf_counter()
+        ref.forward_at([int(toks[p]) for p in pos], pos, nxt, tail)
+        rates[th] = len(pos) / (time.perf_counter() - t)
+    detref.set_threads(0)
+    return {"value": round(rates[cores], 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "at_8_threads": round(rates[8], 3),
+            "sample": f"{len(pos)} positions spread over the {n}-position window (every {stride}th, each at "
+                      f"its own context length: forward + next-token symbol range), C oracle with AVX2 "
+                      f"integer dots, timed at {cores} threads and at 8"}
+
+
+def golden(name: str):
+    p = ROOT / "tests" / "golden" / f"workload_{name}.json"
+    return json.loads(p.read_text()) if p.exists() else None
+
+
+def encode_leg(name: str, chunk: int, steps: int) -> dict:
+    """Chunked encode of a workload's whole token stream (dtl_forward_ranges,
+    chunks of `chunk` in flight) with the next token's symbol range (256
+    byte escapes): tokens/s, the ranges against the committed golden, and the
+    per-class kernel times of one chunk-at-a-time pass."""
+    import hashlib
+    import struct
+
+    import numpy as np
+
+    from detllm_amd import synth
+    from detllm_amd.model import F32Llama
+
+    w = synth.WORKLOADS[name]
+    m = F32Llama.from_gguf(synth.build_model(w))
+    toks = synth.tokens(w)
+    n = toks.size
+    rows = np.arange(n, dtype=np.uint32)
+    nxt = np.concatenate([toks[1:], np.zeros(1, np.uint32)])
+    with m.forward_workspace(w.ctx, chunk) as s:
+        first = s.forward_ranges(toks, 0, rows, nxt, 256)
+        t = time.perf_counter()
+        for _ in range(steps):
+            got = s.forward_ranges(toks, 0, rows, nxt, 256)
+        dt = (time.perf_counter() - t) / steps
+        same = all(np.array_equal(a, b) for a, b in zip(first, got))
+        s.set_profiling(True)
+        for p in range(0, n, chunk):
+            s.forward_chunk(toks[p:p + chunk], p)
+        prof = s.profile()
+        s.set_profiling(False)
+    h = hashlib.sha256()
+    for c, f, tt in zip(*got):
+        h.update(struct.pack("<QIQ", int(c), int(f), int(tt)))
+    g = golden(name)
+    kernels = {}
+    for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["total_ms"]):
+        e = {"ms_per_pass": round(v["total_ms"], 3), "launches": v["launches"]}
+        if v["macs"] > 0 and v["total_ms"] > 0:
+            e["achieved_tops"] = round(2.0 * v["macs"] / (v["total_ms"] * 1e-3) / 1e12, 2)
+        kernels[k] = e
+    del m
+    return {"workload": name, "positions": int(n), "chunk": chunk, "tokens_per_s": round(n / dt, 1),
+            "ms_per_pass": round(dt * 1e3, 2), "deterministic": same,
+            "ranges_match_golden": g is not None and h.hexdigest() == g.get("next_token_ranges_sha256"),
+            "kernels_chunk_at_a_time": kernels}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--workload", default="tinyllama")
-    ap.add_argument("--cpu-tokens", type=int, default=96)
+    ap.add_argument("--cpu-stride", type=int, default=32,
+                    help="CPU baseline: every stride-th position of the window")
     ap.add_argument("--decode-positions", type=int, default=64)
     ap.add_argument("--decode-workload", default="qwen05",
                     help="model of the decode leg (qwen05: Q8_0 with a 145 MB output projection)")
@@ -222,6 +317,8 @@ def main() -> int:
                     help="only run a plain copy of this many MiB (counter calibration) and exit")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--encode-workload", default="qwen05",
+                    help="second chunked-encode leg (Q8_0 on the int8 matrix cores); '' to skip")
     ap.add_argument("--no-kernel-timing", action="store_true",
                     help="time the steps without per-launch events (no roofline object)")
     ap.add_argument("--traffic-kib", default=None,
@@ -324,14 +421,14 @@ def main() -> int:
         achieved = per_launch_flops / (avg_ms * 1e-3) / 1e12
         roofline = {"bound": "valu", "achieved": round(achieved, 3), "peak": FP32_VECTOR_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / FP32_VECTOR_PEAK_TFLOPS, 4),
-                    "unfused_issue_peak": FP32_UNFUSED_ISSUE_PEAK_TOPS,
-                    "frac_of_unfused_issue_peak": round(achieved / FP32_UNFUSED_ISSUE_PEAK_TOPS, 4)}
+                    "unfused_peak": FP32_UNFUSED_PEAK_TFLOPS,
+                    "frac_of_unfused_peak": round(achieved / FP32_UNFUSED_PEAK_TFLOPS, 4)}
     else:
         achieved = per_launch_bytes / (avg_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBS, 4)}
     roofline["timed_over"] = ("one chunk-at-a-time step timing the dominant class alone (launches not "
-                              "overlapped); the timed steps run three chunks in flight")
+                              "overlapped); the timed steps run four chunks in flight")
     roofline.update({"kernel": dom_name, "avg_launch_us": round(avg_ms * 1e3, 2), "launches": dom["launches"],
                      "algorithmic_bytes_per_launch": per_launch_bytes,
                      "algorithmic_flops_per_launch": per_launch_flops})
@@ -363,6 +460,18 @@ def main() -> int:
         lg = s2.forward_chunk(toks[:check_n], 0, want_logits=True)
     parity &= bool(np.array_equal(lg.view(np.uint32), ref_logits.view(np.uint32)))
     log(f"[bench] parity vs oracle on {check_n} positions: {parity}; deterministic: {deterministic}")
+    # The metric's logits hash: every position's logits of the window through
+    # the chunked forward, hashed as the reference does (SHA-256 of the f32
+    # bits, positions ascending), against the golden the oracle wrote.
+    logits_sha = model.logits_hash_for_tokens_chunked(toks, chunk).hex()
+    gold = golden(w.name)
+    logits_hash_match = gold is not None and logits_sha == gold["logits_sha256"]
+    log(f"[bench] logits hash {logits_sha[:16]}.. matches the oracle golden: {logits_hash_match}")
+    enc2 = None
+    if args.encode_workload:
+        enc2 = encode_leg(args.encode_workload, 64, 3)
+        log(f"[bench] {enc2['workload']} encode {enc2['tokens_per_s']} tok/s, "
+            f"ranges match golden {enc2['ranges_match_golden']}")
 
     # single-position decode of the same model (the per-token forward)
     decode_main = None
@@ -371,7 +480,7 @@ def main() -> int:
         log(f"[bench] {w.name} decode {decode_main['tokens_per_s']} tok/s")
     decode = None
     codec = None
-    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    threads = args.cpu_threads or host_cores()
     if args.decode_positions > 0 or args.codec_bytes > 0:
         dw = synth.WORKLOADS[args.decode_workload]
         ddata = data if dw.name == w.name else synth.build_model(dw)
@@ -395,18 +504,9 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu_baseline:
-        detref.set_threads(threads)
-        detref.set_simd(True)
-        k = args.cpu_tokens
-        t = time.perf_counter()
-        lgc = ref.logits(toks[:k])
-        for i in range(k):
-            detref.symbol_range(lgc[i], int(toks[i + 1]), tail)
-        dt = time.perf_counter() - t
-        cpu = {"value": round(k / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-               "sample": f"first {k} positions of the same 2048-token encode (forward + symbol range), "
-                         f"C oracle with {threads} threads and AVX2 integer dots"}
-        log(f"[bench] cpu baseline {cpu['value']} tok/s ({dt:.1f}s)")
+        cpu = cpu_baseline(ref, toks, tail, args.cpu_stride, args.cpu_threads)
+        log(f"[bench] cpu baseline {cpu['value']} tok/s at {cpu['cores']} threads, "
+            f"{cpu['at_8_threads']} tok/s at 8")
 
     line = {
         "metric": "encode tokens/s + % HBM roofline, 1.1B Q4_K/Q6_K, 1 GPU; logits hash match",
@@ -427,7 +527,10 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "parity_vs_oracle": parity,
+        "logits_sha256": logits_sha,
+        "logits_hash_match": logits_hash_match,
         "deterministic": deterministic,
+        "encode_q8_0": enc2,
         "kernels": kernels,
         "decode_main_workload": decode_main,
         "decode": decode,
@@ -439,7 +542,8 @@ def main() -> int:
     configs_ok = per_config is None or (per_config["C1"]["oracle_match"] and
                                         per_config["C2"]["parity_first_3_positions"] and
                                         per_config["C3"]["parity_first_3_positions"])
-    return 0 if parity and deterministic and codec_ok and configs_ok else 1
+    enc_ok = enc2 is None or (enc2["ranges_match_golden"] and enc2["deterministic"])
+    return 0 if parity and deterministic and logits_hash_match and codec_ok and configs_ok and enc_ok else 1
 
 
 if __name__ == "__main__":

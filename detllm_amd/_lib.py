@@ -106,11 +106,14 @@ _SIGS = {
     "dtl_decoder_lookup": (C.c_int, [C.c_void_p, sz, sz, C.c_uint64, u32p, u64p, u32p, u64p]),
     "dtl_logits_to_cdf": (C.c_int, [f32p, sz, sz, u32p, u64p, u64p]),
     "dtl_logits_to_symbol_range": (C.c_int, [f32p, sz, sz, sz, u64p, u32p, u64p]),
+    "dtl_uniform_cdf": (C.c_int, [sz, u32p, u64p, u64p]),
     "dtl_uniform_symbol_range": (C.c_int, [sz, sz, u64p, u32p, u64p]),
     "dtl_range_encoder_new": (C.c_int, [vpp]),
     "dtl_range_encode": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64]),
     "dtl_range_encoder_finish": (C.c_int, [C.c_void_p, u8p, sz, C.POINTER(sz)]),
     "dtl_range_encoder_free": (None, [C.c_void_p]),
+    "dtl_range_encoder_snapshot": (C.c_int, [C.c_void_p, u64p, u64p, u8p, sz, C.POINTER(sz)]),
+    "dtl_range_encoder_from_snapshot": (C.c_int, [C.c_uint64, C.c_uint64, u8p, sz, vpp]),
     "dtl_range_decoder_new": (C.c_int, [u8p, sz, vpp]),
     "dtl_range_decode_freq": (C.c_int, [C.c_void_p, C.c_uint64, u64p]),
     "dtl_range_decode_advance": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64]),

@@ -95,6 +95,21 @@ def logits_to_symbol_range_with_byte_escapes(logits, symbol: int) -> SymbolRange
     return _range(logits, symbol, BYTE_ESCAPE_SYMBOLS)
 
 
+def uniform_cdf(symbols: int) -> Cdf:
+    """uniform_cdf (cdf.rs:302-320)."""
+    freq = np.empty(max(symbols, 1), np.uint32)
+    cum = np.empty(max(symbols, 1), np.uint64)
+    total = C.c_uint64()
+    check(lib.dtl_uniform_cdf(symbols, ptr(freq, C.c_uint32), ptr(cum, C.c_uint64), C.byref(total)),
+          "uniform_cdf")
+    return Cdf(freq[:symbols], cum[:symbols], int(total.value))
+
+
+def uniform_cdf_with_byte_escapes(vocab_len: int) -> Cdf:
+    """uniform_cdf_with_byte_escapes (cdf.rs:102-106): vocabulary + 256 escape symbols."""
+    return uniform_cdf(vocab_len + BYTE_ESCAPE_SYMBOLS)
+
+
 def uniform_symbol_range(symbol: int, symbols: int) -> SymbolRange:
     """uniform_symbol_range (cdf.rs:322-341)."""
     cum, total = C.c_uint64(), C.c_uint64()
@@ -102,6 +117,14 @@ def uniform_symbol_range(symbol: int, symbols: int) -> SymbolRange:
     check(lib.dtl_uniform_symbol_range(symbol, symbols, C.byref(cum), C.byref(freq), C.byref(total)),
           "uniform_symbol_range")
     return SymbolRange(int(cum.value), int(freq.value), int(total.value))
+
+
+@dataclass
+class RangeEncoderSnapshot:
+    """RangeEncoderSnapshot (range.rs:17-22)."""
+    low: int
+    range: int
+    out: bytes
 
 
 class RangeEncoder:
@@ -114,6 +137,28 @@ class RangeEncoder:
 
     def encode(self, cum: int, freq: int, total: int) -> None:
         check(lib.dtl_range_encode(self._h, cum, freq, total), "RangeEncoder::encode")
+
+    def snapshot(self) -> RangeEncoderSnapshot:
+        """RangeEncoder::snapshot (range.rs:48-54)."""
+        low, rng, n = C.c_uint64(), C.c_uint64(), C.c_size_t()
+        check(lib.dtl_range_encoder_snapshot(self._h, C.byref(low), C.byref(rng), None, 0, C.byref(n)),
+              "RangeEncoder::snapshot")
+        buf = (C.c_uint8 * max(n.value, 1))()
+        check(lib.dtl_range_encoder_snapshot(self._h, C.byref(low), C.byref(rng), buf, n.value, C.byref(n)),
+              "RangeEncoder::snapshot")
+        return RangeEncoderSnapshot(int(low.value), int(rng.value), bytes(buf)[:n.value])
+
+    @classmethod
+    def from_snapshot(cls, snap: "RangeEncoderSnapshot") -> "RangeEncoder":
+        """RangeEncoder::from_snapshot (range.rs:37-46)."""
+        self = cls.__new__(cls)
+        data = (C.c_uint8 * max(len(snap.out), 1)).from_buffer_copy(bytes(snap.out) or b"\0")
+        h = C.c_void_p()
+        self._h = C.c_void_p()
+        check(lib.dtl_range_encoder_from_snapshot(snap.low, snap.range, data, len(snap.out), C.byref(h)),
+              "RangeEncoder::from_snapshot")
+        self._h = h
+        return self
 
     def finish(self) -> bytes:
         n = C.c_size_t()

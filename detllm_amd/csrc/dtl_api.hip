@@ -1788,6 +1788,18 @@ int dtl_logits_to_symbol_range(const float* logits, size_t n, size_t symbol, siz
   return run_cdf_host(logits, n, tail, 0, (uint32_t)symbol, cum, freq, total, nullptr, nullptr);
 }
 
+int dtl_uniform_cdf(size_t symbols, uint32_t* freq, uint64_t* cum, uint64_t* total) {
+  if (!freq || !cum || !total) return DTL_ERR_INVALID_ARGUMENT;
+  if (symbols == 0) return DTL_ERR_CDF_EMPTY;
+  if (symbols > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
+  for (size_t i = 0; i < symbols; i++) {
+    freq[i] = 1;
+    cum[i] = i;
+  }
+  *total = symbols;
+  return DTL_OK;
+}
+
 int dtl_uniform_symbol_range(size_t symbol, size_t symbols, uint64_t* cum, uint32_t* freq,
                              uint64_t* total) {
   if (!cum || !freq || !total) return DTL_ERR_INVALID_ARGUMENT;

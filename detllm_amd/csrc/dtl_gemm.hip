@@ -969,38 +969,27 @@ int rows_per_wave(int rows) {
   return 1;
 }
 
-// Rows per wave for the f32-weight Q4_K kernel (DETLLM_Q4K_NK overrides):
-// one row per wave keeps two waves per SIMD on 2k-row single matrices at 64
-// positions (measured fastest for wo and ffn_down); the gate/up pair, the
-// concatenated wq+wk and very tall matrices run faster amortising each
-// activation read over two rows.
+// Rows per wave for the f32-weight Q4_K kernel: one row per wave keeps two
+// waves per SIMD on 2k-row single matrices at 64 positions (measured
+// fastest for wo and ffn_down); the gate/up pair, the concatenated wq+wk and
+// very tall matrices run faster amortising each activation read over two
+// rows.
 int q4k_nk(int mode, int rows_total) {
-  static int forced = [] {
-    const char* e = getenv("DETLLM_Q4K_NK");
-    return e ? atoi(e) : 0;
-  }();
-  if (forced == 1 || forced == 2) return forced;
   if (mode == MODE_PAIR || mode == MODE_CAT) return 2;
   return rows_total >= 8192 ? 2 : 1;
 }
 
 // Tile of the split mapping as PW * 100 + WP * 10 + WR (0: k_q4k_f32w), per
-// mode; DETLLM_Q4K_MAP="single,pair,cat" overrides.  Measured at 64
-// positions on the 2048-column TinyLlama shapes: single matrices (wo, 2048 x
-// 2048, and ffn_down, 2048 x 5632) 26% faster with 8 positions x 8 rows per
-// wave and 2 x 4 waves, the wq+wk concatenation 14% faster with 2 x 2 waves;
-// the gate/up pair (two chains per lane at 16 positions x 4 rows, or four
-// in k_q4k_f32w) runs at the same rate either way and keeps k_q4k_f32w,
-// which overlapped better with the other chunks in flight.
+// mode.  Measured at 64 positions on the 2048-column TinyLlama shapes:
+// single matrices (wo, 2048 x 2048, and ffn_down, 2048 x 5632) 26% faster
+// with 8 positions x 8 rows per wave and 2 x 4 waves, the wq+wk
+// concatenation 14% faster with 2 x 2 waves; the gate/up pair (two chains
+// per lane at 16 positions x 4 rows, or four in k_q4k_f32w) runs at the same
+// rate either way and keeps k_q4k_f32w, which overlapped better with the
+// other chunks in flight.
 int q4k_map(int mode) {
-  static const std::array<int, 3> forced = [] {
-    std::array<int, 3> f{-1, -1, -1};
-    if (const char* e = getenv("DETLLM_Q4K_MAP")) sscanf(e, "%d,%d,%d", &f[0], &f[1], &f[2]);
-    return f;
-  }();
-  if (forced[mode] >= 0) return forced[mode];
-  static constexpr int kDefault[3] = {842, 0, 822};  // single, pair, cat
-  return kDefault[mode];
+  static constexpr int kMap[3] = {842, 0, 822};  // single, pair, cat
+  return kMap[mode];
 }
 
 template <int PW, int WP, int WR, int MODE>

@@ -949,12 +949,6 @@ size_t q4k_pc_smem(int T, int cols, int NR, int SL, bool prologue, bool v6) {
   return f * sizeof(float);
 }
 
-// DETLLM_Q4K_GEMV_CHAIN=1 keeps the one-lane-per-row Q4_K decode kernel.
-bool q4k_pc_enabled() {
-  static const bool on = !getenv("DETLLM_Q4K_GEMV_CHAIN");
-  return on;
-}
-
 // Rows per workgroup and columns per stage.  A chain wave runs far slower
 // when it shares its SIMD with another one, so the rows are spread over at
 // most one workgroup per CU (at least eight rows each); the chain lanes
@@ -962,7 +956,7 @@ bool q4k_pc_enabled() {
 // kPcMaxPer float4 per thread.  256-column stages where those allow.
 bool q4k_pc_plan(int mode, int rows_total, int cols, int T, bool prologue, bool v6, int* RB,
                  int* SL, size_t* smem) {
-  if (!q4k_pc_enabled() || cols % 256 != 0 || T < 1) return false;
+  if (cols % 256 != 0 || T < 1) return false;
   static const int cus = [] {
     int dev = 0, n = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -1211,12 +1205,6 @@ void launch_q8(const DevMat& W, const DevAct& A, int T, float* out, const float*
 }
 }  // namespace
 
-// DETLLM_Q6K_GEMV_LANE_PER_SUPERBLOCK=1 keeps k_gemv_q6k.
-static bool q6k_split_enabled() {
-  static const bool on = !getenv("DETLLM_Q6K_GEMV_LANE_PER_SUPERBLOCK");
-  return on;
-}
-
 bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const float* bias, int epi,
                  int* err, hipStream_t s) {
   if (W.type == kGgmlQ8_0 && W.nb <= 32 && W.rows >= 16384) {
@@ -1257,7 +1245,7 @@ bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const floa
   // Split superblocks for the per-layer matrices (ffn_down: 11.9 -> 10.0 us
   // per launch); the tall output projection keeps k_gemv_q6k (24.6 us, the
   // split's one workgroup per row measured 29.1).
-  if (W.type == kGgmlQ6K && W.nb <= 32 && W.rows <= 16384 && q6k_split_enabled()) {
+  if (W.type == kGgmlQ6K && W.nb <= 32 && W.rows <= 16384) {
     const int threads = (8 * W.nb + 63) / 64 * 64;
     launch_kernel(k_gemv_q6k_split, dim3(W.rows, T), dim3(threads), 0, s, W, A.qk, A.dk, out, bias,
                   epi, err);

@@ -1585,12 +1585,8 @@ void launch_attention_dec(const float* q, const RopeIn& R, int layer, int T, int
   // sized for the whole window.
   const int maxlen = pos_dev ? n_ctx : pos0 + T;
   const size_t smem = (size_t)maxlen * sizeof(float);
-  static const bool single = [] {
-    const char* e = getenv("DETLLM_ATTN_DEC_SINGLE");
-    return e && *e && *e != '0';
-  }();
   const size_t pv_smem = split_pv_smem(maxlen);
-  if (!single && maxlen <= kSplitMaxRows && pv_smem <= 158 * 1024) {
+  if (maxlen <= kSplitMaxRows && pv_smem <= 158 * 1024) {
     static bool attr_pv_set = false;
     if (!attr_pv_set) {
       (void)hipFuncSetAttribute((const void*)k_attn_split_pv,
@@ -1603,8 +1599,7 @@ void launch_attention_dec(const float* q, const RopeIn& R, int layer, int T, int
                   layer, pos0, H, KV, n_ctx, maxlen, out, pos_dev, err);
     return;
   }
-  // Longer windows (or DETLLM_ATTN_DEC_SINGLE=1): one workgroup per
-  // (head, position).
+  // Longer windows: one workgroup per (head, position).
   static bool attr_dec_set = false;
   if (!attr_dec_set) {
     (void)hipFuncSetAttribute((const void*)k_attention_dec,
@@ -1622,17 +1617,11 @@ bool attention_quantizes_q8a(int hd, int H, int KV, int T, int pos0, int n_ctx) 
          attention_hd64_smem(G, ((pos0 + T) + 3) & ~3) <= 150 * 1024;
 }
 
-// DETLLM_ATTN_WAVE_PER_HEAD=1 keeps k_attention_hd64 for groups of <= 8 heads.
-static bool attn_split_lanes() {
-  static const bool on = !getenv("DETLLM_ATTN_WAVE_PER_HEAD");
-  return on;
-}
-
 void launch_attention(const float* q, const float* kc, const float* vc, int layer, int T, int pos0,
                       int H, int KV, int hd, int n_ctx, float scale, float* scores, float* out,
                       int* err, hipStream_t s, int8_t* qa, float* da, float* af) {
   int G = H / KV;
-  if (hd == 64 && G >= 1 && G <= 8 && attn_split_lanes()) {
+  if (hd == 64 && G >= 1 && G <= 8) {
     const int scs = attn_split_lane_stride(pos0 + T);
     const size_t smem = attention_hd64s_smem(G, scs);
     if (smem <= 150 * 1024) {

@@ -77,6 +77,36 @@ int dtl_range_encode(dtl_range_encoder* e, uint64_t cum, uint64_t freq, uint64_t
   return DTL_OK;
 }
 
+// RangeEncoder::snapshot (range.rs:48-54): the coder state (low, range) and
+// the bytes emitted so far; out may be null to ask for their count in *len.
+int dtl_range_encoder_snapshot(const dtl_range_encoder* e, uint64_t* low, uint64_t* range, uint8_t* out,
+                               size_t cap, size_t* len) {
+  if (!e || !low || !range || !len) return DTL_ERR_INVALID_ARGUMENT;
+  *low = e->low;
+  *range = e->range;
+  *len = e->out.size();
+  if (!out) return DTL_OK;
+  if (cap < e->out.size()) return DTL_ERR_BUFFER_TOO_SMALL;
+  if (!e->out.empty()) std::memcpy(out, e->out.data(), e->out.size());
+  return DTL_OK;
+}
+
+// RangeEncoder::from_snapshot (range.rs:37-46): a zero range is rejected as
+// RangeError::InvalidFrequency.
+int dtl_range_encoder_from_snapshot(uint64_t low, uint64_t range, const uint8_t* bytes, size_t len,
+                                    dtl_range_encoder** out) {
+  if (!out || (len && !bytes)) return DTL_ERR_INVALID_ARGUMENT;
+  *out = nullptr;
+  if (range == 0) return DTL_ERR_RANGE_INVALID_FREQUENCY;
+  dtl_range_encoder* e = new (std::nothrow) dtl_range_encoder();
+  if (!e) return DTL_ERR_OUT_OF_MEMORY;
+  e->low = low;
+  e->range = range;
+  e->out.assign(bytes, bytes + len);
+  *out = e;
+  return DTL_OK;
+}
+
 int dtl_range_encoder_finish(dtl_range_encoder* e, uint8_t* out, size_t cap, size_t* len) {
   if (!e || !len) return DTL_ERR_INVALID_ARGUMENT;
   size_t n = e->out.size() + 8;

@@ -234,6 +234,10 @@ int dtl_logits_to_symbol_range(const float *logits, size_t n, size_t symbol, siz
                                uint64_t *cum, uint32_t *freq, uint64_t *total);
 
 /* uniform_symbol_range (cdf.rs:322-341). */
+/* uniform_cdf (cdf.rs:302-320): freq[i] = 1, cum[i] = i over `symbols`
+ * entries, total = symbols (the CDF of a window's first position, context
+ * length 0, with vocab + 256 symbols when byte escapes are on). */
+int dtl_uniform_cdf(size_t symbols, uint32_t *freq, uint64_t *cum, uint64_t *total);
 int dtl_uniform_symbol_range(size_t symbol, size_t symbols, uint64_t *cum, uint32_t *freq,
                              uint64_t *total);
 
@@ -247,6 +251,15 @@ int dtl_range_encode(dtl_range_encoder *enc, uint64_t cum, uint64_t freq, uint64
 /* Appends the 8 flush bytes and copies min(len, cap) bytes; *len = full size.
  * The encoder stays usable (finish does not consume it). */
 int dtl_range_encoder_finish(dtl_range_encoder *enc, uint8_t *out, size_t cap, size_t *len);
+/* RangeEncoder::snapshot (det-coder range.rs:48-54): low, range and the
+ * bytes emitted so far (out NULL: only their count in *len;
+ * DTL_ERR_BUFFER_TOO_SMALL when cap < *len).  The encoder is unchanged. */
+int dtl_range_encoder_snapshot(const dtl_range_encoder *enc, uint64_t *low, uint64_t *range,
+                               uint8_t *out, size_t cap, size_t *len);
+/* RangeEncoder::from_snapshot (range.rs:37-46): a new encoder resuming from
+ * (low, range, bytes); range 0 is DTL_ERR_RANGE_INVALID_FREQUENCY. */
+int dtl_range_encoder_from_snapshot(uint64_t low, uint64_t range, const uint8_t *bytes, size_t len,
+                                    dtl_range_encoder **out);
 void dtl_range_encoder_free(dtl_range_encoder *enc);
 
 /* RangeDecoder::{new, decode_freq, advance} (det-coder range.rs:94-159). */

@@ -156,6 +156,26 @@ class Model:
         _chk(lib().ref_logits_hash(self._h, _p(t, C.c_uint32), t.size, chunk, out), "ref_logits_hash")
         return bytes(out)
 
+    def forward_at(self, tokens, positions, next_symbols=None, tail: int = 0):
+        """forward_one (det-model lib.rs:1249-1400) of tokens[i] at positions[i]
+        in one session, in the order given: the cache rows below each position
+        are whatever the session holds (zeros, or earlier calls' rows).  With
+        next_symbols, also the symbol range of next_symbols[i] under each
+        position's logits.  Used to time positions spread over a window."""
+        st = C.c_int()
+        s = lib().ref_session_new(self._h, int(max(positions)) + 1, C.byref(st))
+        if not s:
+            raise OracleError(st.value, "ref_session_new")
+        out = np.empty(self.vocab, np.float32)
+        try:
+            for i, (t, p) in enumerate(zip(tokens, positions)):
+                _chk(lib().ref_forward_one(s, int(t), int(p), _p(out, C.c_float)), "ref_forward_one")
+                if next_symbols is not None:
+                    symbol_range(out, int(next_symbols[i]), tail)
+        finally:
+            lib().ref_session_free(s)
+        return out
+
     def rope_table(self, positions: int):
         half = int(self.cfg[6]) // 2
         c = np.empty(positions * half, np.float32)

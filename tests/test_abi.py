@@ -88,3 +88,59 @@ def test_dtlz_header_roundtrip():
     assert len(raw) == HEADER_LEN == 56 and raw[:4] == b"DTLZ"
     assert raw == h.encode()
     assert DtlzHeader.decode(raw) == h
+
+
+def test_range_encoder_snapshot_resumes_canonical_stream():
+    # det-coder range.rs:208-230: encode a prefix, snapshot, restore, encode
+    # the rest: the same bytes as one uninterrupted encoder.
+    from detllm_amd._lib import DetllmError
+    from detllm_amd.coder import RangeEncoder, RangeEncoderSnapshot
+
+    cum = [0, 1, 0, 2, 1, 3, 0, 2]
+    freq = [1, 1, 2, 1, 2, 1, 1, 2]
+    one = RangeEncoder()
+    for c, f in zip(cum, freq):
+        one.encode(c, f, 4)
+    part = RangeEncoder()
+    for c, f in zip(cum[:4], freq[:4]):
+        part.encode(c, f, 4)
+    snap = part.snapshot()
+    resumed = RangeEncoder.from_snapshot(snap)
+    for c, f in zip(cum[4:], freq[4:]):
+        resumed.encode(c, f, 4)
+    assert resumed.finish() == one.finish()
+    # a long stream through several snapshots equals the oracle's bytes
+    rng = np.random.default_rng(3)
+    triples = []
+    for _ in range(5000):
+        total = int(rng.integers(2, 1 << 20))
+        f = int(rng.integers(1, total + 1))
+        triples.append((int(rng.integers(0, total - f + 1)), f, total))
+    enc = RangeEncoder()
+    for i, t in enumerate(triples):
+        if i % 997 == 0:
+            enc = RangeEncoder.from_snapshot(enc.snapshot())
+        enc.encode(*t)
+    assert enc.finish() == detref.range_encode(triples)
+    try:
+        RangeEncoder.from_snapshot(RangeEncoderSnapshot(snap.low, 0, snap.out))
+        raise AssertionError("range 0 accepted")
+    except DetllmError as e:
+        assert e.status == 30  # RangeError::InvalidFrequency
+
+
+def test_uniform_cdf():
+    # det-coder cdf.rs:684-705
+    from detllm_amd._lib import DetllmError
+    from detllm_amd.coder import uniform_cdf, uniform_cdf_with_byte_escapes
+
+    c = uniform_cdf(4)
+    assert c.freq.tolist() == [1, 1, 1, 1] and c.cum.tolist() == [0, 1, 2, 3] and c.total == 4
+    c = uniform_cdf_with_byte_escapes(151936)
+    assert c.total == 152192 and c.cum[-1] == 152191 and int(c.freq.sum()) == 152192
+    for n, st in ((0, 20), ((1 << 18) + 1, 24)):
+        try:
+            uniform_cdf(n)
+            raise AssertionError(n)
+        except DetllmError as e:
+            assert e.status == st

@@ -207,3 +207,26 @@ def test_standalone_cdf_kernel_matches_oracle(V):
         for s in (0, V // 2, V - 1, V + tail - 1):
             r = coder._range(lg, s, tail)
             assert (r.cum, r.freq, r.total) == detref.symbol_range(lg, s, tail)
+
+
+@pytest.mark.parametrize("graph", [True, False])
+def test_decode_window_over_2048_matches_oracle(monkeypatch, graph):
+    # A session window over 2048 positions: the decode attention runs one
+    # workgroup per (head, position) (k_attention_dec) instead of the split
+    # score / P.V launches; with the captured graph the grids are sized for
+    # the whole 4096-position window.
+    import dataclasses
+
+    from detllm_amd import synth
+
+    if not graph:
+        monkeypatch.setenv("DETLLM_NO_GRAPH", "1")
+    w = dataclasses.replace(synth.WORKLOADS["smollm2"], ctx=4096)
+    data = synth.build_model(w, layers=1)
+    toks = [int(t) for t in synth.tokens(w, 9)]
+    ref = detref.Model(data).logits(toks)
+    m = _model(data)
+    with m.forward_workspace(4096, 1) as s:
+        for p, tok in enumerate(toks):
+            got = s.forward_one(tok, p)
+            assert np.array_equal(got.view(np.uint32), ref[p].view(np.uint32)), p

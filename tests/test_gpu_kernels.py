@@ -166,6 +166,9 @@ GEMV_CASES = [
     (2, 40, 64, 2), (2, 17, 512, 1), (2, 66000, 64, 1), (2, 5000, 96, 3),
     (12, 45, 2048, 1), (12, 7, 5632, 3), (12, 30, 512, 64), (12, 9000, 256, 1), (12, 13, 256, 8),
     (12, 45, 256, 37), (12, 100, 768, 20),
+    # 8 positions x 5632 columns: the split decode kernel's LDS does not hold
+    # the activations, so the one-lane-per-row Q4_K kernel serves it
+    (12, 20, 5632, 8),
     (14, 50, 2048, 1), (14, 9, 5632, 2), (14, 20, 512, 64), (14, 300, 256, 1), (14, 33, 4096, 1),
     # Q8_0 / Q4_0 on the int8 matrix cores (T >= 16): odd block counts (a
     # half block pair), row tiles of 16 / 32 / 64, partial position tiles
