@@ -108,6 +108,10 @@ _SIGS = {
     "dtl_logits_to_symbol_range": (C.c_int, [f32p, sz, sz, sz, u64p, u32p, u64p]),
     "dtl_uniform_cdf": (C.c_int, [sz, u32p, u64p, u64p]),
     "dtl_uniform_symbol_range": (C.c_int, [sz, sz, u64p, u32p, u64p]),
+    # device pointers throughout (logits, symbols, cum, freq, total, status word, stream)
+    "dtl_symbol_ranges_static": (C.c_int, [C.c_void_p, sz, sz, C.c_void_p, sz, C.c_void_p, C.c_void_p,
+                                           C.c_void_p, C.c_void_p, C.c_void_p]),
+    "dtl_status_from_bits": (C.c_int, [C.c_int]),
     "dtl_range_encoder_new": (C.c_int, [vpp]),
     "dtl_range_encode": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64]),
     "dtl_range_encoder_finish": (C.c_int, [C.c_void_p, u8p, sz, C.POINTER(sz)]),

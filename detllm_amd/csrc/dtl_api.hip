@@ -3,6 +3,7 @@
 // sequence of the decoder forward and the C ABI declared in detllm.h.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstdio>
@@ -1178,6 +1179,7 @@ const char* dtl_status_string(int status) {
     case DTL_ERR_INVALID_ARGUMENT: return "invalid argument";
     case DTL_ERR_NO_DEVICE: return "no HIP device";
     case DTL_ERR_BUFFER_TOO_SMALL: return "output buffer too small";
+    case DTL_ERR_STATIC_SCRATCH_LIMIT: return "call exceeds the static scratch (rows <= 8, vocab + tail <= 2^18)";
     case DTL_ERR_TOKEN_MISSING_BYTE_FALLBACK: return "token: missing byte fallback";
     case DTL_ERR_TOKEN_INVALID_TOKEN: return "token: invalid token";
     case DTL_ERR_TOKEN_MISSING_VOCABULARY: return "token: missing vocabulary";
@@ -1810,6 +1812,82 @@ int dtl_uniform_symbol_range(size_t symbol, size_t symbols, uint64_t* cum, uint3
   *freq = 1;
   *total = symbols;
   return DTL_OK;
+}
+
+// ---- symbol ranges without allocation ----------------------------------------
+// Callers that cannot allocate (code under HIP graph capture, serving loops
+// that forbid hipMalloc) get the multi-workgroup CDF's scratch from one
+// file-scope device array per GPU instead of a per-call or per-session
+// buffer.  Its device address comes from hipGetSymbolAddress on the
+// entry point's first call on each device; host code never passes the
+// array's name to a kernel.  Calls on one GPU share the array, so calls
+// that overlap on one GPU race.  No field of the scratch has to start at
+// zero (every kernel writes what the next one reads); the caller's status
+// word is cleared by the first launch of each call, with a kernel rather
+// than a memset so that the call can be captured into a graph.
+}  // extern "C"
+
+namespace {
+constexpr size_t kStaticCdfRows = 8;
+constexpr size_t kStaticCdfScratchBytes = 8u << 20;  // >= cdf_scratch_bytes(8, 1 << 18)
+static __device__ __align__(256) uint8_t scratch[kStaticCdfScratchBytes];
+constexpr int kStaticMaxDevices = 64;
+std::atomic<void*> g_static_scratch[kStaticMaxDevices];
+
+// The device address of this device's scratch array (null on failure).
+void* static_scratch_ptr(int dev) {
+  if (dev < 0 || dev >= kStaticMaxDevices) return nullptr;
+  void* p = g_static_scratch[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  g_static_scratch[dev].store(p, std::memory_order_release);
+  return p;
+}
+
+// Clears the status word and flags symbols outside [0, limit): the range
+// kernels themselves never index with the symbol past the table, so a bad
+// symbol only has to be reported.
+__global__ void k_static_prepare(int* bits, const uint32_t* symbols, int R, uint32_t limit) {
+  __shared__ int bad;
+  if (threadIdx.x == 0) bad = 0;
+  __syncthreads();
+  for (int r = threadIdx.x; r < R; r += blockDim.x)
+    if (symbols[r] >= limit) bad = 1;
+  __syncthreads();
+  if (threadIdx.x == 0) *bits = bad ? ERRBIT_CDF_SYMBOL : 0;
+}
+}  // namespace
+
+extern "C" {
+
+int dtl_symbol_ranges_static(const float* logits, size_t rows, size_t vocab, const uint32_t* symbols,
+                             size_t tail, uint64_t* cum, uint32_t* freq, uint64_t* total,
+                             int* status_bits, void* stream) {
+  if (!logits || !symbols || !cum || !freq || !total || !status_bits) return DTL_ERR_INVALID_ARGUMENT;
+  if (rows == 0 || vocab == 0) return DTL_ERR_CDF_EMPTY;
+  if (vocab + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
+  if (rows > kStaticCdfRows) return DTL_ERR_STATIC_SCRATCH_LIMIT;
+  if (cdf_scratch_bytes((int)rows, (int)vocab) > kStaticCdfScratchBytes) return DTL_ERR_STATIC_SCRATCH_LIMIT;
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  void* ptr = static_scratch_ptr(dev);
+  if (!ptr) return DTL_ERR_DEVICE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  launch_kernel(k_static_prepare, dim3(1), dim3(64), 0, st, status_bits, symbols, (int)rows,
+                (uint32_t)(vocab + tail));
+  launch_cdf_blocks(logits, nullptr, (int)rows, (int)vocab, (int)tail, 0, symbols, nullptr, cum, freq,
+                    total, nullptr, ptr, false, status_bits, st);
+  HIP_TRY(hipGetLastError());
+  return DTL_OK;
+}
+
+int dtl_status_from_bits(int bits) {
+  if (bits & ERRBIT_NON_FINITE) return DTL_ERR_NON_FINITE;
+  if (bits & ERRBIT_CDF_SYMBOL) return DTL_ERR_CDF_SYMBOL_OUT_OF_RANGE;
+  return cdf_status(bits);
 }
 
 int dtl_kernel_exp_f32(const float* in, float* out, size_t n) {

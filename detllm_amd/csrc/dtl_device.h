@@ -41,6 +41,7 @@ enum : int {
   ERRBIT_CDF_NON_FINITE = 2,     // CdfError::NonFiniteLogit
   ERRBIT_CDF_TOTAL = 4,          // CdfError::TotalTooLarge
   ERRBIT_CDF_LOOKUP = 8,         // decoder value outside every symbol
+  ERRBIT_CDF_SYMBOL = 16,        // CdfError::SymbolOutOfRange (symbols held on the device)
 };
 
 // One weight matrix in device layout.  Values are the GGUF values exactly;

@@ -54,6 +54,7 @@ typedef enum {
     DTL_ERR_INVALID_ARGUMENT = 42,
     DTL_ERR_NO_DEVICE = 43,
     DTL_ERR_BUFFER_TOO_SMALL = 44, /* output capacity below the size in *len */
+    DTL_ERR_STATIC_SCRATCH_LIMIT = 45, /* a call larger than dtl_symbol_ranges_static's scratch */
     /* 60-77: det-token TokenError (crates/det-token/src/lib.rs:6-25), in order;
      * 77 also reports a BPE / SentencePiece vocabulary, which this library
      * does not tokenize. */
@@ -225,6 +226,25 @@ int dtl_decoder_total(dtl_session *session, size_t row, size_t tail_symbols, uin
 /* DecoderDistribution::symbol_range (cdf.rs:392-425), run on the device. */
 int dtl_decoder_lookup(dtl_session *session, size_t row, size_t tail_symbols, uint64_t value,
                        uint32_t *symbol, uint64_t *cum, uint32_t *freq, uint64_t *total);
+
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory: code under HIP graph capture, serving loops and harnesses that
+ * forbid hipMalloc.  The symbol ranges of dtl_symbol_ranges /
+ * dtl_logits_to_symbol_range (logits_to_symbol_range_*, det-coder
+ * cdf.rs:122-199) of symbols[i] against row i of logits[rows][vocab], with
+ * every pointer in device memory and the work enqueued on `stream` (a
+ * hipStream_t; NULL is the default stream) without waiting for it.  The
+ * CDF scratch is a static device array of 8 MiB per GPU, held until the
+ * process ends: rows <= 8 and vocab + tail_symbols <= 2^18, else
+ * DTL_ERR_STATIC_SCRATCH_LIMIT.  The call allocates nothing.  *status_bits
+ * (device memory) is overwritten with the call's error bits once the stream
+ * reaches it; dtl_status_from_bits maps them to a dtl_status.  Calls that
+ * overlap on one GPU share the scratch and race. */
+int dtl_symbol_ranges_static(const float *logits, size_t rows, size_t vocab, const uint32_t *symbols,
+                             size_t tail_symbols, uint64_t *cum, uint32_t *freq, uint64_t *total,
+                             int *status_bits, void *stream);
+/* The dtl_status a device status word of dtl_symbol_ranges_static reports. */
+int dtl_status_from_bits(int bits);
 
 /* logits_to_cdf / logits_to_symbol_range on caller logits (host memory):
  * uploads them and runs the same device kernels (cdf.rs:47-199). */
