@@ -976,11 +976,19 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
       if (after) HIP_TRY(hipStreamWaitEvent(st, after->kv_ready[l], 0));
       const RopeIn R{s->ln->k, s->ln->v, s->rope_cos, s->rope_sin, (int)c.rope_dim, c.split_half ? 1 : 0,
                      s->kc, s->vc};
-      P.timed(st, "attention", kv_rows * KV * hd * 8.0 + (double)T * (H + 3 * KV) * hd * 4.0,
-              kv_rows * H * hd * 2.0, [&] {
+      // scores (with RoPE and the cache store), then softmax and P.V: two
+      // classes so the profiler times them apart
+      P.timed(st, "attention_scores", kv_rows * KV * hd * 4.0 + (double)T * (H + 3 * KV) * hd * 4.0,
+              kv_rows * H * hd, [&] {
                 launch_attention_dec(s->ln->q, R, (int)l, T, (int)pos0, H, KV, (int)s->n_ctx,
                                      c.attention_scale, s->ln->scores, s->ln->attn, pos_dev,
-                                     s->ln->err, st);
+                                     s->ln->err, st, 1);
+              });
+      P.timed(st, "attention_pv", kv_rows * KV * hd * 4.0 + (double)T * H * hd * 4.0, kv_rows * H * hd,
+              [&] {
+                launch_attention_dec(s->ln->q, R, (int)l, T, (int)pos0, H, KV, (int)s->n_ctx,
+                                     c.attention_scale, s->ln->scores, s->ln->attn, pos_dev,
+                                     s->ln->err, st, 2);
               });
       if (record_kv) HIP_TRY(hipEventRecord(s->ln->kv_ready[l], st));
     } else {

@@ -1417,39 +1417,48 @@ __global__ void __launch_bounds__(256) k_attn_split_scores(const float* q, RopeI
 
 // softmax_in_place (lib.rs:2361-2388) of the score row, then
 // out[d] = 0; out[d] += p_j * v_j[d] (j ascending, lib.rs:2390-2420) for
-// dimensions [16 blockIdx.x, +16).  Each thread issues its V loads (rows
-// tid / 4 + 64 i, four dimensions) before the softmax, so their latency
-// overlaps it.  The exps are also stored chain-major (element j at chain
-// j % 8, slot j / 8), so each 8-lane Z chain reads its terms four at a time;
-// the products p_j * v_j[d] are stored dimension-major, and lanes 0-15 of
-// wave 0 run the sixteen chains over them without a barrier (chain_sum_lds).
+// dimensions [16 blockIdx.x, +16).  1024 threads, so that the latency-bound
+// phases (the clamped exps, the divides) have four waves per SIMD.  Each
+// thread issues its loads first: the score row, then V as 4 x 4 blocks (four
+// rows of four dimensions), which arrive while the max runs and are stored
+// dimension-major (one float4 per row block and dimension).  The exps are
+// also stored chain-major (element j at chain j % 8, slot j / 8), so each
+// 8-lane Z chain reads its terms four at a time.  After p_j = e_j / Z the
+// products p_j * v_j[d] replace V in place (float4 by float4), and lanes 0-15
+// of wave 0 run the sixteen serial chains over them (chain_sum_lds: a
+// dependent add costs its latency, about 8.5 cycles, whatever feeds it, so
+// the products are formed beforehand by every thread).
 constexpr int kSplitMaxRows = 2048;  // positions the register staging covers
-constexpr int kSplitVPer = kSplitMaxRows / 64;
+constexpr int kPvThreads = 1024;
+constexpr int kSplitVBlocks = kSplitMaxRows / kPvThreads;  // 4-row blocks per thread
+static_assert(kPvThreads / 64 == 16 && 4 * (kPvThreads / 4) == kPvThreads, "one wave per dimension, 256 row quads");
 
 struct SplitLayout {  // LDS of k_attn_split_pv, in floats
-  int len4, zs, stride, zoff, poff, total;
+  int len4, zs, ld, zoff, voff, total;
 };
 
 __host__ __device__ inline SplitLayout split_layout(int maxlen) {
   SplitLayout L;
   L.len4 = (maxlen + 3) & ~3;
   L.zs = (((maxlen + 7) / 8 + 3) & ~3) + 4;  // chain-major row (a multiple of 4)
-  L.stride = L.len4 + 4;                       // product row
+  L.ld = L.len4 + 4;                           // V row of one dimension
   L.zoff = L.len4;
-  L.poff = L.zoff + 8 * L.zs;
-  L.total = L.poff + kSplitDims * L.stride;
+  L.voff = L.zoff + 8 * L.zs;
+  L.total = L.voff + kSplitDims * L.ld;
   return L;
 }
 
 size_t split_pv_smem(int maxlen) { return (size_t)split_layout(maxlen).total * sizeof(float); }
 
-__global__ void __launch_bounds__(256) k_attn_split_pv(const float* scores, RopeIn R, int layer,
-                                                       int pos0, int H, int KV, int n_ctx,
-                                                       int maxlen, float* out,
-                                                       const int* pos_dev, int* err) {
-  // [len4] scores -> probabilities, [8][zs] exps chain-major, [16][stride] products
+__global__ void __launch_bounds__(kPvThreads) k_attn_split_pv(const float* scores, RopeIn R, int layer,
+                                                              int pos0, int H, int KV, int n_ctx,
+                                                              int maxlen, float* out,
+                                                              const int* pos_dev, int* err) {
+  // [len4] scores -> probabilities, [8][zs] exps chain-major, [16][ld] V (then
+  // the products) by dimension
   extern __shared__ __align__(16) float pr[];
-  __shared__ float red[4];
+  constexpr int NW = kPvThreads / 64;
+  __shared__ float red[NW];
   __shared__ float zc[8];
   constexpr int hd = 64;
   const int dg = blockIdx.x, h = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
@@ -1460,7 +1469,7 @@ __global__ void __launch_bounds__(256) k_attn_split_pv(const float* scores, Rope
   const int d0 = dg * kSplitDims;
   const SplitLayout L = split_layout(maxlen);
   float* zcm = pr + L.zoff;
-  float* prod = pr + L.poff;
+  float* vt = pr + L.voff;
   const float* vals = R.vc + ((size_t)layer * KV + g) * n_ctx * hd;
   // chunk rows (j >= pb) come from the raw projection, never from the cache
   auto vrow = [&](int j) -> const float* {
@@ -1472,29 +1481,30 @@ __global__ void __launch_bounds__(256) k_attn_split_pv(const float* scores, Rope
     if (tid < kSplitDims) o[tid] = vrow(0)[d0 + tid];
     return;
   }
-  // The score row is loaded first (the max needs it at once), the V rows
-  // right after, so they arrive while the softmax runs.
+  // Every load is unconditional (indices past len re-read a valid entry), so
+  // the wait before the max counts the V loads still in flight instead of
+  // draining them.
   const float* srow = scores + ((size_t)t * H + h) * n_ctx;
-  // Every load is unconditional (indices past len re-read a valid entry),
-  // so the wait before the max counts the V loads still in flight instead
-  // of draining them.
-  float sv[kSplitMaxRows / 256];
+  float sv[kSplitMaxRows / kPvThreads];
 #pragma unroll
-  for (int k = 0; k < kSplitMaxRows / 256; k++) {
-    const int j = 256 * k + tid;
+  for (int k = 0; k < kSplitMaxRows / kPvThreads; k++) {
+    const int j = kPvThreads * k + tid;
     sv[k] = srow[j < len ? j : 0];
   }
-  const int jr = tid >> 2, c = 4 * (tid & 3);
-  float4 vreg[kSplitVPer];
+  // V block i of this thread: rows 4 (256 i + jq) .. +3, dimensions d0 + c .. +3
+  const int jq = tid >> 2, c = 4 * (tid & 3);
+  float4 vb[kSplitVBlocks][4];
 #pragma unroll
-  for (int i = 0; i < kSplitVPer; i++) {
-    const int j = 64 * i + jr;
-    vreg[i] = *reinterpret_cast<const float4*>(vrow(j < len ? j : len - 1) + d0 + c);
-  }
+  for (int i = 0; i < kSplitVBlocks; i++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int j = 4 * (256 * i + jq) + r;
+      vb[i][r] = *reinterpret_cast<const float4*>(vrow(j < len ? j : len - 1) + d0 + c);
+    }
   float mx = -__builtin_huge_valf();
 #pragma unroll
-  for (int k = 0; k < kSplitMaxRows / 256; k++) {
-    const int j = 256 * k + tid;
+  for (int k = 0; k < kSplitMaxRows / kPvThreads; k++) {
+    const int j = kPvThreads * k + tid;
     if (j < len) {
       pr[j] = sv[k];
       mx = fmaxf(mx, sv[k]);
@@ -1502,19 +1512,36 @@ __global__ void __launch_bounds__(256) k_attn_split_pv(const float* scores, Rope
   }
   for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
   if (lane == 0) red[wave] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  // eight independent exps per thread at a time
-  for (int j0 = 0; j0 < len; j0 += 8 * 256) {
-    float e[8];
+  // V, dimension-major: each 4 x 4 block transposed in registers, one float4
+  // per dimension (rows past len are stored too; no chain reads them)
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const int j = j0 + tid + 256 * k;
+  for (int i = 0; i < kSplitVBlocks; i++) {
+    const int j4 = 4 * (256 * i + jq);
+    if (j4 < len) {
+      *reinterpret_cast<float4*>(vt + (c + 0) * L.ld + j4) =
+          make_float4(vb[i][0].x, vb[i][1].x, vb[i][2].x, vb[i][3].x);
+      *reinterpret_cast<float4*>(vt + (c + 1) * L.ld + j4) =
+          make_float4(vb[i][0].y, vb[i][1].y, vb[i][2].y, vb[i][3].y);
+      *reinterpret_cast<float4*>(vt + (c + 2) * L.ld + j4) =
+          make_float4(vb[i][0].z, vb[i][1].z, vb[i][2].z, vb[i][3].z);
+      *reinterpret_cast<float4*>(vt + (c + 3) * L.ld + j4) =
+          make_float4(vb[i][0].w, vb[i][1].w, vb[i][2].w, vb[i][3].w);
+    }
+  }
+  __syncthreads();
+  mx = red[0];
+#pragma unroll
+  for (int w = 1; w < NW; w++) mx = fmaxf(mx, red[w]);
+  {
+    float e[kSplitMaxRows / kPvThreads];
+#pragma unroll
+    for (int k = 0; k < kSplitMaxRows / kPvThreads; k++) {
+      const int j = tid + kPvThreads * k;
       e[k] = j < len ? exp_clamped(pr[j < len ? j : 0] - mx) : 0.0f;
     }
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const int j = j0 + tid + 256 * k;
+    for (int k = 0; k < kSplitMaxRows / kPvThreads; k++) {
+      const int j = tid + kPvThreads * k;
       if (j < len) {
         pr[j] = e[k];
         zcm[(j & 7) * L.zs + (j >> 3)] = e[k];
@@ -1529,27 +1556,26 @@ __global__ void __launch_bounds__(256) k_attn_split_pv(const float* scores, Rope
   __syncthreads();
   const float z = finish_8lane(zc);
   bad |= !finite(z) || z == 0.0f;
-  for (int j = tid; j < len; j += 256) {
+  for (int j = tid; j < len; j += kPvThreads) {
     const float p = pr[j] / z;
     bad |= !finite(p);
     pr[j] = p;
   }
   __syncthreads();
-  // Products, dimension-major.
-#pragma unroll
-  for (int i = 0; i < kSplitVPer; i++) {
-    const int j = 64 * i + jr;
-    if (j < len) {
-      const float p = pr[j];
-      prod[(c + 0) * L.stride + j] = p * vreg[i].x;
-      prod[(c + 1) * L.stride + j] = p * vreg[i].y;
-      prod[(c + 2) * L.stride + j] = p * vreg[i].z;
-      prod[(c + 3) * L.stride + j] = p * vreg[i].w;
+  // products p_j * v_j[d], in place, a float4 (four j of one d) at a time:
+  // 64 threads per dimension
+  {
+    const int d = tid >> 6;
+    float* vd = vt + d * L.ld;
+    for (int j4 = 4 * lane; j4 < len; j4 += 256) {
+      const float4 pv = *reinterpret_cast<const float4*>(pr + j4);
+      const float4 vv = *reinterpret_cast<const float4*>(vd + j4);
+      *reinterpret_cast<float4*>(vd + j4) = make_float4(pv.x * vv.x, pv.y * vv.y, pv.z * vv.z, pv.w * vv.w);
     }
   }
   __syncthreads();
   if (wave == 0 && lane < kSplitDims) {
-    const float a = chain_sum_lds(0.0f, prod + lane * L.stride, len);
+    const float a = chain_sum_lds(0.0f, vt + lane * L.ld, len);
     bad |= !finite(a);
     o[lane] = a;
   }
@@ -1580,7 +1606,7 @@ bool attention_dec_applies(int hd, int T, int pos0, int n_ctx, bool pos_in_devic
 
 void launch_attention_dec(const float* q, const RopeIn& R, int layer, int T, int pos0, int H,
                           int KV, int n_ctx, float scale, float* scores, float* out,
-                          const int* pos_dev, int* err, hipStream_t s) {
+                          const int* pos_dev, int* err, hipStream_t s, int part) {
   // With the position in device memory the grids and the score buffer are
   // sized for the whole window.
   const int maxlen = pos_dev ? n_ctx : pos0 + T;
@@ -1593,10 +1619,12 @@ void launch_attention_dec(const float* q, const RopeIn& R, int layer, int T, int
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 158 * 1024);
       attr_pv_set = true;
     }
-    launch_kernel(k_attn_split_scores, dim3((maxlen + kSplitKeys - 1) / kSplitKeys, H, T), dim3(256),
-                  0, s, q, R, layer, pos0, H, KV, n_ctx, scale, scores, pos_dev, err);
-    launch_kernel(k_attn_split_pv, dim3(64 / kSplitDims, H, T), dim3(256), pv_smem, s, scores, R,
-                  layer, pos0, H, KV, n_ctx, maxlen, out, pos_dev, err);
+    if (part != 2)
+      launch_kernel(k_attn_split_scores, dim3((maxlen + kSplitKeys - 1) / kSplitKeys, H, T),
+                    dim3(256), 0, s, q, R, layer, pos0, H, KV, n_ctx, scale, scores, pos_dev, err);
+    if (part != 1)
+      launch_kernel(k_attn_split_pv, dim3(64 / kSplitDims, H, T), dim3(kPvThreads), pv_smem, s, scores, R,
+                    layer, pos0, H, KV, n_ctx, maxlen, out, pos_dev, err);
     return;
   }
   // Longer windows: one workgroup per (head, position).
@@ -1606,8 +1634,9 @@ void launch_attention_dec(const float* q, const RopeIn& R, int layer, int T, int
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDecMaxScoreBytes);
     attr_dec_set = true;
   }
-  launch_kernel(k_attention_dec, dim3(H, T), dim3(kDecThreads), smem, s, q, R, layer, pos0, H, KV,
-                n_ctx, scale, out, pos_dev, err);
+  if (part != 1)
+    launch_kernel(k_attention_dec, dim3(H, T), dim3(kDecThreads), smem, s, q, R, layer, pos0, H, KV,
+                  n_ctx, scale, out, pos_dev, err);
 }
 
 bool attention_quantizes_q8a(int hd, int H, int KV, int T, int pos0, int n_ctx) {

@@ -176,6 +176,77 @@ __device__ __forceinline__ float chain_sum_lds(float a, const float* v, int n) {
   return a;
 }
 
+// a += p[j] * v[j] for j = 0 .. n-1 in order, each product rounded and
+// added on its own (the P.V chain, det-model lib.rs:2390-2420), with both
+// operand rows in LDS (16-byte aligned).  Software-pipelined in blocks of 16
+// elements: the products of block b + 1 are formed (independent multiplies)
+// and the operands of block b + 3 read before the 16 dependent adds of block
+// b, so neither the LDS latency nor the multiplies sit on the chain.
+// Operands (four float4 of each row) of one block of 16 elements.
+struct ChainOps16 {
+  float4 p[4], v[4];
+};
+
+__device__ __forceinline__ void chain_load16(ChainOps16& o, const float4* __restrict__ p4,
+                                             const float4* __restrict__ v4, int b) {
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    o.p[k] = p4[4 * b + k];
+    o.v[k] = v4[4 * b + k];
+  }
+}
+
+__device__ __forceinline__ void chain_mul16(float (&d)[16], const ChainOps16& o) {
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    d[4 * k + 0] = o.p[k].x * o.v[k].x;
+    d[4 * k + 1] = o.p[k].y * o.v[k].y;
+    d[4 * k + 2] = o.p[k].z * o.v[k].z;
+    d[4 * k + 3] = o.p[k].w * o.v[k].w;
+  }
+}
+
+__device__ __forceinline__ float chain_dot_lds(float a, const float4* __restrict__ p4,
+                                               const float4* __restrict__ v4, int n) {
+  const int nb = n >> 4;  // blocks of 16
+  int b = 0;
+  if (nb >= 4) {
+    // Operands are read two blocks ahead of their multiplies and products
+    // one block ahead of their adds; loads past the last block re-read it.
+    const int last = nb - 1;
+    ChainOps16 A, B;
+    float x[16], y[16];
+    chain_load16(A, p4, v4, 0);
+    chain_load16(B, p4, v4, 1);
+    chain_mul16(x, A);                 // block 0
+    chain_load16(A, p4, v4, 2);
+    for (; b + 4 <= nb; b += 2) {
+      // x: products of block b; B: operands of b + 1; A: operands of b + 2
+      chain_mul16(y, B);               // block b + 1
+      chain_load16(B, p4, v4, b + 3 < last ? b + 3 : last);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 16; i++) a += x[i];
+      chain_mul16(x, A);               // block b + 2
+      chain_load16(A, p4, v4, b + 4 < last ? b + 4 : last);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 16; i++) a += y[i];
+    }
+    // x: products of block b; B: operands of b + 1 (b + 1 < nb)
+#pragma unroll
+    for (int i = 0; i < 16; i++) a += x[i];
+    chain_mul16(y, B);
+#pragma unroll
+    for (int i = 0; i < 16; i++) a += y[i];
+    b += 2;
+  }
+  const float* p = reinterpret_cast<const float*>(p4);
+  const float* v = reinterpret_cast<const float*>(v4);
+  for (int i = 16 * b; i < n; i++) a += p[i] * v[i];
+  return a;
+}
+
 // silu_f32 (det-num math.rs:30-34).
 __device__ __forceinline__ float silu_det(float x) {
   float t = expf_det(-x);
