@@ -329,11 +329,8 @@ __global__ void __launch_bounds__(256) k_q8_0_tok(DevMat W, const int8_t* __rest
 
 // ---------------------------------------------------------------------------
 // Q4_K from an exact f32 copy of the weights (the values q4_k_value yields,
-// det-quant lib.rs:506-517, computed once at load).  Lanes = positions, NK
-// rows per wave; the workgroup stages each 64-element activation slice of
-// its 64 positions in LDS once for its four waves, and each wave stages its
-// own weight rows there too (read back as broadcasts); both are
-// double-buffered with the next slice's global loads in flight.
+// det-quant lib.rs:506-517, computed once at load), every output one chain
+// of products in element order:
 //   MODE_SINGLE  one matrix
 //   MODE_PAIR    gate and up (same shape): silu(gate)*up (det-model
 //                lib.rs:2420-2434) written in the epilogue
@@ -356,162 +353,32 @@ struct Q4kF32Args {
   int* err;
 };
 
-template <int NK, int MODE>
-__global__ void __launch_bounds__(256) k_q4k_f32w(Q4kF32Args p) {
-  constexpr int NM = MODE == MODE_PAIR ? 2 : 1;
-  constexpr int SL = 64;        // elements per slice
-  constexpr int LD = SL + 4;    // padded LDS row (floats)
-  __shared__ __align__(16) float at[2][64][LD];
-  __shared__ __align__(16) float wt[2][kWaves][NM * NK][SL];
-  const int cols = p.cols, T = p.T;
-  const int rows_total = MODE == MODE_CAT ? p.rows0 + p.rows1 : p.rows0;
-  const float* __restrict__ af = p.af;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int row0 = (blockIdx.x * kWaves + wave) * NK;
-  const int tbase = blockIdx.y * 64;
-  const int t = tbase + lane;
-  float acc[NM * NK];
-#pragma unroll
-  for (int k = 0; k < NM * NK; k++) acc[k] = 0.0f;
-
-  // Each thread moves four float4 of every 64x64 activation tile: the global
-  // loads for the next tile are issued before the current tile is consumed
-  // and written to LDS only afterwards, so their latency overlaps the math.
-  // Float4 j of thread x covers position (x + 256 j) / 16, column 4 ((x + 256 j) % 16).
-  constexpr int PER = 64 * SL / 4 / 256;
-  static_assert(PER == 4, "tile mapping assumes 4 float4 per thread");
-  const int tk0 = threadIdx.x >> 4, c40 = threadIdx.x & 15;
-  const float* asrc[PER];
-#pragma unroll
-  for (int j = 0; j < PER; j++) {
-    int tt = tbase + tk0 + 16 * j;
-    asrc[j] = af + (size_t)(tt < T ? tt : T - 1) * cols + c40 * 4;
-  }
-  float4 p0, p1, p2, p3;
-#define DTL_ISSUE(e0)                                          \
-  do {                                                         \
-    p0 = *(const float4*)(asrc[0] + (e0));                     \
-    p1 = *(const float4*)(asrc[1] + (e0));                     \
-    p2 = *(const float4*)(asrc[2] + (e0));                     \
-    p3 = *(const float4*)(asrc[3] + (e0));                     \
-  } while (0)
-#define DTL_COMMIT(b)                                          \
-  do {                                                         \
-    *(float4*)&at[b][tk0][c40 * 4] = p0;                       \
-    *(float4*)&at[b][tk0 + 16][c40 * 4] = p1;                  \
-    *(float4*)&at[b][tk0 + 32][c40 * 4] = p2;                  \
-    *(float4*)&at[b][tk0 + 48][c40 * 4] = p3;                  \
-  } while (0)
-  // The wave's own weight rows go through LDS the same way (lane -> one
-  // float4 of one row) and are read back as broadcasts.
-  const int wk = lane >> 4, wc4 = lane & 15;
-  const bool wlane = wk < NM * NK;
-  const float* wsrc = p.w0;
-  if (wlane) {
-    if (MODE == MODE_PAIR) {
-      int m = wk / NK, kk = wk % NK;
-      int row = row0 + kk < p.rows0 ? row0 + kk : p.rows0 - 1;
-      wsrc = (m ? p.w1 : p.w0) + (size_t)row * cols + wc4 * 4;
-    } else {
-      int g = row0 + wk < rows_total ? row0 + wk : rows_total - 1;
-      bool m = MODE == MODE_CAT && g >= p.rows0;
-      wsrc = (m ? p.w1 : p.w0) + (size_t)(m ? g - p.rows0 : g) * cols + wc4 * 4;
-    }
-  }
-  float4 wpre = make_float4(0.f, 0.f, 0.f, 0.f);
-#define DTL_ISSUE_W(e0)                                        \
-  do {                                                         \
-    if (wlane) wpre = *(const float4*)(wsrc + (e0));           \
-  } while (0)
-#define DTL_COMMIT_W(b)                                        \
-  do {                                                         \
-    if (wlane) *(float4*)&wt[b][wave][wk][wc4 * 4] = wpre;     \
-  } while (0)
-  DTL_ISSUE(0);
-  DTL_ISSUE_W(0);
-  DTL_COMMIT(0);
-  DTL_COMMIT_W(0);
-  __syncthreads();
-  int buf = 0;
-  for (int e0 = 0; e0 < cols; e0 += SL) {
-    const bool more = e0 + SL < cols;
-    if (more) {
-      DTL_ISSUE(e0 + SL);
-      DTL_ISSUE_W(e0 + SL);
-    }
-#pragma unroll 4
-    for (int i = 0; i < SL; i += 4) {
-      float4 a = *(const float4*)&at[buf][lane][i];
-#pragma unroll
-      for (int k = 0; k < NM * NK; k++) {
-        float4 w = *(const float4*)&wt[buf][wave][k][i];
-        float c = acc[k];
-        c += w.x * a.x;
-        c += w.y * a.y;
-        c += w.z * a.z;
-        c += w.w * a.w;
-        acc[k] = c;
-      }
-    }
-    if (more) {
-      DTL_COMMIT(buf ^ 1);
-      DTL_COMMIT_W(buf ^ 1);
-    }
-    __syncthreads();
-    buf ^= 1;
-  }
-  if (t >= T) return;
-  bool ok = true;
-#pragma unroll
-  for (int k = 0; k < NK; k++) {
-    const int g = row0 + k;
-    if (g >= rows_total) continue;
-    if (MODE == MODE_PAIR) {
-      size_t o = (size_t)t * p.rows0 + g;
-      float gv = acc[k], uv = acc[NK + k];
-      float v = silu_det(gv) * uv;
-      ok &= finite(gv) && finite(uv) && finite(v);
-      p.ffo[o] = v;
-    } else {
-      const bool m = MODE == MODE_CAT && g >= p.rows0;
-      const int local = m ? g - p.rows0 : g;
-      const int R = m ? p.rows1 : p.rows0;
-      ok &= store_epilogue(acc[k], m ? p.out1 : p.out0, (size_t)t * R + local,
-                           m ? p.bias1 : p.bias0, local, p.epi);
-    }
-  }
-  if (!ok) flag(p.err, ERRBIT_NON_FINITE);
-}
-
-#undef DTL_ISSUE
-#undef DTL_COMMIT
-#undef DTL_ISSUE_W
-#undef DTL_COMMIT_W
-
-// The same product with the lanes of a wave split over rows and positions:
-// lane = (position p = lane % PW, row r = lane / PW), RW = 64 / PW rows per
-// wave.  A workgroup is WP x WR waves covering PB = WP * PW positions of
-// RB = WR * RW rows; it stages each 64-element slice of those positions'
-// activations and rows' weights in LDS once (double-buffered, the next
-// slice's global loads in flight) and every lane walks one chain per matrix
-// in element order.  Lanes of one position (or one row) read the same LDS
-// address, so per four elements a wave reads PW activation and RW weight
-// float4 instead of 64 and one: with one chain per lane the activation reads
-// of the one-row-per-wave mapping ask the LDS for as many bytes per cycle as
-// it delivers.
-template <int PW, int WP, int WR, int MODE>
+// The lanes of a wave are split over positions and rows, and each lane
+// holds a PP x RP block of chains: lane = (p = lane % PW, r = lane / PW),
+// RW = 64 / PW; the lane's positions are p + PW i (i < PP) and its rows
+// r + RW j (j < RP) of each matrix, one chain per (position, row, matrix),
+// every chain in element order.  A wave covers PW PP positions of RW RP
+// rows; a workgroup is WP x WR waves covering PB positions of RB rows and
+// stages each 64-element slice of those positions' activations and rows'
+// weights in LDS once (double-buffered, the next slice's global loads in
+// flight).  Per four elements a lane reads PP activation and NM RP weight
+// float4 for NM PP RP chains: the blocking divides the LDS bytes per
+// multiply-add, which bound the one-chain mapping, by the block's size
+// over its perimeter.
+template <int PW, int PP, int RP, int WP, int WR, int MODE>
 __global__ void __launch_bounds__(64 * WP * WR) k_q4k_f32m(Q4kF32Args p) {
   constexpr int NT = 64 * WP * WR;
   constexpr int NM = MODE == MODE_PAIR ? 2 : 1;
   constexpr int RW = 64 / PW;
-  constexpr int PB = WP * PW;            // positions per workgroup
-  constexpr int RB = WR * RW;            // rows per workgroup (of each matrix)
-  constexpr int NR = PB + NM * RB;       // staged LDS rows per slice
-  constexpr int SL = 64, LD = SL + 4;    // elements per slice, padded LDS row
-  constexpr int F = NR * SL / 4;         // float4 per slice
+  constexpr int PWV = PW * PP, RWV = RW * RP;  // positions, rows per wave
+  constexpr int PB = WP * PWV;                 // positions per workgroup
+  constexpr int RB = WR * RWV;                 // rows per workgroup (of each matrix)
+  constexpr int NR = PB + NM * RB;             // staged LDS rows per slice
+  constexpr int SL = 64, LD = SL + 4;          // elements per slice, padded LDS row
+  constexpr int F = NR * SL / 4;               // float4 per slice
   constexpr int PERT = (F + NT - 1) / NT;
-  static_assert(PERT >= 1 && PERT <= 4, "staging slots per thread");
+  static_assert(PERT >= 1 && PERT <= 8, "staging slots per thread");
+  static_assert(2 * NR * LD * 4 <= 64 * 1024, "LDS tile");
   __shared__ __align__(16) float st[2][NR][LD];
   const int cols = p.cols, T = p.T;
   const int rows_total = MODE == MODE_CAT ? p.rows0 + p.rows1 : p.rows0;
@@ -519,12 +386,15 @@ __global__ void __launch_bounds__(64 * WP * WR) k_q4k_f32m(Q4kF32Args p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wp = wave % WP, wr = wave / WP;
   const int pl = lane % PW, rl = lane / PW;
-  const int t = blockIdx.y * PB + wp * PW + pl;
-  const int rloc = wr * RW + rl;
-  const int g = blockIdx.x * RB + rloc;  // this lane's row (of the concatenation)
-  float acc[NM];
+  const int prow = wp * PWV + pl;   // LDS row of position i: prow + PW i
+  const int rrow = wr * RWV + rl;   // workgroup row of row j: rrow + RW j
+  float acc[NM][PP][RP];
 #pragma unroll
-  for (int m = 0; m < NM; m++) acc[m] = 0.0f;
+  for (int m = 0; m < NM; m++)
+#pragma unroll
+    for (int i = 0; i < PP; i++)
+#pragma unroll
+      for (int j = 0; j < RP; j++) acc[m][i][j] = 0.0f;
 
   // Staging slot k of thread x moves float4 f = x + k NT of the slice: LDS
   // row f / 16 (activations of position f / 16 first, then the weight rows,
@@ -547,30 +417,39 @@ __global__ void __launch_bounds__(64 * WP * WR) k_q4k_f32m(Q4kF32Args p) {
     const bool m = MODE == MODE_CAT && gg >= p.rows0;
     return (m ? p.w1 : p.w0) + (size_t)(m ? gg - p.rows0 : gg) * cols + c4 * 4;
   };
+  // Up to eight slots as named registers (an indexed array of them is not
+  // kept in registers by the compiler across the conditional load/store).
   const int x = threadIdx.x;
-  const float* s0 = slot_src(x);
-  const float* s1 = slot_src(x + NT);
-  const float* s2 = slot_src(x + 2 * NT);
-  const float* s3 = slot_src(x + 3 * NT);
-  auto slot_dst = [&](int f) { return (f >> 4) * LD + (f & 15) * 4; };
-  const int d0 = slot_dst(x), d1 = slot_dst(x + NT), d2 = slot_dst(x + 2 * NT),
-            d3 = slot_dst(x + 3 * NT);
-  const bool k0 = x < F, k1 = x + NT < F, k2 = x + 2 * NT < F, k3 = x + 3 * NT < F;
-  float4 q0, q1, q2, q3;
+#define DTL_SLOT_DECL(n)                                                      \
+  const float* s##n = slot_src(x + (n) * NT);                                 \
+  const int d##n = ((x + (n) * NT) >> 4) * LD + ((x + (n) * NT) & 15) * 4;    \
+  const bool k##n = x + (n) * NT < F;                                         \
+  float4 q##n;
+  DTL_SLOT_DECL(0) DTL_SLOT_DECL(1) DTL_SLOT_DECL(2) DTL_SLOT_DECL(3)
+  DTL_SLOT_DECL(4) DTL_SLOT_DECL(5) DTL_SLOT_DECL(6) DTL_SLOT_DECL(7)
+#undef DTL_SLOT_DECL
 #define DTL_ISSUE_M(e0)                                                       \
   do {                                                                        \
     q0 = *(const float4*)(s0 + (e0));                                         \
     if (PERT > 1) q1 = *(const float4*)(s1 + (e0));                           \
     if (PERT > 2) q2 = *(const float4*)(s2 + (e0));                           \
     if (PERT > 3) q3 = *(const float4*)(s3 + (e0));                           \
+    if (PERT > 4) q4 = *(const float4*)(s4 + (e0));                           \
+    if (PERT > 5) q5 = *(const float4*)(s5 + (e0));                           \
+    if (PERT > 6) q6 = *(const float4*)(s6 + (e0));                           \
+    if (PERT > 7) q7 = *(const float4*)(s7 + (e0));                           \
   } while (0)
 #define DTL_COMMIT_M(b)                                                       \
   do {                                                                        \
-    float* sb = &st[b][0][0];                                                 \
-    if (k0) *(float4*)(sb + d0) = q0;                                         \
-    if (PERT > 1 && k1) *(float4*)(sb + d1) = q1;                             \
-    if (PERT > 2 && k2) *(float4*)(sb + d2) = q2;                             \
-    if (PERT > 3 && k3) *(float4*)(sb + d3) = q3;                             \
+    float* sb_ = &st[b][0][0];                                                \
+    if (k0) *(float4*)(sb_ + d0) = q0;                                        \
+    if (PERT > 1 && k1) *(float4*)(sb_ + d1) = q1;                            \
+    if (PERT > 2 && k2) *(float4*)(sb_ + d2) = q2;                            \
+    if (PERT > 3 && k3) *(float4*)(sb_ + d3) = q3;                            \
+    if (PERT > 4 && k4) *(float4*)(sb_ + d4) = q4;                            \
+    if (PERT > 5 && k5) *(float4*)(sb_ + d5) = q5;                            \
+    if (PERT > 6 && k6) *(float4*)(sb_ + d6) = q6;                            \
+    if (PERT > 7 && k7) *(float4*)(sb_ + d7) = q7;                            \
   } while (0)
   DTL_ISSUE_M(0);
   DTL_COMMIT_M(0);
@@ -579,20 +458,30 @@ __global__ void __launch_bounds__(64 * WP * WR) k_q4k_f32m(Q4kF32Args p) {
   for (int e0 = 0; e0 < cols; e0 += SL) {
     const bool more = e0 + SL < cols;
     if (more) DTL_ISSUE_M(e0 + SL);
-    const float* ar = &st[buf][wp * PW + pl][0];
+    const float* sb = &st[buf][0][0];
 #pragma unroll 4
-    for (int i = 0; i < SL; i += 4) {
-      const float4 a = *(const float4*)(ar + i);
+    for (int e = 0; e < SL; e += 4) {
+      float4 a[PP], w[NM][RP];
 #pragma unroll
-      for (int m = 0; m < NM; m++) {
-        const float4 w = *(const float4*)&st[buf][PB + m * RB + rloc][i];
-        float c = acc[m];
-        c += w.x * a.x;
-        c += w.y * a.y;
-        c += w.z * a.z;
-        c += w.w * a.w;
-        acc[m] = c;
-      }
+      for (int i = 0; i < PP; i++) a[i] = *(const float4*)(sb + (prow + PW * i) * LD + e);
+#pragma unroll
+      for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int j = 0; j < RP; j++)
+          w[m][j] = *(const float4*)(sb + (PB + m * RB + rrow + RW * j) * LD + e);
+#pragma unroll
+      for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int i = 0; i < PP; i++)
+#pragma unroll
+          for (int j = 0; j < RP; j++) {
+            float c = acc[m][i][j];
+            c += w[m][j].x * a[i].x;
+            c += w[m][j].y * a[i].y;
+            c += w[m][j].z * a[i].z;
+            c += w[m][j].w * a[i].w;
+            acc[m][i][j] = c;
+          }
     }
     if (more) DTL_COMMIT_M(buf ^ 1);
     __syncthreads();
@@ -600,19 +489,28 @@ __global__ void __launch_bounds__(64 * WP * WR) k_q4k_f32m(Q4kF32Args p) {
   }
 #undef DTL_ISSUE_M
 #undef DTL_COMMIT_M
-  if (t >= T || g >= rows_total) return;
   bool ok = true;
-  if (MODE == MODE_PAIR) {
-    const float gv = acc[0], uv = acc[NM - 1];
-    const float v = silu_det(gv) * uv;
-    ok = finite(gv) && finite(uv) && finite(v);
-    p.ffo[(size_t)t * p.rows0 + g] = v;
-  } else {
-    const bool m = MODE == MODE_CAT && g >= p.rows0;
-    const int local = m ? g - p.rows0 : g;
-    const int R = m ? p.rows1 : p.rows0;
-    ok = store_epilogue(acc[0], m ? p.out1 : p.out0, (size_t)t * R + local, m ? p.bias1 : p.bias0,
-                        local, p.epi);
+#pragma unroll
+  for (int i = 0; i < PP; i++) {
+    const int t = blockIdx.y * PB + prow + PW * i;
+    if (t >= T) continue;
+#pragma unroll
+    for (int j = 0; j < RP; j++) {
+      const int g = blockIdx.x * RB + rrow + RW * j;  // row of the concatenation
+      if (g >= rows_total) continue;
+      if (MODE == MODE_PAIR) {
+        const float gv = acc[0][i][j], uv = acc[NM - 1][i][j];
+        const float v = silu_det(gv) * uv;
+        ok &= finite(gv) && finite(uv) && finite(v);
+        p.ffo[(size_t)t * p.rows0 + g] = v;
+      } else {
+        const bool m = MODE == MODE_CAT && g >= p.rows0;
+        const int local = m ? g - p.rows0 : g;
+        const int R = m ? p.rows1 : p.rows0;
+        ok &= store_epilogue(acc[0][i][j], m ? p.out1 : p.out0, (size_t)t * R + local,
+                             m ? p.bias1 : p.bias0, local, p.epi);
+      }
+    }
   }
   if (!ok) flag(p.err, ERRBIT_NON_FINITE);
 }
@@ -969,54 +867,31 @@ int rows_per_wave(int rows) {
   return 1;
 }
 
-// Rows per wave for the f32-weight Q4_K kernel: one row per wave keeps two
-// waves per SIMD on 2k-row single matrices at 64 positions (measured
-// fastest for wo and ffn_down); the gate/up pair, the concatenated wq+wk and
-// very tall matrices run faster amortising each activation read over two
-// rows.
-int q4k_nk(int mode, int rows_total) {
-  if (mode == MODE_PAIR || mode == MODE_CAT) return 2;
-  return rows_total >= 8192 ? 2 : 1;
-}
-
-// Tile of the split mapping as PW * 100 + WP * 10 + WR (0: k_q4k_f32w), per
-// mode.  Measured at 64 positions on the 2048-column TinyLlama shapes:
-// single matrices (wo, 2048 x 2048, and ffn_down, 2048 x 5632) 26% faster
-// with 8 positions x 8 rows per wave and 2 x 4 waves, the wq+wk
-// concatenation 14% faster with 2 x 2 waves; the gate/up pair (two chains
-// per lane at 16 positions x 4 rows, or four in k_q4k_f32w) runs at the same
-// rate either way and keeps k_q4k_f32w, which overlapped better with the
-// other chunks in flight.
-int q4k_map(int mode) {
-  static constexpr int kMap[3] = {842, 0, 822};  // single, pair, cat
-  return kMap[mode];
-}
-
-template <int PW, int WP, int WR, int MODE>
+// Tiles of the blocked Q4_K kernel (k_q4k_f32m<PW, PP, RP, WP, WR>), chosen
+// on the pipelined TinyLlama encode (64 positions, four chunks in flight):
+//   single (wo, ffn_down)  8 positions x 8 rows of lanes, 1 x 2 chains per
+//                          lane, 4 waves over 32 positions x 16 rows
+//   pair   (gate + up)     4 x 16 lanes, 2 positions x (gate, up) per lane,
+//                          4 waves over 32 positions x 16 rows
+//   cat    (wq + wk)       8 x 8 lanes, 1 x 2 chains, 2 x 2 waves
+// Blocked lanes run fewer waves than one chain per lane: alone, a chunk's
+// launch is up to 45% slower (wo/ffn_down 58 vs 40 ms per step at one
+// chain per lane), but with the other chunks' launches filling the CUs the
+// step is 10% faster (123.7 vs 137.6 ms), the LDS bytes per multiply-add
+// being what bounds the overlapped launches.
+template <int PW, int PP, int RP, int WP, int WR, int MODE>
 void launch_q4k_f32m(const Q4kF32Args& a, int rows_total, hipStream_t s) {
-  constexpr int RB = WR * 64 / PW, PB = WP * PW;
+  constexpr int RB = WR * RP * 64 / PW, PB = WP * PW * PP;
   dim3 grid((rows_total + RB - 1) / RB, (a.T + PB - 1) / PB);
-  launch_kernel(k_q4k_f32m<PW, WP, WR, MODE>, grid, dim3(64 * WP * WR), 0, s, a);
+  launch_kernel(k_q4k_f32m<PW, PP, RP, WP, WR, MODE>, grid, dim3(64 * WP * WR), 0, s, a);
 }
 
 template <int MODE>
 void launch_q4k_f32w(const Q4kF32Args& a, hipStream_t s) {
   const int rows_total = MODE == MODE_CAT ? a.rows0 + a.rows1 : a.rows0;
-  switch (q4k_map(MODE)) {
-    case 841: return launch_q4k_f32m<8, 4, 1, MODE>(a, rows_total, s);
-    case 822: return launch_q4k_f32m<8, 2, 2, MODE>(a, rows_total, s);
-    case 842: return launch_q4k_f32m<8, 4, 2, MODE>(a, rows_total, s);
-    case 1642: return launch_q4k_f32m<16, 4, 2, MODE>(a, rows_total, s);
-    case 1622: return launch_q4k_f32m<16, 2, 2, MODE>(a, rows_total, s);
-    default: break;
-  }
-  const int nk = q4k_nk(MODE, rows_total);
-  dim3 grid((rows_total + kWaves * nk - 1) / (kWaves * nk), (a.T + 63) / 64);
-  dim3 block(kWaves * 64);
-  if (nk == 2)
-    launch_kernel(k_q4k_f32w<2, MODE>, grid, block, 0, s, a);
-  else
-    launch_kernel(k_q4k_f32w<1, MODE>, grid, block, 0, s, a);
+  if (MODE == MODE_SINGLE) return launch_q4k_f32m<8, 1, 2, 4, 1, MODE>(a, rows_total, s);
+  if (MODE == MODE_PAIR) return launch_q4k_f32m<4, 2, 1, 4, 1, MODE>(a, rows_total, s);
+  launch_q4k_f32m<8, 1, 2, 2, 2, MODE>(a, rows_total, s);
 }
 
 Q4kF32Args q4k_args(const DevMat& W0, const DevMat* W1, const DevAct& A, int T, float* out0,
