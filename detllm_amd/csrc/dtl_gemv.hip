@@ -27,6 +27,24 @@ namespace dtl {
 
 namespace {
 
+// Q4_K 6-bit scale and min of sub-block j (det-quant lib.rs:519-529) from
+// the 12 packed bytes held as three little-endian words; the words are
+// selected, not indexed, so that they stay in registers.
+__device__ __forceinline__ void q4k_scale_min3(uint32_t s0, uint32_t s1, uint32_t s2, int j, int* sc,
+                                               int* mn) {
+  auto byte = [&](int i) -> uint32_t {
+    const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
+    return (w >> (8 * (i & 3))) & 0xffu;
+  };
+  if (j < 4) {
+    *sc = (int)(byte(j) & 0x3f);
+    *mn = (int)(byte(j + 4) & 0x3f);
+  } else {
+    *sc = (int)((byte(j + 4) & 0x0f) | ((byte(j - 4) >> 6) << 4));
+    *mn = (int)((byte(j + 4) >> 4) | ((byte(j) >> 6) << 4));
+  }
+}
+
 constexpr int kGgmlQ4_0 = 2, kGgmlQ8_0 = 8, kGgmlQ4K = 12, kGgmlQ6K = 14;
 
 __device__ __forceinline__ void flag(int* err, int bit) { atomicOr(err, bit); }
@@ -614,15 +632,19 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
 }  // namespace
 
 // Q4_K decode with the products and the chains on different lanes.  A
-// workgroup of four waves owns RB rows.  Every thread streams its share of
-// the weight rows through an NS-deep register ring (one SL-column stage per
-// slot, loads issued unconditionally), multiplies them by the activations
-// (all T positions, staged in LDS once) and stores the rounded products
-// row-major in LDS; after the stage's barrier, wave 0's lanes (row r,
-// position t) add their row of products in element order, twelve float4
-// ahead of the adds, while the other waves already form the next stage.
-// The chain, the one serial part, therefore runs one add per element with
-// its operands in LDS; the weights' HBM latency is covered by NS stages.
+// workgroup of eight waves owns RB rows.  Waves 1-7 stream their share of
+// the packed weight rows (16 quant bytes, i.e. 16 elements of two adjacent
+// sub-blocks, plus the superblock's header per unit) through an NS-deep
+// register ring (one SL-column stage per slot, loads issued
+// unconditionally), dequantise them in registers to q4_k_value's
+// (d sc) q - dmin m (det-quant lib.rs:506-517), multiply them by the
+// activations (all T positions, staged in LDS once) and store the rounded
+// products row-major in LDS; after the stage's barrier, wave 0's lanes
+// (row r, position t) add their row of products in element order, twelve
+// float4 ahead of the adds, while the other waves already form the next
+// stage.  The chain, the one serial part, therefore runs one add per
+// element with its operands in LDS; the weights' HBM latency is covered by
+// NS stages, and the weights cost their packed 0.5625 bytes per element.
 template <int N4>
 __device__ __forceinline__ float chain_sum_lds_n(float a, const float* v) {
   constexpr int kRing = N4 < 12 ? N4 : 12;
@@ -665,8 +687,13 @@ __device__ __forceinline__ float chain_sum_lds_n(float a, const float* v) {
 enum { PC_SINGLE = 0, PC_CAT = 1, PC_PAIR = 2 };
 
 struct Q4kPcArgs {
-  const float* w0;
-  const float* w1;
+  // packed Q4_K: per superblock 128 quant bytes (q0/q1) and a 16-byte header
+  // (h0/h1: d, dmin, the 12 scale bytes), nb superblocks per row
+  const uint8_t* q0;
+  const uint8_t* q1;
+  const uint8_t* h0;
+  const uint8_t* h1;
+  int nb;
   int rows0, rows1, cols, T;
   const float* af;      // the Q8A values of the input, or null: formed from x
   const float* x;       // raw input (with af null), normed first when norm_w is set
@@ -699,7 +726,7 @@ __host__ __device__ constexpr size_t q4k_pc_prologue_floats(int cols) {
 
 constexpr int kPcThreads = 512;  // eight waves: wave 0 runs the chains
 constexpr int kPcProducers = kPcThreads - 64;  // waves 1-7 form the products
-constexpr int kPcMaxPer = 4;     // weight float4 per producer thread and stage
+constexpr int kPcMaxUnits = 2;   // 16-byte quant units per producer thread and stage
 
 template <int SL, int NS, int MODE>
 __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB) {
@@ -727,43 +754,53 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int row0 = blockIdx.x * RB;
   const int nst = cols / SL;
-  // weight float4 j of producer thread x = tid - 64: f = x + 448 j, staged
-  // row f / C4, float4 f % C4 of the stage; rows past the end read the last
-  // row, slots past WPS read the workgroup's first row and store nothing.
-  // Wave 0 loads wave 1's slots (unused: it only runs the chains).
-  auto src_of = [&](int f) {
-    const bool ok = f < WPS;
-    const int j = ok ? f / C4 : 0;
-    const float* w;
+  // Unit j of producer thread x = tid - 64 is f = x + 448 j: staged row
+  // f / UPR, bytes 16 (f % UPR) of the row's SL / 2 quant bytes of the
+  // stage.  Rows past the end read the last row, units past WPU read the
+  // workgroup's first row and store nothing.  Wave 0 loads wave 1's units
+  // (unused: it only runs the chains).
+  constexpr int UPR = SL / 32;            // units per row and stage
+  const int WPU = NR * UPR;               // units per stage
+  const int nb = p.nb;
+  auto row_of = [&](int f, int* m) {
+    const int j = f < WPU ? f / UPR : 0;
     int row;
     if (MODE == PC_PAIR) {
-      w = j < RB ? p.w0 : p.w1;
+      *m = j < RB ? 0 : 1;
       row = row0 + j % RB;
       row = row < p.rows0 ? row : p.rows0 - 1;
     } else {
       int g = row0 + j;
       g = g < rows_total ? g : rows_total - 1;
-      const bool m = MODE == PC_CAT && g >= p.rows0;
-      w = m ? p.w1 : p.w0;
-      row = m ? g - p.rows0 : g;
+      *m = MODE == PC_CAT && g >= p.rows0 ? 1 : 0;
+      row = *m ? g - p.rows0 : g;
     }
-    return w + (size_t)row * cols + (ok ? f % C4 : 0) * 4;
+    return row;
   };
   const int ptid = wave == 0 ? tid : tid - 64;
-  const float* s0 = src_of(ptid);
-  const float* s1 = src_of(ptid + kPcProducers);
-  const float* s2 = src_of(ptid + 2 * kPcProducers);
-  const float* s3 = src_of(ptid + 3 * kPcProducers);
+  int m0, m1;
+  const int r0 = row_of(ptid, &m0), r1 = row_of(ptid + kPcProducers, &m1);
+  const uint8_t* qr0 = (m0 ? p.q1 : p.q0) + (size_t)r0 * nb * 128;
+  const uint8_t* hr0 = (m0 ? p.h1 : p.h0) + (size_t)r0 * nb * 16;
+  const uint8_t* qr1 = (m1 ? p.q1 : p.q0) + (size_t)r1 * nb * 128;
+  const uint8_t* hr1 = (m1 ? p.h1 : p.h0) + (size_t)r1 * nb * 16;
+  const int u0 = ptid < WPU ? ptid % UPR : 0;
+  const int u1 = ptid + kPcProducers < WPU ? (ptid + kPcProducers) % UPR : 0;
   // the weights' first NS stages are in flight before the activations load
-  float4 ring0[NS], ring1[NS], ring2[NS], ring3[NS];
+  uint4 qa0[NS], ha0[NS], qa1[NS], ha1[NS];
+#define DTL_PC_LOAD(slot, k)                                                                \
+  do {                                                                                      \
+    const int kk_ = (k) < nst ? (k) : nst - 1;                                              \
+    const int b0_ = kk_ * (SL / 2) + 16 * u0, b1_ = kk_ * (SL / 2) + 16 * u1;               \
+    qa0[slot] = *reinterpret_cast<const uint4*>(qr0 + b0_);                                 \
+    ha0[slot] = *reinterpret_cast<const uint4*>(hr0 + (b0_ >> 7) * 16);                     \
+    if (kPcMaxUnits > 1) {                                                                  \
+      qa1[slot] = *reinterpret_cast<const uint4*>(qr1 + b1_);                               \
+      ha1[slot] = *reinterpret_cast<const uint4*>(hr1 + (b1_ >> 7) * 16);                   \
+    }                                                                                       \
+  } while (0)
 #pragma unroll
-  for (int u = 0; u < NS; u++) {
-    const size_t o = (size_t)(u < nst ? u : nst - 1) * SL;
-    ring0[u] = *reinterpret_cast<const float4*>(s0 + o);
-    ring1[u] = *reinterpret_cast<const float4*>(s1 + o);
-    ring2[u] = *reinterpret_cast<const float4*>(s2 + o);
-    ring3[u] = *reinterpret_cast<const float4*>(s3 + o);
-  }
+  for (int u = 0; u < NS; u++) DTL_PC_LOAD(u, u);
   // The fused Q6_K row's superblock words of this lane (see below), loaded
   // now so that they arrive during the stages; waves past the rows load row 0.
   uint4 v6a{}, v6b{}, v6c{}, v6e{};
@@ -814,13 +851,42 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
   // chain lane = staged row j + NR * position t
   const bool chain = wave == 0 && lane < NR * T;
   float sum = 0.0f;
-  auto products = [&](float* pb, int e, int f, const float4& w) {
-    if (f >= WPS) return;
-    const int r = f / C4, c = (f % C4) * 4;
+  // The 32 products of unit f (staged row r, quant bytes b.. b+15 of the
+  // row): elements b % 32 + [0, 16) of sub-blocks 2 g and 2 g + 1 of
+  // superblock b / 128, g = (b % 128) / 32, at stage columns c and c + 32.
+  auto products = [&](float* pb, int k, int f, uint4 qv, uint4 hv) {
+    if (f >= WPU) return;
+    const int r = f / UPR;
+    const int b = k * (SL / 2) + 16 * (f % UPR);
+    const int g = (b & 127) >> 5;
+    const int c = (b >> 7) * 256 + 64 * g + (b & 31) - k * SL;
+    const float d = f16_to_f32((uint16_t)(hv.x & 0xffffu)), dmin = f16_to_f32((uint16_t)(hv.x >> 16));
+    int sc0, mn0, sc1, mn1;
+    q4k_scale_min3(hv.y, hv.z, hv.w, 2 * g, &sc0, &mn0);
+    q4k_scale_min3(hv.y, hv.z, hv.w, 2 * g + 1, &sc1, &mn1);
+    const float dsc0 = d * (float)sc0, dm0 = dmin * (float)mn0;
+    const float dsc1 = d * (float)sc1, dm1 = dmin * (float)mn1;
+    const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+    float wl[16], wh[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const uint32_t byte = (qw[i >> 2] >> (8 * (i & 3))) & 0xffu;
+      wl[i] = dsc0 * (float)(byte & 0x0fu) - dm0;
+      wh[i] = dsc1 * (float)(byte >> 4) - dm1;
+    }
+    const int e = k * SL;
     for (int t = 0; t < T; t++) {
-      const float4 a = *reinterpret_cast<const float4*>(as + (size_t)t * cols + e + c);
-      *reinterpret_cast<float4*>(pb + (r + NR * t) * LDP + c) =
-          make_float4(w.x * a.x, w.y * a.y, w.z * a.z, w.w * a.w);
+      const float* at = as + (size_t)t * cols + e;
+      float* pr = pb + (r + NR * t) * LDP;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const float4 a = *reinterpret_cast<const float4*>(at + c + 4 * q);
+        *reinterpret_cast<float4*>(pr + c + 4 * q) =
+            make_float4(wl[4 * q] * a.x, wl[4 * q + 1] * a.y, wl[4 * q + 2] * a.z, wl[4 * q + 3] * a.w);
+        const float4 h = *reinterpret_cast<const float4*>(at + c + 32 + 4 * q);
+        *reinterpret_cast<float4*>(pr + c + 32 + 4 * q) =
+            make_float4(wh[4 * q] * h.x, wh[4 * q + 1] * h.y, wh[4 * q + 2] * h.z, wh[4 * q + 3] * h.w);
+      }
     }
   };
   for (int base = 0; base < nst; base += NS) {
@@ -828,22 +894,17 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
     for (int u = 0; u < NS; u++) {
       const int k = base + u;  // stages past the end form unused products
       float* pb = prod + (size_t)(k & 1) * NR * T * LDP;
-      const int e = (k < nst ? k : nst - 1) * SL;
+      const int kk = k < nst ? k : nst - 1;
       if (wave != 0) {
-        products(pb, e, ptid, ring0[u]);
-        products(pb, e, ptid + kPcProducers, ring1[u]);
-        products(pb, e, ptid + 2 * kPcProducers, ring2[u]);
-        products(pb, e, ptid + 3 * kPcProducers, ring3[u]);
+        products(pb, kk, ptid, qa0[u], ha0[u]);
+        if (kPcMaxUnits > 1) products(pb, kk, ptid + kPcProducers, qa1[u], ha1[u]);
       }
-      const size_t o = (size_t)(k + NS < nst ? k + NS : nst - 1) * SL;
-      ring0[u] = *reinterpret_cast<const float4*>(s0 + o);
-      ring1[u] = *reinterpret_cast<const float4*>(s1 + o);
-      ring2[u] = *reinterpret_cast<const float4*>(s2 + o);
-      ring3[u] = *reinterpret_cast<const float4*>(s3 + o);
+      DTL_PC_LOAD(u, k + NS);
       __syncthreads();
       if (chain && k < nst) sum = chain_sum_lds_n<C4>(sum, pb + lane * LDP);
     }
   }
+#undef DTL_PC_LOAD
   if (V6 && p.v6w && wave >= 1) {
     const int r6 = blockIdx.x + (wave - 1) * gridDim.x;
     if (r6 < p.v6rows) {
@@ -953,7 +1014,7 @@ size_t q4k_pc_smem(int T, int cols, int NR, int SL, bool prologue, bool v6) {
 // when it shares its SIMD with another one, so the rows are spread over at
 // most one workgroup per CU (at least eight rows each); the chain lanes
 // (staged rows x positions) must fit one wave and the stage's weights
-// kPcMaxPer float4 per thread.  256-column stages where those allow.
+// kPcMaxUnits 16-byte quant units per thread.
 bool q4k_pc_plan(int mode, int rows_total, int cols, int T, bool prologue, bool v6, int* RB,
                  int* SL, size_t* smem) {
   if (cols % 256 != 0 || T < 1) return false;
@@ -973,10 +1034,10 @@ bool q4k_pc_plan(int mode, int rows_total, int cols, int T, bool prologue, bool 
   // the longest stage (fewest barriers and ring refills) whose weights and
   // products fit
   int sl = 512;
-  while (sl > 128 && (NR * (sl / 4) > kPcMaxPer * kPcProducers ||
+  while (sl > 128 && (NR * (sl / 32) > kPcMaxUnits * kPcProducers ||
                       q4k_pc_smem(T, cols, NR, sl, prologue, v6) > 150 * 1024 || cols % sl != 0))
     sl /= 2;
-  if (NR * (sl / 4) > kPcMaxPer * kPcProducers || cols % sl != 0) return false;
+  if (NR * (sl / 32) > kPcMaxUnits * kPcProducers || cols % sl != 0) return false;
   if (v6 && (mode != PC_CAT || sl != 512)) return false;  // where the kernel has the fused rows
   *RB = rb;
   *SL = sl;
@@ -1258,8 +1319,9 @@ bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const floa
     launch_kernel(k_gemv_q6k, grid, dim3(64), 0, s, W, A.qk, A.dk, out, bias, epi, err);
     return true;
   }
-  if (W.type == kGgmlQ4K && W.w32) {
-    Q4kPcArgs a{W.w32, nullptr, W.rows, 0, W.cols, T, A.af, nullptr, nullptr, 0.0f, nullptr, nullptr,
+  if (W.type == kGgmlQ4K) {
+    Q4kPcArgs a{static_cast<const uint8_t*>(W.w), nullptr, W.hdr, nullptr, W.nb,
+                W.rows, 0, W.cols, T, A.af, nullptr, nullptr, 0.0f, nullptr, nullptr,
                 nullptr, nullptr, 0, 0, nullptr, nullptr, 0, out, nullptr, bias, nullptr, epi, 0, err};
     if (launch_q4k_pc<PC_SINGLE>(a, s)) return true;
   }
@@ -1369,8 +1431,8 @@ bool gemv_q4k_fit(const DevMat& W0, const DevMat* W1, bool pair, bool prologue, 
                   const DevMat* v6) {
   int RB, SL;
   size_t smem;
-  if (T > kGemvMaxT || W0.type != kGgmlQ4K || !W0.w32) return false;
-  if (W1 && (W1->type != kGgmlQ4K || !W1->w32 || W1->cols != W0.cols || (pair && W1->rows != W0.rows)))
+  if (T > kGemvMaxT || W0.type != kGgmlQ4K) return false;
+  if (W1 && (W1->type != kGgmlQ4K || W1->cols != W0.cols || (pair && W1->rows != W0.rows)))
     return false;
   if (v6 && (!prologue || v6->type != kGgmlQ6K || v6->cols != W0.cols || v6->nb > 8)) return false;
   const int mode = pair ? PC_PAIR : (W1 ? PC_CAT : PC_SINGLE);
@@ -1385,7 +1447,8 @@ bool launch_gemv_q4k(const DevMat& W0, const DevMat* W1, bool pair, const Q4kIn&
   if (!gemv_q4k_fit(W0, W1, pair, in.af == nullptr, T, in.v6)) return false;
   if (in.side_qk && (in.af || W0.cols % 256 != 0)) return false;
   const DevMat* v6 = in.v6;
-  Q4kPcArgs a{W0.w32, W1 ? W1->w32 : nullptr, W0.rows, W1 && !pair ? W1->rows : 0, W0.cols, T,
+  Q4kPcArgs a{static_cast<const uint8_t*>(W0.w), W1 ? static_cast<const uint8_t*>(W1->w) : nullptr,
+              W0.hdr, W1 ? W1->hdr : nullptr, W0.nb, W0.rows, W1 && !pair ? W1->rows : 0, W0.cols, T,
               in.af, in.x, in.norm_w, in.eps, in.side_qk, in.side_dk,
               v6 ? static_cast<const uint32_t*>(v6->w) : nullptr, v6 ? v6->d16 : nullptr,
               v6 ? v6->rows : 0, v6 ? v6->nb : 0, in.v6out, in.v6bias, in.v6epi,
