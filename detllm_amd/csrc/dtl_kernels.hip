@@ -864,24 +864,34 @@ __global__ void __launch_bounds__(NT) k_attention_hd64(const float* q, const flo
 
 // Head dimension 64 and at most eight heads per KV group: the arithmetic of
 // k_attention_hd64 with the lanes split over keys and heads.  Eight waves
-// per (KV group, position).
-//   scores  wave w takes keys 8w..8w+7 of each 64-key tile, lane = (key
-//           lane % 8, head lane / 8); a lane holds its head's query row in
-//           registers and reads its key's row (row-major in LDS) as float4.
-//   softmax wave h < G over head h's scores, as in k_attention_hd64.
-//   P.V     lane = (head lane / 8, dimension 8w + lane % 8); the V tile is
-//           stored transposed, so a lane reads four keys' values of its
-//           dimension and its head's four probabilities as two float4.
-// Per four elements a wave reads 8 key rows (scores) or 8 value rows and 8
-// probability rows (P.V) from LDS, each shared by eight lanes, where the
-// wave-per-head kernel reads 64 distinct addresses; its LDS reads then no
-// longer keep pace with the VALU work.
-constexpr int kS64Stride = 68;  // K rows and V^T rows (floats): 8 rows x float4 on 32 banks
+// per (KV group, position), each staging its own share of every 64-key tile
+// in a private LDS area, so the scores and P.V phases run without
+// workgroup barriers (one between the phases); each wave keeps D tiles of
+// its global loads in flight in registers.
+//   scores  wave w takes keys 8w..8w+7 of each tile, lane = (key lane % 8,
+//           head lane / 8); a lane holds its head's query row in registers
+//           and reads its key's row (row-major in the wave's area) as float4.
+//   softmax wave h < G over head h's scores (max, exp_f32, the 8-lane sum,
+//           the divisions), eight elements per lane in flight.
+//   P.V     lane = (head lane / 8, dimension 8w + lane % 8); the wave stores
+//           its eight dimensions of the tile's values transposed, so a lane
+//           reads four keys' values of its dimension and its head's four
+//           probabilities as two float4, in key order.
+constexpr int kS64Stride = 68;  // key rows and value columns (floats) of a wave's area
 constexpr int kS64Buf = 64 * kS64Stride;
 
 __host__ __device__ constexpr int attn_split_lane_stride(int len_max) {
   return ((len_max + 63) & ~63) + 4;  // 8 probability rows x float4 on 32 banks
 }
+
+namespace {
+// Orders one wave's LDS stores before its lanes' later loads of them.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+}  // namespace
 
 template <int D>
 __global__ void __launch_bounds__(512) k_attention_hd64s(const float* q, const float* kc,
@@ -890,7 +900,7 @@ __global__ void __launch_bounds__(512) k_attention_hd64s(const float* q, const f
                                                        float scale, float* out, QuantOut oq,
                                                        int* err) {
   extern __shared__ __align__(16) float smem[];
-  constexpr int hd = 64, NT = 512, PER = 2;  // a 64 x 64 tile is 1024 float4
+  constexpr int hd = 64;
   const int G = H / KV;
   const int g = blockIdx.x, t = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -907,8 +917,8 @@ __global__ void __launch_bounds__(512) k_attention_hd64s(const float* q, const f
     }
     return;
   }
-  float* sc = smem;                         // [G][scs] scores -> probabilities
-  float* tiles = sc + (size_t)G * scs;      // [2][kS64Buf]
+  float* sc = smem;                                  // [G][scs] scores -> probabilities
+  float* pb = sc + (size_t)G * scs + (size_t)wave * 8 * kS64Stride;  // this wave's [8][68]
   bool bad = false;
   const int kk = lane & 7, hh = lane >> 3;  // scores: key and head of the lane
   const int hq = hh < G ? hh : 0;
@@ -925,53 +935,42 @@ __global__ void __launch_bounds__(512) k_attention_hd64s(const float* q, const f
     }
   }
   const int ntiles = (len + 63) / 64;
-  // Tile loads: float4 x = tid + c * 512 covers row x / 16, columns 4 (x % 16);
-  // rows past len read row 0 and are not stored.
-  float4 ring[D][PER];
-  auto issue = [&](float4 (&dst)[PER], const float* base, int j0) {
+  float4 ring[D][2];
+  // Key rows 64 k + 8 wave + f / 16 (float4 f % 16) for f = lane, lane + 64;
+  // rows past len read row 0 and are not used.
+  auto issue_k = [&](float4 (&dst)[2], int k) {
 #pragma unroll
-    for (int c = 0; c < PER; c++) {
-      const int x = tid + c * NT;
-      const int j = x >> 4;
-      dst[c] = *reinterpret_cast<const float4*>(base + (size_t)(j0 + j < len ? j0 + j : 0) * hd + (x & 15) * 4);
+    for (int c = 0; c < 2; c++) {
+      const int f = lane + 64 * c;
+      const int j = 64 * k + 8 * wave + (f >> 4);
+      dst[c] = *reinterpret_cast<const float4*>(keys + (size_t)(j < len ? j : 0) * hd + (f & 15) * 4);
     }
   };
-  auto commit_k = [&](const float4 (&src)[PER], float* buf, int j0) {
+  // Value row 64 k + lane, dimensions 8 wave .. 8 wave + 7.
+  auto issue_v = [&](float4 (&dst)[2], int k) {
+    const int j = 64 * k + lane;
 #pragma unroll
-    for (int c = 0; c < PER; c++) {
-      const int x = tid + c * NT;
-      if (j0 + (x >> 4) < len)
-        *reinterpret_cast<float4*>(buf + (x >> 4) * kS64Stride + (x & 15) * 4) = src[c];
-    }
-  };
-  auto commit_v = [&](const float4 (&src)[PER], float* buf, int j0) {
-#pragma unroll
-    for (int c = 0; c < PER; c++) {
-      const int x = tid + c * NT;
-      const int j = x >> 4, i = (x & 15) * 4;
-      if (j0 + j < len) {
-        buf[(i + 0) * kS64Stride + j] = src[c].x;
-        buf[(i + 1) * kS64Stride + j] = src[c].y;
-        buf[(i + 2) * kS64Stride + j] = src[c].z;
-        buf[(i + 3) * kS64Stride + j] = src[c].w;
-      }
-    }
+    for (int c = 0; c < 2; c++)
+      dst[c] = *reinterpret_cast<const float4*>(vals + (size_t)(j < len ? j : 0) * hd + 8 * wave + 4 * c);
   };
   // scores: dot_f32_ref(q, k_j) * scale (8-lane order).  Tile k sits in ring slot k % D.
 #pragma unroll
-  for (int u = 0; u < D; u++) issue(ring[u], keys, u * 64);
-  commit_k(ring[0], tiles, 0);
-  issue(ring[0], keys, D * 64);
-  __syncthreads();
+  for (int u = 0; u < D; u++) issue_k(ring[u], u);
   for (int k0 = 0; k0 < ntiles; k0 += D) {
 #pragma unroll
     for (int u = 0; u < D; u++) {
       const int k = k0 + u;
       if (k < ntiles) {
-        const int j0 = k * 64;
-        const int j = j0 + 8 * wave + kk;
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+          const int f = lane + 64 * c;
+          *reinterpret_cast<float4*>(pb + (f >> 4) * kS64Stride + (f & 15) * 4) = ring[u][c];
+        }
+        wave_lds_sync();
+        issue_k(ring[u], k + D);
+        const int j = 64 * k + 8 * wave + kk;
         if (j < len && hh < G) {
-          const float* kr = tiles + (k & 1) * kS64Buf + (8 * wave + kk) * kS64Stride;
+          const float* kr = pb + kk * kS64Stride;
           float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
           for (int i4 = 0; i4 < 16; i4++) {
@@ -986,25 +985,35 @@ __global__ void __launch_bounds__(512) k_attention_hd64s(const float* q, const f
           if (!finite(sv)) bad = true;
           sc[(size_t)hh * scs + j] = sv;
         }
-        if (k + 1 < ntiles) commit_k(ring[(u + 1) % D], tiles + ((k + 1) & 1) * kS64Buf, j0 + 64);
+        wave_lds_sync();
       }
-      issue(ring[(u + 1) % D], keys, (k0 + u + 1 + D) * 64);
-      __syncthreads();
     }
   }
   // The first V tiles' loads overlap the softmax.
 #pragma unroll
-  for (int u = 0; u < D; u++) issue(ring[u], vals, u * 64);
+  for (int u = 0; u < D; u++) issue_v(ring[u], u);
+  __syncthreads();
   // softmax_in_place (lib.rs:2361-2388), wave h for head h
   if (wave < G) {
+    constexpr int U = 8;  // elements per lane in flight
     float* my = sc + (size_t)wave * scs;
     float mx = -__builtin_huge_valf();
     for (int j = lane; j < len; j += 64) mx = fmaxf(mx, my[j]);
     for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
-    for (int j = lane; j < len; j += 64) my[j] = exp_clamped(my[j] - mx);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int j0 = lane; j0 < len; j0 += 64 * U) {
+      float e[U];
+#pragma unroll
+      for (int c = 0; c < U; c++) {
+        const int j = j0 + 64 * c;
+        e[c] = j < len ? my[j] : 0.0f;
+      }
+#pragma unroll
+      for (int c = 0; c < U; c++) e[c] = exp_clamped(e[c] - mx);
+#pragma unroll
+      for (int c = 0; c < U; c++)
+        if (j0 + 64 * c < len) my[j0 + 64 * c] = e[c];
+    }
+    wave_lds_sync();
     float zacc = 0.0f;
     if (lane < 8) {
       int j = lane;
@@ -1022,27 +1031,46 @@ __global__ void __launch_bounds__(512) k_attention_hd64s(const float* q, const f
     for (int c = 0; c < 8; c++) part[c] = __shfl(zacc, c);
     const float z = finish_8lane(part);
     if (!finite(z) || z == 0.0f) bad = true;
-    for (int j = lane; j < len; j += 64) {
-      const float p = my[j] / z;
-      if (!finite(p)) bad = true;
-      my[j] = p;
+    for (int j0 = lane; j0 < len; j0 += 64 * U) {
+      float e[U];
+#pragma unroll
+      for (int c = 0; c < U; c++) {
+        const int j = j0 + 64 * c;
+        e[c] = j < len ? my[j] : 0.0f;
+      }
+#pragma unroll
+      for (int c = 0; c < U; c++) e[c] = e[c] / z;
+#pragma unroll
+      for (int c = 0; c < U; c++)
+        if (j0 + 64 * c < len) {
+          if (!finite(e[c])) bad = true;
+          my[j0 + 64 * c] = e[c];
+        }
     }
   }
-  commit_v(ring[0], tiles, 0);
-  issue(ring[0], vals, D * 64);
   __syncthreads();
   // P.V: out[d] = 0.0; out[d] += p_j * v_j[d] for j ascending
-  const int ph = lane >> 3, pd = 8 * wave + (lane & 7);
+  const int ph = lane >> 3, pd = lane & 7;  // head, dimension 8 wave + pd
   const float* prow = sc + (size_t)(ph < G ? ph : 0) * scs;
+  const float* vr = pb + pd * kS64Stride;
   float a = 0.0f;
   for (int k0 = 0; k0 < ntiles; k0 += D) {
 #pragma unroll
     for (int u = 0; u < D; u++) {
       const int k = k0 + u;
       if (k < ntiles) {
+        // the wave's eight dimensions of value rows 64 k .. 64 k + 63, transposed
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+          pb[(4 * c + 0) * kS64Stride + lane] = ring[u][c].x;
+          pb[(4 * c + 1) * kS64Stride + lane] = ring[u][c].y;
+          pb[(4 * c + 2) * kS64Stride + lane] = ring[u][c].z;
+          pb[(4 * c + 3) * kS64Stride + lane] = ring[u][c].w;
+        }
+        wave_lds_sync();
+        issue_v(ring[u], k + D);
         const int j0 = k * 64;
         const int n = len - j0 < 64 ? len - j0 : 64;
-        const float* vr = tiles + (k & 1) * kS64Buf + pd * kS64Stride;
         const float* pr = prow + j0;
         if (n == 64) {
 #pragma unroll
@@ -1057,16 +1085,15 @@ __global__ void __launch_bounds__(512) k_attention_hd64s(const float* q, const f
         } else {
           for (int j = 0; j < n; j++) a += pr[j] * vr[j];
         }
-        if (k + 1 < ntiles) commit_v(ring[(u + 1) % D], tiles + ((k + 1) & 1) * kS64Buf, j0 + 64);
+        wave_lds_sync();
       }
-      issue(ring[(u + 1) % D], vals, (k0 + u + 1 + D) * 64);
-      __syncthreads();
     }
   }
   // out through LDS so that each head's 64 values sit in one wave (its Q8A
   // form is two 32-element blocks)
-  float* ob = tiles;  // [8][64], free after the last tile's barrier
-  if (ph < G) ob[ph * 64 + pd] = a;
+  __syncthreads();
+  float* ob = sc + (size_t)G * scs;  // [8][64] over the waves' areas
+  if (ph < G) ob[ph * 64 + 8 * wave + pd] = a;
   __syncthreads();
   if (wave < G) {
     const float v = ob[wave * 64 + lane];
