@@ -553,12 +553,9 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
 #pragma unroll
       for (int k = 0; k < kProBatch; k++) {
         const int i = base + kStep * k + 4 * tid;
-        xv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-        wv[k] = xv[k];
-        if (i < cols) {
-          xv[k] = *reinterpret_cast<const float4*>(x + i);
-          wv[k] = *reinterpret_cast<const float4*>(in.norm_w + i);
-        }
+        const int il = i < cols ? i : 0;  // unconditional loads (see above), unused past cols
+        xv[k] = *reinterpret_cast<const float4*>(x + il);
+        wv[k] = *reinterpret_cast<const float4*>(in.norm_w + il);
       }
 #pragma unroll
       for (int k = 0; k < kProBatch; k++) {
@@ -610,7 +607,8 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
 #pragma unroll
       for (int k = 0; k < kProBatch; k++) {
         const int e = (s0 + NW * k) * 256 + 4 * lane;
-        f[k] = e < cols ? *reinterpret_cast<const float4*>(x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 v = *reinterpret_cast<const float4*>(x + (e < cols ? e : 0));
+        f[k] = e < cols ? v : make_float4(0.f, 0.f, 0.f, 0.f);
       }
 #pragma unroll
       for (int k = 0; k < kProBatch; k++) {
@@ -1136,20 +1134,18 @@ __global__ void __launch_bounds__(64 * NW) k_gemv_q8f(FusedMats M, FusedIn in, i
     uint16_t dsc[NI][NR];
 #pragma unroll
     for (int ii = 0; ii < NI; ii++) {
+      // lanes past the row load its last chunk and store nothing: loads under
+      // a condition would each be waited for before the next is issued
       const int c = cb + 64 * ii + lane;
-      const bool cv = c < nchunk;
-      const int b = TYPE == kGgmlQ8_0 ? c >> 1 : c;
+      const int cl = c < nchunk ? c : nchunk - 1;
+      const int b = TYPE == kGgmlQ8_0 ? cl >> 1 : cl;
 #pragma unroll
       for (int r = 0; r < NR; r++) {
-        w4[ii][r] = make_uint4(0, 0, 0, 0);
-        dsc[ii][r] = 0;
-        if (cv) {
-          if (TYPE == kGgmlQ8_0)
-            w4[ii][r] = *(const uint4*)((const int8_t*)wp[r] + (size_t)srow[r] * cols + (size_t)c * 16);
-          else
-            w4[ii][r] = *(const uint4*)((const uint8_t*)wp[r] + ((size_t)srow[r] * nb + c) * 16);
-          dsc[ii][r] = dp[r][(size_t)srow[r] * nb + b];
-        }
+        if (TYPE == kGgmlQ8_0)
+          w4[ii][r] = *(const uint4*)((const int8_t*)wp[r] + (size_t)srow[r] * cols + (size_t)cl * 16);
+        else
+          w4[ii][r] = *(const uint4*)((const uint8_t*)wp[r] + ((size_t)srow[r] * nb + cl) * 16);
+        dsc[ii][r] = dp[r][(size_t)srow[r] * nb + b];
       }
     }
     if (cb == 0)
