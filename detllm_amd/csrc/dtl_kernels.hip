@@ -1455,6 +1455,33 @@ __global__ void __launch_bounds__(256) k_attn_split_scores(const float* q, RopeI
 // of wave 0 run the sixteen serial chains over them (chain_sum_lds: a
 // dependent add costs its latency, about 8.5 cycles, whatever feeds it, so
 // the products are formed beforehand by every thread).
+namespace {
+// Raw buffer loads with a byte bound: a read past num_records returns zeros
+// and generates no memory request.  Descriptor word 3 as for gfx9 targets.
+typedef int BufRsrc __attribute__((ext_vector_type(4)));
+typedef float F32x4 __attribute__((ext_vector_type(4)));
+__device__ F32x4 raw_buffer_load_f32x4(BufRsrc rsrc, int voffset, int soffset, int aux) __asm(
+    "llvm.amdgcn.raw.buffer.load.v4f32");
+__device__ float raw_buffer_load_f32(BufRsrc rsrc, int voffset, int soffset, int aux) __asm(
+    "llvm.amdgcn.raw.buffer.load.f32");
+__device__ __forceinline__ BufRsrc buf_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  BufRsrc r;
+  r.x = (int)(uint32_t)a;
+  r.y = (int)((uint32_t)(a >> 32) & 0xffffu);  // stride 0
+  r.z = (int)bytes;
+  r.w = 0x00020000;
+  return r;
+}
+__device__ __forceinline__ float4 buf_load_f32x4(const BufRsrc& r, int byte_off) {
+  const F32x4 v = raw_buffer_load_f32x4(r, byte_off, 0, 0);
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float buf_load_f32(const BufRsrc& r, int byte_off) {
+  return raw_buffer_load_f32(r, byte_off, 0, 0);
+}
+}  // namespace
+
 constexpr int kSplitMaxRows = 2048;  // positions the register staging covers
 constexpr int kPvThreads = 1024;
 constexpr int kSplitVBlocks = kSplitMaxRows / kPvThreads;  // 4-row blocks per thread
@@ -1508,26 +1535,25 @@ __global__ void __launch_bounds__(kPvThreads) k_attn_split_pv(const float* score
     if (tid < kSplitDims) o[tid] = vrow(0)[d0 + tid];
     return;
   }
-  // Every load is unconditional (indices past len re-read a valid entry), so
-  // the wait before the max counts the V loads still in flight instead of
-  // draining them.
+  // The score row and the V rows are read with buffer loads bounded by len:
+  // past it they return zeros without touching memory, so every load stays
+  // unconditional (the wait before the max counts the V loads still in
+  // flight) and a short row costs only its own bytes.  The current
+  // positions' K and V rows are in the cache: the scores launch stores them.
   const float* srow = scores + ((size_t)t * H + h) * n_ctx;
+  const BufRsrc srs = buf_rsrc(srow, (uint32_t)len * 4u);
+  const BufRsrc vrs = buf_rsrc(vals, (uint32_t)len * hd * 4u);
   float sv[kSplitMaxRows / kPvThreads];
 #pragma unroll
-  for (int k = 0; k < kSplitMaxRows / kPvThreads; k++) {
-    const int j = kPvThreads * k + tid;
-    sv[k] = srow[j < len ? j : 0];
-  }
+  for (int k = 0; k < kSplitMaxRows / kPvThreads; k++) sv[k] = buf_load_f32(srs, 4 * (kPvThreads * k + tid));
   // V block i of this thread: rows 4 (256 i + jq) .. +3, dimensions d0 + c .. +3
   const int jq = tid >> 2, c = 4 * (tid & 3);
   float4 vb[kSplitVBlocks][4];
 #pragma unroll
   for (int i = 0; i < kSplitVBlocks; i++)
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int j = 4 * (256 * i + jq) + r;
-      vb[i][r] = *reinterpret_cast<const float4*>(vrow(j < len ? j : len - 1) + d0 + c);
-    }
+    for (int r = 0; r < 4; r++)
+      vb[i][r] = buf_load_f32x4(vrs, (4 * (256 * i + jq) + r) * hd * 4 + (d0 + c) * 4);
   float mx = -__builtin_huge_valf();
 #pragma unroll
   for (int k = 0; k < kSplitMaxRows / kPvThreads; k++) {
