@@ -46,15 +46,19 @@ FP32_VECTOR_PEAK_TFLOPS = 157.3        # FMA counted as two flops
 FP32_UNFUSED_PEAK_TFLOPS = 78.6
 
 
-# HBM bytes per launch of the dominant kernel, from two rocprofv3 --pmc
-# passes over this script's default run (FETCH_SIZE, then WRITE_SIZE, KiB
-# per dispatch averaged over the kernel's dispatches), each multiplied by
-# the factor that maps the same counter onto the known bytes of a plain
-# copy (--copy-probe-mib).  Keyed by kernel class; the summaries sit in
-# profiles/ under the same name.
+# HBM bytes per launch of the encode's Q4_K kernel classes (any of them can
+# be the dominant one), from two rocprofv3 --pmc passes over this script's
+# encode leg (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch averaged over
+# the kernel's dispatches), each multiplied by the factor that maps the same
+# counter onto the known bytes of a plain copy (--copy-probe-mib).  The
+# summary with the commands is the `source` file.
 MEASURED_TRAFFIC = {
-    "gemm_q4_k_gate_up": {"bytes": (47141.5 * 2.000 + 1408.0 * 1.000) * 1024.0,
-                          "source": "profiles/k_q4k_f32w_pair_tinyllama_encode_chunk64.md"},
+    "gemm_q4_k": {"bytes": (16778.5 * 2.000 + 512.0 * 1.000) * 1024.0,
+                  "source": "profiles/k_q4k_f32m_tinyllama_encode_chunk64.md"},
+    "gemm_q4_k_gate_up": {"bytes": (58912.9 * 2.000 + 1408.0 * 1.000) * 1024.0,
+                          "source": "profiles/k_q4k_f32m_tinyllama_encode_chunk64.md"},
+    "gemm_q4_k_qk": {"bytes": (11291.5 * 2.000 + 576.0 * 1.000) * 1024.0,
+                     "source": "profiles/k_q4k_f32m_tinyllama_encode_chunk64.md"},
 }
 
 
