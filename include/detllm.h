@@ -253,11 +253,11 @@ int dtl_logits_to_cdf(const float *logits, size_t n, size_t tail_symbols, uint32
 int dtl_logits_to_symbol_range(const float *logits, size_t n, size_t symbol, size_t tail_symbols,
                                uint64_t *cum, uint32_t *freq, uint64_t *total);
 
-/* uniform_symbol_range (cdf.rs:322-341). */
 /* uniform_cdf (cdf.rs:302-320): freq[i] = 1, cum[i] = i over `symbols`
  * entries, total = symbols (the CDF of a window's first position, context
  * length 0, with vocab + 256 symbols when byte escapes are on). */
 int dtl_uniform_cdf(size_t symbols, uint32_t *freq, uint64_t *cum, uint64_t *total);
+/* uniform_symbol_range (cdf.rs:322-341). */
 int dtl_uniform_symbol_range(size_t symbol, size_t symbols, uint64_t *cum, uint32_t *freq,
                              uint64_t *total);
 
