@@ -210,6 +210,65 @@ def codec_leg(gguf: bytes, workload: str, nbytes: int, cpu_bytes: int, threads: 
     return res
 
 
+def codec_full(args) -> int:
+    """C5 at its stated size over several runs: DTLZ compress of the whole
+    `--codec-bytes` Markov stream, then dtl_decompress_part slices of
+    decoding until `--codec-part-seconds` have passed; the compressed file,
+    the symbols so far and the range decoder's state go to `--codec-state`,
+    from which the next run continues.  The run that finishes checks the
+    decompressed bytes against the input (after the library's canonical
+    re-encode check) and prints one JSON line with the totals."""
+    import numpy as np
+
+    from detllm_amd import _lib, synth
+    from detllm_amd.codec import LoadedModel, compress, decompress_part
+
+    n_ctx = 2048
+    path = Path(args.codec_state)
+    lm = LoadedModel.load(synth.build_model(synth.WORKLOADS["qwen05"]))
+    data = synth.markov_bytes(0xDE711005, args.codec_bytes)
+    if path.exists():
+        z = np.load(path, allow_pickle=False)
+        out = z["dtlz"].tobytes()
+        prior = z["symbols"].astype(np.uint32)
+        st = _lib.RangeDecoderState(*[int(v) for v in z["state"]])
+        rec = json.loads(str(z["record"]))
+        log(f"[c5] resuming after {prior.size} symbols ({rec['decode_s']:.1f} s of decoding so far)")
+    else:
+        t = time.perf_counter()
+        out = compress(lm, data, n_ctx)
+        rec = {"bytes": len(data), "file_bytes": len(out), "compress_s": round(time.perf_counter() - t, 2),
+               "decode_s": 0.0, "runs": 0}
+        prior, st = np.zeros(0, np.uint32), None
+        log(f"[c5] compressed {len(data)} bytes into {len(out)} in {rec['compress_s']} s")
+    rec["runs"] += 1
+    t0 = time.perf_counter()
+    done, back = False, None
+    while not done and time.perf_counter() - t0 < args.codec_part_seconds:
+        t = time.perf_counter()
+        part = decompress_part(lm, out, prior, st, max_new=8192)
+        rec["decode_s"] += time.perf_counter() - t
+        prior = np.concatenate([prior, part.symbols.astype(np.uint32)])
+        st, done, back = part.state, part.done, part.data
+        log(f"[c5] {prior.size} symbols decoded ({rec['decode_s']:.1f} s)")
+    np.savez(path, dtlz=np.frombuffer(out, np.uint8), symbols=prior,
+             state=np.array([st.low, st.range, st.code, st.pos], np.uint64), record=json.dumps(rec))
+    if not done:
+        log(f"[c5] stopped after {prior.size} symbols; continue with --codec-state {path}")
+        return 0
+    import hashlib
+
+    rec.update({"symbols": int(prior.size), "roundtrip": back == data,
+                "decompress_bytes_per_s": round(len(data) / rec["decode_s"], 1),
+                "compress_bytes_per_s": round(len(data) / rec["compress_s"], 1),
+                "payload_sha256": hashlib.sha256(out[56:]).hexdigest(),
+                "canonical_check": "the final run re-encodes every symbol and compares with the file",
+                "n_ctx": n_ctx, "overlap": n_ctx // 4, "workload": "qwen05",
+                "data": "seeded order-3 Markov text (printable ASCII + newline, Zipf word lengths)"})
+    print(json.dumps({"c5": rec}), flush=True)
+    return 0 if rec["roundtrip"] else 1
+
+
 def host_cores() -> int:
     """Cores this process may use (the box's share for one GPU is 16)."""
     try:
@@ -325,6 +384,10 @@ def main() -> int:
                     help="second chunked-encode leg (Q8_0 on the int8 matrix cores); '' to skip")
     ap.add_argument("--no-kernel-timing", action="store_true",
                     help="time the steps without per-launch events (no roofline object)")
+    ap.add_argument("--codec-state", default=None,
+                    help="C5 at --codec-bytes over several runs: the state file to start or continue")
+    ap.add_argument("--codec-part-seconds", type=float, default=900.0,
+                    help="decoding time of one --codec-state run")
     ap.add_argument("--traffic-kib", default=None,
                     help="FETCH_KiB,WRITE_KiB per launch of the dominant kernel from rocprofv3 --pmc")
     args = ap.parse_args()
@@ -332,6 +395,8 @@ def main() -> int:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus})",
               file=sys.stderr)
         return 2
+    if args.codec_state:
+        return codec_full(args)
     if args.copy_probe_mib:
         return copy_probe(args.copy_probe_mib)
 

@@ -72,6 +72,12 @@ class ModelConfig(C.Structure):
     ]
 
 
+class RangeDecoderState(C.Structure):
+    """dtl_range_decoder_state: low, range, code and the input bytes consumed."""
+
+    _fields_ = [("low", C.c_uint64), ("range", C.c_uint64), ("code", C.c_uint64), ("pos", C.c_uint64)]
+
+
 class KernelStat(C.Structure):
     _fields_ = [
         ("name", C.c_char * 32),
@@ -122,6 +128,8 @@ _SIGS = {
     "dtl_range_decode_freq": (C.c_int, [C.c_void_p, C.c_uint64, u64p]),
     "dtl_range_decode_advance": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64]),
     "dtl_range_decoder_free": (None, [C.c_void_p]),
+    "dtl_range_decoder_snapshot": (C.c_int, [C.c_void_p, C.POINTER(RangeDecoderState)]),
+    "dtl_range_decoder_from_snapshot": (C.c_int, [u8p, sz, C.POINTER(RangeDecoderState), vpp]),
     "dtl_tokenizer_from_gguf": (C.c_int, [C.c_char_p, sz, vpp]),
     "dtl_tokenizer_free": (None, [C.c_void_p]),
     "dtl_tokenizer_vocab_len": (sz, [C.c_void_p]),
@@ -140,6 +148,11 @@ _SIGS = {
     ),
     "dtl_compress": (C.c_int, [C.c_void_p, C.c_void_p, u8p, u8p, sz, sz, sz, C.POINTER(u8p), C.POINTER(sz)]),
     "dtl_decompress": (C.c_int, [C.c_void_p, C.c_void_p, u8p, u8p, sz, sz, C.POINTER(u8p), C.POINTER(sz)]),
+    "dtl_decompress_part": (
+        C.c_int,
+        [C.c_void_p, C.c_void_p, u8p, u8p, sz, sz, u32p, sz, C.POINTER(RangeDecoderState), sz, u32p, sz,
+         C.POINTER(sz), C.POINTER(RangeDecoderState), C.POINTER(C.c_int), C.POINTER(u8p), C.POINTER(sz)],
+    ),
     "dtl_bytes_free": (None, [u8p]),
     "dtl_kernel_exp_f32": (C.c_int, [f32p, f32p, sz]),
     "dtl_kernel_silu_f32": (C.c_int, [f32p, f32p, sz]),

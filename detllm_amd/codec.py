@@ -253,6 +253,39 @@ def decompress(loaded: Optional[LoadedModel], file: bytes, max_chunk: int = CODE
     return _take(out, size.value)
 
 
+@dataclass
+class DecompressPart:
+    symbols: np.ndarray              # the symbols this call decoded
+    state: "_lib.RangeDecoderState"  # the range decoder's state after them
+    done: bool
+    data: Optional[bytes]            # the decompressed bytes once done
+
+
+def decompress_part(loaded: LoadedModel, file: bytes, prior: Sequence[int] = (),
+                    state: Optional["_lib.RangeDecoderState"] = None, max_new: int = 1 << 16,
+                    max_chunk: int = CODEC_CHUNK) -> DecompressPart:
+    """decompress over several calls (no counterpart in the reference): up to
+    max_new symbols after `prior` (all symbols of the earlier calls), resuming
+    the range decoder from `state`; once the symbols cover the original
+    length, the canonical check runs and `data` holds the bytes."""
+    src, n = _u8(file)
+    sha, _ = _u8(loaded.model_sha256)
+    pr = np.ascontiguousarray(np.asarray(prior, dtype=np.uint32))
+    out_sym = np.empty(max(max_new, 1), np.uint32)
+    n_new = C.c_size_t()
+    st_out = _lib.RangeDecoderState()
+    done = C.c_int()
+    out = _lib.u8p()
+    size = C.c_size_t()
+    check(lib.dtl_decompress_part(loaded.model._h, loaded.tokenizer._h, sha, src, n, max_chunk,
+                                  ptr(pr, C.c_uint32) if pr.size else None, pr.size,
+                                  C.byref(state) if state is not None else None, max_new,
+                                  ptr(out_sym, C.c_uint32), out_sym.size, C.byref(n_new), C.byref(st_out),
+                                  C.byref(done), C.byref(out), C.byref(size)), "decompress_part")
+    data = _take(out, size.value) if done.value else None
+    return DecompressPart(out_sym[: n_new.value].copy(), st_out, bool(done.value), data)
+
+
 def next_window_start(pos: int, window_start: int, n_ctx: int, overlap: int) -> int:
     """next_window_start (main.rs:801-808)."""
     return int(lib.dtl_codec_next_window_start(pos, window_start, n_ctx, overlap))
@@ -260,7 +293,8 @@ def next_window_start(pos: int, window_start: int, n_ctx: int, overlap: int) -> 
 
 __all__ = [
     "BYTE_ESCAPE_SYMBOLS", "CodecError", "DecodedBytes", "DtlzHeader", "FLAG_BYTE_ESCAPES", "HEADER_LEN",
-    "LoadedModel", "TokenError", "Tokenizer", "compress", "decode_bytes_with_model",
-    "decode_tokens_with_model", "decompress", "encode_symbols_with_model", "encode_tokens_with_model",
+    "DecompressPart", "LoadedModel", "TokenError", "Tokenizer", "compress", "decode_bytes_with_model",
+    "decode_tokens_with_model", "decompress", "decompress_part", "encode_symbols_with_model",
+    "encode_tokens_with_model",
     "next_window_start",
 ]

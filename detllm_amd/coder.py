@@ -14,6 +14,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
+from . import _lib
 from ._lib import DetllmError, check, lib, ptr
 
 M = 16_777_216
@@ -192,6 +193,23 @@ class RangeDecoder:
 
     def advance(self, cum: int, freq: int, total: int) -> None:
         check(lib.dtl_range_decode_advance(self._h, cum, freq, total), "RangeDecoder::advance")
+
+    def snapshot(self) -> "_lib.RangeDecoderState":
+        """The state between two symbols (low, range, code, bytes consumed); no
+        counterpart in the reference, for a decode continued in a later call."""
+        st = _lib.RangeDecoderState()
+        check(lib.dtl_range_decoder_snapshot(self._h, C.byref(st)), "RangeDecoder::snapshot")
+        return st
+
+    @classmethod
+    def from_snapshot(cls, data: bytes, state: "_lib.RangeDecoderState") -> "RangeDecoder":
+        self = cls.__new__(cls)
+        self._buf = (C.c_uint8 * max(len(data), 1)).from_buffer_copy(bytes(data) or b"\0")
+        h = C.c_void_p()
+        check(lib.dtl_range_decoder_from_snapshot(self._buf, len(data), C.byref(state), C.byref(h)),
+              "RangeDecoder::from_snapshot")
+        self._h = h
+        return self
 
     def __del__(self):
         try:

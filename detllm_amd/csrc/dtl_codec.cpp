@@ -146,19 +146,53 @@ int encode_payload(dtl_session* s, const uint32_t* symbols, size_t n, size_t ove
 
 // decode_bytes_with_model (main.rs:573-632) over WindowedModelState
 // (main.rs:634-799), symbols appended to *out.
+//
+// A decode may continue an earlier one (dtl_decompress_part): `prior` holds
+// the symbols decoded so far and `resume` the range decoder's state after
+// them.  The window schedule and the context are replayed from `prior`, and
+// the current window's tokens are forwarded again, as at a window rollover,
+// so the session then holds the same rows as the uninterrupted decode would.
+// With `final_state` the decoder's state after the last symbol is returned.
 int decode_symbols(dtl_session* s, const uint8_t* payload, size_t plen, size_t overlap,
                    int byte_escapes, const uint8_t* piece_len, size_t byte_len, size_t max_symbols,
-                   std::vector<uint32_t>* out) {
+                   std::vector<uint32_t>* out, const uint32_t* prior = nullptr, size_t n_prior = 0,
+                   const dtl_range_decoder_state* resume = nullptr,
+                   dtl_range_decoder_state* final_state = nullptr) {
   Info in;
   int st = session_info(s, &in);
   if (st) return st;
   if ((st = validate_window(in.n_ctx, overlap))) return st;
   const size_t V = in.vocab, tail = byte_escapes ? kEscapes : 0;
+  if ((n_prior != 0) != (resume != nullptr)) return DTL_ERR_INVALID_ARGUMENT;
   dtl_range_decoder* dec = nullptr;
-  if ((st = dtl_range_decoder_new(payload, plen, &dec))) return st;
+  st = resume ? dtl_range_decoder_from_snapshot(payload, plen, resume, &dec)
+              : dtl_range_decoder_new(payload, plen, &dec);
+  if (st) return st;
   std::vector<uint32_t> context;
   size_t window_start = 0, context_len = 0, last_row = 0, bytes = 0;
   if ((st = dtl_session_reset(s))) goto done;
+  for (size_t k = 0; k < n_prior; k++) {
+    const uint32_t sym = prior[k];
+    if (sym >= V + tail) {
+      st = DTL_ERR_INVALID_ARGUMENT;
+      goto done;
+    }
+    const size_t pos = context.size();
+    window_start = dtl_codec_next_window_start(pos, window_start, in.n_ctx, overlap);
+    if (piece_len) bytes += piece_len[sym];
+    if (sym < V) context.push_back(sym);
+  }
+  if (n_prior) {
+    // the rows of the current window, as a rollover replays them
+    const size_t pos = context.size();
+    window_start = dtl_codec_next_window_start(pos, window_start, in.n_ctx, overlap);
+    for (size_t p0 = window_start; p0 < pos; p0 += in.max_chunk) {
+      const size_t T = std::min(in.max_chunk, pos - p0);
+      if ((st = dtl_forward_chunk(s, context.data() + p0, T, p0 - window_start, nullptr))) goto done;
+      context_len += T;
+      last_row = T - 1;
+    }
+  }
   while (out->size() < max_symbols && (piece_len ? bytes < byte_len : true)) {
     const size_t pos = context.size();
     const size_t next = dtl_codec_next_window_start(pos, window_start, in.n_ctx, overlap);
@@ -214,6 +248,7 @@ int decode_symbols(dtl_session* s, const uint8_t* payload, size_t plen, size_t o
     }
   }
 done:
+  if (st == DTL_OK && final_state) st = dtl_range_decoder_snapshot(dec, final_state);
   dtl_range_decoder_free(dec);
   return st;
 }
@@ -375,59 +410,129 @@ int dtl_compress(const dtl_model* model, const dtl_tokenizer* tok, const uint8_t
 // decompress (main.rs:464-512): header first (before any model work), model
 // hash check, window check, decode to the original length, then the
 // canonical re-encode check.
+namespace {
+// The header checks and symbol tables shared by dtl_decompress and
+// dtl_decompress_part.
+struct DecompressPlan {
+  uint32_t n_ctx = 0, overlap = 0;
+  uint64_t orig_len = 0;
+  int escapes = 0;
+  std::vector<uint8_t> piece, one;
+};
+
+int plan_decompress(const dtl_model* model, const dtl_tokenizer* tok, const uint8_t model_sha256[32],
+                    const uint8_t* file, size_t len, DecompressPlan* P) {
+  uint16_t flags;
+  uint8_t sha[32];
+  int st = dtl_dtlz_header_decode(file, len, &flags, sha, &P->n_ctx, &P->overlap, &P->orig_len);
+  if (st) return st;
+  if (!model || !tok || !model_sha256) return DTL_ERR_INVALID_ARGUMENT;
+  dtl_model_config cfg;
+  if ((st = dtl_model_get_config(model, &cfg))) return st;
+  if ((st = check_codec_model(cfg, tok))) return st;
+  if (std::memcmp(sha, model_sha256, 32) != 0) return DTL_ERR_CODEC_MODEL_MISMATCH;
+  if (P->n_ctx > cfg.context_length) return DTL_ERR_FILE_INVALID_CONTEXT;
+  P->escapes = (flags & DTL_DTLZ_FLAG_BYTE_ESCAPES) ? 1 : 0;
+  const size_t V = cfg.vocab;
+  // bytes of each symbol (0: decodes to nothing) and, for the byte-fallback
+  // kind, the one byte itself
+  P->piece.assign(V + kEscapes, 0);
+  P->one.assign(V + kEscapes, 0);
+  for (size_t sym = 0; sym < V + kEscapes; sym++) {
+    size_t nb = 0;
+    uint8_t b;
+    if (dtl_tokenizer_decode_symbol(tok, (uint32_t)sym, V, &b, 1, &nb) == DTL_OK && nb == 1) {
+      P->piece[sym] = 1;
+      P->one[sym] = b;
+    }
+  }
+  return DTL_OK;
+}
+
+// The canonical check (the payload re-encoded from the symbols must equal
+// the file's) and the decompressed bytes.
+int finish_decompress(dtl_session* s, const DecompressPlan& P, const uint8_t* file, size_t len,
+                      const std::vector<uint32_t>& symbols, uint8_t** out, size_t* out_len) {
+  std::vector<uint8_t> again;
+  int st = encode_payload(s, symbols.data(), symbols.size(), P.overlap, P.escapes, &again);
+  if (st) return st;
+  if (again.size() != len - DTL_DTLZ_HEADER_LEN ||
+      std::memcmp(again.data(), file + DTL_DTLZ_HEADER_LEN, again.size()) != 0)
+    return DTL_ERR_CODEC_NOT_CANONICAL;
+  std::vector<uint8_t> bytes;
+  bytes.reserve(symbols.size());
+  for (uint32_t sym : symbols) bytes.push_back(P.one[sym]);
+  bytes.resize((size_t)P.orig_len);
+  return hand_out(bytes, out, out_len);
+}
+}  // namespace
+
 int dtl_decompress(const dtl_model* model, const dtl_tokenizer* tok,
                    const uint8_t model_sha256[32], const uint8_t* file, size_t len,
                    size_t max_chunk, uint8_t** out, size_t* out_len) {
   if ((!file && len) || !out || !out_len) return DTL_ERR_INVALID_ARGUMENT;
   *out = nullptr;
   *out_len = 0;
-  uint16_t flags;
-  uint8_t sha[32];
-  uint32_t n_ctx, overlap;
-  uint64_t orig_len;
-  int st = dtl_dtlz_header_decode(file, len, &flags, sha, &n_ctx, &overlap, &orig_len);
-  if (st) return st;
-  if (!model || !tok || !model_sha256) return DTL_ERR_INVALID_ARGUMENT;
   try {
-    dtl_model_config cfg;
-    if ((st = dtl_model_get_config(model, &cfg))) return st;
-    if ((st = check_codec_model(cfg, tok))) return st;
-    if (std::memcmp(sha, model_sha256, 32) != 0) return DTL_ERR_CODEC_MODEL_MISMATCH;
-    if (n_ctx > cfg.context_length) return DTL_ERR_FILE_INVALID_CONTEXT;
-    const int escapes = (flags & DTL_DTLZ_FLAG_BYTE_ESCAPES) ? 1 : 0;
-    const size_t V = cfg.vocab;
-    // bytes of each symbol (0: decodes to nothing) and, for the byte-fallback
-    // kind, the one byte itself
-    std::vector<uint8_t> piece(V + kEscapes, 0), one(V + kEscapes, 0);
-    for (size_t sym = 0; sym < V + kEscapes; sym++) {
-      size_t nb = 0;
-      uint8_t b;
-      if (dtl_tokenizer_decode_symbol(tok, (uint32_t)sym, V, &b, 1, &nb) == DTL_OK && nb == 1) {
-        piece[sym] = 1;
-        one[sym] = b;
-      }
-    }
+    DecompressPlan P;
+    int st = plan_decompress(model, tok, model_sha256, file, len, &P);
+    if (st) return st;
     dtl_session* s = nullptr;
-    if ((st = dtl_session_new(model, n_ctx, max_chunk ? max_chunk : 64, &s))) return st;
+    if ((st = dtl_session_new(model, P.n_ctx, max_chunk ? max_chunk : 64, &s))) return st;
     std::vector<uint32_t> symbols;
-    symbols.reserve((size_t)std::min<uint64_t>(orig_len, 8192));
+    symbols.reserve((size_t)std::min<uint64_t>(P.orig_len, 8192));
     // orig_len beyond what the payload codes ends in a range-coder error
     // (UnexpectedEof), as in the reference
-    st = decode_symbols(s, file + DTL_DTLZ_HEADER_LEN, len - DTL_DTLZ_HEADER_LEN, overlap, escapes,
-                        piece.data(), orig_len > SIZE_MAX ? SIZE_MAX : (size_t)orig_len, SIZE_MAX,
+    st = decode_symbols(s, file + DTL_DTLZ_HEADER_LEN, len - DTL_DTLZ_HEADER_LEN, P.overlap, P.escapes,
+                        P.piece.data(), P.orig_len > SIZE_MAX ? SIZE_MAX : (size_t)P.orig_len, SIZE_MAX,
                         &symbols);
-    std::vector<uint8_t> again;
-    if (st == DTL_OK) st = encode_payload(s, symbols.data(), symbols.size(), overlap, escapes, &again);
+    if (st == DTL_OK) st = finish_decompress(s, P, file, len, symbols, out, out_len);
     dtl_session_free(s);
+    return st;
+  } catch (const std::bad_alloc&) {
+    return DTL_ERR_OUT_OF_MEMORY;
+  }
+}
+
+int dtl_decompress_part(const dtl_model* model, const dtl_tokenizer* tok,
+                        const uint8_t model_sha256[32], const uint8_t* file, size_t len,
+                        size_t max_chunk, const uint32_t* prior, size_t n_prior,
+                        const dtl_range_decoder_state* state_in, size_t max_new, uint32_t* symbols,
+                        size_t cap, size_t* n_new, dtl_range_decoder_state* state_out, int* done,
+                        uint8_t** out, size_t* out_len) {
+  if ((!file && len) || (!prior && n_prior) || (!symbols && cap) || !n_new || !state_out || !done ||
+      !out || !out_len || cap < max_new || (n_prior != 0) != (state_in != nullptr))
+    return DTL_ERR_INVALID_ARGUMENT;
+  *n_new = 0;
+  *done = 0;
+  *out = nullptr;
+  *out_len = 0;
+  try {
+    DecompressPlan P;
+    int st = plan_decompress(model, tok, model_sha256, file, len, &P);
     if (st) return st;
-    if (again.size() != len - DTL_DTLZ_HEADER_LEN ||
-        std::memcmp(again.data(), file + DTL_DTLZ_HEADER_LEN, again.size()) != 0)
-      return DTL_ERR_CODEC_NOT_CANONICAL;
-    std::vector<uint8_t> bytes;
-    bytes.reserve(symbols.size());
-    for (uint32_t sym : symbols) bytes.push_back(one[sym]);
-    bytes.resize((size_t)orig_len);
-    return hand_out(bytes, out, out_len);
+    dtl_session* s = nullptr;
+    if ((st = dtl_session_new(model, P.n_ctx, max_chunk ? max_chunk : 64, &s))) return st;
+    std::vector<uint32_t> fresh;
+    fresh.reserve(std::min<size_t>(max_new, 1 << 16));
+    const size_t byte_len = P.orig_len > SIZE_MAX ? SIZE_MAX : (size_t)P.orig_len;
+    st = decode_symbols(s, file + DTL_DTLZ_HEADER_LEN, len - DTL_DTLZ_HEADER_LEN, P.overlap, P.escapes,
+                        P.piece.data(), byte_len, max_new, &fresh, prior, n_prior, state_in, state_out);
+    if (st == DTL_OK) {
+      if (!fresh.empty()) std::memcpy(symbols, fresh.data(), fresh.size() * 4);
+      *n_new = fresh.size();
+      size_t bytes = 0;
+      for (size_t k = 0; k < n_prior; k++) bytes += P.piece[prior[k]];
+      for (uint32_t sym : fresh) bytes += P.piece[sym];
+      if (bytes >= byte_len) {
+        std::vector<uint32_t> all(prior, prior + n_prior);
+        all.insert(all.end(), fresh.begin(), fresh.end());
+        st = finish_decompress(s, P, file, len, all, out, out_len);
+        if (st == DTL_OK) *done = 1;
+      }
+    }
+    dtl_session_free(s);
+    return st;
   } catch (const std::bad_alloc&) {
     return DTL_ERR_OUT_OF_MEMORY;
   }

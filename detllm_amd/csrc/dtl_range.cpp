@@ -144,6 +144,35 @@ int dtl_range_decoder_new(const uint8_t* data, size_t len, dtl_range_decoder** o
   return DTL_OK;
 }
 
+// The decoder's state between symbols (no pending decode_freq), for a
+// decode that continues in a later call.
+int dtl_range_decoder_snapshot(const dtl_range_decoder* d, dtl_range_decoder_state* st) {
+  if (!d || !st) return DTL_ERR_INVALID_ARGUMENT;
+  if (d->pending) return DTL_ERR_RANGE_INVALID_FREQUENCY;
+  st->low = d->low;
+  st->range = d->range;
+  st->code = d->code;
+  st->pos = d->pos;
+  return DTL_OK;
+}
+
+int dtl_range_decoder_from_snapshot(const uint8_t* data, size_t len, const dtl_range_decoder_state* st,
+                                    dtl_range_decoder** out) {
+  if (!out || !st || (!data && len)) return DTL_ERR_INVALID_ARGUMENT;
+  *out = nullptr;
+  if (st->pos > len || st->pos < 8 || st->range == 0) return DTL_ERR_INVALID_ARGUMENT;
+  dtl_range_decoder* d = new (std::nothrow) dtl_range_decoder();
+  if (!d) return DTL_ERR_OUT_OF_MEMORY;
+  d->in = data;
+  d->len = len;
+  d->pos = (size_t)st->pos;
+  d->low = st->low;
+  d->range = st->range;
+  d->code = st->code;
+  *out = d;
+  return DTL_OK;
+}
+
 int dtl_range_decode_freq(dtl_range_decoder* d, uint64_t total, uint64_t* value) {
   if (!d || !value) return DTL_ERR_INVALID_ARGUMENT;
   if (d->pending || total == 0 || total >= kTotalLimit) return DTL_ERR_RANGE_INVALID_FREQUENCY;

@@ -287,6 +287,19 @@ int dtl_range_decoder_new(const uint8_t *data, size_t len, dtl_range_decoder **o
 int dtl_range_decode_freq(dtl_range_decoder *dec, uint64_t total, uint64_t *value);
 int dtl_range_decode_advance(dtl_range_decoder *dec, uint64_t cum, uint64_t freq, uint64_t total);
 void dtl_range_decoder_free(dtl_range_decoder *dec);
+/* A range decoder's state between two symbols: the RangeDecoder fields low,
+ * range and code (det-coder range.rs:85-92) and the input bytes consumed.
+ * No counterpart in the reference, whose decoder runs in one call: for a
+ * long payload decoded across several calls (dtl_decompress_part). */
+typedef struct dtl_range_decoder_state {
+    uint64_t low, range, code, pos;
+} dtl_range_decoder_state;
+/* Copies the state (DTL_ERR_RANGE_INVALID_FREQUENCY between decode_freq and
+ * advance). */
+int dtl_range_decoder_snapshot(const dtl_range_decoder *dec, dtl_range_decoder_state *state);
+/* A decoder over data[0, len) resuming from `state` (pos in [8, len]). */
+int dtl_range_decoder_from_snapshot(const uint8_t *data, size_t len, const dtl_range_decoder_state *state,
+                                    dtl_range_decoder **out);
 
 /* ---- det-token byte-fallback tokenizer (host) ---------------------------- */
 typedef struct dtl_tokenizer dtl_tokenizer;
@@ -353,6 +366,23 @@ int dtl_compress(const dtl_model *model, const dtl_tokenizer *tok, const uint8_t
 int dtl_decompress(const dtl_model *model, const dtl_tokenizer *tok,
                    const uint8_t model_sha256[32], const uint8_t *file, size_t len,
                    size_t max_chunk, uint8_t **out, size_t *out_len);
+/* dtl_decompress in several calls, for a payload too long to decode in one
+ * (no counterpart in the reference, whose decompress runs in one call: for
+ * callers that bound the time of a call).  The first call passes
+ * n_prior = 0 and state_in = NULL; each call decodes up to max_new further
+ * symbols after `prior` (every symbol the earlier calls returned, in order)
+ * into `symbols` (cap >= max_new), and returns their count and the range
+ * decoder's state after them.  The window schedule is replayed from `prior`
+ * and the current window's tokens are forwarded again, so the symbols are
+ * those of one uninterrupted decode.  When they cover the header's original
+ * length, *done = 1 and, after the canonical check over all symbols, *out
+ * holds the bytes (as for dtl_decompress). */
+int dtl_decompress_part(const dtl_model *model, const dtl_tokenizer *tok,
+                        const uint8_t model_sha256[32], const uint8_t *file, size_t len,
+                        size_t max_chunk, const uint32_t *prior, size_t n_prior,
+                        const dtl_range_decoder_state *state_in, size_t max_new, uint32_t *symbols,
+                        size_t cap, size_t *n_new, dtl_range_decoder_state *state_out, int *done,
+                        uint8_t **out, size_t *out_len);
 /* Releases a buffer returned by dtl_compress / dtl_decompress. */
 void dtl_bytes_free(uint8_t *p);
 

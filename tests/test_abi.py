@@ -4,6 +4,7 @@ import ctypes as C
 import re
 
 import numpy as np
+import pytest
 
 import detref
 from conftest import ROOT
@@ -88,6 +89,58 @@ def test_dtlz_header_roundtrip():
     assert len(raw) == HEADER_LEN == 56 and raw[:4] == b"DTLZ"
     assert raw == h.encode()
     assert DtlzHeader.decode(raw) == h
+
+
+def test_range_decoder_snapshot_resumes_mid_stream():
+    """A decoder restored from a snapshot taken between two symbols decodes
+    the rest of the stream as the uninterrupted decoder does, through the
+    renormalisations the stream holds; a snapshot between decode_freq and
+    advance, a position before the 8 code bytes or past the input, and a
+    zero range are rejected."""
+    from detllm_amd._lib import DetllmError, RangeDecoderState
+    from detllm_amd.coder import RangeDecoder, RangeEncoder
+
+    rng = np.random.default_rng(11)
+    triples = []
+    for _ in range(3000):
+        total = int(rng.integers(2, 1 << 20))
+        f = int(rng.integers(1, total + 1))
+        triples.append((int(rng.integers(0, total - f + 1)), f, total))
+    enc = RangeEncoder()
+    for t in triples:
+        enc.encode(*t)
+    data = enc.finish()
+
+    def run(dec, ts):
+        got = []
+        for c, f, t in ts:
+            v = dec.decode_freq(t)
+            assert c <= v < c + f
+            dec.advance(c, f, t)
+            got.append(v)
+        return got
+
+    whole = RangeDecoder(data)
+    want = run(whole, triples)
+    end = whole.snapshot()
+    for cut in (0, 1, 777, 2999):
+        dec = RangeDecoder(data)
+        got = run(dec, triples[:cut])
+        resumed = RangeDecoder.from_snapshot(data, dec.snapshot())
+        got += run(resumed, triples[cut:])
+        assert got == want
+        fin = resumed.snapshot()
+        assert (fin.low, fin.range, fin.code, fin.pos) == (end.low, end.range, end.code, end.pos)
+    dec = RangeDecoder(data)
+    dec.decode_freq(triples[0][2])
+    with pytest.raises(DetllmError):
+        dec.snapshot()
+    good = RangeDecoder(data).snapshot()
+    for bad in (RangeDecoderState(good.low, good.range, good.code, 7),
+                RangeDecoderState(good.low, good.range, good.code, len(data) + 1),
+                RangeDecoderState(good.low, 0, good.code, good.pos)):
+        with pytest.raises(DetllmError):
+            RangeDecoder.from_snapshot(data, bad)
 
 
 def test_range_encoder_snapshot_resumes_canonical_stream():

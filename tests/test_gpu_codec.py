@@ -200,3 +200,63 @@ def test_compress_bytes_independent_of_chunk_size():
     b = compress(lm, data, 256)
     assert a == b
     assert decompress(lm, b) == data
+
+
+def test_decompress_in_parts_equals_one_call():
+    """dtl_decompress_part: a payload of many windows (escapes included)
+    decoded in parts cut mid-window, right at and after a rollover and one
+    symbol at a time across one gives the symbols, the canonical check and
+    the bytes of one dtl_decompress call; a tampered state never decodes the
+    same symbols."""
+    from detllm_amd import synth as sy
+    from detllm_amd._lib import DetllmError, RangeDecoderState
+    from detllm_amd.codec import (DtlzHeader, LoadedModel, compress, decompress, decompress_part,
+                                  next_window_start)
+
+    w = sy.WORKLOADS["smollm2"]
+    lm = LoadedModel.load(sy.build_model(w, layers=1))
+    data = sy.markov_bytes(5, 700)
+    n_ctx = 96
+    out = compress(lm, data, n_ctx, max_chunk=16)
+    overlap = DtlzHeader.decode(out).overlap
+    print(f"decompress in parts: {len(data)} bytes, n_ctx {n_ctx}, overlap {overlap}", flush=True)
+    assert decompress(lm, out, max_chunk=16) == data
+    ref = decompress_part(lm, out, max_new=len(data) + 64, max_chunk=16)
+    assert ref.done and ref.data == data
+    syms = [int(x) for x in ref.symbols]
+    V = lm.model.vocab
+    assert sum(1 for x in syms if x >= V) >= 2  # byte escapes present
+    # indices of the symbols decoded first in each new window
+    ctx, ws, rollovers = 0, 0, []
+    for k, x in enumerate(syms):
+        nxt = next_window_start(ctx, ws, n_ctx, overlap)
+        if nxt != ws:
+            rollovers.append(k)
+            ws = nxt
+        if x < V:
+            ctx += 1
+    assert len(rollovers) >= 3
+    cuts = sorted({1, 50, rollovers[0], rollovers[0] + 1, rollovers[1] - 1, rollovers[2], len(syms) - 3})
+    prior, state, part = [], None, None
+    for c in cuts + [len(syms)]:
+        part = decompress_part(lm, out, prior, state, max_new=c - len(prior), max_chunk=16)
+        assert [int(x) for x in part.symbols] == syms[len(prior):c], f"cut at {c}"
+        prior += [int(x) for x in part.symbols]
+        state = part.state
+        assert part.done == (c == len(syms))
+    assert part.data == data
+    # one symbol at a time across the first rollover
+    a = rollovers[0] - 3
+    first = decompress_part(lm, out, max_new=a, max_chunk=16)
+    prior, state = [int(x) for x in first.symbols], first.state
+    for k in range(a, a + 6):
+        p = decompress_part(lm, out, prior, state, max_new=1, max_chunk=16)
+        assert [int(x) for x in p.symbols] == [syms[k]], f"symbol {k}"
+        prior.append(syms[k])
+        state = p.state
+    bad = RangeDecoderState(state.low, state.range, state.code ^ (1 << 40), state.pos)
+    try:
+        p = decompress_part(lm, out, prior, bad, max_new=20, max_chunk=16)
+        assert [int(x) for x in p.symbols] != syms[len(prior):len(prior) + 20]
+    except DetllmError:
+        pass
