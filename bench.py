@@ -269,6 +269,46 @@ def codec_full(args) -> int:
     return 0 if rec["roundtrip"] else 1
 
 
+def codec_cpu_check(args) -> int:
+    """GPU-encode -> CPU-decode for the C5 stream: the oracle (on the host
+    cores, no GPU) decodes the first --codec-cpu-bytes of the DTLZ file a
+    --codec-state run wrote and compares them with the input."""
+    import numpy as np
+
+    from detllm_amd import synth
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import detref
+
+    z = np.load(args.codec_cpu_check, allow_pickle=False)
+    out = z["dtlz"].tobytes()
+    n_ctx = 2048
+    gguf = synth.build_model(synth.WORKLOADS["qwen05"])
+    tokens, types = synth.vocabulary(synth.WORKLOADS["qwen05"].vocab)
+    _, t2b = detref.byte_fallback_tables(tokens, [1 if ty in (1, 4, 6) else 0 for ty in types])
+    threads = args.cpu_threads or host_cores()
+    detref.set_threads(threads)
+    detref.set_simd(True)
+    k = args.codec_cpu_bytes
+    data = synth.markov_bytes(0xDE711005, k)
+    t = time.perf_counter()
+    sym, got = detref.codec_decode(detref.Model(gguf), t2b, out[56:], k, n_ctx, n_ctx // 4, True)
+    dt = time.perf_counter() - t
+    from detllm_amd.codec import next_window_start  # host code only
+
+    V = synth.WORKLOADS["qwen05"].vocab
+    ctx, ws, rollovers = 0, 0, 0
+    for x in sym:
+        nxt = next_window_start(ctx, ws, n_ctx, n_ctx // 4)
+        rollovers += nxt != ws
+        ws = nxt
+        ctx += int(x) < V
+    print(json.dumps({"c5_cpu_decode_prefix": {
+        "bytes": k, "symbols": len(sym), "tokens": ctx, "window_rollovers": rollovers, "ok": got == data,
+        "s": round(dt, 1), "threads": threads}}), flush=True)
+    return 0 if got == data else 1
+
+
 def host_cores() -> int:
     """Cores this process may use (the box's share for one GPU is 16)."""
     try:
@@ -388,6 +428,8 @@ def main() -> int:
                     help="C5 at --codec-bytes over several runs: the state file to start or continue")
     ap.add_argument("--codec-part-seconds", type=float, default=900.0,
                     help="decoding time of one --codec-state run")
+    ap.add_argument("--codec-cpu-check", default=None,
+                    help="decode the first --codec-cpu-bytes of a --codec-state file on the host (oracle)")
     ap.add_argument("--traffic-kib", default=None,
                     help="FETCH_KiB,WRITE_KiB per launch of the dominant kernel from rocprofv3 --pmc")
     args = ap.parse_args()
@@ -397,6 +439,8 @@ def main() -> int:
         return 2
     if args.codec_state:
         return codec_full(args)
+    if args.codec_cpu_check:
+        return codec_cpu_check(args)
     if args.copy_probe_mib:
         return copy_probe(args.copy_probe_mib)
 

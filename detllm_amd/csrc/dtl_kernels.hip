@@ -1105,8 +1105,11 @@ __global__ void __launch_bounds__(512) k_attention_hd64s(const float* q, const f
   if (bad) flag(err, ERRBIT_NON_FINITE);
 }
 
+constexpr int kHd64sRing = 4;  // tiles in flight per wave
+
 size_t attention_hd64s_smem(int G, int scs) {
-  return ((size_t)G * scs + 2 * kS64Buf) * sizeof(float);
+  // the score rows, then each wave's [8][68] area (the output's [8][64] reuses it)
+  return ((size_t)G * scs + 8 * 8 * kS64Stride) * sizeof(float);
 }
 
 // Decode shape (a few positions): one workgroup of 1024 threads per (head,
@@ -1707,12 +1710,12 @@ void launch_attention(const float* q, const float* kc, const float* vc, int laye
     const int scs = attn_split_lane_stride(pos0 + T);
     const size_t smem = attention_hd64s_smem(G, scs);
     if (smem <= 150 * 1024) {
-      static const bool attr = hipFuncSetAttribute((const void*)k_attention_hd64s<8>,
+      static const bool attr = hipFuncSetAttribute((const void*)k_attention_hd64s<kHd64sRing>,
                                                    hipFuncAttributeMaxDynamicSharedMemorySize,
                                                    150 * 1024) == hipSuccess;
       (void)attr;
       const QuantOut oq{qa, da, af, nullptr, nullptr};
-      launch_kernel(k_attention_hd64s<8>, dim3(KV, T), dim3(512), smem, s, q, kc, vc, layer, pos0, H,
+      launch_kernel(k_attention_hd64s<kHd64sRing>, dim3(KV, T), dim3(512), smem, s, q, kc, vc, layer, pos0, H,
                     KV, n_ctx, scs, scale, out, oq, err);
       return;
     }
