@@ -722,27 +722,48 @@ __host__ __device__ constexpr size_t q4k_pc_prologue_floats(int cols) {
   return 2 * (size_t)cols + 8 * (size_t)((((cols + 7) / 8) + 3) & ~3) + 16 + cols / 32 + cols / 4;
 }
 
-constexpr int kPcThreads = 512;  // eight waves: wave 0 runs the chains
-constexpr int kPcProducers = kPcThreads - 64;  // waves 1-7 form the products
-constexpr int kPcMaxUnits = 2;   // 16-byte quant units per producer thread and stage
+constexpr int kPcThreads = 512;    // eight waves
+constexpr int kPcChainWaves = 3;   // waves 0-2 run the chains
+constexpr int kPcProducers = kPcThreads - 64 * kPcChainWaves;  // waves 3-7 form the products
+constexpr int kPcMaxUnits = 2;     // 16-byte quant units per producer thread and stage
 
-template <int SL, int NS, int MODE>
+// Chains per chain wave: a DPP row of 16 lanes per chain (CR = 16) while
+// they fit, else a quad of 4 (CR = 4).
+__host__ __device__ constexpr int q4k_pc_chains(int CR) { return kPcChainWaves * (64 / CR); }
+
+// LDS bytes: activations, two product buffers and, when the kernel forms
+// the activations itself, the prologue's row, norm weights, chain-major
+// squares, scratch, scales and int8 values.
+// Activation rows and product rows keep four floats of padding after every
+// 64 columns (column c at c + 4 (c / 64)): the sixteen-float units a
+// producer wave writes and reads then fall on different LDS banks.
+__host__ __device__ constexpr int q4k_pc_skew(int c) { return c + ((c >> 6) << 2); }
+__host__ __device__ constexpr int q4k_pc_ldp(int SL) { return q4k_pc_skew(SL) + 4; }
+
+__host__ __device__ inline size_t q4k_pc_smem(int T, int cols, int NR, int SL, bool prologue, bool v6) {
+  size_t f = (size_t)T * q4k_pc_skew(cols) + (size_t)2 * NR * T * q4k_pc_ldp(SL);
+  if (prologue || v6) f += q4k_pc_prologue_floats(cols);
+  if (v6) f += (size_t)T * cols / 4 + (size_t)T * (cols / 256) + 7 * 64 + 7 * 8;
+  return f * sizeof(float);
+}
+
+template <int SL, int NS, int MODE, int CR>
 __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB) {
   constexpr int NM = MODE == PC_PAIR ? 2 : 1;
   // fused Q6_K rows: wq+wk launches with 512-column stages only (the
   // 128-column variants have no registers to spare for them)
   constexpr bool V6 = MODE == PC_CAT && SL == 512;
-  constexpr int LDP = SL + 4;             // product row stride (floats)
-  constexpr int C4 = SL / 4;              // float4 per row and stage
+  constexpr int LDP = q4k_pc_ldp(SL);     // product row stride (floats)
+  constexpr int G = 64 / CR;              // chains per chain wave
   const int NR = NM * RB;                 // staged rows (gate rows, then up rows)
-  const int WPS = NR * C4;                // weight float4 per stage
   extern __shared__ __align__(16) float smem[];
   const int cols = p.cols, T = p.T;
   const int rows_total = MODE == PC_CAT ? p.rows0 + p.rows1 : p.rows0;
-  float* as = smem;                       // [T][cols] activations
-  float* prod = smem + (size_t)T * cols;  // [2][NR * T][LDP] products
+  const int ACS = q4k_pc_skew(cols);      // activation row stride
+  float* as = smem;                       // [T][ACS] activations
+  float* prod = smem + (size_t)T * ACS;   // [2][NR * T][LDP] products
   // fused Q6_K rows: the input's Q8_K form [T][cols] (int8) and scales
-  // [T][cols / 256], then per wave 1-7 eight superblocks' class sums and scales
+  // [T][cols / 256], then per producer wave eight superblocks' class sums and scales
   float* v6area = prod + (size_t)2 * NR * T * LDP + q4k_pc_prologue_floats(cols);
   int8_t* v6q = reinterpret_cast<int8_t*>(v6area);
   float* v6dk = v6area + (size_t)T * cols / 4;
@@ -750,13 +771,13 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
   float* v6ds = reinterpret_cast<float*>(v6aux + 7 * 64);                 // [7][8]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool producer = wave >= kPcChainWaves;
   const int row0 = blockIdx.x * RB;
   const int nst = cols / SL;
-  // Unit j of producer thread x = tid - 64 is f = x + 448 j: staged row
-  // f / UPR, bytes 16 (f % UPR) of the row's SL / 2 quant bytes of the
-  // stage.  Rows past the end read the last row, units past WPU read the
-  // workgroup's first row and store nothing.  Wave 0 loads wave 1's units
-  // (unused: it only runs the chains).
+  // Unit j of producer thread x = tid - 64 kPcChainWaves is f = x + kPcProducers j:
+  // staged row f / UPR, bytes 16 (f % UPR) of the row's SL / 2 quant bytes of
+  // the stage.  Rows past the end read the last row, units past WPU read the
+  // workgroup's first row and store nothing.
   constexpr int UPR = SL / 32;            // units per row and stage
   const int WPU = NR * UPR;               // units per stage
   const int nb = p.nb;
@@ -775,7 +796,27 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
     }
     return row;
   };
-  const int ptid = wave == 0 ? tid : tid - 64;
+  const int ptid = producer ? tid - 64 * kPcChainWaves : 0;
+  // The fused Q6_K row's superblock words of this lane (see below), loaded
+  // now so that they arrive during the stages; waves past the rows load row 0.
+  uint4 v6a{}, v6b{}, v6c{}, v6e{};
+  uint32_t v6sc = 0;
+  uint16_t v6dw = 0;
+  if (V6 && p.v6w && producer) {
+    int r6 = blockIdx.x + (wave - kPcChainWaves) * gridDim.x;
+    r6 = r6 < p.v6rows ? r6 : 0;
+    const int sb = lane >> 3, h = (lane >> 2) & 1, pp = lane & 3;
+    const int sbl = sb < p.v6nb ? sb : 0;
+    const uint32_t* body = p.v6w + ((size_t)r6 * p.v6nb + sbl) * 52;
+    v6a = reinterpret_cast<const uint4*>(body + 16 * h + 8 * (pp & 1))[0];
+    v6b = reinterpret_cast<const uint4*>(body + 16 * h + 8 * (pp & 1))[1];
+    v6c = reinterpret_cast<const uint4*>(body + 32 + 8 * h)[0];
+    v6e = reinterpret_cast<const uint4*>(body + 32 + 8 * h)[1];
+    v6sc = body[48 + 2 * h + (pp >> 1)];
+    v6dw = p.v6d[(size_t)r6 * p.v6nb + sbl];
+  }
+  // the producers' weights: the first NS stages are in flight before the
+  // activations load
   int m0, m1;
   const int r0 = row_of(ptid, &m0), r1 = row_of(ptid + kPcProducers, &m1);
   const uint8_t* qr0 = (m0 ? p.q1 : p.q0) + (size_t)r0 * nb * 128;
@@ -784,7 +825,6 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
   const uint8_t* hr1 = (m1 ? p.h1 : p.h0) + (size_t)r1 * nb * 16;
   const int u0 = ptid < WPU ? ptid % UPR : 0;
   const int u1 = ptid + kPcProducers < WPU ? (ptid + kPcProducers) % UPR : 0;
-  // the weights' first NS stages are in flight before the activations load
   uint4 qa0[NS], ha0[NS], qa1[NS], ha1[NS];
 #define DTL_PC_LOAD(slot, k)                                                                \
   do {                                                                                      \
@@ -797,29 +837,16 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
       ha1[slot] = *reinterpret_cast<const uint4*>(hr1 + (b1_ >> 7) * 16);                   \
     }                                                                                       \
   } while (0)
+  if (producer) {
 #pragma unroll
-  for (int u = 0; u < NS; u++) DTL_PC_LOAD(u, u);
-  // The fused Q6_K row's superblock words of this lane (see below), loaded
-  // now so that they arrive during the stages; waves past the rows load row 0.
-  uint4 v6a{}, v6b{}, v6c{}, v6e{};
-  uint32_t v6sc = 0;
-  uint16_t v6dw = 0;
-  if (V6 && p.v6w) {
-    int r6 = blockIdx.x + (wave > 0 ? wave - 1 : 0) * gridDim.x;
-    r6 = r6 < p.v6rows ? r6 : 0;
-    const int sb = lane >> 3, h = (lane >> 2) & 1, pp = lane & 3;
-    const int sbl = sb < p.v6nb ? sb : 0;
-    const uint32_t* body = p.v6w + ((size_t)r6 * p.v6nb + sbl) * 52;
-    v6a = reinterpret_cast<const uint4*>(body + 16 * h + 8 * (pp & 1))[0];
-    v6b = reinterpret_cast<const uint4*>(body + 16 * h + 8 * (pp & 1))[1];
-    v6c = reinterpret_cast<const uint4*>(body + 32 + 8 * h)[0];
-    v6e = reinterpret_cast<const uint4*>(body + 32 + 8 * h)[1];
-    v6sc = body[48 + 2 * h + (pp >> 1)];
-    v6dw = p.v6d[(size_t)r6 * p.v6nb + sbl];
+    for (int u = 0; u < NS; u++) DTL_PC_LOAD(u, u);
   }
   if (p.af) {
-    for (int i = tid; i < T * cols / 4; i += kPcThreads)
-      reinterpret_cast<float4*>(as)[i] = reinterpret_cast<const float4*>(p.af)[i];
+    for (int i = tid; i < T * cols / 4; i += kPcThreads) {
+      const int t = 4 * i / cols, e = 4 * i - t * cols;
+      *reinterpret_cast<float4*>(as + (size_t)t * ACS + q4k_pc_skew(e)) =
+          reinterpret_cast<const float4*>(p.af)[i];
+    }
   } else {
     // The input's rmsnorm (with norm_w) and Q8A quantisation, as the
     // separate kernels form them, into the f32 values d * q.
@@ -840,15 +867,12 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
                                            da_s, misc, p.v6w ? v6q : (side ? p.side_qk : nullptr),
                                            p.v6w ? v6dk : (side ? p.side_dk : nullptr));
       for (int e = tid; e < cols; e += kPcThreads)
-        as[(size_t)t * cols + e] = da_s[e / 32] * (float)qa_s[e];
+        as[(size_t)t * ACS + q4k_pc_skew(e)] = da_s[e / 32] * (float)qa_s[e];
       __syncthreads();
     }
     if (bad && tid == 0) flag(p.err, ERRBIT_NON_FINITE);
   }
   __syncthreads();
-  // chain lane = staged row j + NR * position t
-  const bool chain = wave == 0 && lane < NR * T;
-  float sum = 0.0f;
   // The 32 products of unit f (staged row r, quant bytes b.. b+15 of the
   // row): elements b % 32 + [0, 16) of sub-blocks 2 g and 2 g + 1 of
   // superblock b / 128, g = (b % 128) / 32, at stage columns c and c + 32.
@@ -872,39 +896,92 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
       wl[i] = dsc0 * (float)(byte & 0x0fu) - dm0;
       wh[i] = dsc1 * (float)(byte >> 4) - dm1;
     }
-    const int e = k * SL;
+    // columns c and c + 32 lie in one 64-column group, k SL is a multiple of 64
+    const int cs = q4k_pc_skew(c);
+    const int e = q4k_pc_skew(k * SL);
     for (int t = 0; t < T; t++) {
-      const float* at = as + (size_t)t * cols + e;
+      const float* at = as + (size_t)t * ACS + e;
       float* pr = pb + (r + NR * t) * LDP;
+      // all eight activation reads before the first product store (the
+      // compiler cannot move a read above a store to the same LDS)
+      float4 a[4], h[4];
 #pragma unroll
       for (int q = 0; q < 4; q++) {
-        const float4 a = *reinterpret_cast<const float4*>(at + c + 4 * q);
-        *reinterpret_cast<float4*>(pr + c + 4 * q) =
-            make_float4(wl[4 * q] * a.x, wl[4 * q + 1] * a.y, wl[4 * q + 2] * a.z, wl[4 * q + 3] * a.w);
-        const float4 h = *reinterpret_cast<const float4*>(at + c + 32 + 4 * q);
-        *reinterpret_cast<float4*>(pr + c + 32 + 4 * q) =
-            make_float4(wh[4 * q] * h.x, wh[4 * q + 1] * h.y, wh[4 * q + 2] * h.z, wh[4 * q + 3] * h.w);
+        a[q] = *reinterpret_cast<const float4*>(at + cs + 4 * q);
+        h[q] = *reinterpret_cast<const float4*>(at + cs + 32 + 4 * q);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        *reinterpret_cast<float4*>(pr + cs + 4 * q) = make_float4(
+            wl[4 * q] * a[q].x, wl[4 * q + 1] * a[q].y, wl[4 * q + 2] * a[q].z, wl[4 * q + 3] * a[q].w);
+        *reinterpret_cast<float4*>(pr + cs + 32 + 4 * q) = make_float4(
+            wh[4 * q] * h[q].x, wh[4 * q + 1] * h[q].y, wh[4 * q + 2] * h[q].z, wh[4 * q + 3] * h[q].w);
       }
     }
   };
-  for (int base = 0; base < nst; base += NS) {
+  if (producer) {
+    // Stage k's products go to buffer k & 1; the barrier after them hands
+    // the buffer to the chain waves, which add it while the next stage forms.
+    for (int base = 0; base < nst; base += NS) {
 #pragma unroll
-    for (int u = 0; u < NS; u++) {
-      const int k = base + u;  // stages past the end form unused products
-      float* pb = prod + (size_t)(k & 1) * NR * T * LDP;
-      const int kk = k < nst ? k : nst - 1;
-      if (wave != 0) {
+      for (int u = 0; u < NS; u++) {
+        const int k = base + u;  // stages past the end form unused products
+        float* pb = prod + (size_t)(k & 1) * NR * T * LDP;
+        const int kk = k < nst ? k : nst - 1;
         products(pb, kk, ptid, qa0[u], ha0[u]);
         if (kPcMaxUnits > 1) products(pb, kk, ptid + kPcProducers, qa1[u], ha1[u]);
+        DTL_PC_LOAD(u, k + NS);
+        __syncthreads();
       }
-      DTL_PC_LOAD(u, k + NS);
-      __syncthreads();
-      if (chain && k < nst) sum = chain_sum_lds_n<C4>(sum, pb + lane * LDP);
     }
+  } else {
+    // Chain c = G wave + group: staged row c % NR, position c / NR (with
+    // the gate and up chains of one row and position in adjacent groups for
+    // the pair).  Groups past the chains add chain 0's products and store
+    // nothing, so the whole wave runs every DPP add.
+    const int grp = lane / CR, c = G * wave + grp;
+    int chain_row;
+    if (MODE == PC_PAIR) {
+      const int pc = c >> 1, j = pc % RB, t = pc / RB;
+      chain_row = pc < RB * T ? ((c & 1) ? RB + j : j) + NR * t : 0;
+    } else {
+      chain_row = c < NR * T ? c : 0;
+    }
+    float sum = 0.0f;
+    for (int base = 0; base < nst; base += NS) {
+#pragma unroll
+      for (int u = 0; u < NS; u++) {
+        const int k = base + u;
+        __syncthreads();
+        if (k < nst)
+          sum = chain_group_lds<CR, true>(sum, prod + (size_t)(k & 1) * NR * T * LDP + (size_t)chain_row * LDP, SL);
+      }
+    }
+    if ((lane & (CR - 1)) != 0) return;
+    if (MODE == PC_PAIR) {
+      const float u = __shfl(sum, lane + CR);  // the up chain of the same row and position
+      const int pc = c >> 1, j = pc % RB, t = pc / RB;
+      const int row = row0 + j;
+      if ((c & 1) || pc >= RB * T || row >= p.rows0) return;
+      const float v = silu_det(sum) * u;
+      p.out0[(size_t)t * p.rows0 + row] = v;
+      if (!(finite(sum) && finite(u) && finite(v))) flag(p.err, ERRBIT_NON_FINITE);
+      return;
+    }
+    if (c >= NR * T) return;
+    const int j = c % NR, t = c / NR;
+    const int g = row0 + j;
+    if (g >= rows_total) return;
+    const bool m = MODE == PC_CAT && g >= p.rows0;
+    const int row = m ? g - p.rows0 : g, R = m ? p.rows1 : p.rows0;
+    if (!epilogue(sum, m ? p.out1 : p.out0, (size_t)t * R + row, m ? p.bias1 : p.bias0, row,
+                  m ? p.epi1 : p.epi0))
+      flag(p.err, ERRBIT_NON_FINITE);
+    return;
   }
 #undef DTL_PC_LOAD
-  if (V6 && p.v6w && wave >= 1) {
-    const int r6 = blockIdx.x + (wave - 1) * gridDim.x;
+  if (V6 && p.v6w) {
+    const int r6 = blockIdx.x + (wave - kPcChainWaves) * gridDim.x;
     if (r6 < p.v6rows) {
       // dot_q6_k_q8k (det-quant lib.rs:353-397): lane = (superblock sb,
       // half h, part pp) forms its share of the eight class sums (exact
@@ -918,8 +995,8 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
       const uint32_t qhw[8] = {v6c.x, v6c.y, v6c.z, v6c.w, v6e.x, v6e.y, v6e.z, v6e.w};
       const uint32_t scw = v6sc;
       const float dwf = f16_to_f32(v6dw);
-      int* aux_w = v6aux + (wave - 1) * 64;
-      float* ds_w = v6ds + (wave - 1) * 8;
+      int* aux_w = v6aux + (wave - kPcChainWaves) * 64;
+      float* ds_w = v6ds + (wave - kPcChainWaves) * 8;
       for (int t = 0; t < T; t++) {
         const uint32_t* act = reinterpret_cast<const uint32_t*>(v6q + (size_t)t * cols + (size_t)sbl * 256);
         int aux[8];
@@ -978,43 +1055,16 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
       }
     }
   }
-  if (wave != 0) return;
-  const int j = lane % NR, t = lane / NR;
-  if (MODE == PC_PAIR) {
-    const float u = __shfl(sum, lane + RB);  // the up chain of the same row and position
-    const int row = row0 + j;
-    if (!chain || j >= RB || row >= p.rows0) return;
-    const float v = silu_det(sum) * u;
-    p.out0[(size_t)t * p.rows0 + row] = v;
-    if (!(finite(sum) && finite(u) && finite(v))) flag(p.err, ERRBIT_NON_FINITE);
-    return;
-  }
-  const int g = row0 + j;
-  if (!chain || g >= rows_total) return;
-  const bool m = MODE == PC_CAT && g >= p.rows0;
-  const int row = m ? g - p.rows0 : g, R = m ? p.rows1 : p.rows0;
-  if (!epilogue(sum, m ? p.out1 : p.out0, (size_t)t * R + row, m ? p.bias1 : p.bias0, row,
-                m ? p.epi1 : p.epi0))
-    flag(p.err, ERRBIT_NON_FINITE);
 }
 
-// LDS bytes: activations, two product buffers and, when the kernel forms
-// the activations itself, the prologue's row, norm weights, chain-major
-// squares, scratch, scales and int8 values.
-size_t q4k_pc_smem(int T, int cols, int NR, int SL, bool prologue, bool v6) {
-  size_t f = (size_t)T * cols + (size_t)2 * NR * T * (SL + 4);
-  if (prologue || v6) f += q4k_pc_prologue_floats(cols);
-  if (v6) f += (size_t)T * cols / 4 + (size_t)T * (cols / 256) + 7 * 64 + 7 * 8;
-  return f * sizeof(float);
-}
-
-// Rows per workgroup and columns per stage.  A chain wave runs far slower
-// when it shares its SIMD with another one, so the rows are spread over at
-// most one workgroup per CU (at least eight rows each); the chain lanes
-// (staged rows x positions) must fit one wave and the stage's weights
-// kPcMaxUnits 16-byte quant units per thread.
+// Rows per workgroup, columns per stage and the chain grouping.  A chain
+// wave runs far slower when it shares its SIMD with another busy wave, so
+// the rows are spread over at most one workgroup per CU (at least eight
+// rows each); the chains (staged rows x positions) must fit the chain waves
+// (twelve as DPP rows, 48 as quads) and the stage's weights kPcMaxUnits
+// 16-byte quant units per producer thread.
 bool q4k_pc_plan(int mode, int rows_total, int cols, int T, bool prologue, bool v6, int* RB,
-                 int* SL, size_t* smem) {
+                 int* SL, int* CR, size_t* smem) {
   if (cols % 256 != 0 || T < 1) return false;
   static const int cus = [] {
     int dev = 0, n = 0;
@@ -1026,9 +1076,10 @@ bool q4k_pc_plan(int mode, int rows_total, int cols, int T, bool prologue, bool 
   const int NM = mode == PC_PAIR ? 2 : 1;
   int rb = (rows_total + cus - 1) / cus;  // rows_total: of each matrix for the pair
   rb = rb < 8 ? 8 : rb;
-  if (NM * rb * T > 64) rb = 64 / (NM * T);
+  if (NM * rb * T > q4k_pc_chains(4)) rb = q4k_pc_chains(4) / (NM * T);
   if (rb < 1) return false;
   const int NR = NM * rb;
+  *CR = NR * T <= q4k_pc_chains(16) ? 16 : 4;
   // the longest stage (fewest barriers and ring refills) whose weights and
   // products fit
   int sl = 512;
@@ -1046,24 +1097,31 @@ bool q4k_pc_plan(int mode, int rows_total, int cols, int T, bool prologue, bool 
 template <int MODE>
 bool launch_q4k_pc(const Q4kPcArgs& a, hipStream_t s) {
   const int rows_total = MODE == PC_CAT ? a.rows0 + a.rows1 : a.rows0;
-  int RB, SL;
+  int RB, SL, CR;
   size_t smem;
-  if (!q4k_pc_plan(MODE, rows_total, a.cols, a.T, a.af == nullptr, a.v6w != nullptr, &RB, &SL, &smem))
+  if (!q4k_pc_plan(MODE, rows_total, a.cols, a.T, a.af == nullptr, a.v6w != nullptr, &RB, &SL, &CR, &smem))
     return false;
   const dim3 grid((rows_total + RB - 1) / RB);
-  // the fused Q6_K rows need waves 1-7 of the grid to cover them
-  if (a.v6w && (a.af || a.v6nb > 8 || (int)grid.x * (kPcThreads / 64 - 1) < a.v6rows)) return false;
-#define DTL_Q4K_PC(sl, ns)                                                                       \
+  // the fused Q6_K rows need the producer waves of the grid to cover them
+  if (a.v6w && (a.af || a.v6nb > 8 || (int)grid.x * (kPcThreads / 64 - kPcChainWaves) < a.v6rows))
+    return false;
+#define DTL_Q4K_PC(sl, ns, cr)                                                                   \
   do {                                                                                           \
-    static const bool attr = hipFuncSetAttribute((const void*)k_gemv_q4k_pc<sl, ns, MODE>,         \
+    static const bool attr = hipFuncSetAttribute((const void*)k_gemv_q4k_pc<sl, ns, MODE, cr>,     \
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,      \
                                                  150 * 1024) == hipSuccess;                       \
     (void)attr;                                                                                  \
-    launch_kernel((k_gemv_q4k_pc<sl, ns, MODE>), grid, dim3(kPcThreads), smem, s, a, RB);         \
+    launch_kernel((k_gemv_q4k_pc<sl, ns, MODE, cr>), grid, dim3(kPcThreads), smem, s, a, RB);     \
   } while (0)
-  if (SL == 512) DTL_Q4K_PC(512, 3);
-  else if (SL == 256) DTL_Q4K_PC(256, 4);
-  else DTL_Q4K_PC(128, 6);
+  if (CR == 16) {
+    if (SL == 512) DTL_Q4K_PC(512, 3, 16);
+    else if (SL == 256) DTL_Q4K_PC(256, 4, 16);
+    else DTL_Q4K_PC(128, 6, 16);
+  } else {
+    if (SL == 512) DTL_Q4K_PC(512, 3, 4);
+    else if (SL == 256) DTL_Q4K_PC(256, 4, 4);
+    else DTL_Q4K_PC(128, 6, 4);
+  }
 #undef DTL_Q4K_PC
   return true;
 }
@@ -1433,8 +1491,9 @@ bool gemv_q4k_fit(const DevMat& W0, const DevMat* W1, bool pair, bool prologue, 
   if (v6 && (!prologue || v6->type != kGgmlQ6K || v6->cols != W0.cols || v6->nb > 8)) return false;
   const int mode = pair ? PC_PAIR : (W1 ? PC_CAT : PC_SINGLE);
   const int rows = pair || !W1 ? W0.rows : W0.rows + W1->rows;
-  if (!q4k_pc_plan(mode, rows, W0.cols, T, prologue, v6 != nullptr, &RB, &SL, &smem)) return false;
-  return !v6 || ((rows + RB - 1) / RB) * (kPcThreads / 64 - 1) >= v6->rows;
+  int CR;
+  if (!q4k_pc_plan(mode, rows, W0.cols, T, prologue, v6 != nullptr, &RB, &SL, &CR, &smem)) return false;
+  return !v6 || ((rows + RB - 1) / RB) * (kPcThreads / 64 - kPcChainWaves) >= v6->rows;
 }
 
 bool launch_gemv_q4k(const DevMat& W0, const DevMat* W1, bool pair, const Q4kIn& in, int T,

@@ -953,59 +953,75 @@ __global__ void __launch_bounds__(512) k_attention_hd64s(const float* q, const f
     for (int c = 0; c < 2; c++)
       dst[c] = *reinterpret_cast<const float4*>(vals + (size_t)(j < len ? j : 0) * hd + 8 * wave + 4 * c);
   };
-  // scores: dot_f32_ref(q, k_j) * scale (8-lane order).  Tile k sits in ring slot k % D.
+  // scores: dot_f32_ref(q, k_j) * scale (8-lane order).  Tile k sits in ring
+  // slot k % D.  Every pass stores and refills its slot, past the last tile
+  // too: with the refill under a branch the compiler waits for every load
+  // in flight there, and the ring would hold one tile.  Each lane also keeps
+  // the maximum of its scores (fmax is exact in any order).
+  float lmax = -__builtin_huge_valf();
+  // issued in slot order (the scheduler would otherwise reorder them, and the
+  // loop's first wait would then cover every slot)
 #pragma unroll
-  for (int u = 0; u < D; u++) issue_k(ring[u], u);
+  for (int u = 0; u < D; u++) {
+    issue_k(ring[u], u);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   for (int k0 = 0; k0 < ntiles; k0 += D) {
 #pragma unroll
     for (int u = 0; u < D; u++) {
       const int k = k0 + u;
-      if (k < ntiles) {
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-          const int f = lane + 64 * c;
-          *reinterpret_cast<float4*>(pb + (f >> 4) * kS64Stride + (f & 15) * 4) = ring[u][c];
-        }
-        wave_lds_sync();
-        issue_k(ring[u], k + D);
-        const int j = 64 * k + 8 * wave + kk;
-        if (j < len && hh < G) {
-          const float* kr = pb + kk * kS64Stride;
-          float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-          for (int i4 = 0; i4 < 16; i4++) {
-            const float4 kv = *reinterpret_cast<const float4*>(kr + 4 * i4);
-            const int i = 4 * i4;
-            acc[(i + 0) & 7] += qr[i + 0] * kv.x;
-            acc[(i + 1) & 7] += qr[i + 1] * kv.y;
-            acc[(i + 2) & 7] += qr[i + 2] * kv.z;
-            acc[(i + 3) & 7] += qr[i + 3] * kv.w;
-          }
-          const float sv = finish_8lane(acc) * scale;
-          if (!finite(sv)) bad = true;
-          sc[(size_t)hh * scs + j] = sv;
-        }
-        wave_lds_sync();
+      for (int c = 0; c < 2; c++) {
+        const int f = lane + 64 * c;
+        *reinterpret_cast<float4*>(pb + (f >> 4) * kS64Stride + (f & 15) * 4) = ring[u][c];
       }
+      wave_lds_sync();
+      issue_k(ring[u], k + D);
+      const int j = 64 * k + 8 * wave + kk;
+      if (j < len && hh < G) {
+        const float* kr = pb + kk * kS64Stride;
+        float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int i4 = 0; i4 < 16; i4++) {
+          const float4 kv = *reinterpret_cast<const float4*>(kr + 4 * i4);
+          const int i = 4 * i4;
+          acc[(i + 0) & 7] += qr[i + 0] * kv.x;
+          acc[(i + 1) & 7] += qr[i + 1] * kv.y;
+          acc[(i + 2) & 7] += qr[i + 2] * kv.z;
+          acc[(i + 3) & 7] += qr[i + 3] * kv.w;
+        }
+        const float sv = finish_8lane(acc) * scale;
+        if (!finite(sv)) bad = true;
+        lmax = fmaxf(lmax, sv);
+        sc[(size_t)hh * scs + j] = sv;
+      }
+      wave_lds_sync();
     }
   }
+  // the head's maximum over the wave's eight key lanes, then (below) over the waves
+  lmax = fmaxf(lmax, __shfl_xor(lmax, 1));
+  lmax = fmaxf(lmax, __shfl_xor(lmax, 2));
+  lmax = fmaxf(lmax, __shfl_xor(lmax, 4));
+  if (kk == 0) pb[hh] = lmax;  // the wave's own area, free until P.V
   // The first V tiles' loads overlap the softmax.
 #pragma unroll
   for (int u = 0; u < D; u++) issue_v(ring[u], u);
   __syncthreads();
-  // softmax_in_place (lib.rs:2361-2388), wave h for head h
+  // softmax_in_place (lib.rs:2361-2388), wave h for head h.  Loads are
+  // clamped to the row, stores past it skipped, so no load sits under a
+  // per-element branch.
   if (wave < G) {
     constexpr int U = 8;  // elements per lane in flight
     float* my = sc + (size_t)wave * scs;
     float mx = -__builtin_huge_valf();
-    for (int j = lane; j < len; j += 64) mx = fmaxf(mx, my[j]);
-    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+#pragma unroll
+    for (int w = 0; w < 8; w++) mx = fmaxf(mx, sc[(size_t)G * scs + (size_t)w * 8 * kS64Stride + wave]);
     for (int j0 = lane; j0 < len; j0 += 64 * U) {
       float e[U];
 #pragma unroll
       for (int c = 0; c < U; c++) {
         const int j = j0 + 64 * c;
-        e[c] = j < len ? my[j] : 0.0f;
+        e[c] = my[j < len ? j : len - 1];
       }
 #pragma unroll
       for (int c = 0; c < U; c++) e[c] = exp_clamped(e[c] - mx);
@@ -1036,7 +1052,7 @@ __global__ void __launch_bounds__(512) k_attention_hd64s(const float* q, const f
 #pragma unroll
       for (int c = 0; c < U; c++) {
         const int j = j0 + 64 * c;
-        e[c] = j < len ? my[j] : 0.0f;
+        e[c] = my[j < len ? j : len - 1];
       }
 #pragma unroll
       for (int c = 0; c < U; c++) e[c] = e[c] / z;
@@ -1049,7 +1065,8 @@ __global__ void __launch_bounds__(512) k_attention_hd64s(const float* q, const f
     }
   }
   __syncthreads();
-  // P.V: out[d] = 0.0; out[d] += p_j * v_j[d] for j ascending
+  // P.V: out[d] = 0.0; out[d] += p_j * v_j[d] for j ascending.  As in the
+  // scores, every pass stores and refills its ring slot.
   const int ph = lane >> 3, pd = lane & 7;  // head, dimension 8 wave + pd
   const float* prow = sc + (size_t)(ph < G ? ph : 0) * scs;
   const float* vr = pb + pd * kS64Stride;
@@ -1058,17 +1075,17 @@ __global__ void __launch_bounds__(512) k_attention_hd64s(const float* q, const f
 #pragma unroll
     for (int u = 0; u < D; u++) {
       const int k = k0 + u;
-      if (k < ntiles) {
-        // the wave's eight dimensions of value rows 64 k .. 64 k + 63, transposed
+      // the wave's eight dimensions of value rows 64 k .. 64 k + 63, transposed
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-          pb[(4 * c + 0) * kS64Stride + lane] = ring[u][c].x;
-          pb[(4 * c + 1) * kS64Stride + lane] = ring[u][c].y;
-          pb[(4 * c + 2) * kS64Stride + lane] = ring[u][c].z;
-          pb[(4 * c + 3) * kS64Stride + lane] = ring[u][c].w;
-        }
-        wave_lds_sync();
-        issue_v(ring[u], k + D);
+      for (int c = 0; c < 2; c++) {
+        pb[(4 * c + 0) * kS64Stride + lane] = ring[u][c].x;
+        pb[(4 * c + 1) * kS64Stride + lane] = ring[u][c].y;
+        pb[(4 * c + 2) * kS64Stride + lane] = ring[u][c].z;
+        pb[(4 * c + 3) * kS64Stride + lane] = ring[u][c].w;
+      }
+      wave_lds_sync();
+      issue_v(ring[u], k + D);
+      if (k < ntiles) {
         const int j0 = k * 64;
         const int n = len - j0 < 64 ? len - j0 : 64;
         const float* pr = prow + j0;
@@ -1085,8 +1102,8 @@ __global__ void __launch_bounds__(512) k_attention_hd64s(const float* q, const f
         } else {
           for (int j = 0; j < n; j++) a += pr[j] * vr[j];
         }
-        wave_lds_sync();
       }
+      wave_lds_sync();
     }
   }
   // out through LDS so that each head's 64 values sit in one wave (its Q8A

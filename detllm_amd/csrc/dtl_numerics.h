@@ -176,6 +176,84 @@ __device__ __forceinline__ float chain_sum_lds(float a, const float* v, int n) {
   return a;
 }
 
+// Serial chains whose terms reach the adding lane by DPP broadcast.  A wave
+// issues an LDS read in about 14 cycles and a dependent add in about 4.6, so
+// a chain that reads its own terms (one float4 per four adds) runs at about
+// 9 cycles per term.  Here the R lanes of a group (a DPP row of 16, or a
+// quad of 4) read 4R consecutive terms of the group's chain with one float4
+// each, and every add takes its term from lane k of the group
+// (v_add_f32_dpp with row_newbcast:k or quad_perm:[k,k,k,k]): one LDS read
+// per 4R terms, and each term costs one add.  All R lanes of a group run the
+// same chain (the same sums, in the same order).
+//
+// a + v[0] + ... + v[n - 1] in order, per group; v points at the group's
+// chain (the same pointer on its R lanes), 16-byte aligned, with
+// ((n + 3) & ~3) floats readable; terms past n count as +0.0f (exact: a sum
+// that starts at +0.0f and adds rounded terms is never -0.0f).  n must be the
+// same on every lane of the wave, and the whole wave must be active (DPP
+// reads other lanes' registers).
+#define DTL_RNB(k)                                                                    \
+  "v_add_f32_dpp %0, %1, %0 row_newbcast:" #k " row_mask:0xf bank_mask:0xf\n"         \
+  "v_add_f32_dpp %0, %2, %0 row_newbcast:" #k " row_mask:0xf bank_mask:0xf\n"         \
+  "v_add_f32_dpp %0, %3, %0 row_newbcast:" #k " row_mask:0xf bank_mask:0xf\n"         \
+  "v_add_f32_dpp %0, %4, %0 row_newbcast:" #k " row_mask:0xf bank_mask:0xf\n"
+#define DTL_QB(k)                                                                     \
+  "v_add_f32_dpp %0, %1, %0 quad_perm:[" #k "," #k "," #k "," #k "] row_mask:0xf bank_mask:0xf\n" \
+  "v_add_f32_dpp %0, %2, %0 quad_perm:[" #k "," #k "," #k "," #k "] row_mask:0xf bank_mask:0xf\n" \
+  "v_add_f32_dpp %0, %3, %0 quad_perm:[" #k "," #k "," #k "," #k "] row_mask:0xf bank_mask:0xf\n" \
+  "v_add_f32_dpp %0, %4, %0 quad_perm:[" #k "," #k "," #k "," #k "] row_mask:0xf bank_mask:0xf\n"
+
+// The 4R terms held by the group's lanes (lane k: terms 4k .. 4k + 3), added
+// in order.  The leading s_nop covers the two wait states a DPP source
+// needs after a VALU write.
+template <int R>
+__device__ __forceinline__ float chain_group_add(float a, float4 x) {
+  static_assert(R == 16 || R == 4, "DPP rows or quads");
+  if (R == 16) {
+    asm("s_nop 1\n" DTL_RNB(0) DTL_RNB(1) DTL_RNB(2) DTL_RNB(3) DTL_RNB(4) DTL_RNB(5) DTL_RNB(6)
+            DTL_RNB(7) DTL_RNB(8) DTL_RNB(9) DTL_RNB(10) DTL_RNB(11) DTL_RNB(12) DTL_RNB(13)
+                DTL_RNB(14) DTL_RNB(15)
+        : "+v"(a)
+        : "v"(x.x), "v"(x.y), "v"(x.z), "v"(x.w));
+  } else {
+    asm("s_nop 1\n" DTL_QB(0) DTL_QB(1) DTL_QB(2) DTL_QB(3)
+        : "+v"(a)
+        : "v"(x.x), "v"(x.y), "v"(x.z), "v"(x.w));
+  }
+  return a;
+}
+#undef DTL_RNB
+#undef DTL_QB
+
+// With SKEW, term e sits at v[e + 4 (e / 64)] (four floats of padding after
+// every 64 terms, which spreads the writers of a 64-term group over the LDS
+// banks).
+template <int R, bool SKEW = false>
+__device__ __forceinline__ float chain_group_lds(float a, const float* v, int n) {
+  constexpr int B = 4 * R;  // terms per group read
+  const int k = threadIdx.x & (R - 1);
+  const int nb = (n + B - 1) / B;
+  auto load = [&](int b) {
+    const int e = b * B + 4 * k;
+    const int ec = e < n ? e : 0;
+    float4 x = *reinterpret_cast<const float4*>(v + (SKEW ? ec + ((ec >> 6) << 2) : ec));
+    x.x = e < n ? x.x : 0.0f;
+    x.y = e + 1 < n ? x.y : 0.0f;
+    x.z = e + 2 < n ? x.z : 0.0f;
+    x.w = e + 3 < n ? x.w : 0.0f;
+    return x;
+  };
+  // two reads in flight ahead of the adds
+  float4 x0 = load(0), x1 = load(1);
+  for (int b = 0; b < nb; b += 2) {
+    a = chain_group_add<R>(a, x0);
+    x0 = load(b + 2);
+    if (b + 1 < nb) a = chain_group_add<R>(a, x1);
+    x1 = load(b + 3);
+  }
+  return a;
+}
+
 // a += p[j] * v[j] for j = 0 .. n-1 in order, each product rounded and
 // added on its own (the P.V chain, det-model lib.rs:2390-2420), with both
 // operand rows in LDS (16-byte aligned).  Software-pipelined in blocks of 16
