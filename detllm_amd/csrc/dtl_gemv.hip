@@ -532,19 +532,55 @@ namespace {
 template <int NW>
 constexpr int pro_batch() { return NW >= 16 ? 1 : 4; }
 
-template <int NW>  // waves per workgroup
-// k_qk / k_dk (optional): also the Q8_K form of the (normed) row, written
-// to memory for position t.
+// The first batch of a prologue's row loads, issued ahead (q8a_row_loads)
+// by a kernel that then issues its first weight loads: those are younger
+// than the row's, so the in-order wait for the row does not wait for them.
+// (named members, not an array: the row's registers must not go to scratch)
+template <int NW>
+struct RowLoads {
+  static constexpr int kX = pro_batch<NW>() < 3 ? pro_batch<NW>() : 3;  // plain pass: x only
+  float4 x0, x1, x2, w0;                                               // norm pass: x0 and w0
+  __device__ float4 x(int k) const { return k == 0 ? x0 : (k == 1 ? x1 : x2); }
+};
+
+// The loads of the first batch, in the order and with the clamped
+// addresses q8a_prologue uses (the norm pass: its first float4 of x and of
+// the weights; the plain pass: the first kX of its spans).
+template <int NW>
+__device__ __forceinline__ void q8a_row_loads(const FusedIn& in, int t, int cols, bool norm,
+                                              RowLoads<NW>& rl) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const float* x = in.x + (size_t)t * cols;
+  auto ld = [&](int i) { return *reinterpret_cast<const float4*>(x + (i < cols ? i : 0)); };
+  if (norm) {
+    rl.x0 = ld(4 * tid);
+    rl.w0 = *reinterpret_cast<const float4*>(in.norm_w + (4 * tid < cols ? 4 * tid : 0));
+  } else {
+    rl.x0 = ld(wave * 256 + 4 * lane);
+    if (RowLoads<NW>::kX > 1) rl.x1 = ld((wave + NW) * 256 + 4 * lane);
+    if (RowLoads<NW>::kX > 2) rl.x2 = ld((wave + 2 * NW) * 256 + 4 * lane);
+  }
+}
+
+// NW: waves per workgroup.  k_qk / k_dk (optional): also the Q8_K form of
+// the (normed) row, written to memory for position t.  With use_pre, pre
+// holds the first batch's loads, issued by q8a_row_loads.  af_s (optional):
+// the f32 values d q of the Q8A form, in the skewed row layout of QuantOut.
+// DPP_CHAIN: the eight sum-of-squares chains on DPP rows of waves 0 and 1
+// (needs the whole of both waves and cols % 8 == 0), else on lanes 0-7.
+template <int NW, bool DPP_CHAIN = false>
 __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols, bool norm,
                                              float* xs, float* ws, float* sq, int cs,
                                              int8_t* qa_s, float* da_s, float* misc,
-                                             int8_t* k_qk = nullptr, float* k_dk = nullptr) {
+                                             int8_t* k_qk = nullptr, float* k_dk = nullptr,
+                                             bool use_pre = false, RowLoads<NW> pre = {},
+                                             float* af_s = nullptr) {
   constexpr int kProBatch = pro_batch<NW>();
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const float* x = in.x + (size_t)t * cols;
   const bool want_k = k_qk != nullptr;
-  const QuantOut q{qa_s, da_s, nullptr, want_k ? k_qk + (size_t)t * cols : nullptr,
-                   want_k ? k_dk + (size_t)t * (cols / 256) : nullptr};
+  const QuantOut q{qa_s, da_s, af_s, want_k ? k_qk + (size_t)t * cols : nullptr,
+                   want_k ? k_dk + (size_t)t * (cols / 256) : nullptr, 1};
   bool bad = false;
   if (norm) {
     constexpr int kStep = 4 * 64 * NW;  // elements per float4 pass of the workgroup
@@ -554,8 +590,13 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
       for (int k = 0; k < kProBatch; k++) {
         const int i = base + kStep * k + 4 * tid;
         const int il = i < cols ? i : 0;  // unconditional loads (see above), unused past cols
-        xv[k] = *reinterpret_cast<const float4*>(x + il);
-        wv[k] = *reinterpret_cast<const float4*>(in.norm_w + il);
+        if (use_pre && base == 0 && k == 0) {
+          xv[k] = pre.x0;
+          wv[k] = pre.w0;
+        } else {
+          xv[k] = *reinterpret_cast<const float4*>(x + il);
+          wv[k] = *reinterpret_cast<const float4*>(in.norm_w + il);
+        }
       }
 #pragma unroll
       for (int k = 0; k < kProBatch; k++) {
@@ -574,7 +615,15 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
       }
     }
     __syncthreads();
-    if (tid < 8) misc[tid] = chain_sum_lds(0.0f, sq + tid * cs, (cols - tid + 7) / 8);
+    if (DPP_CHAIN && cols % 8 == 0) {
+      if (wave < 2) {
+        const int c = 4 * wave + (lane >> 4);
+        const float sum = chain_group_lds<16>(0.0f, sq + c * cs, cols / 8);
+        if ((lane & 15) == 0) misc[c] = sum;
+      }
+    } else if (tid < 8) {
+      misc[tid] = chain_sum_lds(0.0f, sq + tid * cs, (cols - tid + 7) / 8);
+    }
     __syncthreads();
     if (tid == 0) {
       const float ss = finish_8lane(misc);
@@ -607,7 +656,9 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
 #pragma unroll
       for (int k = 0; k < kProBatch; k++) {
         const int e = (s0 + NW * k) * 256 + 4 * lane;
-        const float4 v = *reinterpret_cast<const float4*>(x + (e < cols ? e : 0));
+        const float4 v = use_pre && s0 == wave && k < RowLoads<NW>::kX
+                             ? pre.x(k)
+                             : *reinterpret_cast<const float4*>(x + (e < cols ? e : 0));
         f[k] = e < cols ? v : make_float4(0.f, 0.f, 0.f, 0.f);
       }
 #pragma unroll
@@ -717,9 +768,9 @@ struct Q4kPcArgs {
 };
 
 // Floats of the input prologue's scratch: row, norm weights, chain-major
-// squares, 16 of scratch, Q8A scales and int8 values.
+// squares and 16 of scratch.
 __host__ __device__ constexpr size_t q4k_pc_prologue_floats(int cols) {
-  return 2 * (size_t)cols + 8 * (size_t)((((cols + 7) / 8) + 3) & ~3) + 16 + cols / 32 + cols / 4;
+  return 2 * (size_t)cols + 8 * (size_t)((((cols + 7) / 8) + 3) & ~3) + 16;
 }
 
 constexpr int kPcThreads = 512;    // eight waves
@@ -733,7 +784,7 @@ __host__ __device__ constexpr int q4k_pc_chains(int CR) { return kPcChainWaves *
 
 // LDS bytes: activations, two product buffers and, when the kernel forms
 // the activations itself, the prologue's row, norm weights, chain-major
-// squares, scratch, scales and int8 values.
+// squares and scratch.
 // Activation rows and product rows keep four floats of padding after every
 // 64 columns (column c at c + 4 (c / 64)): the sixteen-float units a
 // producer wave writes and reads then fall on different LDS banks.
@@ -837,6 +888,11 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
       ha1[slot] = *reinterpret_cast<const uint4*>(hr1 + (b1_ >> 7) * 16);                   \
     }                                                                                       \
   } while (0)
+  // The input row's first loads, then the first NS stages' weights (younger,
+  // so the prologue's wait for the row does not wait for them).
+  const FusedIn in{p.x, p.norm_w, p.eps};
+  RowLoads<kPcThreads / 64> pre;
+  if (!p.af) q8a_row_loads<kPcThreads / 64>(in, 0, cols, p.norm_w != nullptr, pre);
   if (producer) {
 #pragma unroll
     for (int u = 0; u < NS; u++) DTL_PC_LOAD(u, u);
@@ -855,20 +911,17 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
     float* ws = xs + cols;
     float* sq = ws + cols;
     float* misc = sq + 8 * cs;
-    float* da_s = misc + 16;
-    int8_t* qa_s = reinterpret_cast<int8_t*>(da_s + cols / 32);
-    const FusedIn in{p.x, p.norm_w, p.eps};
     bool bad = false;
     for (int t = 0; t < T; t++) {
       // the Q8_K form: to LDS for the fused Q6_K rows, else (first
       // workgroup) to memory for a separate Q6_K launch
       const bool side = blockIdx.x == 0 && p.side_qk;
-      bad |= q8a_prologue<kPcThreads / 64>(in, t, cols, p.norm_w != nullptr, xs, ws, sq, cs, qa_s,
-                                           da_s, misc, p.v6w ? v6q : (side ? p.side_qk : nullptr),
-                                           p.v6w ? v6dk : (side ? p.side_dk : nullptr));
-      for (int e = tid; e < cols; e += kPcThreads)
-        as[(size_t)t * ACS + q4k_pc_skew(e)] = da_s[e / 32] * (float)qa_s[e];
-      __syncthreads();
+      int8_t* kq = p.v6w ? v6q : (side ? p.side_qk : nullptr);
+      float* kd = p.v6w ? v6dk : (side ? p.side_dk : nullptr);
+      // the Q8A values d q straight into the activation rows
+      bad |= q8a_prologue<kPcThreads / 64, true>(in, t, cols, p.norm_w != nullptr, xs, ws, sq, cs,
+                                                 nullptr, nullptr, misc, kq, kd, t == 0, pre,
+                                                 as + (size_t)t * ACS);
     }
     if (bad && tid == 0) flag(p.err, ERRBIT_NON_FINITE);
   }
@@ -1116,11 +1169,11 @@ bool launch_q4k_pc(const Q4kPcArgs& a, hipStream_t s) {
   if (CR == 16) {
     if (SL == 512) DTL_Q4K_PC(512, 3, 16);
     else if (SL == 256) DTL_Q4K_PC(256, 4, 16);
-    else DTL_Q4K_PC(128, 6, 16);
+    else DTL_Q4K_PC(128, 4, 16);
   } else {
     if (SL == 512) DTL_Q4K_PC(512, 3, 4);
     else if (SL == 256) DTL_Q4K_PC(256, 4, 4);
-    else DTL_Q4K_PC(128, 6, 4);
+    else DTL_Q4K_PC(128, 4, 4);
   }
 #undef DTL_Q4K_PC
   return true;

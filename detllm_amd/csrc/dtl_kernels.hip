@@ -322,7 +322,14 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* x, const float* w,
     }
   }
   __syncthreads();
-  if (threadIdx.x < 8) {
+  if (n % 8 == 0) {
+    // the eight chains on the DPP rows of waves 0 and 1
+    if (wave < 2) {
+      const int c = 4 * wave + (lane >> 4);
+      const float sum = chain_group_lds<16>(0.0f, sq + c * cs, n / 8);
+      if ((lane & 15) == 0) lane_sum[c] = sum;
+    }
+  } else if (threadIdx.x < 8) {
     const int c = threadIdx.x;  // elements c, c+8, ... below n
     lane_sum[c] = chain_sum_lds(0.0f, sq + c * cs, (n - c + 7) / 8);
   }

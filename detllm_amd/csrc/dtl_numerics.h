@@ -176,6 +176,25 @@ __device__ __forceinline__ float chain_sum_lds(float a, const float* v, int n) {
   return a;
 }
 
+// Lane exchanges by DPP (a VALU operand modifier, no LDS round trip), for
+// reductions whose combine is commutative and associative or exact: after
+// the two quad steps every quad holds its result, the half-row mirror (lane
+// i <-> 7 - i) then pairs each quad with the other quad of its eight lanes,
+// and the row mirror (i <-> 15 - i) each eight with the other eight of its
+// sixteen.  Every lane of the group must be active.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+  return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(dpp_i32<CTRL>(__float_as_int(v)));
+}
+constexpr int kDppXor1 = 0xb1;      // quad_perm:[1,0,3,2]
+constexpr int kDppXor2 = 0x4e;      // quad_perm:[2,3,0,1]
+constexpr int kDppMirror8 = 0x141;  // row_half_mirror
+constexpr int kDppMirror16 = 0x140; // row_mirror
+
 // Serial chains whose terms reach the adding lane by DPP broadcast.  A wave
 // issues an LDS read in about 14 cycles and a dependent add in about 4.6, so
 // a chain that reads its own terms (one float4 per four adds) runs at about

@@ -13,18 +13,37 @@
 
 namespace dtl {
 
+// Null outputs are not written.  With af_skew, the f32 values d q go to
+// af[e + 4 (e / 64)] (a row with four floats of padding after every 64).
 struct QuantOut {
   int8_t* qa;
   float* da;
   float* af;
   int8_t* qk;
   float* dk;
+  int af_skew = 0;
 };
+
+// v / d rounded to nearest, given rd = 1 / d rounded to nearest: q0 = v rd,
+// then one fma correction, q0 + (v - q0 d) rd (Markstein's theorem: with rd
+// correctly rounded and q0 within an ulp of the quotient, the corrected
+// value is the rounded quotient while nothing underflows).  For the
+// quantiser's operands (d = amax / 127 >= 2^-92 / 127, |v| <= amax) the host
+// check in tests/test_div_recip.py compares it with the division: every
+// float v in [2^-100, amax] for a dozen amax, random pairs across the
+// exponent range, and every amax for d = amax / 127 itself.  For
+// |v| < 2^-100 both quotients are below 0.5 in magnitude and round to 0.
+__device__ __forceinline__ float div_recip(float v, float d, float rd) {
+  const float q0 = v * rd;
+  const float r = __builtin_fmaf(-q0, d, v);
+  return __builtin_fmaf(r, rd, q0);
+}
 
 // v: the lane's four elements; in: whether they exist; base: element offset
 // of the span (a multiple of 256 within the [T][n] array).
 __device__ __forceinline__ void quantize_span(const float v[4], bool in, size_t base, bool want_q8a,
                                               bool want_q8k, const QuantOut& q) {
+  // (every lane of the wave must be active: the reductions exchange lanes by DPP)
   const int lane = threadIdx.x & 63;
   const size_t off = base + 4 * lane;
   float ax[4];
@@ -33,19 +52,33 @@ __device__ __forceinline__ void quantize_span(const float v[4], bool in, size_t 
   if (want_q8a) {
     // amax over the 32-element block (max is order independent).
     float amax = fmaxf(fmaxf(ax[0], ax[1]), fmaxf(ax[2], ax[3]));
-#pragma unroll
-    for (int m = 4; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
+    amax = fmaxf(amax, dpp_f32<kDppXor1>(amax));
+    amax = fmaxf(amax, dpp_f32<kDppXor2>(amax));
+    amax = fmaxf(amax, dpp_f32<kDppMirror8>(amax));
     if (in) {
       int8_t qv[4];
       float fv[4];
-      float d = amax / 127.0f;
+      // d = amax / 127 and the quotients v / d, each rounded to nearest.
+      // From amax = 2^-92 up, by reciprocals and one fma correction
+      // (div_recip); below, and for amax = 0, by division.
+      float d, yv[4];
+      if (amax >= 0x1p-92f) {
+        d = div_recip(amax, 127.0f, 1.0f / 127.0f);
+        const float rd = 1.0f / d;
+#pragma unroll
+        for (int c = 0; c < 4; c++) yv[c] = div_recip(v[c], d, rd);
+      } else {
+        d = amax / 127.0f;
+#pragma unroll
+        for (int c = 0; c < 4; c++) yv[c] = v[c] / d;
+      }
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         if (amax == 0.0f) {
           qv[c] = 0;
           fv[c] = 0.0f;
         } else {
-          float y = v[c] / d;
+          const float y = yv[c];
           int r = y < 0.0f ? f32_as_i32(y - 0.5f) : f32_as_i32(y + 0.5f);
           r = r < -127 ? -127 : (r > 127 ? 127 : r);
           qv[c] = (int8_t)r;
@@ -54,9 +87,11 @@ __device__ __forceinline__ void quantize_span(const float v[4], bool in, size_t 
       }
       uint32_t packed = (uint32_t)(uint8_t)qv[0] | ((uint32_t)(uint8_t)qv[1] << 8) |
                         ((uint32_t)(uint8_t)qv[2] << 16) | ((uint32_t)(uint8_t)qv[3] << 24);
-      *reinterpret_cast<uint32_t*>(q.qa + off) = packed;
-      if (q.af) *reinterpret_cast<float4*>(q.af + off) = make_float4(fv[0], fv[1], fv[2], fv[3]);
-      if ((lane & 7) == 0) q.da[off / 32] = amax == 0.0f ? 0.0f : d;
+      if (q.qa) *reinterpret_cast<uint32_t*>(q.qa + off) = packed;
+      if (q.af)
+        *reinterpret_cast<float4*>(q.af + (q.af_skew ? off + ((off >> 6) << 2) : off)) =
+            make_float4(fv[0], fv[1], fv[2], fv[3]);
+      if (q.da && (lane & 7) == 0) q.da[off / 32] = amax == 0.0f ? 0.0f : d;
     }
   }
   if (want_q8k) {
@@ -71,16 +106,21 @@ __device__ __forceinline__ void quantize_span(const float v[4], bool in, size_t 
         bv = v[c];
         bi = 4 * lane + c;
       }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      float ox = __shfl_xor(bx, m), ov = __shfl_xor(bv, m);
-      int oi = __shfl_xor(bi, m);
+    // the combine is commutative and associative: DPP steps within each
+    // sixteen lanes, then the two exchanges across rows
+    auto take = [&](float ox, float ov, int oi) {
       if (ox > bx || (ox == bx && oi < bi)) {
         bx = ox;
         bi = oi;
         bv = ov;
       }
-    }
+    };
+    take(dpp_f32<kDppXor1>(bx), dpp_f32<kDppXor1>(bv), dpp_i32<kDppXor1>(bi));
+    take(dpp_f32<kDppXor2>(bx), dpp_f32<kDppXor2>(bv), dpp_i32<kDppXor2>(bi));
+    take(dpp_f32<kDppMirror8>(bx), dpp_f32<kDppMirror8>(bv), dpp_i32<kDppMirror8>(bi));
+    take(dpp_f32<kDppMirror16>(bx), dpp_f32<kDppMirror16>(bv), dpp_i32<kDppMirror16>(bi));
+#pragma unroll
+    for (int m = 16; m <= 32; m <<= 1) take(__shfl_xor(bx, m), __shfl_xor(bv, m), __shfl_xor(bi, m));
     float mx = bx == 0.0f ? 0.0f : bv;
     if (in) {
       // Stored class-major inside the 256-block (element e at (e % 8) * 32 + e / 8),
