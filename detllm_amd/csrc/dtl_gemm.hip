@@ -588,6 +588,11 @@ void launch_q6k_planes(const DevMat& W, int8_t* planes, hipStream_t s) {
                 planes);
 }
 
+// K steps in flight per wave in the int8 MFMA GEMMs (slots r0, r1, ...):
+// the Q6_K superblock's operands are four times a Q8_0 block pair's.
+constexpr int kQ6kRing = 2;
+constexpr int kMfmaRing = 4;
+
 template <int NT>
 __global__ void __launch_bounds__(256) k_q6k_mfma(const int8_t* __restrict__ planes,
                                                   const uint16_t* __restrict__ d16, int rows,
@@ -657,7 +662,10 @@ __global__ void __launch_bounds__(256) k_q6k_mfma(const int8_t* __restrict__ pla
 #pragma unroll
     for (int j = 0; j < NT; j++) o.da[j] = dsrc[j][sb];
   };
-  auto compute = [&](const Ops& o) {
+  // valid false (a ring slot past the last superblock): every term added is
+  // +0.0f, which leaves the sums' bits unchanged (a sum that starts at +0.0f
+  // is never -0.0f), so the loop needs no branch around it.
+  auto compute = [&](const Ops& o, bool valid) {
     float dd[NT][4];
 #pragma unroll
     for (int j = 0; j < NT; j++)
@@ -673,20 +681,33 @@ __global__ void __launch_bounds__(256) k_q6k_mfma(const int8_t* __restrict__ pla
         acc = acc * 64;
         acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, o.b[j][c], acc, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; i++) sums[j][c][i] += dd[j][i] * (float)acc[i];
+        for (int i = 0; i < 4; i++) {
+          const float term = dd[j][i] * (float)acc[i];
+          sums[j][c][i] += valid ? term : 0.0f;
+        }
       }
     }
   };
-  Ops x0, x1;
-  load(x0, 0);
-  int sb = 0;
-  for (; sb + 2 <= nb; sb += 2) {
-    load(x1, sb + 1);
-    compute(x0);
-    if (sb + 2 < nb) load(x0, sb + 2);
-    compute(x1);
+  // kQ6kRing superblocks in flight.  Every pass refills its slot (the
+  // index clamped to the last superblock): with the refill under a branch
+  // the compiler waits for every load in flight before the next compute.
+  // (Named slots, not an array, and each refill after the last use of the
+  // slot: otherwise the loop-carried registers get copies at the back edge,
+  // and the copies wait for the loads.)
+  auto last = [&](int i) { return i < nb ? i : nb - 1; };
+  Ops r0, r1;
+  load(r0, last(0));
+  load(r1, last(1));
+#define DTL_MFMA_STEP(r, i)                                                                \
+  compute(r, (i) < nb);                                                                    \
+  __builtin_amdgcn_sched_barrier(0);                                                       \
+  load(r, last((i) + kQ6kRing));                                                           \
+  __builtin_amdgcn_sched_barrier(0)
+  for (int s0 = 0; s0 < nb; s0 += kQ6kRing) {
+    DTL_MFMA_STEP(r0, s0);
+    DTL_MFMA_STEP(r1, s0 + 1);
   }
-  if (sb < nb) compute(x0);
+#undef DTL_MFMA_STEP
 #pragma unroll
   for (int c = 0; c < 2; c++)
 #pragma unroll
@@ -793,10 +814,12 @@ __global__ void __launch_bounds__(256) k_q8_mfma(const int8_t* __restrict__ w8,
       o.dav[1][j] = dsrc[j][b1];
     }
   };
-  auto compute = [&](const Ops& o, bool two) {
+  // valid[h]: whether block 2 pr + h exists; a missing block adds +0.0f
+  // terms, which leave the sums' bits unchanged (as in k_q6k_mfma).
+  auto compute = [&](const Ops& o, bool valid0, bool valid1) {
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-      if (h == 1 && !two) break;
+      const bool valid = h == 0 ? valid0 : valid1;
       const dtl_v4i a = (q >> 1) == h ? o.a : zero;
       float dw[4];
 #pragma unroll
@@ -807,22 +830,38 @@ __global__ void __launch_bounds__(256) k_q8_mfma(const int8_t* __restrict__ w8,
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const float dd = dw[i] * o.dav[h][j];
-          sums[j][i] += dd * (float)acc[i];
+          const float term = dd * (float)acc[i];
+          sums[j][i] += valid ? term : 0.0f;
         }
       }
     }
   };
+  // Block pairs in flight, refilled unconditionally as in k_q6k_mfma
   const int np = (nb + 1) / 2;
-  Ops x0, x1;
-  load(x0, 0);
-  int pr = 0;
-  for (; pr + 2 <= np; pr += 2) {
-    load(x1, pr + 1);
-    compute(x0, 2 * pr + 1 < nb);
-    if (pr + 2 < np) load(x0, pr + 2);
-    compute(x1, 2 * pr + 3 < nb);
+  // (four slots with one position tile per wave, two with more)
+  constexpr int D = NT == 1 ? kMfmaRing : 2;
+  auto last = [&](int i) { return i < np ? i : np - 1; };
+  Ops r0, r1, r2, r3;
+  load(r0, last(0));
+  load(r1, last(1));
+  if (D == 4) {
+    load(r2, last(2));
+    load(r3, last(3));
   }
-  if (pr < np) compute(x0, 2 * pr + 1 < nb);
+#define DTL_MFMA_STEP(r, i)                                                                \
+  compute(r, (i) < np, 2 * (i) + 1 < nb);                                                  \
+  __builtin_amdgcn_sched_barrier(0);                                                       \
+  load(r, last((i) + D));                                                                  \
+  __builtin_amdgcn_sched_barrier(0)
+  for (int p0 = 0; p0 < np; p0 += D) {
+    DTL_MFMA_STEP(r0, p0);
+    DTL_MFMA_STEP(r1, p0 + 1);
+    if (D == 4) {
+      DTL_MFMA_STEP(r2, p0 + 2);
+      DTL_MFMA_STEP(r3, p0 + 3);
+    }
+  }
+#undef DTL_MFMA_STEP
   bool ok = true;
 #pragma unroll
   for (int j = 0; j < NT; j++) {

@@ -39,27 +39,16 @@ __device__ __forceinline__ int32_t f32_as_i32(float x) {
 
 // f16 bits -> f32 by integer construction (det-num f16.rs:6-34); exact for
 // every input including subnormals, independent of the hardware f16 mode.
+// Written with selects: a subnormal f16 is frac * 2^-24 (exact in f32), a
+// normal one rebiases its exponent, Inf / NaN keep their fraction.
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
-  uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
-  uint32_t exp = (h >> 10) & 0x1fu;
-  uint32_t frac = h & 0x3ffu;
-  uint32_t out;
-  if (exp == 0) {
-    if (frac == 0) {
-      out = sign;
-    } else {
-      // Normalise: move the leading one of frac up to bit 10.
-      int lead = 31 - __clz(frac);          // 0..9
-      int shift = 10 - lead;
-      uint32_t f = (frac << shift) & 0x3ffu;
-      out = sign | ((uint32_t)(127 - 14 - shift) << 23) | (f << 13);
-    }
-  } else if (exp == 0x1f) {
-    out = sign | 0x7f800000u | (frac << 13);
-  } else {
-    out = sign | ((exp + 112u) << 23) | (frac << 13);
-  }
-  return u2f(out);
+  const uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+  const uint32_t exp = (h >> 10) & 0x1fu;
+  const uint32_t frac = h & 0x3ffu;
+  const uint32_t normal = sign | ((exp + 112u) << 23) | (frac << 13);
+  const uint32_t sub = sign | f2u((float)frac * 0x1p-24f);
+  const uint32_t special = sign | 0x7f800000u | (frac << 13);
+  return u2f(exp == 0 ? sub : (exp == 0x1f ? special : normal));
 }
 
 // 8-lane finishing tree (det-num reduce.rs:36-38).
