@@ -81,6 +81,19 @@ __device__ __forceinline__ float scalbnf(float x, int n) {
   return x * u2f((uint32_t)(0x7f + n) << 23);
 }
 
+// v / d rounded to nearest, given rd = 1 / d rounded to nearest: q0 = v rd,
+// then one fma correction, q0 + (v - q0 d) rd (Markstein's theorem: with rd
+// correctly rounded and q0 within an ulp of the quotient, the corrected
+// value is the rounded quotient while nothing underflows).  Three
+// instructions where the division takes about ten, for a caller that
+// divides by one d many times.  tests/div_recip_check.c compares it with
+// the division over its caller's operands (the Q8A quantiser's).
+__device__ __forceinline__ float div_recip(float v, float d, float rd) {
+  const float q0 = v * rd;
+  const float r = __builtin_fmaf(-q0, d, v);
+  return __builtin_fmaf(r, rd, q0);
+}
+
 // exp_f32 (det-num math.rs:5-7): the FreeBSD e_expf method restated from
 // its published description -- round x/ln2 to k, reduce with a two-part
 // ln2, approximate with x*c/(2-c), c = x - x^2(P1 + x^2 P2), scale by 2^k.

@@ -24,21 +24,6 @@ struct QuantOut {
   int af_skew = 0;
 };
 
-// v / d rounded to nearest, given rd = 1 / d rounded to nearest: q0 = v rd,
-// then one fma correction, q0 + (v - q0 d) rd (Markstein's theorem: with rd
-// correctly rounded and q0 within an ulp of the quotient, the corrected
-// value is the rounded quotient while nothing underflows).  For the
-// quantiser's operands (d = amax / 127 >= 2^-92 / 127, |v| <= amax) the host
-// check in tests/test_div_recip.py compares it with the division: every
-// float v in [2^-100, amax] for a dozen amax, random pairs across the
-// exponent range, and every amax for d = amax / 127 itself.  For
-// |v| < 2^-100 both quotients are below 0.5 in magnitude and round to 0.
-__device__ __forceinline__ float div_recip(float v, float d, float rd) {
-  const float q0 = v * rd;
-  const float r = __builtin_fmaf(-q0, d, v);
-  return __builtin_fmaf(r, rd, q0);
-}
-
 // v: the lane's four elements; in: whether they exist; base: element offset
 // of the span (a multiple of 256 within the [T][n] array).
 __device__ __forceinline__ void quantize_span(const float v[4], bool in, size_t base, bool want_q8a,

@@ -1,4 +1,4 @@
-/* Host check of div_recip (detllm_amd/csrc/dtl_quant.h): q0 = v * rd,
+/* Host check of div_recip (detllm_amd/csrc/dtl_numerics.h): q0 = v * rd,
  * q1 = fma(fma(-q0, d, v), rd, q0) with rd = 1 / d must equal the rounded
  * quotient v / d for the Q8A quantiser's operands: d = amax / 127 with
  * amax >= 2^-92 and 2^-100 <= |v| <= amax; and d itself, amax / 127 by the

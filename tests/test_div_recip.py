@@ -1,8 +1,8 @@
-"""The quantiser's division by reciprocal and fma correction (div_recip in
-detllm_amd/csrc/dtl_quant.h) against correctly rounded division, on the
-host: tests/div_recip_check.c compares both over the quantiser's operand
-range (every third float dividend for four scales, 2^24 random pairs of
-both signs, every seventh scale for the scale's own division)."""
+"""Division by reciprocal and fma correction (div_recip in
+detllm_amd/csrc/dtl_numerics.h) against correctly rounded division, on the
+host: tests/div_recip_check.c compares both over its caller's operands (the
+Q8A quantiser: every third float dividend for four scales, 2^24 random
+pairs of both signs, every seventh scale for the scale's own division)."""
 import shutil
 import subprocess
 
