@@ -1372,11 +1372,18 @@ constexpr int kSplitDims = 16;    // dimensions per P.V workgroup
 
 // RoPE (lib.rs:2011-2051) of the query head and of the chunk's keys of its
 // group into LDS, from the raw projections; returns whether any input or
-// output is non-finite.
+// output is non-finite.  Each thread takes at most one rotated pair (the
+// launch has at least (kDecMaxT + 1) * 32 threads), whose table entries it
+// loads together with the raw rows, before the first barrier.
 __device__ bool split_rope_rows(const float* q, const RopeIn& R, int h, int g, int t, int KV, int H,
                                 int pb, float* qs, float (*kn)[64]) {
   constexpr int hd = 64;
   const int tid = threadIdx.x, nt = blockDim.x, half = R.rope_dim / 2;
+  const int np = (t + 2) * half;
+  const int p = tid < np ? tid : 0;
+  const int pr = half > 0 ? p / half : 0, pj = p - pr * half;
+  const int ppos = pr == 0 ? pb + t : pb + pr - 1;
+  const float c = R.rc[(size_t)ppos * half + pj], sn = R.rs[(size_t)ppos * half + pj];
   bool bad = false;
   for (int i = tid; i < (t + 2) * hd; i += nt) {
     const int r = i >> 6, d = i & 63;
@@ -1386,14 +1393,11 @@ __device__ bool split_rope_rows(const float* q, const RopeIn& R, int h, int g, i
     else kn[r - 1][d] = v;
   }
   __syncthreads();
-  for (int p = tid; p < (t + 2) * half; p += nt) {
-    const int r = p / half, j = p - r * half;
-    float* base = r == 0 ? qs : kn[r - 1];
-    const int ppos = r == 0 ? pb + t : pb + r - 1;
-    const int ia = R.split_half ? j : 2 * j;
-    const int ib = R.split_half ? j + half : 2 * j + 1;
+  if (tid < np) {
+    float* base = pr == 0 ? qs : kn[pr - 1];
+    const int ia = R.split_half ? pj : 2 * pj;
+    const int ib = R.split_half ? pj + half : 2 * pj + 1;
     const float x0 = base[ia], x1 = base[ib];
-    const float c = R.rc[(size_t)ppos * half + j], sn = R.rs[(size_t)ppos * half + j];
     const float y0 = x0 * c - x1 * sn;
     const float y1 = x0 * sn + x1 * c;
     bad |= any_nonfinite(y0, y1);
@@ -1420,6 +1424,23 @@ __global__ void __launch_bounds__(256) k_attn_split_scores(const float* q, RopeI
   const int pos = pb + t, len = pos + 1;
   const int j0 = b * kSplitKeys;
   if (j0 >= len) return;  // the grid covers the longest row the launch can see
+  // Eight lanes per key: lane r forms the 8-lane accumulator r (dims r,
+  // r + 8, ..., r + 56 in order); three shuffle levels give
+  // ((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)).  All four rounds' cached key rows
+  // are loaded before the RoPE phase, whose loads and barriers they then
+  // overlap (rows outside the cached part read row 0 and are replaced from
+  // LDS at use; a barrier waits for LDS only, not for these loads).
+  constexpr int kRounds = kSplitKeys / 32;
+  const float* keys = R.kc + ((size_t)layer * KV + g) * n_ctx * hd;
+  const int r = tid & 7, kq = tid >> 3;
+  float kb[kRounds][8];
+#pragma unroll
+  for (int d = 0; d < kRounds; d++) {
+    const int j = j0 + kq + 32 * d;
+    const float* kr = keys + (size_t)(j < pb ? j : 0) * hd + r;
+#pragma unroll
+    for (int u = 0; u < 8; u++) kb[d][u] = kr[8 * u];
+  }
   bool bad = split_rope_rows(q, R, h, g, t, KV, H, pb, qs, kn);
   if (h % G == 0 && pos / kSplitKeys == b && tid < hd) {
     const size_t off = (((size_t)layer * KV + g) * n_ctx + pos) * hd + tid;
@@ -1429,26 +1450,10 @@ __global__ void __launch_bounds__(256) k_attn_split_scores(const float* q, RopeI
     R.vc[off] = vv;
   }
   if (len > 1) {  // a single score is never formed (the output copies V)
-    const float* keys = R.kc + ((size_t)layer * KV + g) * n_ctx * hd;
     float* srow = scores + ((size_t)t * H + h) * n_ctx;
-    // Eight lanes per key: lane r forms the 8-lane accumulator r (dims r,
-    // r + 8, ..., r + 56 in order); three shuffle levels give
-    // ((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)).  All four rounds' key rows are
-    // loaded first (rows outside the cached part read row 0 and are
-    // replaced from LDS at use).
-    constexpr int kRounds = kSplitKeys / 32;
-    const int r = tid & 7, kq = tid >> 3;
     float qr[8];
 #pragma unroll
     for (int u = 0; u < 8; u++) qr[u] = qs[r + 8 * u];
-    float kb[kRounds][8];
-#pragma unroll
-    for (int d = 0; d < kRounds; d++) {
-      const int j = j0 + kq + 32 * d;
-      const float* kr = keys + (size_t)(j < pb ? j : 0) * hd + r;
-#pragma unroll
-      for (int u = 0; u < 8; u++) kb[d][u] = kr[8 * u];
-    }
 #pragma unroll
     for (int d = 0; d < kRounds; d++) {
       const int j = j0 + kq + 32 * d;
@@ -1476,12 +1481,12 @@ __global__ void __launch_bounds__(256) k_attn_split_scores(const float* q, RopeI
 // thread issues its loads first: the score row, then V as 4 x 4 blocks (four
 // rows of four dimensions), which arrive while the max runs and are stored
 // dimension-major (one float4 per row block and dimension).  The exps are
-// also stored chain-major (element j at chain j % 8, slot j / 8), so each
-// 8-lane Z chain reads its terms four at a time.  After p_j = e_j / Z the
-// products p_j * v_j[d] replace V in place (float4 by float4), and lanes 0-15
-// of wave 0 run the sixteen serial chains over them (chain_sum_lds: a
-// dependent add costs its latency, about 8.5 cycles, whatever feeds it, so
-// the products are formed beforehand by every thread).
+// also stored chain-major (element j at chain j % 8, slot j / 8) for the
+// eight Z chains.  After p_j = e_j / Z the products p_j * v_j[d] replace V
+// in place (float4 by float4), formed beforehand by every thread, and the
+// sixteen serial chains run over them.  The Z and P.V chains are DPP chains
+// (chain_group_lds: one chain per 16-lane row, each add's operand broadcast
+// from the lane holding it, about 5 cycles per dependent add).
 namespace {
 // Raw buffer loads with a byte bound: a read past num_records returns zeros
 // and generates no memory request.  Descriptor word 3 as for gfx9 targets.
@@ -1619,19 +1624,22 @@ __global__ void __launch_bounds__(kPvThreads) k_attn_split_pv(const float* score
       const int j = tid + kPvThreads * k;
       e[k] = j < len ? exp_clamped(pr[j < len ? j : 0] - mx) : 0.0f;
     }
+    // The chain-major rows are padded to the longest chain's length with
+    // +0.0 (e is zero past len), which no sum of exps changes.
 #pragma unroll
     for (int k = 0; k < kSplitMaxRows / kPvThreads; k++) {
       const int j = tid + kPvThreads * k;
-      if (j < len) {
-        pr[j] = e[k];
-        zcm[(j & 7) * L.zs + (j >> 3)] = e[k];
-      }
+      if (j < len) pr[j] = e[k];
+      if (j < ((len + 7) & ~7)) zcm[(j & 7) * L.zs + (j >> 3)] = e[k];
     }
   }
   __syncthreads();
-  if (tid < 8) {
-    const int cnt = (len - tid + 7) / 8;  // terms of chain tid
-    zc[tid] = chain_sum_lds(0.0f, zcm + tid * L.zs, cnt);
+  // The eight Z chains as DPP chains: chain c on the 16-lane row c % 4 of
+  // wave c / 4.
+  if (tid < 128) {
+    const int c = tid >> 4;
+    const float zs = chain_group_lds<16>(0.0f, zcm + c * L.zs, (len + 7) / 8);
+    if ((tid & 15) == 0) zc[c] = zs;
   }
   __syncthreads();
   const float z = finish_8lane(zc);
@@ -1654,10 +1662,15 @@ __global__ void __launch_bounds__(kPvThreads) k_attn_split_pv(const float* score
     }
   }
   __syncthreads();
-  if (wave == 0 && lane < kSplitDims) {
-    const float a = chain_sum_lds(0.0f, vt + lane * L.ld, len);
-    bad |= !finite(a);
-    o[lane] = a;
+  // The sixteen P.V chains as DPP chains: dimension d on the 16-lane row
+  // d % 4 of wave d / 4.
+  if (tid < 64 * (kSplitDims / 4)) {
+    const int d = tid >> 4;
+    const float a = chain_group_lds<16>(0.0f, vt + d * L.ld, len);
+    if ((tid & 15) == 0) {
+      bad |= !finite(a);
+      o[d] = a;
+    }
   }
   if (bad) flag(err, ERRBIT_NON_FINITE);
 }
@@ -2179,44 +2192,55 @@ __global__ void __launch_bounds__(256) k_cdf_bexp(const float* logits, const uin
   }
 }
 
-// Z = sum_f32_ref(e): lanes 0-7 of wave 0 each run one chain (i = c mod 8,
-// ascending) over a three-deep LDS ring that waves 1-3 fill from the
-// chain-major buffer.
+// Z = sum_f32_ref(e): chain c (i = c mod 8, ascending) runs on the 16-lane
+// row c % 4 of wave c / 4 as a DPP chain (chain_group_lds), over a three-deep
+// LDS ring that waves 2-3 fill from the chain-major buffer.
 __global__ void __launch_bounds__(256) k_cdf_z(int V, CdfScratch cs) {
-  // Lanes 0-7 of wave 0 run the eight chains; waves 1-3 stream the chain-
-  // major exps through a ring of LDS segments.  A producer thread holds the
-  // next segment in registers for a whole segment's worth of adds before it
-  // stores it, so the global-load latency never reaches the chain.
+  // A producer thread holds the next segment in registers for a whole
+  // segment's worth of adds before it stores it, so the global-load latency
+  // never reaches the chains.  Entries past a chain's own length are stored
+  // as +0.0, so all eight chains add the same number of terms (the longest
+  // chain's) without changing any sum's bits: a sum of non-negative exps
+  // that starts at +0.0 is never -0.0.
   constexpr int kSeg = 1024;  // elements per chain per ring slot
   constexpr int kSlots = 3;
-  constexpr int kProducers = 192;
+  constexpr int kChainThreads = 128;
+  constexpr int kProducers = 256 - kChainThreads;
   constexpr int kF4 = 8 * kSeg / 4;                            // float4 per segment
-  constexpr int kPer = (kF4 + kProducers - 1) / kProducers;    // per producer thread
+  constexpr int kPer = kF4 / kProducers;                       // per producer thread
+  static_assert(kF4 % kProducers == 0, "whole float4 rounds per producer");
   extern __shared__ __align__(16) float zring[];               // [kSlots][8][kSeg]
   __shared__ float zc[8];
   const int r = blockIdx.x, tid = threadIdx.x;
   const int v8 = cdf_v8(V);
   const float* e = cs.ebuf + (size_t)r * 8 * v8;
-  const int nseg = (v8 + kSeg - 1) / kSeg;
+  const int cnt_max = (V + 7) / 8;  // chain 0, the longest
+  const int nseg = (cnt_max + kSeg - 1) / kSeg;
   float4 pre[kPer];
   auto load = [&](int sg) {
 #pragma unroll
     for (int k = 0; k < kPer; k++) {
-      const int x = tid - 64 + kProducers * k;
+      const int x = tid - kChainThreads + kProducers * k;
       const int c = x / (kSeg / 4), j = sg * kSeg + 4 * (x % (kSeg / 4));
-      pre[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (x < kF4 && j + 3 < v8) pre[k] = *reinterpret_cast<const float4*>(e + (size_t)c * v8 + j);
+      const int cnt = (V - c + 7) / 8;  // elements of chain c
+      float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (j < v8) f = *reinterpret_cast<const float4*>(e + (size_t)c * v8 + j);
+      f.x = j < cnt ? f.x : 0.0f;
+      f.y = j + 1 < cnt ? f.y : 0.0f;
+      f.z = j + 2 < cnt ? f.z : 0.0f;
+      f.w = j + 3 < cnt ? f.w : 0.0f;
+      pre[k] = f;
     }
   };
   auto store = [&](int sg) {
     float* dst = zring + (size_t)(sg % kSlots) * 8 * kSeg;
 #pragma unroll
     for (int k = 0; k < kPer; k++) {
-      const int x = tid - 64 + kProducers * k;
-      if (x < kF4) reinterpret_cast<float4*>(dst)[x] = pre[k];  // [c][j]: x = c * kSeg / 4 + j / 4
+      const int x = tid - kChainThreads + kProducers * k;
+      reinterpret_cast<float4*>(dst)[x] = pre[k];  // [c][j]: x = c * kSeg / 4 + j / 4
     }
   };
-  if (tid >= 64) {
+  if (tid >= kChainThreads) {
     load(0);
     store(0);
     if (nseg > 1) {
@@ -2226,55 +2250,20 @@ __global__ void __launch_bounds__(256) k_cdf_z(int V, CdfScratch cs) {
     if (nseg > 2) load(2);
   }
   __syncthreads();
+  const int c = 4 * (tid >> 6) + ((tid & 63) >> 4);  // chain waves only
   float acc = 0.0f;
   for (int sg = 0; sg < nseg; sg++) {
-    if (tid >= 64) {
+    if (tid >= kChainThreads) {
       if (sg + 2 < nseg) store(sg + 2);  // slot of segment sg - 1, released at the last barrier
       if (sg + 3 < nseg) load(sg + 3);
-    } else if (tid < 8) {
-      const int c = tid;
-      const int cnt_total = (V - c + 7) / 8;  // elements of chain c
-      int cnt = cnt_total - sg * kSeg;
-      cnt = cnt < kSeg ? cnt : kSeg;
-      const float* my = zring + (size_t)(sg % kSlots) * 8 * kSeg + (size_t)c * kSeg;
-      int j = 0;
-      if (cnt == kSeg) {
-        // A full segment through a ring of twelve float4: each read is
-        // issued twelve float4 (48 adds) before its values are added, so the
-        // chain waits on its own adds, not on LDS.
-        constexpr int kRing = 12;
-        const float4* my4 = reinterpret_cast<const float4*>(my);
-        float4 v[kRing];
-#pragma unroll
-        for (int q = 0; q < kRing; q++) v[q] = my4[q];
-#pragma unroll
-        for (int q = 0; q < kSeg / 4; q++) {
-          const float4 w = v[q % kRing];
-          if (q + kRing < kSeg / 4) v[q % kRing] = my4[q + kRing];
-          acc += w.x;
-          acc += w.y;
-          acc += w.z;
-          acc += w.w;
-          // keeps the scheduler from sinking the read back to its use
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        j = kSeg;
-      }
-      for (; j + 16 <= cnt; j += 16) {
-        float4 f0 = *reinterpret_cast<const float4*>(my + j);
-        float4 f1 = *reinterpret_cast<const float4*>(my + j + 4);
-        float4 f2 = *reinterpret_cast<const float4*>(my + j + 8);
-        float4 f3 = *reinterpret_cast<const float4*>(my + j + 12);
-        acc += f0.x; acc += f0.y; acc += f0.z; acc += f0.w;
-        acc += f1.x; acc += f1.y; acc += f1.z; acc += f1.w;
-        acc += f2.x; acc += f2.y; acc += f2.z; acc += f2.w;
-        acc += f3.x; acc += f3.y; acc += f3.z; acc += f3.w;
-      }
-      for (; j < cnt; j++) acc += my[j];
+    } else {
+      int n = cnt_max - sg * kSeg;  // the same for every lane of the wave
+      n = n < kSeg ? n : kSeg;
+      acc = chain_group_lds<16>(acc, zring + (size_t)(sg % kSlots) * 8 * kSeg + (size_t)c * kSeg, n);
     }
     __syncthreads();
   }
-  if (tid < 8) zc[tid] = acc;
+  if (tid < kChainThreads && (tid & 15) == 0) zc[c] = acc;
   __syncthreads();
   if (tid == 0) cs.z[r] = finish_8lane(zc);
 }
