@@ -713,8 +713,11 @@ struct dtl_session {
   Lane lanes[kMaxLanes];
   int nlanes = 1;        // lanes set up (the rest stay empty)
   Lane* ln = &lanes[0];  // the lane the launches below go to
-  // Captured single-position forward (see forward_device), on lane 0.
-  hipGraphExec_t graph = nullptr;
+  // Captured single-position forwards (see forward_device), on lane 0:
+  // [0] for rows up to attention_fused_max_len() keys, [1] for the whole
+  // window.  graph_maxlen: the row bound of the graph being captured.
+  hipGraphExec_t graph[2] = {nullptr, nullptr};
+  int graph_maxlen = 0;
   bool graph_failed = false;
   int* pos_dev = nullptr;   // device copy of the position for the graph
   int* pos_host = nullptr;  // pinned staging for it
@@ -731,7 +734,8 @@ struct dtl_session {
                       (void*)L.h_cum, (void*)L.h_total, (void*)L.h_err, (void*)L.h_io})
         if (p) (void)hipHostFree(p);
     }
-    if (graph) (void)hipGraphExecDestroy(graph);
+    for (hipGraphExec_t g : graph)
+      if (g) (void)hipGraphExecDestroy(g);
     if (pos_host) (void)hipHostFree(pos_host);
   }
 };
@@ -976,19 +980,11 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
       if (after) HIP_TRY(hipStreamWaitEvent(st, after->kv_ready[l], 0));
       const RopeIn R{s->ln->k, s->ln->v, s->rope_cos, s->rope_sin, (int)c.rope_dim, c.split_half ? 1 : 0,
                      s->kc, s->vc};
-      // scores (with RoPE and the cache store), then softmax and P.V: two
-      // classes so the profiler times them apart
-      P.timed(st, "attention_scores", kv_rows * KV * hd * 4.0 + (double)T * (H + 3 * KV) * hd * 4.0,
-              kv_rows * H * hd, [&] {
+      P.timed(st, "attention_dec", 2.0 * kv_rows * KV * hd * 4.0 + (double)T * (2 * H + 3 * KV) * hd * 4.0,
+              2.0 * kv_rows * H * hd, [&] {
                 launch_attention_dec(s->ln->q, R, (int)l, T, (int)pos0, H, KV, (int)s->n_ctx,
-                                     c.attention_scale, s->ln->scores, s->ln->attn, pos_dev,
-                                     s->ln->err, st, 1);
-              });
-      P.timed(st, "attention_pv", kv_rows * KV * hd * 4.0 + (double)T * H * hd * 4.0, kv_rows * H * hd,
-              [&] {
-                launch_attention_dec(s->ln->q, R, (int)l, T, (int)pos0, H, KV, (int)s->n_ctx,
-                                     c.attention_scale, s->ln->scores, s->ln->attn, pos_dev,
-                                     s->ln->err, st, 2);
+                                     s->graph_maxlen, c.attention_scale, s->ln->scores, s->ln->attn,
+                                     pos_dev, s->ln->err, st);
               });
       if (record_kv) HIP_TRY(hipEventRecord(s->ln->kv_ready[l], st));
     } else {
@@ -1089,26 +1085,35 @@ int enqueue_forward(dtl_session* s, int T, size_t pos0, const int* pos_dev,
   return DTL_OK;
 }
 
-// Single-position forwards replay one captured graph of the whole pass: the
-// position reaches the kernels through s->pos_dev, copied in before each
-// replay.  DETLLM_NO_GRAPH=1 keeps the eager launches.
+// Single-position forwards replay a captured graph of the whole pass, one
+// for positions whose rows fit the one-launch decode attention and one for
+// the rest of the window: the position reaches the kernels through
+// s->pos_dev, copied in before each replay.  DETLLM_NO_GRAPH=1 keeps the
+// eager launches.
 bool graph_eligible(const dtl_session* s) {
   return !s->prof.on && !s->graph_failed && !env_flag("DETLLM_NO_GRAPH") &&
          attention_pos_dev_supported((int)s->m->head_dim, 1, (int)s->n_ctx);
 }
 
-int capture_decode_graph(dtl_session* s) {
+// The replayed forward of regime k serves positions below decode_graph_bound(k).
+int decode_graph_bound(const dtl_session* s, int k) {
+  const int fused = attention_fused_max_len();
+  return k == 0 && (size_t)fused < s->n_ctx ? fused : (int)s->n_ctx;
+}
+
+int capture_decode_graph(dtl_session* s, int k) {
   hipStream_t st = s->ln->stream;
+  s->graph_maxlen = decode_graph_bound(s, k);
   HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
   int rc = enqueue_forward(s, 1, 0, s->pos_dev);
   hipGraph_t g = nullptr;
   hipError_t e = hipStreamEndCapture(st, &g);
   if (rc == DTL_OK && e == hipSuccess && g)
-    e = hipGraphInstantiate(&s->graph, g, nullptr, nullptr, 0);
+    e = hipGraphInstantiate(&s->graph[k], g, nullptr, nullptr, 0);
   if (g) (void)hipGraphDestroy(g);
   if (rc != DTL_OK || e != hipSuccess) {
     (void)hipGetLastError();
-    s->graph = nullptr;
+    s->graph[k] = nullptr;
     s->graph_failed = true;
     return DTL_ERR_DEVICE;
   }
@@ -1127,11 +1132,12 @@ int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t po
   HIP_TRY(hipMemcpyAsync(s->ln->tokens, tokens_host, T * sizeof(uint32_t), hipMemcpyHostToDevice, st));
   bool replayed = false;
   if (T == 1 && graph_eligible(s)) {
-    if (!s->graph) (void)capture_decode_graph(s);
-    if (s->graph) {
+    const int k = pos0 < (size_t)decode_graph_bound(s, 0) ? 0 : 1;
+    if (!s->graph[k]) (void)capture_decode_graph(s, k);
+    if (s->graph[k]) {
       *s->pos_host = (int)pos0;
       HIP_TRY(hipMemcpyAsync(s->pos_dev, s->pos_host, sizeof(int), hipMemcpyHostToDevice, st));
-      HIP_TRY(hipGraphLaunch(s->graph, st));
+      HIP_TRY(hipGraphLaunch(s->graph[k], st));
       replayed = true;
     }
   }

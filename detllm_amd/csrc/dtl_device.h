@@ -212,16 +212,18 @@ struct RopeIn {
   float* kc;  // [layer][KV][n_ctx][hd] caches
   float* vc;
 };
-// part: 0 every launch, 1 the scores (and the cache store) only, 2 the
-// softmax and P.V only (the profiler times the two separately).
 // Whether launch_attention_dec takes this shape (hd 64, at most four
 // positions, the score row within LDS).
 bool attention_dec_applies(int hd, int T, int pos0, int n_ctx, bool pos_in_device);
-// scores: scratch of T * H * n_ctx floats.
+// Rows up to this many keys run the decode attention in one launch (scores
+// in LDS); longer rows run the split pair (scores through memory).
+int attention_fused_max_len();
+// scores: scratch of T * H * n_ctx floats.  maxlen_dev: with pos_dev, the
+// longest row (pos + 1) the launches may see; the caller keeps every
+// position it copies to pos_dev below it.
 void launch_attention_dec(const float* q, const RopeIn& R, int layer, int T, int pos0, int H,
-                          int KV, int n_ctx, float scale, float* scores, float* out,
-                          const int* pos_dev, int* err, hipStream_t s,
-                          int part = 0);
+                          int KV, int n_ctx, int maxlen_dev, float scale, float* scores, float* out,
+                          const int* pos_dev, int* err, hipStream_t s);
 // Whether the decode attention (launch_attention_dec) takes the position
 // from device memory for this shape (graph replay of single-position forwards).
 bool attention_pos_dev_supported(int hd, int T, int n_ctx);

@@ -1675,6 +1675,196 @@ __global__ void __launch_bounds__(kPvThreads) k_attn_split_pv(const float* score
   if (bad) flag(err, ERRBIT_NON_FINITE);
 }
 
+// Decode attention in one launch for rows of at most kFusedMaxLen keys: the
+// work of k_attn_split_scores and k_attn_split_pv for (16 dimensions, head,
+// position) in one workgroup.  Each of a head's four workgroups forms the
+// whole score row itself (the scores never leave LDS), which costs a read of
+// the head's cached keys per workgroup: cheap for short rows, where the
+// second launch would cost more than the repeated scores.  Values and order
+// are those of the split pair: the same 8-lane dots and scaling, max,
+// clamped exps, Z chains, divisions and P.V chains.  The cache store of the
+// positions' key and value rows is done by the first workgroup of each group
+// (dimension block 0 of the group's first head); no workgroup reads a cache
+// row at or past the launch's first position, which come from the raw
+// projections instead (keys after RoPE in LDS).
+constexpr int kFusedMaxLen = 1024;
+constexpr int kFusedVBlocks = kFusedMaxLen / kPvThreads;  // 4-row V blocks per thread
+constexpr int kFusedKeyBatch = 4;                         // rounds of 128 keys per batch of loads
+static_assert(kFusedMaxLen % (128 * kFusedKeyBatch) == 0 && kFusedVBlocks >= 1, "whole batches");
+
+__global__ void __launch_bounds__(kPvThreads) k_attn_fused(const float* q, RopeIn R, int layer,
+                                                           int pos0, int H, int KV, int n_ctx,
+                                                           int maxlen, float scale, float* out,
+                                                           const int* pos_dev, int* err) {
+  // [len4] scores -> probabilities, [8][zs] exps chain-major, [16][ld] V (then
+  // the products) by dimension
+  extern __shared__ __align__(16) float pr[];
+  constexpr int NW = kPvThreads / 64;
+  constexpr int hd = 64;
+  __shared__ __align__(16) float qs[64];
+  __shared__ __align__(16) float kn[kDecMaxT][64];
+  __shared__ float red[NW];
+  __shared__ float zc[8];
+  const int dg = blockIdx.x, h = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int G = H / KV, g = h / G;
+  const int pb = pos_dev ? *pos_dev : pos0;
+  const int pos = pb + t, len = pos + 1;
+  const int d0 = dg * kSplitDims;
+  const SplitLayout L = split_layout(maxlen);
+  float* zcm = pr + L.zoff;
+  float* vt = pr + L.voff;
+  const float* keys = R.kc + ((size_t)layer * KV + g) * n_ctx * hd;
+  const float* vals = R.vc + ((size_t)layer * KV + g) * n_ctx * hd;
+  float* o = out + ((size_t)t * H + h) * hd + d0;
+  bool bad = false;
+  // Loads first.  V rows of the cached part through buffer loads bounded by
+  // pb rows (past it they return zeros without a memory request); the raw V
+  // rows of the chunk positions this row sees (row pb + tid / 16, dimension
+  // d0 + tid % 16); the first batch of cached key rows (eight lanes per key,
+  // rows outside the cached part read row 0 and are replaced from LDS).
+  const BufRsrc vrs = buf_rsrc(vals, (uint32_t)pb * hd * 4u);
+  const int jq = tid >> 2, c = 4 * (tid & 3);
+  float4 vb[kFusedVBlocks][4];
+#pragma unroll
+  for (int i = 0; i < kFusedVBlocks; i++)
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+      vb[i][r] = buf_load_f32x4(vrs, (4 * (256 * i + jq) + r) * hd * 4 + (d0 + c) * 4);
+  const int nv = len - pb;  // t + 1 chunk rows
+  const int vj = (tid >> 4) < nv ? (tid >> 4) : 0;
+  const float vraw = R.v[((size_t)vj * KV + g) * hd + d0 + (tid & 15)];
+  const int r8 = tid & 7, kq = tid >> 3;
+  float kb[kFusedKeyBatch][8];
+#pragma unroll
+  for (int d = 0; d < kFusedKeyBatch; d++) {
+    const int j = kq + 128 * d;
+    const float* kr = keys + (size_t)(j < pb ? j : 0) * hd + r8;
+#pragma unroll
+    for (int u = 0; u < 8; u++) kb[d][u] = kr[8 * u];
+  }
+  bad |= split_rope_rows(q, R, h, g, t, KV, H, pb, qs, kn);
+  if (dg == 0 && h % G == 0 && tid < hd) {
+    const size_t off = (((size_t)layer * KV + g) * n_ctx + pos) * hd + tid;
+    const float kv = kn[t][tid], vv = R.v[((size_t)t * KV + g) * hd + tid];
+    bad |= any_nonfinite(kv, vv);
+    R.kc[off] = kv;
+    R.vc[off] = vv;
+  }
+  if (len == 1) {  // a single score copies V exactly (lib.rs:2319-2321)
+    if (tid < kSplitDims) o[tid] = vraw;
+    if (bad) flag(err, ERRBIT_NON_FINITE);
+    return;
+  }
+  // Scores, 128 keys per round, straight into the probability row.
+  float qr[8];
+#pragma unroll
+  for (int u = 0; u < 8; u++) qr[u] = qs[r8 + 8 * u];
+  float mx = -__builtin_huge_valf();
+  for (int jb = 0; jb < len; jb += 128 * kFusedKeyBatch) {
+    if (jb > 0) {
+#pragma unroll
+      for (int d = 0; d < kFusedKeyBatch; d++) {
+        const int j = jb + kq + 128 * d;
+        const float* kr = keys + (size_t)(j < pb ? j : 0) * hd + r8;
+#pragma unroll
+        for (int u = 0; u < 8; u++) kb[d][u] = kr[8 * u];
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < kFusedKeyBatch; d++) {
+      const int j = jb + kq + 128 * d;
+      const int jv = j - pb < 0 ? 0 : (j - pb < kDecMaxT ? j - pb : kDecMaxT - 1);
+      float acc = 0.0f;
+#pragma unroll
+      for (int u = 0; u < 8; u++) acc += qr[u] * (j < pb ? kb[d][u] : kn[jv][r8 + 8 * u]);
+      const float s1 = acc + __shfl_xor(acc, 1);
+      const float s2 = s1 + __shfl_xor(s1, 2);
+      const float s3 = s2 + __shfl_xor(s2, 4);
+      if (r8 == 0 && j < len) {
+        const float sv = s3 * scale;
+        bad |= !finite(sv);
+        pr[j] = sv;
+        mx = fmaxf(mx, sv);
+      }
+    }
+  }
+  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  if (lane == 0) red[wave] = mx;
+  // V, dimension-major: each 4 x 4 block transposed in registers, one float4
+  // per dimension (rows past len are stored too; no chain reads them)
+#pragma unroll
+  for (int i = 0; i < kFusedVBlocks; i++) {
+    const int j4 = 4 * (256 * i + jq);
+    if (j4 < len) {
+      *reinterpret_cast<float4*>(vt + (c + 0) * L.ld + j4) =
+          make_float4(vb[i][0].x, vb[i][1].x, vb[i][2].x, vb[i][3].x);
+      *reinterpret_cast<float4*>(vt + (c + 1) * L.ld + j4) =
+          make_float4(vb[i][0].y, vb[i][1].y, vb[i][2].y, vb[i][3].y);
+      *reinterpret_cast<float4*>(vt + (c + 2) * L.ld + j4) =
+          make_float4(vb[i][0].z, vb[i][1].z, vb[i][2].z, vb[i][3].z);
+      *reinterpret_cast<float4*>(vt + (c + 3) * L.ld + j4) =
+          make_float4(vb[i][0].w, vb[i][1].w, vb[i][2].w, vb[i][3].w);
+    }
+  }
+  __syncthreads();
+  // the chunk rows, which the bounded loads above returned as zeros
+  if (tid < nv * kSplitDims) vt[(tid & 15) * L.ld + pb + (tid >> 4)] = vraw;
+  mx = red[0];
+#pragma unroll
+  for (int w = 1; w < NW; w++) mx = fmaxf(mx, red[w]);
+  {
+    float e[kFusedVBlocks];
+#pragma unroll
+    for (int k = 0; k < kFusedVBlocks; k++) {
+      const int j = tid + kPvThreads * k;
+      e[k] = j < len ? exp_clamped(pr[j < len ? j : 0] - mx) : 0.0f;
+    }
+    // The chain-major rows are padded to the longest chain's length with
+    // +0.0 (e is zero past len), which no sum of exps changes.
+#pragma unroll
+    for (int k = 0; k < kFusedVBlocks; k++) {
+      const int j = tid + kPvThreads * k;
+      if (j < len) pr[j] = e[k];
+      if (j < ((len + 7) & ~7)) zcm[(j & 7) * L.zs + (j >> 3)] = e[k];
+    }
+  }
+  __syncthreads();
+  if (tid < 128) {
+    const int cz = tid >> 4;
+    const float zsum = chain_group_lds<16>(0.0f, zcm + cz * L.zs, (len + 7) / 8);
+    if ((tid & 15) == 0) zc[cz] = zsum;
+  }
+  __syncthreads();
+  const float z = finish_8lane(zc);
+  bad |= !finite(z) || z == 0.0f;
+  for (int j = tid; j < len; j += kPvThreads) {
+    const float p = pr[j] / z;
+    bad |= !finite(p);
+    pr[j] = p;
+  }
+  __syncthreads();
+  {
+    const int d = tid >> 6;
+    float* vd = vt + d * L.ld;
+    for (int j4 = 4 * lane; j4 < len; j4 += 256) {
+      const float4 pv = *reinterpret_cast<const float4*>(pr + j4);
+      const float4 vv = *reinterpret_cast<const float4*>(vd + j4);
+      *reinterpret_cast<float4*>(vd + j4) = make_float4(pv.x * vv.x, pv.y * vv.y, pv.z * vv.z, pv.w * vv.w);
+    }
+  }
+  __syncthreads();
+  if (tid < 64 * (kSplitDims / 4)) {
+    const int d = tid >> 4;
+    const float a = chain_group_lds<16>(0.0f, vt + d * L.ld, len);
+    if ((tid & 15) == 0) {
+      bad |= !finite(a);
+      o[d] = a;
+    }
+  }
+  if (bad) flag(err, ERRBIT_NON_FINITE);
+}
+
 size_t attention_hd64_smem(int G, int sc_stride) {
   return ((size_t)G * sc_stride + 2 * kA64Buf + (size_t)G * 64) * sizeof(float);
 }
@@ -1697,14 +1887,27 @@ bool attention_dec_applies(int hd, int T, int pos0, int n_ctx, bool pos_in_devic
   return hd == 64 && T <= kDecMaxT && smem <= kDecMaxScoreBytes;
 }
 
+int attention_fused_max_len() { return kFusedMaxLen; }
+
 void launch_attention_dec(const float* q, const RopeIn& R, int layer, int T, int pos0, int H,
-                          int KV, int n_ctx, float scale, float* scores, float* out,
-                          const int* pos_dev, int* err, hipStream_t s, int part) {
-  // With the position in device memory the grids and the score buffer are
-  // sized for the whole window.
-  const int maxlen = pos_dev ? n_ctx : pos0 + T;
+                          int KV, int n_ctx, int maxlen_dev, float scale, float* scores, float* out,
+                          const int* pos_dev, int* err, hipStream_t s) {
+  // With the position in device memory the grids and LDS are sized for the
+  // longest row the replays may see.
+  const int maxlen = pos_dev ? maxlen_dev : pos0 + T;
   const size_t smem = (size_t)maxlen * sizeof(float);
   const size_t pv_smem = split_pv_smem(maxlen);
+  if (maxlen <= kFusedMaxLen) {
+    static bool attr_fused_set = false;
+    if (!attr_fused_set) {
+      (void)hipFuncSetAttribute((const void*)k_attn_fused, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                158 * 1024);
+      attr_fused_set = true;
+    }
+    launch_kernel(k_attn_fused, dim3(64 / kSplitDims, H, T), dim3(kPvThreads), pv_smem, s, q, R, layer,
+                  pos0, H, KV, n_ctx, maxlen, scale, out, pos_dev, err);
+    return;
+  }
   if (maxlen <= kSplitMaxRows && pv_smem <= 158 * 1024) {
     static bool attr_pv_set = false;
     if (!attr_pv_set) {
@@ -1712,12 +1915,10 @@ void launch_attention_dec(const float* q, const RopeIn& R, int layer, int T, int
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 158 * 1024);
       attr_pv_set = true;
     }
-    if (part != 2)
-      launch_kernel(k_attn_split_scores, dim3((maxlen + kSplitKeys - 1) / kSplitKeys, H, T),
-                    dim3(256), 0, s, q, R, layer, pos0, H, KV, n_ctx, scale, scores, pos_dev, err);
-    if (part != 1)
-      launch_kernel(k_attn_split_pv, dim3(64 / kSplitDims, H, T), dim3(kPvThreads), pv_smem, s, scores, R,
-                    layer, pos0, H, KV, n_ctx, maxlen, out, pos_dev, err);
+    launch_kernel(k_attn_split_scores, dim3((maxlen + kSplitKeys - 1) / kSplitKeys, H, T), dim3(256), 0,
+                  s, q, R, layer, pos0, H, KV, n_ctx, scale, scores, pos_dev, err);
+    launch_kernel(k_attn_split_pv, dim3(64 / kSplitDims, H, T), dim3(kPvThreads), pv_smem, s, scores, R,
+                  layer, pos0, H, KV, n_ctx, maxlen, out, pos_dev, err);
     return;
   }
   // Longer windows: one workgroup per (head, position).
@@ -1727,9 +1928,8 @@ void launch_attention_dec(const float* q, const RopeIn& R, int layer, int T, int
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDecMaxScoreBytes);
     attr_dec_set = true;
   }
-  if (part != 1)
-    launch_kernel(k_attention_dec, dim3(H, T), dim3(kDecThreads), smem, s, q, R, layer, pos0, H, KV,
-                  n_ctx, scale, out, pos_dev, err);
+  launch_kernel(k_attention_dec, dim3(H, T), dim3(kDecThreads), smem, s, q, R, layer, pos0, H, KV,
+                n_ctx, scale, out, pos_dev, err);
 }
 
 bool attention_quantizes_q8a(int hd, int H, int KV, int T, int pos0, int n_ctx) {
