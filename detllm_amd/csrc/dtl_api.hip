@@ -719,6 +719,7 @@ struct dtl_session {
   hipGraphExec_t graph[2] = {nullptr, nullptr};
   int graph_maxlen = 0;
   bool graph_failed = false;
+  bool overlapped = false;  // dtl_forward_ranges has chunks in flight on several lanes
   int* pos_dev = nullptr;   // device copy of the position for the graph
   int* pos_host = nullptr;  // pinned staging for it
   Profiler prof;
@@ -805,6 +806,7 @@ DevAct session_act(dtl_session* s, const float* x) {
   a.af = s->ln->af;
   a.qk = s->ln->qk;
   a.dk = s->ln->dk;
+  a.overlapped = s->overlapped;
   return a;
 }
 
@@ -1545,8 +1547,10 @@ int dtl_forward_ranges(dtl_session* s, const uint32_t* tokens, size_t n, size_t 
     ~Restore() {
       for (int li = 0; li < s->nlanes; li++) (void)hipStreamSynchronize(s->lanes[li].stream);
       s->ln = &s->lanes[0];
+      s->overlapped = false;
     }
   } restore{s};
+  s->overlapped = s->nlanes > 1;
   for (Lane& L : s->lanes) {
     L.rows_valid = 0;
     L.cdf_ready_row = SIZE_MAX;

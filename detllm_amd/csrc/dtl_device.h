@@ -86,6 +86,9 @@ struct DevAct {
   const float* af;   // [T][cols]      Q8A dequantised: da * qa (Q4_K chain input)
   const int8_t* qk;  // [T][cols]      Q8_K quants
   const float* dk;   // [T][cols/256]  Q8_K scales
+  // Other chunks' launches share the chip with this one (the pipelined
+  // encode): the GEMMs then pick tiles for an occupied chip.
+  bool overlapped = false;
 };
 
 enum GemmEpilogue : int { EPI_STORE = 0, EPI_BIAS = 1, EPI_RESIDUAL = 2 };

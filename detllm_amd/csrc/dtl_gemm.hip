@@ -913,11 +913,14 @@ int rows_per_wave(int rows) {
 //   pair   (gate + up)     4 x 16 lanes, 2 positions x (gate, up) per lane,
 //                          4 waves over 32 positions x 16 rows
 //   cat    (wq + wk)       8 x 8 lanes, 1 x 2 chains, 2 x 2 waves
-// Blocked lanes run fewer waves than one chain per lane: alone, a chunk's
-// launch is up to 45% slower (wo/ffn_down 58 vs 40 ms per step at one
-// chain per lane), but with the other chunks' launches filling the CUs the
-// step is 10% faster (123.7 vs 137.6 ms), the LDS bytes per multiply-add
-// being what bounds the overlapped launches.
+// Blocked lanes run fewer waves than one chain per lane: with the other
+// chunks' launches filling the CUs the LDS bytes per multiply-add bound the
+// launches, and the blocked tiles make the step 10% faster (123.7 vs 137.6
+// ms), but a launch that has the chip to itself then has too few waves.  A
+// launch with no other chunk in flight (dtl_forward_chunk, the decode-size
+// chunks) runs one chain per lane instead, 8 x 8 lanes, 2 x 2 waves over 16
+// positions x 16 rows: wo / ffn_down 59.9 -> 41.6 ms and wq + wk 26.3 ->
+// 24.2 ms per chunk-at-a-time step.  The gate + up pair keeps its tile.
 template <int PW, int PP, int RP, int WP, int WR, int MODE>
 void launch_q4k_f32m(const Q4kF32Args& a, int rows_total, hipStream_t s) {
   constexpr int RB = WR * RP * 64 / PW, PB = WP * PW * PP;
@@ -926,8 +929,9 @@ void launch_q4k_f32m(const Q4kF32Args& a, int rows_total, hipStream_t s) {
 }
 
 template <int MODE>
-void launch_q4k_f32w(const Q4kF32Args& a, hipStream_t s) {
+void launch_q4k_f32w(const Q4kF32Args& a, bool overlapped, hipStream_t s) {
   const int rows_total = MODE == MODE_CAT ? a.rows0 + a.rows1 : a.rows0;
+  if (MODE != MODE_PAIR && !overlapped) return launch_q4k_f32m<8, 1, 1, 2, 2, MODE>(a, rows_total, s);
   if (MODE == MODE_SINGLE) return launch_q4k_f32m<8, 1, 2, 4, 1, MODE>(a, rows_total, s);
   if (MODE == MODE_PAIR) return launch_q4k_f32m<4, 2, 1, 4, 1, MODE>(a, rows_total, s);
   launch_q4k_f32m<8, 1, 2, 2, 2, MODE>(a, rows_total, s);
@@ -965,7 +969,7 @@ void launch_gemm_tok(const DevMat& W, const DevAct& A, int T, float* out, const 
   DevMat none{};
   if (W.type == kGgmlQ4K && W.w32) {
     launch_q4k_f32w<MODE_SINGLE>(
-        q4k_args(W, nullptr, A, T, out, nullptr, nullptr, bias, nullptr, epi, err), s);
+        q4k_args(W, nullptr, A, T, out, nullptr, nullptr, bias, nullptr, epi, err), A.overlapped, s);
     return;
   }
   if (W.type == kGgmlQ6K && W.planes) {
@@ -1032,7 +1036,7 @@ void launch_gemm_pair_swiglu_q4k(const DevMat& G, const DevMat& U, const DevAct&
                                  float* u, float* ffo, int* err, hipStream_t s) {
   if (G.w32 && U.w32 && !g && !u) {
     launch_q4k_f32w<MODE_PAIR>(
-        q4k_args(G, &U, A, T, nullptr, nullptr, ffo, nullptr, nullptr, EPI_STORE, err), s);
+        q4k_args(G, &U, A, T, nullptr, nullptr, ffo, nullptr, nullptr, EPI_STORE, err), A.overlapped, s);
     return;
   }
   int R = rows_per_wave(2 * G.rows) >= 2 ? 2 : 1;
@@ -1050,7 +1054,8 @@ bool launch_gemm_cat_q4k(const DevMat& W0, const DevMat& W1, const DevAct& A, in
   if (T < 16 || W0.type != kGgmlQ4K || W1.type != kGgmlQ4K || !W0.w32 || !W1.w32 ||
       W0.cols != W1.cols)
     return false;
-  launch_q4k_f32w<MODE_CAT>(q4k_args(W0, &W1, A, T, out0, out1, nullptr, bias0, bias1, epi, err), s);
+  launch_q4k_f32w<MODE_CAT>(q4k_args(W0, &W1, A, T, out0, out1, nullptr, bias0, bias1, epi, err),
+                            A.overlapped, s);
   return true;
 }
 

@@ -1680,15 +1680,17 @@ __global__ void __launch_bounds__(kPvThreads) k_attn_split_pv(const float* score
 // position) in one workgroup.  Each of a head's four workgroups forms the
 // whole score row itself (the scores never leave LDS), which costs a read of
 // the head's cached keys per workgroup: cheap for short rows, where the
-// second launch would cost more than the repeated scores.  Values and order
+// second launch would cost more than the repeated scores (on Qwen2.5-0.5B
+// and TinyLlama-1.1B shapes the one launch is faster up to about 512 keys,
+// the pair beyond).  Values and order
 // are those of the split pair: the same 8-lane dots and scaling, max,
 // clamped exps, Z chains, divisions and P.V chains.  The cache store of the
 // positions' key and value rows is done by the first workgroup of each group
 // (dimension block 0 of the group's first head); no workgroup reads a cache
 // row at or past the launch's first position, which come from the raw
 // projections instead (keys after RoPE in LDS).
-constexpr int kFusedMaxLen = 1024;
-constexpr int kFusedVBlocks = kFusedMaxLen / kPvThreads;  // 4-row V blocks per thread
+constexpr int kFusedMaxLen = 512;
+constexpr int kFusedVBlocks = (kFusedMaxLen + kPvThreads - 1) / kPvThreads;  // 4-row V blocks per thread
 constexpr int kFusedKeyBatch = 4;                         // rounds of 128 keys per batch of loads
 static_assert(kFusedMaxLen % (128 * kFusedKeyBatch) == 0 && kFusedVBlocks >= 1, "whole batches");
 
