@@ -2424,9 +2424,9 @@ __global__ void __launch_bounds__(256) k_cdf_z(int V, CdfScratch cs) {
     for (int k = 0; k < kPer; k++) {
       const int x = tid - kChainThreads + kProducers * k;
       const int c = x / (kSeg / 4), j = sg * kSeg + 4 * (x % (kSeg / 4));
-      const int cnt = (V - c + 7) / 8;  // elements of chain c
-      float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (j < v8) f = *reinterpret_cast<const float4*>(e + (size_t)c * v8 + j);
+      const int cnt = (V - c + 7) / 8;  // elements of chain c (at most v8)
+      // unconditional: a load under a branch waits for every load before it
+      float4 f = *reinterpret_cast<const float4*>(e + (size_t)c * v8 + (j < v8 ? j : 0));
       f.x = j < cnt ? f.x : 0.0f;
       f.y = j + 1 < cnt ? f.y : 0.0f;
       f.z = j + 2 < cnt ? f.z : 0.0f;

@@ -257,20 +257,40 @@ __device__ __forceinline__ float chain_group_lds(float a, const float* v, int n)
   auto load = [&](int b) {
     const int e = b * B + 4 * k;
     const int ec = e < n ? e : 0;
-    float4 x = *reinterpret_cast<const float4*>(v + (SKEW ? ec + ((ec >> 6) << 2) : ec));
+    return *reinterpret_cast<const float4*>(v + (SKEW ? ec + ((ec >> 6) << 2) : ec));
+  };
+  // Terms past n are zeroed just before their group's adds, not at the
+  // read: a select on a value right after its read would wait for the read.
+  auto live = [&](float4 x, int b) {
+    const int e = b * B + 4 * k;
     x.x = e < n ? x.x : 0.0f;
     x.y = e + 1 < n ? x.y : 0.0f;
     x.z = e + 2 < n ? x.z : 0.0f;
     x.w = e + 3 < n ? x.w : 0.0f;
     return x;
   };
-  // two reads in flight ahead of the adds
+  // Two reads in flight ahead of the adds, over pairs of full groups (every
+  // term below n).  The scheduling barrier after each read keeps it where it
+  // is: without one the compiler merges the reads that feed the loop-carried
+  // slot into one read at the top of the loop, next to the adds that wait
+  // for it.
+  const int nfull = n / B;
   float4 x0 = load(0), x1 = load(1);
-  for (int b = 0; b < nb; b += 2) {
+  __builtin_amdgcn_sched_barrier(0);
+  int b = 0;
+  for (; b + 1 < nfull; b += 2) {
     a = chain_group_add<R>(a, x0);
     x0 = load(b + 2);
-    if (b + 1 < nb) a = chain_group_add<R>(a, x1);
+    __builtin_amdgcn_sched_barrier(0);
+    a = chain_group_add<R>(a, x1);
     x1 = load(b + 3);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (b < nfull) {  // one full group, then perhaps a partial one
+    a = chain_group_add<R>(a, x0);
+    if (b + 1 < nb) a = chain_group_add<R>(a, live(x1, b + 1));
+  } else if (b < nb) {  // a partial group
+    a = chain_group_add<R>(a, live(x0, b));
   }
   return a;
 }
