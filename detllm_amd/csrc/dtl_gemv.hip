@@ -868,14 +868,22 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
   }
   // the producers' weights: the first NS stages are in flight before the
   // activations load
+  // Units past the first round of kPcProducers: when there are at most half
+  // as many, each goes to two lanes as halves (the sixteen elements of one
+  // of its two sub-blocks), so that a wave's second round costs half a unit
+  // (the gate+up launch: 352 units, 32 past the first round).
+  const int E = WPU - kPcProducers;
+  const bool halves = E > 0 && 2 * E <= kPcProducers;
+  const int f2 = halves ? (ptid < 2 * E ? kPcProducers + (ptid >> 1) : WPU) : ptid + kPcProducers;
+  const int hi2 = ptid & 1;
   int m0, m1;
-  const int r0 = row_of(ptid, &m0), r1 = row_of(ptid + kPcProducers, &m1);
+  const int r0 = row_of(ptid, &m0), r1 = row_of(f2, &m1);
   const uint8_t* qr0 = (m0 ? p.q1 : p.q0) + (size_t)r0 * nb * 128;
   const uint8_t* hr0 = (m0 ? p.h1 : p.h0) + (size_t)r0 * nb * 16;
   const uint8_t* qr1 = (m1 ? p.q1 : p.q0) + (size_t)r1 * nb * 128;
   const uint8_t* hr1 = (m1 ? p.h1 : p.h0) + (size_t)r1 * nb * 16;
   const int u0 = ptid < WPU ? ptid % UPR : 0;
-  const int u1 = ptid + kPcProducers < WPU ? (ptid + kPcProducers) % UPR : 0;
+  const int u1 = f2 < WPU ? f2 % UPR : 0;
   uint4 qa0[NS], ha0[NS], qa1[NS], ha1[NS];
 #define DTL_PC_LOAD(slot, k)                                                                \
   do {                                                                                      \
@@ -972,6 +980,40 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
       }
     }
   };
+  // One sub-block of unit f (hi: the high nibbles, columns c + 32 ..), with
+  // the values and order of the full unit's.
+  auto products_half = [&](float* pb, int k, int f, int hi, uint4 qv, uint4 hv) {
+    if (f >= WPU) return;
+    const int r = f / UPR;
+    const int b = k * (SL / 2) + 16 * (f % UPR);
+    const int g = (b & 127) >> 5;
+    const int c = (b >> 7) * 256 + 64 * g + (b & 31) - k * SL;
+    const float d = f16_to_f32((uint16_t)(hv.x & 0xffffu)), dmin = f16_to_f32((uint16_t)(hv.x >> 16));
+    int sc, mn;
+    q4k_scale_min3(hv.y, hv.z, hv.w, 2 * g + hi, &sc, &mn);
+    const float dsc = d * (float)sc, dm = dmin * (float)mn;
+    const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+    float w[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const uint32_t byte = (qw[i >> 2] >> (8 * (i & 3))) & 0xffu;
+      w[i] = dsc * (float)((byte >> (4 * hi)) & 0x0fu) - dm;
+    }
+    // c + 32 lies in the 64-column group of c
+    const int cs = q4k_pc_skew(c) + 32 * hi;
+    const int e = q4k_pc_skew(k * SL);
+    for (int t = 0; t < T; t++) {
+      const float* at = as + (size_t)t * ACS + e;
+      float* pr = pb + (r + NR * t) * LDP;
+      float4 a[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) a[q] = *reinterpret_cast<const float4*>(at + cs + 4 * q);
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        *reinterpret_cast<float4*>(pr + cs + 4 * q) = make_float4(
+            w[4 * q] * a[q].x, w[4 * q + 1] * a[q].y, w[4 * q + 2] * a[q].z, w[4 * q + 3] * a[q].w);
+    }
+  };
   if (producer) {
     // Stage k's products go to buffer k & 1; the barrier after them hands
     // the buffer to the chain waves, which add it while the next stage forms.
@@ -982,7 +1024,12 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
         float* pb = prod + (size_t)(k & 1) * NR * T * LDP;
         const int kk = k < nst ? k : nst - 1;
         products(pb, kk, ptid, qa0[u], ha0[u]);
-        if (kPcMaxUnits > 1) products(pb, kk, ptid + kPcProducers, qa1[u], ha1[u]);
+        if (kPcMaxUnits > 1) {
+          if (halves)
+            products_half(pb, kk, f2, hi2, qa1[u], ha1[u]);
+          else
+            products(pb, kk, f2, qa1[u], ha1[u]);
+        }
         DTL_PC_LOAD(u, k + NS);
         __syncthreads();
       }
