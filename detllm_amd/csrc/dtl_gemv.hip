@@ -200,10 +200,13 @@ __global__ void __launch_bounds__(256) k_gemv_q8(DevMat W, const int8_t* __restr
 // ---------------------------------------------------------------------------
 // Q8_0 streaming variant for tall matrices with at most 1024 columns (the
 // output projection of the small-vocabulary-heavy shapes): every wave walks
-// groups of R rows in a grid-stride loop, loading the next group's weights
-// and scales while it reduces the current one, so HBM sees a steady stream
-// rather than one burst per wave.  Lane c owns 16-byte chunk c of every row
-// (nchunk <= 64), so the activation chunk is loaded once per wave.
+// groups of R rows in a grid-stride loop with two groups' weights and scales
+// in flight, refilling a slot as soon as its group is reduced.  Lane c owns
+// 16-byte chunk c of every row (nchunk <= 64), so the activation chunk is
+// loaded once per wave.  Every load is unconditional (lanes past the row's
+// chunks and groups past the end read valid addresses whose values are not
+// stored): a load under a branch makes the compiler wait for every load in
+// flight at the branch, which took the prefetch away.
 template <int R>
 __global__ void __launch_bounds__(256) k_gemv_q8_0_stream(DevMat W, const int8_t* __restrict__ qa,
                                                           const float* __restrict__ da, float* out,
@@ -215,69 +218,73 @@ __global__ void __launch_bounds__(256) k_gemv_q8_0_stream(DevMat W, const int8_t
   const int nchunk = 2 * nb;
   const int c = lane, b = c >> 1;
   const bool cv = c < nchunk;
+  const int cc = cv ? c : 0, bc = cv ? b : 0;  // clamped chunk and block of this lane
   const int nbs = nb_stride(nb);
   float* mine = vb + (size_t)wave * R * nbs;
   const int ngroups = (rows + R - 1) / R;
   const int stride = gridDim.x * 4;
-  uint4 a0 = make_uint4(0, 0, 0, 0);
-  float dact = 0.0f;
-  if (cv) {
-    a0 = *(const uint4*)(qa + (size_t)t * cols + (size_t)c * 16);
-    dact = da[(size_t)t * nb + b];
-  }
-  uint4 w4[2][R];
-  uint16_t dsc[2][R];
-  auto load = [&](int slot, int g) {
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-      int row = g * R + r;
-      row = row < rows ? row : rows - 1;
-      w4[slot][r] = make_uint4(0, 0, 0, 0);
-      dsc[slot][r] = 0;
-      if (cv) {
-        w4[slot][r] = *(const uint4*)((const int8_t*)W.w + (size_t)row * cols + (size_t)c * 16);
-        dsc[slot][r] = W.d16[(size_t)row * nb + b];
-      }
-    }
-  };
-  auto reduce = [&](int slot, int g) {
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-      int isum = 0;
-      isum = dot4(w4[slot][r].x, a0.x, isum);
-      isum = dot4(w4[slot][r].y, a0.y, isum);
-      isum = dot4(w4[slot][r].z, a0.z, isum);
-      isum = dot4(w4[slot][r].w, a0.w, isum);
-      isum += __shfl_xor(isum, 1);
-      if (cv && !(c & 1)) mine[r * nbs + b] = (f16_to_f32(dsc[slot][r]) * dact) * (float)isum;
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    if (lane < R) {
-      const int row = g * R + lane;
-      if (row < rows) {
-        float v = chain_sum_lds(0.0f, mine + lane * nbs, nb);
-        if (!epilogue(v, out, (size_t)t * rows + row, bias, row, epi)) flag(err, ERRBIT_NON_FINITE);
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-  };
   int g = blockIdx.x * 4 + wave;
   if (g >= ngroups) return;
-  load(0, g);
+  const uint4 a0 = *(const uint4*)(qa + (size_t)t * cols + (size_t)cc * 16);
+  const float dact = da[(size_t)t * nb + bc];
+  const int8_t* wbase = (const int8_t*)W.w + (size_t)cc * 16;
+  const uint16_t* dbase = W.d16 + bc;
+  uint4 w0[R], w1[R];
+  // scales as 32-bit values: packed two to a register, each pair would be
+  // waited for right after its loads are issued
+  uint32_t s0[R], s1[R];
+  // group gg's rows, the group clamped to the last one
+#define DTL_STREAM_LOAD(WV, SV, GG)                                        \
+  do {                                                                    \
+    const int gc_ = (GG) < ngroups ? (GG) : ngroups - 1;                  \
+    _Pragma("unroll") for (int r = 0; r < R; r++) {                       \
+      int row = gc_ * R + r;                                              \
+      row = row < rows ? row : rows - 1;                                  \
+      WV[r] = *(const uint4*)(wbase + (size_t)row * cols);                 \
+      SV[r] = dbase[(size_t)row * nb];                                    \
+    }                                                                     \
+  } while (0)
+#define DTL_STREAM_REDUCE(WV, SV, GG)                                                           \
+  do {                                                                                         \
+    _Pragma("unroll") for (int r = 0; r < R; r++) {                                            \
+      int isum = 0;                                                                            \
+      isum = dot4(WV[r].x, a0.x, isum);                                                         \
+      isum = dot4(WV[r].y, a0.y, isum);                                                         \
+      isum = dot4(WV[r].z, a0.z, isum);                                                         \
+      isum = dot4(WV[r].w, a0.w, isum);                                                         \
+      isum += __shfl_xor(isum, 1);                                                             \
+      if (cv && !(c & 1)) mine[r * nbs + b] = (f16_to_f32((uint16_t)SV[r]) * dact) * (float)isum;        \
+    }                                                                                          \
+    __builtin_amdgcn_wave_barrier();                                                           \
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");                                     \
+    if (lane < R) {                                                                            \
+      const int row = (GG) * R + lane;                                                         \
+      if (row < rows) {                                                                        \
+        float v = chain_sum_lds(0.0f, mine + lane * nbs, nb);                                  \
+        if (!epilogue(v, out, (size_t)t * rows + row, bias, row, epi)) flag(err, ERRBIT_NON_FINITE); \
+      }                                                                                        \
+    }                                                                                          \
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");                                     \
+    __builtin_amdgcn_wave_barrier();                                                           \
+  } while (0)
+  DTL_STREAM_LOAD(w0, s0, g);
+  DTL_STREAM_LOAD(w1, s1, g + stride);
   for (;;) {
-    const int gn = g + stride;
-    if (gn < ngroups) load(1, gn);
-    reduce(0, g);
-    if (gn >= ngroups) break;
-    g = gn;
-    const int gn2 = g + stride;
-    if (gn2 < ngroups) load(0, gn2);
-    reduce(1, g);
-    if (gn2 >= ngroups) break;
-    g = gn2;
+    DTL_STREAM_REDUCE(w0, s0, g);
+    __builtin_amdgcn_sched_barrier(0);
+    DTL_STREAM_LOAD(w0, s0, g + 2 * stride);
+    __builtin_amdgcn_sched_barrier(0);
+    g += stride;
+    if (g >= ngroups) break;
+    DTL_STREAM_REDUCE(w1, s1, g);
+    __builtin_amdgcn_sched_barrier(0);
+    DTL_STREAM_LOAD(w1, s1, g + 2 * stride);
+    __builtin_amdgcn_sched_barrier(0);
+    g += stride;
+    if (g >= ngroups) break;
   }
+#undef DTL_STREAM_LOAD
+#undef DTL_STREAM_REDUCE
 }
 
 // ---------------------------------------------------------------------------
