@@ -170,6 +170,9 @@ GEMV_CASES = [
     # the activations, so the one-lane-per-row Q4_K kernel serves it
     (12, 20, 5632, 8),
     (14, 50, 2048, 1), (14, 9, 5632, 2), (14, 20, 512, 64), (14, 300, 256, 1), (14, 33, 4096, 1),
+    # Q6_K decode at full TinyLlama ffn_down size (T = 8), odd row counts, and
+    # a 16384-row matrix (the split-superblock kernel's largest)
+    (14, 2048, 5632, 8), (14, 1000, 5632, 3), (14, 2049, 5632, 1), (14, 16384, 2048, 1),
     # Q8_0 / Q4_0 on the int8 matrix cores (T >= 16): odd block counts (a
     # half block pair), row tiles of 16 / 32 / 64, partial position tiles
     (8, 40, 32, 16), (8, 37, 96, 33), (8, 2100, 160, 17), (8, 8200, 64, 16), (8, 100, 896, 64),
