@@ -51,6 +51,24 @@ __device__ __forceinline__ bool store_epilogue(float v, float* out, size_t o, co
   return ok && finite(v);
 }
 
+// The value the epilogue adds (bias[r], or the residual out[o]), read
+// without a branch so that a kernel can load it ahead, long before its
+// store: a load under a branch is waited for at once, and one such wait per
+// output put a round trip per output on the kernel's tail.  With EPI_STORE
+// the read (of out[o]) goes unused.
+__device__ __forceinline__ float epilogue_operand(const float* out, size_t o, const float* bias, int r,
+                                                  int epi) {
+  return *(epi == EPI_BIAS ? bias + r : out + o);
+}
+
+__device__ __forceinline__ bool store_epilogue_pre(float v, float pre, float* out, size_t o, int epi) {
+  bool ok = finite(v);
+  if (epi == EPI_BIAS) v = v + pre;
+  else if (epi == EPI_RESIDUAL) v = pre + v;
+  out[o] = v;
+  return ok && finite(v);
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -698,6 +716,18 @@ __global__ void __launch_bounds__(256) k_q6k_mfma(const int8_t* __restrict__ pla
   Ops r0, r1;
   load(r0, last(0));
   load(r1, last(1));
+  // the epilogue's operands of this wave's outputs (see the final combine),
+  // in flight with the first superblocks
+  float pre[NT];
+#pragma unroll
+  for (int k = 0; k < NT; k++) {
+    const int o = wave + 4 * k, j = o >> 2, i = o & 3;
+    int pos = p0 + 16 * j + li;
+    pos = pos < T ? pos : T - 1;
+    int row = rt * 16 + 4 * q + i;
+    row = row < rows ? row : rows - 1;
+    pre[k] = epilogue_operand(out, (size_t)pos * rows + row, bias, row, epi);
+  }
 #define DTL_MFMA_STEP(r, i)                                                                \
   compute(r, (i) < nb);                                                                    \
   __builtin_amdgcn_sched_barrier(0);                                                       \
@@ -718,15 +748,16 @@ __global__ void __launch_bounds__(256) k_q6k_mfma(const int8_t* __restrict__ pla
   // Final combine 0 + sums[0] + ... + sums[7] in class order; the four
   // waves split the (position tile, register) outputs.
   bool ok = true;
-  for (int o = wave; o < NT * 4; o += 4) {
-    const int j = o >> 2, i = o & 3;
+#pragma unroll
+  for (int k = 0; k < NT; k++) {
+    const int o = wave + 4 * k, j = o >> 2, i = o & 3;
     const int pos = p0 + 16 * j + li;
     const int row = rt * 16 + 4 * q + i;
     if (row < rows && pos < T) {
       float v = 0.0f;
 #pragma unroll
       for (int c = 0; c < 8; c++) v += part[c][j][i][lane];
-      ok &= store_epilogue(v, out, (size_t)pos * rows + row, bias, row, epi);
+      ok &= store_epilogue_pre(v, pre[k], out, (size_t)pos * rows + row, epi);
     }
   }
   if (!ok) flag(err, ERRBIT_NON_FINITE);
@@ -747,7 +778,7 @@ __global__ void __launch_bounds__(256) k_q6k_mfma(const int8_t* __restrict__ pla
 // and K quarter l / 16 (16 bytes); result register i of lane l is row
 // 4 (l / 16) + i, position l % 16.  A wave covers 16 rows x 16 NT
 // positions; a workgroup 4 / (4 / NT) row tiles x 64 positions.
-template <int NT>
+template <int NT, bool EVEN>
 __global__ void __launch_bounds__(256) k_q8_mfma(const int8_t* __restrict__ w8,
                                                  const uint16_t* __restrict__ d16, int rows, int nb,
                                                  const int8_t* __restrict__ qa,
@@ -789,10 +820,14 @@ __global__ void __launch_bounds__(256) k_q8_mfma(const int8_t* __restrict__ w8,
   // Operands of one block pair; the next pair's are in flight while the
   // current one is multiplied.  In an odd last pair the second block's
   // quarters re-read the first block's bytes and are zeroed.
+  // EVEN (an even block count, so every pair is whole and starts at an even
+  // block): the pair's two weight scales of a row are one 32-bit load and
+  // its two activation scales one 64-bit load (each load costs issue time;
+  // a value packed from two loads would be waited for as soon as loaded).
   struct Ops {
     dtl_v4i a;
     dtl_v4i b[NT];
-    uint16_t dw[2][4];
+    uint32_t dw[2][4];  // EVEN: dw[0][i] holds both halves
     float dav[2][NT];
   };
   auto load = [&](Ops& o, int pr) {
@@ -803,15 +838,26 @@ __global__ void __launch_bounds__(256) k_q8_mfma(const int8_t* __restrict__ w8,
 #pragma unroll
     for (int j = 0; j < NT; j++) o.b[j] = *(const dtl_v4i*)(bsrc[j] + off);
     const int b1 = two ? b0 + 1 : b0;
+    if constexpr (EVEN) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      o.dw[0][i] = dwsrc[i][b0];
-      o.dw[1][i] = dwsrc[i][b1];
-    }
+      for (int i = 0; i < 4; i++) o.dw[0][i] = *(const uint32_t*)(dwsrc[i] + b0);
 #pragma unroll
-    for (int j = 0; j < NT; j++) {
-      o.dav[0][j] = dsrc[j][b0];
-      o.dav[1][j] = dsrc[j][b1];
+      for (int j = 0; j < NT; j++) {
+        const float2 d2 = *(const float2*)(dsrc[j] + b0);
+        o.dav[0][j] = d2.x;
+        o.dav[1][j] = d2.y;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        o.dw[0][i] = dwsrc[i][b0];
+        o.dw[1][i] = dwsrc[i][b1];
+      }
+#pragma unroll
+      for (int j = 0; j < NT; j++) {
+        o.dav[0][j] = dsrc[j][b0];
+        o.dav[1][j] = dsrc[j][b1];
+      }
     }
   };
   // valid[h]: whether block 2 pr + h exists; a missing block adds +0.0f
@@ -823,7 +869,8 @@ __global__ void __launch_bounds__(256) k_q8_mfma(const int8_t* __restrict__ w8,
       const dtl_v4i a = (q >> 1) == h ? o.a : zero;
       float dw[4];
 #pragma unroll
-      for (int i = 0; i < 4; i++) dw[i] = f16_to_f32(o.dw[h][i]);
+      for (int i = 0; i < 4; i++)
+        dw[i] = f16_to_f32((uint16_t)(EVEN ? (h == 0 ? o.dw[0][i] & 0xffffu : o.dw[0][i] >> 16) : o.dw[h][i]));
 #pragma unroll
       for (int j = 0; j < NT; j++) {
         const dtl_v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, o.b[j], zero, 0, 0, 0);
@@ -848,6 +895,20 @@ __global__ void __launch_bounds__(256) k_q8_mfma(const int8_t* __restrict__ w8,
     load(r2, last(2));
     load(r3, last(3));
   }
+  // the epilogue's operands (clamped positions and rows), in flight with the
+  // first block pairs
+  float pre[NT][4];
+#pragma unroll
+  for (int j = 0; j < NT; j++) {
+    int pos = p0 + 16 * j + li;
+    pos = pos < T ? pos : T - 1;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      int row = row0 + 4 * q + i;
+      row = row < rows ? row : rows - 1;
+      pre[j][i] = epilogue_operand(out, (size_t)pos * rows + row, bias, row, epi);
+    }
+  }
 #define DTL_MFMA_STEP(r, i)                                                                \
   compute(r, (i) < np, 2 * (i) + 1 < nb);                                                  \
   __builtin_amdgcn_sched_barrier(0);                                                       \
@@ -870,7 +931,7 @@ __global__ void __launch_bounds__(256) k_q8_mfma(const int8_t* __restrict__ w8,
     for (int i = 0; i < 4; i++) {
       const int row = row0 + 4 * q + i;
       if (row < rows && pos < T)
-        ok &= store_epilogue(sums[j][i], out, (size_t)pos * rows + row, bias, row, epi);
+        ok &= store_epilogue_pre(sums[j][i], pre[j][i], out, (size_t)pos * rows + row, epi);
     }
   }
   if (!ok) flag(err, ERRBIT_NON_FINITE);
@@ -959,6 +1020,23 @@ Q4kF32Args q4k_args(const DevMat& W0, const DevMat* W1, const DevAct& A, int T, 
 }
 }  // namespace
 
+namespace {
+template <bool EVEN>
+void launch_q8_mfma(const int8_t* w8, const DevMat& W, const DevAct& A, int T, float* out, const float* bias,
+                    int epi, int* err, hipStream_t s) {
+  const int py = (T + 63) / 64;
+  if (W.rows >= 8192)
+    launch_kernel((k_q8_mfma<4, EVEN>), dim3((W.rows + 63) / 64, py), dim3(256), 0, s, w8, W.d16, W.rows,
+                  W.nb, A.qa, A.da, T, out, bias, epi, err);
+  else if (W.rows >= 2048)
+    launch_kernel((k_q8_mfma<2, EVEN>), dim3((W.rows + 31) / 32, py), dim3(256), 0, s, w8, W.d16, W.rows,
+                  W.nb, A.qa, A.da, T, out, bias, epi, err);
+  else
+    launch_kernel((k_q8_mfma<1, EVEN>), dim3((W.rows + 15) / 16, py), dim3(256), 0, s, w8, W.d16, W.rows,
+                  W.nb, A.qa, A.da, T, out, bias, epi, err);
+}
+}  // namespace
+
 bool gemm_tok_supported(const DevMat& W) {
   return W.type == kGgmlQ4K || W.type == kGgmlQ6K || W.type == kGgmlQ8_0 ||
          (W.type == kGgmlQ4_0 && W.i8);
@@ -989,16 +1067,10 @@ void launch_gemm_tok(const DevMat& W, const DevAct& A, int T, float* out, const 
     // Q8_0 / Q4_0 on the int8 matrix cores: one workgroup per 64 positions
     // and 16 (short matrices: every wave its own 16 positions), 32 or 64 rows.
     const int8_t* w8 = W.type == kGgmlQ8_0 ? (const int8_t*)W.w : W.i8;
-    const dim3 gy(1, (T + 63) / 64);
-    if (W.rows >= 8192)
-      launch_kernel(k_q8_mfma<4>, dim3((W.rows + 63) / 64, gy.y), dim3(256), 0, s, w8, W.d16, W.rows,
-                    W.nb, A.qa, A.da, T, out, bias, epi, err);
-    else if (W.rows >= 2048)
-      launch_kernel(k_q8_mfma<2>, dim3((W.rows + 31) / 32, gy.y), dim3(256), 0, s, w8, W.d16, W.rows,
-                    W.nb, A.qa, A.da, T, out, bias, epi, err);
+    if (W.nb % 2 == 0)
+      launch_q8_mfma<true>(w8, W, A, T, out, bias, epi, err, s);
     else
-      launch_kernel(k_q8_mfma<1>, dim3((W.rows + 15) / 16, gy.y), dim3(256), 0, s, w8, W.d16, W.rows,
-                    W.nb, A.qa, A.da, T, out, bias, epi, err);
+      launch_q8_mfma<false>(w8, W, A, T, out, bias, epi, err, s);
     return;
   }
   int R = rows_per_wave(W.rows);
