@@ -59,6 +59,23 @@ __device__ __forceinline__ bool epilogue(float v, float* out, size_t o, const fl
   return ok && finite(v);
 }
 
+// The value the epilogue adds (bias[r], or the residual out[o]), read without
+// a branch so that a kernel can load it at its start: read at the end it put
+// a round trip after the last chain.  With EPI_STORE the read (of out[o])
+// goes unused.
+__device__ __forceinline__ float epilogue_operand(const float* out, size_t o, const float* bias, int r,
+                                                  int epi) {
+  return *(epi == EPI_BIAS ? bias + r : out + o);
+}
+
+__device__ __forceinline__ bool epilogue_pre(float v, float pre, float* out, size_t o, int epi) {
+  bool ok = finite(v);
+  if (epi == EPI_BIAS) v = v + pre;
+  else if (epi == EPI_RESIDUAL) v = pre + v;
+  out[o] = v;
+  return ok && finite(v);
+}
+
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
@@ -85,6 +102,10 @@ __global__ void __launch_bounds__(256) k_gemv_q8(DevMat W, const int8_t* __restr
   float* mine = vb + (size_t)wave * R * nbs;
   const int8_t* arow = qa + (size_t)t * cols;
   const float* drow = da + (size_t)t * nb;
+  // the epilogue operand of this lane's row (lanes below R), loaded first
+  int prow = row0 + (lane < R ? lane : 0);
+  prow = prow < rows ? prow : rows - 1;
+  const float pre = epilogue_operand(out, (size_t)t * rows + prow, bias, prow, epi);
   // Q8_0: a 32-byte block is two 16-byte chunks (lanes c, c^1); Q4_0: one
   // 16-byte block of nibbles per lane.  A pass covers 64 chunks.
   const int nchunk = TYPE == kGgmlQ8_0 ? 2 * nb : nb;
@@ -192,7 +213,7 @@ __global__ void __launch_bounds__(256) k_gemv_q8(DevMat W, const int8_t* __restr
     const int row = row0 + lane;
     if (row < rows) {
       float v = chain_sum_lds(0.0f, mine + lane * nbs, nb);
-      if (!epilogue(v, out, (size_t)t * rows + row, bias, row, epi)) flag(err, ERRBIT_NON_FINITE);
+      if (!epilogue_pre(v, pre, out, (size_t)t * rows + row, epi)) flag(err, ERRBIT_NON_FINITE);
     }
   }
 }
@@ -424,6 +445,8 @@ __global__ void __launch_bounds__(256) k_gemv_q6k_split(DevMat W, const int8_t* 
   for (int k = 0; k < 8; k++) aw[k] = act[8 * k + 4 * h + pp];
   const uint16_t dw = W.d16[(size_t)r * nsb + sbl];
   const float da = dk[(size_t)t * nsb + sbl];
+  // the epilogue operand (thread 0 stores the row), loaded with the weights
+  const float pre = epilogue_operand(out, (size_t)t * rows + r, bias, r, epi);
   const uint32_t qlw[8] = {qa4.x, qa4.y, qa4.z, qa4.w, qb4.x, qb4.y, qb4.z, qb4.w};
   const uint32_t qhw[8] = {ha4.x, ha4.y, ha4.z, ha4.w, hb4.x, hb4.y, hb4.z, hb4.w};
   int aux[8];
@@ -470,7 +493,7 @@ __global__ void __launch_bounds__(256) k_gemv_q6k_split(DevMat W, const int8_t* 
     float v = 0.0f;
 #pragma unroll
     for (int l = 0; l < 8; l++) v += sums[l];
-    if (!epilogue(v, out, (size_t)t * rows + r, bias, r, epi)) flag(err, ERRBIT_NON_FINITE);
+    if (!epilogue_pre(v, pre, out, (size_t)t * rows + r, epi)) flag(err, ERRBIT_NON_FINITE);
   }
 }
 
@@ -1291,6 +1314,19 @@ __global__ void __launch_bounds__(64 * NW) k_gemv_q8f(FusedMats M, FusedIn in, i
   }
   const int nchunk = TYPE == kGgmlQ8_0 ? 2 * nb : nb;
   bool bad = false;
+  // the epilogue operand of this lane's row (lanes below R; the pair stores
+  // its SwiGLU product and reads nothing)
+  float pre = 0.0f;
+  if (!PAIR) {
+    int gr = row0 + (lane < R ? lane : 0);
+    gr = gr < M.total_rows ? gr : M.total_rows - 1;
+    const int mi = gr < M.row_end[0] ? 0 : (gr < M.row_end[1] ? 1 : 2);
+    const int row = gr - (mi == 0 ? 0 : (mi == 1 ? M.row_end[0] : M.row_end[1]));
+    const int rows = mi == 0 ? M.rows[0] : (mi == 1 ? M.rows[1] : M.rows[2]);
+    pre = epilogue_operand(mi == 0 ? M.out[0] : (mi == 1 ? M.out[1] : M.out[2]), (size_t)t * rows + row,
+                           mi == 0 ? M.bias[0] : (mi == 1 ? M.bias[1] : M.bias[2]), row,
+                           mi == 0 ? M.epi[0] : (mi == 1 ? M.epi[1] : M.epi[2]));
+  }
   // One chunk column of 64 lanes per pass (batching several passes' loads
   // measured slower: the extra registers cost more than the round trips).
   constexpr int NI = 1;
@@ -1391,7 +1427,8 @@ __global__ void __launch_bounds__(64 * NW) k_gemv_q8f(FusedMats M, FusedIn in, i
         const int epi = mi == 0 ? M.epi[0] : (mi == 1 ? M.epi[1] : M.epi[2]);
         const int rows = mi == 0 ? M.rows[0] : (mi == 1 ? M.rows[1] : M.rows[2]);
         const float v = chain_sum_lds(0.0f, mine + lane * nbs, nb);
-        if (!epilogue(v, out, (size_t)t * rows + row, bias, row, epi)) bad = true;
+        (void)bias;
+        if (!epilogue_pre(v, pre, out, (size_t)t * rows + row, epi)) bad = true;
       }
     }
   }
