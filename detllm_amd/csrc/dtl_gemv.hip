@@ -111,41 +111,35 @@ __global__ void __launch_bounds__(256) k_gemv_q8(DevMat W, const int8_t* __restr
   const int nchunk = TYPE == kGgmlQ8_0 ? 2 * nb : nb;
   struct Pass {
     uint4 w4[R];
-    uint16_t dsc[R];
+    uint32_t dsc[R];  // 32-bit: packed two to a register, a pair is waited for when loaded
     uint4 a0, a1;
     float dact;
   };
   // Every load of a pass (R weight chunks, their block scales, the
-  // activation and its scale) is issued before any of its arithmetic.
+  // activation and its scale) is issued before any of its arithmetic, and
+  // unconditionally: lanes past the row's chunks read its last chunk and
+  // store nothing (a load under a branch is waited for before the next one).
   auto load = [&](Pass& P, int c0) __attribute__((always_inline)) {
     const int c = c0 + lane;
-    const bool cv = c < nchunk;
-    const int b = TYPE == kGgmlQ8_0 ? c >> 1 : c;
+    const int cl = c < nchunk ? c : nchunk - 1;
+    const int b = TYPE == kGgmlQ8_0 ? cl >> 1 : cl;
 #pragma unroll
     for (int r = 0; r < R; r++) {
       const int row = row0 + r < rows ? row0 + r : rows - 1;
-      P.w4[r] = make_uint4(0, 0, 0, 0);
-      P.dsc[r] = 0;
-      if (cv) {
-        if (TYPE == kGgmlQ8_0)
-          P.w4[r] = *(const uint4*)((const int8_t*)W.w + (size_t)row * cols + (size_t)c * 16);
-        else
-          P.w4[r] = *(const uint4*)((const uint8_t*)W.w + ((size_t)row * nb + c) * 16);
-        P.dsc[r] = W.d16[(size_t)row * nb + b];
-      }
+      if (TYPE == kGgmlQ8_0)
+        P.w4[r] = *(const uint4*)((const int8_t*)W.w + (size_t)row * cols + (size_t)cl * 16);
+      else
+        P.w4[r] = *(const uint4*)((const uint8_t*)W.w + ((size_t)row * nb + cl) * 16);
+      P.dsc[r] = W.d16[(size_t)row * nb + b];
     }
-    P.a0 = make_uint4(0, 0, 0, 0);
-    P.a1 = make_uint4(0, 0, 0, 0);
-    P.dact = 0.0f;
-    if (cv) {
-      if (TYPE == kGgmlQ8_0) {
-        P.a0 = *(const uint4*)(arow + (size_t)c * 16);
-      } else {
-        P.a0 = *(const uint4*)(arow + (size_t)c * 32);
-        P.a1 = *(const uint4*)(arow + (size_t)c * 32 + 16);
-      }
-      P.dact = drow[b];
+    if (TYPE == kGgmlQ8_0) {
+      P.a0 = *(const uint4*)(arow + (size_t)cl * 16);
+      P.a1 = make_uint4(0, 0, 0, 0);
+    } else {
+      P.a0 = *(const uint4*)(arow + (size_t)cl * 32);
+      P.a1 = *(const uint4*)(arow + (size_t)cl * 32 + 16);
     }
+    P.dact = drow[b];
   };
   auto reduce = [&](const Pass& P, int c0) __attribute__((always_inline)) {
     const int c = c0 + lane;
@@ -186,7 +180,7 @@ __global__ void __launch_bounds__(256) k_gemv_q8(DevMat W, const int8_t* __restr
         isum -= 8 * asum;
       }
       const bool writer = TYPE == kGgmlQ8_0 ? cv && !(c & 1) : cv;
-      if (writer && row0 + r < rows) mine[r * nbs + b] = (f16_to_f32(P.dsc[r]) * P.dact) * (float)isum;
+      if (writer && row0 + r < rows) mine[r * nbs + b] = (f16_to_f32((uint16_t)P.dsc[r]) * P.dact) * (float)isum;
     }
   };
   // Rows of up to kPre passes (8192 Q8_0 columns) with few rows per wave:
@@ -195,9 +189,9 @@ __global__ void __launch_bounds__(256) k_gemv_q8(DevMat W, const int8_t* __restr
   const int npass = (nchunk + 63) / 64;
   if (kPre > 1 && npass <= kPre) {
     Pass P[kPre];
+    // passes past npass reload pass 0 (unconditional loads) and are not reduced
 #pragma unroll
-    for (int p = 0; p < kPre; p++)
-      if (p < npass) load(P[p], 64 * p);
+    for (int p = 0; p < kPre; p++) load(P[p], p < npass ? 64 * p : 0);
 #pragma unroll
     for (int p = 0; p < kPre; p++)
       if (p < npass) reduce(P[p], 64 * p);
