@@ -1482,11 +1482,13 @@ __global__ void __launch_bounds__(256) k_attn_split_scores(const float* q, RopeI
 // rows of four dimensions), which arrive while the max runs and are stored
 // dimension-major (one float4 per row block and dimension).  The exps are
 // also stored chain-major (element j at chain j % 8, slot j / 8) for the
-// eight Z chains.  After p_j = e_j / Z the products p_j * v_j[d] replace V
-// in place (float4 by float4), formed beforehand by every thread, and the
-// sixteen serial chains run over them.  The Z and P.V chains are DPP chains
-// (chain_group_lds: one chain per 16-lane row, each add's operand broadcast
-// from the lane holding it, about 5 cycles per dependent add).
+// eight Z chains.  After p_j = e_j / Z the sixteen serial P.V chains run
+// over p and the dimension-major V, each product p_j * v_j[d] formed just
+// before its add (a separate pass writing the products back into LDS was
+// bound by LDS bandwidth: 2.4k cycles at 1500 keys).  The Z and P.V chains
+// are DPP chains (chain_group_lds / chain_group_dot_lds: one chain per
+// 16-lane row, each add's operand broadcast from the lane holding it, about
+// 5 cycles per dependent add).
 namespace {
 // Raw buffer loads with a byte bound: a read past num_records returns zeros
 // and generates no memory request.  Descriptor word 3 as for gfx9 targets.
@@ -1650,23 +1652,11 @@ __global__ void __launch_bounds__(kPvThreads) k_attn_split_pv(const float* score
     pr[j] = p;
   }
   __syncthreads();
-  // products p_j * v_j[d], in place, a float4 (four j of one d) at a time:
-  // 64 threads per dimension
-  {
-    const int d = tid >> 6;
-    float* vd = vt + d * L.ld;
-    for (int j4 = 4 * lane; j4 < len; j4 += 256) {
-      const float4 pv = *reinterpret_cast<const float4*>(pr + j4);
-      const float4 vv = *reinterpret_cast<const float4*>(vd + j4);
-      *reinterpret_cast<float4*>(vd + j4) = make_float4(pv.x * vv.x, pv.y * vv.y, pv.z * vv.z, pv.w * vv.w);
-    }
-  }
-  __syncthreads();
-  // The sixteen P.V chains as DPP chains: dimension d on the 16-lane row
-  // d % 4 of wave d / 4.
+  // The sixteen P.V chains as DPP chains, each product formed just before
+  // its add: dimension d on the 16-lane row d % 4 of wave d / 4.
   if (tid < 64 * (kSplitDims / 4)) {
     const int d = tid >> 4;
-    const float a = chain_group_lds<16>(0.0f, vt + d * L.ld, len);
+    const float a = chain_group_dot_lds<16>(0.0f, pr, vt + d * L.ld, len);
     if ((tid & 15) == 0) {
       bad |= !finite(a);
       o[d] = a;
@@ -1846,19 +1836,9 @@ __global__ void __launch_bounds__(kPvThreads) k_attn_fused(const float* q, RopeI
     pr[j] = p;
   }
   __syncthreads();
-  {
-    const int d = tid >> 6;
-    float* vd = vt + d * L.ld;
-    for (int j4 = 4 * lane; j4 < len; j4 += 256) {
-      const float4 pv = *reinterpret_cast<const float4*>(pr + j4);
-      const float4 vv = *reinterpret_cast<const float4*>(vd + j4);
-      *reinterpret_cast<float4*>(vd + j4) = make_float4(pv.x * vv.x, pv.y * vv.y, pv.z * vv.z, pv.w * vv.w);
-    }
-  }
-  __syncthreads();
   if (tid < 64 * (kSplitDims / 4)) {
     const int d = tid >> 4;
-    const float a = chain_group_lds<16>(0.0f, vt + d * L.ld, len);
+    const float a = chain_group_dot_lds<16>(0.0f, pr, vt + d * L.ld, len);
     if ((tid & 15) == 0) {
       bad |= !finite(a);
       o[d] = a;

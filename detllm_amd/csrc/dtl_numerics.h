@@ -295,6 +295,52 @@ __device__ __forceinline__ float chain_group_lds(float a, const float* v, int n)
   return a;
 }
 
+// a += p[j] * v[j] for j = 0 .. n-1 in order as a DPP chain (one chain per
+// row of R lanes, as chain_group_lds): each lane reads a float4 of p and of
+// v, forms the four rounded products fl(p[j] * v[j]) just before the group's
+// adds, and the adds take them from the lanes holding them.  Same values as
+// forming the products into LDS first and running chain_group_lds over them.
+template <int R>
+__device__ __forceinline__ float chain_group_dot_lds(float a, const float* p, const float* v, int n) {
+  constexpr int B = 4 * R;
+  const int k = threadIdx.x & (R - 1);
+  const int nb = (n + B - 1) / B;
+  auto load = [&](const float* base, int b) {
+    const int e = b * B + 4 * k;
+    return *reinterpret_cast<const float4*>(base + (e < n ? e : 0));
+  };
+  auto prod = [&](float4 x, float4 y) { return make_float4(x.x * y.x, x.y * y.y, x.z * y.z, x.w * y.w); };
+  auto live = [&](float4 x, int b) {
+    const int e = b * B + 4 * k;
+    x.x = e < n ? x.x : 0.0f;
+    x.y = e + 1 < n ? x.y : 0.0f;
+    x.z = e + 2 < n ? x.z : 0.0f;
+    x.w = e + 3 < n ? x.w : 0.0f;
+    return x;
+  };
+  const int nfull = n / B;
+  float4 p0 = load(p, 0), v0 = load(v, 0), p1 = load(p, 1), v1 = load(v, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  int b = 0;
+  for (; b + 1 < nfull; b += 2) {
+    a = chain_group_add<R>(a, prod(p0, v0));
+    p0 = load(p, b + 2);
+    v0 = load(v, b + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    a = chain_group_add<R>(a, prod(p1, v1));
+    p1 = load(p, b + 3);
+    v1 = load(v, b + 3);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (b < nfull) {
+    a = chain_group_add<R>(a, prod(p0, v0));
+    if (b + 1 < nb) a = chain_group_add<R>(a, live(prod(p1, v1), b + 1));
+  } else if (b < nb) {
+    a = chain_group_add<R>(a, live(prod(p0, v0), b));
+  }
+  return a;
+}
+
 // a += p[j] * v[j] for j = 0 .. n-1 in order, each product rounded and
 // added on its own (the P.V chain, det-model lib.rs:2390-2420), with both
 // operand rows in LDS (16-byte aligned).  Software-pipelined in blocks of 16
