@@ -981,7 +981,9 @@ int rows_per_wave(int rows) {
 // launch with no other chunk in flight (dtl_forward_chunk, the decode-size
 // chunks) runs one chain per lane instead, 8 x 8 lanes, 2 x 2 waves over 16
 // positions x 16 rows: wo / ffn_down 59.9 -> 41.6 ms and wq + wk 26.3 ->
-// 24.2 ms per chunk-at-a-time step.  The gate + up pair keeps its tile.
+// 24.2 ms per chunk-at-a-time step.  The gate + up pair keeps its tile;
+// pair tiles of eight chains per lane (2 x 2, 4 x 1 and 4 x 1 over two
+// waves) were 0.7-9% slower over the pipelined step (fewer waves per CU).
 template <int PW, int PP, int RP, int WP, int WR, int MODE>
 void launch_q4k_f32m(const Q4kF32Args& a, int rows_total, hipStream_t s) {
   constexpr int RB = WR * RP * 64 / PW, PB = WP * PW * PP;
