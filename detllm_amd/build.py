@@ -20,6 +20,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OUT_DIR = PKG / "_build"
 LIB_NAME = "libdetllm_amd.so"
+STATIC_LIB_NAME = "libdetllm_amd.a"
 ARCH = os.environ.get("DETLLM_AMD_ARCH", "gfx950")
 
 SOURCES = [
@@ -55,12 +56,18 @@ def _run(cmd, verbose: bool) -> None:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed with exit code {res.returncode}: {' '.join(cmd[-3:])}")
+        raise RuntimeError(f"{Path(cmd[0]).name} failed with exit code {res.returncode}: {' '.join(cmd[-3:])}")
 
 
 def build_library(verbose: bool = False, jobs: int = 0) -> Path:
-    """Compiles every source (one hipcc per file, in parallel) and links
-    them into one shared library; returns its path."""
+    """Compiles every source (one hipcc per file, in parallel), links them
+    into one shared library and archives the same objects as the static
+    library libdetllm_amd.a; returns the shared library's path.
+
+    The archive's objects are ordinary (non-relocatable-device-code) HIP
+    objects: each carries its own gfx950 code object and registers it from
+    a static constructor, so a host linker pulling them from the archive
+    needs only -lamdhip64 and the C++ runtime beside it."""
     OUT_DIR.mkdir(exist_ok=True)
     out = OUT_DIR / LIB_NAME
     tmp = OUT_DIR / (LIB_NAME + ".tmp")
@@ -75,6 +82,11 @@ def build_library(verbose: bool = False, jobs: int = 0) -> Path:
     _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *[str(o) for o in objs], "-o", str(tmp)],
          verbose)
     os.replace(tmp, out)
+    archive = OUT_DIR / STATIC_LIB_NAME
+    archive_tmp = OUT_DIR / (STATIC_LIB_NAME + ".tmp")
+    archive_tmp.unlink(missing_ok=True)
+    _run(["ar", "rcs", str(archive_tmp), *[str(o) for o in objs]], verbose)
+    os.replace(archive_tmp, archive)
     return out
 
 
