@@ -427,7 +427,7 @@ def main() -> int:
                     help="skip the C1 hash / C2 and C3 decode legs")
     ap.add_argument("--codec-bytes", type=int, default=8192,
                     help="prefix of the 1 MiB Markov stream compressed + decompressed (0: skip)")
-    ap.add_argument("--codec-cpu-bytes", type=int, default=96,
+    ap.add_argument("--codec-cpu-bytes", type=int, default=1024,
                     help="bytes of the device payload the oracle decodes on the host")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain copy of this many MiB (counter calibration) and exit")

@@ -1847,7 +1847,11 @@ int dtl_uniform_symbol_range(size_t symbol, size_t symbols, uint64_t* cum, uint3
 
 namespace {
 constexpr size_t kStaticCdfRows = 8;
-constexpr size_t kStaticCdfScratchBytes = 8u << 20;  // >= cdf_scratch_bytes(8, 1 << 18)
+// The largest call: kStaticCdfRows rows of vocab 2^18 (the scratch depends
+// on the vocabulary, not on the tail), rounded up to 256 bytes: 8,399,360.
+constexpr size_t kStaticCdfScratchBytes = (cdf_scratch_bytes_for(kStaticCdfRows, kMaxSymbols) + 255) & ~(size_t)255;
+static_assert(kStaticCdfScratchBytes >= cdf_scratch_bytes_for(kStaticCdfRows, kMaxSymbols), "static scratch");
+static_assert(kStaticCdfScratchBytes == 8399360, "static scratch size as documented");
 static __device__ __align__(256) uint8_t scratch[kStaticCdfScratchBytes];
 constexpr int kStaticMaxDevices = 64;
 std::atomic<void*> g_static_scratch[kStaticMaxDevices];
@@ -1931,6 +1935,22 @@ int dtl_kernel_silu_f32(const float* in, float* out, size_t n) {
   if ((st = sc.arena.upload(&di, in, n))) return st;
   if ((st = sc.arena.alloc(&dout, n))) return st;
   launch_exp_f32(di, dout, (int)n, 1, sc.stream);
+  HIP_TRY(hipMemcpyAsync(out, dout, n * 4, hipMemcpyDeviceToHost, sc.stream));
+  int bits;
+  return sc.finish(&bits);
+}
+
+int dtl_kernel_exp_clamped_f32(const float* in, float* out, size_t n) {
+  if (!in || !out) return DTL_ERR_INVALID_ARGUMENT;
+  for (size_t i = 0; i < n; i++)
+    if (in[i] > 0.0f) return DTL_ERR_INVALID_ARGUMENT;  // outside exp_clamped's domain
+  Scratch sc;
+  int st = sc.init();
+  if (st) return st;
+  float *di, *dout;
+  if ((st = sc.arena.upload(&di, in, n))) return st;
+  if ((st = sc.arena.alloc(&dout, n))) return st;
+  launch_exp_f32(di, dout, (int)n, 2, sc.stream);
   HIP_TRY(hipMemcpyAsync(out, dout, n * 4, hipMemcpyDeviceToHost, sc.stream));
   int bits;
   return sc.finish(&bits);

@@ -255,6 +255,15 @@ void launch_cdf(const float* logits, int R, int V, int tail, int mode, const uin
 // (device, optional): row r of the launch is logits row rows[r].
 // finish_only: the scratch already holds this row's block results (a
 // decoder total for the same row and tail): only the per-row finish runs.
+constexpr size_t kCdfBlockElems = 4096;  // logits per workgroup of the block kernels
+constexpr size_t cdf_scratch_bytes_for(size_t R, size_t V) {
+  // per row: block maxima (f32), exps chain-major (8 x v8 f32, v8 = V/8
+  // rounded up to a multiple of 4), Z, block sums and sums below (u64),
+  // the symbol's frequency; + 256 for the 16-byte rounding of each part
+  return R * (((V + kCdfBlockElems - 1) / kCdfBlockElems) * 4 + 8 * ((((V + 7) / 8) + 3) & ~(size_t)3) * 4 + 4 +
+              ((V + kCdfBlockElems - 1) / kCdfBlockElems) * 16 + 4) +
+         256;
+}
 size_t cdf_scratch_bytes(int R, int V);
 void launch_cdf_blocks(const float* logits, const uint32_t* rows, int R, int V, int tail, int mode,
                        const uint32_t* symbols, const uint64_t* values, uint64_t* cum,

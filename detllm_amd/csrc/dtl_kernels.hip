@@ -2270,16 +2270,13 @@ __global__ void __launch_bounds__(256) k_cdf(const float* logits, int V, int tai
 // serial Z chains, block frequency sums, and a per-row finish with the exact
 // integer sums / search.  Every f32 operation is the one k_cdf performs.
 namespace {
-constexpr int kCdfBlk = 4096;  // elements per workgroup (256 threads x 16)
+constexpr int kCdfBlk = (int)kCdfBlockElems;  // elements per workgroup (256 threads x 16)
 
 __host__ __device__ inline int cdf_nblk(int V) { return (V + kCdfBlk - 1) / kCdfBlk; }
 __host__ __device__ inline int cdf_v8(int V) { return (((V + 7) / 8) + 3) & ~3; }
 }  // namespace
 
-size_t cdf_scratch_bytes(int R, int V) {
-  const size_t nb = (size_t)cdf_nblk(V);
-  return (size_t)R * (nb * 4 + 8 * (size_t)cdf_v8(V) * 4 + 4 + nb * 16 + 4) + 256;
-}
+size_t cdf_scratch_bytes(int R, int V) { return cdf_scratch_bytes_for((size_t)R, (size_t)V); }
 
 namespace {
 struct CdfScratch {
@@ -2620,7 +2617,9 @@ void launch_cdf(const float* logits, int R, int V, int tail, int mode, const uin
 __global__ void k_exp(const float* in, float* out, int n, int which) {
   int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  out[i] = which == 0 ? expf_det(in[i]) : silu_det(in[i]);
+  // which 2: the softmax / CDF exp restated for t <= 0 (t > 0 is outside
+  // its domain; callers of the parity entry pass t <= 0 or NaN)
+  out[i] = which == 0 ? expf_det(in[i]) : which == 1 ? silu_det(in[i]) : exp_clamped(in[i]);
 }
 
 void launch_exp_f32(const float* in, float* out, int n, int which, hipStream_t s) {

@@ -427,8 +427,14 @@ __device__ __forceinline__ float silu_det(float x) {
 // overflow, underflow or NaN paths, k in [-127, 0], the k = 0 reduction as
 // the general one (x - 0 ln2_hi = x, 0 ln2_lo = 0) and scalbnf as one
 // multiply (two for k = -127, as its downward step takes them).  About a
-// third of expf_det's instructions; equal to it for every float t <= 0
-// (tests/exp_nonpos_check.c).  NaN gives NaN; t > 0 is outside the domain.
+// third of expf_det's instructions.  Checks: a host restatement of this
+// function equals the host restatement of expf_det on all 2^31 floats with
+// the sign bit set and on +0 (tests/exp_nonpos_check.c); this device
+// function equals the oracle's exp_f32(max(t, -88)) on every 61st such
+// pattern and on dense bands around its branch points
+// (tests/test_gpu_kernels.py::test_exp_clamped_device_matches_oracle), and
+// through the softmax and CDF parity tests.  NaN gives NaN; t > 0 is
+// outside the domain.
 __device__ __forceinline__ float exp_clamped(float t) {
   const float ln2_hi = u2f(0x3f317200u);
   const float ln2_lo = u2f(0x35bfbe8eu);

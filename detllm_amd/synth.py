@@ -384,6 +384,11 @@ def codec_fixture_gguf() -> bytes:
     return g.to_bytes()
 
 
+# Seed of the end-to-end codec workload's byte stream (1 MiB compressed and
+# decompressed with the Qwen2.5-0.5B-shaped model at n_ctx 2048).
+C5_SEED = 0xDE711005
+
+
 def markov_bytes(seed: int, n: int) -> bytes:
     """n bytes of seeded order-3 Markov text over printable ASCII + newline.
 

@@ -234,7 +234,8 @@ int dtl_decoder_lookup(dtl_session *session, size_t row, size_t tail_symbols, ui
  * cdf.rs:122-199) of symbols[i] against row i of logits[rows][vocab], with
  * every pointer in device memory and the work enqueued on `stream` (a
  * hipStream_t; NULL is the default stream) without waiting for it.  The
- * CDF scratch is a static device array of 8 MiB per GPU, held until the
+ * CDF scratch is a static device array of 8,399,360 bytes per GPU (the
+ * scratch of 8 rows at vocab 2^18), held until the
  * process ends: rows <= 8 and vocab + tail_symbols <= 2^18, else
  * DTL_ERR_STATIC_SCRATCH_LIMIT.  The call allocates nothing.  *status_bits
  * (device memory) is overwritten with the call's error bits once the stream
@@ -392,6 +393,11 @@ void dtl_bytes_free(uint8_t *p);
 int dtl_kernel_exp_f32(const float *in, float *out, size_t n);
 /* silu_f32 (math.rs:30-34). */
 int dtl_kernel_silu_f32(const float *in, float *out, size_t n);
+/* exp_f32(max(t, -88)) as softmax_in_place (det-model lib.rs:2361-2388) and
+ * the CDF (det-coder cdf.rs:255-300) use it, for t <= 0 (every caller passes
+ * t = x - max): the device's restatement for that domain.  A t > 0 is
+ * DTL_ERR_INVALID_ARGUMENT. */
+int dtl_kernel_exp_clamped_f32(const float *in, float *out, size_t n);
 /* f16 -> f32 (det-num f16.rs:6-34) on the device. */
 int dtl_kernel_f16_to_f32(const uint16_t *in, float *out, size_t n);
 /* sqrt and division as used by rmsnorm / softmax / quantisers. */

@@ -50,6 +50,7 @@ enum {
 
 /* ---- det-num ---------------------------------------------------------- */
 float ref_exp_f32(float x);
+void ref_exp_f32_array(const float *x, float *out, size_t n, int clamp);
 double ref_exp_f64(double x);
 double ref_ln_f64(double x);
 double ref_sin_f64(double x);

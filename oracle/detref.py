@@ -30,6 +30,7 @@ def load() -> C.CDLL:
     sz = C.c_size_t
     sigs = {
         "ref_exp_f32": (C.c_float, [C.c_float]),
+        "ref_exp_f32_array": (None, [C.POINTER(C.c_float), C.POINTER(C.c_float), sz, C.c_int]),
         "ref_silu_f32": (C.c_float, [C.c_float]),
         "ref_exp_f64": (C.c_double, [C.c_double]),
         "ref_ln_f64": (C.c_double, [C.c_double]),
@@ -266,6 +267,15 @@ def apply_rope(x, heads: int, head_dim: int, rope_dim: int, split_half: bool, co
 def exp_f32(x: np.ndarray) -> np.ndarray:
     f = lib().ref_exp_f32
     return np.array([f(float(v)) for v in np.asarray(x, np.float32)], np.float32)
+
+
+def exp_f32_array(x: np.ndarray, clamp: bool = False) -> np.ndarray:
+    """exp_f32 of every element in C (bit patterns pass unchanged, NaN
+    payloads included); clamp: of max(x, -88)."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    lib().ref_exp_f32_array(_p(x, C.c_float), _p(out, C.c_float), x.size, int(clamp))
+    return out
 
 
 def range_encode(triples) -> bytes:

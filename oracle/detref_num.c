@@ -201,6 +201,17 @@ float ref_exp_f32(float x) {
     return k == 0 ? y : scalbn_f32(y, k);
 }
 
+/* exp_f32 over an array; clamp != 0 applies max(x, -88) first, as
+ * softmax_in_place (det-model lib.rs:2375) and the CDF (det-coder
+ * cdf.rs:291) do before calling exp_f32. */
+void ref_exp_f32_array(const float *x, float *out, size_t n, int clamp) {
+    for (size_t i = 0; i < n; i++) {
+        float v = x[i];
+        if (clamp && v < -88.0f) v = -88.0f;
+        out[i] = ref_exp_f32(v);
+    }
+}
+
 /* silu: crates/det-num/src/math.rs:30-34 */
 float ref_silu_f32(float x) {
     float t = ref_exp_f32(-x);

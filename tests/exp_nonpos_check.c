@@ -1,9 +1,9 @@
 /* Host check of exp_clamped (detllm_amd/csrc/dtl_numerics.h), restated for
  * t <= 0: against the general expf_det path (the FreeBSD expf restated, as in
- * oracle/detref_num.c) applied to max(t, -88), for every third float t <= 0
- * and +0 (all 2^31 sign-bit patterns agreed when this check was first run).
- * Exit status 0 when all agree bit for bit (NaN inputs go to the general
- * path and are not compared). */
+ * oracle/detref_num.c) applied to max(t, -88), for every float with the sign
+ * bit set (all 2^31 patterns: -0, subnormals, normals, -inf) and +0.  Exit
+ * status 0 when all agree bit for bit (NaN inputs go to the general path and
+ * are not compared).  About 40 s on 8 cores. */
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -73,7 +73,7 @@ static float exp_nonpos(float t) {
 int main(void) {
   long bad = 0, n = 0;
 #pragma omp parallel for reduction(+ : bad, n) schedule(static)
-  for (long u = 0x80000000L; u <= 0xffffffffL; u += 3) {
+  for (long u = 0x80000000L; u <= 0xffffffffL; u += 1) {
     float t = u2f((uint32_t)u);
     if (t != t) continue;
     float want = expf_ref(t < -88.0f ? -88.0f : t), got = exp_nonpos(t);

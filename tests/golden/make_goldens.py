@@ -10,9 +10,12 @@ det-model's logits_hash_for_tokens_chunked does (crates/det-model/src/
 lib.rs:1402-1465).  Each JSON file records the SHA-256 of all positions'
 logits (f32 little-endian bits, positions ascending: the reference's logits
 hash) and a 16-hex-digit digest of every single position, so a GPU mismatch
-names its first position.  qwen05 also records the next-token symbol range
-(cum, freq, total) of every position with the 256 byte-escape symbols
-(det-coder cdf.rs:130-199).  The codec file is the windowed payload of a
+names its first position.  qwen05 and tinyllama also record the next-token
+symbol range (cum, freq, total) of every position with the 256 byte-escape
+symbols (det-coder cdf.rs:130-199): their SHA-256 (u64 cum, u32 freq, u64
+total, little-endian, positions ascending), and for tinyllama every row's
+triple, so a mismatch names its row.  The next token of the last position
+is 0.  The codec file is the windowed payload of a
 prefix of the byte stream of the end-to-end workload on the qwen05 model at
 n_ctx 2048 (det-cli main.rs:521-551), long enough for three window
 rollovers.
@@ -70,14 +73,18 @@ def logits_golden(name: str) -> dict:
     out = {"workload": wname, "layers": layers or w.layers, "positions": int(len(toks)),
            "model_sha256": hashlib.sha256(g).hexdigest()}
     out["logits_sha256"], out["position_digests"] = _digests(rows)
-    if wname == "qwen05":
+    if wname in ("qwen05", "tinyllama"):
         nxt = [int(t) for t in toks[1:]] + [0]
         h = hashlib.sha256()
+        triples = []
         for i in range(len(toks)):
             cum, freq, total = detref.symbol_range(rows[i], nxt[i], 256)
             h.update(struct.pack("<QIQ", cum, freq, total))
+            triples.append([cum, freq, total])
         out["next_token_ranges_sha256"] = h.hexdigest()
         out["range_tail"] = 256
+        if wname == "tinyllama":
+            out["next_token_ranges"] = triples
     out["oracle_seconds"] = round(time.time() - t0, 1)
     return out
 
@@ -102,7 +109,7 @@ def codec_golden() -> dict:
 
 
 def main(argv) -> None:
-    detref.set_threads(os.cpu_count() or 1)
+    detref.set_threads(int(os.environ.get("GOLDEN_THREADS", 0)) or os.cpu_count() or 1)
     todo = argv or ["smollm2", "qwen05", "tinyllama", "smollm2_l1", "codec"]
     for name in todo:
         t0 = time.time()

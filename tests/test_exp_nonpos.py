@@ -1,6 +1,9 @@
 """exp_clamped restated for non-positive arguments (detllm_amd/csrc/
 dtl_numerics.h) against the general expf_det path, on the host:
-tests/exp_nonpos_check.c compares both for every third float t <= 0."""
+tests/exp_nonpos_check.c compares both for every float t <= 0 (all 2^31
+patterns with the sign bit set, and +0).  The device function itself is
+checked against the oracle's exp_f32 by
+tests/test_gpu_kernels.py::test_exp_clamped_device_matches_oracle."""
 import shutil
 import subprocess
 

@@ -260,3 +260,38 @@ def test_decompress_in_parts_equals_one_call():
         assert [int(x) for x in p.symbols] != syms[len(prior):len(prior) + 20]
     except DetllmError:
         pass
+
+
+@pytest.mark.timeout(600)
+def test_c5_markov_64kib_round_trip_on_qwen05():
+    """The end-to-end configuration (DTLZ compress / decompress on the
+    24-layer Qwen2.5-0.5B-shaped model at n_ctx 2048, det-cli
+    main.rs:431-512) over the first 64 KiB of its seeded order-3 Markov
+    stream: about 45 windows, so 44 rollovers with 512 replayed tokens each.
+    Decompression runs in parts (dtl_decompress_part) so that progress shows;
+    the last part runs the canonical re-encode check (main.rs:498-506) and
+    returns the bytes, which must equal the input.  Byte-level parity of the
+    payload with the oracle is pinned on the 6 KiB prefix
+    (test_codec_prefix_payload_matches_golden)."""
+    import time
+
+    from detllm_amd.codec import DtlzHeader, compress, decompress_part
+
+    w = synth.WORKLOADS["qwen05"]
+    lm = _loaded(synth.build_model(w))
+    data = synth.markov_bytes(synth.C5_SEED, 64 * 1024)
+    t0 = time.time()
+    out = compress(lm, data, 2048)
+    h = DtlzHeader.decode(out)
+    assert (h.n_ctx, h.overlap, h.orig_len) == (2048, 512, len(data))
+    print(f"c5 64 KiB: compressed to {len(out)} bytes in {time.time() - t0:.1f} s", flush=True)
+    prior, state, part = [], None, None
+    while True:
+        part = decompress_part(lm, out, prior, state, max_new=8192)
+        prior += [int(x) for x in part.symbols]
+        state = part.state
+        print(f"c5 64 KiB: {len(prior)} symbols decoded, {time.time() - t0:.1f} s", flush=True)
+        if part.done:
+            break
+        assert len(part.symbols) == 8192
+    assert part.data == data

@@ -210,11 +210,19 @@ def test_standalone_cdf_kernel_matches_oracle(V):
 
 
 @pytest.mark.parametrize("graph", [True, False])
-def test_decode_window_over_2048_matches_oracle(monkeypatch, graph):
-    # A session window over 2048 positions: the decode attention runs one
-    # workgroup per (head, position) (k_attention_dec) instead of the split
-    # score / P.V launches; with the captured graph the grids are sized for
-    # the whole 4096-position window.
+def test_decode_attention_regimes_match_oracle(monkeypatch, graph):
+    """Single-position forwards in a 4096-position window (1-layer SmolLM2
+    shape) through every decode attention they can take, bit for bit against
+    the oracle.
+
+    graph: positions below 512 replay the graph whose attention is one launch
+    (k_attn_fused); from 512 on, the graph sized for the whole window, whose
+    attention runs one workgroup per (head, position) (k_attention_dec).
+    eager (DETLLM_NO_GRAPH=1, the path under profiling or after a failed
+    capture): the launch is sized by the row: k_attn_fused up to 512 keys,
+    the split pair (k_attn_split_scores + k_attn_split_pv) up to 2048,
+    k_attention_dec beyond; the positions between are forwarded in chunks of
+    64 (chunk attention)."""
     import dataclasses
 
     from detllm_amd import synth
@@ -223,10 +231,27 @@ def test_decode_window_over_2048_matches_oracle(monkeypatch, graph):
         monkeypatch.setenv("DETLLM_NO_GRAPH", "1")
     w = dataclasses.replace(synth.WORKLOADS["smollm2"], ctx=4096)
     data = synth.build_model(w, layers=1)
-    toks = [int(t) for t in synth.tokens(w, 9)]
+    if graph:
+        singles = list(range(524))
+        n = 524
+    else:
+        singles = [0, 1, 2, 3, 600, 601, 602, 603, 2048, 2049, 2050, 2051, 2052, 2053]
+        n = 2054
+    toks = [int(t) for t in synth.tokens(w, n)]
+    print(f"oracle logits of {n} positions", flush=True)
     ref = detref.Model(data).logits(toks)
     m = _model(data)
-    with m.forward_workspace(4096, 1) as s:
-        for p, tok in enumerate(toks):
-            got = s.forward_one(tok, p)
-            assert np.array_equal(got.view(np.uint32), ref[p].view(np.uint32)), p
+    with m.forward_workspace(4096, 64) as s:
+        p = 0
+        while p < n:
+            if p in singles:
+                if p in (0, 512, 600, 2048):
+                    print(f"{'graph' if graph else 'eager'} single-position forwards from {p}", flush=True)
+                got = s.forward_one(toks[p], p)
+                assert np.array_equal(got.view(np.uint32), ref[p].view(np.uint32)), p
+                p += 1
+            else:
+                end = min(n, p + 64, min((q for q in singles if q > p), default=n))
+                lg = s.forward_chunk(toks[p:end], p, want_logits=True)
+                assert np.array_equal(lg[-1].view(np.uint32), ref[end - 1].view(np.uint32)), end - 1
+                p = end

@@ -61,6 +61,29 @@ def test_exp_f32_strided_all_bit_patterns():
     assert np.array_equal(got[~nan], want)
 
 
+def test_exp_clamped_device_matches_oracle():
+    """The device's exp for softmax and the CDF (exp_f32(max(t, -88)) restated
+    for t <= 0) against the oracle's exp_f32 of max(t, -88): every 61st
+    pattern with the sign bit set (-0, subnormals, normals, -inf), every
+    pattern in the bands around its branch points (|t| near 2^-13, ln2/2,
+    1.5 ln2, the -88 clamp and the k = -126 / -127 scaling steps), and +0.
+    The host check tests/exp_nonpos_check.c covers all 2^31 patterns of the
+    same restatement."""
+    L = _lib()
+    bits = np.arange(0x80000000, 0x100000000, 61, dtype=np.uint64).astype(np.uint32)
+    bands = [np.arange(c - 4096, c + 4096, dtype=np.uint64).astype(np.uint32) | np.uint32(0x80000000)
+             for c in (0x39000000, 0x3EB17218, 0x3F851592, 0x42B00000, 0x42AEAC50, 0x42AF0000, 0x42AE0000)]
+    x = np.concatenate([bits, *bands, np.array([0], np.uint32)]).view(np.float32)
+    x = np.ascontiguousarray(x[~np.isnan(x)])
+    out = np.empty_like(x)
+    L.check(L.lib.dtl_kernel_exp_clamped_f32(_p(x, C.c_float), _p(out, C.c_float), x.size), "exp_clamped")
+    want = detref.exp_f32_array(x, clamp=True)
+    assert np.array_equal(out.view(np.uint32), want.view(np.uint32))
+    # outside the domain: refused on the host
+    y = np.array([-1.0, 0.5], np.float32)
+    assert L.lib.dtl_kernel_exp_clamped_f32(_p(y, C.c_float), _p(out, C.c_float), 2) == 42
+
+
 def test_silu_bitexact():
     rng = np.random.default_rng(1)
     x = np.concatenate([rng.normal(0, 4, 100000), rng.uniform(-100, 100, 50000)]).astype(np.float32)

@@ -107,28 +107,46 @@ def test_qwen05_decode_ranges_and_pipeline_match_golden():
     assert m.logits_hash_for_tokens_chunked(toks, 64).hex() == gold["logits_sha256"]
 
 
-def test_tinyllama_encode_and_decode_match_golden():
+def test_tinyllama_encode_and_decode_match_golden(monkeypatch):
+    """The benchmark's own workload end to end: the timed encode
+    (dtl_forward_ranges, chunks of 64 in flight on 4 lanes as the bench
+    runs it, and on 3) must code every one of the 2048 next tokens with the
+    reference's (cum, freq, total), as det-cli's encode loop does
+    (main.rs:521-551; cdf.rs:130-199).  Expected ranges: the golden's
+    (the oracle's logits and symbol_range in the build container), and the
+    oracle's symbol_range over this run's chunked logits once every row's
+    digest equals the golden's."""
+    import detref
     from detllm_amd.model import Session
 
     gold, w, m, toks = _setup("tinyllama")
     n = len(toks)
-    print(f"tinyllama: 22 layers, {n} positions, chunks of 64", flush=True)
-    rows = []
-    m.visit_logits_for_tokens_chunked(toks, 64, lambda r: rows.append(r.copy()))
-    _check_rows(rows, gold, "chunk 64")
-    # the pipelined encode codes each next token with the same ranges as
-    # coding the chunked path's logits one row at a time
     nxt = toks[1:] + [0]
-    from detllm_amd.coder import logits_to_symbol_range_with_byte_escapes as rng
+    print(f"tinyllama: 22 layers, {n} positions, chunks of 64", flush=True)
+    want = []
 
-    probe = list(range(0, n, 97)) + [n - 1]
-    want = [rng(rows[i], nxt[i]) for i in probe]
-    print("tinyllama: pipelined encode", flush=True)
-    with Session(m, 2048, 64) as s:
-        c, f, tt = s.forward_ranges(toks, 0, list(range(n)), nxt, 256)
-    for j, i in enumerate(probe):
-        assert (int(c[i]), int(f[i]), int(tt[i])) == (want[j].cum, want[j].freq, want[j].total), f"row {i}"
-    del rows
+    def visit(r):
+        i = len(want)
+        b = np.ascontiguousarray(r, np.float32).tobytes()
+        assert hashlib.sha256(b).hexdigest()[:16] == gold["position_digests"][i], f"chunk 64: position {i}"
+        want.append(tuple(int(v) for v in detref.symbol_range(r, nxt[i], 256)))
+
+    assert m.logits_hash_for_tokens_chunked(toks, 64).hex() == gold["logits_sha256"]
+    m.visit_logits_for_tokens_chunked(toks, 64, visit)
+    assert len(want) == n
+    if "next_token_ranges" in gold:
+        assert [tuple(t) for t in gold["next_token_ranges"]] == want
+    if "next_token_ranges_sha256" in gold:
+        assert _ranges_hash(*zip(*want)) == gold["next_token_ranges_sha256"]
+    for lanes in ("4", "3"):
+        monkeypatch.setenv("DETLLM_LANES", lanes)  # read when the session is created
+        print(f"tinyllama: pipelined encode on {lanes} lanes", flush=True)
+        with Session(m, 2048, 64) as s:
+            c, f, tt = s.forward_ranges(toks, 0, list(range(n)), nxt, 256)
+        got = [(int(a), int(b), int(d)) for a, b, d in zip(c, f, tt)]
+        bad = [i for i in range(n) if got[i] != want[i]]
+        assert not bad, f"{lanes} lanes: {len(bad)} rows differ, first {bad[0]}"
+    monkeypatch.delenv("DETLLM_LANES")
     print("tinyllama: single-token decode", flush=True)
     _check_rows(_decode_rows(m, toks, 2048), gold, "decode")
 

@@ -330,3 +330,16 @@ def test_range_coder_roundtrip():
         assert cum <= v.value < cum + freq
         assert L.ref_range_decode_advance(d, cum, freq, total) == 0
     L.ref_range_decoder_free(d)
+
+
+def test_oracle_exp_array_matches_scalar_binding():
+    """The array form of the oracle's exp_f32 (used to check the device's
+    exp over millions of bit patterns) agrees with the scalar form, which
+    the reference's anchors above pin, on a strided sweep of both signs;
+    with clamp it is exp_f32(max(x, -88))."""
+    bits = np.arange(0, 2**32, 65521, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[~np.isnan(x)]
+    assert np.array_equal(detref.exp_f32_array(x).view(np.uint32), detref.exp_f32(x).view(np.uint32))
+    want = detref.exp_f32(np.maximum(x, np.float32(-88.0)))
+    assert np.array_equal(detref.exp_f32_array(x, clamp=True).view(np.uint32), want.view(np.uint32))
