@@ -454,7 +454,8 @@ namespace {
 // kernels then serve every chunk size.
 // Copies the chunked-encode GEMMs read instead of the GGUF blocks: the
 // exact f32 value of every Q4_K weight, the int8 matrix-core planes of
-// every Q6_K matrix and the int8 values of every Q4_0 matrix.  DETLLM_NO_F32_MIRROR=1 keeps Q4_K packed only and
+// every Q6_K matrix and the int8 values of every Q4_0 matrix; and the
+// decode GEMV's layout of tall Q6_K matrices (the output projection).  DETLLM_NO_F32_MIRROR=1 keeps Q4_K packed only and
 // DETLLM_NO_Q6K_PLANES=1 keeps Q6_K packed only (the GEMMs then decode the
 // superblocks themselves; results are identical either way).
 bool env_flag(const char* name) {
@@ -465,11 +466,12 @@ bool f32_mirror_enabled() { return !env_flag("DETLLM_NO_F32_MIRROR"); }
 bool q6k_planes_enabled() { return !env_flag("DETLLM_NO_Q6K_PLANES"); }
 
 int build_encode_copies(dtl_model* m) {
-  std::vector<DevMat*> q4k, q6k, q40;
+  std::vector<DevMat*> q4k, q6k, q40, q6d;
   auto add = [&](DevMat* M) {
     if (M->type == GGML_Q4_K && f32_mirror_enabled()) q4k.push_back(M);
     if (M->type == GGML_Q6_K && q6k_planes_enabled()) q6k.push_back(M);
     if (M->type == GGML_Q4_0) q40.push_back(M);
+    if (M->type == GGML_Q6_K && q6k_decode_layout_applies(*M)) q6d.push_back(M);
   };
   for (Layer& L : m->layers)
     for (DevMat* M : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down}) add(M);
@@ -478,7 +480,19 @@ int build_encode_copies(dtl_model* m) {
   for (DevMat* M : q4k) need += (size_t)M->rows * M->cols * sizeof(float);
   for (DevMat* M : q6k) need += q6k_planes_bytes(*M);
   for (DevMat* M : q40) need += (size_t)M->rows * M->cols;
-  if (q4k.empty() && q6k.empty() && q40.empty()) return DTL_OK;
+  // the decode layouts are not optional copies: always built
+  for (DevMat* M : q6d) {
+    uint4* p;
+    int st = m->arena.alloc(&p, q6k_decode_layout_bytes(*M) / sizeof(uint4));
+    if (st) return st;
+    launch_q6k_decode_layout(*M, p, nullptr);
+    M->q6d = p;
+  }
+  if (q4k.empty() && q6k.empty() && q40.empty()) {
+    HIP_TRY(hipGetLastError());
+    HIP_TRY(hipDeviceSynchronize());
+    return DTL_OK;
+  }
   size_t free_b = 0, total_b = 0;
   HIP_TRY(hipMemGetInfo(&free_b, &total_b));
   if (need + (size_t(4) << 30) > free_b) return DTL_OK;
@@ -2097,6 +2111,12 @@ int dtl_kernel_gemv(int ggml_type, const uint8_t* weights, size_t rows, size_t c
     if ((st = sc.arena.alloc(&i8, rows * cols))) return st;
     launch_q4_0_i8(W, i8, sc.stream);
     W.i8 = i8;
+  }
+  if (W.type == GGML_Q6_K && q6k_decode_layout_applies(W)) {
+    uint4* q6d;
+    if ((st = sc.arena.alloc(&q6d, q6k_decode_layout_bytes(W) / sizeof(uint4)))) return st;
+    launch_q6k_decode_layout(W, q6d, sc.stream);
+    W.q6d = q6d;
   }
   float *dx, *dout, *af, *da, *dk;
   int8_t *qa, *qk;

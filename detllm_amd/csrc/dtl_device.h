@@ -75,7 +75,34 @@ struct DevMat {
   // element order, the A operand of the chunked-encode GEMM on the int8
   // matrix cores (Q8_0 uses w itself).
   const int8_t* i8;
+  // Q6_K only (tall matrices whose superblocks per row divide 16): the
+  // decode GEMV's layout of the 208-byte bodies (q6k_decode_layout_*).
+  const uint4* q6d;
 };
+
+// Q6_K decode layout.  Inside a superblock the 208 body bytes are re-cut
+// into 13 words of 16 bytes with the 6-bit quants class-major (class c =
+// element index mod 8, elements c + 8j, j = 0..31): for class pair p
+// (classes 2p, 2p + 1), word (p, 0) holds the low nibbles of class 2p and
+// word (p, 1) those of class 2p + 1 (dword k, byte i: j = 8k + i in bits
+// 0-3, j = 8k + 4 + i in bits 4-7), word (p, 2) their high bit pairs (dwords
+// 0-1 for class 2p, 2-3 for 2p + 1; dword k, byte i: j = 16k + 4m + i in
+// bits 2m, 2m + 1); the 16 scales are the 13th word.  16 consecutive (row,
+// superblock) pairs form a group (16 / nb rows, superblock s = row % (16 /
+// nb) * nb + superblock) of 13 * 16 words: word (p, k) of superblock s at
+// group * 208 + k * 64 + s * 4 + p, the scales at group * 208 + 192 + s, so
+// that the wave load of word k of the group's 16 * 4 (superblock, class
+// pair) lanes reads one contiguous KiB.  Superblocks past the last row are
+// zero.
+constexpr int kQ6dGroupWords = 208;
+inline bool q6k_decode_layout_applies(const DevMat& W) {
+  return W.nb > 0 && 16 % W.nb == 0 && W.rows > 16384;
+}
+inline size_t q6k_decode_layout_bytes(const DevMat& W) {
+  const size_t rpg = 16 / (size_t)W.nb, groups = ((size_t)W.rows + rpg - 1) / rpg;
+  return groups * kQ6dGroupWords * 16;
+}
+void launch_q6k_decode_layout(const DevMat& W, uint4* out, hipStream_t s);
 
 // Activations of T positions for one GEMM input of width cols, in every
 // form a weight type consumes (det-quant Q8A for Q8_0/Q4_0/Q4_K, Q8_K for Q6_K).

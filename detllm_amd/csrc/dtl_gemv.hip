@@ -410,6 +410,188 @@ __global__ void __launch_bounds__(64) k_gemv_q6k(DevMat W, const int8_t* __restr
   }
 }
 
+// ---------------------------------------------------------------------------
+// Q6_K decode layout (see q6k_decode_layout_applies): one thread per
+// (superblock, class) of the padded groups writes its class's low nibbles and
+// high bit pairs; class 0 also writes the scales.  Quant q6u of element e
+// decoded as q6_k_quant does (det-quant lib.rs:537-556), kept unsigned
+// (0..63; the kernel subtracts 32).
+__global__ void k_q6k_decode_layout(DevMat W, uint32_t* out, int groups) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  const int c = i & 7, s = (i >> 3) & 15, g = i >> 7;
+  if (g >= groups) return;
+  const int nb = W.nb, rpg = 16 / nb;
+  const int row = g * rpg + s / nb, sb = s % nb;
+  const int p = c >> 1, ci = c & 1;
+  uint32_t* grp = out + (size_t)g * kQ6dGroupWords * 4;  // dwords
+  uint32_t lo[4] = {0, 0, 0, 0}, hi[2] = {0, 0}, sc[4] = {0, 0, 0, 0};
+  if (row < W.rows) {
+    const uint8_t* body = (const uint8_t*)W.w + ((size_t)row * nb + sb) * 208;
+    for (int j = 0; j < 32; j++) {
+      const int e = c + 8 * j, half = e / 128, within = e % 128, l = within % 32, part = within / 32;
+      const uint8_t qlb = body[64 * half + l + 32 * (part & 1)];
+      const uint32_t nib = (part >> 1) ? (qlb >> 4) : (qlb & 0x0fu);
+      const uint32_t h2 = (body[128 + 32 * half + l] >> (2 * part)) & 0x03u;
+      lo[j >> 3] |= nib << (8 * (j & 3) + 4 * ((j >> 2) & 1));
+      hi[j >> 4] |= h2 << (8 * (j & 3) + 2 * ((j >> 2) & 3));
+    }
+    for (int k = 0; k < 16; k++) sc[k >> 2] |= (uint32_t)body[192 + k] << (8 * (k & 3));
+  }
+  uint32_t* lw = grp + (size_t)(ci * 64 + s * 4 + p) * 4;
+  for (int k = 0; k < 4; k++) lw[k] = lo[k];
+  uint32_t* hw = grp + (size_t)(2 * 64 + s * 4 + p) * 4 + 2 * ci;
+  hw[0] = hi[0];
+  hw[1] = hi[1];
+  if (c == 0) {
+    uint32_t* sw = grp + (size_t)(192 + s) * 4;
+    for (int k = 0; k < 4; k++) sw[k] = sc[k];
+  }
+}
+
+void launch_q6k_decode_layout(const DevMat& W, uint4* out, hipStream_t s) {
+  const int rpg = 16 / W.nb, groups = (W.rows + rpg - 1) / rpg;
+  const int threads = groups * 128;
+  launch_kernel(k_q6k_decode_layout, dim3((threads + 255) / 256), dim3(256), 0, s, W, (uint32_t*)out, groups);
+}
+
+// dot_q6_k_q8k (det-quant lib.rs:353-397) over the decode layout, for tall
+// matrices (the output projection).  Lane (s, p) = (lane / 4, lane % 4) of a
+// wave owns class pair p of superblock s of each 16-superblock group the
+// wave visits (grid-stride, the next group's four words loaded as soon as a
+// group is reduced, unconditionally with the group clamped); the lane's
+// superblock column and classes are the same in every group, so its share
+// of the Q8_K activations is prepared once, in registers: for elements
+// j = 4m .. 4m + 3 of a class, the activation dword masked to its first and
+// second halves (the two scales j >> 1 = 2m, 2m + 1) and, for each half,
+// -32 times its sum.  The class sums are then exact integers from unsigned
+// quants q (0..63): dot4(q, half, -32 * sum of half) = sum (q - 32) * a, times
+// the half's scale.  Each lane forms d * aux[c] (d = w.d * a.d) for its two
+// classes; then one lane per (row, class) runs sums[c] += ... over the row's
+// superblocks in order, and one lane per row the final sum of sums[0..7], as
+// the reference does.
+template <int NB>
+__global__ void __launch_bounds__(256) k_gemv_q6k_cm(const uint4* __restrict__ q6d,
+                                                     const uint16_t* __restrict__ d16, int rows,
+                                                     const int8_t* __restrict__ qk,
+                                                     const float* __restrict__ dk, float* out,
+                                                     const float* bias, int epi, int* err) {
+  constexpr int RPG = 16 / NB;
+  __shared__ float terms[4][16][9];
+  __shared__ float sums_s[4][RPG][8];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = blockIdx.y;
+  const int s = lane >> 2, p = lane & 3, sb = s % NB;
+  const int ngroups = (rows + RPG - 1) / RPG;
+  const int stride = gridDim.x * 4;
+  int g = blockIdx.x * 4 + wave;
+  if (g >= ngroups) return;
+  // activation-side operands of classes 2p, 2p + 1 of superblock column sb
+  uint32_t ah[2][2][8], ak[2][2][8];
+  {
+    const uint4* ap = (const uint4*)(qk + (size_t)t * NB * 256 + (size_t)sb * 256 + p * 64);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint4 v = ap[k];
+      const uint32_t a4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int ci = k >> 1, m = 4 * (k & 1) + i;
+        ah[ci][0][m] = a4[i] & 0x0000ffffu;
+        ah[ci][1][m] = a4[i] & 0xffff0000u;
+        ak[ci][0][m] = (uint32_t)dot4(0xe0e0e0e0u, ah[ci][0][m], 0);
+        ak[ci][1][m] = (uint32_t)dot4(0xe0e0e0e0u, ah[ci][1][m], 0);
+      }
+    }
+  }
+  const float da = dk[(size_t)t * NB + sb];
+  float(*mine)[9] = terms[wave];
+  for (;;) {
+    const uint4* gp = q6d + (size_t)g * kQ6dGroupWords;
+    const uint4 l0 = gp[lane], l1 = gp[64 + lane], hw = gp[128 + lane], sw = gp[192 + s];
+    int row = g * RPG + s / NB;
+    row = row < rows ? row : rows - 1;
+    const float d = f16_to_f32(d16[(size_t)row * NB + sb]) * da;
+    const uint32_t scw[4] = {sw.x, sw.y, sw.z, sw.w};
+#pragma unroll
+    for (int ci = 0; ci < 2; ci++) {
+      const uint4 lw4 = ci ? l1 : l0;
+      const uint32_t L[4] = {lw4.x, lw4.y, lw4.z, lw4.w};
+      const uint32_t H[2] = {ci ? hw.z : hw.x, ci ? hw.w : hw.y};
+      int acc = 0;
+#pragma unroll
+      for (int m = 0; m < 8; m++) {
+        const uint32_t lw = (m & 1) ? L[m >> 1] >> 4 : L[m >> 1];
+        const uint32_t h = H[m >> 2];
+        const uint32_t hs = (m & 3) == 0 ? h << 4 : (m & 3) == 1 ? h << 2 : (m & 3) == 2 ? h : h >> 2;
+        const uint32_t q = (hs & 0x30303030u) | (lw & 0x0f0f0f0fu);
+        const int c0 = dot4(q, ah[ci][0][m], (int)ak[ci][0][m]);
+        const int c1 = dot4(q, ah[ci][1][m], (int)ak[ci][1][m]);
+        const int s0 = (int)(int8_t)((scw[m >> 1] >> (16 * (m & 1))) & 0xffu);
+        const int s1 = (int)(int8_t)((scw[m >> 1] >> (16 * (m & 1) + 8)) & 0xffu);
+        acc += __mul24(s0, c0) + __mul24(s1, c1);
+      }
+      mine[s][2 * p + ci] = d * (float)acc;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const int g0 = g;
+    g += stride;
+    const bool more = g < ngroups;
+    for (int rc = lane; rc < 8 * RPG; rc += 64) {  // (row, class) pairs: 128 when NB = 1
+      const int rl = rc >> 3, c = rc & 7;
+      float sm = 0.0f;
+#pragma unroll
+      for (int b = 0; b < NB; b++) sm += mine[rl * NB + b][c];
+      sums_s[wave][rl][c] = sm;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    if (lane < RPG) {
+      const int r = g0 * RPG + lane;
+      if (r < rows) {
+        float v = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; c++) v += sums_s[wave][lane][c];
+        if (!epilogue(v, out, (size_t)t * rows + r, bias, r, epi)) flag(err, ERRBIT_NON_FINITE);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    if (!more) break;
+  }
+}
+
+template <int NB>
+void launch_q6k_cm_nb(const DevMat& W, const DevAct& A, int T, float* out, const float* bias, int epi,
+                      int* err, hipStream_t s) {
+  // as many workgroups as stay resident, each wave walking groups grid-stride
+  static const int resident = [] {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemv_q6k_cm<NB>, 256, 0) != hipSuccess ||
+        cus <= 0 || per_cu <= 0)
+      return 256;
+    return cus * per_cu;
+  }();
+  const int ngroups = (W.rows + 16 / NB - 1) / (16 / NB);
+  int wgs = (ngroups + 3) / 4;
+  if (wgs > resident) wgs = resident;
+  launch_kernel(k_gemv_q6k_cm<NB>, dim3(wgs, T), dim3(256), 0, s, W.q6d, W.d16, W.rows, A.qk, A.dk, out, bias,
+                epi, err);
+}
+
+void launch_q6k_cm(const DevMat& W, const DevAct& A, int T, float* out, const float* bias, int epi, int* err,
+                   hipStream_t s) {
+  switch (W.nb) {
+    case 1: launch_q6k_cm_nb<1>(W, A, T, out, bias, epi, err, s); break;
+    case 2: launch_q6k_cm_nb<2>(W, A, T, out, bias, epi, err, s); break;
+    case 4: launch_q6k_cm_nb<4>(W, A, T, out, bias, epi, err, s); break;
+    case 8: launch_q6k_cm_nb<8>(W, A, T, out, bias, epi, err, s); break;
+    default: launch_q6k_cm_nb<16>(W, A, T, out, bias, epi, err, s); break;
+  }
+}
+
 // Q6_K with each superblock split over eight lanes: one row per workgroup
 // of 8 * nsb lanes (rounded up to whole waves), lane = (superblock sb, half
 // h, part pp) as in the fused wv rows of k_gemv_q4k_pc.  A lane forms its
@@ -1493,6 +1675,10 @@ bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const floa
       launch_q8<kGgmlQ8_0>(W, A, T, out, bias, epi, err, s, R);
     else
       launch_q8<kGgmlQ4_0>(W, A, T, out, bias, epi, err, s, R);
+    return true;
+  }
+  if (W.type == kGgmlQ6K && W.q6d) {
+    launch_q6k_cm(W, A, T, out, bias, epi, err, s);
     return true;
   }
   // Split superblocks for the per-layer matrices (ffn_down: 11.9 -> 10.0 us

@@ -196,6 +196,11 @@ GEMV_CASES = [
     # Q6_K decode at full TinyLlama ffn_down size (T = 8), odd row counts, and
     # a 16384-row matrix (the split-superblock kernel's largest)
     (14, 2048, 5632, 8), (14, 1000, 5632, 3), (14, 2049, 5632, 1), (14, 16384, 2048, 1),
+    # tall Q6_K on the decode layout (k_gemv_q6k_cm): the TinyLlama output
+    # projection, every superblock count that divides 16 (1 to 16 per row),
+    # partial last groups and several positions
+    (14, 32000, 2048, 1), (14, 16385, 256, 3), (14, 17000, 512, 1), (14, 20001, 1024, 2),
+    (14, 16400, 4096, 1), (14, 16390, 8192, 2), (14, 16401, 256, 1), (14, 8, 16384, 1),
     # Q8_0 / Q4_0 on the int8 matrix cores (T >= 16): odd block counts (a
     # half block pair), row tiles of 16 / 32 / 64, partial position tiles
     (8, 40, 32, 16), (8, 37, 96, 33), (8, 2100, 160, 17), (8, 8200, 64, 16), (8, 100, 896, 64),
