@@ -38,12 +38,15 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 FP32_VECTOR_PEAK_TFLOPS = 157.3        # FMA counted as two flops
 # The reference's f32 chains allow no FMA: every multiply-accumulate is a
-# separately rounded multiply and add, two VALU instructions.  A wave64 f32
-# VALU instruction issues every two cycles per SIMD (measured: 58 T lane-ops/s
-# from an unrolled mul/add loop at 8 waves per SIMD), i.e. 256 CU x 4 SIMD x
-# 32 lanes x 2.4 GHz = 78.6 T instructions/s: 39.3 T MAC/s = 78.6 TFLOP/s,
-# half the FMA peak.
-FP32_UNFUSED_PEAK_TFLOPS = 78.6
+# separately rounded multiply and add, two VALU instructions, and packed f32
+# instructions are not used.  A SIMD retires a wave64 f32 VALU instruction
+# every four cycles (16 lanes per clock): 256 CU x 4 SIMD x 16 lanes x
+# 2.4 GHz = 39.3 T lane-operations/s = 19.7 T MAC/s = 39.3 TFLOP/s counting
+# the multiply and the add, a quarter of the packed-FMA peak above.  The
+# library's dtl_valu_probe measures the same mix live (eight independent
+# multiply and eight add chains per lane, eight waves per SIMD: about 36 T
+# lane-operations/s, at the clock the chip holds under load).
+FP32_UNFUSED_PEAK_TFLOPS = 39.3
 
 
 # HBM bytes per launch of the encode's Q4_K kernel classes (any of them can
@@ -457,9 +460,11 @@ def main() -> int:
     if args.copy_probe_mib:
         return copy_probe(args.copy_probe_mib)
 
+    import ctypes
+
     import numpy as np
 
-    from detllm_amd import synth
+    from detllm_amd import _lib, synth
     from detllm_amd.model import F32Llama
 
     w = synth.WORKLOADS[args.workload]
@@ -545,10 +550,15 @@ def main() -> int:
     compute_bound = dom["macs"] > 0 and per_launch_flops / per_launch_bytes > 20.0
     if compute_bound:
         achieved = per_launch_flops / (avg_ms * 1e-3) / 1e12
+        probe = ctypes.c_double()
+        _lib.check(_lib.lib.dtl_valu_probe(ctypes.byref(probe)), "dtl_valu_probe")
+        measured = probe.value / 1e12
         roofline = {"bound": "valu", "achieved": round(achieved, 3), "peak": FP32_VECTOR_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / FP32_VECTOR_PEAK_TFLOPS, 4),
                     "unfused_peak": FP32_UNFUSED_PEAK_TFLOPS,
-                    "frac_of_unfused_peak": round(achieved / FP32_UNFUSED_PEAK_TFLOPS, 4)}
+                    "frac_of_unfused_peak": round(achieved / FP32_UNFUSED_PEAK_TFLOPS, 4),
+                    "unfused_peak_measured": round(measured, 2),
+                    "frac_of_measured_unfused_peak": round(achieved / measured, 4)}
     else:
         achieved = per_launch_bytes / (avg_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -1970,6 +1970,35 @@ int dtl_kernel_exp_clamped_f32(const float* in, float* out, size_t n) {
   return sc.finish(&bits);
 }
 
+int dtl_valu_probe(double* lane_ops_per_s) {
+  if (!lane_ops_per_s) return DTL_ERR_INVALID_ARGUMENT;
+  Scratch sc;
+  int st = sc.init();
+  if (st) return st;
+  int dev = 0, cus = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  float* out;
+  if ((st = sc.arena.alloc(&out, 1024))) return st;
+  // two 1024-thread workgroups per CU: eight waves on every SIMD
+  const int wgs = 2 * cus, iters = 20000;
+  hipEvent_t e0, e1;
+  HIP_TRY(hipEventCreate(&e0));
+  HIP_TRY(hipEventCreate(&e1));
+  launch_valu_probe(out, wgs, 64, sc.stream);
+  HIP_TRY(hipEventRecord(e0, sc.stream));
+  launch_valu_probe(out, wgs, iters, sc.stream);
+  HIP_TRY(hipEventRecord(e1, sc.stream));
+  HIP_TRY(hipEventSynchronize(e1));
+  float ms = 0.0f;
+  HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *lane_ops_per_s = (double)wgs * 1024.0 * iters * 16.0 / (ms * 1e-3);
+  int bits;
+  return sc.finish(&bits);
+}
+
 int dtl_kernel_f16_to_f32(const uint16_t* in, float* out, size_t n) {
   if (!in || !out) return DTL_ERR_INVALID_ARGUMENT;
   Scratch sc;

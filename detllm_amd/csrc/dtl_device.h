@@ -301,5 +301,8 @@ void launch_cdf_blocks(const float* logits, const uint32_t* rows, int R, int V, 
 void launch_exp_f32(const float* in, float* out, int n, int which, hipStream_t s);
 void launch_f16_to_f32(const uint16_t* in, float* out, int n, hipStream_t s);
 void launch_div_sqrt(const float* a, const float* b, float* q, float* r, int n, hipStream_t s);
+// 1024-thread workgroups of 16 VALU instructions (8 f32 multiplies, 8 f32
+// adds, independent chains) per iteration per lane.
+void launch_valu_probe(float* out, int workgroups, int iters, hipStream_t s);
 
 }  // namespace dtl

@@ -2646,4 +2646,35 @@ void launch_div_sqrt(const float* a, const float* b, float* q, float* r, int n, 
   launch_kernel(k_div_sqrt, dim3((n + 255) / 256), dim3(256), 0, s, a, b, q, r, n);
 }
 
+// ---------------------------------------------------------------------------
+// Measurement support: the issue rate of the instruction mix of the
+// reference's f32 chains, separately rounded multiplies and adds (no FMA, no
+// packed math).  Every lane runs eight independent multiply chains and eight
+// independent add chains, 16 VALU instructions per iteration, so the rate
+// is the VALU's, not a dependency's.  The result is written only for a value
+// no input produces, which keeps the work live.
+__global__ void __launch_bounds__(1024) k_valu_probe(float* out, float a, float b, int iters) {
+  float x[8], y[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    x[i] = (float)threadIdx.x * 1e-3f + (float)i;
+    y[i] = x[i] * 0.5f;
+  }
+  for (int it = 0; it < iters; it++) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      x[i] = x[i] * a;
+      y[i] = y[i] + b;
+    }
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) s = s + (x[i] + y[i]);
+  if (s == -1.0f) out[threadIdx.x] = s;
+}
+
+void launch_valu_probe(float* out, int workgroups, int iters, hipStream_t s) {
+  launch_kernel(k_valu_probe, dim3(workgroups), dim3(1024), 0, s, out, 1.0001f, 1e-7f, iters);
+}
+
 }  // namespace dtl

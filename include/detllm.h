@@ -398,6 +398,13 @@ int dtl_kernel_silu_f32(const float *in, float *out, size_t n);
  * t = x - max): the device's restatement for that domain.  A t > 0 is
  * DTL_ERR_INVALID_ARGUMENT. */
 int dtl_kernel_exp_clamped_f32(const float *in, float *out, size_t n);
+/* No counterpart in the reference: measurement support for the roofline of
+ * the f32 chain kernels.  Runs 16 f32 VALU instructions per iteration (eight
+ * separately rounded multiplies, eight adds, independent chains) on eight
+ * waves of every SIMD and returns the lanes' operations per second, the
+ * issue ceiling of the reference's multiply-then-add arithmetic without
+ * fused or packed instructions. */
+int dtl_valu_probe(double *lane_ops_per_s);
 /* f16 -> f32 (det-num f16.rs:6-34) on the device. */
 int dtl_kernel_f16_to_f32(const uint16_t *in, float *out, size_t n);
 /* sqrt and division as used by rmsnorm / softmax / quantisers. */

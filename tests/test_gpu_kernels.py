@@ -242,3 +242,15 @@ def test_rope_table_bitexact(theta, rope_dim):
     wc, ws = m.rope_table(positions)
     assert np.array_equal(c.view(np.uint32), wc.view(np.uint32))
     assert np.array_equal(s.view(np.uint32), ws.view(np.uint32))
+
+
+def test_valu_probe_rate_is_the_unfused_f32_issue_rate():
+    """dtl_valu_probe (measurement support for the bench's roofline): separately
+    rounded f32 multiplies and adds on eight waves of every SIMD.  A SIMD
+    retires 16 lanes of such an instruction per clock: 256 CU x 4 SIMD x 16
+    lanes at up to 2.4 GHz is at most 39.3 T lane-operations/s; under load the
+    clock stays above 1.5 GHz (24.6 T)."""
+    L = _lib()
+    r = C.c_double()
+    L.check(L.lib.dtl_valu_probe(C.byref(r)), "valu probe")
+    assert 24.6e12 < r.value <= 39.4e12, r.value
