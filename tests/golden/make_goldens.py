@@ -108,6 +108,17 @@ def codec_golden() -> dict:
             "oracle_seconds": round(time.time() - t0, 1)}
 
 
+def dumps(res: dict) -> str:
+    """JSON with one-space indents, and the per-row range triples one per line."""
+    triples = res.get("next_token_ranges")
+    if triples is None:
+        return json.dumps(res, indent=1) + "\n"
+    head = dict(res)
+    head["next_token_ranges"] = "@RANGES@"
+    rows = ",\n  ".join(json.dumps(t) for t in triples)
+    return json.dumps(head, indent=1).replace('"@RANGES@"', "[\n  " + rows + "\n ]") + "\n"
+
+
 def main(argv) -> None:
     detref.set_threads(int(os.environ.get("GOLDEN_THREADS", 0)) or os.cpu_count() or 1)
     todo = argv or ["smollm2", "qwen05", "tinyllama", "smollm2_l1", "codec"]
@@ -116,7 +127,7 @@ def main(argv) -> None:
         res = codec_golden() if name == "codec" else logits_golden(name)
         res["generator"] = "tests/golden/make_goldens.py"
         path = HERE / f"workload_{name}.json"
-        path.write_text(json.dumps(res, indent=1) + "\n")
+        path.write_text(dumps(res))
         print(f"{name}: {time.time() - t0:.0f} s -> {path.name}", flush=True)
 
 
