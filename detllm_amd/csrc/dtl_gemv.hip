@@ -812,10 +812,16 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
           const float we[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
           *reinterpret_cast<float4*>(xs + i) = xv[k];
           *reinterpret_cast<float4*>(ws + i) = wv[k];
+          // the element index through an empty asm: the four chain-major
+          // addresses are formed here, not at the kernel's start and held
+          // through the loads (at a 1024-thread launch's 128 registers they
+          // went to scratch)
+          int ia = i;
+          asm volatile("" : "+v"(ia));
 #pragma unroll
           for (int c = 0; c < 4; c++) {
             bad |= any_nonfinite(xe[c], we[c]);
-            sq[((i & 7) + c) * cs + (i >> 3)] = xe[c] * xe[c];
+            sq[((ia & 7) + c) * cs + (ia >> 3)] = xe[c] * xe[c];
           }
         }
       }

@@ -718,9 +718,14 @@ __global__ void __launch_bounds__(NT) k_attention_hd64(const float* q, const flo
   // 0, which commit never stores), so the compiler counts the loads in
   // flight instead of draining them at every tile.
   auto issue = [&](float4 (&dst)[PER], const float* base, int j0) {
+    // At 1024 threads (128 registers) the lane's thread index goes through
+    // an empty asm, so the V phase's per-lane addresses are formed where they
+    // are used rather than held from the kernel's start (they went to scratch)
+    int tx = threadIdx.x;
+    if constexpr (NT > 512) asm volatile("" : "+v"(tx));
 #pragma unroll
     for (int c = 0; c < PER; c++) {
-      const int x = threadIdx.x + c * nthreads;
+      const int x = tx + c * nthreads;
       const int j = x >> 4;
       const bool ok = x < 1024 && j0 + j < len;
       dst[c] = *reinterpret_cast<const float4*>(base + (size_t)(ok ? j0 + j : 0) * hd + (x & 15) * 4);
