@@ -39,14 +39,21 @@ HBM_PEAK_GBS = 8000.0
 FP32_VECTOR_PEAK_TFLOPS = 157.3        # FMA counted as two flops
 # The reference's f32 chains allow no FMA: every multiply-accumulate is a
 # separately rounded multiply and add, two VALU instructions, and packed f32
-# instructions are not used.  A SIMD retires a wave64 f32 VALU instruction
-# every four cycles (16 lanes per clock): 256 CU x 4 SIMD x 16 lanes x
-# 2.4 GHz = 39.3 T lane-operations/s = 19.7 T MAC/s = 39.3 TFLOP/s counting
-# the multiply and the add, a quarter of the packed-FMA peak above.  The
-# library's dtl_valu_probe measures the same mix live (eight independent
-# multiply and eight add chains per lane, eight waves per SIMD: about 36 T
-# lane-operations/s, at the clock the chip holds under load).
-FP32_UNFUSED_PEAK_TFLOPS = 39.3
+# instructions are not used.  A SIMD issues such instructions from two waves
+# at once, 16 lanes each per clock (the published 157.3 TFLOP/s is that rate
+# with FMA counted twice): 256 CU x 4 SIMD x 32 lanes x 2.4 GHz = 78.6 T
+# lane-operations/s = 39.3 T MAC/s = 78.6 TFLOP/s counting the multiply and
+# the add.  The library's dtl_valu_probe measures the mix live (eight
+# independent multiply and eight add chains per lane, operands in per-lane
+# registers, eight waves per SIMD).
+FP32_UNFUSED_PEAK_TFLOPS = 78.6
+
+# Kernel classes that form their products on the matrix cores (k_q4k_mfp) in
+# the chunk-at-a-time step the roofline is timed on: f32 16x16x1 MFMA outer
+# products, then one VALU add per multiply-add.  A SIMD runs the two one
+# after the other, so their bound is the pattern's own rate, which
+# dtl_mfp_probe measures live.
+MFMA_PRODUCT_CLASSES = {"gemm_q4_k_gate_up"}
 
 
 # HBM bytes per launch of the encode's Q4_K kernel classes (any of them can
@@ -58,8 +65,6 @@ FP32_UNFUSED_PEAK_TFLOPS = 39.3
 MEASURED_TRAFFIC = {
     "gemm_q4_k": {"bytes": (16778.5 * 2.000 + 512.0 * 1.000) * 1024.0,
                   "source": "profiles/k_q4k_f32m_tinyllama_encode_chunk64.md"},
-    "gemm_q4_k_gate_up": {"bytes": (58912.9 * 2.000 + 1408.0 * 1.000) * 1024.0,
-                          "source": "profiles/k_q4k_f32m_tinyllama_encode_chunk64.md"},
     "gemm_q4_k_qk": {"bytes": (11291.5 * 2.000 + 576.0 * 1.000) * 1024.0,
                      "source": "profiles/k_q4k_f32m_tinyllama_encode_chunk64.md"},
 }
@@ -551,14 +556,22 @@ def main() -> int:
     if compute_bound:
         achieved = per_launch_flops / (avg_ms * 1e-3) / 1e12
         probe = ctypes.c_double()
-        _lib.check(_lib.lib.dtl_valu_probe(ctypes.byref(probe)), "dtl_valu_probe")
-        measured = probe.value / 1e12
-        roofline = {"bound": "valu", "achieved": round(achieved, 3), "peak": FP32_VECTOR_PEAK_TFLOPS,
-                    "unit": "TFLOP/s", "frac": round(achieved / FP32_VECTOR_PEAK_TFLOPS, 4),
-                    "unfused_peak": FP32_UNFUSED_PEAK_TFLOPS,
-                    "frac_of_unfused_peak": round(achieved / FP32_UNFUSED_PEAK_TFLOPS, 4),
-                    "unfused_peak_measured": round(measured, 2),
-                    "frac_of_measured_unfused_peak": round(achieved / measured, 4)}
+        roofline = {"achieved": round(achieved, 3), "peak": FP32_VECTOR_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(achieved / FP32_VECTOR_PEAK_TFLOPS, 4)}
+        if dom_name in MFMA_PRODUCT_CLASSES:
+            _lib.check(_lib.lib.dtl_mfp_probe(ctypes.byref(probe)), "dtl_mfp_probe")
+            ceiling = 2.0 * probe.value / 1e12  # multiply and add counted
+            roofline.update({"bound": "mfma+valu", "ceiling_measured": round(ceiling, 2),
+                             "ceiling_source": "dtl_mfp_probe (4 f32 16x16x1 MFMAs + 64 adds per lane, "
+                                               "4 waves per SIMD)",
+                             "frac_of_measured_ceiling": round(achieved / ceiling, 4)})
+        else:
+            _lib.check(_lib.lib.dtl_valu_probe(ctypes.byref(probe)), "dtl_valu_probe")
+            measured = probe.value / 1e12  # lane-ops/s = flop/s at two instructions per MAC
+            roofline.update({"bound": "valu", "unfused_peak": FP32_UNFUSED_PEAK_TFLOPS,
+                             "frac_of_unfused_peak": round(achieved / FP32_UNFUSED_PEAK_TFLOPS, 4),
+                             "unfused_peak_measured": round(measured, 2),
+                             "frac_of_measured_unfused_peak": round(achieved / measured, 4)})
     else:
         achieved = per_launch_bytes / (avg_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -158,6 +158,7 @@ _SIGS = {
     "dtl_kernel_silu_f32": (C.c_int, [f32p, f32p, sz]),
     "dtl_kernel_exp_clamped_f32": (C.c_int, [f32p, f32p, sz]),
     "dtl_valu_probe": (C.c_int, [C.POINTER(C.c_double)]),
+    "dtl_mfp_probe": (C.c_int, [C.POINTER(C.c_double)]),
     "dtl_kernel_f16_to_f32": (C.c_int, [u16p, f32p, sz]),
     "dtl_kernel_div_sqrt": (C.c_int, [f32p, f32p, f32p, f32p, sz]),
     "dtl_kernel_quantize": (C.c_int, [f32p, sz, sz, f32p, i8p, f32p, i8p]),

@@ -28,6 +28,7 @@ SOURCES = [
     "dtl_gemm.hip",
     "dtl_gemv.hip",
     "dtl_api.hip",
+    "dtl_mfp.hip",
     "dtl_gguf.cpp",
     "dtl_range.cpp",
     "dtl_token.cpp",
@@ -41,6 +42,12 @@ NUMERIC_FLAGS = [
     "-fno-gpu-flush-denormals-to-zero",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
+
+# Per-source additions: the MFMA-product GEMMs take their results in VGPRs
+# (the VALU adds read them; in accumulation registers each would need a copy).
+EXTRA_FLAGS = {
+    "dtl_mfp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
 
 
 def hipcc() -> str:
@@ -74,7 +81,8 @@ def build_library(verbose: bool = False, jobs: int = 0) -> Path:
     common = [hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", *NUMERIC_FLAGS,
               "-Wno-unused-result"]
     objs = [OUT_DIR / (Path(s).stem + ".o") for s in SOURCES]
-    cmds = [common + ["-c", str(CSRC / s), "-o", str(o)] for s, o in zip(SOURCES, objs)]
+    cmds = [common + EXTRA_FLAGS.get(s, []) + ["-c", str(CSRC / s), "-o", str(o)]
+            for s, o in zip(SOURCES, objs)]
     jobs = jobs or min(len(cmds), os.cpu_count() or 1, 16)
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         for f in [ex.submit(_run, c, verbose) for c in cmds]:

@@ -1999,6 +1999,36 @@ int dtl_valu_probe(double* lane_ops_per_s) {
   return sc.finish(&bits);
 }
 
+int dtl_mfp_probe(double* macs_per_s) {
+  if (!macs_per_s) return DTL_ERR_INVALID_ARGUMENT;
+  Scratch sc;
+  int st = sc.init();
+  if (st) return st;
+  int dev = 0, cus = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  float* out;
+  if ((st = sc.arena.alloc(&out, 256))) return st;
+  // four 256-thread workgroups per CU: four waves on every SIMD
+  const int wgs = 4 * cus, iters = 20000;
+  hipEvent_t e0, e1;
+  HIP_TRY(hipEventCreate(&e0));
+  HIP_TRY(hipEventCreate(&e1));
+  launch_mfp_probe(out, wgs, 64, sc.stream);
+  HIP_TRY(hipEventRecord(e0, sc.stream));
+  launch_mfp_probe(out, wgs, iters, sc.stream);
+  HIP_TRY(hipEventRecord(e1, sc.stream));
+  HIP_TRY(hipEventSynchronize(e1));
+  float ms = 0.0f;
+  HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  // 4096 products (and adds) per wave per iteration, four waves per workgroup
+  *macs_per_s = (double)wgs * 4.0 * iters * 4096.0 / (ms * 1e-3);
+  int bits;
+  return sc.finish(&bits);
+}
+
 int dtl_kernel_f16_to_f32(const uint16_t* in, float* out, size_t n) {
   if (!in || !out) return DTL_ERR_INVALID_ARGUMENT;
   Scratch sc;

@@ -120,6 +120,36 @@ struct DevAct {
 
 enum GemmEpilogue : int { EPI_STORE = 0, EPI_BIAS = 1, EPI_RESIDUAL = 2 };
 
+// Q4_K chunk GEMMs from the exact f32 weight copy (the values q4_k_value
+// yields, det-quant lib.rs:506-517), every output one chain of products in
+// element order:
+//   MODE_SINGLE  one matrix
+//   MODE_PAIR    gate and up (same shape): silu(gate)*up (det-model
+//                lib.rs:2420-2434) written in the epilogue
+//   MODE_CAT     two matrices with the same input (e.g. wq and wk), their
+//                rows concatenated into one grid, separate outputs
+enum { MODE_SINGLE = 0, MODE_PAIR = 1, MODE_CAT = 2 };
+
+struct Q4kF32Args {
+  const float* w0;
+  const float* w1;
+  int rows0, rows1, cols;
+  const float* af;
+  int T;
+  float* out0;
+  float* out1;
+  float* ffo;
+  const float* bias0;
+  const float* bias1;
+  int epi;
+  int* err;
+};
+
+// The products on the matrix cores (k_q4k_mfp, dtl_mfp.hip), and the probe
+// of their inner pattern's rate.
+void launch_q4k_mfp(const Q4kF32Args& a, int mode, hipStream_t s);
+void launch_mfp_probe(float* out, int workgroups, int iters, hipStream_t s);
+
 // Positions up to which the decode GEMVs (one weight pass per position)
 // replace the chunked-encode GEMMs.
 constexpr int kGemvMaxT = 8;

@@ -346,51 +346,29 @@ __global__ void __launch_bounds__(256) k_q8_0_tok(DevMat W, const int8_t* __rest
 }
 
 // ---------------------------------------------------------------------------
-// Q4_K from an exact f32 copy of the weights (the values q4_k_value yields,
-// det-quant lib.rs:506-517, computed once at load), every output one chain
-// of products in element order:
-//   MODE_SINGLE  one matrix
-//   MODE_PAIR    gate and up (same shape): silu(gate)*up (det-model
-//                lib.rs:2420-2434) written in the epilogue
-//   MODE_CAT     two matrices with the same input (e.g. wq and wk), their
-//                rows concatenated into one grid, separate outputs
-enum { MODE_SINGLE = 0, MODE_PAIR = 1, MODE_CAT = 2 };
-
-struct Q4kF32Args {
-  const float* w0;
-  const float* w1;
-  int rows0, rows1, cols;
-  const float* af;
-  int T;
-  float* out0;
-  float* out1;
-  float* ffo;
-  const float* bias0;
-  const float* bias1;
-  int epi;
-  int* err;
-};
-
-// The lanes of a wave are split over positions and rows, and each lane
+// Q4_K from an exact f32 copy of the weights (Q4kF32Args, the modes in
+// dtl_device.h; one matrix, or two concatenated), every output one chain of
+// products in element order.  The lanes of a wave are split over positions and rows, and each lane
 // holds a PP x RP block of chains: lane = (p = lane % PW, r = lane / PW),
 // RW = 64 / PW; the lane's positions are p + PW i (i < PP) and its rows
-// r + RW j (j < RP) of each matrix, one chain per (position, row, matrix),
-// every chain in element order.  A wave covers PW PP positions of RW RP
+// r + RW j (j < RP), one chain per (position, row), every chain in
+// element order.  A wave covers PW PP positions of RW RP
 // rows; a workgroup is WP x WR waves covering PB positions of RB rows and
 // stages each 64-element slice of those positions' activations and rows'
 // weights in LDS once (double-buffered, the next slice's global loads in
-// flight).  Per four elements a lane reads PP activation and NM RP weight
-// float4 for NM PP RP chains: the blocking divides the LDS bytes per
+// flight).  Per four elements a lane reads PP activation and RP weight
+// float4 for PP RP chains: the blocking divides the LDS bytes per
 // multiply-add, which bound the one-chain mapping, by the block's size
 // over its perimeter.
 template <int PW, int PP, int RP, int WP, int WR, int MODE>
 __global__ void __launch_bounds__(64 * WP * WR) k_q4k_f32m(Q4kF32Args p) {
+  static_assert(MODE != MODE_PAIR, "gate + up runs on k_q4k_mfp");
   constexpr int NT = 64 * WP * WR;
-  constexpr int NM = MODE == MODE_PAIR ? 2 : 1;
+  constexpr int NM = 1;
   constexpr int RW = 64 / PW;
   constexpr int PWV = PW * PP, RWV = RW * RP;  // positions, rows per wave
   constexpr int PB = WP * PWV;                 // positions per workgroup
-  constexpr int RB = WR * RWV;                 // rows per workgroup (of each matrix)
+  constexpr int RB = WR * RWV;                 // rows per workgroup
   constexpr int NR = PB + NM * RB;             // staged LDS rows per slice
   constexpr int SL = 64, LD = SL + 4;          // elements per slice, padded LDS row
   constexpr int F = NR * SL / 4;               // float4 per slice
@@ -426,10 +404,6 @@ __global__ void __launch_bounds__(64 * WP * WR) k_q4k_f32m(Q4kF32Args p) {
       return p.af + (size_t)(tt < T ? tt : T - 1) * cols + c4 * 4;
     }
     const int wrow = sr - PB;
-    if (MODE == MODE_PAIR) {
-      const int m = wrow / RB, rr = blockIdx.x * RB + wrow % RB;
-      return (m ? p.w1 : p.w0) + (size_t)(rr < p.rows0 ? rr : p.rows0 - 1) * cols + c4 * 4;
-    }
     int gg = blockIdx.x * RB + wrow;
     gg = gg < rows_total ? gg : rows_total - 1;
     const bool m = MODE == MODE_CAT && gg >= p.rows0;
@@ -516,18 +490,11 @@ __global__ void __launch_bounds__(64 * WP * WR) k_q4k_f32m(Q4kF32Args p) {
     for (int j = 0; j < RP; j++) {
       const int g = blockIdx.x * RB + rrow + RW * j;  // row of the concatenation
       if (g >= rows_total) continue;
-      if (MODE == MODE_PAIR) {
-        const float gv = acc[0][i][j], uv = acc[NM - 1][i][j];
-        const float v = silu_det(gv) * uv;
-        ok &= finite(gv) && finite(uv) && finite(v);
-        p.ffo[(size_t)t * p.rows0 + g] = v;
-      } else {
-        const bool m = MODE == MODE_CAT && g >= p.rows0;
-        const int local = m ? g - p.rows0 : g;
-        const int R = m ? p.rows1 : p.rows0;
-        ok &= store_epilogue(acc[0][i][j], m ? p.out1 : p.out0, (size_t)t * R + local,
-                             m ? p.bias1 : p.bias0, local, p.epi);
-      }
+      const bool m = MODE == MODE_CAT && g >= p.rows0;
+      const int local = m ? g - p.rows0 : g;
+      const int R = m ? p.rows1 : p.rows0;
+      ok &= store_epilogue(acc[0][i][j], m ? p.out1 : p.out0, (size_t)t * R + local,
+                           m ? p.bias1 : p.bias0, local, p.epi);
     }
   }
   if (!ok) flag(p.err, ERRBIT_NON_FINITE);
@@ -967,23 +934,17 @@ int rows_per_wave(int rows) {
   return 1;
 }
 
-// Tiles of the blocked Q4_K kernel (k_q4k_f32m<PW, PP, RP, WP, WR>), chosen
-// on the pipelined TinyLlama encode (64 positions, four chunks in flight):
-//   single (wo, ffn_down)  8 positions x 8 rows of lanes, 1 x 2 chains per
-//                          lane, 4 waves over 32 positions x 16 rows
-//   pair   (gate + up)     4 x 16 lanes, 2 positions x (gate, up) per lane,
-//                          4 waves over 32 positions x 16 rows
-//   cat    (wq + wk)       8 x 8 lanes, 1 x 2 chains, 2 x 2 waves
-// Blocked lanes run fewer waves than one chain per lane: with the other
-// chunks' launches filling the CUs the LDS bytes per multiply-add bound the
-// launches, and the blocked tiles make the step 10% faster (123.7 vs 137.6
-// ms), but a launch that has the chip to itself then has too few waves.  A
-// launch with no other chunk in flight (dtl_forward_chunk, the decode-size
-// chunks) runs one chain per lane instead, 8 x 8 lanes, 2 x 2 waves over 16
-// positions x 16 rows: wo / ffn_down 59.9 -> 41.6 ms and wq + wk 26.3 ->
-// 24.2 ms per chunk-at-a-time step.  The gate + up pair keeps its tile;
-// pair tiles of eight chains per lane (2 x 2, 4 x 1 and 4 x 1 over two
-// waves) were 0.7-9% slower over the pipelined step (fewer waves per CU).
+// Which Q4_K chunk GEMM serves a launch.  The products on the matrix cores
+// (k_q4k_mfp) own 16 x 16 (row, position) chains per wave, so a launch of
+// wo / ffn_down or wq + wk at 64 positions has 512-576 waves: with other
+// chunks' launches in flight (the pipelined encode) they and the gate + up
+// pair (2816 waves) run there, the pipelined TinyLlama step taking 98.5 ms
+// against 118.5 with k_q4k_f32m.  A launch alone on the chip
+// (dtl_forward_chunk, the decode-size chunks) keeps one chain per lane of
+// k_q4k_f32m for wo / ffn_down and wq + wk, 8 x 8 lanes, 2 x 2 waves over
+// 16 positions x 16 rows, which fills the chip (chunk-at-a-time step: wo /
+// ffn_down 39.9 ms against 58.1 on the matrix cores, wq + wk 23.1 against
+// 24.9); gate + up takes the matrix cores there too (45.4 against 56.3 ms).
 template <int PW, int PP, int RP, int WP, int WR, int MODE>
 void launch_q4k_f32m(const Q4kF32Args& a, int rows_total, hipStream_t s) {
   constexpr int RB = WR * RP * 64 / PW, PB = WP * PW * PP;
@@ -993,11 +954,9 @@ void launch_q4k_f32m(const Q4kF32Args& a, int rows_total, hipStream_t s) {
 
 template <int MODE>
 void launch_q4k_f32w(const Q4kF32Args& a, bool overlapped, hipStream_t s) {
+  if (MODE == MODE_PAIR || overlapped) return launch_q4k_mfp(a, MODE, s);
   const int rows_total = MODE == MODE_CAT ? a.rows0 + a.rows1 : a.rows0;
-  if (MODE != MODE_PAIR && !overlapped) return launch_q4k_f32m<8, 1, 1, 2, 2, MODE>(a, rows_total, s);
-  if (MODE == MODE_SINGLE) return launch_q4k_f32m<8, 1, 2, 4, 1, MODE>(a, rows_total, s);
-  if (MODE == MODE_PAIR) return launch_q4k_f32m<4, 2, 1, 4, 1, MODE>(a, rows_total, s);
-  launch_q4k_f32m<8, 1, 2, 2, 2, MODE>(a, rows_total, s);
+  launch_q4k_f32m<8, 1, 1, 2, 2, MODE == MODE_CAT ? MODE_CAT : MODE_SINGLE>(a, rows_total, s);
 }
 
 Q4kF32Args q4k_args(const DevMat& W0, const DevMat* W1, const DevAct& A, int T, float* out0,

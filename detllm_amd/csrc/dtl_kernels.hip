@@ -2656,15 +2656,21 @@ void launch_div_sqrt(const float* a, const float* b, float* q, float* r, int n, 
 // reference's f32 chains, separately rounded multiplies and adds (no FMA, no
 // packed math).  Every lane runs eight independent multiply chains and eight
 // independent add chains, 16 VALU instructions per iteration, so the rate
-// is the VALU's, not a dependency's.  The result is written only for a value
-// no input produces, which keeps the work live.
-__global__ void __launch_bounds__(1024) k_valu_probe(float* out, float a, float b, int iters) {
+// is the VALU's, not a dependency's.  Both operands are per-lane registers,
+// as in the kernels (their operands come from LDS and memory): a SIMD
+// issues two such instructions from different waves at once, where an
+// operand read from a scalar register halves the rate.  The result is
+// written only for a value no input produces, which keeps the work live.
+__global__ void __launch_bounds__(1024) k_valu_probe(float* out, float a0, float b0, int iters) {
   float x[8], y[8];
 #pragma unroll
   for (int i = 0; i < 8; i++) {
     x[i] = (float)threadIdx.x * 1e-3f + (float)i;
     y[i] = x[i] * 0.5f;
   }
+  // per-lane copies of the operands (the asm hides that they are uniform)
+  float a = a0, b = b0;
+  asm volatile("" : "+v"(a), "+v"(b));
   for (int it = 0; it < iters; it++) {
 #pragma unroll
     for (int i = 0; i < 8; i++) {

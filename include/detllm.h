@@ -400,11 +400,17 @@ int dtl_kernel_silu_f32(const float *in, float *out, size_t n);
 int dtl_kernel_exp_clamped_f32(const float *in, float *out, size_t n);
 /* No counterpart in the reference: measurement support for the roofline of
  * the f32 chain kernels.  Runs 16 f32 VALU instructions per iteration (eight
- * separately rounded multiplies, eight adds, independent chains) on eight
- * waves of every SIMD and returns the lanes' operations per second, the
- * issue ceiling of the reference's multiply-then-add arithmetic without
- * fused or packed instructions. */
+ * separately rounded multiplies, eight adds, independent chains, operands in
+ * per-lane registers) on eight waves of every SIMD and returns the lanes'
+ * operations per second, the issue ceiling of the reference's
+ * multiply-then-add arithmetic without fused or packed instructions. */
 int dtl_valu_probe(double *lane_ops_per_s);
+/* No counterpart in the reference: measurement support for the roofline of
+ * the Q4_K chunk GEMMs.  Runs their inner pattern (four f32 16x16x1 MFMA
+ * outer products, then 64 ordered adds per lane) on four waves of every SIMD
+ * and returns multiply-adds per second: the SIMD runs the MFMAs and the adds
+ * one after the other, so this bounds those kernels. */
+int dtl_mfp_probe(double *macs_per_s);
 /* f16 -> f32 (det-num f16.rs:6-34) on the device. */
 int dtl_kernel_f16_to_f32(const uint16_t *in, float *out, size_t n);
 /* sqrt and division as used by rmsnorm / softmax / quantisers. */

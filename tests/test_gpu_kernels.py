@@ -189,6 +189,9 @@ GEMV_CASES = [
     (2, 40, 64, 2), (2, 17, 512, 1), (2, 66000, 64, 1), (2, 5000, 96, 3),
     (12, 45, 2048, 1), (12, 7, 5632, 3), (12, 30, 512, 64), (12, 9000, 256, 1), (12, 13, 256, 8),
     (12, 45, 256, 37), (12, 100, 768, 20),
+    # Q4_K chunk GEMMs: partial row and position tiles, one and several
+    # slices per superblock, the ffn_down width
+    (12, 17, 2048, 16), (12, 130, 1024, 33), (12, 48, 5632, 64), (12, 1, 256, 17),
     # 8 positions x 5632 columns: the split decode kernel's LDS does not hold
     # the activations, so the one-lane-per-row Q4_K kernel serves it
     (12, 20, 5632, 8),
@@ -246,11 +249,25 @@ def test_rope_table_bitexact(theta, rope_dim):
 
 def test_valu_probe_rate_is_the_unfused_f32_issue_rate():
     """dtl_valu_probe (measurement support for the bench's roofline): separately
-    rounded f32 multiplies and adds on eight waves of every SIMD.  A SIMD
-    retires 16 lanes of such an instruction per clock: 256 CU x 4 SIMD x 16
-    lanes at up to 2.4 GHz is at most 39.3 T lane-operations/s; under load the
-    clock stays above 1.5 GHz (24.6 T)."""
+    rounded f32 multiplies and adds with per-lane register operands on eight
+    waves of every SIMD.  A SIMD issues such instructions from two waves at
+    once, 16 lanes each per clock: 256 CU x 4 SIMD x 32 lanes at up to 2.4 GHz
+    is at most 78.6 T lane-operations/s, and the rate must exceed what one
+    issue per SIMD allows at that clock (39.3 T)."""
     L = _lib()
     r = C.c_double()
     L.check(L.lib.dtl_valu_probe(C.byref(r)), "valu probe")
-    assert 24.6e12 < r.value <= 39.4e12, r.value
+    assert 39.4e12 < r.value <= 78.7e12, r.value
+
+
+def test_mfp_probe_rate_is_between_the_units_alone():
+    """dtl_mfp_probe: k_q4k_mfp's inner pattern (four f32 16x16x1 outer
+    products, 64 ordered adds per lane) on four waves of every SIMD.  The
+    MFMAs alone would allow 32 products per clock per SIMD (78.6 T/s at
+    2.4 GHz); the adds share the SIMD with them, and the pattern must still
+    beat the two VALU instructions per multiply-add of the VALU-only chains
+    at one issue per SIMD (19.7 T/s)."""
+    L = _lib()
+    r = C.c_double()
+    L.check(L.lib.dtl_mfp_probe(C.byref(r)), "mfp probe")
+    assert 19.7e12 < r.value <= 78.7e12, r.value

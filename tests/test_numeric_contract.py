@@ -26,8 +26,10 @@ gfx950 assembly:
 - no hardware transcendental approximation (v_exp/v_log/v_sin/v_cos/v_rsq;
   v_rcp_f32 and v_rcp_iflag_f32 remain as the seeds of the correctly rounded
   divide expansion and of integer division, whose results are exact);
-- matrix-core instructions only in the chunked encode GEMMs (dtl_gemm.hip),
-  and only the exact int8 form.
+- matrix-core instructions only in the chunked encode GEMMs: the exact int8
+  form (dtl_gemm.hip), and the f32 outer product with one element of K
+  (dtl_mfp.hip), every one with the literal 0 as its accumulator, so that
+  each result is one rounded product and no MFMA adds.
 
 Sources: no platform transcendental or fast intrinsic is called, and the
 only explicit fma is div_recip's.
@@ -55,7 +57,7 @@ def device_code(tmp_path_factory):
     def one(src, kind):
         out = d / f"{Path(src).stem}.{kind}"
         extra = ["-emit-llvm", "-S"] if kind == "ll" else ["-S"]
-        res = subprocess.run([cc, *FLAGS, *extra, str(B.CSRC / src), "-o", str(out)],
+        res = subprocess.run([cc, *FLAGS, *B.EXTRA_FLAGS.get(src, []), *extra, str(B.CSRC / src), "-o", str(out)],
                              capture_output=True, text=True)
         assert res.returncode == 0, res.stderr[-2000:]
         return out.read_text()
@@ -154,6 +156,7 @@ _SCALAR_WRITE = re.compile(r"^\s*s_(?:store|buffer_store|scratch_store|atomic|bu
 _PACKED_F32 = re.compile(r"^\s*v_pk_(?:add|mul|fma|mov)_f32", re.M)
 _HW_APPROX = re.compile(r"^\s*v_(?:exp|log|sin|cos|rsq|exp_legacy|log_legacy)_f32", re.M)
 _MFMA = re.compile(r"^\s*(v_mfma_\w+)", re.M)
+_MFMA_F32_LINE = re.compile(r"^\s*v_mfma_f32_\w+[^\n]*", re.M)
 
 
 def test_asm_has_no_packed_f32_scalar_writes_or_hw_approximations(device_code):
@@ -165,6 +168,10 @@ def test_asm_has_no_packed_f32_scalar_writes_or_hw_approximations(device_code):
         mfma = set(_MFMA.findall(asm))
         if src == "dtl_gemm.hip":
             assert mfma == {"v_mfma_i32_16x16x64_i8"}, mfma
+        elif src == "dtl_mfp.hip":
+            assert mfma == {"v_mfma_f32_16x16x1_4b_f32"}, mfma
+            lines = _MFMA_F32_LINE.findall(asm)
+            assert lines and all(ln.split(";")[0].rstrip().endswith(", 0") for ln in lines), lines[:4]
         else:
             assert not mfma, (src, mfma)
 
