@@ -63,6 +63,8 @@ MFMA_PRODUCT_CLASSES = {"gemm_q4_k_gate_up"}
 # counter onto the known bytes of a plain copy (--copy-probe-mib).  The
 # summary with the commands is the `source` file.
 MEASURED_TRAFFIC = {
+    "gemm_q4_k_gate_up": {"bytes": (63899.2 * 2.000 + 1408.1 * 1.000) * 1024.0,
+                          "source": "profiles/k_q4k_mfp_tinyllama_encode_chunk64.md"},
     "gemm_q4_k": {"bytes": (16778.5 * 2.000 + 512.0 * 1.000) * 1024.0,
                   "source": "profiles/k_q4k_f32m_tinyllama_encode_chunk64.md"},
     "gemm_q4_k_qk": {"bytes": (11291.5 * 2.000 + 576.0 * 1.000) * 1024.0,
