@@ -164,6 +164,7 @@ _SIGS = {
     "dtl_kernel_quantize": (C.c_int, [f32p, sz, sz, f32p, i8p, f32p, i8p]),
     "dtl_kernel_rmsnorm": (C.c_int, [f32p, f32p, C.c_float, sz, sz, f32p]),
     "dtl_kernel_gemv": (C.c_int, [C.c_int, u8p, sz, sz, f32p, sz, f32p]),
+    "dtl_kernel_q4k_chunk": (C.c_int, [C.c_int, C.c_int, u8p, sz, u8p, sz, sz, f32p, sz, f32p, f32p]),
     "dtl_kernel_rope_table": (C.c_int, [C.c_float, sz, sz, f32p, f32p]),
 }
 

@@ -2114,17 +2114,16 @@ int dtl_kernel_rmsnorm(const float* x, const float* w, float eps, size_t rows, s
   return bits ? DTL_ERR_NON_FINITE : DTL_OK;
 }
 
-int dtl_kernel_gemv(int ggml_type, const uint8_t* weights, size_t rows, size_t cols,
-                    const float* x, size_t T, float* out) {
-  if (!weights || !x || !out || rows == 0 || cols == 0 || T == 0) return DTL_ERR_INVALID_ARGUMENT;
+namespace {
+// A matrix of raw GGUF blocks on the device as a loaded model holds it: the
+// bytes are wrapped in a one-tensor GGUF container so that the load-time
+// repack path (upload_matrix) is the one under test, then the encode-GEMM
+// and decode-layout copies a loaded model keeps are built.
+int upload_raw_matrix(Scratch& sc, int ggml_type, const uint8_t* weights, size_t rows, size_t cols,
+                      DevMat* out) {
   uint64_t tb, bs;
   if (!ggml_type_size((uint32_t)ggml_type, &tb, &bs)) return DTL_ERR_UNSUPPORTED_TENSOR_TYPE;
   if (cols % bs) return DTL_ERR_SHAPE;
-  Scratch sc;
-  int st = sc.init();
-  if (st) return st;
-  // Wrap the bytes in a one-tensor GGUF container so the load-time repack
-  // path (upload_matrix) is the one under test.
   size_t row_bytes = cols / bs * tb;
   std::vector<uint8_t> file;
   auto put = [&](const void* p, size_t k) {
@@ -2151,8 +2150,8 @@ int dtl_kernel_gemv(int ggml_type, const uint8_t* weights, size_t rows, size_t c
   const GgufTensor* gt;
   if (g.tensor("w", &gt) != GgufError::None) return DTL_ERR_GGUF;
   DevMat W{};
+  int st;
   if ((st = upload_matrix(g, *gt, rows, cols, sc.arena, &W))) return st;
-  // The same encode-GEMM copies a loaded model keeps.
   if (W.type == GGML_Q4_K && f32_mirror_enabled()) {
     float* w32;
     if ((st = sc.arena.alloc(&w32, rows * cols))) return st;
@@ -2177,6 +2176,19 @@ int dtl_kernel_gemv(int ggml_type, const uint8_t* weights, size_t rows, size_t c
     launch_q6k_decode_layout(W, q6d, sc.stream);
     W.q6d = q6d;
   }
+  *out = W;
+  return DTL_OK;
+}
+}  // namespace
+
+int dtl_kernel_gemv(int ggml_type, const uint8_t* weights, size_t rows, size_t cols,
+                    const float* x, size_t T, float* out) {
+  if (!weights || !x || !out || rows == 0 || cols == 0 || T == 0) return DTL_ERR_INVALID_ARGUMENT;
+  Scratch sc;
+  int st = sc.init();
+  if (st) return st;
+  DevMat W{};
+  if ((st = upload_raw_matrix(sc, ggml_type, weights, rows, cols, &W))) return st;
   float *dx, *dout, *af, *da, *dk;
   int8_t *qa, *qk;
   if ((st = sc.arena.upload(&dx, x, T * cols))) return st;
@@ -2192,6 +2204,47 @@ int dtl_kernel_gemv(int ggml_type, const uint8_t* weights, size_t rows, size_t c
   DevAct a{dx, qa, da, af, qk, dk};
   launch_gemm(W, a, (int)T, dout, nullptr, EPI_STORE, sc.err, sc.stream);
   HIP_TRY(hipMemcpyAsync(out, dout, T * rows * 4, hipMemcpyDeviceToHost, sc.stream));
+  int bits = 0;
+  if ((st = sc.finish(&bits))) return st;
+  return bits ? DTL_ERR_NON_FINITE : DTL_OK;
+}
+
+int dtl_kernel_q4k_chunk(int mode, int overlapped, const uint8_t* w0, size_t rows0, const uint8_t* w1,
+                         size_t rows1, size_t cols, const float* x, size_t T, float* out0, float* out1) {
+  if (mode < 0 || mode > 2 || !w0 || !x || !out0 || rows0 == 0 || cols == 0 || T == 0)
+    return DTL_ERR_INVALID_ARGUMENT;
+  if (mode != 0 && !w1) return DTL_ERR_INVALID_ARGUMENT;
+  if (mode == 2 && (!out1 || rows1 == 0)) return DTL_ERR_INVALID_ARGUMENT;
+  if (mode == 1) rows1 = rows0;  // gate and up have the same shape
+  if (T < 16 || cols % 256) return DTL_ERR_SHAPE;
+  if (!f32_mirror_enabled()) return DTL_ERR_UNSUPPORTED_TENSOR_TYPE;
+  Scratch sc;
+  int st = sc.init();
+  if (st) return st;
+  DevMat W0{}, W1{};
+  if ((st = upload_raw_matrix(sc, GGML_Q4_K, w0, rows0, cols, &W0))) return st;
+  if (mode != 0 && (st = upload_raw_matrix(sc, GGML_Q4_K, w1, rows1, cols, &W1))) return st;
+  float *dx, *d0, *d1 = nullptr, *af, *da;
+  int8_t* qa;
+  if ((st = sc.arena.upload(&dx, x, T * cols))) return st;
+  if ((st = sc.arena.alloc(&d0, T * rows0))) return st;
+  if (mode == 2 && (st = sc.arena.alloc(&d1, T * rows1))) return st;
+  if ((st = sc.arena.alloc(&qa, T * cols))) return st;
+  if ((st = sc.arena.alloc(&af, T * cols))) return st;
+  if ((st = sc.arena.alloc(&da, T * cols / 32 + 1))) return st;
+  launch_quantize(dx, (int)T, (int)cols, true, false, qa, da, af, nullptr, nullptr, sc.err, sc.stream);
+  DevAct a{dx, qa, da, af, nullptr, nullptr};
+  a.overlapped = overlapped != 0;
+  if (mode == 0) {
+    launch_gemm_tok(W0, a, (int)T, d0, nullptr, EPI_STORE, sc.err, sc.stream);
+  } else if (mode == 1) {
+    launch_gemm_pair_swiglu_q4k(W0, W1, a, (int)T, nullptr, nullptr, d0, sc.err, sc.stream);
+  } else if (!launch_gemm_cat_q4k(W0, W1, a, (int)T, d0, d1, nullptr, nullptr, EPI_STORE, sc.err,
+                                  sc.stream)) {
+    return DTL_ERR_SHAPE;
+  }
+  HIP_TRY(hipMemcpyAsync(out0, d0, T * rows0 * 4, hipMemcpyDeviceToHost, sc.stream));
+  if (mode == 2) HIP_TRY(hipMemcpyAsync(out1, d1, T * rows1 * 4, hipMemcpyDeviceToHost, sc.stream));
   int bits = 0;
   if ((st = sc.finish(&bits))) return st;
   return bits ? DTL_ERR_NON_FINITE : DTL_OK;

@@ -426,6 +426,17 @@ int dtl_kernel_rmsnorm(const float *x, const float *w, float eps, size_t rows, s
  * (det-model lib.rs:445-490) computes each token's row dots. */
 int dtl_kernel_gemv(int ggml_type, const uint8_t *weights, size_t rows, size_t cols,
                     const float *x, size_t T, float *out);
+/* No counterpart in the reference: test support for the Q4_K chunk GEMMs of
+ * the encode, every output a dot_q4_k_q8a chain (det-quant lib.rs:281-315)
+ * of the Q8A form of x ([T][cols] f32, quantised first as the forward does).
+ * mode 0: out0[T][rows0] = W0 x; mode 1: W0 gate and W1 up of the same shape,
+ * out0[T][rows0] = silu(W0 x) * (W1 x) (det-model lib.rs:2420-2434); mode 2:
+ * W0 and W1 (wq, wk) in one launch, out0[T][rows0] and out1[T][rows1].
+ * overlapped != 0 runs the kernels the pipelined encode runs with other
+ * chunks in flight, 0 those of a launch alone.  Needs T >= 16 and cols a
+ * multiple of 256 (DTL_ERR_SHAPE otherwise). */
+int dtl_kernel_q4k_chunk(int mode, int overlapped, const uint8_t *w0, size_t rows0, const uint8_t *w1,
+                         size_t rows1, size_t cols, const float *x, size_t T, float *out0, float *out1);
 /* RopeTables::llama (det-model lib.rs:813-847) computed on the device. */
 int dtl_kernel_rope_table(float rope_freq_base, size_t rope_dim, size_t positions, float *cos_out,
                           float *sin_out);

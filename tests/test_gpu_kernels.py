@@ -228,6 +228,54 @@ def test_gemv_bitexact_against_oracle(ggml_type, rows, cols, T):
         assert np.array_equal(out[t].view(np.uint32), want.view(np.uint32)), (t,)
 
 
+# (mode, overlapped, rows0, rows1, cols, T): the Q4_K chunk GEMMs of the
+# encode.  mode 0 one matrix, 1 gate + up + SwiGLU, 2 two matrices (wq + wk)
+# in one launch; overlapped 1 runs the products on the matrix cores
+# (k_q4k_mfp), 0 a launch alone (k_q4k_f32m for modes 0 and 2).  Partial row
+# tiles (16 per wave, 8 of each matrix for gate + up), partial position
+# tiles, a wq + wk boundary inside a tile, one to 22 superblocks per row.
+Q4K_CHUNK_CASES = [
+    (0, 1, 17, 0, 256, 16), (0, 1, 130, 0, 1024, 33), (0, 1, 48, 0, 5632, 64), (0, 1, 1, 0, 512, 70),
+    (0, 0, 37, 0, 512, 20),
+    (1, 1, 13, 0, 256, 16), (1, 1, 40, 0, 2048, 64), (1, 1, 9, 0, 768, 37), (1, 0, 21, 0, 512, 17),
+    (2, 1, 40, 8, 512, 16), (2, 1, 64, 16, 2048, 64), (2, 1, 23, 5, 256, 33), (2, 0, 30, 9, 512, 19),
+]
+
+
+@pytest.mark.parametrize("mode,overlapped,rows0,rows1,cols,T", Q4K_CHUNK_CASES)
+def test_q4k_chunk_gemm_bitexact_against_oracle(mode, overlapped, rows0, rows1, cols, T):
+    L = _lib()
+    rng = np.random.default_rng(mode * 100 + rows0 + cols + T)
+    if mode == 1:
+        rows1 = rows0
+    w0 = qblocks.random_row(rng, 12, rows0, cols)
+    w1 = qblocks.random_row(rng, 12, rows1, cols) if mode else bytes(1)
+    x = rng.normal(0, 3, (T, cols)).astype(np.float32)
+    out0 = np.empty((T, rows0), np.float32)
+    out1 = np.empty((T, max(rows1, 1)), np.float32)
+    b0 = np.frombuffer(w0, np.uint8).copy()
+    b1 = np.frombuffer(w1, np.uint8).copy()
+    L.check(L.lib.dtl_kernel_q4k_chunk(mode, overlapped, _p(b0, C.c_uint8), rows0, _p(b1, C.c_uint8),
+                                       rows1, cols, _p(x, C.c_float), T, _p(out0, C.c_float),
+                                       _p(out1, C.c_float)), "q4k chunk")
+    rb = qblocks.ROW_BYTES[12](cols)
+    silu = detref.lib().ref_silu_f32
+    for t in range(T):
+        d0 = np.array([detref.dot_row(12, w0[r * rb:(r + 1) * rb], cols, x[t]) for r in range(rows0)],
+                      np.float32)
+        if mode == 1:
+            d1 = np.array([detref.dot_row(12, w1[r * rb:(r + 1) * rb], cols, x[t]) for r in range(rows1)],
+                          np.float32)
+            want = np.array([silu(float(g)) for g in d0], np.float32) * d1
+            assert np.array_equal(out0[t].view(np.uint32), want.view(np.uint32)), (t,)
+            continue
+        assert np.array_equal(out0[t].view(np.uint32), d0.view(np.uint32)), (t,)
+        if mode == 2:
+            d1 = np.array([detref.dot_row(12, w1[r * rb:(r + 1) * rb], cols, x[t]) for r in range(rows1)],
+                          np.float32)
+            assert np.array_equal(out1[t, :rows1].view(np.uint32), d1.view(np.uint32)), (t,)
+
+
 @pytest.mark.parametrize("theta,rope_dim", [(1e4, 64), (1e5, 64), (1e6, 64), (1e4, 16)])
 def test_rope_table_bitexact(theta, rope_dim):
     L = _lib()
