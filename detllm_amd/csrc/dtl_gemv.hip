@@ -989,6 +989,11 @@ constexpr int kPcThreads = 512;    // eight waves
 constexpr int kPcChainWaves = 3;   // waves 0-2 run the chains
 constexpr int kPcProducers = kPcThreads - 64 * kPcChainWaves;  // waves 3-7 form the products
 constexpr int kPcMaxUnits = 2;     // 16-byte quant units per producer thread and stage
+// With PT threads per workgroup (512, or 1024 for the gate+up pair): the
+// producer lanes, and the units each forms per stage (one at 1024: 832
+// lanes cover every stage the plan allows).
+__host__ __device__ constexpr int pc_producers(int PT) { return PT - 64 * kPcChainWaves; }
+__host__ __device__ constexpr int pc_max_units(int PT) { return PT > 512 ? 1 : kPcMaxUnits; }
 
 // Chains per chain wave: a DPP row of 16 lanes per chain (CR = 16) while
 // they fit, else a quad of 4 (CR = 4).
@@ -1003,15 +1008,19 @@ __host__ __device__ constexpr int q4k_pc_chains(int CR) { return kPcChainWaves *
 __host__ __device__ constexpr int q4k_pc_skew(int c) { return c + ((c >> 6) << 2); }
 __host__ __device__ constexpr int q4k_pc_ldp(int SL) { return q4k_pc_skew(SL) + 4; }
 
-__host__ __device__ inline size_t q4k_pc_smem(int T, int cols, int NR, int SL, bool prologue, bool v6) {
+__host__ __device__ inline size_t q4k_pc_smem(int T, int cols, int NR, int SL, bool prologue, bool v6,
+                                              int pt = kPcThreads) {
+  const int pw = pt / 64 - kPcChainWaves;  // producer waves
   size_t f = (size_t)T * q4k_pc_skew(cols) + (size_t)2 * NR * T * q4k_pc_ldp(SL);
   if (prologue || v6) f += q4k_pc_prologue_floats(cols);
-  if (v6) f += (size_t)T * cols / 4 + (size_t)T * (cols / 256) + 7 * 64 + 7 * 8;
+  if (v6) f += (size_t)T * cols / 4 + (size_t)T * (cols / 256) + (size_t)pw * 64 + (size_t)pw * 8;
   return f * sizeof(float);
 }
 
-template <int SL, int NS, int MODE, int CR>
-__global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB) {
+template <int SL, int NS, int MODE, int CR, int PT = kPcThreads>
+__global__ void __launch_bounds__(PT) k_gemv_q4k_pc(Q4kPcArgs p, int RB) {
+  constexpr int kPcProducers = pc_producers(PT);  // this launch's producer lanes
+  constexpr int kPcMaxUnits = pc_max_units(PT);
   constexpr int NM = MODE == PC_PAIR ? 2 : 1;
   // fused Q6_K rows: wq+wk launches with 512-column stages only (the
   // 128-column variants have no registers to spare for them)
@@ -1030,8 +1039,9 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
   float* v6area = prod + (size_t)2 * NR * T * LDP + q4k_pc_prologue_floats(cols);
   int8_t* v6q = reinterpret_cast<int8_t*>(v6area);
   float* v6dk = v6area + (size_t)T * cols / 4;
-  int* v6aux = reinterpret_cast<int*>(v6dk + (size_t)T * (cols / 256));  // [7][8][8]
-  float* v6ds = reinterpret_cast<float*>(v6aux + 7 * 64);                 // [7][8]
+  // [producer waves][8][8], then [producer waves][8]
+  int* v6aux = reinterpret_cast<int*>(v6dk + (size_t)T * (cols / 256));
+  float* v6ds = reinterpret_cast<float*>(v6aux + (PT / 64 - kPcChainWaves) * 64);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool producer = wave >= kPcChainWaves;
@@ -1065,7 +1075,10 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
   uint4 v6a{}, v6b{}, v6c{}, v6e{};
   uint32_t v6sc = 0;
   uint16_t v6dw = 0;
-  if (V6 && p.v6w && producer) {
+  // (at 1024 threads there are no registers to hold them through the
+  // stages: they are loaded where they are used)
+  constexpr bool kV6Early = PT <= 512;
+  auto v6_loads = [&]() {
     int r6 = blockIdx.x + (wave - kPcChainWaves) * gridDim.x;
     r6 = r6 < p.v6rows ? r6 : 0;
     const int sb = lane >> 3, h = (lane >> 2) & 1, pp = lane & 3;
@@ -1077,7 +1090,8 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
     v6e = reinterpret_cast<const uint4*>(body + 32 + 8 * h)[1];
     v6sc = body[48 + 2 * h + (pp >> 1)];
     v6dw = p.v6d[(size_t)r6 * p.v6nb + sbl];
-  }
+  };
+  if (V6 && kV6Early && p.v6w && producer) v6_loads();
   // the producers' weights: the first NS stages are in flight before the
   // activations load
   // Units past the first round of kPcProducers: when there are at most half
@@ -1111,14 +1125,16 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
   // The input row's first loads, then the first NS stages' weights (younger,
   // so the prologue's wait for the row does not wait for them).
   const FusedIn in{p.x, p.norm_w, p.eps};
-  RowLoads<kPcThreads / 64> pre;
-  if (!p.af) q8a_row_loads<kPcThreads / 64>(in, 0, cols, p.norm_w != nullptr, pre);
+  // (at 1024 threads the registers for holding them are not there)
+  constexpr bool kPre = PT <= 512;
+  RowLoads<PT / 64> pre;
+  if (kPre && !p.af) q8a_row_loads<PT / 64>(in, 0, cols, p.norm_w != nullptr, pre);
   if (producer) {
 #pragma unroll
     for (int u = 0; u < NS; u++) DTL_PC_LOAD(u, u);
   }
   if (p.af) {
-    for (int i = tid; i < T * cols / 4; i += kPcThreads) {
+    for (int i = tid; i < T * cols / 4; i += PT) {
       const int t = 4 * i / cols, e = 4 * i - t * cols;
       *reinterpret_cast<float4*>(as + (size_t)t * ACS + q4k_pc_skew(e)) =
           reinterpret_cast<const float4*>(p.af)[i];
@@ -1139,8 +1155,8 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
       int8_t* kq = p.v6w ? v6q : (side ? p.side_qk : nullptr);
       float* kd = p.v6w ? v6dk : (side ? p.side_dk : nullptr);
       // the Q8A values d q straight into the activation rows
-      bad |= q8a_prologue<kPcThreads / 64, true>(in, t, cols, p.norm_w != nullptr, xs, ws, sq, cs,
-                                                 nullptr, nullptr, misc, kq, kd, t == 0, pre,
+      bad |= q8a_prologue<PT / 64, true>(in, t, cols, p.norm_w != nullptr, xs, ws, sq, cs,
+                                                 nullptr, nullptr, misc, kq, kd, kPre && t == 0, pre,
                                                  as + (size_t)t * ACS);
     }
     if (bad && tid == 0) flag(p.err, ERRBIT_NON_FINITE);
@@ -1293,6 +1309,7 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
   }
 #undef DTL_PC_LOAD
   if (V6 && p.v6w) {
+    if (!kV6Early) v6_loads();
     const int r6 = blockIdx.x + (wave - kPcChainWaves) * gridDim.x;
     if (r6 < p.v6rows) {
       // dot_q6_k_q8k (det-quant lib.rs:353-397): lane = (superblock sb,
@@ -1376,7 +1393,7 @@ __global__ void __launch_bounds__(kPcThreads) k_gemv_q4k_pc(Q4kPcArgs p, int RB)
 // (twelve as DPP rows, 48 as quads) and the stage's weights kPcMaxUnits
 // 16-byte quant units per producer thread.
 bool q4k_pc_plan(int mode, int rows_total, int cols, int T, bool prologue, bool v6, int* RB,
-                 int* SL, int* CR, size_t* smem) {
+                 int* SL, int* CR, size_t* smem, int pt = kPcThreads) {
   if (cols % 256 != 0 || T < 1) return false;
   static const int cus = [] {
     int dev = 0, n = 0;
@@ -1395,14 +1412,15 @@ bool q4k_pc_plan(int mode, int rows_total, int cols, int T, bool prologue, bool 
   // the longest stage (fewest barriers and ring refills) whose weights and
   // products fit
   int sl = 512;
-  while (sl > 128 && (NR * (sl / 32) > kPcMaxUnits * kPcProducers ||
-                      q4k_pc_smem(T, cols, NR, sl, prologue, v6) > 150 * 1024 || cols % sl != 0))
+  const int units = pc_max_units(pt) * pc_producers(pt);
+  while (sl > 128 && (NR * (sl / 32) > units ||
+                      q4k_pc_smem(T, cols, NR, sl, prologue, v6, pt) > 150 * 1024 || cols % sl != 0))
     sl /= 2;
-  if (NR * (sl / 32) > kPcMaxUnits * kPcProducers || cols % sl != 0) return false;
+  if (NR * (sl / 32) > units || cols % sl != 0) return false;
   if (v6 && (mode != PC_CAT || sl != 512)) return false;  // where the kernel has the fused rows
   *RB = rb;
   *SL = sl;
-  *smem = q4k_pc_smem(T, cols, NR, sl, prologue, v6);
+  *smem = q4k_pc_smem(T, cols, NR, sl, prologue, v6, pt);
   return *smem <= 150 * 1024;
 }
 
@@ -1411,28 +1429,47 @@ bool launch_q4k_pc(const Q4kPcArgs& a, hipStream_t s) {
   const int rows_total = MODE == PC_CAT ? a.rows0 + a.rows1 : a.rows0;
   int RB, SL, CR;
   size_t smem;
-  if (!q4k_pc_plan(MODE, rows_total, a.cols, a.T, a.af == nullptr, a.v6w != nullptr, &RB, &SL, &CR, &smem))
+  // Sixteen waves (thirteen producing) where the plan fits, else eight.
+  int pt = 1024;
+  if (!q4k_pc_plan(MODE, rows_total, a.cols, a.T, a.af == nullptr, a.v6w != nullptr, &RB, &SL, &CR, &smem, pt))
+    pt = kPcThreads;
+  if (!q4k_pc_plan(MODE, rows_total, a.cols, a.T, a.af == nullptr, a.v6w != nullptr, &RB, &SL, &CR, &smem, pt))
     return false;
   const dim3 grid((rows_total + RB - 1) / RB);
   // the fused Q6_K rows need the producer waves of the grid to cover them
-  if (a.v6w && (a.af || a.v6nb > 8 || (int)grid.x * (kPcThreads / 64 - kPcChainWaves) < a.v6rows))
+  if (a.v6w && (a.af || a.v6nb > 8 || (int)grid.x * (pt / 64 - kPcChainWaves) < a.v6rows))
     return false;
-#define DTL_Q4K_PC(sl, ns, cr)                                                                   \
+#define DTL_Q4K_PC(sl, ns, cr, npt)                                                               \
   do {                                                                                           \
-    static const bool attr = hipFuncSetAttribute((const void*)k_gemv_q4k_pc<sl, ns, MODE, cr>,     \
+    static const bool attr = hipFuncSetAttribute((const void*)k_gemv_q4k_pc<sl, ns, MODE, cr, npt>, \
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,      \
                                                  150 * 1024) == hipSuccess;                       \
     (void)attr;                                                                                  \
-    launch_kernel((k_gemv_q4k_pc<sl, ns, MODE, cr>), grid, dim3(kPcThreads), smem, s, a, RB);     \
+    launch_kernel((k_gemv_q4k_pc<sl, ns, MODE, cr, npt>), grid, dim3(npt), smem, s, a, RB);       \
   } while (0)
+  // At sixteen waves: two stages of weights in flight (three measured 1602
+  // against 1584 us per TinyLlama decode token with the gate+up launch
+  // alone at sixteen waves)
+  if (pt == 1024) {
+    if (CR == 16) {
+      if (SL == 512) DTL_Q4K_PC(512, 2, 16, 1024);
+      else if (SL == 256) DTL_Q4K_PC(256, 2, 16, 1024);
+      else DTL_Q4K_PC(128, 2, 16, 1024);
+    } else {
+      if (SL == 512) DTL_Q4K_PC(512, 2, 4, 1024);
+      else if (SL == 256) DTL_Q4K_PC(256, 2, 4, 1024);
+      else DTL_Q4K_PC(128, 2, 4, 1024);
+    }
+    return true;
+  }
   if (CR == 16) {
-    if (SL == 512) DTL_Q4K_PC(512, 3, 16);
-    else if (SL == 256) DTL_Q4K_PC(256, 4, 16);
-    else DTL_Q4K_PC(128, 4, 16);
+    if (SL == 512) DTL_Q4K_PC(512, 3, 16, 512);
+    else if (SL == 256) DTL_Q4K_PC(256, 4, 16, 512);
+    else DTL_Q4K_PC(128, 4, 16, 512);
   } else {
-    if (SL == 512) DTL_Q4K_PC(512, 3, 4);
-    else if (SL == 256) DTL_Q4K_PC(256, 4, 4);
-    else DTL_Q4K_PC(128, 4, 4);
+    if (SL == 512) DTL_Q4K_PC(512, 3, 4, 512);
+    else if (SL == 256) DTL_Q4K_PC(256, 4, 4, 512);
+    else DTL_Q4K_PC(128, 4, 4, 512);
   }
 #undef DTL_Q4K_PC
   return true;
