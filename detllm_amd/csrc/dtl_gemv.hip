@@ -84,6 +84,13 @@ __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
 // Block-term rows in LDS start on 16-byte boundaries (chain_sum_lds reads
 // them four at a time): row stride nb rounded up to a multiple of 4.
 __host__ __device__ inline int nb_stride(int nb) { return (nb + 3) & ~3; }
+
+// A 16-byte load marked non-temporal (streamed once, not kept in the caches).
+typedef unsigned int dtl_v4u __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_nt16(const void* p) {
+  const dtl_v4u v = __builtin_nontemporal_load(reinterpret_cast<const dtl_v4u*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -221,9 +228,16 @@ __global__ void __launch_bounds__(256) k_gemv_q8(DevMat W, const int8_t* __restr
 // loaded once per wave.  Every load is unconditional (lanes past the row's
 // chunks and groups past the end read valid addresses whose values are not
 // stored): a load under a branch makes the compiler wait for every load in
-// flight at the branch, which took the prefetch away.
+// flight at the branch, which took the prefetch away.  The weight loads are
+// non-temporal (the matrix is read once per position and is larger than the
+// last-level cache), and the rows' chains use the short ring of
+// chain_sum_lds32: with four rows per group (and the waves-per-SIMD hint,
+// without which the epilogue's registers tip it to 73) that leaves 68
+// registers and seven waves per SIMD (the 145 MB Qwen2.5 output projection: 26.7 us per
+// launch by events, against 30.5 with eight rows, the general chain and
+// cached loads).
 template <int R>
-__global__ void __launch_bounds__(256) k_gemv_q8_0_stream(DevMat W, const int8_t* __restrict__ qa,
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) k_gemv_q8_0_stream(DevMat W, const int8_t* __restrict__ qa,
                                                           const float* __restrict__ da, float* out,
                                                           const float* bias, int epi, int* err) {
   extern __shared__ __align__(16) float vb[];
@@ -255,7 +269,7 @@ __global__ void __launch_bounds__(256) k_gemv_q8_0_stream(DevMat W, const int8_t
     _Pragma("unroll") for (int r = 0; r < R; r++) {                       \
       int row = gc_ * R + r;                                              \
       row = row < rows ? row : rows - 1;                                  \
-      WV[r] = *(const uint4*)(wbase + (size_t)row * cols);                 \
+      WV[r] = load_nt16(wbase + (size_t)row * cols);                      \
       SV[r] = dbase[(size_t)row * nb];                                    \
     }                                                                     \
   } while (0)
@@ -275,7 +289,7 @@ __global__ void __launch_bounds__(256) k_gemv_q8_0_stream(DevMat W, const int8_t
     if (lane < R) {                                                                            \
       const int row = (GG) * R + lane;                                                         \
       if (row < rows) {                                                                        \
-        float v = chain_sum_lds(0.0f, mine + lane * nbs, nb);                                  \
+        float v = chain_sum_lds32(0.0f, mine + lane * nbs, nb);                                  \
         if (!epilogue(v, out, (size_t)t * rows + row, bias, row, epi)) flag(err, ERRBIT_NON_FINITE); \
       }                                                                                        \
     }                                                                                          \
@@ -456,19 +470,20 @@ void launch_q6k_decode_layout(const DevMat& W, uint4* out, hipStream_t s) {
 
 // dot_q6_k_q8k (det-quant lib.rs:353-397) over the decode layout, for tall
 // matrices (the output projection).  Lane (s, p) = (lane / 4, lane % 4) of a
-// wave owns class pair p of superblock s of each 16-superblock group the
-// wave visits (grid-stride, the next group's four words loaded as soon as a
-// group is reduced, unconditionally with the group clamped); the lane's
-// superblock column and classes are the same in every group, so its share
-// of the Q8_K activations is prepared once, in registers: for elements
-// j = 4m .. 4m + 3 of a class, the activation dword masked to its first and
-// second halves (the two scales j >> 1 = 2m, 2m + 1) and, for each half,
-// -32 times its sum.  The class sums are then exact integers from unsigned
-// quants q (0..63): dot4(q, half, -32 * sum of half) = sum (q - 32) * a, times
-// the half's scale.  Each lane forms d * aux[c] (d = w.d * a.d) for its two
-// classes; then one lane per (row, class) runs sums[c] += ... over the row's
-// superblocks in order, and one lane per row the final sum of sums[0..7], as
-// the reference does.
+// wave owns class pair p of superblock s of the wave's 16-superblock group
+// (one group per wave, every group its own wave: a resident grid walking
+// groups in a loop streamed slower here, 12.2 against 11.4 us on the
+// 32000 x 2048 TinyLlama output, since its activation operands held in
+// registers left four waves per SIMD where this kernel has eight).  The
+// group's four words are loaded non-temporally (read once per position).
+// For elements j = 4m .. 4m + 3 of a class, the activation dword is masked
+// to its first and second halves (the two scales j >> 1 = 2m, 2m + 1) and,
+// for each half, -32 times its sum is formed; the class sums are then exact
+// integers from unsigned quants q (0..63): dot4(q, half, -32 * sum of half)
+// = sum (q - 32) * a, times the half's scale.  Each lane forms d * aux[c]
+// (d = w.d * a.d) for its two classes; then one lane per (row, class) runs
+// sums[c] += ... over the row's superblocks in order, and one lane per row
+// the final sum of sums[0..7], as the reference does.
 template <int NB>
 __global__ void __launch_bounds__(256) k_gemv_q6k_cm(const uint4* __restrict__ q6d,
                                                      const uint16_t* __restrict__ d16, int rows,
@@ -482,103 +497,75 @@ __global__ void __launch_bounds__(256) k_gemv_q6k_cm(const uint4* __restrict__ q
   const int t = blockIdx.y;
   const int s = lane >> 2, p = lane & 3, sb = s % NB;
   const int ngroups = (rows + RPG - 1) / RPG;
-  const int stride = gridDim.x * 4;
-  int g = blockIdx.x * 4 + wave;
+  const int g = blockIdx.x * 4 + wave;
   if (g >= ngroups) return;
-  // activation-side operands of classes 2p, 2p + 1 of superblock column sb
-  uint32_t ah[2][2][8], ak[2][2][8];
+  const uint4* gp = q6d + (size_t)g * kQ6dGroupWords;
+  const uint4 l0 = load_nt16(gp + lane), l1 = load_nt16(gp + 64 + lane), hw = load_nt16(gp + 128 + lane),
+              sw = load_nt16(gp + 192 + s);
+  int row = g * RPG + s / NB;
+  row = row < rows ? row : rows - 1;
+  const uint16_t dw = d16[(size_t)row * NB + sb];
+  // the Q8_K activations of classes 2p, 2p + 1 of superblock column sb
+  uint4 av[4];
   {
     const uint4* ap = (const uint4*)(qk + (size_t)t * NB * 256 + (size_t)sb * 256 + p * 64);
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const uint4 v = ap[k];
-      const uint32_t a4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int ci = k >> 1, m = 4 * (k & 1) + i;
-        ah[ci][0][m] = a4[i] & 0x0000ffffu;
-        ah[ci][1][m] = a4[i] & 0xffff0000u;
-        ak[ci][0][m] = (uint32_t)dot4(0xe0e0e0e0u, ah[ci][0][m], 0);
-        ak[ci][1][m] = (uint32_t)dot4(0xe0e0e0e0u, ah[ci][1][m], 0);
-      }
-    }
+    for (int k = 0; k < 4; k++) av[k] = ap[k];
   }
-  const float da = dk[(size_t)t * NB + sb];
+  const float d = f16_to_f32(dw) * dk[(size_t)t * NB + sb];
   float(*mine)[9] = terms[wave];
-  for (;;) {
-    const uint4* gp = q6d + (size_t)g * kQ6dGroupWords;
-    const uint4 l0 = gp[lane], l1 = gp[64 + lane], hw = gp[128 + lane], sw = gp[192 + s];
-    int row = g * RPG + s / NB;
-    row = row < rows ? row : rows - 1;
-    const float d = f16_to_f32(d16[(size_t)row * NB + sb]) * da;
-    const uint32_t scw[4] = {sw.x, sw.y, sw.z, sw.w};
+  const uint32_t scw[4] = {sw.x, sw.y, sw.z, sw.w};
 #pragma unroll
-    for (int ci = 0; ci < 2; ci++) {
-      const uint4 lw4 = ci ? l1 : l0;
-      const uint32_t L[4] = {lw4.x, lw4.y, lw4.z, lw4.w};
-      const uint32_t H[2] = {ci ? hw.z : hw.x, ci ? hw.w : hw.y};
-      int acc = 0;
+  for (int ci = 0; ci < 2; ci++) {
+    const uint4 lw4 = ci ? l1 : l0;
+    const uint32_t L[4] = {lw4.x, lw4.y, lw4.z, lw4.w};
+    const uint32_t H[2] = {ci ? hw.z : hw.x, ci ? hw.w : hw.y};
+    const uint32_t A[8] = {av[2 * ci].x,     av[2 * ci].y,     av[2 * ci].z,     av[2 * ci].w,
+                           av[2 * ci + 1].x, av[2 * ci + 1].y, av[2 * ci + 1].z, av[2 * ci + 1].w};
+    int acc = 0;
 #pragma unroll
-      for (int m = 0; m < 8; m++) {
-        const uint32_t lw = (m & 1) ? L[m >> 1] >> 4 : L[m >> 1];
-        const uint32_t h = H[m >> 2];
-        const uint32_t hs = (m & 3) == 0 ? h << 4 : (m & 3) == 1 ? h << 2 : (m & 3) == 2 ? h : h >> 2;
-        const uint32_t q = (hs & 0x30303030u) | (lw & 0x0f0f0f0fu);
-        const int c0 = dot4(q, ah[ci][0][m], (int)ak[ci][0][m]);
-        const int c1 = dot4(q, ah[ci][1][m], (int)ak[ci][1][m]);
-        const int s0 = (int)(int8_t)((scw[m >> 1] >> (16 * (m & 1))) & 0xffu);
-        const int s1 = (int)(int8_t)((scw[m >> 1] >> (16 * (m & 1) + 8)) & 0xffu);
-        acc += __mul24(s0, c0) + __mul24(s1, c1);
-      }
-      mine[s][2 * p + ci] = d * (float)acc;
+    for (int m = 0; m < 8; m++) {
+      const uint32_t lw = (m & 1) ? L[m >> 1] >> 4 : L[m >> 1];
+      const uint32_t h = H[m >> 2];
+      const uint32_t hs = (m & 3) == 0 ? h << 4 : (m & 3) == 1 ? h << 2 : (m & 3) == 2 ? h : h >> 2;
+      const uint32_t q = (hs & 0x30303030u) | (lw & 0x0f0f0f0fu);
+      const uint32_t a0 = A[m] & 0x0000ffffu, a1 = A[m] & 0xffff0000u;
+      const int c0 = dot4(q, a0, dot4(0xe0e0e0e0u, a0, 0));
+      const int c1 = dot4(q, a1, dot4(0xe0e0e0e0u, a1, 0));
+      const int s0 = (int)(int8_t)((scw[m >> 1] >> (16 * (m & 1))) & 0xffu);
+      const int s1 = (int)(int8_t)((scw[m >> 1] >> (16 * (m & 1) + 8)) & 0xffu);
+      acc += __mul24(s0, c0) + __mul24(s1, c1);
     }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    const int g0 = g;
-    g += stride;
-    const bool more = g < ngroups;
-    for (int rc = lane; rc < 8 * RPG; rc += 64) {  // (row, class) pairs: 128 when NB = 1
-      const int rl = rc >> 3, c = rc & 7;
-      float sm = 0.0f;
+    mine[s][2 * p + ci] = d * (float)acc;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  for (int rc = lane; rc < 8 * RPG; rc += 64) {  // (row, class) pairs: 128 when NB = 1
+    const int rl = rc >> 3, c = rc & 7;
+    float sm = 0.0f;
 #pragma unroll
-      for (int b = 0; b < NB; b++) sm += mine[rl * NB + b][c];
-      sums_s[wave][rl][c] = sm;
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    if (lane < RPG) {
-      const int r = g0 * RPG + lane;
-      if (r < rows) {
-        float v = 0.0f;
+    for (int b = 0; b < NB; b++) sm += mine[rl * NB + b][c];
+    sums_s[wave][rl][c] = sm;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  if (lane < RPG) {
+    const int r = g * RPG + lane;
+    if (r < rows) {
+      float v = 0.0f;
 #pragma unroll
-        for (int c = 0; c < 8; c++) v += sums_s[wave][lane][c];
-        if (!epilogue(v, out, (size_t)t * rows + r, bias, r, epi)) flag(err, ERRBIT_NON_FINITE);
-      }
+      for (int c = 0; c < 8; c++) v += sums_s[wave][lane][c];
+      if (!epilogue(v, out, (size_t)t * rows + r, bias, r, epi)) flag(err, ERRBIT_NON_FINITE);
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    if (!more) break;
   }
 }
 
 template <int NB>
 void launch_q6k_cm_nb(const DevMat& W, const DevAct& A, int T, float* out, const float* bias, int epi,
                       int* err, hipStream_t s) {
-  // as many workgroups as stay resident, each wave walking groups grid-stride
-  static const int resident = [] {
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemv_q6k_cm<NB>, 256, 0) != hipSuccess ||
-        cus <= 0 || per_cu <= 0)
-      return 256;
-    return cus * per_cu;
-  }();
   const int ngroups = (W.rows + 16 / NB - 1) / (16 / NB);
-  int wgs = (ngroups + 3) / 4;
-  if (wgs > resident) wgs = resident;
-  launch_kernel(k_gemv_q6k_cm<NB>, dim3(wgs, T), dim3(256), 0, s, W.q6d, W.d16, W.rows, A.qk, A.dk, out, bias,
-                epi, err);
+  launch_kernel(k_gemv_q6k_cm<NB>, dim3((ngroups + 3) / 4, T), dim3(256), 0, s, W.q6d, W.d16, W.rows, A.qk,
+                A.dk, out, bias, epi, err);
 }
 
 void launch_q6k_cm(const DevMat& W, const DevAct& A, int T, float* out, const float* bias, int epi, int* err,
@@ -1689,7 +1676,7 @@ bool launch_gemv(const DevMat& W, const DevAct& A, int T, float* out, const floa
     // Tall, narrow Q8_0 (the output projection): streaming waves, as many
     // workgroups as stay resident at once (a second round of workgroups
     // would start only when the first ones end, doubling the launch).
-    constexpr int R = 8;
+    constexpr int R = 4;
     const int ngroups = (W.rows + R - 1) / R;
     size_t smem = (size_t)4 * R * nb_stride(W.nb) * sizeof(float);
     static const int resident = [] {

@@ -178,6 +178,30 @@ __device__ __forceinline__ float chain_sum_lds(float a, const float* v, int n) {
   return a;
 }
 
+// chain_sum_lds for n <= 32 (at most eight float4): the same adds in the
+// same order from a ring of four reads, sixteen registers where the general
+// ring holds forty-eight (which a streaming kernel spends on loads in flight).
+__device__ __forceinline__ float chain_sum_lds32(float a, const float* v, int n) {
+  const float4* v4 = reinterpret_cast<const float4*>(v);
+  const int n4 = n >> 2;
+  float4 r[4];
+#pragma unroll
+  for (int q = 0; q < 4; q++) r[q] = v4[q < n4 ? q : 0];
+#pragma unroll
+  for (int q = 0; q < 8; q++) {
+    if (q < n4) {
+      const float4 w = r[q & 3];
+      if (q + 4 < 8) r[q & 3] = v4[q + 4 < n4 ? q + 4 : 0];
+      a += w.x;
+      a += w.y;
+      a += w.z;
+      a += w.w;
+    }
+  }
+  for (int i = 4 * n4; i < n; i++) a += v[i];
+  return a;
+}
+
 // Lane exchanges by DPP (a VALU operand modifier, no LDS round trip), for
 // reductions whose combine is commutative and associative or exact: after
 // the two quad steps every quad holds its result, the half-row mirror (lane

@@ -186,6 +186,10 @@ GEMV_CASES = [
     (0, 37, 64, 3), (0, 20, 128, 1),
     (8, 61, 576, 1), (8, 33, 896, 5), (8, 9, 4864, 2), (8, 5000, 64, 1), (8, 17000, 64, 2),
     (8, 66000, 32, 1), (8, 300, 8192, 1), (8, 20, 576, 12),
+    # the streaming Q8_0 kernel (tall, at most 32 blocks per row): the Qwen2.5
+    # output width (28 blocks), the 32-block maximum, and 3 blocks (a chain
+    # shorter than one float4 read)
+    (8, 20001, 896, 1), (8, 16390, 1024, 2), (8, 16400, 96, 3),
     (2, 40, 64, 2), (2, 17, 512, 1), (2, 66000, 64, 1), (2, 5000, 96, 3),
     (12, 45, 2048, 1), (12, 7, 5632, 3), (12, 30, 512, 64), (12, 9000, 256, 1), (12, 13, 256, 8),
     (12, 45, 256, 37), (12, 100, 768, 20),
