@@ -173,7 +173,7 @@ __global__ void __launch_bounds__(256) k_gemv_q8(DevMat W, const int8_t* __restr
         isum = dot4(P.w4[r].y, P.a0.y, isum);
         isum = dot4(P.w4[r].z, P.a0.z, isum);
         isum = dot4(P.w4[r].w, P.a0.w, isum);
-        isum += __shfl_xor(isum, 1);
+        isum += dpp_i32<kDppXor1>(isum);
       } else {
         const uint32_t m = 0x0f0f0f0fu;
         isum = dot4(P.w4[r].x & m, P.a0.x, isum);
@@ -281,7 +281,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) k
       isum = dot4(WV[r].y, a0.y, isum);                                                         \
       isum = dot4(WV[r].z, a0.z, isum);                                                         \
       isum = dot4(WV[r].w, a0.w, isum);                                                         \
-      isum += __shfl_xor(isum, 1);                                                             \
+      isum += dpp_i32<kDppXor1>(isum); /* lane c^1's half block, by DPP */                     \
       if (cv && !(c & 1)) mine[r * nbs + b] = (f16_to_f32((uint16_t)SV[r]) * dact) * (float)isum;        \
     }                                                                                          \
     __builtin_amdgcn_wave_barrier();                                                           \
@@ -636,9 +636,10 @@ __global__ void __launch_bounds__(256) k_gemv_q6k_split(DevMat W, const int8_t* 
   }
 #pragma unroll
   for (int k = 0; k < 8; k++) {
-    aux[k] += __shfl_xor(aux[k], 1);
-    aux[k] += __shfl_xor(aux[k], 2);
-    aux[k] += __shfl_xor(aux[k], 4);
+    // the eight lanes of the superblock, by DPP: quads, then the other quad
+    aux[k] += dpp_i32<kDppXor1>(aux[k]);
+    aux[k] += dpp_i32<kDppXor2>(aux[k]);
+    aux[k] += dpp_i32<kDppMirror8>(aux[k]);
   }
   if ((lane & 7) == 0 && sb < nsb) {
 #pragma unroll
@@ -1340,9 +1341,9 @@ __global__ void __launch_bounds__(PT) k_gemv_q4k_pc(Q4kPcArgs p, int RB) {
         }
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-          aux[k] += __shfl_xor(aux[k], 1);
-          aux[k] += __shfl_xor(aux[k], 2);
-          aux[k] += __shfl_xor(aux[k], 4);
+          aux[k] += dpp_i32<kDppXor1>(aux[k]);
+          aux[k] += dpp_i32<kDppXor2>(aux[k]);
+          aux[k] += dpp_i32<kDppMirror8>(aux[k]);
         }
         if ((lane & 7) == 0 && sb < nsb) {
 #pragma unroll
@@ -1593,7 +1594,7 @@ __global__ void __launch_bounds__(64 * NW) k_gemv_q8f(FusedMats M, FusedIn in, i
           isum = dot4(w4[ii][r].y, a0.y, isum);
           isum = dot4(w4[ii][r].z, a0.z, isum);
           isum = dot4(w4[ii][r].w, a0.w, isum);
-          isum += __shfl_xor(isum, 1);
+          isum += dpp_i32<kDppXor1>(isum);
         } else {
           const uint32_t m = 0x0f0f0f0fu;
           isum = dot4(w4[ii][r].x & m, a0.x, isum);
