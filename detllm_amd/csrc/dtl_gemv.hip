@@ -91,6 +91,19 @@ __device__ __forceinline__ uint4 load_nt16(const void* p) {
   const dtl_v4u v = __builtin_nontemporal_load(reinterpret_cast<const dtl_v4u*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+
+// Byte B of x as f32 (exact), one v_cvt_f32_ubyteB: written out because the
+// compiler turns (x >> 8 B) & 0xff of a nibble-masked dword into a bit-field
+// extract and a conversion of byte 0.
+template <int B>
+__device__ __forceinline__ float ubyte_f32(uint32_t x) {
+  float f;
+  if (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(x));
+  else if (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(x));
+  else if (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(x));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(x));
+  return f;
+}
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -1090,13 +1103,22 @@ __global__ void __launch_bounds__(PT) k_gemv_q4k_pc(Q4kPcArgs p, int RB) {
   const bool halves = E > 0 && 2 * E <= kPcProducers;
   const int f2 = halves ? (ptid < 2 * E ? kPcProducers + (ptid >> 1) : WPU) : ptid + kPcProducers;
   const int hi2 = ptid & 1;
+  // Gate+up with one unit per lane (1024 threads) and at most half as many
+  // units as producer lanes: every unit goes to two lanes as halves (lane
+  // 2 f + h: sub-block h of unit f's two).  There the chains waited on the
+  // producers (384 units for 832 lanes): stages of 2.5-2.9k cycles became
+  // 2.3-2.6k and the launch 16.3 -> 15.8 us; the other launches, whose
+  // chains set the pace, gained nothing and keep whole units.
+  const bool split = MODE == PC_PAIR && kPcMaxUnits == 1 && 2 * WPU <= kPcProducers;
+  const int f0 = split ? ptid >> 1 : ptid;
+  const int hi0 = ptid & 1;
   int m0, m1;
-  const int r0 = row_of(ptid, &m0), r1 = row_of(f2, &m1);
+  const int r0 = row_of(f0, &m0), r1 = row_of(f2, &m1);
   const uint8_t* qr0 = (m0 ? p.q1 : p.q0) + (size_t)r0 * nb * 128;
   const uint8_t* hr0 = (m0 ? p.h1 : p.h0) + (size_t)r0 * nb * 16;
   const uint8_t* qr1 = (m1 ? p.q1 : p.q0) + (size_t)r1 * nb * 128;
   const uint8_t* hr1 = (m1 ? p.h1 : p.h0) + (size_t)r1 * nb * 16;
-  const int u0 = ptid < WPU ? ptid % UPR : 0;
+  const int u0 = f0 < WPU ? f0 % UPR : 0;
   const int u1 = f2 < WPU ? f2 % UPR : 0;
   uint4 qa0[NS], ha0[NS], qa1[NS], ha1[NS];
 #define DTL_PC_LOAD(slot, k)                                                                \
@@ -1167,11 +1189,18 @@ __global__ void __launch_bounds__(PT) k_gemv_q4k_pc(Q4kPcArgs p, int RB) {
     const float dsc1 = d * (float)sc1, dm1 = dmin * (float)mn1;
     const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
     float wl[16], wh[16];
+    // the nibbles of a dword masked at once, each byte then converted by
+    // v_cvt_f32_ubyte0-3 (no per-element extraction)
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const uint32_t byte = (qw[i >> 2] >> (8 * (i & 3))) & 0xffu;
-      wl[i] = dsc0 * (float)(byte & 0x0fu) - dm0;
-      wh[i] = dsc1 * (float)(byte >> 4) - dm1;
+    for (int j = 0; j < 4; j++) {
+      const uint32_t lo = qw[j] & 0x0f0f0f0fu, hi = (qw[j] >> 4) & 0x0f0f0f0fu;
+      const float fl[4] = {ubyte_f32<0>(lo), ubyte_f32<1>(lo), ubyte_f32<2>(lo), ubyte_f32<3>(lo)};
+      const float fh[4] = {ubyte_f32<0>(hi), ubyte_f32<1>(hi), ubyte_f32<2>(hi), ubyte_f32<3>(hi)};
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        wl[4 * j + b] = dsc0 * fl[b] - dm0;
+        wh[4 * j + b] = dsc1 * fh[b] - dm1;
+      }
     }
     // columns c and c + 32 lie in one 64-column group, k SL is a multiple of 64
     const int cs = q4k_pc_skew(c);
@@ -1211,9 +1240,11 @@ __global__ void __launch_bounds__(PT) k_gemv_q4k_pc(Q4kPcArgs p, int RB) {
     const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
     float w[16];
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const uint32_t byte = (qw[i >> 2] >> (8 * (i & 3))) & 0xffu;
-      w[i] = dsc * (float)((byte >> (4 * hi)) & 0x0fu) - dm;
+    for (int j = 0; j < 4; j++) {
+      const uint32_t nib = (qw[j] >> (4 * hi)) & 0x0f0f0f0fu;
+      const float f[4] = {ubyte_f32<0>(nib), ubyte_f32<1>(nib), ubyte_f32<2>(nib), ubyte_f32<3>(nib)};
+#pragma unroll
+      for (int b = 0; b < 4; b++) w[4 * j + b] = dsc * f[b] - dm;
     }
     // c + 32 lies in the 64-column group of c
     const int cs = q4k_pc_skew(c) + 32 * hi;
@@ -1239,7 +1270,10 @@ __global__ void __launch_bounds__(PT) k_gemv_q4k_pc(Q4kPcArgs p, int RB) {
         const int k = base + u;  // stages past the end form unused products
         float* pb = prod + (size_t)(k & 1) * NR * T * LDP;
         const int kk = k < nst ? k : nst - 1;
-        products(pb, kk, ptid, qa0[u], ha0[u]);
+        if (split)
+          products_half(pb, kk, f0, hi0, qa0[u], ha0[u]);
+        else
+          products(pb, kk, ptid, qa0[u], ha0[u]);
         if (kPcMaxUnits > 1) {
           if (halves)
             products_half(pb, kk, f2, hi2, qa1[u], ha1[u]);
