@@ -299,6 +299,31 @@ __device__ __forceinline__ float chain_group_lds(float a, const float* v, int n)
   // slot into one read at the top of the loop, next to the adds that wait
   // for it.
   const int nfull = n / B;
+  if constexpr (R == 4) {
+    // Quads: a read feeds only sixteen adds (about 80 cycles), less than an
+    // LDS read takes while producer waves load the LDS, so six reads are in
+    // flight (slot i holds group b + i).
+    constexpr int A = 6;
+    float4 x[A];
+#pragma unroll
+    for (int i = 0; i < A; i++) x[i] = load(i);
+    __builtin_amdgcn_sched_barrier(0);
+    int b = 0;
+    for (; b + A <= nfull; b += A) {
+#pragma unroll
+      for (int i = 0; i < A; i++) {
+        a = chain_group_add<R>(a, x[i]);
+        x[i] = load(b + A + i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < A; i++) {
+      if (b + i < nfull) a = chain_group_add<R>(a, x[i]);
+      else if (b + i < nb) a = chain_group_add<R>(a, live(x[i], b + i));
+    }
+    return a;
+  }
   float4 x0 = load(0), x1 = load(1);
   __builtin_amdgcn_sched_barrier(0);
   int b = 0;
