@@ -220,6 +220,8 @@ constexpr int kDppXor1 = 0xb1;      // quad_perm:[1,0,3,2]
 constexpr int kDppXor2 = 0x4e;      // quad_perm:[2,3,0,1]
 constexpr int kDppMirror8 = 0x141;  // row_half_mirror
 constexpr int kDppMirror16 = 0x140; // row_mirror
+constexpr int kDppRowBcast15 = 0x142;  // row_bcast:15 (lane 15 of each row to the next row)
+constexpr int kDppRowBcast31 = 0x143;  // row_bcast:31 (lane 31 to rows 2 and 3)
 
 // Serial chains whose terms reach the adding lane by DPP broadcast.  A wave
 // issues an LDS read in about 14 cycles and a dependent add in about 4.6, so

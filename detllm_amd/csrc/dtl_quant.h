@@ -57,18 +57,17 @@ __device__ __forceinline__ void quantize_span(const float v[4], bool in, size_t 
 #pragma unroll
         for (int c = 0; c < 4; c++) yv[c] = v[c] / d;
       }
+      // Selects, not branches (per-element branches cost a mask round trip
+      // each): y - 0.5 and y + (-0.5) are the same rounded sum, and an
+      // all-zero block (whose quotients are 0 / 0) stores 0.
+      const bool zero = amax == 0.0f;
 #pragma unroll
       for (int c = 0; c < 4; c++) {
-        if (amax == 0.0f) {
-          qv[c] = 0;
-          fv[c] = 0.0f;
-        } else {
-          const float y = yv[c];
-          int r = y < 0.0f ? f32_as_i32(y - 0.5f) : f32_as_i32(y + 0.5f);
-          r = r < -127 ? -127 : (r > 127 ? 127 : r);
-          qv[c] = (int8_t)r;
-          fv[c] = d * (float)r;
-        }
+        const float y = yv[c];
+        int r = f32_as_i32(y + (y < 0.0f ? -0.5f : 0.5f));
+        r = r < -127 ? -127 : (r > 127 ? 127 : r);
+        qv[c] = zero ? (int8_t)0 : (int8_t)r;
+        fv[c] = zero ? 0.0f : d * (float)r;
       }
       uint32_t packed = (uint32_t)(uint8_t)qv[0] | ((uint32_t)(uint8_t)qv[1] << 8) |
                         ((uint32_t)(uint8_t)qv[2] << 16) | ((uint32_t)(uint8_t)qv[3] << 24);
@@ -104,8 +103,18 @@ __device__ __forceinline__ void quantize_span(const float v[4], bool in, size_t 
     take(dpp_f32<kDppXor2>(bx), dpp_f32<kDppXor2>(bv), dpp_i32<kDppXor2>(bi));
     take(dpp_f32<kDppMirror8>(bx), dpp_f32<kDppMirror8>(bv), dpp_i32<kDppMirror8>(bi));
     take(dpp_f32<kDppMirror16>(bx), dpp_f32<kDppMirror16>(bv), dpp_i32<kDppMirror16>(bi));
-#pragma unroll
-    for (int m = 16; m <= 32; m <<= 1) take(__shfl_xor(bx, m), __shfl_xor(bv, m), __shfl_xor(bi, m));
+    // across the four rows by DPP row broadcasts: rows 1 and 3 take rows 0
+    // and 2 (lane 15, lane 47), then rows 2 and 3 take lane 31 (rows 0-1),
+    // so lane 63 holds the wave's; rows not written keep their own values
+    // and combine with themselves
+    take(__int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(bx), __float_as_int(bx), kDppRowBcast15, 0xa, 0xf, false)),
+         __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(bv), __float_as_int(bv), kDppRowBcast15, 0xa, 0xf, false)),
+         __builtin_amdgcn_update_dpp(bi, bi, kDppRowBcast15, 0xa, 0xf, false));
+    take(__int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(bx), __float_as_int(bx), kDppRowBcast31, 0xc, 0xf, false)),
+         __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(bv), __float_as_int(bv), kDppRowBcast31, 0xc, 0xf, false)),
+         __builtin_amdgcn_update_dpp(bi, bi, kDppRowBcast31, 0xc, 0xf, false));
+    bx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx), 63));
+    bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), 63));
     float mx = bx == 0.0f ? 0.0f : bv;
     if (in) {
       // Stored class-major inside the 256-block (element e at (e % 8) * 32 + e / 8),
@@ -114,13 +123,10 @@ __device__ __forceinline__ void quantize_span(const float v[4], bool in, size_t 
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         int e = 4 * lane + c;
-        int r = 0;
-        if (mx != 0.0f) {
-          float val = iscale * v[c] + 12582912.0f;
-          r = (int)(f2u(val) & 0x007fffffu) - 0x00400000;
-          if (r > 127) r = 127;
-        }
-        q.qk[base + (e & 7) * 32 + (e >> 3)] = (int8_t)r;
+        const float val = iscale * v[c] + 12582912.0f;
+        int r = (int)(f2u(val) & 0x007fffffu) - 0x00400000;
+        r = r > 127 ? 127 : r;
+        q.qk[base + (e & 7) * 32 + (e >> 3)] = mx != 0.0f ? (int8_t)r : (int8_t)0;
       }
       if (lane == 0) q.dk[base / 256] = mx == 0.0f ? 0.0f : 1.0f / iscale;
     }

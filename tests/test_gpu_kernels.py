@@ -134,6 +134,12 @@ def test_quantize_q8a_q8k_bitexact():
     x[1, 10], x[1, 20] = -7.5, 7.5         # |x| tie: first one wins in Q8_K
     x[2, 0:32] = np.float32(2 ** -140)     # subnormal block
     x[3, 64:96] = rng.integers(-3, 4, 32)  # many exact .5 ratios
+    # |x| ties across the rows of sixteen lanes of a 256-block (lane = local
+    # index / 4): row 0 against row 3, row 0 against row 2, row 2 against
+    # row 3; the first index wins
+    x[4, 3], x[4, 200] = -20.0, 20.0
+    x[4, 560], x[4, 700] = -19.0, 19.0
+    x[4, 900], x[4, 1000] = 18.0, -18.0
     da = np.empty(rows * n // 32, np.float32)
     qa = np.empty(rows * n, np.int8)
     dk = np.empty(rows * n // 256, np.float32)
