@@ -1139,9 +1139,59 @@ __global__ void __launch_bounds__(PT) k_gemv_q4k_pc(Q4kPcArgs p, int RB) {
   constexpr bool kPre = PT <= 512;
   RowLoads<PT / 64> pre;
   if (kPre && !p.af) q8a_row_loads<PT / 64>(in, 0, cols, p.norm_w != nullptr, pre);
+  // Stage 0 of gate+up on the chain waves: each chain's lanes load their
+  // own first-stage weights here (lane k of a group of CR: the quant dword
+  // holding its elements 4 k .. 4 k + 3 of every group, and the stage's
+  // superblock headers) and, after the prologue, form those products just
+  // before their adds, so the chains start without waiting for a producer
+  // pass and its barrier; the producers begin at stage 1.  Only gate+up,
+  // whose chains waited on the producers, gains (14.95 -> 14.6 us); where
+  // the chains set the pace (wq+wk, wo, ffn_down: sixteen-lane chains),
+  // the chain waves' own dequantisation in front of every group of adds
+  // cost more than the first stage's wait (12.4 -> 14.5 us, 9.2 -> 10.1).
+  constexpr int G0 = SL / (4 * CR);        // groups of 4 CR terms per stage
+  constexpr bool kDirect0 = MODE == PC_PAIR && G0 <= 16;
+  constexpr int H0 = (SL + 255) / 256;     // superblock headers per stage
+  constexpr int K0 = kDirect0 ? 1 : 0;     // the producers' first stage
+  // Groups (and headers) loaded at the start: at most 256 columns' worth,
+  // the rest when stage 0 begins, behind the first groups' adds (held
+  // through the prologue, a 512-column stage's sixteen registers spilled
+  // at the 1024-thread cap).
+  constexpr int GE = G0 * 4 * CR > 256 ? 256 / (4 * CR) : G0;
+  constexpr int HE = (GE * 4 * CR + 255) / 256;
+  // Chain c = G wave + group: staged row c % NR, position c / NR (with
+  // the gate and up chains of one row and position in adjacent groups for
+  // the pair).  Groups past the chains add chain 0's products and store
+  // nothing, so the whole wave runs every DPP add.
+  const int grp = lane / CR, cidx = G * wave + grp;
+  int chain_row;
+  if (MODE == PC_PAIR) {
+    const int pc = cidx >> 1, j = pc % RB, t = pc / RB;
+    chain_row = pc < RB * T ? ((cidx & 1) ? RB + j : j) + NR * t : 0;
+  } else {
+    chain_row = cidx < NR * T ? cidx : 0;
+  }
+  uint32_t cq[kDirect0 ? G0 : 1];
+  uint4 ch[kDirect0 ? H0 : 1];
+  if (kDirect0 && !producer) {
+    int mc;
+    const int rc = row_of((chain_row % NR) * UPR, &mc);
+    const uint8_t* qrow = (mc ? p.q1 : p.q0) + (size_t)rc * nb * 128;
+    const uint8_t* hrow = (mc ? p.h1 : p.h0) + (size_t)rc * nb * 16;
+    const int kl = lane & (CR - 1);
+#pragma unroll
+    for (int g = 0; g < GE; g++) {
+      // element e0 of the row lies in 32-byte block e0 / 64, byte e0 % 32
+      // (the low nibbles hold the block's first 32 elements)
+      const int e0 = 4 * CR * g + 4 * kl;
+      cq[g] = *reinterpret_cast<const uint32_t*>(qrow + (e0 >> 6) * 32 + (e0 & 31));
+    }
+#pragma unroll
+    for (int hh = 0; hh < HE; hh++) ch[hh] = *reinterpret_cast<const uint4*>(hrow + hh * 16);
+  }
   if (producer) {
 #pragma unroll
-    for (int u = 0; u < NS; u++) DTL_PC_LOAD(u, u);
+    for (int u = 0; u < NS; u++) DTL_PC_LOAD(u, u + K0);
   }
   if (p.af) {
     for (int i = tid; i < T * cols / 4; i += PT) {
@@ -1264,7 +1314,7 @@ __global__ void __launch_bounds__(PT) k_gemv_q4k_pc(Q4kPcArgs p, int RB) {
   if (producer) {
     // Stage k's products go to buffer k & 1; the barrier after them hands
     // the buffer to the chain waves, which add it while the next stage forms.
-    for (int base = 0; base < nst; base += NS) {
+    for (int base = K0; base < nst; base += NS) {
 #pragma unroll
       for (int u = 0; u < NS; u++) {
         const int k = base + u;  // stages past the end form unused products
@@ -1285,20 +1335,43 @@ __global__ void __launch_bounds__(PT) k_gemv_q4k_pc(Q4kPcArgs p, int RB) {
       }
     }
   } else {
-    // Chain c = G wave + group: staged row c % NR, position c / NR (with
-    // the gate and up chains of one row and position in adjacent groups for
-    // the pair).  Groups past the chains add chain 0's products and store
-    // nothing, so the whole wave runs every DPP add.
-    const int grp = lane / CR, c = G * wave + grp;
-    int chain_row;
-    if (MODE == PC_PAIR) {
-      const int pc = c >> 1, j = pc % RB, t = pc / RB;
-      chain_row = pc < RB * T ? ((c & 1) ? RB + j : j) + NR * t : 0;
-    } else {
-      chain_row = c < NR * T ? c : 0;
-    }
+    const int c = cidx;
     float sum = 0.0f;
-    for (int base = 0; base < nst; base += NS) {
+    if (kDirect0) {
+      // stage 0: the products of this lane's four terms of each group,
+      // formed as the producers form them ((d sc) q - dmin m, times the
+      // activation), then the group's adds
+      const float* arow = as + (size_t)(chain_row / NR) * ACS;
+      const int kl = lane & (CR - 1);
+      if (GE < G0) {
+        int mc;
+        const int rc = row_of((chain_row % NR) * UPR, &mc);
+        const uint8_t* qrow = (mc ? p.q1 : p.q0) + (size_t)rc * nb * 128;
+        const uint8_t* hrow = (mc ? p.h1 : p.h0) + (size_t)rc * nb * 16;
+#pragma unroll
+        for (int g = GE; g < G0; g++) {
+          const int e0 = 4 * CR * g + 4 * kl;
+          cq[g] = *reinterpret_cast<const uint32_t*>(qrow + (e0 >> 6) * 32 + (e0 & 31));
+        }
+#pragma unroll
+        for (int hh = HE; hh < H0; hh++) ch[hh] = *reinterpret_cast<const uint4*>(hrow + hh * 16);
+      }
+#pragma unroll
+      for (int g = 0; g < G0; g++) {
+        const int e0 = 4 * CR * g + 4 * kl;
+        const uint4 h = ch[(4 * CR * g) >> 8];
+        const float d = f16_to_f32((uint16_t)(h.x & 0xffffu)), dmin = f16_to_f32((uint16_t)(h.x >> 16));
+        int sc, mn;
+        q4k_scale_min3(h.y, h.z, h.w, (e0 & 255) >> 5, &sc, &mn);
+        const float dsc = d * (float)sc, dm = dmin * (float)mn;
+        const uint32_t nib = (cq[g] >> (4 * ((e0 >> 5) & 1))) & 0x0f0f0f0fu;
+        const float4 a = *reinterpret_cast<const float4*>(arow + q4k_pc_skew(e0));
+        const float w0 = dsc * ubyte_f32<0>(nib) - dm, w1 = dsc * ubyte_f32<1>(nib) - dm;
+        const float w2 = dsc * ubyte_f32<2>(nib) - dm, w3 = dsc * ubyte_f32<3>(nib) - dm;
+        sum = chain_group_add<CR>(sum, make_float4(w0 * a.x, w1 * a.y, w2 * a.z, w3 * a.w));
+      }
+    }
+    for (int base = K0; base < nst; base += NS) {
 #pragma unroll
       for (int u = 0; u < NS; u++) {
         const int k = base + u;
