@@ -838,15 +838,11 @@ __device__ __forceinline__ bool q8a_prologue(const FusedIn& in, int t, int cols,
       misc[tid] = chain_sum_lds(0.0f, sq + tid * cs, (cols - tid + 7) / 8);
     }
     __syncthreads();
-    if (tid == 0) {
-      const float ss = finish_8lane(misc);
-      const float m = ss / (float)cols;
-      const float r = 1.0f / sqrtf(m + in.eps);
-      if (!finite(r)) bad = true;
-      misc[8] = r;
-    }
-    __syncthreads();
-    const float r = misc[8];
+    // every thread forms r from the eight sums (no thread-0 pass and barrier)
+    const float ss = finish_8lane(misc);
+    const float m = ss / (float)cols;
+    const float r = 1.0f / sqrtf(m + in.eps);
+    if (!finite(r)) bad = true;
     for (int span = wave; span * 256 < cols; span += NW) {
       const int e = span * 256 + 4 * lane;
       const bool inb = e < cols;
