@@ -261,7 +261,6 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* x, const float* w,
                                                  QuantOut q, int* err) {
   extern __shared__ __align__(16) float xs[];  // [n] row, then [8][cs] squares
   __shared__ float lane_sum[8];
-  __shared__ float r_sh;
   constexpr int kMaxSpansPerWave = 4;  // n <= 4096 keeps w in registers
   const int t = blockIdx.x;
   const int cs = (((n + 7) / 8) + 3) & ~3;    // per-chain stride, float4 aligned
@@ -334,15 +333,11 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* x, const float* w,
     lane_sum[c] = chain_sum_lds(0.0f, sq + c * cs, (n - c + 7) / 8);
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    float ss = finish_8lane(lane_sum);
-    float m = ss / (float)n;
-    float r = 1.0f / sqrtf(m + eps);
-    if (!finite(r)) bad = true;
-    r_sh = r;
-  }
-  __syncthreads();
-  const float r = r_sh;
+  // every thread forms r from the eight sums (no thread-0 pass and barrier)
+  const float ss = finish_8lane(lane_sum);
+  const float m = ss / (float)n;
+  const float r = 1.0f / sqrtf(m + eps);
+  if (!finite(r)) bad = true;
 #pragma unroll
   for (int k = 0; k < kMaxSpansPerWave; k++) {
     const int span = wave + 4 * k;
