@@ -519,7 +519,7 @@ __global__ void __launch_bounds__(64) k_attention(const float* q, const float* k
     sc[j] = s;
     mx = fmaxf(mx, s);
   }
-  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  mx = wave_fmax(mx);
   for (int j = lane; j < len; j += 64) sc[j] = exp_clamped(sc[j] - mx);
   __syncthreads();
   // Z = sum_f32_ref(e): lane c < 8 walks chain c in ascending order.
@@ -601,7 +601,7 @@ __global__ void __launch_bounds__(1024) k_attention_grp(const float* q, const fl
   // softmax_in_place (lib.rs:2361-2388), per wave
   float mx = -__builtin_huge_valf();
   for (int j = lane; j < len; j += 64) mx = fmaxf(mx, my[j]);
-  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  mx = wave_fmax(mx);
   for (int j = lane; j < len; j += 64) my[j] = exp_clamped(my[j] - mx);
   __syncthreads();
   float acc = 0.0f;
@@ -799,7 +799,7 @@ __global__ void __launch_bounds__(NT) k_attention_hd64(const float* q, const flo
   // softmax_in_place (lib.rs:2361-2388), per wave
   float mx = -__builtin_huge_valf();
   for (int j = lane; j < len; j += 64) mx = fmaxf(mx, my[j]);
-  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  mx = wave_fmax(mx);
   for (int j = lane; j < len; j += 64) my[j] = exp_clamped(my[j] - mx);
   __syncthreads();
   float zacc = 0.0f;
@@ -1006,9 +1006,9 @@ __global__ void __launch_bounds__(512) k_attention_hd64s(const float* q, const f
     }
   }
   // the head's maximum over the wave's eight key lanes, then (below) over the waves
-  lmax = fmaxf(lmax, __shfl_xor(lmax, 1));
-  lmax = fmaxf(lmax, __shfl_xor(lmax, 2));
-  lmax = fmaxf(lmax, __shfl_xor(lmax, 4));
+  lmax = fmaxf(lmax, dpp_f32<kDppXor1>(lmax));
+  lmax = fmaxf(lmax, dpp_f32<kDppXor2>(lmax));
+  lmax = fmaxf(lmax, dpp_f32<kDppMirror8>(lmax));
   if (kk == 0) pb[hh] = lmax;  // the wave's own area, free until P.V
   // The first V tiles' loads overlap the softmax.
 #pragma unroll
@@ -1246,9 +1246,7 @@ __global__ void __launch_bounds__(kDecThreads) k_attention_dec(const float* q, R
         float acc = 0.0f;
 #pragma unroll
         for (int u = 0; u < 8; u++) acc += qr[u] * (j < pb ? kb[d][u] : kn[jv][r + 8 * u]);
-        const float s1 = acc + __shfl_xor(acc, 1);
-        const float s2 = s1 + __shfl_xor(s1, 2);
-        const float s3 = s2 + __shfl_xor(s2, 4);
+        const float s3 = finish_8lane_dpp(acc);
         if (r == 0 && j < len) {
           const float sv = s3 * scale;
           if (!finite(sv)) bad = true;
@@ -1262,7 +1260,7 @@ __global__ void __launch_bounds__(kDecThreads) k_attention_dec(const float* q, R
   // softmax_in_place (lib.rs:2361-2388)
   float mx = -__builtin_huge_valf();
   for (int j = tid; j < len; j += kDecThreads) mx = fmaxf(mx, sc[j]);
-  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  mx = wave_fmax(mx);
   if (lane == 0) red[wave] = mx;
   __syncthreads();
   mx = red[0];
@@ -1461,9 +1459,7 @@ __global__ void __launch_bounds__(256) k_attn_split_scores(const float* q, RopeI
       float acc = 0.0f;
 #pragma unroll
       for (int u = 0; u < 8; u++) acc += qr[u] * (j < pb ? kb[d][u] : kn[jv][r + 8 * u]);
-      const float s1 = acc + __shfl_xor(acc, 1);
-      const float s2 = s1 + __shfl_xor(s1, 2);
-      const float s3 = s2 + __shfl_xor(s2, 4);
+      const float s3 = finish_8lane_dpp(acc);
       if (r == 0 && j < len) {
         const float sv = s3 * scale;
         bad |= !finite(sv);
@@ -1597,7 +1593,7 @@ __global__ void __launch_bounds__(kPvThreads) k_attn_split_pv(const float* score
       mx = fmaxf(mx, sv[k]);
     }
   }
-  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  mx = wave_fmax(mx);
   if (lane == 0) red[wave] = mx;
   // V, dimension-major: each 4 x 4 block transposed in registers, one float4
   // per dimension (rows past len are stored too; no chain reads them)
@@ -1770,9 +1766,7 @@ __global__ void __launch_bounds__(kPvThreads) k_attn_fused(const float* q, RopeI
       float acc = 0.0f;
 #pragma unroll
       for (int u = 0; u < 8; u++) acc += qr[u] * (j < pb ? kb[d][u] : kn[jv][r8 + 8 * u]);
-      const float s1 = acc + __shfl_xor(acc, 1);
-      const float s2 = s1 + __shfl_xor(s1, 2);
-      const float s3 = s2 + __shfl_xor(s2, 4);
+      const float s3 = finish_8lane_dpp(acc);
       if (r8 == 0 && j < len) {
         const float sv = s3 * scale;
         bad |= !finite(sv);
@@ -1781,7 +1775,7 @@ __global__ void __launch_bounds__(kPvThreads) k_attn_fused(const float* q, RopeI
       }
     }
   }
-  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  mx = wave_fmax(mx);
   if (lane == 0) red[wave] = mx;
   // V, dimension-major: each 4 x 4 block transposed in registers, one float4
   // per dimension (rows past len are stored too; no chain reads them)
@@ -2088,7 +2082,7 @@ __global__ void __launch_bounds__(256) k_cdf(const float* logits, int V, int tai
       mx = fmaxf(mx, v[k]);
     }
   }
-  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  mx = wave_fmax(mx);
   if ((tid & 63) == 0) red[tid / 64] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -2307,7 +2301,7 @@ CdfScratch cdf_scratch(void* base, int R, int V) {
 }
 
 __device__ float block_max_256(float v, float* red) {
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+  v = wave_fmax(v);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));

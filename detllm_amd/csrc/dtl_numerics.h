@@ -223,6 +223,33 @@ constexpr int kDppMirror16 = 0x140; // row_mirror
 constexpr int kDppRowBcast15 = 0x142;  // row_bcast:15 (lane 15 of each row to the next row)
 constexpr int kDppRowBcast31 = 0x143;  // row_bcast:31 (lane 31 to rows 2 and 3)
 
+// The maximum over the wave's 64 lanes, returned to every lane (fmax is
+// exact in any order): within rows by DPP, across rows by row broadcasts
+// (lane 63 ends with the wave's), then read from lane 63.  Every lane of the
+// wave must be active.
+__device__ __forceinline__ float wave_fmax(float v) {
+  v = fmaxf(v, dpp_f32<kDppXor1>(v));
+  v = fmaxf(v, dpp_f32<kDppXor2>(v));
+  v = fmaxf(v, dpp_f32<kDppMirror8>(v));
+  v = fmaxf(v, dpp_f32<kDppMirror16>(v));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v),
+                                                         kDppRowBcast15, 0xa, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v),
+                                                         kDppRowBcast31, 0xc, 0xf, false)));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// finish_8lane over the eight lanes 8 i .. 8 i + 7 holding a[0..7] of one
+// dot product, by DPP: ((a0 + a1) + (a2 + a3)) + ((a4 + a5) + (a6 + a7)),
+// exact at the group's first lane (whose partner in the last step, lane 7,
+// holds (a7 + a6) + (a5 + a4): the same sums, each operand pair swapped,
+// and IEEE addition commutes).  Every lane of the wave must be active.
+__device__ __forceinline__ float finish_8lane_dpp(float a) {
+  const float s1 = a + dpp_f32<kDppXor1>(a);
+  const float s2 = s1 + dpp_f32<kDppXor2>(s1);
+  return s2 + dpp_f32<kDppMirror8>(s2);
+}
+
 // Serial chains whose terms reach the adding lane by DPP broadcast.  A wave
 // issues an LDS read in about 14 cycles and a dependent add in about 4.6, so
 // a chain that reads its own terms (one float4 per four adds) runs at about
