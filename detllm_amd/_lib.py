@@ -110,6 +110,8 @@ _SIGS = {
     "dtl_cdf": (C.c_int, [C.c_void_p, sz, sz, u32p, u64p, u64p]),
     "dtl_decoder_total": (C.c_int, [C.c_void_p, sz, sz, u64p]),
     "dtl_decoder_lookup": (C.c_int, [C.c_void_p, sz, sz, C.c_uint64, u32p, u64p, u32p, u64p]),
+    "dtl_decoder_decode": (C.c_int, [C.c_void_p, sz, sz, C.c_void_p, u32p]),
+    "dtl_forward_decode": (C.c_int, [C.c_void_p, C.c_uint32, sz, sz, C.c_void_p, u32p]),
     "dtl_logits_to_cdf": (C.c_int, [f32p, sz, sz, u32p, u64p, u64p]),
     "dtl_logits_to_symbol_range": (C.c_int, [f32p, sz, sz, sz, u64p, u32p, u64p]),
     "dtl_uniform_cdf": (C.c_int, [sz, u32p, u64p, u64p]),

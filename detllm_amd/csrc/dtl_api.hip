@@ -1136,7 +1136,10 @@ int capture_decode_graph(dtl_session* s, int k) {
   return DTL_OK;
 }
 
-int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t pos0) {
+// check: wait for the forward and report its non-finite check here; without
+// it the caller's next wait reads the error bits (the forward's launches
+// clear them first) and sets rows_valid.
+int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t pos0, bool check = true) {
   const dtl_model* m = s->m;
   if (T <= 0 || (size_t)T > s->max_chunk || pos0 + (size_t)T > s->n_ctx) return DTL_ERR_SHAPE;
   for (int t = 0; t < T; t++)
@@ -1161,6 +1164,7 @@ int forward_device(dtl_session* s, const uint32_t* tokens_host, int T, size_t po
     int rc = enqueue_forward(s, T, pos0, nullptr);
     if (rc) return rc;
   }
+  if (!check) return DTL_OK;
   int bits = 0;
   int rc = read_err(s, &bits);
   if (rc) return rc;
@@ -1178,6 +1182,43 @@ int cdf_status(int bits) {
 }
 
 constexpr size_t kMaxSymbols = 1u << 18;
+
+// The decode step's device round trip (dtl_decoder_decode, dtl_forward_decode):
+// the CDF of logits row `row` and, on the device, decode_freq's value from
+// the decoder's window and its lookup; one copy out, one wait.  Then the
+// host's own decode_freq, which must give the device's value, and advance.
+// after_forward: the forward of that row was enqueued unchecked just before.
+int decode_step(dtl_session* s, size_t row, size_t tail, dtl_range_decoder* dec,
+                const dtl_range_decoder_state& ds, uint32_t* symbol, bool after_forward) {
+  Lane& L = *s->ln;
+  const size_t V = s->m->vocab;
+  if (!after_forward) clear_err(s);
+  launch_cdf_decode(L.logits + row * V, (int)V, (int)tail, ds.code - ds.low, ds.range, L.c_scratch, L.c_pack,
+                    L.err, L.stream);
+  uint64_t* io = L.h_io;  // [1] symbol, [2] cum, [3] freq, [4] total, [5] error bits, [6] value, [7] valid
+  HIP_TRY(hipMemcpyAsync(io + 1, L.c_pack, 7 * sizeof(uint64_t), hipMemcpyDeviceToHost, L.stream));
+  HIP_TRY(hipStreamSynchronize(L.stream));
+  s->prof.collect();
+  const int bits = (int)(uint32_t)io[5];
+  if (after_forward) {
+    if (bits & ERRBIT_NON_FINITE) return DTL_ERR_NON_FINITE;
+    L.rows_valid = 1;
+  }
+  // the distribution's own errors, as dtl_decoder_total reports them
+  int st = cdf_status(bits & ~ERRBIT_CDF_LOOKUP);
+  if (st) return st;
+  // the scratch holds this row's block results, as after dtl_decoder_total
+  L.cdf_ready_row = row;
+  L.cdf_ready_tail = tail;
+  const uint64_t total = io[4];
+  uint64_t value = 0;
+  if ((st = dtl_range_decode_freq(dec, total, &value))) return st;
+  if (io[7] != 1 || io[6] != value) return DTL_ERR_DEVICE;  // the device formed another value
+  if ((st = cdf_status(bits))) return st;                     // no symbol covers the value
+  if ((st = dtl_range_decode_advance(dec, io[2], io[3], total))) return st;
+  *symbol = (uint32_t)io[1];
+  return DTL_OK;
+}
 
 }  // namespace
 
@@ -1700,6 +1741,28 @@ int dtl_decoder_total(dtl_session* s, size_t row, size_t tail, uint64_t* total) 
     s->ln->cdf_ready_tail = tail;
   }
   return st;
+}
+
+int dtl_decoder_decode(dtl_session* s, size_t row, size_t tail, dtl_range_decoder* dec, uint32_t* symbol) {
+  if (!s || !dec || !symbol) return DTL_ERR_INVALID_ARGUMENT;
+  const size_t V = s->m->vocab;
+  if (row >= s->ln->rows_valid) return DTL_ERR_SHAPE;
+  if (V + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
+  dtl_range_decoder_state ds;
+  if (int st = dtl_range_decoder_snapshot(dec, &ds)) return st;  // between decode_freq and advance
+  HIP_TRY(hipSetDevice(s->m->device));
+  return decode_step(s, row, tail, dec, ds, symbol, false);
+}
+
+int dtl_forward_decode(dtl_session* s, uint32_t token, size_t pos, size_t tail, dtl_range_decoder* dec,
+                       uint32_t* symbol) {
+  if (!s || !dec || !symbol) return DTL_ERR_INVALID_ARGUMENT;
+  if (s->m->vocab + tail > kMaxSymbols) return DTL_ERR_CDF_TOO_MANY_SYMBOLS;
+  dtl_range_decoder_state ds;
+  if (int st = dtl_range_decoder_snapshot(dec, &ds)) return st;
+  int st = forward_device(s, &token, 1, pos, false);
+  if (st) return st;
+  return decode_step(s, 0, tail, dec, ds, symbol, true);
 }
 
 int dtl_decoder_lookup(dtl_session* s, size_t row, size_t tail, uint64_t value, uint32_t* symbol,

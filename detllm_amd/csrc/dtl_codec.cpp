@@ -170,6 +170,11 @@ int decode_symbols(dtl_session* s, const uint8_t* payload, size_t plen, size_t o
   if (st) return st;
   std::vector<uint32_t> context;
   size_t window_start = 0, context_len = 0, last_row = 0, bytes = 0;
+  // A decoded token whose forward (advance) is enqueued with the next
+  // symbol's decode, one wait for both; a window replay forwards it instead.
+  bool pend = false;
+  uint32_t pend_tok = 0;
+  size_t pend_pos = 0;
   if ((st = dtl_session_reset(s))) goto done;
   for (size_t k = 0; k < n_prior; k++) {
     const uint32_t sym = prior[k];
@@ -200,6 +205,7 @@ int decode_symbols(dtl_session* s, const uint8_t* payload, size_t plen, size_t o
       // replay (main.rs:690-701): fresh cache, the window's tokens re-forwarded
       window_start = next;
       context_len = 0;
+      pend = false;
       if ((st = dtl_session_reset(s))) goto done;
       for (size_t p0 = next; p0 < pos; p0 += in.max_chunk) {
         const size_t T = std::min(in.max_chunk, pos - p0);
@@ -216,13 +222,14 @@ int decode_symbols(dtl_session* s, const uint8_t* payload, size_t plen, size_t o
       if ((st = dtl_range_decode_freq(dec, total, &value))) goto done;
       sym = (uint32_t)value;
       if ((st = dtl_range_decode_advance(dec, value, 1, total))) goto done;
+    } else if (pend) {
+      // advance(token) + decode_symbol (main.rs:570-575)
+      pend = false;
+      if ((st = dtl_forward_decode(s, pend_tok, pend_pos, tail, dec, &sym))) goto done;
+      last_row = 0;
     } else {
-      uint64_t total, cum;
-      uint32_t freq;
-      if ((st = dtl_decoder_total(s, last_row, tail, &total))) goto done;
-      if ((st = dtl_range_decode_freq(dec, total, &value))) goto done;
-      if ((st = dtl_decoder_lookup(s, last_row, tail, value, &sym, &cum, &freq, &total))) goto done;
-      if ((st = dtl_range_decode_advance(dec, cum, freq, total))) goto done;
+      // decode_symbol after a window replay or a byte escape
+      if ((st = dtl_decoder_decode(s, last_row, tail, dec, &sym))) goto done;
     }
     if (!byte_escapes && sym >= V) {
       st = DTL_ERR_CODEC_ESCAPE_IN_TOKEN_STREAM;
@@ -241,12 +248,15 @@ int decode_symbols(dtl_session* s, const uint8_t* payload, size_t plen, size_t o
         st = DTL_ERR_SHAPE;
         goto done;
       }
-      if ((st = dtl_forward_one(s, sym, context_len, nullptr))) goto done;
+      pend = true;
+      pend_tok = sym;
+      pend_pos = context_len;
       context.push_back(sym);
       context_len++;
-      last_row = 0;
     }
   }
+  // the last token's advance, whose decode never comes
+  if (pend) st = dtl_forward_one(s, pend_tok, pend_pos, nullptr);
 done:
   if (st == DTL_OK && final_state) st = dtl_range_decoder_snapshot(dec, final_state);
   dtl_range_decoder_free(dec);

@@ -326,6 +326,12 @@ void launch_cdf_blocks(const float* logits, const uint32_t* rows, int R, int V, 
                        const uint32_t* symbols, const uint64_t* values, uint64_t* cum,
                        uint32_t* freq, uint64_t* total, uint32_t* sym, void* scratch,
                        bool finish_only, int* err, hipStream_t s);
+// One row's decoder step: the block pass, then the lookup of the value
+// RangeDecoder::decode_freq forms from the decoder's window (cml = code -
+// low, rng = range) against the row's total.  pack[0..6]: symbol, cum, freq,
+// total, error bits (with those already set in *err), value, valid.
+void launch_cdf_decode(const float* logits, int V, int tail, uint64_t cml, uint64_t rng, void* scratch,
+                       uint64_t* pack, int* err, hipStream_t s);
 
 // Kernel-level parity entry points.
 void launch_exp_f32(const float* in, float* out, int n, int which, hipStream_t s);

@@ -2481,15 +2481,23 @@ __global__ void __launch_bounds__(256) k_cdf_bfreq(int V, int mode, const uint32
 
 // Per-row finish: totals (and the CdfError::TotalTooLarge check), the
 // symbol range (mode 0) or the decoder lookup (mode 2: block search, then a
-// scan of the f_i of that block in symbol order).
+// scan of the f_i of that block in symbol order).  Mode 4 (one row) is the
+// lookup of RangeDecoder::decode_freq's value (det-coder range.rs:110-126),
+// formed here from the decoder's window cml = code - low and rng = range:
+// value = cml / (rng / total), valid when 0 < total < 2^31, rng / total > 0
+// and value < total (the host's decode_freq accepts exactly these).  Its
+// results go to pack[0..6]: symbol, cum, freq, total, error bits, value,
+// valid (1 or 0), for one copy to the host.
 __global__ void __launch_bounds__(256) k_cdf_finish(int V, int nb, int tail, int mode,
                                                     const uint32_t* symbols,
                                                     const uint64_t* values, uint64_t* cum,
                                                     uint32_t* freq, uint64_t* total, uint32_t* sym,
-                                                    CdfScratch cs, int* err) {
+                                                    CdfScratch cs, int* err, uint64_t cml,
+                                                    uint64_t rng, uint64_t* pack) {
   __shared__ uint64_t scan[256];
   __shared__ int blk_sh;
   __shared__ uint64_t off_sh;
+  __shared__ uint64_t found[3];  // mode 4: symbol, cum, freq
   const int r = blockIdx.x, tid = threadIdx.x;
   // Row totals: the block sums in order (exact, order free).
   uint64_t run = 0, below = 0;
@@ -2498,7 +2506,11 @@ __global__ void __launch_bounds__(256) k_cdf_finish(int V, int nb, int tail, int
     if (mode == 0) below += cs.bbelow[(size_t)r * nb + b];
   }
   const uint64_t tot_all = run + (uint64_t)tail;
-  if (tid == 0 && (run >= (1ull << 31) || tot_all >= (1ull << 31))) flag(err, ERRBIT_CDF_TOTAL);
+  int mybits = 0;  // thread 0's own flags, for the pack
+  if (tid == 0 && (run >= (1ull << 31) || tot_all >= (1ull << 31))) {
+    flag(err, ERRBIT_CDF_TOTAL);
+    mybits |= ERRBIT_CDF_TOTAL;
+  }
   if (mode == 0) {
     if (tid == 0) {
       const uint32_t s = symbols[r];
@@ -2517,13 +2529,36 @@ __global__ void __launch_bounds__(256) k_cdf_finish(int V, int nb, int tail, int
     if (tid == 0) total[r] = tot_all;
     return;
   }
-  // mode 2
-  const uint64_t target = values[r];
+  // modes 2 and 4; every thread forms the same target
+  uint64_t target;
+  bool valid = true;
+  if (mode == 4) {
+    valid = tot_all != 0 && tot_all < (1ull << 31);
+    const uint64_t q = valid ? rng / tot_all : 0;
+    valid = valid && q != 0;
+    target = valid ? cml / q : 0;
+    valid = valid && target < tot_all;
+  } else {
+    target = values[r];
+  }
+  auto put = [&](uint32_t sy, uint64_t cu, uint32_t fr) {
+    if (mode == 4) {
+      found[0] = sy;
+      found[1] = cu;
+      found[2] = fr;
+    } else {
+      sym[r] = sy;
+      cum[r] = cu;
+      freq[r] = fr;
+    }
+  };
   if (tid == 0) {
-    total[r] = tot_all;
+    if (mode != 4) total[r] = tot_all;
+    found[0] = found[1] = found[2] = 0;
     int blk = -1;
     uint64_t off = 0;
-    if (target < run) {
+    if (!valid) {
+    } else if (target < run) {
       for (int b = 0; b < nb; b++) {
         const uint64_t sb = cs.bsum[(size_t)r * nb + b];
         if (target < off + sb) {
@@ -2535,11 +2570,10 @@ __global__ void __launch_bounds__(256) k_cdf_finish(int V, int nb, int tail, int
     } else {
       const uint64_t o = target - run;
       if (o < (uint64_t)tail) {
-        sym[r] = (uint32_t)(V + o);
-        cum[r] = target;
-        freq[r] = 1;
+        put((uint32_t)(V + o), target, 1u);
       } else {
         flag(err, ERRBIT_CDF_LOOKUP);
+        mybits |= ERRBIT_CDF_LOOKUP;
       }
     }
     blk_sh = blk;
@@ -2547,33 +2581,62 @@ __global__ void __launch_bounds__(256) k_cdf_finish(int V, int nb, int tail, int
   }
   __syncthreads();
   const int blk = blk_sh;
-  if (blk < 0) return;
-  const int v8 = cdf_v8(V);
-  const float* e = cs.ebuf + (size_t)r * 8 * v8;
-  const float z = cs.z[r];
-  // thread tid owns symbols blk*4096 + 16 tid .. +15 (ascending)
-  uint32_t f[16];
-  uint64_t local = 0;
-  const int i0 = blk * kCdfBlk + 16 * tid;
+  if (blk >= 0) {
+    const int v8 = cdf_v8(V);
+    const float* e = cs.ebuf + (size_t)r * 8 * v8;
+    const float z = cs.z[r];
+    // thread tid owns symbols blk*4096 + 16 tid .. +15 (ascending)
+    uint32_t f[16];
+    uint64_t local = 0;
+    const int i0 = blk * kCdfBlk + 16 * tid;
 #pragma unroll
-  for (int k = 0; k < 16; k++) {
-    const int i = i0 + k;
-    f[k] = i < V ? cdf_freq(e[(size_t)(i & 7) * v8 + (i >> 3)], z) : 0u;
-    local += f[k];
-  }
-  uint64_t tot;
-  const uint64_t incl = block_scan_u64(local, scan, &tot);
-  uint64_t c0 = off_sh + incl - local;
-#pragma unroll
-  for (int k = 0; k < 16; k++) {
-    const int i = i0 + k;
-    if (i < V && target >= c0 && target < c0 + f[k]) {
-      sym[r] = (uint32_t)i;
-      cum[r] = c0;
-      freq[r] = f[k];
+    for (int k = 0; k < 16; k++) {
+      const int i = i0 + k;
+      f[k] = i < V ? cdf_freq(e[(size_t)(i & 7) * v8 + (i >> 3)], z) : 0u;
+      local += f[k];
     }
-    c0 += f[k];
+    uint64_t tot;
+    const uint64_t incl = block_scan_u64(local, scan, &tot);
+    uint64_t c0 = off_sh + incl - local;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      const int i = i0 + k;
+      if (i < V && target >= c0 && target < c0 + f[k]) put((uint32_t)i, c0, f[k]);
+      c0 += f[k];
+    }
   }
+  if (mode != 4) return;
+  __syncthreads();
+  if (tid == 0) {
+    // the flags of the launches before this one (the forward's, the block
+    // kernels'), read past the L1, and this thread's own
+    const int prior = __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    pack[0] = found[0];
+    pack[1] = found[1];
+    pack[2] = found[2];
+    pack[3] = tot_all;
+    pack[4] = (uint64_t)(uint32_t)(prior | mybits);
+    pack[5] = target;
+    pack[6] = valid ? 1u : 0u;
+  }
+}
+
+// The block kernels of launch_cdf_blocks: block maxima, exps, Z and block
+// sums (mode 0: also the sums below symbols[r]).
+void launch_cdf_block_pass(const float* logits, const uint32_t* rows, int R, int V, int mode,
+                           const uint32_t* symbols, const CdfScratch& cs, int* err, hipStream_t s) {
+  const int nb = cdf_nblk(V);
+  launch_kernel(k_cdf_bmax, dim3(nb, R), dim3(256), 0, s, logits, rows, V, cs, err);
+  launch_kernel(k_cdf_bexp, dim3(nb, R), dim3(256), 0, s, logits, rows, V, cs);
+  constexpr size_t kZRing = 3 * 8 * 1024 * sizeof(float);  // k_cdf_z's segment ring
+  static bool z_attr_set = false;
+  if (!z_attr_set) {
+    (void)hipFuncSetAttribute((const void*)k_cdf_z, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)kZRing);
+    z_attr_set = true;
+  }
+  launch_kernel(k_cdf_z, dim3(R), dim3(256), kZRing, s, V, cs);
+  launch_kernel(k_cdf_bfreq, dim3(nb, R), dim3(256), 0, s, V, mode, symbols, cs);
 }
 
 void launch_cdf_blocks(const float* logits, const uint32_t* rows, int R, int V, int tail, int mode,
@@ -2582,21 +2645,19 @@ void launch_cdf_blocks(const float* logits, const uint32_t* rows, int R, int V, 
                        bool finish_only, int* err, hipStream_t s) {
   const int nb = cdf_nblk(V);
   CdfScratch cs = cdf_scratch(scratch, R, V);
-  if (!finish_only) {
-    launch_kernel(k_cdf_bmax, dim3(nb, R), dim3(256), 0, s, logits, rows, V, cs, err);
-    launch_kernel(k_cdf_bexp, dim3(nb, R), dim3(256), 0, s, logits, rows, V, cs);
-    constexpr size_t kZRing = 3 * 8 * 1024 * sizeof(float);  // k_cdf_z's segment ring
-    static bool z_attr_set = false;
-    if (!z_attr_set) {
-      (void)hipFuncSetAttribute((const void*)k_cdf_z, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)kZRing);
-      z_attr_set = true;
-    }
-    launch_kernel(k_cdf_z, dim3(R), dim3(256), kZRing, s, V, cs);
-    launch_kernel(k_cdf_bfreq, dim3(nb, R), dim3(256), 0, s, V, mode, symbols, cs);
-  }
+  if (!finish_only) launch_cdf_block_pass(logits, rows, R, V, mode, symbols, cs, err, s);
   launch_kernel(k_cdf_finish, dim3(R), dim3(256), 0, s, V, nb, tail, mode, symbols, values, cum,
-                freq, total, sym, cs, err);
+                freq, total, sym, cs, err, (uint64_t)0, (uint64_t)0, (uint64_t*)nullptr);
+}
+
+void launch_cdf_decode(const float* logits, int V, int tail, uint64_t cml, uint64_t rng, void* scratch,
+                       uint64_t* pack, int* err, hipStream_t s) {
+  const int nb = cdf_nblk(V);
+  CdfScratch cs = cdf_scratch(scratch, 1, V);
+  launch_cdf_block_pass(logits, nullptr, 1, V, 4, nullptr, cs, err, s);
+  launch_kernel(k_cdf_finish, dim3(1), dim3(256), 0, s, V, nb, tail, 4, (const uint32_t*)nullptr,
+                (const uint64_t*)nullptr, (uint64_t*)nullptr, (uint32_t*)nullptr, (uint64_t*)nullptr,
+                (uint32_t*)nullptr, cs, err, cml, rng, pack);
 }
 
 void launch_cdf(const float* logits, int R, int V, int tail, int mode, const uint32_t* symbols,

@@ -314,3 +314,20 @@ class Session:
         check(lib.dtl_decoder_lookup(self._h, row, tail_symbols, int(value), C.byref(sym), C.byref(cum),
                                      C.byref(freq), C.byref(total)), "dtl_decoder_lookup")
         return int(sym.value), int(cum.value), int(freq.value), int(total.value)
+
+    def decode_symbol(self, dec, row: int = 0, tail_symbols: int = 0) -> int:
+        """decode_symbol's model branch (det-cli main.rs:724-750) on row `row`:
+        distribution, decode_freq, symbol_range and advance of the
+        coder.RangeDecoder `dec`, one wait for the device."""
+        sym = C.c_uint32()
+        check(lib.dtl_decoder_decode(self._h, row, tail_symbols, dec._h, C.byref(sym)), "dtl_decoder_decode")
+        return int(sym.value)
+
+    def forward_decode(self, token: int, pos: int, dec, tail_symbols: int = 0) -> int:
+        """advance(token) then decode_symbol (det-cli main.rs:570-575): the
+        forward of `token` at `pos` and the next symbol from its logits."""
+        sym = C.c_uint32()
+        check(lib.dtl_forward_decode(self._h, int(token), int(pos), tail_symbols, dec._h, C.byref(sym)),
+              "dtl_forward_decode")
+        self.rows = 1
+        return int(sym.value)

@@ -302,6 +302,27 @@ int dtl_range_decoder_snapshot(const dtl_range_decoder *dec, dtl_range_decoder_s
 int dtl_range_decoder_from_snapshot(const uint8_t *data, size_t len, const dtl_range_decoder_state *state,
                                     dtl_range_decoder **out);
 
+/* The model branch of decode_symbol (det-cli main.rs:724-750) for logits
+ * row `row`: logits_to_decoder_distribution_* (cdf.rs:108-121, 201-245),
+ * RangeDecoder::decode_freq of its total (range.rs:110-126),
+ * DecoderDistribution::symbol_range (cdf.rs:392-425) and
+ * RangeDecoder::advance, with one wait for the device: the device forms
+ * decode_freq's value from the decoder's state for the lookup, the host
+ * forms it again and advances `dec`.  The same symbol, decoder state and
+ * errors as dtl_decoder_total, dtl_range_decode_freq, dtl_decoder_lookup
+ * and dtl_range_decode_advance in turn (DTL_ERR_DEVICE if the two values
+ * differ). */
+int dtl_decoder_decode(dtl_session *session, size_t row, size_t tail_symbols, dtl_range_decoder *dec,
+                       uint32_t *symbol);
+
+/* One step of the decode loop (det-cli main.rs:570-575, 604-626): advance
+ * (main.rs:753-771, forward_one_with_workspace of `token` at `pos`) and
+ * then decode_symbol of its logits, as dtl_decoder_decode of row 0, with
+ * one wait for the device for both.  The forward's errors come first, as
+ * from dtl_forward_one. */
+int dtl_forward_decode(dtl_session *session, uint32_t token, size_t pos, size_t tail_symbols,
+                       dtl_range_decoder *dec, uint32_t *symbol);
+
 /* ---- det-token byte-fallback tokenizer (host) ---------------------------- */
 typedef struct dtl_tokenizer dtl_tokenizer;
 

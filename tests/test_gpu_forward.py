@@ -190,6 +190,68 @@ def test_cdf_on_device_logits_matches_oracle():
             assert s.decoder_total(2, tail) == rt
 
 
+@pytest.mark.parametrize("tail", [0, 256])
+def test_fused_decode_steps_match_oracle_ranges(tail):
+    """dtl_forward_decode / dtl_decoder_decode against a payload coded with
+    the oracle's symbol ranges: the symbols and, after every step, the range
+    decoder's state equal a host decoder fed the oracle's ranges.  The
+    symbols sit on the 4096-symbol work-block edges, at the vocabulary's end,
+    on the most likely token and (tail 256) on byte escapes, which are not
+    forwarded, so the next decode reads the same row again."""
+    from detllm_amd import coder, synth
+    from detllm_amd._lib import DetllmError
+
+    w = synth.WORKLOADS["smollm2"]
+    data = synth.build_model(w, layers=2)
+    m = _model(data)
+    V = w.vocab
+    t0 = int(synth.tokens(w, 1)[0])
+    esc = (V + 3, V + 255) if tail else (17, 30000)
+    with m.forward_workspace(16, 1) as s:
+        lg = s.forward_one(t0, 0)
+        syms = [4095, 4096, V - 1, esc[0], None, 8192, 0, esc[1], 12345, 4097]  # None: the argmax
+        enc, ranges, pos = coder.RangeEncoder(), [], 1
+        for i, want in enumerate(syms):
+            if want is None:
+                want = syms[i] = int(np.argmax(lg))
+            r = detref.symbol_range(lg, want, tail)
+            enc.encode(*r)
+            ranges.append(r)
+            if want < V:
+                lg = s.forward_one(want, pos)
+                pos += 1
+        payload = enc.finish()
+
+    def state(d):
+        st = d.snapshot()
+        return st.low, st.range, st.code, st.pos
+
+    with m.forward_workspace(16, 1) as s:
+        dec, host = coder.RangeDecoder(payload), coder.RangeDecoder(payload)
+        s.forward_one(t0, 0, want_logits=False)
+        pos, pend = 1, None
+        for want, (cum, freq, total) in zip(syms, ranges):
+            if pend is None:
+                got = s.decode_symbol(dec, 0, tail)
+            else:
+                got = s.forward_decode(pend, pos, dec, tail)
+                pos += 1
+            v = host.decode_freq(total)
+            assert cum <= v < cum + freq
+            host.advance(cum, freq, total)
+            assert got == want
+            assert state(dec) == state(host)
+            pend = got if got < V else None
+        # a decoder between decode_freq and advance, a token outside the vocabulary
+        host.decode_freq(ranges[0][2])
+        with pytest.raises(DetllmError) as e:
+            s.decode_symbol(host, 0, tail)
+        assert e.value.status == 30
+        with pytest.raises(DetllmError) as e:
+            s.forward_decode(V, pos, dec, tail)
+        assert e.value.status == 1
+
+
 @pytest.mark.parametrize("V", [4, 256, 32000, 151936])
 def test_standalone_cdf_kernel_matches_oracle(V):
     from detllm_amd import coder
