@@ -441,8 +441,9 @@ __global__ void __launch_bounds__(64) k_gemv_q6k(DevMat W, const int8_t* __restr
 // Q6_K decode layout (see q6k_decode_layout_applies): one thread per
 // (superblock, class) of the padded groups writes its class's low nibbles and
 // high bit pairs; class 0 also writes the scales.  Quant q6u of element e
-// decoded as q6_k_quant does (det-quant lib.rs:537-556), kept unsigned
-// (0..63; the kernel subtracts 32).
+// decoded as q6_k_quant does (det-quant lib.rs:537-556); its bit 5 is stored
+// flipped (q6u ^ 32), so that the kernel's byte with the six bits at the top
+// is the signed 4 (q6u - 32).
 __global__ void k_q6k_decode_layout(DevMat W, uint32_t* out, int groups) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   const int c = i & 7, s = (i >> 3) & 15, g = i >> 7;
@@ -458,7 +459,9 @@ __global__ void k_q6k_decode_layout(DevMat W, uint32_t* out, int groups) {
       const int e = c + 8 * j, half = e / 128, within = e % 128, l = within % 32, part = within / 32;
       const uint8_t qlb = body[64 * half + l + 32 * (part & 1)];
       const uint32_t nib = (part >> 1) ? (qlb >> 4) : (qlb & 0x0fu);
-      const uint32_t h2 = (body[128 + 32 * half + l] >> (2 * part)) & 0x03u;
+      // the high pair with its top bit (bit 5 of q) flipped: the kernel's
+      // byte (q ^ 0x20) << 2 is then the signed value 4 (q - 32)
+      const uint32_t h2 = ((body[128 + 32 * half + l] >> (2 * part)) & 0x03u) ^ 0x02u;
       lo[j >> 3] |= nib << (8 * (j & 3) + 4 * ((j >> 2) & 1));
       hi[j >> 4] |= h2 << (8 * (j & 3) + 2 * ((j >> 2) & 3));
     }
@@ -489,11 +492,12 @@ void launch_q6k_decode_layout(const DevMat& W, uint4* out, hipStream_t s) {
 // 32000 x 2048 TinyLlama output, since its activation operands held in
 // registers left four waves per SIMD where this kernel has eight).  The
 // group's four words are loaded non-temporally (read once per position).
-// For elements j = 4m .. 4m + 3 of a class, the activation dword is masked
-// to its first and second halves (the two scales j >> 1 = 2m, 2m + 1) and,
-// for each half, -32 times its sum is formed; the class sums are then exact
-// integers from unsigned quants q (0..63): dot4(q, half, -32 * sum of half)
-// = sum (q - 32) * a, times the half's scale.  Each lane forms d * aux[c]
+// For elements j = 4m .. 4m + 3 of a class, the quant bytes are built with
+// the six bits at the top, the stored bit 5 flipped: the signed byte
+// 4 (q - 32).  The activation dword is masked to its first and second halves
+// (the two scales j >> 1 = 2m, 2m + 1), and dot4(quants, half) =
+// 4 sum (q - 32) * a, times the half's scale, exact in 32 bits; the class
+// sum is that total shifted right by two (exact: a multiple of four).  Each lane forms d * aux[c]
 // (d = w.d * a.d) for its two classes; then one lane per (row, class) runs
 // sums[c] += ... over the row's superblocks in order, and one lane per row
 // the final sum of sums[0..7], as the reference does.
@@ -535,21 +539,21 @@ __global__ void __launch_bounds__(256) k_gemv_q6k_cm(const uint4* __restrict__ q
     const uint32_t H[2] = {ci ? hw.z : hw.x, ci ? hw.w : hw.y};
     const uint32_t A[8] = {av[2 * ci].x,     av[2 * ci].y,     av[2 * ci].z,     av[2 * ci].w,
                            av[2 * ci + 1].x, av[2 * ci + 1].y, av[2 * ci + 1].z, av[2 * ci + 1].w};
-    int acc = 0;
+    int acc = 0;  // four times the class sum
 #pragma unroll
     for (int m = 0; m < 8; m++) {
-      const uint32_t lw = (m & 1) ? L[m >> 1] >> 4 : L[m >> 1];
+      const uint32_t lw = (m & 1) ? L[m >> 1] >> 2 : L[m >> 1] << 2;
       const uint32_t h = H[m >> 2];
-      const uint32_t hs = (m & 3) == 0 ? h << 4 : (m & 3) == 1 ? h << 2 : (m & 3) == 2 ? h : h >> 2;
-      const uint32_t q = (hs & 0x30303030u) | (lw & 0x0f0f0f0fu);
+      const uint32_t hs = (m & 3) == 0 ? h << 6 : (m & 3) == 1 ? h << 4 : (m & 3) == 2 ? h << 2 : h;
+      const uint32_t q = (hs & 0xc0c0c0c0u) | (lw & 0x3c3c3c3cu);
       const uint32_t a0 = A[m] & 0x0000ffffu, a1 = A[m] & 0xffff0000u;
-      const int c0 = dot4(q, a0, dot4(0xe0e0e0e0u, a0, 0));
-      const int c1 = dot4(q, a1, dot4(0xe0e0e0e0u, a1, 0));
+      const int c0 = dot4(q, a0, 0);
+      const int c1 = dot4(q, a1, 0);
       const int s0 = (int)(int8_t)((scw[m >> 1] >> (16 * (m & 1))) & 0xffu);
       const int s1 = (int)(int8_t)((scw[m >> 1] >> (16 * (m & 1) + 8)) & 0xffu);
       acc += __mul24(s0, c0) + __mul24(s1, c1);
     }
-    mine[s][2 * p + ci] = d * (float)acc;
+    mine[s][2 * p + ci] = d * (float)(acc >> 2);
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
