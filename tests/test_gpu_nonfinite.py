@@ -125,6 +125,17 @@ def test_forward_overflow_returns_non_finite(case):
         assert _status(lambda: s.forward_one(toks[0], 0)) == NON_FINITE
         # a session that reported the error still serves later calls
         assert _status(lambda: s.forward_one(toks[1], 1)) == NON_FINITE
+        # the decode step (forward and CDF in one wait) reports the forward's
+        # error first and leaves the range decoder where it was; no row is
+        # valid afterwards
+        from detllm_amd import coder
+
+        dec = coder.RangeDecoder(bytes(range(16)))
+        before = dec.snapshot()
+        assert _status(lambda: s.forward_decode(toks[2], 2, dec, 256)) == NON_FINITE
+        after = dec.snapshot()
+        assert (after.low, after.range, after.code, after.pos) == (before.low, before.range, before.code, before.pos)
+        assert _status(lambda: s.decode_symbol(dec, 0, 256)) == 1
         s.reset()
         assert _status(lambda: s.forward_chunk(toks[:n], 0)) == NON_FINITE
         assert _status(lambda: s.forward_chunk(toks[:3], 0)) == NON_FINITE
