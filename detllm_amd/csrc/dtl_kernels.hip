@@ -1129,7 +1129,11 @@ __global__ void __launch_bounds__(512) k_attention_hd64s(const float* q, const f
   if (bad) flag(err, ERRBIT_NON_FINITE);
 }
 
-constexpr int kHd64sRing = 4;  // tiles in flight per wave
+// Tiles in flight per wave.  One: in an A/B of the pipelined TinyLlama
+// encode on one box (ms per 2048-token step) 97.1-97.3 against 97.4-97.5 for
+// two, 97.8-97.9 for four, 99.0 for six and 99.4 for eight; the fewer
+// registers leave room for the other chunks' waves.
+constexpr int kHd64sRing = 1;
 
 size_t attention_hd64s_smem(int G, int scs) {
   // the score rows, then each wave's [8][68] area (the output's [8][64] reuses it)
