@@ -1,7 +1,7 @@
 """Full decoder forward on the GPU: logits bit-identical to the reference.
 
 The tiny-f32 / tiny-qmix fixtures are checked against the reference's own
-committed SHA-256 values; the BASELINE-shaped synthetic models against the
+committed SHA-256 values; the SmolLM2-, Qwen2.5- and TinyLlama-shaped synthetic models against the
 oracle at full width (a few positions, truncated depth where noted) and
 through size-independent properties (chunk invariance, repeatability).
 """
