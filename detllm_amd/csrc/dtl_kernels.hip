@@ -441,6 +441,9 @@ __global__ void __launch_bounds__(256) k_rope_store(float* q, float* k, const fl
                                                     int split_half, float* kc, float* vc,
                                                     int layer, int n_ctx, const int* pos_dev,
                                                     int* err) {
+  // One pass without barriers: every rotation pair is read, checked,
+  // rotated and written by one thread (a key pair also into the cache), and
+  // every element outside the pairs and every value is copied by one thread.
   int t = blockIdx.x;
   int pos = (pos_dev ? *pos_dev : pos0) + t;
   int half = rope_dim / 2;
@@ -450,11 +453,7 @@ __global__ void __launch_bounds__(256) k_rope_store(float* q, float* k, const fl
   const float* vt = v + (size_t)t * KV * hd;
   const float* ct = rc + (size_t)pos * half;
   const float* st = rs + (size_t)pos * half;
-  for (int i = threadIdx.x; i < H * hd; i += blockDim.x)
-    if (!finite(qt[i])) bad = true;
-  for (int i = threadIdx.x; i < KV * hd; i += blockDim.x)
-    if (!finite(kt[i])) bad = true;
-  __syncthreads();
+  auto cache = [&](int kvh, int dd) { return (((size_t)layer * KV + kvh) * n_ctx + pos) * hd + dd; };
   for (int p = threadIdx.x; p < (H + KV) * half; p += blockDim.x) {
     int head = p / half, j = p % half;
     float* base = head < H ? qt + head * hd : kt + (head - H) * hd;
@@ -464,18 +463,26 @@ __global__ void __launch_bounds__(256) k_rope_store(float* q, float* k, const fl
     float c = ct[j], s = st[j];
     float y0 = x0 * c - x1 * s;
     float y1 = x0 * s + x1 * c;
-    if (!finite(y0) || !finite(y1)) bad = true;
+    if (!finite(x0) || !finite(x1) || !finite(y0) || !finite(y1)) bad = true;
     base[a] = y0;
     base[b] = y1;
+    if (head >= H) {
+      kc[cache(head - H, a)] = y0;
+      kc[cache(head - H, b)] = y1;
+    }
   }
-  __syncthreads();
+  // dimensions past the rotated pairs (rope_dim < hd), unchanged
+  const int r0 = 2 * half, rest = hd - r0;
+  for (int i = threadIdx.x; i < (H + KV) * rest; i += blockDim.x) {
+    int head = i / rest, dd = r0 + i % rest;
+    float x = head < H ? qt[head * hd + dd] : kt[(head - H) * hd + dd];
+    if (!finite(x)) bad = true;
+    if (head >= H) kc[cache(head - H, dd)] = x;
+  }
   for (int i = threadIdx.x; i < KV * hd; i += blockDim.x) {
-    int kvh = i / hd, dd = i % hd;
-    size_t off = (((size_t)layer * KV + kvh) * n_ctx + pos) * hd + dd;
-    float kv = kt[i], vv = vt[i];
-    if (!finite(kv) || !finite(vv)) bad = true;
-    kc[off] = kv;
-    vc[off] = vv;
+    float vv = vt[i];
+    if (!finite(vv)) bad = true;
+    vc[cache(i / hd, i % hd)] = vv;
   }
   if (bad) flag(err, ERRBIT_NON_FINITE);
 }
